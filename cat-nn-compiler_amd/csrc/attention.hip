@@ -1,0 +1,322 @@
+// Attention core on gfx950: ctx = softmax(q·kᵀ/√dh)·v per (batch, head),
+// non-causal (the reference op, cpu.rs:252-295) or causal (the masking of
+// moe::gqa, crates/catnn-compile/src/kernel/moe.rs:104-121: query i sees keys
+// j ≤ i, masked scores are −∞, inv = 1/max(Σ, 1e-30)).  The reference
+// materialises an S×S score matrix per (b,h) and walks it sequentially; here
+// the scores never leave registers.
+//
+// d_head = 64 runs on fp32 MFMA with an online softmax.  The kernel works
+// in the transposed frame so that each lane owns one query:
+//   Sᵀ[j][i] = Σ_d K[j][d]·Q[i][d]   (A = K from LDS, B = Q from registers)
+//   Oᵀ[d][i] += Σ_j V[j][d]·P[i][j]  (A = V from LDS, B = P from registers)
+// With the 32×32 accumulator layout (lane l holds column l%32), lane l holds
+// Sᵀ and Oᵀ entries of query i = l%32 only: the row max / row sum need one
+// exchange with lane l^32, and the rescale of O is lane-local.  The P values
+// sit in exactly the registers the second MFMA reads as its B operand, so P
+// never goes through LDS.
+//
+// Block: 4 wavefronts × 32 queries = 128 queries of one (b, h); K/V tiles of
+// 64 keys are staged in LDS, double-buffered behind register prefetch.
+// Other head sizes use a one-wavefront-per-query kernel (the reference's
+// small demo blocks have d_head = 4).
+#include <hip/hip_runtime.h>
+
+#include "common.hpp"
+#include "devmath.hpp"
+#include "kernels.hpp"
+
+namespace catnn {
+namespace k {
+
+namespace {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+template <int DH>
+__global__ __launch_bounds__(256, 2) void attn_mfma_kernel(const float *__restrict__ q,
+                                                           const float *__restrict__ k,
+                                                           const float *__restrict__ v,
+                                                           int64_t ld, float *__restrict__ o,
+                                                           int64_t ldo, int S, int H,
+                                                           float qscale, int causal,
+                                                           int n_qblocks) {
+    static_assert(DH == 64, "MFMA attention is written for d_head = 64");
+    constexpr int BQ = 128, BKV = 64, LDK = DH + 4;
+    constexpr int KV_IT = BKV * DH / 4 / 256;  // float4 per thread per tile, per operand
+    __shared__ float Ks[2][BKV][LDK];
+    __shared__ float Vs[2][BKV][LDK];
+
+    const int bid = blockIdx.x;
+    // Causal work grows with the query block: start the heavy ones first.
+    const int qb = n_qblocks - 1 - (bid % n_qblocks);
+    const int bh = bid / n_qblocks;
+    const int b = bh / H, h = bh % H;
+    const int q0 = qb * BQ;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int lr = lane & 31, g = lane >> 5;
+    const int qi = q0 + wave * 32 + lr;
+    const int wave_qmax = q0 + wave * 32 + 31;
+    const int64_t row_base = (int64_t)b * S;
+
+    // This lane's query, pre-scaled into the log2 domain: Q[i][32g + s].
+    float qf[32];
+    if (qi < S) {
+        const float4 *src =
+            reinterpret_cast<const float4 *>(q + (row_base + qi) * ld + (int64_t)h * DH + 32 * g);
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            const float4 t = src[c];
+            qf[4 * c + 0] = t.x * qscale;
+            qf[4 * c + 1] = t.y * qscale;
+            qf[4 * c + 2] = t.z * qscale;
+            qf[4 * c + 3] = t.w * qscale;
+        }
+    } else {
+#pragma unroll
+        for (int s = 0; s < 32; ++s) qf[s] = 0.f;
+    }
+
+    f32x16 oacc[DH / 32];
+#pragma unroll
+    for (int db = 0; db < DH / 32; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) oacc[db][r] = 0.f;
+    float m = -INFINITY, l = 0.f;
+
+    const int kv_end = causal ? min(S, q0 + BQ) : S;
+    const int ntiles = (kv_end + BKV - 1) / BKV;
+
+    float4 pk[KV_IT], pv[KV_IT];
+    auto gload = [&](int t) {
+#pragma unroll
+        for (int it = 0; it < KV_IT; ++it) {
+            const int idx = tid + it * 256;
+            const int key = t * BKV + idx / (DH / 4);
+            const int c4 = idx % (DH / 4);
+            if (key < S) {
+                const int64_t off = (row_base + key) * ld + (int64_t)h * DH + 4 * c4;
+                pk[it] = *reinterpret_cast<const float4 *>(k + off);
+                pv[it] = *reinterpret_cast<const float4 *>(v + off);
+            } else {
+                pk[it] = make_float4(0.f, 0.f, 0.f, 0.f);
+                pv[it] = make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+        }
+    };
+    auto sstore = [&](int buf) {
+#pragma unroll
+        for (int it = 0; it < KV_IT; ++it) {
+            const int idx = tid + it * 256;
+            const int key = idx / (DH / 4), c4 = idx % (DH / 4);
+            *reinterpret_cast<float4 *>(&Ks[buf][key][4 * c4]) = pk[it];
+            *reinterpret_cast<float4 *>(&Vs[buf][key][4 * c4]) = pv[it];
+        }
+    };
+
+    gload(0);
+    sstore(0);
+    __syncthreads();
+    for (int t = 0; t < ntiles; ++t) {
+        const int buf = t & 1;
+        const bool more = t + 1 < ntiles;
+        if (more) gload(t + 1);
+        const int j0 = t * BKV;
+
+        f32x16 sacc[BKV / 32];
+        bool active[BKV / 32];
+#pragma unroll
+        for (int kb = 0; kb < BKV / 32; ++kb) {
+            const int jb = j0 + kb * 32;
+            active[kb] = jb < S && (!causal || jb <= wave_qmax);  // wave-uniform
+#pragma unroll
+            for (int r = 0; r < 16; ++r) sacc[kb][r] = 0.f;
+            if (active[kb]) {
+                const float *krow = &Ks[buf][kb * 32 + lr][32 * g];
+#pragma unroll
+                for (int c = 0; c < 8; ++c) {
+                    const float4 kv = *reinterpret_cast<const float4 *>(krow + 4 * c);
+                    sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.x, qf[4 * c + 0], sacc[kb], 0, 0, 0);
+                    sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.y, qf[4 * c + 1], sacc[kb], 0, 0, 0);
+                    sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.z, qf[4 * c + 2], sacc[kb], 0, 0, 0);
+                    sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.w, qf[4 * c + 3], sacc[kb], 0, 0, 0);
+                }
+            }
+        }
+
+        // Mask and running max for this lane's query.  Entry r of block kb
+        // is key j0 + 32kb + 8(r/4) + 4g + r%4.
+        float mx = -INFINITY;
+#pragma unroll
+        for (int kb = 0; kb < BKV / 32; ++kb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int j = j0 + kb * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+                const bool ok = active[kb] && j < S && (!causal || j <= qi);
+                const float sv = ok ? sacc[kb][r] : -INFINITY;
+                sacc[kb][r] = sv;
+                mx = fmaxf(mx, sv);
+            }
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float m_new = fmaxf(m, mx);
+        // All keys so far masked (only possible for padded queries ≥ S).
+        const bool none = m_new == -INFINITY;
+        const float factor = none ? 1.f : exp2f(m - m_new);
+        float psum = 0.f;
+#pragma unroll
+        for (int kb = 0; kb < BKV / 32; ++kb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float p = none ? 0.f : exp2f(sacc[kb][r] - m_new);
+                sacc[kb][r] = p;
+                psum += p;
+            }
+        psum += __shfl_xor(psum, 32, 64);
+        l = l * factor + psum;
+        m = m_new;
+#pragma unroll
+        for (int db = 0; db < DH / 32; ++db)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) oacc[db][r] *= factor;
+
+        // Oᵀ += Vᵀ·Pᵀ: step s feeds key 32kb + 8(s/4) + 4g + s%4 from lane
+        // half g — the key whose probability this lane holds in sacc[kb][s].
+#pragma unroll
+        for (int kb = 0; kb < BKV / 32; ++kb) {
+            if (!active[kb]) continue;
+#pragma unroll
+            for (int s = 0; s < 16; ++s) {
+                const int jl = kb * 32 + 8 * (s >> 2) + 4 * g + (s & 3);
+#pragma unroll
+                for (int db = 0; db < DH / 32; ++db)
+                    oacc[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(Vs[buf][jl][db * 32 + lr],
+                                                                    sacc[kb][s], oacc[db], 0, 0, 0);
+            }
+        }
+        if (more) sstore(buf ^ 1);
+        __syncthreads();
+    }
+
+    if (qi < S) {
+        const float inv = 1.0f / fmaxf(l, 1e-30f);
+        float *dst = o + (row_base + qi) * ldo + (int64_t)h * DH;
+#pragma unroll
+        for (int db = 0; db < DH / 32; ++db)
+#pragma unroll
+            for (int r4 = 0; r4 < 4; ++r4) {
+                const int d = db * 32 + 8 * r4 + 4 * g;
+                *reinterpret_cast<float4 *>(dst + d) =
+                    make_float4(oacc[db][4 * r4 + 0] * inv, oacc[db][4 * r4 + 1] * inv,
+                                oacc[db][4 * r4 + 2] * inv, oacc[db][4 * r4 + 3] * inv);
+            }
+    }
+}
+
+// Any head size up to 256: one wavefront per (b, h, query), lanes over the
+// head dimension, online softmax over the keys.
+__global__ __launch_bounds__(256) void attn_generic_kernel(const float *__restrict__ q,
+                                                           const float *__restrict__ k,
+                                                           const float *__restrict__ v,
+                                                           int64_t ld, float *__restrict__ o,
+                                                           int64_t ldo, int B, int S, int H,
+                                                           int DH, float scale, int causal) {
+    const int lane = threadIdx.x & 63;
+    const int64_t gw = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int64_t total = (int64_t)B * H * S;
+    if (gw >= total) return;
+    const int i = (int)(gw % S);
+    const int64_t bh = gw / S;
+    const int h = (int)(bh % H), b = (int)(bh / H);
+    const int64_t row_base = (int64_t)b * S;
+    float qv[4], acc[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const int d = lane + 64 * c;
+        qv[c] = d < DH ? q[(row_base + i) * ld + (int64_t)h * DH + d] : 0.f;
+        acc[c] = 0.f;
+    }
+    float m = -INFINITY, l = 0.f;
+    const int jend = causal ? i + 1 : S;
+    for (int j = 0; j < jend; ++j) {
+        const float *kr = k + (row_base + j) * ld + (int64_t)h * DH;
+        float part = 0.f;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int d = lane + 64 * c;
+            if (d < DH) part += qv[c] * kr[d];
+        }
+        const float sc = wave_sum(part) * scale;
+        const float m_new = fmaxf(m, sc);
+        const float factor = expf(m - m_new);
+        const float p = expf(sc - m_new);
+        l = l * factor + p;
+        m = m_new;
+        const float *vr = v + (row_base + j) * ld + (int64_t)h * DH;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int d = lane + 64 * c;
+            acc[c] = acc[c] * factor + (d < DH ? p * vr[d] : 0.f);
+        }
+    }
+    const float inv = 1.0f / fmaxf(l, 1e-30f);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const int d = lane + 64 * c;
+        if (d < DH) o[(row_base + i) * ldo + (int64_t)h * DH + d] = acc[c] * inv;
+    }
+}
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+}  // namespace
+
+void attention_core_f32(hipStream_t s, const float *q, const float *k, const float *v,
+                        int64_t ld_qkv, float *ctx, int64_t ldo, int64_t batch, int64_t seq,
+                        int64_t n_heads, int64_t d_head, bool causal) {
+    CATNN_REQUIRE(batch >= 0 && seq >= 0 && n_heads > 0 && d_head > 0, CATNN_ERR_SHAPE_MISMATCH,
+                  "attention: bad dims");
+    CATNN_REQUIRE(d_head <= 256, CATNN_ERR_SHAPE_MISMATCH, "attention: d_head > 256");
+    CATNN_REQUIRE(n_heads * d_head <= ld_qkv && n_heads * d_head <= ldo, CATNN_ERR_SHAPE_MISMATCH,
+                  "attention: heads exceed the row width");
+    CATNN_REQUIRE(batch * seq < (1ll << 31), CATNN_ERR_SHAPE_MISMATCH, "attention: too many rows");
+    if (batch == 0 || seq == 0) return;
+    const float scale = 1.0f / sqrtf((float)d_head);
+    const bool mfma = d_head == 64 && ld_qkv % 4 == 0 && ldo % 4 == 0 && aligned16(q) &&
+                      aligned16(k) && aligned16(v) && aligned16(ctx);
+    if (mfma) {
+        const int nqb = (int)((seq + 127) / 128);
+        const int64_t blocks = batch * n_heads * nqb;
+        CATNN_REQUIRE(blocks < (1ll << 31), CATNN_ERR_SHAPE_MISMATCH, "attention: grid too large");
+        attn_mfma_kernel<64><<<(unsigned)blocks, 256, 0, s>>>(
+            q, k, v, ld_qkv, ctx, ldo, (int)seq, (int)n_heads, scale * kLog2e, causal ? 1 : 0, nqb);
+    } else {
+        const int64_t waves = batch * n_heads * seq;
+        const int64_t blocks = (waves + 3) / 4;
+        CATNN_REQUIRE(blocks < (1ll << 31), CATNN_ERR_SHAPE_MISMATCH, "attention: grid too large");
+        attn_generic_kernel<<<(unsigned)blocks, 256, 0, s>>>(q, k, v, ld_qkv, ctx, ldo, (int)batch,
+                                                             (int)seq, (int)n_heads, (int)d_head,
+                                                             scale, causal ? 1 : 0);
+    }
+    CATNN_HIP(hipGetLastError());
+}
+
+}  // namespace k
+}  // namespace catnn
+
+using namespace catnn;
+
+extern "C" int catnn_hip_attention_core_f32(catnn_hip_device *dev, const float *q, const float *k,
+                                            const float *v, float *ctx, int64_t batch, int64_t seq,
+                                            int64_t d_model, int64_t n_heads, int64_t d_head,
+                                            int32_t causal) {
+    return guard([&] {
+        require_device(dev);
+        CATNN_REQUIRE((q && k && v && ctx) || batch * seq == 0, CATNN_ERR_INVALID_ARGUMENT,
+                      "attention: null operand");
+        CATNN_REQUIRE(n_heads * d_head == d_model, CATNN_ERR_SHAPE_MISMATCH,
+                      "attention: n_heads*d_head != d_model");
+        k::attention_core_f32(dev->stream, q, k, v, d_model, ctx, d_model, batch, seq, n_heads,
+                              d_head, causal != 0);
+    });
+}

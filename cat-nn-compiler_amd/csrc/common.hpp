@@ -1,0 +1,94 @@
+// Internal plumbing shared by the runtime translation units: error
+// propagation across the C ABI, HIP status checks, and the device handle.
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+
+#include <chrono>
+#include <cstdint>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "catnn_hip.h"
+
+namespace catnn {
+
+// Internal failure carrying a catnn_status code; converted to a return code
+// and a thread-local message at the C boundary (see guard()).
+struct Failure {
+    int code;
+    std::string msg;
+};
+
+[[noreturn]] void fail(int code, const std::string &msg);
+void set_last_error(const std::string &msg);
+
+#define CATNN_HIP(expr)                                                            \
+    do {                                                                           \
+        hipError_t catnn_e_ = (expr);                                              \
+        if (catnn_e_ != hipSuccess)                                                \
+            ::catnn::fail(CATNN_ERR_DEVICE,                                        \
+                          std::string(#expr) + ": " + hipGetErrorString(catnn_e_)); \
+    } while (0)
+
+#define CATNN_REQUIRE(cond, code, msg)                   \
+    do {                                                 \
+        if (!(cond)) ::catnn::fail((code), (msg));       \
+    } while (0)
+
+// Run `f` and translate a Failure (or any exception) into a status code.
+template <class F>
+int guard(F &&f) {
+    try {
+        f();
+        set_last_error("");
+        return CATNN_OK;
+    } catch (const Failure &e) {
+        set_last_error(e.msg);
+        return e.code;
+    } catch (const std::exception &e) {
+        set_last_error(std::string("internal: ") + e.what());
+        return CATNN_ERR_INVALID_ARGUMENT;
+    }
+}
+
+struct Binding {
+    uint64_t offset;
+    uint64_t bytes;
+};
+
+// Growable device scratch owned by a device (MoE permutation buffers,
+// per-slot expert outputs).  Grown with hipMalloc, never shrunk.
+struct Workspace {
+    void *ptr = nullptr;
+    uint64_t bytes = 0;
+};
+
+}  // namespace catnn
+
+struct catnn_hip_device {
+    int ordinal = 0;
+    hipStream_t stream = nullptr;
+    hipEvent_t t_start = nullptr, t_stop = nullptr;
+    void *arena = nullptr;
+    uint64_t arena_bytes = 0;
+    std::unordered_map<std::string, catnn::Binding> bindings;
+    std::vector<void *> allocations;
+    std::vector<catnn_event> events;
+    std::chrono::steady_clock::time_point epoch;
+    catnn::Workspace moe_ws;
+    int cu_count = 0;
+};
+
+namespace catnn {
+
+void require_device(catnn_hip_device *dev);
+// Resolve a bound arena buffer; fails with UNKNOWN_PORT naming the id.
+void *buffer(catnn_hip_device *dev, const std::string &id, uint64_t *bytes = nullptr);
+// Make sure dev->moe_ws holds at least `bytes`.
+void *workspace(catnn_hip_device *dev, Workspace &ws, uint64_t bytes);
+void push_event(catnn_hip_device *dev, const std::string &op, int kind, uint64_t checksum);
+uint64_t fnv1a_f32(const float *data, uint64_t n);
+
+}  // namespace catnn

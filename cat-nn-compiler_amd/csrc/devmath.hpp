@@ -1,0 +1,64 @@
+// Device-side scalar helpers shared by the kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+namespace catnn {
+namespace k {
+
+// GELU, tanh form: 0.5·z·(1 + tanh(√(2/π)·(z + 0.044715·z³))), with the
+// constant rounded to f32 and the cube evaluated left to right as
+// crates/catnn-compile/src/kernel/cpu.rs:20-29 does.
+__device__ __forceinline__ float gelu_tanh(float z) {
+    const float c = 0.797884523868560791f;  // f32 sqrt(f32(2) / f32(pi))
+    const float inner = c * (z + 0.044715f * z * z * z);
+    return 0.5f * z * (1.0f + tanhf(inner));
+}
+
+// SiLU, crates/catnn-compile/src/kernel/moe.rs:12-14: x / (1 + e^{-x}).
+__device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
+
+__device__ __forceinline__ float apply_act(float v, int act) {
+    if (act == 2) return fmaxf(v, 0.0f);
+    if (act == 3) return gelu_tanh(v);
+    return v;
+}
+
+// Butterfly reductions across the 64 lanes of a wavefront.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+// Blocks of one launch are dealt round-robin to the 8 XCDs of an MI355X
+// (block b runs on XCD b % 8), and each XCD has its own L2.  Renumber so
+// that each XCD owns one contiguous range of logical tiles; neighbouring
+// tiles share operand panels, so their reuse stays inside one L2.
+__device__ __forceinline__ int xcd_remap(int pid, int nblocks) {
+    if ((nblocks & 7) != 0) return pid;
+    return (pid & 7) * (nblocks >> 3) + (pid >> 3);
+}
+
+// Grouped tile order: walk `group` row-tiles down a column of tiles before
+// moving right, so that blocks resident together reuse the same B panel
+// and a small set of A panels.
+__device__ __forceinline__ void grouped_tile(int lid, int tiles_m, int tiles_n, int group,
+                                             int &tm, int &tn) {
+    const int per_group = group * tiles_n;
+    const int g = lid / per_group;
+    const int first_m = g * group;
+    const int gsz = min(tiles_m - first_m, group);
+    const int in_group = lid - g * per_group;
+    tm = first_m + in_group % gsz;
+    tn = in_group / gsz;
+}
+
+}  // namespace k
+}  // namespace catnn

@@ -1,0 +1,501 @@
+// Mixture-of-experts layer on gfx950.
+//
+// Replaces moe::moe (crates/catnn-compile/src/kernel/moe.rs:197-223), which
+// loops over tokens and, per (token, selected expert), runs a [1,H] SwiGLU
+// GEMV streaming the expert's three weight matrices (moe.rs:159-174).  Here
+// the layer runs as five launches over all tokens at once:
+//
+//  1. route     logits = x·gate with the exact summation order of
+//               cpu::linear_seq (cpu.rs:115-126: s = 0; s += x[p]·g[p] for
+//               p ascending, separate multiply and add), then per token the
+//               top-k of a stable descending order (ties → lower expert id,
+//               lens/moe.rs:175-187) and w = exp(l − max)·(1/max(Σ, 1e-30)).
+//               Bit-exact logits make the indices bit-exact.
+//  2. permute   stable counting sort of the flattened slots s = t·k + k'
+//               by expert: per-block histograms, a scan, and a scatter that
+//               ranks slots inside each wavefront with ballot + popcount.
+//  3. gate/up   grouped fp32 MFMA GEMM over each expert's row segment, A rows
+//               gathered from x through the permutation, W1 and W3 tiles
+//               side by side, epilogue silu(a)·c → h[pos].
+//  4. down      grouped fp32 MFMA GEMM h[pos]·W2 → y[pos].
+//  5. combine   out[t] = (0 + w[t,0]·y[pos(t,0)]) + w[t,1]·y[pos(t,1)] …,
+//               ascending k with separate multiply and add, as moe.rs:212-220.
+// No floating-point atomics anywhere, so results are run-to-run identical.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstring>
+#include <vector>
+
+#include "common.hpp"
+#include "devmath.hpp"
+#include "gemm_f32.hpp"
+#include "kernels.hpp"
+
+namespace catnn {
+namespace k {
+
+namespace {
+
+constexpr int kRouteChunk = 64;   // hidden elements staged per LDS pass
+constexpr int kPermChunk = 4096;  // slots per permutation block
+constexpr int kMaxRouteExperts = 256;
+constexpr int kMaxTopK = 16;
+
+// One thread per (token, expert); tokens_per_block = 256 / E.
+__global__ __launch_bounds__(256) void route_kernel(const float *__restrict__ x,
+                                                    const float *__restrict__ gate, int T, int H,
+                                                    int E, int K, int tpb,
+                                                    int32_t *__restrict__ idx_out,
+                                                    float *__restrict__ w_out,
+                                                    float *__restrict__ logits_out) {
+#pragma clang fp contract(off)
+    extern __shared__ float smem[];
+    float *xs = smem;                                  // [tpb][kRouteChunk + 1]
+    float *gs = xs + tpb * (kRouteChunk + 1);          // [kRouteChunk][E]
+    float *lg = gs + kRouteChunk * E;                  // [tpb][E]
+    const int tid = threadIdx.x;
+    const int t0 = blockIdx.x * tpb;
+    const int tl = tid / E, e = tid % E;
+    const bool active = tl < tpb && t0 + tl < T;
+    float s = 0.0f;
+    for (int p0 = 0; p0 < H; p0 += kRouteChunk) {
+        const int pc = min(kRouteChunk, H - p0);
+        for (int i = tid; i < tpb * kRouteChunk; i += 256) {
+            const int r = i / kRouteChunk, c = i % kRouteChunk;
+            xs[r * (kRouteChunk + 1) + c] =
+                (t0 + r < T && c < pc) ? x[(int64_t)(t0 + r) * H + p0 + c] : 0.f;
+        }
+        for (int i = tid; i < kRouteChunk * E; i += 256) {
+            const int r = i / E;
+            gs[i] = r < pc ? gate[(int64_t)(p0 + r) * E + (i % E)] : 0.f;
+        }
+        __syncthreads();
+        if (active) {
+            const float *xr = xs + tl * (kRouteChunk + 1);
+            for (int p = 0; p < pc; ++p) {
+                const float prod = xr[p] * gs[p * E + e];
+                s = s + prod;
+            }
+        }
+        __syncthreads();
+    }
+    if (active) {
+        lg[tl * E + e] = s;
+        if (logits_out) logits_out[(int64_t)(t0 + tl) * E + e] = s;
+    }
+    __syncthreads();
+    if (!active || e != 0) return;
+    // Top-k of a stable descending order: repeated first-maximum selection.
+    const float *row = lg + tl * E;
+    int sel[kMaxTopK];
+    unsigned long long taken[kMaxRouteExperts / 64] = {0, 0, 0, 0};
+    for (int kk = 0; kk < K; ++kk) {
+        int best = -1;
+        for (int c = 0; c < E; ++c) {
+            if ((taken[c >> 6] >> (c & 63)) & 1ull) continue;
+            if (best < 0 || row[c] > row[best]) best = c;
+        }
+        sel[kk] = best;
+        taken[best >> 6] |= 1ull << (best & 63);
+    }
+    float mx = -INFINITY;
+    for (int kk = 0; kk < K; ++kk) mx = fmaxf(mx, row[sel[kk]]);
+    float ex[kMaxTopK];
+    float sum = 0.f;
+    for (int kk = 0; kk < K; ++kk) {
+        ex[kk] = expf(row[sel[kk]] - mx);
+        sum = sum + ex[kk];
+    }
+    const float inv = 1.0f / fmaxf(sum, 1e-30f);
+    const int64_t base = (int64_t)(t0 + tl) * K;
+    for (int kk = 0; kk < K; ++kk) {
+        if (idx_out) idx_out[base + kk] = sel[kk];
+        if (w_out) w_out[base + kk] = ex[kk] * inv;
+    }
+}
+
+// Per-block expert histogram of the slots [b·chunk, (b+1)·chunk).  Slots
+// with an expert id outside [0, E) are counted in bad[0] and skipped.
+__global__ __launch_bounds__(256) void perm_count_kernel(const int32_t *__restrict__ idx,
+                                                         int64_t n, int E,
+                                                         int32_t *__restrict__ block_counts,
+                                                         int32_t *__restrict__ bad) {
+    __shared__ int cnt[kMaxExperts];
+    for (int e = threadIdx.x; e < E; e += 256) cnt[e] = 0;
+    __syncthreads();
+    const int64_t base = (int64_t)blockIdx.x * kPermChunk;
+    for (int i = threadIdx.x; i < kPermChunk; i += 256) {
+        const int64_t s = base + i;
+        if (s < n) {
+            const int e = idx[s];
+            if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
+            else atomicAdd(bad, 1);
+        }
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < E; e += 256) block_counts[(int64_t)blockIdx.x * E + e] = cnt[e];
+}
+
+// counts, offsets (exclusive prefix, length E+1) and each block's starting
+// position per expert.  One wavefront; thread e owns expert e.
+__global__ void perm_scan_kernel(const int32_t *__restrict__ block_counts, int nb, int E,
+                                 int32_t *__restrict__ block_base, int32_t *__restrict__ counts,
+                                 int32_t *__restrict__ offsets) {
+    __shared__ int tot[kMaxExperts + 1];
+    const int e = threadIdx.x;
+    if (e < E) {
+        int run = 0;
+        for (int b = 0; b < nb; ++b) {
+            block_base[(int64_t)b * E + e] = run;
+            run += block_counts[(int64_t)b * E + e];
+        }
+        tot[e] = run;
+        counts[e] = run;
+    }
+    __syncthreads();
+    if (e == 0) {
+        int acc = 0;
+        for (int c = 0; c < E; ++c) {
+            const int t = tot[c];
+            tot[c] = acc;
+            offsets[c] = acc;
+            acc += t;
+        }
+        offsets[E] = acc;
+    }
+    __syncthreads();
+    if (e < E) {
+        const int off = tot[e];
+        for (int b = 0; b < nb; ++b) block_base[(int64_t)b * E + e] += off;
+    }
+}
+
+// Stable scatter: slot s goes to offsets[e] + (number of earlier slots with
+// the same expert).  Slots are visited in ascending order, 256 at a time;
+// inside a wavefront the rank among equal experts is the popcount of the
+// ballot below the lane, across wavefronts it is the counts of the lower
+// wavefronts, across iterations and blocks the running totals.
+__global__ __launch_bounds__(256) void perm_scatter_kernel(const int32_t *__restrict__ idx,
+                                                           int64_t n, int E,
+                                                           const int32_t *__restrict__ block_base,
+                                                           int32_t *__restrict__ slot_of_pos,
+                                                           int32_t *__restrict__ pos_of_slot) {
+    __shared__ int running[kMaxExperts];
+    __shared__ int wave_cnt[4][kMaxExperts];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    for (int e = tid; e < E; e += 256) running[e] = block_base[(int64_t)blockIdx.x * E + e];
+    __syncthreads();
+    const int64_t base = (int64_t)blockIdx.x * kPermChunk;
+    const unsigned long long below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    for (int it = 0; it < kPermChunk / 256; ++it) {
+        const int64_t s = base + it * 256 + tid;
+        int e = s < n ? idx[s] : -1;
+        if (e >= E) e = -1;
+        int rank = 0;
+        for (int c = 0; c < E; ++c) {
+            const unsigned long long m = __ballot(e == c);
+            if (e == c) rank = __popcll(m & below);
+            if (lane == 0) wave_cnt[wave][c] = __popcll(m);
+        }
+        __syncthreads();
+        if (e >= 0) {
+            int pos = running[e] + rank;
+            for (int w = 0; w < wave; ++w) pos += wave_cnt[w][e];
+            slot_of_pos[pos] = (int32_t)s;
+            pos_of_slot[s] = pos;
+        } else if (s < n) {
+            pos_of_slot[s] = -1;
+        }
+        __syncthreads();
+        for (int c = tid; c < E; c += 256)
+            running[c] += wave_cnt[0][c] + wave_cnt[1][c] + wave_cnt[2][c] + wave_cnt[3][c];
+        __syncthreads();
+    }
+}
+
+// out[t, c] = Σ_k (ascending) w[t,k]·y[pos(t,k), c], starting from 0.
+__global__ __launch_bounds__(256) void combine_kernel(const float *__restrict__ y,
+                                                      const int32_t *__restrict__ pos_of_slot,
+                                                      const float *__restrict__ w, int T, int K,
+                                                      int H, float *__restrict__ out) {
+#pragma clang fp contract(off)
+    const int t = blockIdx.x;
+    if (t >= T) return;
+    for (int c = threadIdx.x; c < H; c += 256) {
+        float acc = 0.0f;
+        for (int kk = 0; kk < K; ++kk) {
+            const int64_t slot = (int64_t)t * K + kk;
+            const float prod = w[slot] * y[(int64_t)pos_of_slot[slot] * H + c];
+            acc = acc + prod;
+        }
+        out[(int64_t)t * H + c] = acc;
+    }
+}
+
+__global__ __launch_bounds__(256) void combine4_kernel(const float *__restrict__ y,
+                                                       const int32_t *__restrict__ pos_of_slot,
+                                                       const float *__restrict__ w, int T, int K,
+                                                       int H, float *__restrict__ out) {
+#pragma clang fp contract(off)
+    const int t = blockIdx.x;
+    if (t >= T) return;
+    const int h4 = H / 4;
+    for (int c = threadIdx.x; c < h4; c += 256) {
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int kk = 0; kk < K; ++kk) {
+            const int64_t slot = (int64_t)t * K + kk;
+            const float ws = w[slot];
+            const float4 v =
+                reinterpret_cast<const float4 *>(y + (int64_t)pos_of_slot[slot] * H)[c];
+            const float px = ws * v.x, py = ws * v.y, pz = ws * v.z, pw = ws * v.w;
+            acc.x = acc.x + px;
+            acc.y = acc.y + py;
+            acc.z = acc.z + pz;
+            acc.w = acc.w + pw;
+        }
+        reinterpret_cast<float4 *>(out + (int64_t)t * H)[c] = acc;
+    }
+}
+
+uint64_t align256(uint64_t v) { return (v + 255) & ~uint64_t(255); }
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+}  // namespace
+
+void moe_route_f32(hipStream_t s, const float *x, const float *gate, int64_t tokens, int64_t hidden,
+                   int64_t n_experts, int64_t top_k, int32_t *idx, float *w, float *logits) {
+    CATNN_REQUIRE(tokens >= 0 && hidden > 0 && n_experts > 0, CATNN_ERR_SHAPE_MISMATCH,
+                  "route: bad dims");
+    CATNN_REQUIRE(n_experts <= kMaxRouteExperts, CATNN_ERR_SHAPE_MISMATCH,
+                  "route: more than 256 experts");
+    CATNN_REQUIRE(top_k >= 1 && top_k <= n_experts && top_k <= kMaxTopK, CATNN_ERR_SHAPE_MISMATCH,
+                  "route: top_k must be in [1, min(n_experts, 16)]");
+    CATNN_REQUIRE(tokens < (1ll << 31) && hidden < (1ll << 31), CATNN_ERR_SHAPE_MISMATCH,
+                  "route: dims exceed 2^31");
+    if (tokens == 0) return;
+    const int E = (int)n_experts;
+    const int tpb = std::min(64, 256 / E);  // ≤ 64 tokens keeps the LDS stage under 20 KB
+    const int64_t blocks = (tokens + tpb - 1) / tpb;
+    const size_t smem = sizeof(float) * ((size_t)tpb * (kRouteChunk + 1) +
+                                         (size_t)kRouteChunk * E + (size_t)tpb * E);
+    route_kernel<<<(unsigned)blocks, 256, smem, s>>>(x, gate, (int)tokens, (int)hidden, E,
+                                                     (int)top_k, tpb, idx, w, logits);
+    CATNN_HIP(hipGetLastError());
+}
+
+uint64_t moe_permute_scratch_bytes(int64_t tokens, int64_t top_k, int64_t n_experts) {
+    const int64_t n = tokens * top_k;
+    const int64_t nb = (n + kPermChunk - 1) / kPermChunk;
+    // block_counts + block_base + bad counter
+    return align256((uint64_t)nb * n_experts * 4) * 2 + 256;
+}
+
+void moe_permute(hipStream_t s, const int32_t *idx, int64_t tokens, int64_t top_k, int64_t n_experts,
+                 int32_t *counts, int32_t *offsets, int32_t *slot_of_pos, int32_t *pos_of_slot,
+                 void *scratch) {
+    CATNN_REQUIRE(n_experts > 0 && n_experts <= kMaxExperts, CATNN_ERR_SHAPE_MISMATCH,
+                  "permute: n_experts must be in [1, 64]");
+    CATNN_REQUIRE(tokens >= 0 && top_k >= 1 && tokens * top_k < (1ll << 31),
+                  CATNN_ERR_SHAPE_MISMATCH, "permute: slot count out of range");
+    const int64_t n = tokens * top_k;
+    const int E = (int)n_experts;
+    const int64_t nb = (n + kPermChunk - 1) / kPermChunk;
+    char *sc = static_cast<char *>(scratch);
+    int32_t *block_counts = reinterpret_cast<int32_t *>(sc);
+    int32_t *block_base = reinterpret_cast<int32_t *>(sc + align256((uint64_t)nb * E * 4));
+    int32_t *bad = reinterpret_cast<int32_t *>(sc + 2 * align256((uint64_t)nb * E * 4));
+    CATNN_HIP(hipMemsetAsync(bad, 0, 4, s));
+    if (nb > 0) {
+        perm_count_kernel<<<(unsigned)nb, 256, 0, s>>>(idx, n, E, block_counts, bad);
+        CATNN_HIP(hipGetLastError());
+    }
+    perm_scan_kernel<<<1, 64, 0, s>>>(block_counts, (int)nb, E, block_base, counts, offsets);
+    CATNN_HIP(hipGetLastError());
+    if (nb > 0) {
+        perm_scatter_kernel<<<(unsigned)nb, 256, 0, s>>>(idx, n, E, block_base, slot_of_pos,
+                                                         pos_of_slot);
+        CATNN_HIP(hipGetLastError());
+    }
+}
+
+MoeWorkspaceLayout moe_workspace_layout(int64_t tokens, int64_t hidden, int64_t intermediate,
+                                        int64_t n_experts, int64_t top_k) {
+    MoeWorkspaceLayout L{};
+    const uint64_t n = (uint64_t)(tokens * top_k);
+    const uint64_t max_tiles = (n + gemm_tile_rows() - 1) / gemm_tile_rows() + n_experts;
+    uint64_t off = 0;
+    auto take = [&](uint64_t bytes) {
+        const uint64_t o = off;
+        off += align256(bytes ? bytes : 1);
+        return o;
+    };
+    L.idx = take(n * 4);
+    L.w = take(n * 4);
+    L.counts = take((uint64_t)n_experts * 4);
+    L.offsets = take((uint64_t)(n_experts + 1) * 4);
+    L.slot_of_pos = take(n * 4);
+    L.pos_of_slot = take(n * 4);
+    L.perm_scratch = take(moe_permute_scratch_bytes(tokens, top_k, n_experts));
+    L.tiles = take((2 * max_tiles + 1) * 4);
+    L.ptrs = 0;
+    L.h = take(n * (uint64_t)intermediate * 4);
+    L.y = take(n * (uint64_t)hidden * 4);
+    L.total = off;
+    return L;
+}
+
+void moe_f32(hipStream_t s, const float *x, const float *gate, const float *const *w1s,
+             const float *const *w3s, const float *const *w2s, int64_t tokens, int64_t hidden,
+             int64_t intermediate, int64_t n_experts, int64_t top_k, float *out, void *ws,
+             const MoeWorkspaceLayout &L) {
+    CATNN_REQUIRE(n_experts >= 1 && n_experts <= kMaxExperts, CATNN_ERR_SHAPE_MISMATCH,
+                  "moe: n_experts must be in [1, 64]");
+    CATNN_REQUIRE(tokens >= 0 && hidden > 0 && intermediate > 0, CATNN_ERR_SHAPE_MISMATCH,
+                  "moe: bad dims");
+    CATNN_REQUIRE(tokens * top_k < (1ll << 31) && intermediate < (1ll << 31) &&
+                      hidden < (1ll << 31),
+                  CATNN_ERR_SHAPE_MISMATCH, "moe: dims exceed 2^31");
+    if (tokens == 0) return;
+    char *base = static_cast<char *>(ws);
+    int32_t *idx = reinterpret_cast<int32_t *>(base + L.idx);
+    float *w = reinterpret_cast<float *>(base + L.w);
+    int32_t *counts = reinterpret_cast<int32_t *>(base + L.counts);
+    int32_t *offsets = reinterpret_cast<int32_t *>(base + L.offsets);
+    int32_t *slot_of_pos = reinterpret_cast<int32_t *>(base + L.slot_of_pos);
+    int32_t *pos_of_slot = reinterpret_cast<int32_t *>(base + L.pos_of_slot);
+    const int64_t n = tokens * top_k;
+    const int max_tiles = (int)((n + gemm_tile_rows() - 1) / gemm_tile_rows() + n_experts);
+    int32_t *tile_expert = reinterpret_cast<int32_t *>(base + L.tiles);
+    int32_t *tile_row0 = tile_expert + max_tiles;
+    int32_t *n_tiles = tile_row0 + max_tiles;
+    float *h = reinterpret_cast<float *>(base + L.h);
+    float *y = reinterpret_cast<float *>(base + L.y);
+
+    moe_route_f32(s, x, gate, tokens, hidden, n_experts, top_k, idx, w, nullptr);
+    moe_permute(s, idx, tokens, top_k, n_experts, counts, offsets, slot_of_pos, pos_of_slot,
+                base + L.perm_scratch);
+    build_tiles(s, offsets, (int)n_experts, tile_expert, tile_row0, n_tiles);
+
+    GemmParams g{};
+    g.tile_expert = tile_expert;
+    g.tile_row0 = tile_row0;
+    g.n_tiles = n_tiles;
+    g.seg_offsets = offsets;
+    g.max_tiles = max_tiles;
+    g.n_experts = (int)n_experts;
+    g.act = ACT_NONE;
+
+    // gate/up: h[pos] = silu(x[token(pos)]·w1) ⊙ (x[token(pos)]·w3)
+    g.A = x;
+    g.lda = hidden;
+    g.a_rows = slot_of_pos;
+    g.a_row_div = (int)top_k;
+    for (int e = 0; e < n_experts; ++e) {
+        g.B_e[e] = w1s[e];
+        g.B2_e[e] = w3s[e];
+    }
+    g.ldb = intermediate;
+    g.C = h;
+    g.ldc = intermediate;
+    g.N = (int)intermediate;
+    g.K = (int)hidden;
+    gemm_grouped_launch(s, g, true);
+
+    // down: y[pos] = h[pos]·w2
+    g.A = h;
+    g.lda = intermediate;
+    g.a_rows = nullptr;
+    g.a_row_div = 1;
+    for (int e = 0; e < n_experts; ++e) {
+        g.B_e[e] = w2s[e];
+        g.B2_e[e] = nullptr;
+    }
+    g.ldb = hidden;
+    g.C = y;
+    g.ldc = hidden;
+    g.N = (int)hidden;
+    g.K = (int)intermediate;
+    gemm_grouped_launch(s, g, false);
+
+    if (hidden % 4 == 0 && aligned16(out))
+        combine4_kernel<<<(unsigned)tokens, 256, 0, s>>>(y, pos_of_slot, w, (int)tokens,
+                                                         (int)top_k, (int)hidden, out);
+    else
+        combine_kernel<<<(unsigned)tokens, 256, 0, s>>>(y, pos_of_slot, w, (int)tokens, (int)top_k,
+                                                        (int)hidden, out);
+    CATNN_HIP(hipGetLastError());
+}
+
+}  // namespace k
+}  // namespace catnn
+
+using namespace catnn;
+
+extern "C" {
+
+int catnn_hip_moe_route_f32(catnn_hip_device *dev, const float *x, const float *gate,
+                            int64_t tokens, int64_t hidden, int64_t n_experts, int64_t top_k,
+                            int32_t *idx, float *w, float *logits) {
+    return guard([&] {
+        require_device(dev);
+        CATNN_REQUIRE((x && gate) || tokens == 0, CATNN_ERR_INVALID_ARGUMENT,
+                      "route: null operand");
+        k::moe_route_f32(dev->stream, x, gate, tokens, hidden, n_experts, top_k, idx, w, logits);
+    });
+}
+
+int catnn_hip_moe_permute(catnn_hip_device *dev, const int32_t *idx, int64_t tokens, int64_t top_k,
+                          int64_t n_experts, int32_t *counts, int32_t *offsets,
+                          int32_t *slot_of_pos, int32_t *pos_of_slot) {
+    return guard([&] {
+        require_device(dev);
+        CATNN_REQUIRE(counts && offsets && ((idx && slot_of_pos && pos_of_slot) || tokens == 0),
+                      CATNN_ERR_INVALID_ARGUMENT, "permute: null operand");
+        const uint64_t bytes = k::moe_permute_scratch_bytes(tokens, top_k, n_experts);
+        void *scratch = workspace(dev, dev->moe_ws, bytes);
+        k::moe_permute(dev->stream, idx, tokens, top_k, n_experts, counts, offsets, slot_of_pos,
+                       pos_of_slot, scratch);
+        // Caller-supplied ids may be out of range: report instead of guessing.
+        int32_t bad = 0;
+        CATNN_HIP(hipMemcpyAsync(&bad, static_cast<char *>(scratch) + bytes - 256, 4,
+                                 hipMemcpyDeviceToHost, dev->stream));
+        CATNN_HIP(hipStreamSynchronize(dev->stream));
+        CATNN_REQUIRE(bad == 0, CATNN_ERR_SHAPE_MISMATCH,
+                      "permute: " + std::to_string(bad) + " expert ids outside [0, n_experts)");
+    });
+}
+
+int catnn_hip_moe_f32(catnn_hip_device *dev, const float *x, const float *gate,
+                      const float *const *w1s, const float *const *w3s, const float *const *w2s,
+                      int64_t tokens, int64_t hidden, int64_t intermediate, int64_t n_experts,
+                      int64_t top_k, float *out, int32_t *idx, float *w, int32_t *counts) {
+    return guard([&] {
+        require_device(dev);
+        CATNN_REQUIRE(w1s && w3s && w2s, CATNN_ERR_INVALID_ARGUMENT, "moe: null weight table");
+        CATNN_REQUIRE((x && gate && out) || tokens == 0, CATNN_ERR_INVALID_ARGUMENT,
+                      "moe: null operand");
+        CATNN_REQUIRE(n_experts >= 1 && n_experts <= k::kMaxExperts, CATNN_ERR_SHAPE_MISMATCH,
+                      "moe: n_experts must be in [1, 64]");
+        for (int64_t e = 0; e < n_experts; ++e)
+            CATNN_REQUIRE(w1s[e] && w3s[e] && w2s[e], CATNN_ERR_INVALID_ARGUMENT,
+                          "moe: null expert weight " + std::to_string(e));
+        const k::MoeWorkspaceLayout L =
+            k::moe_workspace_layout(tokens, hidden, intermediate, n_experts, top_k);
+        void *ws = workspace(dev, dev->moe_ws, L.total);
+        k::moe_f32(dev->stream, x, gate, w1s, w3s, w2s, tokens, hidden, intermediate, n_experts,
+                   top_k, out, ws, L);
+        char *base = static_cast<char *>(ws);
+        const uint64_t n = (uint64_t)(tokens * top_k);
+        if (idx && n)
+            CATNN_HIP(hipMemcpyAsync(idx, base + L.idx, n * 4, hipMemcpyDeviceToDevice, dev->stream));
+        if (w && n)
+            CATNN_HIP(hipMemcpyAsync(w, base + L.w, n * 4, hipMemcpyDeviceToDevice, dev->stream));
+        if (counts)
+            CATNN_HIP(hipMemcpyAsync(counts, base + L.counts, (uint64_t)n_experts * 4,
+                                     hipMemcpyDeviceToDevice, dev->stream));
+    });
+}
+
+}  // extern "C"

@@ -1,0 +1,374 @@
+/*
+ * catnn_hip.h — C ABI of the MI355X (gfx950) execution backend for catnn's
+ * lowered IR.
+ *
+ * The reference (dkarapetyan-afk/cat-nn-compiler, Rust) executes every IR node
+ * through `DeviceHandler::run_kernel(&mut self, node: &IrNode,
+ * inputs: &[Tensor]) -> CatResult<Tensor>` (crates/catnn-rt/src/handler.rs:34),
+ * which calls `kernel::eval_cpu` (crates/catnn-compile/src/kernel/mod.rs:21)
+ * even for GPU-placed nodes (handler.rs:43-46).  This header is what a Rust
+ * `-sys` crate (or any FFI) binds to replace that call for a new
+ * `KernelBackend::Hip` target.  Every function is `extern "C"`, takes plain
+ * pointers and sizes, returns an `int` status (0 = ok, otherwise one of the
+ * CATNN_ERR_* codes that map 1:1 onto `CatError` variants,
+ * crates/catnn-core/src/error.rs:9-54), and leaves a message in the calling
+ * thread's `catnn_hip_last_error()`.
+ *
+ * Threading contract (mirrors the reference's wave model, dist.rs:441-517):
+ * a device handle is used by one host thread at a time; each device owns one
+ * in-order HIP stream, so arena buffers whose lifetimes do not overlap may
+ * alias safely.
+ *
+ * Ownership: host pointers passed in are borrowed for the duration of the
+ * call only.  Device pointers returned by catnn_hip_buffer_ptr /
+ * catnn_hip_alloc stay owned by the library.
+ */
+#ifndef CATNN_HIP_H
+#define CATNN_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------------------------------------------------------- status */
+/* CatError variants, crates/catnn-core/src/error.rs:9-54 (same order). */
+enum catnn_status {
+    CATNN_OK = 0,
+    CATNN_ERR_INTERFACE_MISMATCH = 1,   /* error.rs:11 */
+    CATNN_ERR_SHAPE_MISMATCH = 2,       /* error.rs:14 */
+    CATNN_ERR_DTYPE_MISMATCH = 3,       /* error.rs:17 */
+    CATNN_ERR_UNKNOWN_PORT = 4,         /* error.rs:20 */
+    CATNN_ERR_UNKNOWN_COMPONENT = 5,    /* error.rs:23 */
+    CATNN_ERR_UNKNOWN_ARCHITECTURE = 6, /* error.rs:26 */
+    CATNN_ERR_UNKNOWN_REALIZATION = 7,  /* error.rs:29 */
+    CATNN_ERR_WIRING = 8,               /* error.rs:32 (cycles, missing preds) */
+    CATNN_ERR_PARSE = 9,                /* error.rs:35 */
+    CATNN_ERR_FIBRATION = 10,           /* error.rs:38 (arena overflow, schedule.rs:101-105) */
+    CATNN_ERR_WITNESS = 11,             /* error.rs:41 */
+    CATNN_ERR_DESCENT = 12,             /* error.rs:44 */
+    CATNN_ERR_INTERVAL = 13,            /* error.rs:47 */
+    CATNN_ERR_UNLAWFUL = 14,            /* error.rs:50 */
+    CATNN_ERR_IO = 15,                  /* error.rs:53 */
+    /* Backend-only conditions with no CatError counterpart: */
+    CATNN_ERR_DEVICE = 100,             /* a HIP runtime call failed, or no GPU */
+    CATNN_ERR_UNSUPPORTED = 101,        /* op kind not executable on this backend */
+    CATNN_ERR_INVALID_ARGUMENT = 102    /* null handle / pointer, bad enum value */
+};
+
+/* Message for the last failing call on this thread ("" after success). */
+const char *catnn_hip_last_error(void);
+
+/* ------------------------------------------------------------ data types */
+/* DType tag, crates/catnn-core/src/tensor.rs:17-27.  Storage is always f32
+ * on the host, as in the reference (tensor.rs:223-229). */
+enum catnn_dtype {
+    CATNN_F32 = 0, CATNN_F16 = 1, CATNN_BF16 = 2, CATNN_FP8 = 3,
+    CATNN_FP4 = 4, CATNN_I32 = 5, CATNN_BOOL = 6
+};
+
+#define CATNN_MAX_RANK 8
+
+/* Host tensor: `Tensor { ty: TensorType { shape, dtype }, data: Vec<f32> }`
+ * (tensor.rs:181-229).  `data` may be NULL when only the type matters
+ * (IrNode.output_ty). */
+typedef struct catnn_tensor {
+    float *data;
+    int64_t dims[CATNN_MAX_RANK];
+    int32_t rank;
+    int32_t dtype;
+} catnn_tensor;
+
+/* OpenOp discriminant, crates/catnn-core/src/category/morphism.rs:19-116
+ * (declaration order). */
+enum catnn_op_kind {
+    CATNN_OP_IDENTITY = 0,
+    CATNN_OP_LINEAR = 1,        /* a = {in_features, out_features, bias} */
+    CATNN_OP_RELU = 2,
+    CATNN_OP_GELU = 3,
+    CATNN_OP_SOFTMAX = 4,       /* a = {axis} (last axis only, as cpu.rs:31) */
+    CATNN_OP_LAYER_NORM = 5,    /* a = {eps_e6} */
+    CATNN_OP_ADD = 6,
+    CATNN_OP_MUL = 7,
+    CATNN_OP_MATMUL = 8,        /* executed as Linear with param "w" */
+    CATNN_OP_TRANSPOSE = 9,     /* a = {dim0, dim1}; data copy as eval_cpu */
+    CATNN_OP_RESHAPE = 10,      /* a = {out dims...}; data copy as eval_cpu */
+    CATNN_OP_ATTENTION = 11,    /* a = {n_heads, d_model, d_head} */
+    CATNN_OP_RESIDUAL_ADD = 12,
+    CATNN_OP_EMBEDDING = 13,
+    CATNN_OP_RMS_NORM = 14,
+    CATNN_OP_GQA_ATTENTION = 15,
+    CATNN_OP_SWIGLU = 16,
+    CATNN_OP_ROUTER = 17,
+    CATNN_OP_MOE = 18,          /* a = {n_experts, top_k, hidden, intermediate} */
+    CATNN_OP_LM_HEAD = 19,
+    CATNN_OP_MLA = 20,
+    CATNN_OP_DEEPSEEK_MOE = 21,
+    CATNN_OP_MIX = 22
+};
+
+/* Attention extension: causal mask with the masking convention of
+ * moe::gqa (crates/catnn-compile/src/kernel/moe.rs:105-121).  The reference
+ * Attention op has no mask (cpu.rs:235-298); with the flag clear the backend
+ * computes exactly that. */
+#define CATNN_FLAG_CAUSAL 0x1
+
+typedef struct catnn_op {
+    int32_t kind;      /* enum catnn_op_kind */
+    int32_t flags;     /* CATNN_FLAG_* */
+    int64_t a[8];      /* the variant's fields in declaration order */
+} catnn_op;
+
+/* One entry of `IrNode.params: IndexMap<String, Tensor>` (ir.rs:22-23). */
+typedef struct catnn_param {
+    const char *port;
+    catnn_tensor value;
+} catnn_param;
+
+/* `IrNode { id, name, op, output_ty, params }` (crates/catnn-compile/src/ir.rs:17-24). */
+typedef struct catnn_node {
+    uint32_t id;
+    const char *name;
+    catnn_op op;
+    catnn_tensor output_ty;
+    const catnn_param *params;
+    int32_t n_params;
+} catnn_node;
+
+/* ------------------------------------------------------------ the arena */
+/* `BufferReq` (crates/catnn-compile/src/schedule.rs:61-70); lifetimes are
+ * inclusive logical ticks. */
+typedef struct catnn_buffer_req {
+    const char *id;
+    uint64_t bytes;
+    uint64_t live_from;
+    uint64_t live_to;
+    int32_t checkpoint;
+} catnn_buffer_req;
+
+#define CATNN_ID_CAP 128
+
+/* `ArenaAlloc` (schedule.rs:36-43). */
+typedef struct catnn_arena_alloc {
+    char id[CATNN_ID_CAP];
+    uint64_t bytes;
+    uint64_t offset;
+    uint64_t live_from;
+    uint64_t live_to;
+} catnn_arena_alloc;
+
+/* First-fit placement with aliased lifetimes; replaces `place_arena`
+ * (schedule.rs:79-116).  `out` has room for `n` entries and receives them
+ * in placement order.  Host-only (no GPU needed).  Overflow of `cap`
+ * returns CATNN_ERR_FIBRATION naming the buffer. */
+int catnn_place_arena(const catnn_buffer_req *reqs, int32_t n, uint64_t cap,
+                      catnn_arena_alloc *out);
+
+/* `arena_conflict` (schedule.rs:123-136): sets *conflict to 1 and the pair
+ * (i, j) when two simultaneously live allocations overlap, else 0. */
+int catnn_arena_conflict(const catnn_arena_alloc *allocs, int32_t n,
+                         int32_t *conflict, int32_t *i, int32_t *j);
+
+/* ------------------------------------------------------------ the graph */
+/* `IrGraph { name, nodes, edges, inputs, outputs }` (ir.rs:35-41), built on
+ * the host.  Host-only (no GPU needed). */
+typedef struct catnn_graph catnn_graph;
+
+int catnn_graph_new(const char *name, catnn_graph **out);
+int catnn_graph_free(catnn_graph *g);
+/* Copies the node, its name and its params. */
+int catnn_graph_add_node(catnn_graph *g, const catnn_node *node);
+/* `IrEdge { src, dst, src_port, dst_port }` (ir.rs:26-32).  Insertion order
+ * fixes the order of a node's inputs (`preds`, ir.rs:58-60). */
+int catnn_graph_add_edge(catnn_graph *g, uint32_t src, uint32_t dst,
+                         const char *src_port, const char *dst_port);
+int catnn_graph_add_input(catnn_graph *g, uint32_t id);
+int catnn_graph_add_output(catnn_graph *g, uint32_t id);
+/* `Realization.fusions` entry (FusionGroup, realization.rs:40-45): the named
+ * ops run as one kernel when they are placed on the same device. */
+int catnn_graph_add_fusion(catnn_graph *g, const char *const *op_names, int32_t n);
+/* Kahn order as `IrGraph::topo` (ir.rs:67-92); cycles → CATNN_ERR_WIRING. */
+int catnn_graph_topo(const catnn_graph *g, uint32_t *order, int32_t cap, int32_t *n);
+
+/* ------------------------------------------------------------ the device */
+typedef struct catnn_hip_device catnn_hip_device;
+
+int catnn_hip_device_count(int32_t *n);
+/* Opens GPU `ordinal`, creates its stream.  Fails with CATNN_ERR_DEVICE
+ * when no GPU is present: there is no CPU fallback. */
+int catnn_hip_open(int32_t ordinal, catnn_hip_device **out);
+int catnn_hip_close(catnn_hip_device *dev);
+int catnn_hip_sync(catnn_hip_device *dev);
+/* Device name and HBM size, for the MI355X region profile. */
+int catnn_hip_device_info(catnn_hip_device *dev, char *name, int32_t cap,
+                          uint64_t *hbm_bytes, int32_t *cu_count);
+
+/* One hipMalloc backing the device's buffer region.  Replaces any earlier
+ * arena (all bindings are dropped). */
+int catnn_hip_arena_reserve(catnn_hip_device *dev, uint64_t bytes);
+/* Bind `buffer_id` ("act:{node}", "param:{node}:{port}", …, as
+ * pipeline.rs:319-379) to arena[offset, offset+bytes). */
+int catnn_hip_bind(catnn_hip_device *dev, const char *buffer_id,
+                   uint64_t offset, uint64_t bytes);
+int catnn_hip_buffer_ptr(catnn_hip_device *dev, const char *buffer_id,
+                         void **dptr, uint64_t *bytes);
+int catnn_hip_upload(catnn_hip_device *dev, const char *buffer_id,
+                     const void *host, uint64_t bytes);
+int catnn_hip_download(catnn_hip_device *dev, const char *buffer_id,
+                       void *host, uint64_t bytes);
+
+/* Plain device memory outside the arena (test and bench plumbing). */
+int catnn_hip_alloc(catnn_hip_device *dev, uint64_t bytes, void **dptr);
+int catnn_hip_free(catnn_hip_device *dev, void *dptr);
+int catnn_hip_h2d(catnn_hip_device *dev, void *dst, const void *src, uint64_t bytes);
+int catnn_hip_d2h(catnn_hip_device *dev, void *dst, const void *src, uint64_t bytes);
+int catnn_hip_memset(catnn_hip_device *dev, void *dst, int32_t value, uint64_t bytes);
+
+/* Stream-ordered timer on the device's stream (hipEvent pair). */
+int catnn_hip_timer_start(catnn_hip_device *dev);
+int catnn_hip_timer_stop(catnn_hip_device *dev, float *ms);
+
+/* ---------------------------------------------------- the handler seam */
+/* Drop-in for `DeviceHandler::run_kernel` (handler.rs:34-57) with
+ * host tensors in and out: params ride inside `node` (as the reference
+ * clones them per call, coord.rs:320-323), inputs are the node's preds in
+ * edge order.  `out->data` must hold the output's numel floats; dims, rank
+ * and dtype are written.  Records KernelStart/KernelEnd events. */
+int catnn_hip_run_kernel(catnn_hip_device *dev, const catnn_node *node,
+                         const catnn_tensor *inputs, int32_t n_inputs,
+                         catnn_tensor *out);
+
+/* Device-resident variant: inputs, output and params are arena buffer ids
+ * (params bound as "param:{node.name}:{port}"; the node's params need only
+ * dims here, data may be NULL).  `in_types` gives each input's type (data
+ * ignored), as the Tensors of run_kernel do.  `fused_act` applies a
+ * following Relu (2) or Gelu (3) from a FusionGroup in the Linear epilogue;
+ * `residual_id` (or NULL) adds a following ResidualAdd's other operand in
+ * the epilogue.  Scratch (attention q/k/v, MoE permutation) comes from a
+ * per-device workspace. */
+int catnn_hip_run_node(catnn_hip_device *dev, const catnn_node *node,
+                       const char *const *in_ids, const catnn_tensor *in_types,
+                       int32_t n_in, const char *out_id, int32_t fused_act,
+                       const char *residual_id);
+
+/* ------------------------------------------------------- the program */
+/* A graph installed on a device: arena planned by catnn_place_arena over
+ * forward lifetimes (act:{node} live from its topo index to its last
+ * consumer's, params live throughout), reserved with one hipMalloc, params
+ * uploaded once.  Replaces `eval_graph_cpu` (crates/catnn-compile/src/lib.rs:48-68)
+ * for a graph placed on this device. */
+typedef struct catnn_hip_program catnn_hip_program;
+
+int catnn_hip_install(catnn_hip_device *dev, const catnn_graph *g,
+                      catnn_hip_program **out);
+int catnn_hip_program_free(catnn_hip_program *p);
+/* Host input bound to every graph input node; host output of the last
+ * output node (lib.rs:57-67). */
+int catnn_hip_forward(catnn_hip_program *p, const catnn_tensor *input,
+                      catnn_tensor *output);
+/* Same, with the input already in the program's input buffer and the
+ * output left in the output buffer (no host copies, no sync). */
+int catnn_hip_forward_resident(catnn_hip_program *p);
+/* Device buffers of the program's input and output. */
+int catnn_hip_program_io(catnn_hip_program *p, void **in_dptr, uint64_t *in_bytes,
+                         void **out_dptr, uint64_t *out_bytes);
+/* The program's arena plan (one entry per placed buffer). */
+int catnn_hip_program_arena(catnn_hip_program *p, catnn_arena_alloc *out,
+                            int32_t cap, int32_t *n, uint64_t *reserved_bytes);
+
+/* ------------------------------------------------------------- events */
+/* Sheaf events (crates/catnn-rt/src/sheaf.rs:55-79) recorded by the
+ * handler seam: times in ns from device open, checksum = FNV-1a over the
+ * output's f32 bits on KernelEnd (tensor.rs:279-288). */
+enum catnn_event_kind {
+    CATNN_EV_KERNEL_START = 0, CATNN_EV_KERNEL_END = 1,
+    CATNN_EV_TRANSFER_START = 2, CATNN_EV_TRANSFER_END = 3
+};
+typedef struct catnn_event {
+    uint64_t t_ns;
+    char op[CATNN_ID_CAP];
+    int32_t kind;
+    uint64_t checksum;
+} catnn_event;
+int catnn_hip_events(catnn_hip_device *dev, catnn_event *buf, int32_t cap, int32_t *n);
+int catnn_hip_clear_events(catnn_hip_device *dev);
+
+/* ------------------------------------------------ kernels on raw buffers */
+/* These are the kernels the seams above dispatch to, exposed on device
+ * pointers for tests and benchmarks.  All tensors are row-major f32 in
+ * device memory; they run on the device's stream and return without
+ * synchronising. */
+
+/* y[m,n] = act(x[m,k]·w[k,n] + b[n]) + r[m,n]; b and r may be NULL.
+ * Replaces cpu::linear (cpu.rs:135-184) followed by cpu::relu / cpu::gelu
+ * (cpu.rs:14-29) and cpu::add (cpu.rs:80-98).  act: 0 none, 2 relu, 3 gelu
+ * (the OpenOp discriminants). */
+int catnn_hip_linear_f32(catnn_hip_device *dev, const float *x, const float *w,
+                         const float *b, const float *r, float *y,
+                         int64_t m, int64_t k, int64_t n, int32_t act);
+
+/* Replaces cpu::relu / cpu::gelu (cpu.rs:14-29) as standalone passes. */
+int catnn_hip_act_f32(catnn_hip_device *dev, const float *x, float *y,
+                      int64_t n, int32_t act);
+/* Replaces cpu::add (cpu.rs:80-98): same-length add when nb == na, bias
+ * broadcast over the last dim (length nb) otherwise. */
+int catnn_hip_add_f32(catnn_hip_device *dev, const float *a, const float *b,
+                      float *y, int64_t na, int64_t nb);
+/* Replaces cpu::mul (cpu.rs:100-109). */
+int catnn_hip_mul_f32(catnn_hip_device *dev, const float *a, const float *b,
+                      float *y, int64_t n);
+/* Replaces cpu::layer_norm (cpu.rs:54-78). */
+int catnn_hip_layer_norm_f32(catnn_hip_device *dev, const float *x,
+                             const float *gamma, const float *beta, float *y,
+                             int64_t rows, int64_t cols, float eps);
+/* Replaces cpu::softmax_last (cpu.rs:31-52). */
+int catnn_hip_softmax_f32(catnn_hip_device *dev, const float *x, float *y,
+                          int64_t rows, int64_t cols);
+/* The score/softmax/PV core of cpu::attention (cpu.rs:252-295) on
+ * projected q, k, v [B,S,D] (head h at columns h·dh..(h+1)·dh):
+ * ctx = softmax(q·kᵀ/√dh)·v per (b,h), causal when `causal` != 0
+ * (masking as moe.rs:105-121). */
+int catnn_hip_attention_core_f32(catnn_hip_device *dev, const float *q,
+                                 const float *k, const float *v, float *ctx,
+                                 int64_t batch, int64_t seq, int64_t d_model,
+                                 int64_t n_heads, int64_t d_head, int32_t causal);
+
+/* MoE router, replaces moe::route (crates/catnn-compile/src/kernel/moe.rs:177-195)
+ * with lens::moe::topk_softmax (crates/catnn-core/src/lens/moe.rs:175-187):
+ * logits[t,e] = Σ_p x[t,p]·gate[p,e] in sequential p order without fused
+ * multiply-add (bit-equal to cpu::linear_seq, cpu.rs:115-126); idx[t,k]
+ * = k-th expert by descending logit, ties to the lower id; w[t,k] =
+ * exp(l−max)/max(Σ,1e-30).  Any output pointer may be NULL. */
+int catnn_hip_moe_route_f32(catnn_hip_device *dev, const float *x, const float *gate,
+                            int64_t tokens, int64_t hidden, int64_t n_experts,
+                            int64_t top_k, int32_t *idx, float *w, float *logits);
+
+/* Token permutation (no reference counterpart: the reference loops over
+ * tokens, moe.rs:207-221).  Stable counting sort of the flattened slots
+ * s = t·top_k + k by expert id: counts[e]; offsets[e] = Σ_{e'<e} counts[e']
+ * (length n_experts+1); slot_of_pos[offsets[e] + r] = the r-th slot, in
+ * ascending s, routed to e; pos_of_slot is its inverse. */
+int catnn_hip_moe_permute(catnn_hip_device *dev, const int32_t *idx,
+                          int64_t tokens, int64_t top_k, int64_t n_experts,
+                          int32_t *counts, int32_t *offsets,
+                          int32_t *slot_of_pos, int32_t *pos_of_slot);
+
+/* Whole MoE layer, replaces moe::moe (moe.rs:197-223):
+ * out[t] = Σ_{k ascending} w[t,k]·swiglu_{idx[t,k]}(x_t) with
+ * swiglu(x) = (silu(x·w1) ⊙ (x·w3))·w2 (moe.rs:159-174).  w1s, w3s, w2s
+ * are arrays of n_experts device pointers ([hidden,inter], [hidden,inter],
+ * [inter,hidden]).  Workspace is allocated on first use and kept per device.
+ * idx/w/counts may be NULL; if given they receive the routing. */
+int catnn_hip_moe_f32(catnn_hip_device *dev, const float *x, const float *gate,
+                      const float *const *w1s, const float *const *w3s,
+                      const float *const *w2s, int64_t tokens, int64_t hidden,
+                      int64_t intermediate, int64_t n_experts, int64_t top_k,
+                      float *out, int32_t *idx, float *w, int32_t *counts);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CATNN_HIP_H */
