@@ -1,0 +1,235 @@
+#!/usr/bin/env python3
+"""IR forward throughput of the catnn MI355X backend on one GPU.
+
+Workload: the GEMM-heavy MLP forward, fp32,
+batch 8192, 4096 → 16384 (bias, GELU) → 4096 (bias), built through the
+reference's `.catnn` spec path (parse → architecture → lower) with the
+Linear+GELU fusion that place::propose_fusions records, installed as one
+program (params and input resident in HBM) and run step after step.
+
+A step is one forward of the whole graph: two launches of the fp32 MFMA
+GEMM kernel (fc1 with the bias+GELU epilogue, fc2 with the bias
+epilogue).  Reported:
+  * value       — algorithmic GFLOP/s of the step (2·M·K·N per Linear);
+  * roofline    — that GEMM kernel's algorithmic TFLOP/s per launch over its
+                  average launch duration, timed with hipEvents on the
+                  program's stream inside the timed region, against the
+                  157.3 TFLOP/s dense fp32 MFMA peak;
+  * cpu_baseline — the oracle's restatement of the reference CPU path
+                  (cpu::linear with OpenMP over rows where the reference uses
+                  Rayon, then cpu::gelu and the bias pass) on a row subset of
+                  the same inputs, timed on this host;
+  * secondary   — the same measurement for the MoE layer (config 4,
+                  tokens/s) and the pre-LN transformer block (config 3).
+Only one GPU is used: --gpus above 1 exits with a message.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "cat-nn-compiler_amd"))
+
+FP32_MFMA_PEAK_TFLOPS = 157.3
+HBM_PEAK_GBS = 8000.0
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def time_program(dev, prog, x, steps, warmup):
+    """Upload x, run `warmup` untimed forwards, then time `steps` forwards
+    with hipEvents on the program's stream (synchronised on both sides)."""
+    prog.forward(x)  # uploads the input into the program's input buffer
+    for _ in range(warmup):
+        prog.forward_resident()
+    dev.sync()
+    prog.profile(True)
+    dev.sync()
+    t0 = time.perf_counter()
+    dev.timer_start()
+    for _ in range(steps):
+        prog.forward_resident()
+    ms = dev.timer_stop()
+    dev.sync()
+    wall = time.perf_counter() - t0
+    timings = prog.timings()
+    prog.profile(False)
+    return ms / steps, wall, timings
+
+
+def cpu_baseline_mlp(wl, target_s):
+    """Oracle restatement of the reference CPU path on a row subset."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import numpy as np
+    import oracle
+
+    x = wl.x.numpy()
+    p1, p2 = wl.graph.nodes[1].params, wl.graph.nodes[3].params
+    w1, b1, w2, b2 = (p1["w"].numpy(), p1["b"].numpy(), p2["w"].numpy(), p2["b"].numpy())
+    d, hidden = w1.shape
+
+    def run(rows):
+        t0 = time.perf_counter()
+        h = oracle.gelu(oracle.linear(x[:rows], w1, b1))
+        oracle.linear(h, w2, b2)
+        return time.perf_counter() - t0
+
+    cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    probe_rows = max(2, min(cores, 16))
+    t = run(probe_rows)
+    rows = int(min(x.shape[0], max(probe_rows, probe_rows * target_s / max(t, 1e-3))))
+    rows = max(probe_rows, (rows // probe_rows) * probe_rows)
+    t = run(rows)
+    flops = 2 * rows * (d * hidden + hidden * d)
+    return {"value": round(flops / t / 1e9, 3), "unit": "GFLOP/s", "cores": cores, "kind": "port",
+            "sample": f"{rows} of {x.shape[0]} rows of the config-2 forward (fc1+bias, GELU, "
+                      f"fc2+bias) in {t:.1f} s; OpenMP over rows where the reference uses Rayon"}
+
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemm_f32_config2_hbm_traffic.txt")
+COPY_FLOATS = 128 << 20  # 512 MiB read + 512 MiB written by the calibration copy
+
+
+def measured_traffic():
+    """HBM bytes per GEMM launch from the committed rocprofv3 --pmc summary
+    (FETCH_SIZE and WRITE_SIZE scaled by a copy kernel of known size)."""
+    try:
+        for line in open(TRAFFIC_FILE):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
+def pmc_probe(which):
+    """Kernel sequence for the rocprofv3 --pmc runs: a plain copy kernel
+    (act_f32 with no activation: reads and writes COPY_FLOATS·4 bytes),
+    then the workload's forwards."""
+    import catnn_amd
+    from catnn_amd import configs
+    from catnn_amd import device as D
+
+    dev = catnn_amd.Device(0)
+    a, b = dev.alloc(COPY_FLOATS * 4), dev.alloc(COPY_FLOATS * 4)
+    a.zero()
+    for i in range(3):
+        D.act(dev, a, b, COPY_FLOATS, 0)
+        dev.sync()
+        log(f"copy {i} done")
+    a.free()
+    b.free()
+    builders = {"config2": configs.config2, "config3": configs.config3, "config4": configs.config4}
+    for name in (builders if which == "all" else [which]):
+        wl = builders[name]()
+        prog = catnn_amd.Program(dev, wl.graph)
+        prog.forward(wl.x)
+        for _ in range(2):
+            prog.forward_resident()
+        dev.sync()
+        log(f"{name}: 3 forwards done")
+        prog.free()
+    dev.close()
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--pmc-probe", choices=["config2", "config3", "config4", "all"],
+                    help="run the copy calibration and the workload for rocprofv3 --pmc, then exit")
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+                    help="target CPU time of the cpu_baseline sample")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-secondary", action="store_true")
+    args = ap.parse_args()
+    if args.pmc_probe:
+        pmc_probe(args.pmc_probe)
+        return
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: this build runs on a single MI355X "
+              "(no collectives); run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import catnn_amd
+    from catnn_amd import configs
+
+    dev = catnn_amd.Device(0)
+    name, hbm, cus = dev.info()
+    log(f"device {name}, {hbm / 2**30:.0f} GiB HBM, {cus} CUs")
+
+    wl = configs.config2()
+    log("config 2 built")
+    prog = catnn_amd.Program(dev, wl.graph)
+    ms, wall, timings = time_program(dev, prog, wl.x, args.steps, args.warmup)
+    value = wl.flops / (ms / 1e3) / 1e9
+    gemm = [t for t in timings if t[1] == "linear"]
+    launches = sum(t[2] for t in gemm)
+    gemm_ms = sum(t[3] for t in gemm) / max(launches, 1)
+    M, K, N = 8192, 4096, 16384
+    per_launch = 2 * M * K * N  # both Linear layers do the same FLOPs
+    achieved = per_launch / (gemm_ms / 1e3) / 1e12
+    log(f"config 2: {ms:.3f} ms/step, {value:.0f} GFLOP/s; GEMM {gemm_ms:.3f} ms/launch "
+        f"({achieved:.1f} TFLOP/s); steps {[(t[0], round(t[3] / max(t[2], 1), 3)) for t in timings]}")
+    prog.free()
+
+    result = {
+        "metric": "IR fwd GFLOP/s",
+        "value": round(value, 1),
+        "unit": "GFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded SplitMix64/Box-Muller, N(0,1/fan_in) weights)",
+        "config": {"workload": "config2: MLP forward 8192x(4096->16384->4096), bias+GELU, fp32, "
+                               "IR program via .catnn spec path",
+                   "batch": M, "layers": [K, N, K], "activation": "gelu"},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2),
+                     "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4),
+                     "traffic": measured_traffic(),
+                     "kernel": "gemm_plain_kernel<128,128,16> (fp32 MFMA 32x32x2)",
+                     "per_launch_flop": per_launch, "avg_launch_ms": round(gemm_ms, 4)},
+    }
+
+    if not args.no_secondary:
+        sec = {}
+        w4 = configs.config4()
+        p4 = catnn_amd.Program(dev, w4.graph)
+        ms4, _, t4 = time_program(dev, p4, w4.x, max(3, args.steps // 2), 2)
+        sec["moe_layer_config4"] = {
+            "tokens_per_s": round(w4.tokens / (ms4 / 1e3)), "ms_per_step": round(ms4, 4),
+            "GFLOP_per_s": round(w4.flops / (ms4 / 1e3) / 1e9, 1),
+            "mfma_frac": round(w4.flops / (ms4 / 1e3) / 1e12 / FP32_MFMA_PEAK_TFLOPS, 4)}
+        p4.free()
+        del w4
+        log(f"config 4: {ms4:.3f} ms/step")
+        w3 = configs.config3()
+        p3 = catnn_amd.Program(dev, w3.graph)
+        ms3, _, t3 = time_program(dev, p3, w3.x, max(3, args.steps // 2), 2)
+        sec["prenorm_block_config3"] = {
+            "ms_per_step": round(ms3, 4), "GFLOP_per_s": round(w3.flops / (ms3 / 1e3) / 1e9, 1),
+            "steps_ms": {t[0]: round(t[3] / max(t[2], 1), 4) for t in t3}}
+        p3.free()
+        log(f"config 3: {ms3:.3f} ms/step")
+        result["secondary"] = sec
+
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline_mlp(wl, args.cpu_seconds)
+        log(f"cpu baseline: {result['cpu_baseline']}")
+    dev.close()
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

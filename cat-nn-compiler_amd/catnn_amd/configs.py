@@ -1,0 +1,168 @@
+"""The benchmark configurations as IR graphs with seeded synthetic weights.
+
+  1  MLP 256×(784→512→512→10), ReLU — the reference's `.catnn` spec path
+     (parse_catnn → to_architecture → lower_architecture), weights
+     N(0, 2/fan_in), biases 0, input U(−1, 1).
+  2  MLP 8192×(4096→16384→4096), GELU — same path, weights N(0, 1/fan_in),
+     biases N(0, 0.01), input N(0, 1).
+  3  Pre-LN transformer block [8,1024,1024], 16 heads × 64, causal, FFN ×4
+     with GELU, two residual adds — an explicit IrGraph (chain lowering
+     cannot express the skips, lower.rs:38-55).  Weights N(0, 0.02),
+     biases N(0, 0.02), γ = 1, β = 0, input N(0, 1).
+  4  MoE layer: 16384 tokens × 1024, 8 SwiGLU experts 1024→3584→1024,
+     top-2; gate N(0, 0.5), experts N(0, 0.02), input N(0, 1).
+
+N(0, v) gives the variance.  Tensor i of config c is drawn from the
+SplitMix64 stream seeded 1000·c + i.  Every builder takes smaller shapes
+for parity tests.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import List, Optional
+
+import numpy as np
+
+from . import synth
+from .ir import FusionGroup, IrGraph, IrNode, OpenOp, Tensor, TensorType
+from .spec import lower_architecture, parse_catnn, propose_fusions, to_architecture
+
+
+@dataclass
+class Workload:
+    name: str
+    graph: IrGraph
+    x: Tensor
+    flops: int            # algorithmic FLOPs of one forward
+    min_bytes: int        # compulsory HBM traffic of one forward
+    tokens: int
+
+
+def _seq(config: int):
+    i = 0
+    while True:
+        yield 1000 * config + i
+        i += 1
+
+
+def mlp_text(name: str, batch: int, dims: List[int], act: str) -> str:
+    lines = [f"network {name} batch {batch}"]
+    for li in range(len(dims) - 1):
+        lines.append(f"linear fc{li + 1} {dims[li]} {dims[li + 1]}")
+        if li + 2 < len(dims):
+            lines.append(f"{act} act{li + 1}")
+    lines.append("compose sequential")
+    return "\n".join(lines) + "\n"
+
+
+def _mlp(config: int, name: str, batch: int, dims: List[int], act: str, w_var_num: float,
+         bias_var: float, x_kind: str) -> Workload:
+    arch = to_architecture(parse_catnn(mlp_text(name, batch, dims, act)))
+    g = lower_architecture(arch)
+    seeds = _seq(config)
+    for node in g.nodes.values():
+        if node.op.kind != "linear":
+            continue
+        fan_in, fan_out = node.op.fields[0], node.op.fields[1]
+        node.params["w"] = Tensor(TensorType.f32([fan_in, fan_out]),
+                                  synth.normal(fan_in * fan_out, next(seeds), w_var_num / fan_in))
+        b = (synth.normal(fan_out, next(seeds), bias_var) if bias_var > 0
+             else np.zeros(fan_out, np.float32))
+        node.params["b"] = Tensor(TensorType.f32([fan_out]), b)
+    g.fusions = propose_fusions(g)
+    n_x = batch * dims[0]
+    xs = (synth.uniform(n_x, next(seeds), -1.0, 1.0) if x_kind == "uniform"
+          else synth.normal(n_x, next(seeds), 1.0))
+    x = Tensor(TensorType.f32([batch, dims[0]]), xs)
+    flops = sum(2 * batch * dims[i] * dims[i + 1] for i in range(len(dims) - 1))
+    w_bytes = sum(4 * (dims[i] * dims[i + 1] + dims[i + 1]) for i in range(len(dims) - 1))
+    act_bytes = 4 * batch * (dims[0] + dims[-1] + 2 * sum(dims[1:-1]))
+    return Workload(name, g, x, flops, w_bytes + act_bytes, batch)
+
+
+def config1(batch: int = 256) -> Workload:
+    return _mlp(1, "mlp", batch, [784, 512, 512, 10], "relu", 2.0, 0.0, "uniform")
+
+
+def config2(batch: int = 8192, d: int = 4096, hidden: int = 16384) -> Workload:
+    return _mlp(2, "mlp_gemm", batch, [d, hidden, d], "gelu", 1.0, 0.01, "normal")
+
+
+def attention_flops(batch: int, seq: int, heads: int, d_head: int, causal: bool) -> int:
+    """QKᵀ and PV: 2·dh per (query, key) pair attended, each."""
+    pairs = seq * (seq + 1) // 2 if causal else seq * seq
+    return 2 * 2 * batch * heads * pairs * d_head
+
+
+def config3(batch: int = 8, seq: int = 1024, d: int = 1024, heads: int = 16, ffn: int = 4096,
+            causal: bool = True) -> Workload:
+    seeds = _seq(3)
+    var = 0.02
+    T = batch * seq
+    ty = TensorType.f32([batch, seq, d])
+
+    def w(shape):
+        n = int(np.prod(shape))
+        return Tensor(TensorType.f32(shape), synth.normal(n, next(seeds), var))
+
+    g = IrGraph("prenorm_block")
+    ones = lambda n: Tensor(TensorType.f32([n]), np.ones(n, np.float32))
+    zeros = lambda n: Tensor(TensorType.f32([n]), np.zeros(n, np.float32))
+    g.add_node(IrNode(0, "block.in", OpenOp.identity(), ty))
+    g.add_node(IrNode(1, "ln1", OpenOp.layer_norm(1), ty, {"gamma": ones(d), "beta": zeros(d)}))
+    g.add_node(IrNode(2, "attn", OpenOp.attention(heads, d, d // heads, causal), ty,
+                      {"wq": w([d, d]), "wk": w([d, d]), "wv": w([d, d]), "wo": w([d, d])}))
+    g.add_node(IrNode(3, "res1", OpenOp.residual_add(), ty))
+    g.add_node(IrNode(4, "ln2", OpenOp.layer_norm(1), ty, {"gamma": ones(d), "beta": zeros(d)}))
+    g.add_node(IrNode(5, "ff1", OpenOp.linear(d, ffn, True), TensorType.f32([batch, seq, ffn]),
+                      {"w": w([d, ffn]), "b": w([ffn])}))
+    g.add_node(IrNode(6, "ff_act", OpenOp.gelu(), TensorType.f32([batch, seq, ffn])))
+    g.add_node(IrNode(7, "ff2", OpenOp.linear(ffn, d, True), ty, {"w": w([ffn, d]), "b": w([d])}))
+    g.add_node(IrNode(8, "res2", OpenOp.residual_add(), ty))
+    for s, t in [(0, 1), (1, 2), (0, 3), (2, 3), (3, 4), (4, 5), (5, 6), (6, 7), (3, 8), (7, 8)]:
+        g.add_edge(s, t)
+    g.inputs.append(0)
+    g.outputs.append(8)
+    g.fusions = propose_fusions(g)
+    x = Tensor(ty, synth.normal(T * d, next(seeds), 1.0))
+    dh = d // heads
+    flops = (2 * T * d * 3 * d + attention_flops(batch, seq, heads, dh, causal) + 2 * T * d * d
+             + 2 * 2 * T * d * ffn)
+    w_bytes = 4 * (4 * d * d + 2 * d * ffn + ffn + d + 4 * d)
+    act_bytes = 4 * T * (2 * d + 2 * d + 3 * d + d + d + d + ffn + ffn + d + d)
+    return Workload("prenorm_block", g, x, flops, w_bytes + act_bytes, T)
+
+
+def moe_weights(n_experts: int, hidden: int, inter: int, seeds, gate_var=0.5, w_var=0.02):
+    gate = synth.normal(hidden * n_experts, next(seeds), gate_var).reshape(hidden, n_experts)
+    w1 = np.empty((n_experts, hidden, inter), np.float32)
+    w3 = np.empty((n_experts, hidden, inter), np.float32)
+    w2 = np.empty((n_experts, inter, hidden), np.float32)
+    for e in range(n_experts):
+        w1[e] = synth.normal(hidden * inter, next(seeds), w_var).reshape(hidden, inter)
+        w3[e] = synth.normal(hidden * inter, next(seeds), w_var).reshape(hidden, inter)
+        w2[e] = synth.normal(inter * hidden, next(seeds), w_var).reshape(inter, hidden)
+    return gate, w1, w3, w2
+
+
+def config4(batch: int = 8, seq: int = 2048, d: int = 1024, n_experts: int = 8, top_k: int = 2,
+            inter: int = 3584) -> Workload:
+    seeds = _seq(4)
+    T = batch * seq
+    ty = TensorType.f32([batch, seq, d])
+    gate, w1, w3, w2 = moe_weights(n_experts, d, inter, seeds)
+    params = {"gate": Tensor(TensorType.f32([d, n_experts]), gate)}
+    for e in range(n_experts):
+        params[f"e{e}.w1"] = Tensor(TensorType.f32([d, inter]), w1[e])
+        params[f"e{e}.w3"] = Tensor(TensorType.f32([d, inter]), w3[e])
+        params[f"e{e}.w2"] = Tensor(TensorType.f32([inter, d]), w2[e])
+    g = IrGraph("moe_layer")
+    g.add_node(IrNode(0, "moe.in", OpenOp.identity(), ty))
+    g.add_node(IrNode(1, "moe", OpenOp.moe(n_experts, top_k, d, inter), ty, params))
+    g.add_edge(0, 1)
+    g.inputs.append(0)
+    g.outputs.append(1)
+    x = Tensor(ty, synth.normal(T * d, next(seeds), 1.0))
+    flops = 2 * T * d * n_experts + T * top_k * 2 * 3 * d * inter
+    min_bytes = 4 * (2 * T * d + d * n_experts + 3 * n_experts * d * inter)
+    return Workload("moe_layer", g, x, flops, min_bytes, T)

@@ -409,6 +409,13 @@ struct catnn_hip_program {
     std::map<std::string, float *> ptr;  // buffer id → device pointer
     std::vector<uint32_t> input_vals;
     uint32_t output_val = 0;
+    // Per-step timing (catnn_hip_program_profile).
+    bool profiling = false;
+    std::vector<size_t> exec_steps;                  // indices of non-input steps
+    std::vector<std::vector<hipEvent_t>> pending;    // one event set per timed forward
+    std::vector<std::vector<hipEvent_t>> event_pool;
+    std::vector<double> total_ms;
+    std::vector<int32_t> calls;
 };
 
 namespace catnn {
@@ -498,6 +505,10 @@ static void build_program(catnn_hip_program &p) {
     }
     CATNN_REQUIRE(p.dims.count(final_out), CATNN_ERR_WIRING, "graph output is not materialised");
     p.output_val = final_out;
+    for (size_t i = 0; i < p.steps.size(); ++i)
+        if (!p.steps[i].is_input) p.exec_steps.push_back(i);
+    p.total_ms.assign(p.exec_steps.size(), 0.0);
+    p.calls.assign(p.exec_steps.size(), 0);
 }
 
 static void plan_and_upload(catnn_hip_program &p) {
@@ -573,6 +584,21 @@ static void plan_and_upload(catnn_hip_program &p) {
 
 static void run_program(catnn_hip_program &p) {
     const catnn_graph &g = p.graph;
+    std::vector<hipEvent_t> *evs = nullptr;
+    if (p.profiling) {
+        std::vector<hipEvent_t> set;
+        if (!p.event_pool.empty()) {
+            set = std::move(p.event_pool.back());
+            p.event_pool.pop_back();
+        } else {
+            set.resize(p.exec_steps.size() + 1);
+            for (auto &e : set) CATNN_HIP(hipEventCreate(&e));
+        }
+        p.pending.push_back(std::move(set));
+        evs = &p.pending.back();
+        CATNN_HIP(hipEventRecord((*evs)[0], p.dev->stream));
+    }
+    size_t executed = 0;
     for (const Step &st : p.steps) {
         if (st.is_input) continue;
         const Node &n = g.node(st.node);
@@ -595,7 +621,31 @@ static void run_program(catnn_hip_program &p) {
             if (it != p.ptr.end()) a.packed_qkv = it->second;
         }
         exec_node(p.dev, n, a);
+        ++executed;
+        if (evs) CATNN_HIP(hipEventRecord((*evs)[executed], p.dev->stream));
     }
+}
+
+static void collect_timings(catnn_hip_program &p) {
+    for (auto &set : p.pending) {
+        CATNN_HIP(hipEventSynchronize(set.back()));
+        for (size_t i = 0; i + 1 < set.size(); ++i) {
+            float ms = 0.f;
+            CATNN_HIP(hipEventElapsedTime(&ms, set[i], set[i + 1]));
+            p.total_ms[i] += ms;
+            p.calls[i] += 1;
+        }
+        p.event_pool.push_back(std::move(set));
+    }
+    p.pending.clear();
+}
+
+static void destroy_events(catnn_hip_program &p) {
+    for (auto *sets : {&p.pending, &p.event_pool})
+        for (auto &set : *sets)
+            for (hipEvent_t e : set) (void)hipEventDestroy(e);
+    p.pending.clear();
+    p.event_pool.clear();
 }
 
 }  // namespace catnn
@@ -804,8 +854,38 @@ int catnn_hip_program_free(catnn_hip_program *p) {
         if (!p) return;
         (void)hipSetDevice(p->dev->ordinal);
         (void)hipStreamSynchronize(p->dev->stream);
+        destroy_events(*p);
         if (p->base) (void)hipFree(p->base);
         delete p;
+    });
+}
+
+int catnn_hip_program_profile(catnn_hip_program *p, int32_t enable) {
+    return guard([&] {
+        CATNN_REQUIRE(p, CATNN_ERR_INVALID_ARGUMENT, "null program");
+        require_device(p->dev);
+        collect_timings(*p);
+        p->profiling = enable != 0;
+        std::fill(p->total_ms.begin(), p->total_ms.end(), 0.0);
+        std::fill(p->calls.begin(), p->calls.end(), 0);
+    });
+}
+
+int catnn_hip_program_timings(catnn_hip_program *p, catnn_step_timing *out, int32_t cap,
+                              int32_t *n) {
+    return guard([&] {
+        CATNN_REQUIRE(p && n, CATNN_ERR_INVALID_ARGUMENT, "null argument");
+        require_device(p->dev);
+        collect_timings(*p);
+        *n = (int32_t)p->exec_steps.size();
+        for (int32_t i = 0; out && i < cap && i < *n; ++i) {
+            const Node &node = p->graph.node(p->steps[p->exec_steps[(size_t)i]].node);
+            std::memset(out[i].name, 0, CATNN_ID_CAP);
+            std::strncpy(out[i].name, node.name.c_str(), CATNN_ID_CAP - 1);
+            out[i].kind = node.op.kind;
+            out[i].calls = p->calls[(size_t)i];
+            out[i].total_ms = p->total_ms[(size_t)i];
+        }
     });
 }
 

@@ -80,6 +80,29 @@ extern "C" {
 
 const char *catnn_hip_last_error(void) { return g_last_error.c_str(); }
 
+// Tensor::lcg, crates/catnn-core/src/tensor.rs:259-268: state = max(seed, 1);
+// per element state = state·6364136223846793005 + 1 (mod 2^64), value =
+// f32(u32(state >> 33)) / f32(u32::MAX) · 2 − 1.
+int catnn_tensor_lcg(uint64_t seed, float *out, int64_t n) {
+    return guard([&] {
+        CATNN_REQUIRE(n >= 0 && (out || n == 0), CATNN_ERR_INVALID_ARGUMENT, "lcg: null output");
+        uint64_t state = seed < 1 ? 1 : seed;
+        for (int64_t i = 0; i < n; ++i) {
+            state = state * 6364136223846793005ull + 1ull;
+            const float unit = (float)(uint32_t)(state >> 33) / (float)UINT32_MAX;
+            out[i] = unit * 2.0f - 1.0f;
+        }
+    });
+}
+
+int catnn_tensor_checksum(const float *data, int64_t n, uint64_t *out) {
+    return guard([&] {
+        CATNN_REQUIRE(out && n >= 0 && (data || n == 0), CATNN_ERR_INVALID_ARGUMENT,
+                      "checksum: null argument");
+        *out = fnv1a_f32(data, (uint64_t)n);
+    });
+}
+
 int catnn_hip_device_count(int32_t *n) {
     return guard([&] {
         CATNN_REQUIRE(n, CATNN_ERR_INVALID_ARGUMENT, "null out pointer");

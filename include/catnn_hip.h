@@ -121,6 +121,14 @@ typedef struct catnn_op {
     int64_t a[8];      /* the variant's fields in declaration order */
 } catnn_op;
 
+/* `Tensor::lcg(ty, seed)` (crates/catnn-core/src/tensor.rs:259-268): the
+ * deterministic fill the reference uses for every materialised param
+ * (lower.rs:117-127) and test input.  Host-only. */
+int catnn_tensor_lcg(uint64_t seed, float *out, int64_t n);
+/* `Tensor::checksum` (tensor.rs:279-288): FNV-1a over the f32 bit patterns.
+ * Host-only. */
+int catnn_tensor_checksum(const float *data, int64_t n, uint64_t *out);
+
 /* One entry of `IrNode.params: IndexMap<String, Tensor>` (ir.rs:22-23). */
 typedef struct catnn_param {
     const char *port;
@@ -277,6 +285,23 @@ int catnn_hip_program_io(catnn_hip_program *p, void **in_dptr, uint64_t *in_byte
 /* The program's arena plan (one entry per placed buffer). */
 int catnn_hip_program_arena(catnn_hip_program *p, catnn_arena_alloc *out,
                             int32_t cap, int32_t *n, uint64_t *reserved_bytes);
+
+/* Per-step device timing: while enabled, every forward records a hipEvent
+ * before each executed step and after the last, on the program's stream
+ * (no extra synchronisation).  `catnn_hip_program_timings` waits for the
+ * recorded forwards and returns, per step, its node name, the number of
+ * timed calls and the summed device milliseconds.  Enabling resets the
+ * sums.  (The reference's note_kernel, handler.rs:61-79, records host
+ * wall-clock spans; these are the device's.) */
+typedef struct catnn_step_timing {
+    char name[CATNN_ID_CAP];
+    int32_t kind;       /* enum catnn_op_kind of the executed node */
+    int32_t calls;
+    double total_ms;
+} catnn_step_timing;
+int catnn_hip_program_profile(catnn_hip_program *p, int32_t enable);
+int catnn_hip_program_timings(catnn_hip_program *p, catnn_step_timing *out,
+                              int32_t cap, int32_t *n);
 
 /* ------------------------------------------------------------- events */
 /* Sheaf events (crates/catnn-rt/src/sheaf.rs:55-79) recorded by the

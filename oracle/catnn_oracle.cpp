@@ -1,0 +1,508 @@
+// catnn oracle — TEST INFRASTRUCTURE ONLY.
+//
+// A CPU restatement of the reference's CPU kernels and naïve reference
+// (dkarapetyan-afk/cat-nn-compiler, Rust), used by tests/, by
+// __graft_entry__.smoke() and by bench.py's cpu_baseline leg as the checker
+// and the timed CPU path.  Nothing in the product links or calls it.
+//
+// Each function follows the cited reference loop nest.  Built with
+// -ffp-contract=off because Rust does not contract a·b + c into a fused
+// multiply-add; f32 exp/tanh/sqrt come from the C library, as Rust's f32
+// methods do on Linux.  OpenMP parallelises exactly the loops the reference
+// runs under Rayon (row loops of cpu::linear, softmax_last, layer_norm);
+// everything else is sequential, as in the reference.
+//
+// Parity status per function (how each is pinned; see tests/test_oracle.py):
+//   lcg, checksum                — reference test tensor.rs:310-315 + the
+//                                  published LCG/FNV-1a definitions (brute
+//                                  force in Python integers).
+//   relu, gelu, softmax_last,
+//   layer_norm, add, mul         — known answers (cpu.rs:318-322), library
+//                                  routines in float64 (torch/scipy), invariants.
+//   matmul_seq / linear_seq      — bit-exact against a float32 sequential sum
+//                                  done element by element in numpy; float64
+//                                  matmul within 1e-6.
+//   linear (f32x8 lane order)    — float64 matmul within 1e-6; the exact low
+//                                  bits depend on `wide` 1.7.1's reduce_add
+//                                  order and are parity unpinned at the bit
+//                                  level (tolerance only, as the reference's
+//                                  own test lib.rs:99-107).
+//   attention (+causal)          — torch float64 scaled_dot_product_attention.
+//   topk_softmax                 — known answer lens/moe.rs:208-213, stable
+//                                  argsort brute force.  NaN logits: parity
+//                                  unpinned (Rust's sort with a non-total
+//                                  comparator is not reproduced).
+//   route / swiglu / moe         — float64 dense evaluation, brute force.
+//   moe_permute                  — build-defined order; bijection and
+//                                  histogram invariants, brute force.
+//   place_arena / arena_conflict — reference tests schedule.rs:479-498 and
+//                                  invariants (no conflicts, cap respected).
+#include <algorithm>
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+#include <numeric>
+#include <string>
+#include <vector>
+
+extern "C" {
+
+// ------------------------------------------------------------- tensor.rs
+
+// Tensor::lcg, crates/catnn-core/src/tensor.rs:259-268.
+void orc_lcg(uint64_t seed, float *out, int64_t n) {
+    uint64_t state = seed < 1 ? 1 : seed;
+    for (int64_t i = 0; i < n; ++i) {
+        state = state * 6364136223846793005ull + 1ull;
+        const float unit = (float)(uint32_t)(state >> 33) / (float)UINT32_MAX;
+        out[i] = unit * 2.0f - 1.0f;
+    }
+}
+
+// Tensor::checksum, tensor.rs:279-288.
+uint64_t orc_checksum(const float *x, int64_t n) {
+    uint64_t h = 0xcbf29ce484222325ull;
+    for (int64_t i = 0; i < n; ++i) {
+        uint32_t bits;
+        std::memcpy(&bits, x + i, 4);
+        h ^= (uint64_t)bits;
+        h *= 0x100000001b3ull;
+    }
+    return h;
+}
+
+// Tensor::max_abs_diff, tensor.rs:270-277.
+float orc_max_abs_diff(const float *a, const float *b, int64_t n) {
+    float m = 0.0f;
+    for (int64_t i = 0; i < n; ++i) m = std::fmax(m, std::fabs(a[i] - b[i]));
+    return m;
+}
+
+// ---------------------------------------------------------------- cpu.rs
+
+// cpu::relu, crates/catnn-compile/src/kernel/cpu.rs:14-18 (f32::max).
+void orc_relu(const float *x, float *y, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) y[i] = std::fmax(x[i], 0.0f);
+}
+
+// cpu::gelu, cpu.rs:20-29 (reference::gelu, reference.rs:17-24, is the same).
+void orc_gelu(const float *x, float *y, int64_t n) {
+    const float c = std::sqrt(2.0f / (float)M_PI);
+    for (int64_t i = 0; i < n; ++i) {
+        const float z = x[i];
+        const float inner = c * (z + 0.044715f * z * z * z);
+        y[i] = 0.5f * z * (1.0f + std::tanh(inner));
+    }
+}
+
+// One row of cpu::softmax_last, cpu.rs:39-50.
+static void softmax_row(const float *in, float *out, int64_t last) {
+    float mx = -INFINITY;
+    for (int64_t j = 0; j < last; ++j) mx = std::fmax(mx, in[j]);
+    float sum = 0.0f;
+    for (int64_t j = 0; j < last; ++j) {
+        out[j] = std::exp(in[j] - mx);
+        sum += out[j];
+    }
+    const float inv = 1.0f / std::fmax(sum, 1e-30f);
+    for (int64_t j = 0; j < last; ++j) out[j] *= inv;
+}
+
+// cpu::softmax_last, cpu.rs:31-52 (Rayon over rows).
+void orc_softmax_last(const float *x, float *y, int64_t rows, int64_t last) {
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < rows; ++r) softmax_row(x + r * last, y + r * last, last);
+}
+
+// reference::softmax_last, reference.rs:26-42 (sequential, same formula).
+void orc_ref_softmax_last(const float *x, float *y, int64_t rows, int64_t last) {
+    for (int64_t r = 0; r < rows; ++r) softmax_row(x + r * last, y + r * last, last);
+}
+
+// One row of cpu::layer_norm, cpu.rs:61-76: mean = Σx/n, var = Σ(x−mean)²/n,
+// inv = 1/sqrt(var + eps), y = (x − mean)·inv·γ + β.
+static void layer_norm_row(const float *in, const float *g, const float *b, float *out,
+                           int64_t last, float eps) {
+    const float n = (float)last;
+    float s = 0.0f;
+    for (int64_t i = 0; i < last; ++i) s += in[i];
+    const float mean = s / n;
+    float q = 0.0f;
+    for (int64_t i = 0; i < last; ++i) {
+        const float d = in[i] - mean;
+        q += d * d;
+    }
+    const float var = q / n;
+    const float inv = 1.0f / std::sqrt(var + eps);
+    for (int64_t i = 0; i < last; ++i) out[i] = (in[i] - mean) * inv * g[i] + b[i];
+}
+
+// cpu::layer_norm, cpu.rs:54-78 (Rayon over rows).
+void orc_layer_norm(const float *x, const float *g, const float *b, float *y, int64_t rows,
+                    int64_t last, float eps) {
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < rows; ++r) layer_norm_row(x + r * last, g, b, y + r * last, last, eps);
+}
+
+// reference::layer_norm, reference.rs:44-57 (sequential).
+void orc_ref_layer_norm(const float *x, const float *g, const float *b, float *y, int64_t rows,
+                        int64_t last, float eps) {
+    for (int64_t r = 0; r < rows; ++r) layer_norm_row(x + r * last, g, b, y + r * last, last, eps);
+}
+
+// cpu::add, cpu.rs:80-98.  Returns 0, or 2 (ShapeMismatch) when b is neither
+// the same length nor the last dim.
+int orc_add(const float *a, int64_t na, const float *b, int64_t nb, int64_t last, float *y) {
+    if (na == nb) {
+        for (int64_t i = 0; i < na; ++i) y[i] = a[i] + b[i];
+        return 0;
+    }
+    if (nb == last && last > 0) {
+        for (int64_t i = 0; i < na; ++i) y[i] = a[i] + b[i % last];
+        return 0;
+    }
+    return 2;
+}
+
+// cpu::mul, cpu.rs:100-109.
+int orc_mul(const float *a, const float *b, float *y, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) y[i] = a[i] * b[i];
+    return 0;
+}
+
+// cpu::matmul_mk_kn_seq, cpu.rs:115-126: s = 0; s += a[i,p]·b[p,j], p ascending.
+void orc_matmul_seq(const float *a, const float *b, float *c, int64_t m, int64_t k, int64_t n) {
+    for (int64_t i = 0; i < m; ++i) {
+        const float *ai = a + i * k;
+        for (int64_t j = 0; j < n; ++j) {
+            float s = 0.0f;
+            for (int64_t p = 0; p < k; ++p) s += ai[p] * b[p * n + j];
+            c[i * n + j] = s;
+        }
+    }
+}
+
+// Bias pass of linear_inner, cpu.rs:173-182.
+static void add_bias(float *y, const float *bias, int64_t m, int64_t n) {
+    if (!bias) return;
+    for (int64_t r = 0; r < m; ++r)
+        for (int64_t j = 0; j < n; ++j) y[r * n + j] += bias[j];
+}
+
+// cpu::linear_seq, cpu.rs:128-132 → linear_inner(parallel = false).
+void orc_linear_seq(const float *x, const float *w, const float *bias, float *y, int64_t m,
+                    int64_t k, int64_t n) {
+    orc_matmul_seq(x, w, y, m, k, n);
+    add_bias(y, bias, m, n);
+}
+
+// cpu::dot_row, cpu.rs:199-232: eight lane accumulators over p in steps of
+// 8 (lane l accumulates a[p+l]·b[(p+l)·n+j], multiply then add), the lanes
+// reduced as wide::f32x8::reduce_add — here (l0+l4, l1+l5, l2+l6, l3+l7),
+// then pairs (0+2, 1+3), then the final add — and a scalar tail.
+static float dot_row(const float *a, const float *b, int64_t k, int64_t n, int64_t j) {
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    int64_t p = 0;
+    for (; p + 8 <= k; p += 8)
+        for (int l = 0; l < 8; ++l) acc[l] += a[p + l] * b[(p + l) * n + j];
+    const float s4[4] = {acc[0] + acc[4], acc[1] + acc[5], acc[2] + acc[6], acc[3] + acc[7]};
+    const float s2[2] = {s4[0] + s4[2], s4[1] + s4[3]};
+    float s = s2[0] + s2[1];
+    for (; p < k; ++p) s += a[p] * b[p * n + j];
+    return s;
+}
+
+// cpu::matmul_mk_kn, cpu.rs:186-197 (Rayon over output rows; column blocks
+// of 32 only change the visiting order, not any value).
+void orc_matmul(const float *a, const float *b, float *c, int64_t m, int64_t k, int64_t n) {
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int64_t i = 0; i < m; ++i) {
+        const float *ai = a + i * k;
+        for (int64_t j = 0; j < n; ++j) c[i * n + j] = dot_row(ai, b, k, n, j);
+    }
+}
+
+// cpu::linear, cpu.rs:135-184.
+void orc_linear(const float *x, const float *w, const float *bias, float *y, int64_t m, int64_t k,
+                int64_t n) {
+    orc_matmul(x, w, y, m, k, n);
+    add_bias(y, bias, m, n);
+}
+
+// reference::linear, reference.rs:63-85: naïve i, j, p with the bias added
+// inside the sum.
+void orc_ref_linear(const float *x, const float *w, const float *bias, float *y, int64_t m,
+                    int64_t k, int64_t n) {
+    for (int64_t i = 0; i < m; ++i)
+        for (int64_t j = 0; j < n; ++j) {
+            float s = 0.0f;
+            for (int64_t p = 0; p < k; ++p) s += x[i * k + p] * w[p * n + j];
+            if (bias) s += bias[j];
+            y[i * n + j] = s;
+        }
+}
+
+// cpu::attention, cpu.rs:235-298, on x [B,S,D] with head h at columns
+// h·dh..(h+1)·dh: q, k, v and the output projection through cpu::linear
+// (linear3, cpu.rs:300-304); scores, softmax and P·V sequential per (b, h).
+// causal != 0 applies the masking of moe::gqa (moe.rs:104-121): query i
+// attends keys j ≤ i only.  Returns 2 when n_heads·d_head > D.
+int orc_attention(const float *x, const float *wq, const float *wk, const float *wv,
+                  const float *wo, int64_t B, int64_t S, int64_t D, int64_t H, int64_t dh,
+                  int32_t causal, float *out) {
+    if (H * dh > D) return 2;
+    const int64_t T = B * S;
+    std::vector<float> q((size_t)(T * D)), k((size_t)(T * D)), v((size_t)(T * D)),
+        ctx((size_t)(T * D), 0.0f);
+    orc_linear(x, wq, nullptr, q.data(), T, D, D);
+    orc_linear(x, wk, nullptr, k.data(), T, D, D);
+    orc_linear(x, wv, nullptr, v.data(), T, D, D);
+    const float scale = 1.0f / std::sqrt((float)dh);
+    std::vector<float> scores((size_t)(S * S));
+    for (int64_t bi = 0; bi < B; ++bi)
+        for (int64_t h = 0; h < H; ++h) {
+            for (int64_t i = 0; i < S; ++i)
+                for (int64_t j = 0; j < S; ++j) {
+                    if (causal && j > i) {
+                        scores[(size_t)(i * S + j)] = -INFINITY;
+                        continue;
+                    }
+                    float dot = 0.0f;
+                    for (int64_t t = 0; t < dh; ++t)
+                        dot += q[(size_t)(bi * S * D + i * D + h * dh + t)] *
+                               k[(size_t)(bi * S * D + j * D + h * dh + t)];
+                    scores[(size_t)(i * S + j)] = dot * scale;
+                }
+            for (int64_t i = 0; i < S; ++i) {
+                float *row = &scores[(size_t)(i * S)];
+                const int64_t len = causal ? i + 1 : S;
+                float mx = -INFINITY;
+                for (int64_t j = 0; j < len; ++j) mx = std::fmax(mx, row[j]);
+                float sum = 0.0f;
+                for (int64_t j = 0; j < len; ++j) {
+                    row[j] = std::exp(row[j] - mx);
+                    sum += row[j];
+                }
+                const float inv = 1.0f / std::fmax(sum, 1e-30f);
+                for (int64_t j = 0; j < len; ++j) row[j] *= inv;
+                for (int64_t j = len; j < S; ++j) row[j] = 0.0f;
+            }
+            for (int64_t i = 0; i < S; ++i) {
+                const int64_t len = causal ? i + 1 : S;
+                for (int64_t t = 0; t < dh; ++t) {
+                    float acc = 0.0f;
+                    for (int64_t j = 0; j < len; ++j)
+                        acc += scores[(size_t)(i * S + j)] * v[(size_t)(bi * S * D + j * D + h * dh + t)];
+                    ctx[(size_t)(bi * S * D + i * D + h * dh + t)] = acc;
+                }
+            }
+        }
+    orc_linear(ctx.data(), wo, nullptr, out, T, D, D);
+    return 0;
+}
+
+// ---------------------------------------------------------------- moe.rs
+
+// lens::moe::topk_softmax, crates/catnn-core/src/lens/moe.rs:175-187: stable
+// sort of expert ids by descending logit (ties keep the lower id first),
+// truncate to k, w = exp(l − max_sel)·(1/max(Σ, 1e-30)).
+void orc_topk_softmax(const float *logits, int64_t E, int64_t k, int32_t *idx, float *w) {
+    std::vector<int32_t> order((size_t)E);
+    std::iota(order.begin(), order.end(), 0);
+    std::stable_sort(order.begin(), order.end(),
+                     [&](int32_t a, int32_t b) { return logits[a] > logits[b]; });
+    const int64_t kk = std::min(k, E);
+    float mx = -INFINITY;
+    for (int64_t i = 0; i < kk; ++i) mx = std::fmax(mx, logits[order[(size_t)i]]);
+    float sum = 0.0f;
+    for (int64_t i = 0; i < kk; ++i) {
+        idx[i] = order[(size_t)i];
+        w[i] = std::exp(logits[order[(size_t)i]] - mx);
+        sum += w[i];
+    }
+    const float inv = 1.0f / std::fmax(sum, 1e-30f);
+    for (int64_t i = 0; i < kk; ++i) w[i] *= inv;
+}
+
+// moe::route, crates/catnn-compile/src/kernel/moe.rs:177-195.
+void orc_route(const float *x, const float *gate, int64_t T, int64_t H, int64_t E, int64_t k,
+               int32_t *idx, float *w, float *logits) {
+    std::vector<float> lg((size_t)(T * E));
+    orc_matmul_seq(x, gate, lg.data(), T, H, E);
+    for (int64_t t = 0; t < T; ++t) orc_topk_softmax(&lg[(size_t)(t * E)], E, k, idx + t * k, w + t * k);
+    if (logits) std::memcpy(logits, lg.data(), lg.size() * 4);
+}
+
+// silu, moe.rs:12-14.
+static float silu(float v) { return v / (1.0f + std::exp(-v)); }
+
+// moe::swiglu, moe.rs:159-174: three linear_seq GEMMs on x [T,H].
+void orc_swiglu(const float *x, const float *w1, const float *w3, const float *w2, int64_t T,
+                int64_t H, int64_t I, float *y) {
+    std::vector<float> a((size_t)(T * I)), c((size_t)(T * I));
+    orc_matmul_seq(x, w1, a.data(), T, H, I);
+    orc_matmul_seq(x, w3, c.data(), T, H, I);
+    for (size_t i = 0; i < a.size(); ++i) a[i] = silu(a[i]) * c[i];
+    orc_matmul_seq(a.data(), w2, y, T, I, H);
+}
+
+// moe::reference::swiglu, moe.rs:353-381 (gate and up accumulated together).
+void orc_ref_swiglu(const float *x, const float *w1, const float *w3, const float *w2, int64_t T,
+                    int64_t H, int64_t I, float *y) {
+    std::vector<float> h((size_t)(T * I));
+    for (int64_t t = 0; t < T; ++t)
+        for (int64_t j = 0; j < I; ++j) {
+            float a = 0.0f, c = 0.0f;
+            for (int64_t i = 0; i < H; ++i) {
+                const float xv = x[t * H + i];
+                a += xv * w1[i * I + j];
+                c += xv * w3[i * I + j];
+            }
+            h[(size_t)(t * I + j)] = silu(a) * c;
+        }
+    for (int64_t t = 0; t < T; ++t)
+        for (int64_t i = 0; i < H; ++i) {
+            float s = 0.0f;
+            for (int64_t j = 0; j < I; ++j) s += h[(size_t)(t * I + j)] * w2[j * H + i];
+            y[t * H + i] = s;
+        }
+}
+
+// moe::moe, moe.rs:197-223: route all tokens, then per token and per
+// selected expert (ascending k) out[t] += w·swiglu_e(x_t).  Expert weights
+// are packed: w1s [E][H][I], w3s [E][H][I], w2s [E][I][H].  `tokens_only`
+// (may be null) restricts the expert loop to a list of token rows, leaving
+// the other rows of `out` untouched — per-token work is independent, so a
+// subset gives the same rows as the full run.
+void orc_moe(const float *x, const float *gate, const float *w1s, const float *w3s,
+             const float *w2s, int64_t T, int64_t H, int64_t I, int64_t E, int64_t k,
+             const int64_t *tokens_only, int64_t n_only, float *out) {
+    std::vector<int32_t> idx((size_t)(T * k));
+    std::vector<float> w((size_t)(T * k));
+    orc_route(x, gate, T, H, E, k, idx.data(), w.data(), nullptr);
+    std::vector<float> y((size_t)H);
+    const int64_t n_rows = tokens_only ? n_only : T;
+    for (int64_t r = 0; r < n_rows; ++r) {
+        const int64_t t = tokens_only ? tokens_only[r] : r;
+        float *o = out + t * H;
+        for (int64_t i = 0; i < H; ++i) o[i] = 0.0f;
+        for (int64_t kk = 0; kk < k; ++kk) {
+            const int64_t e = idx[(size_t)(t * k + kk)];
+            const float wt = w[(size_t)(t * k + kk)];
+            orc_swiglu(x + t * H, w1s + e * H * I, w3s + e * H * I, w2s + e * I * H, 1, H, I, y.data());
+            for (int64_t i = 0; i < H; ++i) o[i] += wt * y[(size_t)i];
+        }
+    }
+}
+
+// moe::reference::moe, moe.rs:383-416 (per-token logits, reference swiglu).
+void orc_ref_moe(const float *x, const float *gate, const float *w1s, const float *w3s,
+                 const float *w2s, int64_t T, int64_t H, int64_t I, int64_t E, int64_t k,
+                 float *out) {
+    std::vector<float> logits((size_t)E), y((size_t)H);
+    std::vector<int32_t> idx((size_t)k);
+    std::vector<float> w((size_t)k);
+    for (int64_t t = 0; t < T; ++t) {
+        for (int64_t e = 0; e < E; ++e) {
+            float s = 0.0f;
+            for (int64_t i = 0; i < H; ++i) s += x[t * H + i] * gate[i * E + e];
+            logits[(size_t)e] = s;
+        }
+        orc_topk_softmax(logits.data(), E, k, idx.data(), w.data());
+        float *o = out + t * H;
+        for (int64_t i = 0; i < H; ++i) o[i] = 0.0f;
+        for (int64_t kk = 0; kk < std::min(k, E); ++kk) {
+            const int64_t e = idx[(size_t)kk];
+            orc_ref_swiglu(x + t * H, w1s + e * H * I, w3s + e * H * I, w2s + e * I * H, 1, H, I, y.data());
+            for (int64_t i = 0; i < H; ++i) o[i] += w[(size_t)kk] * y[(size_t)i];
+        }
+    }
+}
+
+// Token permutation of the backend (the reference has none: it loops over
+// tokens).  Stable counting sort of the flattened slots s = t·k + k' by
+// expert: counts[e], offsets[e] = Σ_{e'<e} counts[e'] (E+1 entries),
+// slot_of_pos[offsets[e] + r] = the r-th slot routed to e in ascending s,
+// pos_of_slot its inverse.  Returns 2 for an id outside [0, E).
+int orc_moe_permute(const int32_t *idx, int64_t T, int64_t k, int64_t E, int32_t *counts,
+                    int32_t *offsets, int32_t *slot_of_pos, int32_t *pos_of_slot) {
+    const int64_t n = T * k;
+    for (int64_t e = 0; e < E; ++e) counts[e] = 0;
+    for (int64_t s = 0; s < n; ++s) {
+        if (idx[s] < 0 || idx[s] >= E) return 2;
+        ++counts[idx[s]];
+    }
+    offsets[0] = 0;
+    for (int64_t e = 0; e < E; ++e) offsets[e + 1] = offsets[e] + counts[e];
+    std::vector<int32_t> next(offsets, offsets + E);
+    for (int64_t s = 0; s < n; ++s) {
+        const int32_t pos = next[(size_t)idx[s]]++;
+        slot_of_pos[pos] = (int32_t)s;
+        pos_of_slot[s] = pos;
+    }
+    return 0;
+}
+
+// ----------------------------------------------------------- schedule.rs
+
+struct OrcReq {
+    uint64_t bytes, live_from, live_to;
+};
+
+// schedule::place_arena, crates/catnn-compile/src/schedule.rs:79-116.
+// Writes offsets[i] for request i (input order).  Returns 0, or 10
+// (Fibration) with *fail_index set on overflow.
+int orc_place_arena(const uint64_t *bytes, const uint64_t *live_from, const uint64_t *live_to,
+                    int64_t n, uint64_t cap, uint64_t *offsets, int64_t *placement_order,
+                    int64_t *fail_index) {
+    std::vector<int64_t> order((size_t)n);
+    std::iota(order.begin(), order.end(), 0);
+    std::stable_sort(order.begin(), order.end(), [&](int64_t a, int64_t b) {
+        if (live_from[a] != live_from[b]) return live_from[a] < live_from[b];
+        return bytes[a] > bytes[b];
+    });
+    std::vector<int64_t> placed;
+    for (int64_t pi = 0; pi < n; ++pi) {
+        const int64_t i = order[(size_t)pi];
+        std::vector<std::pair<uint64_t, uint64_t>> forb;
+        for (int64_t p : placed)
+            if (live_from[p] <= live_to[i] && live_from[i] <= live_to[p])
+                forb.emplace_back(offsets[p], offsets[p] + bytes[p]);
+        std::stable_sort(forb.begin(), forb.end(),
+                         [](const auto &a, const auto &b) { return a.first < b.first; });
+        uint64_t cursor = 0;
+        bool chosen = false;
+        uint64_t off = 0;
+        for (const auto &f : forb) {
+            if (f.first >= cursor + bytes[i]) {
+                off = cursor;
+                chosen = true;
+                break;
+            }
+            cursor = std::max(cursor, f.second);
+        }
+        if (!chosen) off = cursor;
+        if (off + bytes[i] < off || off + bytes[i] > cap) {
+            if (fail_index) *fail_index = i;
+            return 10;
+        }
+        offsets[i] = off;
+        if (placement_order) placement_order[pi] = i;
+        placed.push_back(i);
+    }
+    return 0;
+}
+
+// schedule::arena_conflict, schedule.rs:123-136: 1 when two simultaneously
+// live buffers overlap in the arena.
+int orc_arena_conflict(const uint64_t *bytes, const uint64_t *offsets, const uint64_t *live_from,
+                       const uint64_t *live_to, int64_t n) {
+    for (int64_t i = 0; i < n; ++i)
+        for (int64_t j = i + 1; j < n; ++j)
+            if (live_from[i] <= live_to[j] && live_from[j] <= live_to[i] &&
+                offsets[i] < offsets[j] + bytes[j] && offsets[j] < offsets[i] + bytes[i])
+                return 1;
+    return 0;
+}
+
+}  // extern "C"
