@@ -95,8 +95,8 @@ def attention_flops(batch: int, seq: int, heads: int, d_head: int, causal: bool)
 
 
 def config3(batch: int = 8, seq: int = 1024, d: int = 1024, heads: int = 16, ffn: int = 4096,
-            causal: bool = True) -> Workload:
-    seeds = _seq(3)
+            causal: bool = True, _config: int = 3) -> Workload:
+    seeds = _seq(_config)
     var = 0.02
     T = batch * seq
     ty = TensorType.f32([batch, seq, d])
@@ -130,7 +130,9 @@ def config3(batch: int = 8, seq: int = 1024, d: int = 1024, heads: int = 16, ffn
              + 2 * 2 * T * d * ffn)
     w_bytes = 4 * (4 * d * d + 2 * d * ffn + ffn + d + 4 * d)
     act_bytes = 4 * T * (2 * d + 2 * d + 3 * d + d + d + d + ffn + ffn + d + d)
-    return Workload("prenorm_block", g, x, flops, w_bytes + act_bytes, T)
+    wl = Workload("prenorm_block", g, x, flops, w_bytes + act_bytes, T)
+    wl._seeds = seeds  # config 5 keeps drawing from the same stream
+    return wl
 
 
 def moe_weights(n_experts: int, hidden: int, inter: int, seeds, gate_var=0.5, w_var=0.02):
@@ -166,3 +168,49 @@ def config4(batch: int = 8, seq: int = 2048, d: int = 1024, n_experts: int = 8, 
     flops = 2 * T * d * n_experts + T * top_k * 2 * 3 * d * inter
     min_bytes = 4 * (2 * T * d + d * n_experts + 3 * n_experts * d * inter)
     return Workload("moe_layer", g, x, flops, min_bytes, T)
+
+
+def _moe_params(n_experts, d, inter, seeds):
+    gate, w1, w3, w2 = moe_weights(n_experts, d, inter, seeds)
+    params = {"gate": Tensor(TensorType.f32([d, n_experts]), gate)}
+    for e in range(n_experts):
+        params[f"e{e}.w1"] = Tensor(TensorType.f32([d, inter]), w1[e])
+        params[f"e{e}.w3"] = Tensor(TensorType.f32([d, inter]), w3[e])
+        params[f"e{e}.w2"] = Tensor(TensorType.f32([inter, d]), w2[e])
+    return params
+
+
+@dataclass
+class TrainWorkload:
+    name: str
+    graph: IrGraph
+    x: Tensor
+    target: Tensor
+    lr: float
+    flops: int          # forward + backward (2x forward), the reference's recompute excluded
+    tokens: int
+
+
+def config5(batch: int = 8, seq: int = 1024, d: int = 1024, heads: int = 16, ffn: int = 4096,
+            n_experts: int = 8, top_k: int = 2, inter: int = 3584) -> TrainWorkload:
+    """Config 5: the config-3 block followed by the config-4 MoE layer on the
+    block's T = batch·seq tokens, one training step (forward, MSE against a
+    N(0,1) target, reverse chain, SGD lr 0.05)."""
+    blk = config3(batch, seq, d, heads, ffn, causal=True, _config=5)
+    g = blk.graph
+    g.name = "block_moe_train"
+    seeds = blk._seeds
+    ty = TensorType.f32([batch, seq, d])
+    g.add_node(IrNode(9, "moe", OpenOp.moe(n_experts, top_k, d, inter), ty,
+                      _moe_params(n_experts, d, inter, seeds)))
+    g.add_edge(8, 9)
+    g.outputs = [9]
+    T = batch * seq
+    target = Tensor(ty, synth.normal(T * d, next(seeds), 1.0))
+    moe_flops = 2 * T * d * n_experts + T * top_k * 2 * 3 * d * inter
+    fwd = blk.flops + moe_flops
+    return TrainWorkload("block_moe_train", g, blk.x, target, 0.05, 3 * fwd, T)
+
+
+def config5_graph(**kw) -> IrGraph:
+    return config5(**kw).graph

@@ -506,3 +506,291 @@ int orc_arena_conflict(const uint64_t *bytes, const uint64_t *offsets, const uin
 }
 
 }  // extern "C"
+
+// ============================================================ adjoint.rs
+// Reverse rules of crates/catnn-compile/src/kernel/adjoint.rs, restated loop
+// for loop (sequential: the reference runs them single-threaded).  Pinned by
+// tests/test_oracle_adjoint.py against float64 torch autograd and the
+// reference's known answers (adjoint.rs:1006-1011, :1035-1042,
+// optim.rs:163-176).
+
+extern "C" {
+
+// linear_backward, adjoint.rs:35-61: for i, j: g = dy[i,j]; db[j] += g;
+// for p: dw[p,j] += x[i,p]·g; dx[i,p] += g·w[p,j].
+void orc_linear_backward(const float *x, const float *w, const float *dy, int64_t m, int64_t k,
+                         int64_t n, float *dx, float *dw, float *db) {
+    std::fill(dx, dx + m * k, 0.0f);
+    std::fill(dw, dw + k * n, 0.0f);
+    std::fill(db, db + n, 0.0f);
+    for (int64_t i = 0; i < m; ++i)
+        for (int64_t j = 0; j < n; ++j) {
+            const float g = dy[i * n + j];
+            db[j] += g;
+            for (int64_t p = 0; p < k; ++p) {
+                dw[p * n + j] += x[i * k + p] * g;
+                dx[i * k + p] += g * w[p * n + j];
+            }
+        }
+}
+
+// relu_backward, adjoint.rs:63-74.
+void orc_relu_backward(const float *x, const float *dy, float *dx, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) dx[i] = x[i] <= 0.0f ? 0.0f : dy[i];
+}
+
+// gelu_backward, adjoint.rs:76-90 (derivative of the tanh form).
+void orc_gelu_backward(const float *x, const float *dy, float *dx, int64_t n) {
+    const float C = 0.044715f;
+    const float k = std::sqrt(2.0f / (float)M_PI);
+    for (int64_t i = 0; i < n; ++i) {
+        const float z = x[i];
+        const float u = k * (z + C * z * z * z);
+        const float t = std::tanh(u);
+        const float sech2 = 1.0f - t * t;
+        const float du = k * (1.0f + 3.0f * C * z * z);
+        const float dg = 0.5f * (1.0f + t) + 0.5f * z * sech2 * du;
+        dx[i] = dy[i] * dg;
+    }
+}
+
+// softmax_backward, adjoint.rs:92-104: dx = y·(dy − Σ y·dy) per row.
+void orc_softmax_backward(const float *y, const float *dy, float *dx, int64_t rows, int64_t last) {
+    for (int64_t r = 0; r < rows; ++r) {
+        const float *yr = y + r * last, *gr = dy + r * last;
+        float dot = 0.0f;
+        for (int64_t i = 0; i < last; ++i) dot += yr[i] * gr[i];
+        for (int64_t i = 0; i < last; ++i) dx[r * last + i] = yr[i] * (gr[i] - dot);
+    }
+}
+
+// mse_loss, adjoint.rs:106-119: loss = Σe²/n, d = 2e/n.
+float orc_mse_loss(const float *pred, const float *target, int64_t n, float *d) {
+    const float nf = (float)n;
+    float loss = 0.0f;
+    for (int64_t i = 0; i < n; ++i) {
+        const float e = pred[i] - target[i];
+        loss += e * e;
+        d[i] = 2.0f * e / nf;
+    }
+    return loss / nf;
+}
+
+// layer_norm_backward, adjoint.rs:530-577.
+void orc_layer_norm_backward(const float *x, const float *gamma, const float *dy, int64_t rows,
+                             int64_t last, float eps, float *dx, float *dgamma, float *dbeta) {
+    std::fill(dgamma, dgamma + last, 0.0f);
+    std::fill(dbeta, dbeta + last, 0.0f);
+    const float n = (float)last;
+    std::vector<float> xhat((size_t)last), dxhat((size_t)last);
+    for (int64_t r = 0; r < rows; ++r) {
+        const float *row = x + r * last, *yrow = dy + r * last;
+        float s = 0.0f;
+        for (int64_t i = 0; i < last; ++i) s += row[i];
+        const float mean = s / n;
+        float q = 0.0f;
+        for (int64_t i = 0; i < last; ++i) {
+            const float d = row[i] - mean;
+            q += d * d;
+        }
+        const float var = q / n;
+        const float inv = 1.0f / std::sqrt(var + eps);
+        for (int64_t i = 0; i < last; ++i) {
+            xhat[(size_t)i] = (row[i] - mean) * inv;
+            dbeta[i] += yrow[i];
+            dgamma[i] += yrow[i] * xhat[(size_t)i];
+            dxhat[(size_t)i] = yrow[i] * gamma[i];
+        }
+        float sd = 0.0f, sdx = 0.0f;
+        for (int64_t i = 0; i < last; ++i) sd += dxhat[(size_t)i];
+        for (int64_t i = 0; i < last; ++i) sdx += dxhat[(size_t)i] * xhat[(size_t)i];
+        for (int64_t i = 0; i < last; ++i)
+            dx[r * last + i] = (inv / n) * (n * dxhat[(size_t)i] - sd - xhat[(size_t)i] * sdx);
+    }
+}
+
+// attention_backward, adjoint.rs:582-722 (recomputes the forward with
+// cpu::linear projections).  causal != 0 restricts every row to keys j ≤ i
+// with the window softmax and its adjoint as gqa_backward does
+// (adjoint.rs:372-405).
+int orc_attention_backward(const float *x, const float *wq, const float *wk, const float *wv,
+                           const float *wo, int64_t B, int64_t S, int64_t D, int64_t H, int64_t dh,
+                           int32_t causal, const float *dy, float *dx, float *dwq, float *dwk,
+                           float *dwv, float *dwo) {
+    if (D != H * dh) return 2;
+    const int64_t T = B * S;
+    std::vector<float> q((size_t)(T * D)), k((size_t)(T * D)), v((size_t)(T * D));
+    orc_linear(x, wq, nullptr, q.data(), T, D, D);
+    orc_linear(x, wk, nullptr, k.data(), T, D, D);
+    orc_linear(x, wv, nullptr, v.data(), T, D, D);
+    const float scale = 1.0f / std::sqrt((float)dh);
+    std::vector<float> attn((size_t)(B * H * S * S), 0.0f), ctx((size_t)(T * D), 0.0f);
+    for (int64_t bi = 0; bi < B; ++bi)
+        for (int64_t h = 0; h < H; ++h) {
+            float *sc = &attn[(size_t)((bi * H + h) * S * S)];
+            for (int64_t i = 0; i < S; ++i) {
+                const int64_t len = causal ? i + 1 : S;
+                for (int64_t j = 0; j < len; ++j) {
+                    float dot = 0.0f;
+                    for (int64_t t = 0; t < dh; ++t)
+                        dot += q[(size_t)(bi * S * D + i * D + h * dh + t)] *
+                               k[(size_t)(bi * S * D + j * D + h * dh + t)];
+                    sc[i * S + j] = dot * scale;
+                }
+                float mx = -INFINITY;
+                for (int64_t j = 0; j < len; ++j) mx = std::fmax(mx, sc[i * S + j]);
+                float sum = 0.0f;
+                for (int64_t j = 0; j < len; ++j) {
+                    sc[i * S + j] = std::exp(sc[i * S + j] - mx);
+                    sum += sc[i * S + j];
+                }
+                const float inv = 1.0f / std::fmax(sum, 1e-30f);
+                for (int64_t j = 0; j < len; ++j) sc[i * S + j] *= inv;
+            }
+            for (int64_t i = 0; i < S; ++i) {
+                const int64_t len = causal ? i + 1 : S;
+                for (int64_t t = 0; t < dh; ++t) {
+                    float acc = 0.0f;
+                    for (int64_t j = 0; j < len; ++j)
+                        acc += sc[i * S + j] * v[(size_t)(bi * S * D + j * D + h * dh + t)];
+                    ctx[(size_t)(bi * S * D + i * D + h * dh + t)] = acc;
+                }
+            }
+        }
+    std::vector<float> dctx((size_t)(T * D)), dbias((size_t)D);
+    orc_linear_backward(ctx.data(), wo, dy, T, D, D, dctx.data(), dwo, dbias.data());
+    std::vector<float> dq((size_t)(T * D), 0.0f), dk((size_t)(T * D), 0.0f), dv((size_t)(T * D), 0.0f);
+    std::vector<float> dattn((size_t)S);
+    for (int64_t bi = 0; bi < B; ++bi)
+        for (int64_t h = 0; h < H; ++h) {
+            const float *a = &attn[(size_t)((bi * H + h) * S * S)];
+            for (int64_t i = 0; i < S; ++i) {
+                const int64_t len = causal ? i + 1 : S;
+                for (int64_t j = 0; j < len; ++j) {
+                    float g = 0.0f;
+                    for (int64_t t = 0; t < dh; ++t) {
+                        const float dc = dctx[(size_t)(bi * S * D + i * D + h * dh + t)];
+                        g += dc * v[(size_t)(bi * S * D + j * D + h * dh + t)];
+                        dv[(size_t)(bi * S * D + j * D + h * dh + t)] += a[i * S + j] * dc;
+                    }
+                    dattn[(size_t)j] = g;
+                }
+                float dot = 0.0f;
+                for (int64_t j = 0; j < len; ++j) dot += a[i * S + j] * dattn[(size_t)j];
+                for (int64_t j = 0; j < len; ++j) {
+                    const float g = a[i * S + j] * (dattn[(size_t)j] - dot) * scale;
+                    for (int64_t t = 0; t < dh; ++t) {
+                        dq[(size_t)(bi * S * D + i * D + h * dh + t)] +=
+                            g * k[(size_t)(bi * S * D + j * D + h * dh + t)];
+                        dk[(size_t)(bi * S * D + j * D + h * dh + t)] +=
+                            g * q[(size_t)(bi * S * D + i * D + h * dh + t)];
+                    }
+                }
+            }
+        }
+    std::vector<float> dxq((size_t)(T * D)), dxk((size_t)(T * D)), dxv((size_t)(T * D));
+    orc_linear_backward(x, wq, dq.data(), T, D, D, dxq.data(), dwq, dbias.data());
+    orc_linear_backward(x, wk, dk.data(), T, D, D, dxk.data(), dwk, dbias.data());
+    orc_linear_backward(x, wv, dv.data(), T, D, D, dxv.data(), dwv, dbias.data());
+    for (int64_t i = 0; i < T * D; ++i) dx[i] = dxq[(size_t)i] + dxk[(size_t)i] + dxv[(size_t)i];
+    return 0;
+}
+
+static float silu_grad(float v) {
+    const float s = 1.0f / (1.0f + std::exp(-v));
+    return s + v * s * (1.0f - s);
+}
+
+// swiglu_backward, adjoint.rs:217-251 (gradients accumulate into dw*).
+static void swiglu_backward_acc(const float *x, const float *w1, const float *w3, const float *w2,
+                                int64_t T, int64_t H, int64_t I, const float *dy, float *dx,
+                                float *dw1, float *dw3, float *dw2) {
+    std::vector<float> a((size_t)(T * I)), c((size_t)(T * I)), h((size_t)(T * I));
+    orc_matmul_seq(x, w1, a.data(), T, H, I);
+    orc_matmul_seq(x, w3, c.data(), T, H, I);
+    for (size_t i = 0; i < h.size(); ++i) h[i] = silu(a[i]) * c[i];
+    std::vector<float> dh((size_t)(T * I)), tw2((size_t)(I * H)), tb((size_t)std::max(H, I));
+    orc_linear_backward(h.data(), w2, dy, T, I, H, dh.data(), tw2.data(), tb.data());
+    std::vector<float> da((size_t)(T * I)), dc((size_t)(T * I));
+    for (size_t i = 0; i < h.size(); ++i) {
+        da[i] = dh[i] * c[i] * silu_grad(a[i]);
+        dc[i] = dh[i] * silu(a[i]);
+    }
+    std::vector<float> dx1((size_t)(T * H)), dx3((size_t)(T * H)), tw1((size_t)(H * I)), tw3((size_t)(H * I));
+    orc_linear_backward(x, w1, da.data(), T, H, I, dx1.data(), tw1.data(), tb.data());
+    orc_linear_backward(x, w3, dc.data(), T, H, I, dx3.data(), tw3.data(), tb.data());
+    for (int64_t i = 0; i < T * H; ++i) dx[i] = dx1[(size_t)i] + dx3[(size_t)i];
+    for (int64_t i = 0; i < H * I; ++i) {
+        dw1[i] += tw1[(size_t)i];
+        dw3[i] += tw3[(size_t)i];
+    }
+    for (int64_t i = 0; i < I * H; ++i) dw2[i] += tw2[(size_t)i];
+}
+
+void orc_swiglu_backward(const float *x, const float *w1, const float *w3, const float *w2, int64_t T,
+                         int64_t H, int64_t I, const float *dy, float *dx, float *dw1, float *dw3,
+                         float *dw2) {
+    std::fill(dw1, dw1 + H * I, 0.0f);
+    std::fill(dw3, dw3 + H * I, 0.0f);
+    std::fill(dw2, dw2 + I * H, 0.0f);
+    swiglu_backward_acc(x, w1, w3, w2, T, H, I, dy, dx, dw1, dw3, dw2);
+}
+
+// router_backward_ste, adjoint.rs:255-284: per token, the softmax Jacobian
+// on the selected subset; then linear_backward through the gate.
+void orc_router_backward_ste(const float *x, const float *gate, int64_t T, int64_t H, int64_t E,
+                             int64_t k, const float *d_weights, float *dx, float *dgate) {
+    std::vector<float> logits((size_t)(T * E)), dl((size_t)(T * E), 0.0f), db((size_t)E);
+    orc_matmul_seq(x, gate, logits.data(), T, H, E);
+    std::vector<int32_t> idx((size_t)k);
+    std::vector<float> w((size_t)k);
+    for (int64_t t = 0; t < T; ++t) {
+        orc_topk_softmax(&logits[(size_t)(t * E)], E, k, idx.data(), w.data());
+        float dot = 0.0f;
+        for (int64_t j = 0; j < k; ++j) dot += w[(size_t)j] * d_weights[t * k + j];
+        for (int64_t j = 0; j < k; ++j)
+            dl[(size_t)(t * E + idx[(size_t)j])] += w[(size_t)j] * (d_weights[t * k + j] - dot);
+    }
+    orc_linear_backward(x, gate, dl.data(), T, H, E, dx, dgate, db.data());
+}
+
+// moe_backward, adjoint.rs:471-526.  Expert weights packed as in orc_moe.
+void orc_moe_backward(const float *x, const float *gate, const float *w1s, const float *w3s,
+                      const float *w2s, int64_t T, int64_t H, int64_t I, int64_t E, int64_t k,
+                      const float *dy, float *dx, float *dgate, float *dw1s, float *dw3s,
+                      float *dw2s) {
+    std::vector<int32_t> idx((size_t)(T * k));
+    std::vector<float> wts((size_t)(T * k)), d_wts((size_t)(T * k), 0.0f);
+    orc_route(x, gate, T, H, E, k, idx.data(), wts.data(), nullptr);
+    std::fill(dx, dx + T * H, 0.0f);
+    std::fill(dw1s, dw1s + E * H * I, 0.0f);
+    std::fill(dw3s, dw3s + E * H * I, 0.0f);
+    std::fill(dw2s, dw2s + E * I * H, 0.0f);
+    std::vector<float> y((size_t)H), dye((size_t)H), dxe((size_t)H);
+    for (int64_t t = 0; t < T; ++t) {
+        const float *xt = x + t * H, *dyt = dy + t * H;
+        for (int64_t j = 0; j < k; ++j) {
+            const int64_t e = idx[(size_t)(t * k + j)];
+            const float wt = wts[(size_t)(t * k + j)];
+            const float *w1 = w1s + e * H * I, *w3 = w3s + e * H * I, *w2 = w2s + e * I * H;
+            orc_swiglu(xt, w1, w3, w2, 1, H, I, y.data());
+            float s = 0.0f;
+            for (int64_t i = 0; i < H; ++i) s += y[(size_t)i] * dyt[i];
+            d_wts[(size_t)(t * k + j)] = s;
+            for (int64_t i = 0; i < H; ++i) dye[(size_t)i] = dyt[i] * wt;
+            swiglu_backward_acc(xt, w1, w3, w2, 1, H, I, dye.data(), dxe.data(), dw1s + e * H * I,
+                                dw3s + e * H * I, dw2s + e * I * H);
+            for (int64_t i = 0; i < H; ++i) dx[t * H + i] += dxe[(size_t)i];
+        }
+    }
+    std::vector<float> dxg((size_t)(T * H));
+    orc_router_backward_ste(x, gate, T, H, E, k, d_wts.data(), dxg.data(), dgate);
+    for (int64_t i = 0; i < T * H; ++i) dx[i] += dxg[(size_t)i];
+}
+
+// Sgd::put, crates/catnn-core/src/lens/optim.rs:32-42: p −= lr·g.
+void orc_sgd(float *p, const float *g, int64_t n, float lr) {
+    for (int64_t i = 0; i < n; ++i) p[i] -= lr * g[i];
+}
+
+}  // extern "C"

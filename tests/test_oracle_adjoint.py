@@ -1,0 +1,183 @@
+"""Pins the oracle's restatement of the reference adjoints (adjoint.rs) and
+of one reference_train step against float64 torch autograd — an
+independent derivation of the same gradients — and against the
+reference's own known answers."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import oracle_train as ot
+from conftest import rel_l2
+
+RNG = np.random.default_rng(99)
+T64 = torch.float64
+
+
+def _t(a, grad=False):
+    return torch.tensor(np.asarray(a, np.float64), dtype=T64, requires_grad=grad)
+
+
+def test_relu_backward_known_answer():
+    # adjoint.rs:1006-1011
+    assert ot.relu_backward(np.array([-1.0, 2.0, 0.0]), np.ones(3)).tolist() == [0.0, 1.0, 0.0]
+
+
+def test_softmax_grad_rows_sum_to_zero():
+    # adjoint.rs:1035-1042
+    y = oracle.softmax_last(RNG.standard_normal((4, 9)))
+    dx = ot.softmax_backward(y, RNG.standard_normal((4, 9)))
+    assert np.allclose(dx.sum(-1), 0.0, atol=1e-6)
+
+
+def test_sgd_known_answers():
+    # optim.rs:163-176
+    assert ot.sgd(np.array([1.0, 2.0]), np.array([1.0, -1.0]), 0.5).tolist() == [0.5, 2.5]
+    assert ot.sgd(np.array([3.0, 4.0]), np.zeros(2), 0.1).tolist() == [3.0, 4.0]
+
+
+def test_linear_backward_matches_autograd():
+    x, w = RNG.standard_normal((6, 10)), RNG.standard_normal((10, 7))
+    dy = RNG.standard_normal((6, 7))
+    dx, dw, db = ot.linear_backward(x, w, dy)
+    X, W = _t(x, True), _t(w, True)
+    B = torch.zeros(7, dtype=T64, requires_grad=True)
+    (X @ W + B).backward(_t(dy))
+    assert rel_l2(dx, X.grad) < 1e-6 and rel_l2(dw, W.grad) < 1e-6 and rel_l2(db, B.grad) < 1e-6
+
+
+def test_gelu_and_mse_backward_match_autograd():
+    x, dy = RNG.standard_normal(500) * 3, RNG.standard_normal(500)
+    X = _t(x, True)
+    torch.nn.functional.gelu(X, approximate="tanh").backward(_t(dy))
+    assert rel_l2(ot.gelu_backward(x, dy), X.grad) < 1e-5
+    p, t = RNG.standard_normal((5, 8)), RNG.standard_normal((5, 8))
+    loss, d = ot.mse_loss(p, t)
+    P = _t(p, True)
+    L = torch.mean((P - _t(t)) ** 2)
+    L.backward()
+    assert abs(loss - L.item()) < 1e-5 and rel_l2(d, P.grad) < 1e-6
+
+
+def test_layer_norm_backward_matches_autograd():
+    x = RNG.standard_normal((7, 32)) * 2 + 1
+    g, dy = RNG.standard_normal(32), RNG.standard_normal((7, 32))
+    dx, dg, db = ot.layer_norm_backward(x, g, dy, 1e-6)
+    X, G, Bb = _t(x, True), _t(g, True), torch.zeros(32, dtype=T64, requires_grad=True)
+    torch.nn.functional.layer_norm(X, (32,), G, Bb, eps=1e-6).backward(_t(dy))
+    assert rel_l2(dx, X.grad) < 1e-4 and rel_l2(dg, G.grad) < 1e-5 and rel_l2(db, Bb.grad) < 1e-6
+
+
+def _attn64(X, Wq, Wk, Wv, Wo, H, causal):
+    B, S, D = X.shape
+    dh = D // H
+    q, k, v = [(X @ W).view(B, S, H, dh).transpose(1, 2) for W in (Wq, Wk, Wv)]
+    ctx = torch.nn.functional.scaled_dot_product_attention(q, k, v, is_causal=causal)
+    return ctx.transpose(1, 2).reshape(B, S, D) @ Wo
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_attention_backward_matches_autograd(causal):
+    B, S, D, H = 2, 9, 16, 4
+    x = RNG.standard_normal((B, S, D))
+    ws = [RNG.standard_normal((D, D)) / math.sqrt(D) for _ in range(4)]
+    dy = RNG.standard_normal((B, S, D))
+    got = ot.attention_backward(x, *ws, H, D // H, dy, causal=causal)
+    X, *W = [_t(a, True) for a in (x, *ws)]
+    _attn64(X, *W, H, causal).backward(_t(dy))
+    for g, ref in zip(got, [X.grad] + [w.grad for w in W]):
+        assert rel_l2(g, ref) < 1e-4
+    if causal:  # a wrong mask must not pass
+        nc = ot.attention_backward(x, *ws, H, D // H, dy, causal=False)
+        assert rel_l2(nc[0], X.grad) > 1e-2
+
+
+def _swiglu64(X, W1, W3, W2):
+    a, c = X @ W1, X @ W3
+    return (a * torch.sigmoid(a) * c) @ W2
+
+
+def test_swiglu_backward_matches_autograd():
+    T, H, I = 5, 12, 20
+    x = RNG.standard_normal((T, H))
+    w1, w3 = RNG.standard_normal((H, I)) * 0.3, RNG.standard_normal((H, I)) * 0.3
+    w2 = RNG.standard_normal((I, H)) * 0.3
+    dy = RNG.standard_normal((T, H))
+    got = ot.swiglu_backward(x, w1, w3, w2, dy)
+    X, W1, W3, W2 = [_t(a, True) for a in (x, w1, w3, w2)]
+    _swiglu64(X, W1, W3, W2).backward(_t(dy))
+    for g, ref in zip(got, (X.grad, W1.grad, W3.grad, W2.grad)):
+        assert rel_l2(g, ref) < 1e-5
+
+
+def _moe64(X, G, W1, W3, W2, idx):
+    """Dense float64 MoE with the routing indices held fixed (the STE:
+    gradients flow through the softmax weights of the selected experts)."""
+    logits = X @ G
+    sel = torch.gather(logits, 1, torch.from_numpy(idx.astype(np.int64)))
+    w = torch.softmax(sel, -1)
+    out = torch.zeros_like(X)
+    for j in range(idx.shape[1]):
+        for e in range(W1.shape[0]):
+            m = torch.from_numpy(idx[:, j] == e)
+            if m.any():
+                out[m] = out[m] + w[m, j:j + 1] * _swiglu64(X[m], W1[e], W3[e], W2[e])
+    return out
+
+
+def test_router_and_moe_backward_match_autograd():
+    T, H, I, E, k = 11, 8, 12, 4, 2
+    x = RNG.standard_normal((T, H))
+    gate = RNG.standard_normal((H, E))
+    w1, w3 = RNG.standard_normal((E, H, I)) * 0.3, RNG.standard_normal((E, H, I)) * 0.3
+    w2 = RNG.standard_normal((E, I, H)) * 0.3
+    dy = RNG.standard_normal((T, H))
+    got = ot.moe_backward(x, gate, w1, w3, w2, k, dy)
+    idx, _, _ = oracle.route(x.astype(np.float32), gate.astype(np.float32), k)
+    X, G, W1, W3, W2 = [_t(a, True) for a in (x, gate, w1, w3, w2)]
+    _moe64(X, G, W1, W3, W2, idx).backward(_t(dy))
+    for g, ref in zip(got, (X.grad, G.grad, W1.grad, W3.grad, W2.grad)):
+        assert rel_l2(g, ref) < 1e-4
+    # the router's STE piece alone
+    dwt = RNG.standard_normal((T, k))
+    dx, dg = ot.router_backward_ste(x, gate, k, dwt)
+    X2, G2 = _t(x, True), _t(gate, True)
+    sel = torch.gather(X2 @ G2, 1, torch.from_numpy(idx.astype(np.int64)))
+    (torch.softmax(sel, -1) * _t(dwt)).sum().backward()
+    assert rel_l2(dx, X2.grad) < 1e-5 and rel_l2(dg, G2.grad) < 1e-5
+
+
+def test_train_step_matches_autograd_on_block_plus_moe():
+    from catnn_amd import configs
+
+    g = configs.config5_graph(batch=1, seq=12, d=16, heads=2, ffn=32, n_experts=4, top_k=2, inter=24)
+    x = RNG.standard_normal((1, 12, 16)).astype(np.float32)
+    tgt = RNG.standard_normal((1, 12, 16)).astype(np.float32)
+    loss, grads, new = ot.train_step(g, x, tgt, 0.05)
+    # float64 torch restatement of the same graph
+    P = {nid: {p: _t(t.numpy(), True) for p, t in n.params.items()} for nid, n in g.nodes.items()}
+    X = _t(x)
+    n = g.nodes
+
+    def ln(h, nid):
+        return torch.nn.functional.layer_norm(h, (16,), P[nid]["gamma"], P[nid]["beta"], eps=1e-6)
+
+    h1 = ln(X, 1)
+    a = _attn64(h1, P[2]["wq"], P[2]["wk"], P[2]["wv"], P[2]["wo"], 2, True)
+    r1 = X + a
+    f = torch.nn.functional.gelu(ln(r1, 4) @ P[5]["w"] + P[5]["b"], approximate="tanh")
+    r2 = r1 + (f @ P[7]["w"] + P[7]["b"])
+    mp = P[9]
+    flat = r2.reshape(12, 16)
+    idx, _, _ = oracle.route(flat.detach().numpy().astype(np.float32), mp["gate"].detach().numpy().astype(np.float32), 2)
+    stack = lambda s: torch.stack([mp[f"e{e}.{s}"] for e in range(4)])
+    out = _moe64(flat, mp["gate"], stack("w1"), stack("w3"), stack("w2"), idx)
+    L = torch.mean((out.reshape(1, 12, 16) - _t(tgt)) ** 2)
+    L.backward()
+    assert abs(loss - L.item()) < 1e-4 * max(1.0, abs(L.item()))
+    for nid, dp in grads.items():
+        for port, gr in dp.items():
+            assert rel_l2(gr, P[nid][port].grad) < 1e-3, (n[nid].name, port)
+            assert np.allclose(new[nid][port], n[nid].params[port].numpy() - np.float32(0.05) * gr)
