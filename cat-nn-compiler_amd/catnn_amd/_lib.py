@@ -131,6 +131,15 @@ SIGNATURES = {
     "catnn_hip_program_arena": [_VP, ctypes.POINTER(CArenaAlloc), _I32, _PI32, _PU64],
     "catnn_hip_program_profile": [_VP, _I32],
     "catnn_hip_program_timings": [_VP, ctypes.POINTER(CStepTiming), _I32, _PI32],
+    "catnn_hip_train_install": [_VP, _VP, _F, ctypes.POINTER(_VP)],
+    "catnn_hip_train_free": [_VP],
+    "catnn_hip_train_set_batch": [_VP, ctypes.POINTER(CTensor), ctypes.POINTER(CTensor)],
+    "catnn_hip_train_step": [_VP, ctypes.POINTER(_F)],
+    "catnn_hip_train_read_param": [_VP, ctypes.c_uint32, ctypes.c_char_p, ctypes.POINTER(_F), _I64],
+    "catnn_hip_train_read_grad": [_VP, ctypes.c_uint32, ctypes.c_char_p, ctypes.POINTER(_F), _I64],
+    "catnn_hip_train_read_value": [_VP, ctypes.c_uint32, ctypes.POINTER(_F), _I64],
+    "catnn_hip_train_read_routing": [_VP, ctypes.c_uint32, _PI32, _I64],
+    "catnn_hip_train_arena": [_VP, ctypes.POINTER(CArenaAlloc), _I32, _PI32, _PU64],
     "catnn_hip_events": [_VP, ctypes.POINTER(CEvent), _I32, _PI32],
     "catnn_hip_clear_events": [_VP],
     "catnn_hip_linear_f32": [_VP, _VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _I32],

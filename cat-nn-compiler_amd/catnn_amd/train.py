@@ -1,0 +1,91 @@
+"""One training step of an IrGraph on the GPU (catnn_hip_train_*).
+
+`Trainer.step()` replaces one step of pipeline::reference_train
+(crates/catnn-compile/src/pipeline.rs:476-547) with MSE and SGD: forward,
+loss, reverse-topo adjoints, SGD on fp32 master weights.  GEMM operands are
+bf16 (bf16 MFMA, fp32 accumulation); masters, residual stream, norms,
+router and gradient accumulation are fp32.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import List, Tuple
+
+import numpy as np
+
+from ._lib import CArenaAlloc, check, lib
+from .arena import ArenaAlloc
+from .device import Device
+from .ir import IrGraph, Tensor, ctensor
+
+_FP = ctypes.POINTER(ctypes.c_float)
+
+
+class Trainer:
+    def __init__(self, device: Device, graph: IrGraph, lr: float = 0.05):
+        self.device = device
+        self.graph = graph
+        self.lr = lr
+        h = graph.to_c()
+        self.handle = ctypes.c_void_p()
+        try:
+            check(lib.catnn_hip_train_install(device.handle, h, ctypes.c_float(lr),
+                                              ctypes.byref(self.handle)))
+        finally:
+            lib.catnn_graph_free(h)
+
+    def set_batch(self, x: Tensor, target: Tensor):
+        cx, ct = ctensor(x), ctensor(target)
+        check(lib.catnn_hip_train_set_batch(self.handle, ctypes.byref(cx), ctypes.byref(ct)))
+
+    def step(self, sync: bool = True):
+        """One step; returns the loss (before the update) when `sync`."""
+        if not sync:
+            check(lib.catnn_hip_train_step(self.handle, None))
+            return None
+        loss = ctypes.c_float()
+        check(lib.catnn_hip_train_step(self.handle, ctypes.byref(loss)))
+        return float(loss.value)
+
+    def _read(self, fn, node_id: int, port: str, shape) -> np.ndarray:
+        out = np.empty(shape, np.float32)
+        check(fn(self.handle, node_id, port.encode(), out.ctypes.data_as(_FP), out.size))
+        return out
+
+    def param(self, node_id: int, port: str, shape) -> np.ndarray:
+        return self._read(lib.catnn_hip_train_read_param, node_id, port, shape)
+
+    def grad(self, node_id: int, port: str, shape) -> np.ndarray:
+        return self._read(lib.catnn_hip_train_read_grad, node_id, port, shape)
+
+    def value(self, node_id: int, shape) -> np.ndarray:
+        out = np.empty(shape, np.float32)
+        check(lib.catnn_hip_train_read_value(self.handle, node_id, out.ctypes.data_as(_FP), out.size))
+        return out
+
+    def routing(self, node_id: int, tokens: int, top_k: int) -> np.ndarray:
+        out = np.empty((tokens, top_k), np.int32)
+        check(lib.catnn_hip_train_read_routing(self.handle, node_id,
+                                               out.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)),
+                                               out.size))
+        return out
+
+    def arena(self) -> Tuple[List[ArenaAlloc], int]:
+        n = ctypes.c_int32()
+        reserved = ctypes.c_uint64()
+        check(lib.catnn_hip_train_arena(self.handle, None, 0, ctypes.byref(n), ctypes.byref(reserved)))
+        buf = (CArenaAlloc * max(n.value, 1))()
+        check(lib.catnn_hip_train_arena(self.handle, buf, n.value, ctypes.byref(n), ctypes.byref(reserved)))
+        return ([ArenaAlloc(a.id.decode(), a.bytes, a.offset, a.live_from, a.live_to)
+                 for a in buf[: n.value]], reserved.value)
+
+    def free(self):
+        if self.handle:
+            check(lib.catnn_hip_train_free(self.handle))
+            self.handle = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass

@@ -24,6 +24,7 @@
 #include "common.hpp"
 #include "devmath.hpp"
 #include "kernels.hpp"
+#include "train_ops.hpp"
 
 namespace catnn {
 namespace k {
@@ -39,8 +40,8 @@ __global__ __launch_bounds__(256, 2) void attn_mfma_kernel(const float *__restri
                                                            const float *__restrict__ k,
                                                            const float *__restrict__ v,
                                                            int64_t ld, float *__restrict__ o,
-                                                           int64_t ldo, int S, int H,
-                                                           float qscale, int causal,
+                                                           int64_t ldo, float *__restrict__ lse,
+                                                           int S, int H, float qscale, int causal,
                                                            int n_qblocks) {
     static_assert(DH == 64, "MFMA attention is written for d_head = 64");
     constexpr int BQ = 128, BKV = 64, LDK = DH + 4;
@@ -200,6 +201,7 @@ __global__ __launch_bounds__(256, 2) void attn_mfma_kernel(const float *__restri
 
     if (qi < S) {
         const float inv = 1.0f / fmaxf(l, 1e-30f);
+        if (lse) lse[(row_base + qi) * H + h] = m + log2f(fmaxf(l, 1e-30f));
         float *dst = o + (row_base + qi) * ldo + (int64_t)h * DH;
 #pragma unroll
         for (int db = 0; db < DH / 32; ++db)
@@ -219,8 +221,9 @@ __global__ __launch_bounds__(256) void attn_generic_kernel(const float *__restri
                                                            const float *__restrict__ k,
                                                            const float *__restrict__ v,
                                                            int64_t ld, float *__restrict__ o,
-                                                           int64_t ldo, int B, int S, int H,
-                                                           int DH, float scale, int causal) {
+                                                           int64_t ldo, float *__restrict__ lse,
+                                                           int B, int S, int H, int DH, float scale,
+                                                           int causal) {
     const int lane = threadIdx.x & 63;
     const int64_t gw = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     const int64_t total = (int64_t)B * H * S;
@@ -260,6 +263,7 @@ __global__ __launch_bounds__(256) void attn_generic_kernel(const float *__restri
         }
     }
     const float inv = 1.0f / fmaxf(l, 1e-30f);
+    if (lse && lane == 0) lse[(row_base + i) * H + h] = (m + logf(fmaxf(l, 1e-30f))) * kLog2e;
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
         const int d = lane + 64 * c;
@@ -271,9 +275,9 @@ bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 
 
 }  // namespace
 
-void attention_core_f32(hipStream_t s, const float *q, const float *k, const float *v,
-                        int64_t ld_qkv, float *ctx, int64_t ldo, int64_t batch, int64_t seq,
-                        int64_t n_heads, int64_t d_head, bool causal) {
+static void attention_fwd(hipStream_t s, const float *q, const float *k, const float *v,
+                          int64_t ld_qkv, float *ctx, int64_t ldo, float *lse, int64_t batch,
+                          int64_t seq, int64_t n_heads, int64_t d_head, bool causal) {
     CATNN_REQUIRE(batch >= 0 && seq >= 0 && n_heads > 0 && d_head > 0, CATNN_ERR_SHAPE_MISMATCH,
                   "attention: bad dims");
     CATNN_REQUIRE(d_head <= 256, CATNN_ERR_SHAPE_MISMATCH, "attention: d_head > 256");
@@ -289,16 +293,29 @@ void attention_core_f32(hipStream_t s, const float *q, const float *k, const flo
         const int64_t blocks = batch * n_heads * nqb;
         CATNN_REQUIRE(blocks < (1ll << 31), CATNN_ERR_SHAPE_MISMATCH, "attention: grid too large");
         attn_mfma_kernel<64><<<(unsigned)blocks, 256, 0, s>>>(
-            q, k, v, ld_qkv, ctx, ldo, (int)seq, (int)n_heads, scale * kLog2e, causal ? 1 : 0, nqb);
+            q, k, v, ld_qkv, ctx, ldo, lse, (int)seq, (int)n_heads, scale * kLog2e, causal ? 1 : 0,
+            nqb);
     } else {
         const int64_t waves = batch * n_heads * seq;
         const int64_t blocks = (waves + 3) / 4;
         CATNN_REQUIRE(blocks < (1ll << 31), CATNN_ERR_SHAPE_MISMATCH, "attention: grid too large");
-        attn_generic_kernel<<<(unsigned)blocks, 256, 0, s>>>(q, k, v, ld_qkv, ctx, ldo, (int)batch,
-                                                             (int)seq, (int)n_heads, (int)d_head,
-                                                             scale, causal ? 1 : 0);
+        attn_generic_kernel<<<(unsigned)blocks, 256, 0, s>>>(q, k, v, ld_qkv, ctx, ldo, lse,
+                                                             (int)batch, (int)seq, (int)n_heads,
+                                                             (int)d_head, scale, causal ? 1 : 0);
     }
     CATNN_HIP(hipGetLastError());
+}
+
+void attention_core_f32(hipStream_t s, const float *q, const float *k, const float *v,
+                        int64_t ld_qkv, float *ctx, int64_t ldo, int64_t batch, int64_t seq,
+                        int64_t n_heads, int64_t d_head, bool causal) {
+    attention_fwd(s, q, k, v, ld_qkv, ctx, ldo, nullptr, batch, seq, n_heads, d_head, causal);
+}
+
+void attention_core_fwd_lse(hipStream_t s, const float *q, const float *k, const float *v, int64_t ld,
+                            float *ctx, int64_t ldo, float *lse, int64_t batch, int64_t seq,
+                            int64_t n_heads, int64_t d_head, bool causal) {
+    attention_fwd(s, q, k, v, ld, ctx, ldo, lse, batch, seq, n_heads, d_head, causal);
 }
 
 }  // namespace k

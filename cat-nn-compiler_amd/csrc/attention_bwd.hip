@@ -1,0 +1,450 @@
+// Adjoint of the attention core (the score/softmax/PV part of
+// attention_backward, crates/catnn-compile/src/kernel/adjoint.rs:582-722; the
+// causal window as gqa_backward, adjoint.rs:372-405), fp32 MFMA, from the
+// log-sum-exp the forward stored instead of the S×S probability matrix the
+// reference keeps:
+//   P  = exp2(S·log2e/√dh − lse),   D_i = Σ_d dO[i][d]·O[i][d],
+//   dV = Pᵀ·dO,   dS = P ∘ (dO·Vᵀ − D),   dK = dSᵀ·Q/√dh,   dQ = dS·K/√dh.
+// Two deterministic kernels, no atomics:
+//  * dK/dV: a block owns 128 keys of one (b, h); with S = Q·Kᵀ computed as
+//    A = Q (LDS), B = K (registers), lane l holds the scores of key l%32, so
+//    dVᵀ += dOᵀ·P and dKᵀ += Qᵀ·dS accumulate per key in registers and P, dS
+//    sit exactly where the MFMA reads its B operand;
+//  * dQ: a block owns 128 queries, the transposed frame of the forward
+//    (Sᵀ = K·Qᵀ, dPᵀ = V·dOᵀ, dQᵀ += Kᵀ·dSᵀ), lane l owning query l%32.
+// Other head sizes use one-wavefront-per-row kernels.
+#include <hip/hip_runtime.h>
+
+#include "common.hpp"
+#include "devmath.hpp"
+#include "train_ops.hpp"
+
+namespace catnn {
+namespace k {
+
+namespace {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+// D[row·H + h] = Σ_d dO·O over head h.
+__global__ __launch_bounds__(256) void attn_dot_kernel(const float *__restrict__ o,
+                                                       const float *__restrict__ dout, int64_t ldo,
+                                                       int64_t rows, int H, int DH,
+                                                       float *__restrict__ D) {
+    const int lane = threadIdx.x & 63;
+    const int64_t gw = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (gw >= rows * H) return;
+    const int64_t row = gw / H;
+    const int h = (int)(gw % H);
+    float s = 0.f;
+    for (int d = lane; d < DH; d += 64)
+        s += o[row * ldo + (int64_t)h * DH + d] * dout[row * ldo + (int64_t)h * DH + d];
+    s = wave_sum(s);
+    if (lane == 0) D[gw] = s;
+}
+
+template <int DH>
+__global__ __launch_bounds__(256, 2) void attn_bwd_dkdv_kernel(
+    const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v, int64_t ld,
+    const float *__restrict__ dout, int64_t ldo, const float *__restrict__ lse,
+    const float *__restrict__ Dv, float *__restrict__ dk, float *__restrict__ dv, int64_t ldd, int S,
+    int H, float qscale, float scale, int causal, int n_kblocks) {
+    static_assert(DH == 64, "written for d_head = 64");
+    constexpr int BKEY = 128, BQ = 64, LDQ = DH + 4;
+    constexpr int IT = BQ * DH / 4 / 256;
+    __shared__ float Qs[BQ][LDQ];
+    __shared__ float Os[BQ][LDQ];
+    __shared__ float Ls[BQ], Ds[BQ];
+
+    const int bid = blockIdx.x;
+    const int kb = bid % n_kblocks;  // low key blocks see the most queries: first
+    const int bh = bid / n_kblocks;
+    const int b = bh / H, h = bh % H;
+    const int k0 = kb * BKEY;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int lr = lane & 31, g = lane >> 5;
+    const int kj = k0 + wave * 32 + lr;
+    const int wave_kmin = k0 + wave * 32;
+    const int64_t row_base = (int64_t)b * S;
+
+    float kf[32], vf[32];
+    if (kj < S) {
+        const float4 *ks = reinterpret_cast<const float4 *>(k + (row_base + kj) * ld + (int64_t)h * DH + 32 * g);
+        const float4 *vs = reinterpret_cast<const float4 *>(v + (row_base + kj) * ld + (int64_t)h * DH + 32 * g);
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            const float4 a = ks[c], bb = vs[c];
+            kf[4 * c] = a.x; kf[4 * c + 1] = a.y; kf[4 * c + 2] = a.z; kf[4 * c + 3] = a.w;
+            vf[4 * c] = bb.x; vf[4 * c + 1] = bb.y; vf[4 * c + 2] = bb.z; vf[4 * c + 3] = bb.w;
+        }
+    } else {
+#pragma unroll
+        for (int s = 0; s < 32; ++s) kf[s] = vf[s] = 0.f;
+    }
+    f32x16 dka[DH / 32], dva[DH / 32];
+#pragma unroll
+    for (int db = 0; db < DH / 32; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) dka[db][r] = dva[db][r] = 0.f;
+
+    const int q_start = causal ? (k0 / BQ) * BQ : 0;
+    for (int q0 = q_start; q0 < S; q0 += BQ) {
+#pragma unroll
+        for (int it = 0; it < IT; ++it) {
+            const int idx = tid + it * 256;
+            const int r = idx / (DH / 4), c4 = idx % (DH / 4);
+            const int qi = q0 + r;
+            float4 a = make_float4(0.f, 0.f, 0.f, 0.f), d = a;
+            if (qi < S) {
+                a = *reinterpret_cast<const float4 *>(q + (row_base + qi) * ld + (int64_t)h * DH + 4 * c4);
+                d = *reinterpret_cast<const float4 *>(dout + (row_base + qi) * ldo + (int64_t)h * DH + 4 * c4);
+            }
+            *reinterpret_cast<float4 *>(&Qs[r][4 * c4]) = a;
+            *reinterpret_cast<float4 *>(&Os[r][4 * c4]) = d;
+        }
+        if (tid < BQ) {
+            const int qi = q0 + tid;
+            Ls[tid] = qi < S ? lse[(row_base + qi) * H + h] : 0.f;
+            Ds[tid] = qi < S ? Dv[(row_base + qi) * H + h] : 0.f;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int qb = 0; qb < BQ / 32; ++qb) {
+            const int qs0 = q0 + qb * 32;
+            const bool active = qs0 < S && (!causal || qs0 + 31 >= wave_kmin);  // wave-uniform
+            if (!active) continue;
+            f32x16 sa, pa;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) sa[r] = pa[r] = 0.f;
+            const float *qrow = &Qs[qb * 32 + lr][32 * g];
+            const float *orow = &Os[qb * 32 + lr][32 * g];
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+                const float4 qv = *reinterpret_cast<const float4 *>(qrow + 4 * c);
+                const float4 ov = *reinterpret_cast<const float4 *>(orow + 4 * c);
+                sa = __builtin_amdgcn_mfma_f32_32x32x2f32(qv.x, kf[4 * c + 0], sa, 0, 0, 0);
+                sa = __builtin_amdgcn_mfma_f32_32x32x2f32(qv.y, kf[4 * c + 1], sa, 0, 0, 0);
+                sa = __builtin_amdgcn_mfma_f32_32x32x2f32(qv.z, kf[4 * c + 2], sa, 0, 0, 0);
+                sa = __builtin_amdgcn_mfma_f32_32x32x2f32(qv.w, kf[4 * c + 3], sa, 0, 0, 0);
+                pa = __builtin_amdgcn_mfma_f32_32x32x2f32(ov.x, vf[4 * c + 0], pa, 0, 0, 0);
+                pa = __builtin_amdgcn_mfma_f32_32x32x2f32(ov.y, vf[4 * c + 1], pa, 0, 0, 0);
+                pa = __builtin_amdgcn_mfma_f32_32x32x2f32(ov.z, vf[4 * c + 2], pa, 0, 0, 0);
+                pa = __builtin_amdgcn_mfma_f32_32x32x2f32(ov.w, vf[4 * c + 3], pa, 0, 0, 0);
+            }
+            // Entry r holds query row qs0 + 8(r/4) + 4g + r%4 of key kj.
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int il = qb * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+                const int qi = q0 + il;
+                const bool ok = qi < S && kj < S && (!causal || kj <= qi);
+                const float p = ok ? exp2f(sa[r] * qscale - Ls[il]) : 0.f;
+                pa[r] = p * (pa[r] - Ds[il]);
+                sa[r] = p;
+            }
+            // dVᵀ[d][j] += Σ_i dO[i][d]·P[i][j];  dKᵀ[d][j] += Σ_i Q[i][d]·dS[i][j]
+#pragma unroll
+            for (int s = 0; s < 16; ++s) {
+                const int il = qb * 32 + 8 * (s >> 2) + 4 * g + (s & 3);
+#pragma unroll
+                for (int db = 0; db < DH / 32; ++db) {
+                    dva[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(Os[il][db * 32 + lr], sa[s], dva[db], 0, 0, 0);
+                    dka[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(Qs[il][db * 32 + lr], pa[s], dka[db], 0, 0, 0);
+                }
+            }
+        }
+        __syncthreads();
+    }
+    if (kj < S) {
+        float *dkr = dk + (row_base + kj) * ldd + (int64_t)h * DH;
+        float *dvr = dv + (row_base + kj) * ldd + (int64_t)h * DH;
+#pragma unroll
+        for (int db = 0; db < DH / 32; ++db)
+#pragma unroll
+            for (int r4 = 0; r4 < 4; ++r4) {
+                const int d = db * 32 + 8 * r4 + 4 * g;
+                *reinterpret_cast<float4 *>(dkr + d) =
+                    make_float4(dka[db][4 * r4] * scale, dka[db][4 * r4 + 1] * scale,
+                                dka[db][4 * r4 + 2] * scale, dka[db][4 * r4 + 3] * scale);
+                *reinterpret_cast<float4 *>(dvr + d) =
+                    make_float4(dva[db][4 * r4], dva[db][4 * r4 + 1], dva[db][4 * r4 + 2], dva[db][4 * r4 + 3]);
+            }
+    }
+}
+
+template <int DH>
+__global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(
+    const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v, int64_t ld,
+    const float *__restrict__ dout, int64_t ldo, const float *__restrict__ lse,
+    const float *__restrict__ Dv, float *__restrict__ dq, int64_t ldd, int S, int H, float qscale,
+    float scale, int causal, int n_qblocks) {
+    static_assert(DH == 64, "written for d_head = 64");
+    constexpr int BQ = 128, BKV = 64, LDK = DH + 4;
+    constexpr int KV_IT = BKV * DH / 4 / 256;
+    __shared__ float Ks[1][BKV][LDK];
+    __shared__ float Vs[1][BKV][LDK];
+
+    const int bid = blockIdx.x;
+    const int qb = n_qblocks - 1 - (bid % n_qblocks);
+    const int bh = bid / n_qblocks;
+    const int b = bh / H, h = bh % H;
+    const int q0 = qb * BQ;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int lr = lane & 31, g = lane >> 5;
+    const int qi = q0 + wave * 32 + lr;
+    const int wave_qmax = q0 + wave * 32 + 31;
+    const int64_t row_base = (int64_t)b * S;
+
+    float qf[32], of[32];
+    float lse_i = 0.f, D_i = 0.f;
+    if (qi < S) {
+        const float4 *qs = reinterpret_cast<const float4 *>(q + (row_base + qi) * ld + (int64_t)h * DH + 32 * g);
+        const float4 *os = reinterpret_cast<const float4 *>(dout + (row_base + qi) * ldo + (int64_t)h * DH + 32 * g);
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            const float4 a = qs[c], bb = os[c];
+            qf[4 * c] = a.x * qscale; qf[4 * c + 1] = a.y * qscale;
+            qf[4 * c + 2] = a.z * qscale; qf[4 * c + 3] = a.w * qscale;
+            of[4 * c] = bb.x; of[4 * c + 1] = bb.y; of[4 * c + 2] = bb.z; of[4 * c + 3] = bb.w;
+        }
+        lse_i = lse[(row_base + qi) * H + h];
+        D_i = Dv[(row_base + qi) * H + h];
+    } else {
+#pragma unroll
+        for (int s = 0; s < 32; ++s) qf[s] = of[s] = 0.f;
+    }
+    f32x16 dqa[DH / 32];
+#pragma unroll
+    for (int db = 0; db < DH / 32; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) dqa[db][r] = 0.f;
+
+    const int kv_end = causal ? min(S, q0 + BQ) : S;
+    const int ntiles = (kv_end + BKV - 1) / BKV;
+    for (int t = 0; t < ntiles; ++t) {
+        const int buf = 0;
+#pragma unroll
+        for (int it = 0; it < KV_IT; ++it) {
+            const int idx = tid + it * 256;
+            const int kr = idx / (DH / 4), c4 = idx % (DH / 4);
+            const int key = t * BKV + kr;
+            float4 a = make_float4(0.f, 0.f, 0.f, 0.f), bb = a;
+            if (key < S) {
+                const int64_t off = (row_base + key) * ld + (int64_t)h * DH + 4 * c4;
+                a = *reinterpret_cast<const float4 *>(k + off);
+                bb = *reinterpret_cast<const float4 *>(v + off);
+            }
+            *reinterpret_cast<float4 *>(&Ks[buf][kr][4 * c4]) = a;
+            *reinterpret_cast<float4 *>(&Vs[buf][kr][4 * c4]) = bb;
+        }
+        __syncthreads();
+        const int j0 = t * BKV;
+        for (int kb = 0; kb < BKV / 32; ++kb) {
+            const int jb = j0 + kb * 32;
+            if (!(jb < S && (!causal || jb <= wave_qmax))) continue;  // wave-uniform
+            f32x16 sa, pa;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) sa[r] = pa[r] = 0.f;
+            {
+                const float *krow = &Ks[buf][kb * 32 + lr][32 * g];
+                const float *vrow = &Vs[buf][kb * 32 + lr][32 * g];
+#pragma unroll
+                for (int c = 0; c < 8; ++c) {
+                    const float4 kv = *reinterpret_cast<const float4 *>(krow + 4 * c);
+                    const float4 vv = *reinterpret_cast<const float4 *>(vrow + 4 * c);
+                    sa = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.x, qf[4 * c + 0], sa, 0, 0, 0);
+                    sa = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.y, qf[4 * c + 1], sa, 0, 0, 0);
+                    sa = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.z, qf[4 * c + 2], sa, 0, 0, 0);
+                    sa = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.w, qf[4 * c + 3], sa, 0, 0, 0);
+                    pa = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.x, of[4 * c + 0], pa, 0, 0, 0);
+                    pa = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.y, of[4 * c + 1], pa, 0, 0, 0);
+                    pa = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.z, of[4 * c + 2], pa, 0, 0, 0);
+                    pa = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.w, of[4 * c + 3], pa, 0, 0, 0);
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int j = jb + 8 * (r >> 2) + 4 * g + (r & 3);
+                const bool ok = qi < S && j < S && (!causal || j <= qi);
+                const float p = ok ? exp2f(sa[r] - lse_i) : 0.f;
+                pa[r] = p * (pa[r] - D_i);  // dSᵀ entry
+            }
+            // dQᵀ[d][i] += Σ_j K[j][d]·dSᵀ[j][i]
+#pragma unroll
+            for (int s = 0; s < 16; ++s) {
+                const int jl = kb * 32 + 8 * (s >> 2) + 4 * g + (s & 3);
+#pragma unroll
+                for (int db = 0; db < DH / 32; ++db)
+                    dqa[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(Ks[buf][jl][db * 32 + lr], pa[s], dqa[db], 0, 0, 0);
+            }
+        }
+        __syncthreads();
+    }
+    if (qi < S) {
+        float *dst = dq + (row_base + qi) * ldd + (int64_t)h * DH;
+#pragma unroll
+        for (int db = 0; db < DH / 32; ++db)
+#pragma unroll
+            for (int r4 = 0; r4 < 4; ++r4) {
+                const int d = db * 32 + 8 * r4 + 4 * g;
+                *reinterpret_cast<float4 *>(dst + d) =
+                    make_float4(dqa[db][4 * r4] * scale, dqa[db][4 * r4 + 1] * scale,
+                                dqa[db][4 * r4 + 2] * scale, dqa[db][4 * r4 + 3] * scale);
+            }
+    }
+}
+
+// Any head size ≤ 256: one wavefront per (b, h, query) for dQ ...
+__global__ __launch_bounds__(256) void attn_bwd_dq_generic(
+    const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v, int64_t ld,
+    const float *__restrict__ dout, int64_t ldo, const float *__restrict__ lse,
+    const float *__restrict__ Dv, float *__restrict__ dq, int64_t ldd, int B, int S, int H, int DH,
+    float scale, int causal) {
+    const int lane = threadIdx.x & 63;
+    const int64_t gw = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (gw >= (int64_t)B * H * S) return;
+    const int i = (int)(gw % S);
+    const int64_t bh = gw / S;
+    const int h = (int)(bh % H), b = (int)(bh / H);
+    const int64_t rb = (int64_t)b * S;
+    float qv[4], ov[4], acc[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const int d = lane + 64 * c;
+        qv[c] = d < DH ? q[(rb + i) * ld + (int64_t)h * DH + d] : 0.f;
+        ov[c] = d < DH ? dout[(rb + i) * ldo + (int64_t)h * DH + d] : 0.f;
+        acc[c] = 0.f;
+    }
+    const float l2 = lse[(rb + i) * H + h], Di = Dv[(rb + i) * H + h];
+    const int jend = causal ? i + 1 : S;
+    for (int j = 0; j < jend; ++j) {
+        const float *kr = k + (rb + j) * ld + (int64_t)h * DH;
+        const float *vr = v + (rb + j) * ld + (int64_t)h * DH;
+        float sp = 0.f, dp = 0.f;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int d = lane + 64 * c;
+            if (d < DH) {
+                sp += qv[c] * kr[d];
+                dp += ov[c] * vr[d];
+            }
+        }
+        const float p = exp2f(wave_sum(sp) * scale * kLog2e - l2);
+        const float dsv = p * (wave_sum(dp) - Di);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int d = lane + 64 * c;
+            if (d < DH) acc[c] += dsv * kr[d];
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const int d = lane + 64 * c;
+        if (d < DH) dq[(rb + i) * ldd + (int64_t)h * DH + d] = acc[c] * scale;
+    }
+}
+
+// ... and one wavefront per (b, h, key) for dK and dV.
+__global__ __launch_bounds__(256) void attn_bwd_dkdv_generic(
+    const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v, int64_t ld,
+    const float *__restrict__ dout, int64_t ldo, const float *__restrict__ lse,
+    const float *__restrict__ Dv, float *__restrict__ dk, float *__restrict__ dv, int64_t ldd, int B,
+    int S, int H, int DH, float scale, int causal) {
+    const int lane = threadIdx.x & 63;
+    const int64_t gw = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (gw >= (int64_t)B * H * S) return;
+    const int j = (int)(gw % S);
+    const int64_t bh = gw / S;
+    const int h = (int)(bh % H), b = (int)(bh / H);
+    const int64_t rb = (int64_t)b * S;
+    float kv[4], vv[4], ak[4], av[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const int d = lane + 64 * c;
+        kv[c] = d < DH ? k[(rb + j) * ld + (int64_t)h * DH + d] : 0.f;
+        vv[c] = d < DH ? v[(rb + j) * ld + (int64_t)h * DH + d] : 0.f;
+        ak[c] = av[c] = 0.f;
+    }
+    for (int i = causal ? j : 0; i < S; ++i) {
+        const float *qr = q + (rb + i) * ld + (int64_t)h * DH;
+        const float *orr = dout + (rb + i) * ldo + (int64_t)h * DH;
+        float sp = 0.f, dp = 0.f;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int d = lane + 64 * c;
+            if (d < DH) {
+                sp += qr[d] * kv[c];
+                dp += orr[d] * vv[c];
+            }
+        }
+        const float p = exp2f(wave_sum(sp) * scale * kLog2e - lse[(rb + i) * H + h]);
+        const float dsv = p * (wave_sum(dp) - Dv[(rb + i) * H + h]);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int d = lane + 64 * c;
+            if (d < DH) {
+                av[c] += p * orr[d];
+                ak[c] += dsv * qr[d];
+            }
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const int d = lane + 64 * c;
+        if (d < DH) {
+            dk[(rb + j) * ldd + (int64_t)h * DH + d] = ak[c] * scale;
+            dv[(rb + j) * ldd + (int64_t)h * DH + d] = av[c];
+        }
+    }
+}
+
+bool al16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+}  // namespace
+
+uint64_t attention_bwd_scratch_bytes(int64_t batch, int64_t seq, int64_t n_heads) {
+    return (uint64_t)(batch * seq * n_heads) * 4;
+}
+
+void attention_core_bwd(hipStream_t s, const float *q, const float *k, const float *v, int64_t ld,
+                        const float *o, const float *dout, int64_t ldo, const float *lse, float *dq,
+                        float *dk, float *dv, int64_t ld_d, int64_t batch, int64_t seq,
+                        int64_t n_heads, int64_t d_head, bool causal, float *scratch) {
+    CATNN_REQUIRE(batch >= 0 && seq >= 0 && n_heads > 0 && d_head > 0 && d_head <= 256,
+                  CATNN_ERR_SHAPE_MISMATCH, "attention backward: bad dims");
+    CATNN_REQUIRE(batch * seq * n_heads < (1ll << 31), CATNN_ERR_SHAPE_MISMATCH,
+                  "attention backward: too many rows");
+    if (batch == 0 || seq == 0) return;
+    const int64_t rows = batch * seq;
+    float *D = scratch;
+    attn_dot_kernel<<<(unsigned)((rows * n_heads + 3) / 4), 256, 0, s>>>(o, dout, ldo, rows, (int)n_heads,
+                                                                        (int)d_head, D);
+    CATNN_HIP(hipGetLastError());
+    const float scale = 1.0f / sqrtf((float)d_head);
+    const bool mfma = d_head == 64 && ld % 4 == 0 && ldo % 4 == 0 && ld_d % 4 == 0 && al16(q) &&
+                      al16(k) && al16(v) && al16(dout) && al16(dq) && al16(dk) && al16(dv);
+    if (mfma) {
+        const int nkb = (int)((seq + 127) / 128);
+        attn_bwd_dkdv_kernel<64><<<(unsigned)(batch * n_heads * nkb), 256, 0, s>>>(
+            q, k, v, ld, dout, ldo, lse, D, dk, dv, ld_d, (int)seq, (int)n_heads, scale * kLog2e, scale,
+            causal ? 1 : 0, nkb);
+        CATNN_HIP(hipGetLastError());
+        attn_bwd_dq_kernel<64><<<(unsigned)(batch * n_heads * nkb), 256, 0, s>>>(
+            q, k, v, ld, dout, ldo, lse, D, dq, ld_d, (int)seq, (int)n_heads, scale * kLog2e, scale,
+            causal ? 1 : 0, nkb);
+        CATNN_HIP(hipGetLastError());
+    } else {
+        const unsigned blocks = (unsigned)((batch * n_heads * seq + 3) / 4);
+        attn_bwd_dq_generic<<<blocks, 256, 0, s>>>(q, k, v, ld, dout, ldo, lse, D, dq, ld_d, (int)batch,
+                                                   (int)seq, (int)n_heads, (int)d_head, scale,
+                                                   causal ? 1 : 0);
+        attn_bwd_dkdv_generic<<<blocks, 256, 0, s>>>(q, k, v, ld, dout, ldo, lse, D, dk, dv, ld_d,
+                                                     (int)batch, (int)seq, (int)n_heads, (int)d_head,
+                                                     scale, causal ? 1 : 0);
+        CATNN_HIP(hipGetLastError());
+    }
+}
+
+}  // namespace k
+}  // namespace catnn

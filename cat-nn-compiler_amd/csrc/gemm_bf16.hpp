@@ -1,0 +1,75 @@
+// bf16 MFMA GEMM of the training path (gemm_bf16.hip).
+//
+// C[M,N] = Σ_k A[m][k]·B[n][k]: both operands bf16 and k-contiguous (the
+// second one is stored "transposed", [N,K]); fp32 accumulation.  A weight
+// W [K,N] therefore enters the forward as its transposed bf16 copy and the
+// input-gradient GEMM as its own bf16 copy; weight gradients take both
+// activations transposed.
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+
+#include <cstdint>
+
+#include "gemm_f32.hpp"
+
+namespace catnn {
+namespace k {
+
+typedef uint16_t bf16_t;  // storage type of bf16 values on the host side
+
+enum Bf16Epi : int {
+    EPI_STORE = 0,       // C32 (= or +=) acc, Cb = bf16(acc)
+    EPI_LINEAR = 1,      // v = acc + bias; Z = v; v = act(v); v = R + v; C32/Cb = v
+    EPI_GELU_BWD = 2,    // v = acc · gelu'(Z); C32/Cb = v
+    EPI_SWIGLU_FWD = 3,  // dual B: save a, c (bf16) to S1, S2; Cb = bf16(silu(a)·c)
+    EPI_SWIGLU_BWD = 4,  // a = S1, c = S2: Cb = bf16(acc·c·silu'(a)), Cb2 = bf16(acc·silu(a))
+};
+
+enum Bf16Grid : int { GRID_PLAIN = 0, GRID_ROWS = 1, GRID_SEGK = 2 };
+
+struct GemmBf16Params {
+    const bf16_t *A;
+    int64_t lda;
+    const int32_t *a_rows;  // logical row r reads source row a_rows[r] / a_row_div
+    int a_row_div;
+    const bf16_t *B;
+    const bf16_t *B2;       // dual mode second operand (W3ᵀ)
+    int64_t ldb;
+    int M, N, K;
+    int epi;
+    int act;
+    // outputs
+    float *C32;
+    int64_t ldc32;
+    int accumulate;
+    bf16_t *Cb;
+    int64_t ldcb;
+    bf16_t *Cb2;
+    const float *bias;
+    const float *R;
+    int64_t ldr;
+    float *Z;               // EPI_LINEAR: pre-activation out; EPI_GELU_BWD: pre-activation in
+    int64_t ldz;
+    bf16_t *S1, *S2;        // SwiGLU saved a / c
+    int64_t lds;
+    // grouped grids
+    int grid;
+    const int32_t *tile_expert;
+    const int32_t *tile_row0;
+    const int32_t *n_tiles;
+    const int32_t *seg_offsets;  // segment e starts at seg_offsets[e]
+    const int32_t *seg_counts;   // ... and holds seg_counts[e] rows (null: ends at seg_offsets[e+1])
+    int segk_aligned;            // GRID_SEGK: caller guarantees seg_offsets[e] % 8 == 0
+    int max_tiles;
+    int n_experts;
+    const bf16_t *B_e[kMaxExperts];
+    const bf16_t *B2_e[kMaxExperts];
+    float *C_e[kMaxExperts];  // GRID_SEGK: output of expert e
+};
+
+void gemm_bf16_launch(hipStream_t s, const GemmBf16Params &p);
+int gemm_bf16_tile_rows();
+
+}  // namespace k
+}  // namespace catnn

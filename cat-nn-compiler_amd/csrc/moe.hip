@@ -31,6 +31,7 @@
 #include "devmath.hpp"
 #include "gemm_f32.hpp"
 #include "kernels.hpp"
+#include "train_ops.hpp"
 
 namespace catnn {
 namespace k {
@@ -139,7 +140,8 @@ __global__ __launch_bounds__(256) void perm_count_kernel(const int32_t *__restri
 
 // counts, offsets (exclusive prefix, length E+1) and each block's starting
 // position per expert.  One wavefront; thread e owns expert e.
-__global__ void perm_scan_kernel(const int32_t *__restrict__ block_counts, int nb, int E,
+// With pad > 1 every expert segment starts on a multiple of pad rows.
+__global__ void perm_scan_kernel(const int32_t *__restrict__ block_counts, int nb, int E, int pad,
                                  int32_t *__restrict__ block_base, int32_t *__restrict__ counts,
                                  int32_t *__restrict__ offsets) {
     __shared__ int tot[kMaxExperts + 1];
@@ -160,7 +162,7 @@ __global__ void perm_scan_kernel(const int32_t *__restrict__ block_counts, int n
             const int t = tot[c];
             tot[c] = acc;
             offsets[c] = acc;
-            acc += t;
+            acc += (t + pad - 1) / pad * pad;
         }
         offsets[E] = acc;
     }
@@ -264,6 +266,18 @@ bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 
 
 }  // namespace
 
+void moe_combine(hipStream_t s, const float *y, const int32_t *pos_of_slot, const float *w,
+                 int64_t tokens, int64_t top_k, int64_t hidden, float *out) {
+    if (tokens <= 0) return;
+    if (hidden % 4 == 0 && aligned16(out) && aligned16(y))
+        combine4_kernel<<<(unsigned)tokens, 256, 0, s>>>(y, pos_of_slot, w, (int)tokens, (int)top_k,
+                                                         (int)hidden, out);
+    else
+        combine_kernel<<<(unsigned)tokens, 256, 0, s>>>(y, pos_of_slot, w, (int)tokens, (int)top_k,
+                                                        (int)hidden, out);
+    CATNN_HIP(hipGetLastError());
+}
+
 void moe_route_f32(hipStream_t s, const float *x, const float *gate, int64_t tokens, int64_t hidden,
                    int64_t n_experts, int64_t top_k, int32_t *idx, float *w, float *logits) {
     CATNN_REQUIRE(tokens >= 0 && hidden > 0 && n_experts > 0, CATNN_ERR_SHAPE_MISMATCH,
@@ -311,7 +325,37 @@ void moe_permute(hipStream_t s, const int32_t *idx, int64_t tokens, int64_t top_
         perm_count_kernel<<<(unsigned)nb, 256, 0, s>>>(idx, n, E, block_counts, bad);
         CATNN_HIP(hipGetLastError());
     }
-    perm_scan_kernel<<<1, 64, 0, s>>>(block_counts, (int)nb, E, block_base, counts, offsets);
+    perm_scan_kernel<<<1, 64, 0, s>>>(block_counts, (int)nb, E, 1, block_base, counts, offsets);
+    CATNN_HIP(hipGetLastError());
+    if (nb > 0) {
+        perm_scatter_kernel<<<(unsigned)nb, 256, 0, s>>>(idx, n, E, block_base, slot_of_pos,
+                                                         pos_of_slot);
+        CATNN_HIP(hipGetLastError());
+    }
+}
+
+void moe_permute_padded(hipStream_t s, const int32_t *idx, int64_t tokens, int64_t top_k,
+                        int64_t n_experts, int pad, int64_t n_pos_cap, int32_t *counts,
+                        int32_t *offsets, int32_t *slot_of_pos, int32_t *pos_of_slot,
+                        void *scratch) {
+    CATNN_REQUIRE(n_experts > 0 && n_experts <= kMaxExperts && pad >= 1, CATNN_ERR_SHAPE_MISMATCH,
+                  "permute: bad expert count or pad");
+    const int64_t n = tokens * top_k;
+    CATNN_REQUIRE(n_pos_cap >= n + n_experts * (pad - 1) && n_pos_cap < (1ll << 31),
+                  CATNN_ERR_SHAPE_MISMATCH, "permute: position capacity too small");
+    const int E = (int)n_experts;
+    const int64_t nb = (n + kPermChunk - 1) / kPermChunk;
+    char *sc = static_cast<char *>(scratch);
+    int32_t *block_counts = reinterpret_cast<int32_t *>(sc);
+    int32_t *block_base = reinterpret_cast<int32_t *>(sc + align256((uint64_t)nb * E * 4));
+    int32_t *bad = reinterpret_cast<int32_t *>(sc + 2 * align256((uint64_t)nb * E * 4));
+    CATNN_HIP(hipMemsetAsync(bad, 0, 4, s));
+    CATNN_HIP(hipMemsetAsync(slot_of_pos, 0xff, (size_t)n_pos_cap * 4, s));  // −1: padding
+    if (nb > 0) {
+        perm_count_kernel<<<(unsigned)nb, 256, 0, s>>>(idx, n, E, block_counts, bad);
+        CATNN_HIP(hipGetLastError());
+    }
+    perm_scan_kernel<<<1, 64, 0, s>>>(block_counts, (int)nb, E, pad, block_base, counts, offsets);
     CATNN_HIP(hipGetLastError());
     if (nb > 0) {
         perm_scatter_kernel<<<(unsigned)nb, 256, 0, s>>>(idx, n, E, block_base, slot_of_pos,

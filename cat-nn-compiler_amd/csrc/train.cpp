@@ -1,0 +1,831 @@
+// Training step of an IrGraph on one device: the device counterpart of
+// pipeline::reference_train (crates/catnn-compile/src/pipeline.rs:476-547)
+// for one step with MSE and SGD, i.e. of the three seams that bypass the
+// handler in the reference's training wave — adjoint_of (coord.rs:413),
+// rematerialisation (coord.rs:470, not needed: every tape is kept) and
+// apply_update (coord.rs:481).
+//
+//   forward   topo order; every op stores the tape its adjoint needs;
+//   loss      MSE against the target (adjoint.rs:106-119);
+//   backward  reverse topo order, adjoint_of per node (adjoint.rs:762-951);
+//             a value's cotangent is written by the first of its consumers
+//             to run and accumulated by the others (add_tensors,
+//             adjoint.rs:22-24);
+//   update    p −= lr·g on the fp32 master weights (Sgd::put,
+//             lens/optim.rs:32-42), then the bf16 copies are refreshed.
+//
+// Precision: GEMM operands (activations, weights, cotangents) are bf16 on
+// v_mfma_f32_32x32x16_bf16 with fp32 accumulation; master weights, the
+// residual stream, LayerNorm, softmax statistics, the router and all
+// cotangent accumulation stay fp32.  The attention core runs on fp32 MFMA.
+//
+// Memory: every buffer (params, their bf16 copies and gradients, values,
+// cotangents, tapes, scratch) is a BufferReq on the reference's logical
+// ticks (pipeline.rs:280-284: forward = topo index t, loss = n, backward of
+// t = 2n − t, update = 2n + 1), placed by place_arena and backed by one
+// hipMalloc — the arena of schedule_device (pipeline.rs:272-401) made real.
+#include <algorithm>
+#include <cstring>
+#include <map>
+#include <memory>
+#include <set>
+
+#include "arena.hpp"
+#include "gemm_bf16.hpp"
+#include "graph.hpp"
+#include "kernels.hpp"
+#include "train_ops.hpp"
+
+namespace catnn {
+
+using k::bf16_t;
+
+namespace {
+
+int64_t numel(const std::vector<int64_t> &d) {
+    int64_t n = 1;
+    for (int64_t v : d) n *= v;
+    return n;
+}
+
+constexpr int kPad = 128;  // MoE expert segments start on multiples of the GEMM tile
+
+struct TParam {
+    std::string name;       // "param:{node}:{port}"
+    int64_t rows = 0, cols = 0;
+    std::vector<float> init;  // host values uploaded at install
+    bool want_b = false, want_bt = false;
+    float *master = nullptr, *grad = nullptr;
+    bf16_t *b = nullptr, *bt = nullptr;
+};
+
+struct TNode {
+    uint32_t id;
+    const Node *node;
+    size_t tick;
+    int kind;
+    std::vector<uint32_t> ins;
+    std::vector<std::vector<int64_t>> in_dims;
+    std::vector<bool> first_writer;  // per input: this adjoint overwrites the cotangent
+    std::vector<int64_t> dims;
+    std::map<std::string, TParam *> params;
+    // tapes and scratch (named pointers, assigned after planning)
+    std::map<std::string, void *> buf;
+    void *&B(const std::string &n) { return buf[n]; }
+};
+
+}  // namespace
+}  // namespace catnn
+
+struct catnn_hip_trainer {
+    catnn_hip_device *dev = nullptr;
+    catnn_graph graph;
+    float lr = 0.05f;
+    std::vector<catnn::TNode> nodes;
+    std::map<uint32_t, size_t> index;                 // node id → nodes[]
+    std::vector<std::unique_ptr<catnn::TParam>> params;
+    std::map<uint32_t, float *> val, grad;            // value / cotangent per node id
+    std::map<uint32_t, std::vector<int64_t>> dims;
+    std::set<uint32_t> input_ids;
+    std::set<uint32_t> has_grad;  // ids whose cotangent some adjoint (or the loss) writes
+    uint32_t out_id = 0;
+    float *target = nullptr, *loss = nullptr, *mse_scratch = nullptr;
+    std::vector<catnn::BufferReq> reqs;
+    std::vector<void **> req_slot;
+    std::vector<catnn::ArenaAlloc> plan;
+    void *base = nullptr;
+    uint64_t reserved = 0;
+};
+
+namespace catnn {
+
+namespace {
+
+using Tr = catnn_hip_trainer;
+
+void request(Tr &t, const std::string &id, uint64_t bytes, uint64_t from, uint64_t to, void **slot) {
+    t.reqs.push_back(BufferReq{id, (bytes + 255) & ~uint64_t(255), from, to, false});
+    t.req_slot.push_back(slot);
+}
+
+k::GemmBf16Params gp() {
+    k::GemmBf16Params p{};
+    p.a_row_div = 1;
+    return p;
+}
+
+// C32 (=/+=) A[M,K]·B[N,K]ᵀ on bf16 operands.
+void gemm_nt(hipStream_t s, const bf16_t *A, int64_t lda, const bf16_t *B, int64_t ldb, int M, int N,
+             int K, float *C, int64_t ldc, bool accumulate) {
+    k::GemmBf16Params p = gp();
+    p.A = A;
+    p.lda = lda;
+    p.B = B;
+    p.ldb = ldb;
+    p.M = M;
+    p.N = N;
+    p.K = K;
+    p.epi = k::EPI_STORE;
+    p.C32 = C;
+    p.ldc32 = ldc;
+    p.accumulate = accumulate ? 1 : 0;
+    k::gemm_bf16_launch(s, p);
+}
+
+void add_into(hipStream_t s, float *dst, const float *src, int64_t n, bool overwrite) {
+    if (overwrite) k::copy_f32(s, src, dst, n);
+    else k::add_f32(s, dst, src, dst, n, n);
+}
+
+}  // namespace
+
+static void plan_trainer(Tr &t) {
+    const catnn_graph &g = t.graph;
+    const std::vector<uint32_t> order = g.topo();
+    const uint64_t n = order.size();
+    auto bwd = [&](uint64_t tick) { return 2 * n - tick; };
+    const uint64_t upd = 2 * n + 1;
+    CATNN_REQUIRE(!g.outputs.empty(), CATNN_ERR_WIRING, "graph has no outputs");
+    t.out_id = g.outputs.back();
+    t.input_ids.insert(g.inputs.begin(), g.inputs.end());
+    for (size_t i = 0; i < order.size(); ++i) t.index[order[i]] = i;
+
+    // Shapes and nodes.
+    t.nodes.reserve(order.size());
+    for (size_t i = 0; i < order.size(); ++i) {
+        const uint32_t id = order[i];
+        const Node &nd = g.node(id);
+        TNode tn;
+        tn.id = id;
+        tn.node = &nd;
+        tn.tick = i;
+        tn.kind = nd.op.kind;
+        if (t.input_ids.count(id)) {
+            tn.dims = nd.output_ty.dims;
+        } else {
+            tn.ins = g.preds(id);
+            for (uint32_t v : tn.ins) tn.in_dims.push_back(t.dims.at(v));
+            tn.dims = infer_dims(nd, tn.in_dims);
+            switch (tn.kind) {
+                case CATNN_OP_IDENTITY: case CATNN_OP_RESHAPE: case CATNN_OP_TRANSPOSE:
+                case CATNN_OP_RELU: case CATNN_OP_GELU: case CATNN_OP_LINEAR: case CATNN_OP_MATMUL:
+                case CATNN_OP_LAYER_NORM: case CATNN_OP_ATTENTION: case CATNN_OP_MOE:
+                    break;
+                case CATNN_OP_ADD: case CATNN_OP_RESIDUAL_ADD:
+                    CATNN_REQUIRE(tn.ins.size() != 2 || numel(tn.in_dims[0]) == numel(tn.in_dims[1]),
+                                  CATNN_ERR_UNSUPPORTED,
+                                  "training: broadcast add (" + nd.name + ") has no device adjoint");
+                    break;
+                default:
+                    fail(CATNN_ERR_UNSUPPORTED, "training: op " + op_name(tn.kind) + " (node " + nd.name +
+                                                    ") has no device adjoint");
+            }
+        }
+        t.dims[id] = tn.dims;
+        t.nodes.push_back(std::move(tn));
+    }
+    // Which cotangents exist: the output's, and (backwards) every input of a
+    // node that itself has one.
+    t.has_grad.insert(t.out_id);
+    for (auto it = t.nodes.rbegin(); it != t.nodes.rend(); ++it)
+        if (t.has_grad.count(it->id))
+            for (uint32_t v : it->ins) t.has_grad.insert(v);
+    // Who writes each cotangent first: consumers run their adjoints in reverse
+    // topo order, so the consumer with the largest tick writes first.
+    std::map<uint32_t, size_t> first_consumer_tick;
+    for (auto &tn : t.nodes)
+        for (uint32_t v : tn.ins) {
+            if (!t.has_grad.count(tn.id)) continue;  // skipped in the backward pass
+            auto it = first_consumer_tick.find(v);
+            if (it == first_consumer_tick.end() || tn.tick > it->second) first_consumer_tick[v] = tn.tick;
+        }
+    for (auto &tn : t.nodes) {
+        std::set<uint32_t> seen;
+        for (uint32_t v : tn.ins) {
+            // Only the first occurrence of v in this node's inputs may overwrite.
+            const bool first = first_consumer_tick[v] == tn.tick && !seen.count(v);
+            tn.first_writer.push_back(first);
+            seen.insert(v);
+        }
+    }
+
+    // Values and cotangents.
+    std::map<uint32_t, uint64_t> last_read;  // last tick a value is read
+    for (auto &tn : t.nodes) {
+        last_read[tn.id] = std::max<uint64_t>(last_read[tn.id], tn.tick);
+        for (uint32_t v : tn.ins) last_read[v] = std::max<uint64_t>(last_read[v], bwd(tn.tick));
+    }
+    // The output value stays readable after the step (catnn_hip_train_read_value).
+    last_read[t.out_id] = upd;
+    for (auto &tn : t.nodes) {
+        const uint64_t bytes = (uint64_t)numel(tn.dims) * 4;
+        // The batch (inputs and target) stays resident across steps: set_batch
+        // once, step many times.
+        const bool is_input = t.input_ids.count(tn.id) != 0;
+        request(t, "act:" + std::to_string(tn.id), bytes, is_input ? 0 : tn.tick,
+                is_input ? upd : last_read[tn.id], reinterpret_cast<void **>(&t.val[tn.id]));
+        if (is_input) continue;
+        const uint64_t from = tn.id == t.out_id ? n : bwd(first_consumer_tick.count(tn.id) ? first_consumer_tick[tn.id] : tn.tick);
+        request(t, "grad:" + std::to_string(tn.id), bytes, std::min<uint64_t>(from, bwd(tn.tick)),
+                bwd(tn.tick), reinterpret_cast<void **>(&t.grad[tn.id]));
+    }
+    request(t, "target", (uint64_t)numel(t.dims[t.out_id]) * 4, 0, upd, reinterpret_cast<void **>(&t.target));
+    request(t, "loss", 256, n, upd, reinterpret_cast<void **>(&t.loss));
+    request(t, "mse_scratch", k::mse_scratch_bytes(), n, n, reinterpret_cast<void **>(&t.mse_scratch));
+
+    auto add_param = [&](TNode &tn, const std::string &port, int64_t rows, int64_t cols, bool b, bool bt,
+                         std::vector<float> init) {
+        auto p = std::make_unique<TParam>();
+        p->name = "param:" + tn.node->name + ":" + port;
+        p->rows = rows;
+        p->cols = cols;
+        p->init = std::move(init);
+        p->want_b = b || bt;
+        p->want_bt = bt;
+        const uint64_t e = (uint64_t)(rows * cols);
+        request(t, p->name, e * 4, 0, upd, reinterpret_cast<void **>(&p->master));
+        request(t, "grad:" + p->name, e * 4, bwd(tn.tick), upd, reinterpret_cast<void **>(&p->grad));
+        if (p->want_b) request(t, "bf16:" + p->name, e * 2, 0, upd, reinterpret_cast<void **>(&p->b));
+        if (p->want_bt) request(t, "bf16t:" + p->name, e * 2, 0, upd, reinterpret_cast<void **>(&p->bt));
+        tn.params[port] = p.get();
+        t.params.push_back(std::move(p));
+    };
+    auto host = [](const Node &nd, const std::string &port) {
+        const HostTensor *h = nd.param(port);
+        if (!h) fail(CATNN_ERR_UNKNOWN_PORT, "unknown port " + port + " on interface " + nd.name);
+        return h;
+    };
+    auto tape = [&](TNode &tn, const std::string &nm, uint64_t bytes, bool keep = false) {
+        request(t, "tape:" + tn.node->name + ":" + nm, bytes, tn.tick, keep ? upd : bwd(tn.tick), &tn.B(nm));
+    };
+    auto scratch = [&](TNode &tn, const std::string &nm, uint64_t bytes) {
+        request(t, "scratch:" + tn.node->name + ":" + nm, bytes, bwd(tn.tick), bwd(tn.tick), &tn.B(nm));
+    };
+
+    for (auto &tn : t.nodes) {
+        if (t.input_ids.count(tn.id)) continue;
+        const Node &nd = *tn.node;
+        const auto &x = tn.in_dims.empty() ? tn.dims : tn.in_dims[0];
+        switch (tn.kind) {
+            case CATNN_OP_LINEAR:
+            case CATNN_OP_MATMUL: {
+                const HostTensor *w = nd.param("w") ? nd.param("w") : (nd.params.empty() ? nullptr : &nd.params.front().second);
+                CATNN_REQUIRE(w, CATNN_ERR_UNKNOWN_COMPONENT, "unknown component " + nd.name);
+                const int64_t K = w->dims[0], N = w->dims[1], M = numel(x) / K;
+                add_param(tn, nd.param("w") ? "w" : nd.params.front().first, K, N, true, true, w->data);
+                if (const HostTensor *b = nd.param("b")) add_param(tn, "b", 1, N, false, false, b->data);
+                tape(tn, "xb", (uint64_t)(M * K) * 2);
+                scratch(tn, "xbt", (uint64_t)(M * K) * 2);
+                scratch(tn, "dyb", (uint64_t)(M * N) * 2);
+                scratch(tn, "dybt", (uint64_t)(M * N) * 2);
+                scratch(tn, "colsum", k::colsum_scratch_bytes(M, (int)N));
+                break;
+            }
+            case CATNN_OP_LAYER_NORM: {
+                const int64_t C = x.back(), R = numel(x) / C;
+                add_param(tn, "gamma", 1, C, false, false, host(nd, "gamma")->data);
+                add_param(tn, "beta", 1, C, false, false, host(nd, "beta")->data);
+                tape(tn, "mean", (uint64_t)R * 4);
+                tape(tn, "rstd", (uint64_t)R * 4);
+                scratch(tn, "parts", k::ln_backward_scratch_bytes(R, (int)C));
+                break;
+            }
+            case CATNN_OP_ATTENTION: {
+                const int64_t Bt = x[0], S = x[1], D = x[2], T = Bt * S, H = nd.op.a[0];
+                std::vector<float> packed((size_t)(D * 3 * D));
+                const HostTensor *wq = host(nd, "wq"), *wk = host(nd, "wk"), *wv = host(nd, "wv");
+                for (int64_t r = 0; r < D; ++r) {
+                    std::memcpy(&packed[(size_t)(r * 3 * D)], &wq->data[(size_t)(r * D)], (size_t)D * 4);
+                    std::memcpy(&packed[(size_t)(r * 3 * D + D)], &wk->data[(size_t)(r * D)], (size_t)D * 4);
+                    std::memcpy(&packed[(size_t)(r * 3 * D + 2 * D)], &wv->data[(size_t)(r * D)], (size_t)D * 4);
+                }
+                add_param(tn, "wqkv", D, 3 * D, true, true, std::move(packed));
+                add_param(tn, "wo", D, D, true, true, host(nd, "wo")->data);
+                tape(tn, "xb", (uint64_t)(T * D) * 2);
+                tape(tn, "qkv", (uint64_t)(T * 3 * D) * 4);
+                tape(tn, "ctx", (uint64_t)(T * D) * 4);
+                tape(tn, "ctxb", (uint64_t)(T * D) * 2);
+                tape(tn, "lse", (uint64_t)(T * H) * 4);
+                scratch(tn, "dyb", (uint64_t)(T * D) * 2);
+                scratch(tn, "dybt", (uint64_t)(T * D) * 2);
+                scratch(tn, "ctxt", (uint64_t)(T * D) * 2);
+                scratch(tn, "dctx", (uint64_t)(T * D) * 4);
+                scratch(tn, "dqkv", (uint64_t)(T * 3 * D) * 4);
+                scratch(tn, "dqkvb", (uint64_t)(T * 3 * D) * 2);
+                scratch(tn, "dqkvt", (uint64_t)(T * 3 * D) * 2);
+                scratch(tn, "xbt", (uint64_t)(T * D) * 2);
+                scratch(tn, "dscr", k::attention_bwd_scratch_bytes(Bt, S, H));
+                break;
+            }
+            case CATNN_OP_MOE: {
+                const int64_t E = nd.op.a[0], K = nd.op.a[1], H = x.back(), T = numel(x) / H;
+                const int64_t I = host(nd, "e0.w1")->dims[1];
+                const int64_t P = T * K + E * (kPad - 1);
+                const int64_t Pr = (P + kPad - 1) / kPad * kPad;  // transposed operands' row stride
+                add_param(tn, "gate", H, E, false, false, host(nd, "gate")->data);
+                for (int64_t e = 0; e < E; ++e) {
+                    const std::string p = "e" + std::to_string(e);
+                    add_param(tn, p + ".w1", H, I, true, true, host(nd, p + ".w1")->data);
+                    add_param(tn, p + ".w3", H, I, true, true, host(nd, p + ".w3")->data);
+                    add_param(tn, p + ".w2", I, H, true, true, host(nd, p + ".w2")->data);
+                }
+                const int64_t max_tiles = (T * K + k::gemm_bf16_tile_rows() - 1) / k::gemm_bf16_tile_rows() + E;
+                tape(tn, "xb", (uint64_t)(T * H) * 2);
+                tape(tn, "idx", (uint64_t)(T * K) * 4, true);  // readable after the step
+                tape(tn, "w", (uint64_t)(T * K) * 4);
+                tape(tn, "counts", (uint64_t)E * 4);
+                tape(tn, "offsets", (uint64_t)(E + 1) * 4);
+                tape(tn, "sop", (uint64_t)Pr * 4);
+                tape(tn, "pos", (uint64_t)(T * K) * 4);
+                tape(tn, "tiles", (uint64_t)(2 * max_tiles + 1) * 4);
+                tape(tn, "perm_scratch", k::moe_permute_scratch_bytes(T, K, E));
+                tape(tn, "a", (uint64_t)(Pr * I) * 2);
+                tape(tn, "c", (uint64_t)(Pr * I) * 2);
+                tape(tn, "h", (uint64_t)(Pr * I) * 2);
+                tape(tn, "ys", (uint64_t)(Pr * H) * 4);
+                scratch(tn, "dys", (uint64_t)(Pr * H) * 2);
+                scratch(tn, "dw", (uint64_t)(T * K) * 4);
+                scratch(tn, "da", (uint64_t)(Pr * I) * 2);
+                scratch(tn, "dc", (uint64_t)(Pr * I) * 2);
+                scratch(tn, "dxs", (uint64_t)(Pr * H) * 4);
+                scratch(tn, "xpt", (uint64_t)(H * Pr) * 2);
+                scratch(tn, "ht", (uint64_t)(I * Pr) * 2);
+                scratch(tn, "dyst", (uint64_t)(H * Pr) * 2);
+                scratch(tn, "dat", (uint64_t)(I * Pr) * 2);
+                scratch(tn, "dct", (uint64_t)(I * Pr) * 2);
+                scratch(tn, "dl", (uint64_t)(T * E) * 4);
+                scratch(tn, "router", k::router_backward_scratch_bytes((int)T, (int)H, (int)E));
+                break;
+            }
+            default:
+                break;
+        }
+    }
+}
+
+static void reserve_and_upload(Tr &t) {
+    hipDeviceProp_t prop;
+    CATNN_HIP(hipGetDeviceProperties(&prop, t.dev->ordinal));
+    t.plan = place_arena(t.reqs, prop.totalGlobalMem);
+    t.reserved = 0;
+    for (const auto &a : t.plan) t.reserved = std::max(t.reserved, a.offset + a.bytes);
+    hipError_t e = hipMalloc(&t.base, t.reserved);
+    if (e != hipSuccess)
+        fail(CATNN_ERR_FIBRATION, "training arena: hipMalloc of " + std::to_string(t.reserved) +
+                                      " B failed (" + hipGetErrorString(e) + ")");
+    std::map<std::string, uint64_t> off;
+    for (const auto &a : t.plan) off[a.id] = a.offset;
+    for (size_t i = 0; i < t.reqs.size(); ++i)
+        *t.req_slot[i] = static_cast<char *>(t.base) + off.at(t.reqs[i].id);
+    hipStream_t s = t.dev->stream;
+    for (auto &p : t.params) {
+        CATNN_REQUIRE((int64_t)p->init.size() == p->rows * p->cols, CATNN_ERR_SHAPE_MISMATCH,
+                      p->name + ": parameter size");
+        CATNN_HIP(hipMemcpyAsync(p->master, p->init.data(), p->init.size() * 4, hipMemcpyHostToDevice, s));
+        if (p->want_b) k::cast_f32_bf16(s, p->master, p->b, p->rows * p->cols);
+        if (p->want_bt)
+            k::transpose_bf16(s, p->b, p->cols, nullptr, 1, (int)p->rows, (int)p->cols, p->bt, p->rows);
+    }
+    CATNN_HIP(hipStreamSynchronize(s));
+    for (auto &p : t.params) std::vector<float>().swap(p->init);
+}
+
+// ------------------------------------------------------------ forward
+
+static void forward_node(Tr &t, TNode &tn) {
+    hipStream_t s = t.dev->stream;
+    const Node &nd = *tn.node;
+    float *y = t.val.at(tn.id);
+    const float *x = tn.ins.empty() ? nullptr : t.val.at(tn.ins[0]);
+    const auto &xd = tn.ins.empty() ? tn.dims : tn.in_dims[0];
+    const int64_t nx = numel(xd);
+    switch (tn.kind) {
+        case CATNN_OP_IDENTITY: case CATNN_OP_RESHAPE: case CATNN_OP_TRANSPOSE:
+            if (x) k::copy_f32(s, x, y, nx);
+            else k::fill_f32(s, y, 0.f, numel(tn.dims));
+            break;
+        case CATNN_OP_RELU: case CATNN_OP_GELU:
+            k::act_f32(s, x, y, nx, tn.kind);
+            break;
+        case CATNN_OP_ADD: case CATNN_OP_RESIDUAL_ADD:
+            if (tn.ins.size() > 1) k::add_f32(s, x, t.val.at(tn.ins[1]), y, nx, nx);
+            else k::copy_f32(s, x, y, nx);
+            break;
+        case CATNN_OP_LINEAR: case CATNN_OP_MATMUL: {
+            TParam *w = tn.params.begin()->second;
+            for (auto &kv : tn.params) if (kv.first != "b") w = kv.second;
+            TParam *b = tn.params.count("b") ? tn.params["b"] : nullptr;
+            const int64_t K = w->rows, N = w->cols, M = nx / K;
+            bf16_t *xb = (bf16_t *)tn.B("xb");
+            k::cast_f32_bf16(s, x, xb, M * K);
+            k::GemmBf16Params p = gp();
+            p.A = xb; p.lda = K; p.B = w->bt; p.ldb = K;
+            p.M = (int)M; p.N = (int)N; p.K = (int)K;
+            p.epi = k::EPI_LINEAR; p.bias = b ? b->master : nullptr;
+            p.C32 = y; p.ldc32 = N;
+            k::gemm_bf16_launch(s, p);
+            break;
+        }
+        case CATNN_OP_LAYER_NORM: {
+            const int64_t C = xd.back();
+            const float eps = (float)nd.op.a[0] * 1e-6f;
+            k::ln_forward_train(s, x, tn.params["gamma"]->master, tn.params["beta"]->master, y, nullptr,
+                                (float *)tn.B("mean"), (float *)tn.B("rstd"), nx / C, (int)C, eps);
+            break;
+        }
+        case CATNN_OP_ATTENTION: {
+            const int64_t Bt = xd[0], S = xd[1], D = xd[2], T = Bt * S;
+            const int64_t H = nd.op.a[0], dh = nd.op.a[2];
+            const bool causal = (nd.op.flags & CATNN_FLAG_CAUSAL) != 0;
+            bf16_t *xb = (bf16_t *)tn.B("xb");
+            float *qkv = (float *)tn.B("qkv"), *ctx = (float *)tn.B("ctx");
+            bf16_t *ctxb = (bf16_t *)tn.B("ctxb");
+            k::cast_f32_bf16(s, x, xb, T * D);
+            gemm_nt(s, xb, D, tn.params["wqkv"]->bt, D, (int)T, (int)(3 * D), (int)D, qkv, 3 * D, false);
+            k::attention_core_fwd_lse(s, qkv, qkv + D, qkv + 2 * D, 3 * D, ctx, D, (float *)tn.B("lse"), Bt,
+                                      S, H, dh, causal);
+            k::cast_f32_bf16(s, ctx, ctxb, T * D);
+            gemm_nt(s, ctxb, D, tn.params["wo"]->bt, D, (int)T, (int)D, (int)D, y, D, false);
+            break;
+        }
+        case CATNN_OP_MOE: {
+            const int64_t E = nd.op.a[0], K = nd.op.a[1], H = xd.back(), T = nx / H;
+            const int64_t I = tn.params["e0.w1"]->cols;
+            const int64_t P = T * K + E * (kPad - 1);
+            const int64_t Pr = (P + kPad - 1) / kPad * kPad;
+            int32_t *idx = (int32_t *)tn.B("idx"), *counts = (int32_t *)tn.B("counts");
+            int32_t *offs = (int32_t *)tn.B("offsets"), *sop = (int32_t *)tn.B("sop");
+            int32_t *pos = (int32_t *)tn.B("pos"), *tiles = (int32_t *)tn.B("tiles");
+            float *w = (float *)tn.B("w");
+            const int max_tiles = (int)((T * K + k::gemm_bf16_tile_rows() - 1) / k::gemm_bf16_tile_rows() + E);
+            k::moe_route_f32(s, x, tn.params["gate"]->master, T, H, E, K, idx, w, nullptr);
+            k::moe_permute_padded(s, idx, T, K, E, kPad, Pr, counts, offs, sop, pos, tn.B("perm_scratch"));
+            k::build_tiles(s, offs, (int)E, tiles, tiles + max_tiles, tiles + 2 * max_tiles);
+            bf16_t *xb = (bf16_t *)tn.B("xb");
+            k::cast_f32_bf16(s, x, xb, T * H);
+            k::GemmBf16Params p = gp();
+            p.grid = k::GRID_ROWS;
+            p.tile_expert = tiles; p.tile_row0 = tiles + max_tiles; p.n_tiles = tiles + 2 * max_tiles;
+            p.seg_offsets = offs; p.seg_counts = counts; p.max_tiles = max_tiles; p.n_experts = (int)E;
+            // gate/up: h = silu(x·w1)·(x·w3), a and c kept for the adjoint
+            p.A = xb; p.lda = H; p.a_rows = sop; p.a_row_div = (int)K;
+            for (int64_t e = 0; e < E; ++e) {
+                p.B_e[e] = tn.params["e" + std::to_string(e) + ".w1"]->bt;
+                p.B2_e[e] = tn.params["e" + std::to_string(e) + ".w3"]->bt;
+            }
+            p.ldb = H; p.M = 0; p.N = (int)I; p.K = (int)H;
+            p.epi = k::EPI_SWIGLU_FWD;
+            p.Cb = (bf16_t *)tn.B("h"); p.ldcb = I;
+            p.S1 = (bf16_t *)tn.B("a"); p.S2 = (bf16_t *)tn.B("c"); p.lds = I;
+            k::gemm_bf16_launch(s, p);
+            // down: ys = h·w2
+            k::GemmBf16Params q = p;
+            q.A = (bf16_t *)tn.B("h"); q.lda = I; q.a_rows = nullptr; q.a_row_div = 1;
+            for (int64_t e = 0; e < E; ++e) {
+                q.B_e[e] = tn.params["e" + std::to_string(e) + ".w2"]->bt;
+                q.B2_e[e] = nullptr;
+            }
+            q.ldb = I; q.N = (int)H; q.K = (int)I;
+            q.epi = k::EPI_STORE; q.Cb = nullptr; q.S1 = q.S2 = nullptr;
+            q.C32 = (float *)tn.B("ys"); q.ldc32 = H;
+            k::gemm_bf16_launch(s, q);
+            k::moe_combine(s, (float *)tn.B("ys"), pos, w, T, K, H, y);
+            break;
+        }
+        default:
+            fail(CATNN_ERR_UNSUPPORTED, "training: op " + op_name(tn.kind));
+    }
+}
+
+// ----------------------------------------------------------- backward
+
+static void backward_node(Tr &t, TNode &tn) {
+    hipStream_t s = t.dev->stream;
+    const Node &nd = *tn.node;
+    const float *dy = t.grad.at(tn.id);
+    auto dst = [&](size_t i) -> float * {
+        return t.input_ids.count(tn.ins[i]) ? nullptr : t.grad.at(tn.ins[i]);
+    };
+    const float *x = tn.ins.empty() ? nullptr : t.val.at(tn.ins[0]);
+    const auto &xd = tn.ins.empty() ? tn.dims : tn.in_dims[0];
+    const int64_t nx = numel(xd);
+    switch (tn.kind) {
+        case CATNN_OP_IDENTITY: case CATNN_OP_RESHAPE: case CATNN_OP_TRANSPOSE:
+            if (!tn.ins.empty() && dst(0)) add_into(s, dst(0), dy, nx, tn.first_writer[0]);
+            break;
+        case CATNN_OP_ADD: case CATNN_OP_RESIDUAL_ADD:
+            for (size_t i = 0; i < tn.ins.size(); ++i)
+                if (dst(i)) add_into(s, dst(i), dy, nx, tn.first_writer[i]);
+            break;
+        case CATNN_OP_RELU: case CATNN_OP_GELU:
+            if (dst(0)) k::act_backward(s, x, dy, dst(0), nx, tn.kind, !tn.first_writer[0]);
+            break;
+        case CATNN_OP_LINEAR: case CATNN_OP_MATMUL: {
+            TParam *w = tn.params.begin()->second;
+            for (auto &kv : tn.params) if (kv.first != "b") w = kv.second;
+            TParam *b = tn.params.count("b") ? tn.params["b"] : nullptr;
+            const int64_t K = w->rows, N = w->cols, M = nx / K;
+            bf16_t *dyb = (bf16_t *)tn.B("dyb"), *dybt = (bf16_t *)tn.B("dybt");
+            bf16_t *xb = (bf16_t *)tn.B("xb"), *xbt = (bf16_t *)tn.B("xbt");
+            k::cast_f32_bf16(s, dy, dyb, M * N);
+            if (dst(0)) gemm_nt(s, dyb, N, w->b, N, (int)M, (int)K, (int)N, dst(0), K, !tn.first_writer[0]);
+            k::transpose_bf16(s, dyb, N, nullptr, 1, (int)M, (int)N, dybt, M);
+            k::transpose_bf16(s, xb, K, nullptr, 1, (int)M, (int)K, xbt, M);
+            gemm_nt(s, xbt, M, dybt, M, (int)K, (int)N, (int)M, w->grad, N, false);
+            if (b) k::colsum(s, dy, M, (int)N, b->grad, false, (float *)tn.B("colsum"));
+            break;
+        }
+        case CATNN_OP_LAYER_NORM: {
+            const int64_t C = xd.back();
+            float *dx = dst(0);  // null when the input is the graph input
+            k::ln_backward(s, x, tn.params["gamma"]->master, (float *)tn.B("mean"), (float *)tn.B("rstd"), dy,
+                           dx, dx && !tn.first_writer[0], tn.params["gamma"]->grad,
+                           tn.params["beta"]->grad, false, nx / C, (int)C, (float *)tn.B("parts"));
+            break;
+        }
+        case CATNN_OP_ATTENTION: {
+            const int64_t Bt = xd[0], S = xd[1], D = xd[2], T = Bt * S;
+            const int64_t H = nd.op.a[0], dh = nd.op.a[2];
+            const bool causal = (nd.op.flags & CATNN_FLAG_CAUSAL) != 0;
+            TParam *wqkv = tn.params["wqkv"], *wo = tn.params["wo"];
+            bf16_t *dyb = (bf16_t *)tn.B("dyb"), *dybt = (bf16_t *)tn.B("dybt"), *ctxt = (bf16_t *)tn.B("ctxt");
+            float *dctx = (float *)tn.B("dctx"), *dqkv = (float *)tn.B("dqkv");
+            bf16_t *dqkvb = (bf16_t *)tn.B("dqkvb"), *dqkvt = (bf16_t *)tn.B("dqkvt");
+            bf16_t *xb = (bf16_t *)tn.B("xb"), *xbt = (bf16_t *)tn.B("xbt");
+            float *qkv = (float *)tn.B("qkv");
+            k::cast_f32_bf16(s, dy, dyb, T * D);
+            gemm_nt(s, dyb, D, wo->b, D, (int)T, (int)D, (int)D, dctx, D, false);
+            k::transpose_bf16(s, dyb, D, nullptr, 1, (int)T, (int)D, dybt, T);
+            k::transpose_bf16(s, (bf16_t *)tn.B("ctxb"), D, nullptr, 1, (int)T, (int)D, ctxt, T);
+            gemm_nt(s, ctxt, T, dybt, T, (int)D, (int)D, (int)T, wo->grad, D, false);
+            k::attention_core_bwd(s, qkv, qkv + D, qkv + 2 * D, 3 * D, (float *)tn.B("ctx"), dctx, D,
+                                  (float *)tn.B("lse"), dqkv, dqkv + D, dqkv + 2 * D, 3 * D, Bt, S, H, dh,
+                                  causal, (float *)tn.B("dscr"));
+            k::cast_f32_bf16(s, dqkv, dqkvb, T * 3 * D);
+            if (dst(0))
+                gemm_nt(s, dqkvb, 3 * D, wqkv->b, 3 * D, (int)T, (int)D, (int)(3 * D), dst(0), D,
+                        !tn.first_writer[0]);
+            k::transpose_bf16(s, dqkvb, 3 * D, nullptr, 1, (int)T, (int)(3 * D), dqkvt, T);
+            k::transpose_bf16(s, xb, D, nullptr, 1, (int)T, (int)D, xbt, T);
+            gemm_nt(s, xbt, T, dqkvt, T, (int)D, (int)(3 * D), (int)T, wqkv->grad, 3 * D, false);
+            break;
+        }
+        case CATNN_OP_MOE: {
+            const int64_t E = nd.op.a[0], K = nd.op.a[1], H = xd.back(), T = nx / H;
+            const int64_t I = tn.params["e0.w1"]->cols;
+            const int64_t P = T * K + E * (kPad - 1);
+            const int64_t Pr = (P + kPad - 1) / kPad * kPad;
+            int32_t *idx = (int32_t *)tn.B("idx"), *counts = (int32_t *)tn.B("counts");
+            int32_t *offs = (int32_t *)tn.B("offsets"), *sop = (int32_t *)tn.B("sop");
+            int32_t *pos = (int32_t *)tn.B("pos"), *tiles = (int32_t *)tn.B("tiles");
+            const int max_tiles = (int)((T * K + k::gemm_bf16_tile_rows() - 1) / k::gemm_bf16_tile_rows() + E);
+            float *w = (float *)tn.B("w"), *dw = (float *)tn.B("dw");
+            bf16_t *dys = (bf16_t *)tn.B("dys"), *da = (bf16_t *)tn.B("da"), *dc = (bf16_t *)tn.B("dc");
+            float *dxs = (float *)tn.B("dxs");
+            // Per slot: dys = w·dout[token], dw = <ys, dout[token]> (moe_backward's d_wts).
+            k::moe_slot_grads(s, sop, w, (float *)tn.B("ys"), dy, (int)K, (int)H, (int)Pr, dys, dw);
+            k::GemmBf16Params p = gp();
+            p.grid = k::GRID_ROWS;
+            p.tile_expert = tiles; p.tile_row0 = tiles + max_tiles; p.n_tiles = tiles + 2 * max_tiles;
+            p.seg_offsets = offs; p.seg_counts = counts; p.max_tiles = max_tiles; p.n_experts = (int)E;
+            // dh = dys·w2ᵀ, then da = dh·c·silu'(a), dc = dh·silu(a)
+            p.A = dys; p.lda = H;
+            for (int64_t e = 0; e < E; ++e) p.B_e[e] = tn.params["e" + std::to_string(e) + ".w2"]->b;
+            p.ldb = H; p.N = (int)I; p.K = (int)H;
+            p.epi = k::EPI_SWIGLU_BWD; p.Cb = da; p.Cb2 = dc; p.ldcb = I;
+            p.S1 = (bf16_t *)tn.B("a"); p.S2 = (bf16_t *)tn.B("c"); p.lds = I;
+            k::gemm_bf16_launch(s, p);
+            // dxs = da·w1ᵀ + dc·w3ᵀ
+            k::GemmBf16Params q = p;
+            q.epi = k::EPI_STORE; q.Cb = q.Cb2 = nullptr; q.S1 = q.S2 = nullptr;
+            q.A = da; q.lda = I; q.ldb = I; q.N = (int)H; q.K = (int)I;
+            q.C32 = dxs; q.ldc32 = H; q.accumulate = 0;
+            for (int64_t e = 0; e < E; ++e) q.B_e[e] = tn.params["e" + std::to_string(e) + ".w1"]->b;
+            k::gemm_bf16_launch(s, q);
+            q.A = dc; q.accumulate = 1;
+            for (int64_t e = 0; e < E; ++e) q.B_e[e] = tn.params["e" + std::to_string(e) + ".w3"]->b;
+            k::gemm_bf16_launch(s, q);
+            // Expert weight gradients: each expert reduces over its own segment.
+            bf16_t *xpt = (bf16_t *)tn.B("xpt"), *ht = (bf16_t *)tn.B("ht"), *dyst = (bf16_t *)tn.B("dyst");
+            bf16_t *dat = (bf16_t *)tn.B("dat"), *dct = (bf16_t *)tn.B("dct");
+            k::transpose_bf16(s, (bf16_t *)tn.B("xb"), H, sop, (int)K, (int)Pr, (int)H, xpt, Pr);
+            k::transpose_bf16(s, (bf16_t *)tn.B("h"), I, nullptr, 1, (int)Pr, (int)I, ht, Pr);
+            k::transpose_bf16(s, dys, H, nullptr, 1, (int)Pr, (int)H, dyst, Pr);
+            k::transpose_bf16(s, da, I, nullptr, 1, (int)Pr, (int)I, dat, Pr);
+            k::transpose_bf16(s, dc, I, nullptr, 1, (int)Pr, (int)I, dct, Pr);
+            k::GemmBf16Params r = gp();
+            r.grid = k::GRID_SEGK; r.seg_offsets = offs; r.seg_counts = counts; r.segk_aligned = 1;
+            r.n_experts = (int)E; r.epi = k::EPI_STORE;
+            auto segk = [&](const bf16_t *A, const bf16_t *B, int M, int N, const char *port) {
+                r.A = A; r.lda = Pr; r.B = B; r.ldb = Pr; r.M = M; r.N = N; r.K = (int)Pr; r.ldc32 = N;
+                for (int64_t e = 0; e < E; ++e) r.C_e[e] = tn.params["e" + std::to_string(e) + port]->grad;
+                k::gemm_bf16_launch(s, r);
+            };
+            segk(ht, dyst, (int)I, (int)H, ".w2");
+            segk(xpt, dat, (int)H, (int)I, ".w1");
+            segk(xpt, dct, (int)H, (int)I, ".w3");
+            // Router (straight-through on the indices) and the input cotangent.
+            float *dl = (float *)tn.B("dl");
+            k::router_backward(s, idx, w, dw, x, (int)T, (int)H, (int)E, (int)K, dl, tn.params["gate"]->grad,
+                               (float *)tn.B("router"));
+            if (dst(0))
+                k::moe_dx(s, dxs, pos, dl, tn.params["gate"]->master, (int)T, (int)K, (int)H, (int)E, dst(0),
+                          !tn.first_writer[0]);
+            break;
+        }
+        default:
+            fail(CATNN_ERR_UNSUPPORTED, "training: op " + op_name(tn.kind));
+    }
+}
+
+static void train_step(Tr &t) {
+    hipStream_t s = t.dev->stream;
+    for (auto &tn : t.nodes)
+        if (!t.input_ids.count(tn.id)) forward_node(t, tn);
+    const int64_t n_out = numel(t.dims[t.out_id]);
+    k::mse(s, t.val.at(t.out_id), t.target, t.grad.at(t.out_id), n_out, t.loss, t.mse_scratch);
+    // A node whose output nobody reads receives no cotangent and is skipped,
+    // as reference_train skips ids without an entry in `grads`.
+    for (auto it = t.nodes.rbegin(); it != t.nodes.rend(); ++it)
+        if (!t.input_ids.count(it->id) && t.has_grad.count(it->id)) backward_node(t, *it);
+    // Sgd::put on the parameters of every node that received a cotangent.
+    for (auto &tn : t.nodes) {
+        if (t.input_ids.count(tn.id) || !t.has_grad.count(tn.id)) continue;
+        for (auto &kv : tn.params) {
+            TParam *p = kv.second;
+            k::sgd(s, p->master, p->grad, p->cols, p->rows, (int)p->cols, t.lr, p->want_b ? p->b : nullptr);
+            if (p->want_bt)
+                k::transpose_bf16(s, p->b, p->cols, nullptr, 1, (int)p->rows, (int)p->cols, p->bt, p->rows);
+        }
+    }
+}
+
+static TParam *find_param(Tr &t, uint32_t node_id, const std::string &port, int64_t *col0,
+                          int64_t *ncols) {
+    auto it = t.index.find(node_id);
+    CATNN_REQUIRE(it != t.index.end(), CATNN_ERR_UNKNOWN_COMPONENT, "unknown node " + std::to_string(node_id));
+    TNode &tn = t.nodes[it->second];
+    *col0 = 0;
+    if (tn.kind == CATNN_OP_ATTENTION && (port == "wq" || port == "wk" || port == "wv")) {
+        TParam *p = tn.params.at("wqkv");
+        *col0 = port == "wq" ? 0 : port == "wk" ? p->rows : 2 * p->rows;
+        *ncols = p->rows;
+        return p;
+    }
+    auto pit = tn.params.find(port);
+    CATNN_REQUIRE(pit != tn.params.end(), CATNN_ERR_UNKNOWN_PORT,
+                  "unknown port " + port + " on interface " + tn.node->name);
+    *ncols = pit->second->cols;
+    return pit->second;
+}
+
+// Copies rows × ncols starting at column col0 of a [rows, cols] fp32 buffer.
+static void read_cols(Tr &t, const float *src, int64_t rows, int64_t cols, int64_t col0, int64_t ncols,
+                      float *host, int64_t n) {
+    CATNN_REQUIRE(n == rows * ncols, CATNN_ERR_SHAPE_MISMATCH,
+                  "host buffer holds " + std::to_string(n) + " values, tensor has " + std::to_string(rows * ncols));
+    CATNN_HIP(hipMemcpy2DAsync(host, (size_t)ncols * 4, src + col0, (size_t)cols * 4, (size_t)ncols * 4,
+                               (size_t)rows, hipMemcpyDeviceToHost, t.dev->stream));
+    CATNN_HIP(hipStreamSynchronize(t.dev->stream));
+}
+
+}  // namespace catnn
+
+using namespace catnn;
+
+extern "C" {
+
+int catnn_hip_train_install(catnn_hip_device *dev, const catnn_graph *g, float lr,
+                            catnn_hip_trainer **out) {
+    return guard([&] {
+        require_device(dev);
+        CATNN_REQUIRE(g && out, CATNN_ERR_INVALID_ARGUMENT, "null argument");
+        *out = nullptr;
+        auto *t = new catnn_hip_trainer();
+        try {
+            t->dev = dev;
+            t->graph = *g;
+            t->lr = lr;
+            plan_trainer(*t);
+            reserve_and_upload(*t);
+        } catch (...) {
+            if (t->base) (void)hipFree(t->base);
+            delete t;
+            throw;
+        }
+        *out = t;
+    });
+}
+
+int catnn_hip_train_free(catnn_hip_trainer *t) {
+    return guard([&] {
+        if (!t) return;
+        (void)hipSetDevice(t->dev->ordinal);
+        (void)hipStreamSynchronize(t->dev->stream);
+        if (t->base) (void)hipFree(t->base);
+        delete t;
+    });
+}
+
+int catnn_hip_train_set_batch(catnn_hip_trainer *t, const catnn_tensor *input, const catnn_tensor *target) {
+    return guard([&] {
+        CATNN_REQUIRE(t && input && target, CATNN_ERR_INVALID_ARGUMENT, "null argument");
+        require_device(t->dev);
+        hipStream_t s = t->dev->stream;
+        int64_t ni = 1, nt = 1;
+        for (int i = 0; i < input->rank; ++i) ni *= input->dims[i];
+        for (int i = 0; i < target->rank; ++i) nt *= target->dims[i];
+        CATNN_REQUIRE(nt == numel(t->dims[t->out_id]) && (target->data || nt == 0), CATNN_ERR_SHAPE_MISMATCH,
+                      "target size");
+        for (uint32_t id : t->input_ids) {
+            CATNN_REQUIRE(ni == numel(t->dims[id]) && (input->data || ni == 0), CATNN_ERR_SHAPE_MISMATCH,
+                          "input size");
+            CATNN_HIP(hipMemcpyAsync(t->val.at(id), input->data, (size_t)ni * 4, hipMemcpyHostToDevice, s));
+        }
+        CATNN_HIP(hipMemcpyAsync(t->target, target->data, (size_t)nt * 4, hipMemcpyHostToDevice, s));
+        CATNN_HIP(hipStreamSynchronize(s));
+    });
+}
+
+int catnn_hip_train_step(catnn_hip_trainer *t, float *loss) {
+    return guard([&] {
+        CATNN_REQUIRE(t, CATNN_ERR_INVALID_ARGUMENT, "null trainer");
+        require_device(t->dev);
+        train_step(*t);
+        if (loss) {
+            CATNN_HIP(hipMemcpyAsync(loss, t->loss, 4, hipMemcpyDeviceToHost, t->dev->stream));
+            CATNN_HIP(hipStreamSynchronize(t->dev->stream));
+        }
+    });
+}
+
+int catnn_hip_train_read_param(catnn_hip_trainer *t, uint32_t node_id, const char *port, float *host,
+                               int64_t n) {
+    return guard([&] {
+        CATNN_REQUIRE(t && port && host, CATNN_ERR_INVALID_ARGUMENT, "null argument");
+        require_device(t->dev);
+        int64_t col0, ncols;
+        TParam *p = find_param(*t, node_id, port, &col0, &ncols);
+        read_cols(*t, p->master, p->rows, p->cols, col0, ncols, host, n);
+    });
+}
+
+int catnn_hip_train_read_grad(catnn_hip_trainer *t, uint32_t node_id, const char *port, float *host,
+                              int64_t n) {
+    return guard([&] {
+        CATNN_REQUIRE(t && port && host, CATNN_ERR_INVALID_ARGUMENT, "null argument");
+        require_device(t->dev);
+        int64_t col0, ncols;
+        TParam *p = find_param(*t, node_id, port, &col0, &ncols);
+        read_cols(*t, p->grad, p->rows, p->cols, col0, ncols, host, n);
+    });
+}
+
+int catnn_hip_train_read_value(catnn_hip_trainer *t, uint32_t node_id, float *host, int64_t n) {
+    return guard([&] {
+        CATNN_REQUIRE(t && host, CATNN_ERR_INVALID_ARGUMENT, "null argument");
+        require_device(t->dev);
+        auto it = t->val.find(node_id);
+        CATNN_REQUIRE(it != t->val.end(), CATNN_ERR_UNKNOWN_COMPONENT, "unknown node " + std::to_string(node_id));
+        // Other values share arena space with later buffers once their last reader ran.
+        CATNN_REQUIRE(node_id == t->out_id || t->input_ids.count(node_id), CATNN_ERR_UNSUPPORTED,
+                      "value of node " + std::to_string(node_id) +
+                          " is not kept past its last use; only graph inputs and the output are");
+        read_cols(*t, it->second, 1, numel(t->dims[node_id]), 0, numel(t->dims[node_id]), host, n);
+    });
+}
+
+int catnn_hip_train_read_routing(catnn_hip_trainer *t, uint32_t node_id, int32_t *idx, int64_t n) {
+    return guard([&] {
+        CATNN_REQUIRE(t && idx, CATNN_ERR_INVALID_ARGUMENT, "null argument");
+        require_device(t->dev);
+        auto it = t->index.find(node_id);
+        CATNN_REQUIRE(it != t->index.end() && t->nodes[it->second].kind == CATNN_OP_MOE,
+                      CATNN_ERR_UNKNOWN_COMPONENT, "node " + std::to_string(node_id) + " is not a MoE node");
+        TNode &tn = t->nodes[it->second];
+        const int64_t T = numel(tn.in_dims[0]) / tn.in_dims[0].back();
+        CATNN_REQUIRE(n == T * tn.node->op.a[1], CATNN_ERR_SHAPE_MISMATCH, "routing buffer size");
+        CATNN_HIP(hipMemcpyAsync(idx, tn.B("idx"), (size_t)n * 4, hipMemcpyDeviceToHost, t->dev->stream));
+        CATNN_HIP(hipStreamSynchronize(t->dev->stream));
+    });
+}
+
+int catnn_hip_train_arena(catnn_hip_trainer *t, catnn_arena_alloc *out, int32_t cap, int32_t *n,
+                          uint64_t *reserved_bytes) {
+    return guard([&] {
+        CATNN_REQUIRE(t && n, CATNN_ERR_INVALID_ARGUMENT, "null argument");
+        *n = (int32_t)t->plan.size();
+        if (reserved_bytes) *reserved_bytes = t->reserved;
+        for (int32_t i = 0; out && i < cap && i < *n; ++i) {
+            const auto &a = t->plan[(size_t)i];
+            std::memset(out[i].id, 0, CATNN_ID_CAP);
+            std::strncpy(out[i].id, a.id.c_str(), CATNN_ID_CAP - 1);
+            out[i].bytes = a.bytes;
+            out[i].offset = a.offset;
+            out[i].live_from = a.live_from;
+            out[i].live_to = a.live_to;
+        }
+    });
+}
+
+}  // extern "C"

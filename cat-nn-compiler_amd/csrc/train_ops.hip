@@ -1,0 +1,479 @@
+// Memory-bound kernels of the training step: casts and transposes for the
+// bf16 GEMM operands, LayerNorm with saved statistics and its adjoint,
+// activation adjoints, bias-gradient column sums, MSE, SGD with the bf16
+// weight refresh, and the MoE/router adjoint pieces.  All reductions are
+// two-stage with a fixed order (no floating-point atomics), so a training
+// step is run-to-run identical.
+//
+// Adjoints restate crates/catnn-compile/src/kernel/adjoint.rs:
+// relu_backward :63-74, gelu_backward :76-90, mse_loss :106-119,
+// layer_norm_backward :530-577, router_backward_ste :255-284, the token
+// loop of moe_backward :471-526; SGD is Sgd::put (lens/optim.rs:32-42).
+#include <hip/hip_runtime.h>
+
+#include "common.hpp"
+#include "devmath.hpp"
+#include "kernels.hpp"
+#include "train_ops.hpp"
+
+namespace catnn {
+namespace k {
+
+namespace {
+
+__device__ __forceinline__ bf16_t f2bf(float f) {
+    const uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (bf16_t)((u >> 16) | 0x40);
+    return (bf16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+
+unsigned blocks_for(int64_t n, int per_block) {
+    int64_t b = (n + per_block - 1) / per_block;
+    if (b < 1) b = 1;
+    if (b > (1 << 20)) b = 1 << 20;
+    return (unsigned)b;
+}
+
+__global__ void fill_kernel(float *__restrict__ y, float v, int64_t n) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) y[i] = v;
+}
+
+__global__ void fill_bf16_kernel(bf16_t *__restrict__ y, int64_t n) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) y[i] = 0;
+}
+
+__global__ void cast_kernel(const float *__restrict__ x, bf16_t *__restrict__ y, int64_t n) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+        y[i] = f2bf(x[i]);
+}
+
+// dst[c][r] = src[map(r)][c] for r < rows (map(r) = rows_map[r] / div when
+// given; a negative map entry is a padding row and yields 0), c < cols.
+// 64×64 tiles through LDS so both the read and the write are coalesced.
+template <typename TS>
+__global__ __launch_bounds__(256) void transpose_kernel(const TS *__restrict__ src, int64_t lds,
+                                                        const int32_t *__restrict__ rows_map,
+                                                        int div, int rows, int cols,
+                                                        bf16_t *__restrict__ dst, int64_t ldd) {
+    __shared__ bf16_t t[64][66];
+    const int r0 = blockIdx.y * 64, c0 = blockIdx.x * 64;
+    const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+    for (int i = ty; i < 64; i += 4) {
+        const int r = r0 + i, c = c0 + tx;
+        bf16_t v = 0;
+        if (r < rows && c < cols) {
+            int sr = r;
+            if (rows_map) {
+                const int m = rows_map[r];
+                sr = m < 0 ? -1 : m / div;
+            }
+            if (sr >= 0) {
+                if constexpr (sizeof(TS) == 4) v = f2bf(src[(int64_t)sr * lds + c]);
+                else v = src[(int64_t)sr * lds + c];
+            }
+        }
+        t[i][tx] = v;
+    }
+    __syncthreads();
+    for (int i = ty; i < 64; i += 4) {
+        const int c = c0 + i, r = r0 + tx;
+        if (c < cols && r < rows) dst[(int64_t)c * ldd + r] = t[tx][i];
+    }
+}
+
+// LayerNorm forward for training: y (fp32 and/or bf16), mean and rstd per
+// row.  One wavefront per row; any width.
+__global__ __launch_bounds__(256) void ln_fwd_kernel(const float *__restrict__ x,
+                                                     const float *__restrict__ g,
+                                                     const float *__restrict__ b,
+                                                     float *__restrict__ y, bf16_t *__restrict__ yb,
+                                                     float *__restrict__ mean,
+                                                     float *__restrict__ rstd, int64_t rows,
+                                                     int cols, float eps) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const float *xr = x + row * cols;
+    float s = 0.f;
+    for (int c = lane; c < cols; c += 64) s += xr[c];
+    const float n = (float)cols;
+    const float mu = wave_sum(s) / n;
+    float q = 0.f;
+    for (int c = lane; c < cols; c += 64) {
+        const float d = xr[c] - mu;
+        q += d * d;
+    }
+    const float inv = 1.0f / sqrtf(wave_sum(q) / n + eps);
+    for (int c = lane; c < cols; c += 64) {
+        const float v = (xr[c] - mu) * inv * g[c] + b[c];
+        if (y) y[row * cols + c] = v;
+        if (yb) yb[row * cols + c] = f2bf(v);
+    }
+    if (lane == 0) {
+        mean[row] = mu;
+        rstd[row] = inv;
+    }
+}
+
+// LayerNorm adjoint: dx (+=) per row, and per-block partial sums of dγ, dβ
+// (block b covers rows [b·rows_per_block, ...)).
+constexpr int kLnRowsPerBlock = 64;
+
+__global__ __launch_bounds__(256) void ln_bwd_kernel(const float *__restrict__ x,
+                                                     const float *__restrict__ g,
+                                                     const float *__restrict__ mean,
+                                                     const float *__restrict__ rstd,
+                                                     const float *__restrict__ dy,
+                                                     float *__restrict__ dx, int accumulate,
+                                                     float *__restrict__ part_g,
+                                                     float *__restrict__ part_b, int64_t rows,
+                                                     int cols) {
+    // Phase 1: one wavefront per row, dx.
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t r0 = (int64_t)blockIdx.x * kLnRowsPerBlock;
+    const float n = (float)cols;
+    for (int64_t row = r0 + wave; dx && row < r0 + kLnRowsPerBlock && row < rows; row += 4) {
+        const float mu = mean[row], inv = rstd[row];
+        const float *xr = x + row * cols, *gr = dy + row * cols;
+        float sd = 0.f, sdx = 0.f;
+        for (int c = lane; c < cols; c += 64) {
+            const float xh = (xr[c] - mu) * inv;
+            const float d = gr[c] * g[c];
+            sd += d;
+            sdx += d * xh;
+        }
+        sd = wave_sum(sd);
+        sdx = wave_sum(sdx);
+        for (int c = lane; c < cols; c += 64) {
+            const float xh = (xr[c] - mu) * inv;
+            const float d = gr[c] * g[c];
+            const float v = (inv / n) * (n * d - sd - xh * sdx);
+            float *o = dx + row * cols + c;
+            *o = accumulate ? *o + v : v;
+        }
+    }
+    // Phase 2: column partials over this block's rows (fixed row order).
+    for (int c = threadIdx.x; c < cols; c += 256) {
+        float pg = 0.f, pb = 0.f;
+        for (int64_t row = r0; row < r0 + kLnRowsPerBlock && row < rows; ++row) {
+            const float xh = (x[row * cols + c] - mean[row]) * rstd[row];
+            const float d = dy[row * cols + c];
+            pg += d * xh;
+            pb += d;
+        }
+        part_g[(int64_t)blockIdx.x * cols + c] = pg;
+        part_b[(int64_t)blockIdx.x * cols + c] = pb;
+    }
+}
+
+// out[c] (+)= Σ_b part[b][c], b ascending.
+__global__ void reduce_parts_kernel(const float *__restrict__ part, int nb, int cols,
+                                    float *__restrict__ out, int accumulate) {
+    const int c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= cols) return;
+    float s = 0.f;
+    for (int b = 0; b < nb; ++b) s += part[(int64_t)b * cols + c];
+    out[c] = accumulate ? out[c] + s : s;
+}
+
+// Column partial sums of y [rows, cols] over blocks of 64 rows.
+__global__ void colsum_parts_kernel(const float *__restrict__ y, int64_t rows, int cols,
+                                    float *__restrict__ part) {
+    const int c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= cols) return;
+    const int64_t r0 = (int64_t)blockIdx.y * 64;
+    float s = 0.f;
+    for (int64_t r = r0; r < r0 + 64 && r < rows; ++r) s += y[r * cols + c];
+    part[(int64_t)blockIdx.y * cols + c] = s;
+}
+
+__global__ void act_bwd_kernel(const float *__restrict__ z, const float *__restrict__ dy,
+                               float *__restrict__ dx, int64_t n, int act, int accumulate) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+        const float zz = z[i];
+        float d;
+        if (act == ACT_RELU) {
+            d = zz <= 0.f ? 0.f : dy[i];
+        } else {
+            const float C = 0.044715f, kk = 0.797884523868560791f;
+            const float u = kk * (zz + C * zz * zz * zz);
+            const float t = tanhf(u);
+            const float du = kk * (1.0f + 3.0f * C * zz * zz);
+            d = dy[i] * (0.5f * (1.0f + t) + 0.5f * zz * (1.0f - t * t) * du);
+        }
+        dx[i] = accumulate ? dx[i] + d : d;
+    }
+}
+
+// MSE: d = 2e/n and per-block partial Σe².
+__global__ __launch_bounds__(256) void mse_kernel(const float *__restrict__ pred,
+                                                  const float *__restrict__ tgt,
+                                                  float *__restrict__ d, int64_t n,
+                                                  float *__restrict__ part) {
+    __shared__ float ws[4];
+    const float nf = (float)n;
+    float s = 0.f;
+    const int64_t per = (n + gridDim.x - 1) / gridDim.x;
+    const int64_t lo = (int64_t)blockIdx.x * per, hi = min(n, lo + per);
+    for (int64_t i = lo + threadIdx.x; i < hi; i += 256) {
+        const float e = pred[i] - tgt[i];
+        s += e * e;
+        d[i] = 2.0f * e / nf;
+    }
+    s = wave_sum(s);
+    if ((threadIdx.x & 63) == 0) ws[threadIdx.x >> 6] = s;
+    __syncthreads();
+    if (threadIdx.x == 0) part[blockIdx.x] = (ws[0] + ws[1]) + (ws[2] + ws[3]);
+}
+
+__global__ void mse_finish_kernel(const float *__restrict__ part, int nb, int64_t n,
+                                  float *__restrict__ loss) {
+    if (threadIdx.x != 0) return;
+    float s = 0.f;
+    for (int b = 0; b < nb; ++b) s += part[b];
+    *loss = s / (float)n;
+}
+
+// p −= lr·g; pb = bf16(p) when given.  g may have a row stride (packed
+// gradients): element (r, c) of p [rows, cols] reads g[r·ldg + c].  The
+// product and the difference are rounded separately, as Sgd::put does, so
+// the update is bit-identical to the reference's for the same gradient.
+__global__ void sgd_kernel(float *__restrict__ p, const float *__restrict__ g, int64_t ldg,
+                           int64_t rows, int cols, float lr, bf16_t *__restrict__ pb) {
+#pragma clang fp contract(off)
+    const int64_t n = rows * cols;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+        const int64_t r = i / cols, c = i - r * cols;
+        const float v = p[i] - lr * g[r * ldg + c];
+        p[i] = v;
+        if (pb) pb[i] = f2bf(v);
+    }
+}
+
+// Router STE, per token: dlogits[t, idx_k] = w_k (dw_k − Σ_j w_j dw_j).
+__global__ void router_dlogits_kernel(const int32_t *__restrict__ idx, const float *__restrict__ w,
+                                      const float *__restrict__ dw, int T, int E, int K,
+                                      float *__restrict__ dl) {
+    const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= T) return;
+    float dot = 0.f;
+    for (int j = 0; j < K; ++j) dot += w[(int64_t)t * K + j] * dw[(int64_t)t * K + j];
+    for (int e = 0; e < E; ++e) dl[(int64_t)t * E + e] = 0.f;
+    for (int j = 0; j < K; ++j) {
+        const int e = idx[(int64_t)t * K + j];
+        dl[(int64_t)t * E + e] += w[(int64_t)t * K + j] * (dw[(int64_t)t * K + j] - dot);
+    }
+}
+
+// Partials of dgate[h][e] = Σ_t x[t][h]·dl[t][e] over blocks of 64 tokens.
+__global__ void router_dgate_parts_kernel(const float *__restrict__ x, const float *__restrict__ dl,
+                                          int T, int H, int E, float *__restrict__ part) {
+    const int h = blockIdx.x * blockDim.x + threadIdx.x;
+    if (h >= H) return;
+    const int t0 = blockIdx.y * 64;
+    float acc[64];
+    for (int e = 0; e < E; ++e) acc[e] = 0.f;
+    for (int t = t0; t < t0 + 64 && t < T; ++t) {
+        const float xv = x[(int64_t)t * H + h];
+        for (int e = 0; e < E; ++e) acc[e] += xv * dl[(int64_t)t * E + e];
+    }
+    for (int e = 0; e < E; ++e) part[((int64_t)blockIdx.y * H + h) * E + e] = acc[e];
+}
+
+// Per permuted position: dys[pos] = bf16(w[slot]·dout[tok]) and
+// dw[slot] = Σ_h y[pos][h]·dout[tok][h]; padding positions get zeros.
+__global__ __launch_bounds__(256) void moe_slot_grad_kernel(
+    const int32_t *__restrict__ slot_of_pos, const float *__restrict__ w,
+    const float *__restrict__ y, const float *__restrict__ dout, int K, int H, int n_pos,
+    bf16_t *__restrict__ dys, float *__restrict__ dw) {
+    __shared__ float ws[4];
+    const int pos = blockIdx.x;
+    if (pos >= n_pos) return;
+    const int slot = slot_of_pos[pos];
+    if (slot < 0) {
+        for (int h = threadIdx.x; h < H; h += 256) dys[(int64_t)pos * H + h] = 0;
+        return;
+    }
+    const int t = slot / K;
+    const float wt = w[slot];
+    float s = 0.f;
+    for (int h = threadIdx.x; h < H; h += 256) {
+        const float g = dout[(int64_t)t * H + h];
+        s += y[(int64_t)pos * H + h] * g;
+        dys[(int64_t)pos * H + h] = f2bf(wt * g);
+    }
+    s = wave_sum(s);
+    if ((threadIdx.x & 63) == 0) ws[threadIdx.x >> 6] = s;
+    __syncthreads();
+    if (threadIdx.x == 0) dw[slot] = (ws[0] + ws[1]) + (ws[2] + ws[3]);
+}
+
+// dx[t][h] (+)= Σ_k dxs[pos(t,k)][h] + Σ_e dl[t][e]·gate[h][e].
+__global__ __launch_bounds__(256) void moe_dx_kernel(const float *__restrict__ dxs,
+                                                     const int32_t *__restrict__ pos_of_slot,
+                                                     const float *__restrict__ dl,
+                                                     const float *__restrict__ gate, int T, int K,
+                                                     int H, int E, float *__restrict__ dx,
+                                                     int accumulate) {
+    const int t = blockIdx.x;
+    if (t >= T) return;
+    for (int h = threadIdx.x; h < H; h += 256) {
+        float s = 0.f;
+        for (int kk = 0; kk < K; ++kk)
+            s += dxs[(int64_t)pos_of_slot[(int64_t)t * K + kk] * H + h];
+        float r = 0.f;
+        for (int e = 0; e < E; ++e) r += dl[(int64_t)t * E + e] * gate[(int64_t)h * E + e];
+        s += r;
+        float *o = dx + (int64_t)t * H + h;
+        *o = accumulate ? *o + s : s;
+    }
+}
+
+}  // namespace
+
+void fill_f32(hipStream_t s, float *y, float v, int64_t n) {
+    if (n <= 0) return;
+    fill_kernel<<<blocks_for(n, 256 * 4), 256, 0, s>>>(y, v, n);
+    CATNN_HIP(hipGetLastError());
+}
+
+void fill_bf16_zero(hipStream_t s, bf16_t *y, int64_t n) {
+    if (n <= 0) return;
+    fill_bf16_kernel<<<blocks_for(n, 256 * 4), 256, 0, s>>>(y, n);
+    CATNN_HIP(hipGetLastError());
+}
+
+void cast_f32_bf16(hipStream_t s, const float *x, bf16_t *y, int64_t n) {
+    if (n <= 0) return;
+    cast_kernel<<<blocks_for(n, 256 * 4), 256, 0, s>>>(x, y, n);
+    CATNN_HIP(hipGetLastError());
+}
+
+static dim3 tgrid(int rows, int cols) {
+    return dim3((unsigned)((cols + 63) / 64), (unsigned)((rows + 63) / 64));
+}
+
+void transpose_bf16(hipStream_t s, const bf16_t *src, int64_t lds, const int32_t *rows_map, int div,
+                    int rows, int cols, bf16_t *dst, int64_t ldd) {
+    if (rows <= 0 || cols <= 0) return;
+    CATNN_REQUIRE((rows + 63) / 64 < 65536, CATNN_ERR_SHAPE_MISMATCH, "transpose: too many rows");
+    transpose_kernel<bf16_t><<<tgrid(rows, cols), 256, 0, s>>>(src, lds, rows_map, div, rows, cols,
+                                                               dst, ldd);
+    CATNN_HIP(hipGetLastError());
+}
+
+void transpose_f32_bf16(hipStream_t s, const float *src, int64_t lds, const int32_t *rows_map,
+                        int div, int rows, int cols, bf16_t *dst, int64_t ldd) {
+    if (rows <= 0 || cols <= 0) return;
+    CATNN_REQUIRE((rows + 63) / 64 < 65536, CATNN_ERR_SHAPE_MISMATCH, "transpose: too many rows");
+    transpose_kernel<float><<<tgrid(rows, cols), 256, 0, s>>>(src, lds, rows_map, div, rows, cols,
+                                                              dst, ldd);
+    CATNN_HIP(hipGetLastError());
+}
+
+void ln_forward_train(hipStream_t s, const float *x, const float *g, const float *b, float *y,
+                      bf16_t *yb, float *mean, float *rstd, int64_t rows, int cols, float eps) {
+    if (rows <= 0) return;
+    ln_fwd_kernel<<<(unsigned)((rows + 3) / 4), 256, 0, s>>>(x, g, b, y, yb, mean, rstd, rows, cols,
+                                                             eps);
+    CATNN_HIP(hipGetLastError());
+}
+
+uint64_t ln_backward_scratch_bytes(int64_t rows, int cols) {
+    const int64_t nb = (rows + kLnRowsPerBlock - 1) / kLnRowsPerBlock;
+    return (uint64_t)nb * cols * 4 * 2;
+}
+
+void ln_backward(hipStream_t s, const float *x, const float *g, const float *mean, const float *rstd,
+                 const float *dy, float *dx, bool accumulate, float *dg, float *db, bool acc_params,
+                 int64_t rows, int cols, float *scratch) {
+    if (rows <= 0) return;
+    const int64_t nb = (rows + kLnRowsPerBlock - 1) / kLnRowsPerBlock;
+    float *pg = scratch, *pb = scratch + nb * cols;
+    ln_bwd_kernel<<<(unsigned)nb, 256, 0, s>>>(x, g, mean, rstd, dy, dx, accumulate ? 1 : 0, pg, pb,
+                                               rows, cols);
+    CATNN_HIP(hipGetLastError());
+    reduce_parts_kernel<<<(cols + 255) / 256, 256, 0, s>>>(pg, (int)nb, cols, dg, acc_params);
+    reduce_parts_kernel<<<(cols + 255) / 256, 256, 0, s>>>(pb, (int)nb, cols, db, acc_params);
+    CATNN_HIP(hipGetLastError());
+}
+
+uint64_t colsum_scratch_bytes(int64_t rows, int cols) {
+    return (uint64_t)((rows + 63) / 64) * cols * 4;
+}
+
+void colsum(hipStream_t s, const float *y, int64_t rows, int cols, float *out, bool accumulate,
+            float *scratch) {
+    if (rows <= 0 || cols <= 0) return;
+    const int64_t nb = (rows + 63) / 64;
+    CATNN_REQUIRE(nb < 65536, CATNN_ERR_SHAPE_MISMATCH, "colsum: too many rows");
+    colsum_parts_kernel<<<dim3((cols + 255) / 256, (unsigned)nb), 256, 0, s>>>(y, rows, cols, scratch);
+    reduce_parts_kernel<<<(cols + 255) / 256, 256, 0, s>>>(scratch, (int)nb, cols, out, accumulate);
+    CATNN_HIP(hipGetLastError());
+}
+
+void act_backward(hipStream_t s, const float *z, const float *dy, float *dx, int64_t n, int act,
+                  bool accumulate) {
+    if (n <= 0) return;
+    act_bwd_kernel<<<blocks_for(n, 256 * 4), 256, 0, s>>>(z, dy, dx, n, act, accumulate ? 1 : 0);
+    CATNN_HIP(hipGetLastError());
+}
+
+constexpr int kMseBlocks = 1024;
+
+uint64_t mse_scratch_bytes() { return kMseBlocks * 4; }
+
+void mse(hipStream_t s, const float *pred, const float *tgt, float *d, int64_t n, float *loss,
+         float *scratch) {
+    CATNN_REQUIRE(n > 0, CATNN_ERR_SHAPE_MISMATCH, "mse on empty tensors");
+    mse_kernel<<<kMseBlocks, 256, 0, s>>>(pred, tgt, d, n, scratch);
+    mse_finish_kernel<<<1, 64, 0, s>>>(scratch, kMseBlocks, n, loss);
+    CATNN_HIP(hipGetLastError());
+}
+
+void sgd(hipStream_t s, float *p, const float *g, int64_t ldg, int64_t rows, int cols, float lr,
+         bf16_t *pb) {
+    if (rows * cols <= 0) return;
+    sgd_kernel<<<blocks_for(rows * cols, 256 * 4), 256, 0, s>>>(p, g, ldg, rows, cols, lr, pb);
+    CATNN_HIP(hipGetLastError());
+}
+
+void router_backward(hipStream_t s, const int32_t *idx, const float *w, const float *dw,
+                     const float *x, int T, int H, int E, int K, float *dl, float *dgate,
+                     float *scratch) {
+    CATNN_REQUIRE(E <= 64, CATNN_ERR_SHAPE_MISMATCH, "router backward: more than 64 experts");
+    if (T <= 0) return;
+    router_dlogits_kernel<<<(T + 255) / 256, 256, 0, s>>>(idx, w, dw, T, E, K, dl);
+    const int nb = (T + 63) / 64;
+    router_dgate_parts_kernel<<<dim3((H + 127) / 128, (unsigned)nb), 128, 0, s>>>(x, dl, T, H, E,
+                                                                                 scratch);
+    reduce_parts_kernel<<<(H * E + 255) / 256, 256, 0, s>>>(scratch, nb, H * E, dgate, false);
+    CATNN_HIP(hipGetLastError());
+}
+
+uint64_t router_backward_scratch_bytes(int T, int H, int E) {
+    return (uint64_t)((T + 63) / 64) * H * E * 4;
+}
+
+void moe_slot_grads(hipStream_t s, const int32_t *slot_of_pos, const float *w, const float *y,
+                    const float *dout, int K, int H, int n_pos, bf16_t *dys, float *dw) {
+    if (n_pos <= 0) return;
+    moe_slot_grad_kernel<<<(unsigned)n_pos, 256, 0, s>>>(slot_of_pos, w, y, dout, K, H, n_pos, dys, dw);
+    CATNN_HIP(hipGetLastError());
+}
+
+void moe_dx(hipStream_t s, const float *dxs, const int32_t *pos_of_slot, const float *dl,
+            const float *gate, int T, int K, int H, int E, float *dx, bool accumulate) {
+    if (T <= 0) return;
+    moe_dx_kernel<<<(unsigned)T, 256, 0, s>>>(dxs, pos_of_slot, dl, gate, T, K, H, E, dx,
+                                              accumulate ? 1 : 0);
+    CATNN_HIP(hipGetLastError());
+}
+
+}  // namespace k
+}  // namespace catnn

@@ -1,0 +1,77 @@
+// Launchers of the training-step kernels (train_ops.hip, attention.hip's
+// adjoint, moe.hip's padded permutation).
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+
+#include <cstdint>
+
+#include "gemm_bf16.hpp"
+
+namespace catnn {
+namespace k {
+
+void fill_f32(hipStream_t s, float *y, float v, int64_t n);
+void fill_bf16_zero(hipStream_t s, bf16_t *y, int64_t n);
+void cast_f32_bf16(hipStream_t s, const float *x, bf16_t *y, int64_t n);
+// dst[c][r] = src[map(r)][c]; map(r) = rows_map[r] / div (negative: zero row).
+void transpose_bf16(hipStream_t s, const bf16_t *src, int64_t lds, const int32_t *rows_map, int div,
+                    int rows, int cols, bf16_t *dst, int64_t ldd);
+void transpose_f32_bf16(hipStream_t s, const float *src, int64_t lds, const int32_t *rows_map,
+                        int div, int rows, int cols, bf16_t *dst, int64_t ldd);
+
+void ln_forward_train(hipStream_t s, const float *x, const float *g, const float *b, float *y,
+                      bf16_t *yb, float *mean, float *rstd, int64_t rows, int cols, float eps);
+uint64_t ln_backward_scratch_bytes(int64_t rows, int cols);
+void ln_backward(hipStream_t s, const float *x, const float *g, const float *mean, const float *rstd,
+                 const float *dy, float *dx, bool accumulate, float *dg, float *db, bool acc_params,
+                 int64_t rows, int cols, float *scratch);
+
+uint64_t colsum_scratch_bytes(int64_t rows, int cols);
+void colsum(hipStream_t s, const float *y, int64_t rows, int cols, float *out, bool accumulate,
+            float *scratch);
+void act_backward(hipStream_t s, const float *z, const float *dy, float *dx, int64_t n, int act,
+                  bool accumulate);
+
+uint64_t mse_scratch_bytes();
+void mse(hipStream_t s, const float *pred, const float *tgt, float *d, int64_t n, float *loss,
+         float *scratch);
+void sgd(hipStream_t s, float *p, const float *g, int64_t ldg, int64_t rows, int cols, float lr,
+         bf16_t *pb);
+
+uint64_t router_backward_scratch_bytes(int T, int H, int E);
+void router_backward(hipStream_t s, const int32_t *idx, const float *w, const float *dw,
+                     const float *x, int T, int H, int E, int K, float *dl, float *dgate,
+                     float *scratch);
+void moe_slot_grads(hipStream_t s, const int32_t *slot_of_pos, const float *w, const float *y,
+                    const float *dout, int K, int H, int n_pos, bf16_t *dys, float *dw);
+void moe_dx(hipStream_t s, const float *dxs, const int32_t *pos_of_slot, const float *dl,
+            const float *gate, int T, int K, int H, int E, float *dx, bool accumulate);
+
+// Permutation with every expert segment starting on a multiple of `pad`
+// rows: offsets[e] = Σ_{e'<e} roundup(counts[e'], pad), offsets[E] = total;
+// slot_of_pos is −1 on padding rows.  n_pos_cap must be ≥ T·k + E·(pad−1).
+void moe_permute_padded(hipStream_t s, const int32_t *idx, int64_t tokens, int64_t top_k,
+                        int64_t n_experts, int pad, int64_t n_pos_cap, int32_t *counts,
+                        int32_t *offsets, int32_t *slot_of_pos, int32_t *pos_of_slot,
+                        void *scratch);
+
+// out[t] = Σ_k w[t,k]·y[pos(t,k)] (the MoE combine of moe.hip).
+void moe_combine(hipStream_t s, const float *y, const int32_t *pos_of_slot, const float *w,
+                 int64_t tokens, int64_t top_k, int64_t hidden, float *out);
+
+// Attention forward that also stores the per-(query, head) log-sum-exp
+// (log2 domain, scores pre-scaled by log2e/√dh) for the adjoint.
+void attention_core_fwd_lse(hipStream_t s, const float *q, const float *k, const float *v, int64_t ld,
+                            float *ctx, int64_t ldo, float *lse, int64_t batch, int64_t seq,
+                            int64_t n_heads, int64_t d_head, bool causal);
+// Adjoint of the attention core: dq, dk, dv (row stride ld_d, head h at
+// column h·dh) from q, k, v, o (= ctx), lse and do (row stride ldo).
+uint64_t attention_bwd_scratch_bytes(int64_t batch, int64_t seq, int64_t n_heads);
+void attention_core_bwd(hipStream_t s, const float *q, const float *k, const float *v, int64_t ld,
+                        const float *o, const float *dout, int64_t ldo, const float *lse,
+                        float *dq, float *dk, float *dv, int64_t ld_d, int64_t batch, int64_t seq,
+                        int64_t n_heads, int64_t d_head, bool causal, float *scratch);
+
+}  // namespace k
+}  // namespace catnn

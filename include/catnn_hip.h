@@ -303,6 +303,44 @@ int catnn_hip_program_profile(catnn_hip_program *p, int32_t enable);
 int catnn_hip_program_timings(catnn_hip_program *p, catnn_step_timing *out,
                               int32_t cap, int32_t *n);
 
+/* ------------------------------------------------------------ training */
+/* One training step of an IrGraph on this device: replaces
+ * pipeline::reference_train (crates/catnn-compile/src/pipeline.rs:476-547)
+ * for one step with MSE (kernel/adjoint.rs:106-119) and SGD (Sgd::put,
+ * crates/catnn-core/src/lens/optim.rs:32-42), i.e. the adjoint_of,
+ * rematerialisation and apply_update seams of the training wave
+ * (crates/catnn-rt/src/coord.rs:413, :470, :481), which bypass the handler
+ * in the reference.  Executable ops: Identity, Linear/MatMul, Relu, Gelu,
+ * LayerNorm, Add/ResidualAdd (same length), Attention (causal flag
+ * honoured), MoE.  GEMM operands are bf16 (bf16 MFMA, fp32 accumulation);
+ * master weights, the residual stream, norms, router and accumulation are
+ * fp32.  All buffers live in one hipMalloc arena planned by place_arena on
+ * the reference's training ticks (pipeline.rs:280-284). */
+typedef struct catnn_hip_trainer catnn_hip_trainer;
+
+int catnn_hip_train_install(catnn_hip_device *dev, const catnn_graph *g, float lr,
+                            catnn_hip_trainer **out);
+int catnn_hip_train_free(catnn_hip_trainer *t);
+/* Upload the batch: `input` is bound to every graph input, `target` is the
+ * MSE target of the last output. */
+int catnn_hip_train_set_batch(catnn_hip_trainer *t, const catnn_tensor *input,
+                              const catnn_tensor *target);
+/* forward, loss, backward, SGD on the resident batch; `loss` (or NULL:
+ * no synchronisation) receives the step's MSE before the update. */
+int catnn_hip_train_step(catnn_hip_trainer *t, float *loss);
+/* fp32 master weight / last gradient of param `port` of node `node_id`
+ * (Attention's wq, wk, wv are read out of the packed projection). */
+int catnn_hip_train_read_param(catnn_hip_trainer *t, uint32_t node_id, const char *port,
+                               float *host, int64_t n);
+int catnn_hip_train_read_grad(catnn_hip_trainer *t, uint32_t node_id, const char *port,
+                              float *host, int64_t n);
+/* Forward value of node `node_id` from the last step. */
+int catnn_hip_train_read_value(catnn_hip_trainer *t, uint32_t node_id, float *host, int64_t n);
+/* Expert indices [T, top_k] chosen by MoE node `node_id` in the last step. */
+int catnn_hip_train_read_routing(catnn_hip_trainer *t, uint32_t node_id, int32_t *idx, int64_t n);
+int catnn_hip_train_arena(catnn_hip_trainer *t, catnn_arena_alloc *out, int32_t cap, int32_t *n,
+                          uint64_t *reserved_bytes);
+
 /* ------------------------------------------------------------- events */
 /* Sheaf events (crates/catnn-rt/src/sheaf.rs:55-79) recorded by the
  * handler seam: times in ns from device open, checksum = FNV-1a over the
