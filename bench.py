@@ -20,7 +20,9 @@ epilogue).  Reported:
                   Rayon, then cpu::gelu and the bias pass) on a row subset of
                   the same inputs, timed on this host;
   * secondary   — the same measurement for the MoE layer (config 4,
-                  tokens/s) and the pre-LN transformer block (config 3).
+                  tokens/s) and the pre-LN transformer block (config 3), and
+                  the config-5 training step (block + MoE, forward, MSE,
+                  backward, SGD).
 Only one GPU is used: --gpus above 1 exits with a message.
 """
 import argparse
@@ -59,6 +61,49 @@ def time_program(dev, prog, x, steps, warmup):
     timings = prog.timings()
     prog.profile(False)
     return ms / steps, wall, timings
+
+
+BF16_MFMA_PEAK_TFLOPS = 2500.0
+
+
+def time_train_step(dev, steps, warmup):
+    """Config 5: one training step (forward, MSE, backward, SGD) of the
+    config-3 block followed by the config-4 MoE layer.  Every timed step
+    starts from the installed weights (Trainer.reset, outside the timed
+    region): at this initialisation lr 0.05 drives the weights to NaN within
+    two steps, which would collapse the routing and time another workload."""
+    import catnn_amd
+    from catnn_amd import configs
+
+    wl = configs.config5()
+    log("config 5 built")
+    tr = catnn_amd.Trainer(dev, wl.graph, wl.lr)
+    tr.set_batch(wl.x, wl.target)
+    for _ in range(warmup):
+        tr.reset()
+        tr.step()
+    total = 0.0
+    loss = None
+    for _ in range(steps):
+        tr.reset()
+        dev.sync()
+        dev.timer_start()
+        tr.step(sync=False)
+        total += dev.timer_stop()
+    tr.reset()
+    loss = tr.step()
+    allocs, reserved = tr.arena()
+    tr.free()
+    ms = total / steps
+    tflops = wl.flops / (ms / 1e3) / 1e12
+    log(f"config 5: {ms:.3f} ms/step, {tflops:.1f} TFLOP/s algorithmic, loss {loss:.3f}")
+    return {"ms_per_step": round(ms, 4), "tokens_per_s": round(wl.tokens / (ms / 1e3)),
+            "algorithmic_TFLOP_per_s": round(tflops, 2),
+            "bf16_mfma_frac": round(tflops / BF16_MFMA_PEAK_TFLOPS, 4),
+            "flop_per_step": wl.flops, "first_step_loss": round(loss, 4),
+            "arena_reserved_bytes": reserved, "arena_buffers": len(allocs),
+            "precision": "bf16 MFMA, fp32 accumulation and master weights; split-bf16 forward "
+                         "GEMMs for Linear/attention; attention core fp32 MFMA"}
 
 
 def cpu_baseline_mlp(wl, target_s):
@@ -124,6 +169,17 @@ def pmc_probe(which):
     a.free()
     b.free()
     builders = {"config2": configs.config2, "config3": configs.config3, "config4": configs.config4}
+    if which == "config5":
+        wl = configs.config5()
+        tr = catnn_amd.Trainer(dev, wl.graph, wl.lr)
+        tr.set_batch(wl.x, wl.target)
+        for i in range(3):
+            tr.reset()
+            tr.step()
+            log(f"config5: step {i} done")
+        tr.free()
+        dev.close()
+        return
     for name in (builders if which == "all" else [which]):
         wl = builders[name]()
         prog = catnn_amd.Program(dev, wl.graph)
@@ -138,7 +194,7 @@ def pmc_probe(which):
 
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
-    ap.add_argument("--pmc-probe", choices=["config2", "config3", "config4", "all"],
+    ap.add_argument("--pmc-probe", choices=["config2", "config3", "config4", "config5", "all"],
                     help="run the copy calibration and the workload for rocprofv3 --pmc, then exit")
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
@@ -221,7 +277,9 @@ def main():
             "ms_per_step": round(ms3, 4), "GFLOP_per_s": round(w3.flops / (ms3 / 1e3) / 1e9, 1),
             "steps_ms": {t[0]: round(t[3] / max(t[2], 1), 4) for t in t3}}
         p3.free()
+        del w3
         log(f"config 3: {ms3:.3f} ms/step")
+        sec["train_step_config5"] = time_train_step(dev, max(3, args.steps // 2), 2)
         result["secondary"] = sec
 
     if not args.no_cpu_baseline:

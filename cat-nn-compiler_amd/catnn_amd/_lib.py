@@ -135,6 +135,7 @@ SIGNATURES = {
     "catnn_hip_train_free": [_VP],
     "catnn_hip_train_set_batch": [_VP, ctypes.POINTER(CTensor), ctypes.POINTER(CTensor)],
     "catnn_hip_train_step": [_VP, ctypes.POINTER(_F)],
+    "catnn_hip_train_reset": [_VP],
     "catnn_hip_train_read_param": [_VP, ctypes.c_uint32, ctypes.c_char_p, ctypes.POINTER(_F), _I64],
     "catnn_hip_train_read_grad": [_VP, ctypes.c_uint32, ctypes.c_char_p, ctypes.POINTER(_F), _I64],
     "catnn_hip_train_read_value": [_VP, ctypes.c_uint32, ctypes.POINTER(_F), _I64],

@@ -15,6 +15,7 @@
 from __future__ import annotations
 
 import ctypes
+import weakref
 from dataclasses import dataclass
 from typing import List, Optional, Sequence, Tuple
 
@@ -32,6 +33,12 @@ class Device:
         self.handle = VP()
         check(lib.catnn_hip_open(ordinal, ctypes.byref(self.handle)))
         self.ordinal = ordinal
+        # Programs, trainers and buffers hold the device handle: close() frees
+        # them first so none outlives it.
+        self._owned = weakref.WeakSet()
+
+    def _adopt(self, obj):
+        self._owned.add(obj)
 
     @staticmethod
     def count() -> int:
@@ -51,6 +58,8 @@ class Device:
 
     def close(self):
         if self.handle:
+            for obj in list(self._owned):
+                obj.free()
             check(lib.catnn_hip_close(self.handle))
             self.handle = VP()
 
@@ -121,6 +130,7 @@ class DeviceBuffer:
         self.nbytes = int(nbytes)
         self.ptr = VP()
         check(lib.catnn_hip_alloc(dev.handle, max(self.nbytes, 4), ctypes.byref(self.ptr)))
+        dev._adopt(self)
 
     def upload(self, arr: np.ndarray):
         arr = np.ascontiguousarray(arr)
@@ -202,6 +212,7 @@ class Program:
             check(lib.catnn_hip_install(device.handle, h, ctypes.byref(self.handle)))
         finally:
             lib.catnn_graph_free(h)
+        device._adopt(self)
 
     def forward(self, x: Optional[Tensor]) -> Tensor:
         io = self.io()

@@ -33,6 +33,7 @@ class Trainer:
                                               ctypes.byref(self.handle)))
         finally:
             lib.catnn_graph_free(h)
+        device._adopt(self)
 
     def set_batch(self, x: Tensor, target: Tensor):
         cx, ct = ctensor(x), ctensor(target)
@@ -46,6 +47,10 @@ class Trainer:
         loss = ctypes.c_float()
         check(lib.catnn_hip_train_step(self.handle, ctypes.byref(loss)))
         return float(loss.value)
+
+    def reset(self):
+        """Restore every parameter to its installed value (asynchronous)."""
+        check(lib.catnn_hip_train_reset(self.handle))
 
     def _read(self, fn, node_id: int, port: str, shape) -> np.ndarray:
         out = np.empty(shape, np.float32)

@@ -14,10 +14,15 @@
 //   update    p −= lr·g on the fp32 master weights (Sgd::put,
 //             lens/optim.rs:32-42), then the bf16 copies are refreshed.
 //
-// Precision: GEMM operands (activations, weights, cotangents) are bf16 on
-// v_mfma_f32_32x32x16_bf16 with fp32 accumulation; master weights, the
-// residual stream, LayerNorm, softmax statistics, the router and all
-// cotangent accumulation stay fp32.  The attention core runs on fp32 MFMA.
+// Precision: every GEMM runs on v_mfma_f32_32x32x16_bf16 with fp32
+// accumulation.  The forward GEMMs of Linear and attention take split-bf16
+// operands (hi|hi|lo against hi|lo|hi over 3K: the fp32 product to ~2⁻¹⁶),
+// because with plain bf16 operands there the error of the block's output
+// reaches the MoE layer and moves the step's gradients by more than 1e-2
+// from the fp32 path; the MoE expert forward and every backward GEMM take
+// plain bf16 operands.  Master weights, the residual stream, LayerNorm,
+// softmax statistics, the router and all cotangent accumulation stay fp32;
+// the attention core runs on fp32 MFMA.
 //
 // Memory: every buffer (params, their bf16 copies and gradients, values,
 // cotangents, tapes, scratch) is a BufferReq on the reference's logical
@@ -54,9 +59,10 @@ struct TParam {
     std::string name;       // "param:{node}:{port}"
     int64_t rows = 0, cols = 0;
     std::vector<float> init;  // host values uploaded at install
-    bool want_b = false, want_bt = false;
+    bool want_b = false, want_bt = false, want_bt3 = false;
     float *master = nullptr, *grad = nullptr;
     bf16_t *b = nullptr, *bt = nullptr;
+    bf16_t *bt3 = nullptr;  // [cols, 3·rows] split-bf16 transposed copy (hi | lo | hi)
 };
 
 struct TNode {
@@ -234,7 +240,7 @@ static void plan_trainer(Tr &t) {
     request(t, "mse_scratch", k::mse_scratch_bytes(), n, n, reinterpret_cast<void **>(&t.mse_scratch));
 
     auto add_param = [&](TNode &tn, const std::string &port, int64_t rows, int64_t cols, bool b, bool bt,
-                         std::vector<float> init) {
+                         std::vector<float> init, bool bt3 = false) {
         auto p = std::make_unique<TParam>();
         p->name = "param:" + tn.node->name + ":" + port;
         p->rows = rows;
@@ -242,11 +248,13 @@ static void plan_trainer(Tr &t) {
         p->init = std::move(init);
         p->want_b = b || bt;
         p->want_bt = bt;
+        p->want_bt3 = bt3;
         const uint64_t e = (uint64_t)(rows * cols);
         request(t, p->name, e * 4, 0, upd, reinterpret_cast<void **>(&p->master));
         request(t, "grad:" + p->name, e * 4, bwd(tn.tick), upd, reinterpret_cast<void **>(&p->grad));
         if (p->want_b) request(t, "bf16:" + p->name, e * 2, 0, upd, reinterpret_cast<void **>(&p->b));
         if (p->want_bt) request(t, "bf16t:" + p->name, e * 2, 0, upd, reinterpret_cast<void **>(&p->bt));
+        if (p->want_bt3) request(t, "bf16t3:" + p->name, e * 6, 0, upd, reinterpret_cast<void **>(&p->bt3));
         tn.params[port] = p.get();
         t.params.push_back(std::move(p));
     };
@@ -272,9 +280,9 @@ static void plan_trainer(Tr &t) {
                 const HostTensor *w = nd.param("w") ? nd.param("w") : (nd.params.empty() ? nullptr : &nd.params.front().second);
                 CATNN_REQUIRE(w, CATNN_ERR_UNKNOWN_COMPONENT, "unknown component " + nd.name);
                 const int64_t K = w->dims[0], N = w->dims[1], M = numel(x) / K;
-                add_param(tn, nd.param("w") ? "w" : nd.params.front().first, K, N, true, true, w->data);
+                add_param(tn, nd.param("w") ? "w" : nd.params.front().first, K, N, true, false, w->data, true);
                 if (const HostTensor *b = nd.param("b")) add_param(tn, "b", 1, N, false, false, b->data);
-                tape(tn, "xb", (uint64_t)(M * K) * 2);
+                tape(tn, "x3", (uint64_t)(M * 3 * K) * 2);
                 scratch(tn, "xbt", (uint64_t)(M * K) * 2);
                 scratch(tn, "dyb", (uint64_t)(M * N) * 2);
                 scratch(tn, "dybt", (uint64_t)(M * N) * 2);
@@ -299,12 +307,12 @@ static void plan_trainer(Tr &t) {
                     std::memcpy(&packed[(size_t)(r * 3 * D + D)], &wk->data[(size_t)(r * D)], (size_t)D * 4);
                     std::memcpy(&packed[(size_t)(r * 3 * D + 2 * D)], &wv->data[(size_t)(r * D)], (size_t)D * 4);
                 }
-                add_param(tn, "wqkv", D, 3 * D, true, true, std::move(packed));
-                add_param(tn, "wo", D, D, true, true, host(nd, "wo")->data);
-                tape(tn, "xb", (uint64_t)(T * D) * 2);
+                add_param(tn, "wqkv", D, 3 * D, true, false, std::move(packed), true);
+                add_param(tn, "wo", D, D, true, false, host(nd, "wo")->data, true);
+                tape(tn, "x3", (uint64_t)(T * 3 * D) * 2);
                 tape(tn, "qkv", (uint64_t)(T * 3 * D) * 4);
                 tape(tn, "ctx", (uint64_t)(T * D) * 4);
-                tape(tn, "ctxb", (uint64_t)(T * D) * 2);
+                tape(tn, "ctx3", (uint64_t)(T * 3 * D) * 2);
                 tape(tn, "lse", (uint64_t)(T * H) * 4);
                 scratch(tn, "dyb", (uint64_t)(T * D) * 2);
                 scratch(tn, "dybt", (uint64_t)(T * D) * 2);
@@ -363,6 +371,18 @@ static void plan_trainer(Tr &t) {
     }
 }
 
+// Masters from the host copies, then the bf16 operand copies from the masters.
+static void upload_params(Tr &t) {
+    hipStream_t s = t.dev->stream;
+    for (auto &p : t.params) {
+        CATNN_HIP(hipMemcpyAsync(p->master, p->init.data(), p->init.size() * 4, hipMemcpyHostToDevice, s));
+        if (p->want_b) k::cast_f32_bf16(s, p->master, p->b, p->rows * p->cols);
+        if (p->want_bt)
+            k::transpose_bf16(s, p->b, p->cols, nullptr, 1, (int)p->rows, (int)p->cols, p->bt, p->rows);
+        if (p->want_bt3) k::transpose_split3(s, p->master, p->cols, (int)p->rows, (int)p->cols, p->bt3, 3 * p->rows);
+    }
+}
+
 static void reserve_and_upload(Tr &t) {
     hipDeviceProp_t prop;
     CATNN_HIP(hipGetDeviceProperties(&prop, t.dev->ordinal));
@@ -377,17 +397,11 @@ static void reserve_and_upload(Tr &t) {
     for (const auto &a : t.plan) off[a.id] = a.offset;
     for (size_t i = 0; i < t.reqs.size(); ++i)
         *t.req_slot[i] = static_cast<char *>(t.base) + off.at(t.reqs[i].id);
-    hipStream_t s = t.dev->stream;
-    for (auto &p : t.params) {
+    for (auto &p : t.params)
         CATNN_REQUIRE((int64_t)p->init.size() == p->rows * p->cols, CATNN_ERR_SHAPE_MISMATCH,
                       p->name + ": parameter size");
-        CATNN_HIP(hipMemcpyAsync(p->master, p->init.data(), p->init.size() * 4, hipMemcpyHostToDevice, s));
-        if (p->want_b) k::cast_f32_bf16(s, p->master, p->b, p->rows * p->cols);
-        if (p->want_bt)
-            k::transpose_bf16(s, p->b, p->cols, nullptr, 1, (int)p->rows, (int)p->cols, p->bt, p->rows);
-    }
-    CATNN_HIP(hipStreamSynchronize(s));
-    for (auto &p : t.params) std::vector<float>().swap(p->init);
+    upload_params(t);
+    CATNN_HIP(hipStreamSynchronize(t.dev->stream));
 }
 
 // ------------------------------------------------------------ forward
@@ -416,11 +430,12 @@ static void forward_node(Tr &t, TNode &tn) {
             for (auto &kv : tn.params) if (kv.first != "b") w = kv.second;
             TParam *b = tn.params.count("b") ? tn.params["b"] : nullptr;
             const int64_t K = w->rows, N = w->cols, M = nx / K;
-            bf16_t *xb = (bf16_t *)tn.B("xb");
-            k::cast_f32_bf16(s, x, xb, M * K);
+            // Split-bf16 forward: [hi|hi|lo]·[hi|lo|hi] over 3K ≈ the fp32 product.
+            bf16_t *x3 = (bf16_t *)tn.B("x3");
+            k::split3_rows(s, x, K, M, (int)K, x3, 3 * K);
             k::GemmBf16Params p = gp();
-            p.A = xb; p.lda = K; p.B = w->bt; p.ldb = K;
-            p.M = (int)M; p.N = (int)N; p.K = (int)K;
+            p.A = x3; p.lda = 3 * K; p.B = w->bt3; p.ldb = 3 * K;
+            p.M = (int)M; p.N = (int)N; p.K = (int)(3 * K);
             p.epi = k::EPI_LINEAR; p.bias = b ? b->master : nullptr;
             p.C32 = y; p.ldc32 = N;
             k::gemm_bf16_launch(s, p);
@@ -437,15 +452,16 @@ static void forward_node(Tr &t, TNode &tn) {
             const int64_t Bt = xd[0], S = xd[1], D = xd[2], T = Bt * S;
             const int64_t H = nd.op.a[0], dh = nd.op.a[2];
             const bool causal = (nd.op.flags & CATNN_FLAG_CAUSAL) != 0;
-            bf16_t *xb = (bf16_t *)tn.B("xb");
+            bf16_t *x3 = (bf16_t *)tn.B("x3"), *ctx3 = (bf16_t *)tn.B("ctx3");
             float *qkv = (float *)tn.B("qkv"), *ctx = (float *)tn.B("ctx");
-            bf16_t *ctxb = (bf16_t *)tn.B("ctxb");
-            k::cast_f32_bf16(s, x, xb, T * D);
-            gemm_nt(s, xb, D, tn.params["wqkv"]->bt, D, (int)T, (int)(3 * D), (int)D, qkv, 3 * D, false);
+            // Both projections split-bf16 (K' = 3D), the core on fp32 MFMA.
+            k::split3_rows(s, x, D, T, (int)D, x3, 3 * D);
+            gemm_nt(s, x3, 3 * D, tn.params["wqkv"]->bt3, 3 * D, (int)T, (int)(3 * D), (int)(3 * D), qkv, 3 * D,
+                    false);
             k::attention_core_fwd_lse(s, qkv, qkv + D, qkv + 2 * D, 3 * D, ctx, D, (float *)tn.B("lse"), Bt,
                                       S, H, dh, causal);
-            k::cast_f32_bf16(s, ctx, ctxb, T * D);
-            gemm_nt(s, ctxb, D, tn.params["wo"]->bt, D, (int)T, (int)D, (int)D, y, D, false);
+            k::split3_rows(s, ctx, D, T, (int)D, ctx3, 3 * D);
+            gemm_nt(s, ctx3, 3 * D, tn.params["wo"]->bt3, 3 * D, (int)T, (int)D, (int)(3 * D), y, D, false);
             break;
         }
         case CATNN_OP_MOE: {
@@ -526,11 +542,11 @@ static void backward_node(Tr &t, TNode &tn) {
             TParam *b = tn.params.count("b") ? tn.params["b"] : nullptr;
             const int64_t K = w->rows, N = w->cols, M = nx / K;
             bf16_t *dyb = (bf16_t *)tn.B("dyb"), *dybt = (bf16_t *)tn.B("dybt");
-            bf16_t *xb = (bf16_t *)tn.B("xb"), *xbt = (bf16_t *)tn.B("xbt");
+            bf16_t *x3 = (bf16_t *)tn.B("x3"), *xbt = (bf16_t *)tn.B("xbt");
             k::cast_f32_bf16(s, dy, dyb, M * N);
             if (dst(0)) gemm_nt(s, dyb, N, w->b, N, (int)M, (int)K, (int)N, dst(0), K, !tn.first_writer[0]);
             k::transpose_bf16(s, dyb, N, nullptr, 1, (int)M, (int)N, dybt, M);
-            k::transpose_bf16(s, xb, K, nullptr, 1, (int)M, (int)K, xbt, M);
+            k::transpose_bf16(s, x3, 3 * K, nullptr, 1, (int)M, (int)K, xbt, M);  // hi part of x
             gemm_nt(s, xbt, M, dybt, M, (int)K, (int)N, (int)M, w->grad, N, false);
             if (b) k::colsum(s, dy, M, (int)N, b->grad, false, (float *)tn.B("colsum"));
             break;
@@ -551,12 +567,12 @@ static void backward_node(Tr &t, TNode &tn) {
             bf16_t *dyb = (bf16_t *)tn.B("dyb"), *dybt = (bf16_t *)tn.B("dybt"), *ctxt = (bf16_t *)tn.B("ctxt");
             float *dctx = (float *)tn.B("dctx"), *dqkv = (float *)tn.B("dqkv");
             bf16_t *dqkvb = (bf16_t *)tn.B("dqkvb"), *dqkvt = (bf16_t *)tn.B("dqkvt");
-            bf16_t *xb = (bf16_t *)tn.B("xb"), *xbt = (bf16_t *)tn.B("xbt");
+            bf16_t *x3 = (bf16_t *)tn.B("x3"), *xbt = (bf16_t *)tn.B("xbt");
             float *qkv = (float *)tn.B("qkv");
             k::cast_f32_bf16(s, dy, dyb, T * D);
             gemm_nt(s, dyb, D, wo->b, D, (int)T, (int)D, (int)D, dctx, D, false);
             k::transpose_bf16(s, dyb, D, nullptr, 1, (int)T, (int)D, dybt, T);
-            k::transpose_bf16(s, (bf16_t *)tn.B("ctxb"), D, nullptr, 1, (int)T, (int)D, ctxt, T);
+            k::transpose_bf16(s, (bf16_t *)tn.B("ctx3"), 3 * D, nullptr, 1, (int)T, (int)D, ctxt, T);
             gemm_nt(s, ctxt, T, dybt, T, (int)D, (int)D, (int)T, wo->grad, D, false);
             k::attention_core_bwd(s, qkv, qkv + D, qkv + 2 * D, 3 * D, (float *)tn.B("ctx"), dctx, D,
                                   (float *)tn.B("lse"), dqkv, dqkv + D, dqkv + 2 * D, 3 * D, Bt, S, H, dh,
@@ -566,7 +582,7 @@ static void backward_node(Tr &t, TNode &tn) {
                 gemm_nt(s, dqkvb, 3 * D, wqkv->b, 3 * D, (int)T, (int)D, (int)(3 * D), dst(0), D,
                         !tn.first_writer[0]);
             k::transpose_bf16(s, dqkvb, 3 * D, nullptr, 1, (int)T, (int)(3 * D), dqkvt, T);
-            k::transpose_bf16(s, xb, D, nullptr, 1, (int)T, (int)D, xbt, T);
+            k::transpose_bf16(s, x3, 3 * D, nullptr, 1, (int)T, (int)D, xbt, T);
             gemm_nt(s, xbt, T, dqkvt, T, (int)D, (int)(3 * D), (int)T, wqkv->grad, 3 * D, false);
             break;
         }
@@ -656,6 +672,8 @@ static void train_step(Tr &t) {
             k::sgd(s, p->master, p->grad, p->cols, p->rows, (int)p->cols, t.lr, p->want_b ? p->b : nullptr);
             if (p->want_bt)
                 k::transpose_bf16(s, p->b, p->cols, nullptr, 1, (int)p->rows, (int)p->cols, p->bt, p->rows);
+            if (p->want_bt3)
+                k::transpose_split3(s, p->master, p->cols, (int)p->rows, (int)p->cols, p->bt3, 3 * p->rows);
         }
     }
 }
@@ -756,6 +774,14 @@ int catnn_hip_train_step(catnn_hip_trainer *t, float *loss) {
             CATNN_HIP(hipMemcpyAsync(loss, t->loss, 4, hipMemcpyDeviceToHost, t->dev->stream));
             CATNN_HIP(hipStreamSynchronize(t->dev->stream));
         }
+    });
+}
+
+int catnn_hip_train_reset(catnn_hip_trainer *t) {
+    return guard([&] {
+        CATNN_REQUIRE(t, CATNN_ERR_INVALID_ARGUMENT, "null trainer");
+        require_device(t->dev);
+        upload_params(*t);
     });
 }
 

@@ -84,6 +84,58 @@ __global__ __launch_bounds__(256) void transpose_kernel(const TS *__restrict__ s
     }
 }
 
+// Split-bf16 operands.  v = hi + lo + O(2⁻¹⁷|v|) with hi = bf16(v) and
+// lo = bf16(v − hi).  A row of A' = [hi | hi | lo] against a row of
+// B' = [hi | lo | hi] sums to hi·hi + hi·lo + lo·hi over 3K: an fp32 product
+// to ~2⁻¹⁶ relative on the bf16 matrix cores (the dropped lo·lo term).
+__device__ __forceinline__ void split_bf16(float v, bf16_t &hi, bf16_t &lo) {
+    hi = f2bf(v);
+    lo = f2bf(v - __uint_as_float((uint32_t)hi << 16));
+}
+
+// out[r] = [hi(x[r]) | hi(x[r]) | lo(x[r])], rows of K.
+__global__ void split3_rows_kernel(const float *__restrict__ x, int64_t ldx, int64_t rows, int K,
+                                   bf16_t *__restrict__ out, int64_t ldo) {
+    const int64_t n = rows * K;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+        const int64_t r = i / K;
+        const int c = (int)(i - r * K);
+        bf16_t hi, lo;
+        split_bf16(x[r * ldx + c], hi, lo);
+        bf16_t *o = out + r * ldo;
+        o[c] = hi;
+        o[K + c] = hi;
+        o[2 * K + c] = lo;
+    }
+}
+
+// w [K, N] row-major → out [N, 3K] with out[n] = [hi(w[:,n]) | lo(w[:,n]) | hi(w[:,n])].
+__global__ __launch_bounds__(256) void transpose_split3_kernel(const float *__restrict__ w, int64_t ldw,
+                                                               int K, int N, bf16_t *__restrict__ out,
+                                                               int64_t ldo) {
+    __shared__ bf16_t th[64][66], tl[64][66];
+    const int k0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
+    const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+    for (int i = ty; i < 64; i += 4) {
+        const int k = k0 + i, n = n0 + tx;
+        bf16_t hi = 0, lo = 0;
+        if (k < K && n < N) split_bf16(w[(int64_t)k * ldw + n], hi, lo);
+        th[i][tx] = hi;
+        tl[i][tx] = lo;
+    }
+    __syncthreads();
+    for (int i = ty; i < 64; i += 4) {
+        const int n = n0 + i, k = k0 + tx;
+        if (n < N && k < K) {
+            bf16_t *o = out + (int64_t)n * ldo;
+            o[k] = th[tx][i];
+            o[K + k] = tl[tx][i];
+            o[2 * K + k] = th[tx][i];
+        }
+    }
+}
+
 // LayerNorm forward for training: y (fp32 and/or bf16), mean and rstd per
 // row.  One wavefront per row; any width.
 __global__ __launch_bounds__(256) void ln_fwd_kernel(const float *__restrict__ x,
@@ -373,6 +425,21 @@ void transpose_f32_bf16(hipStream_t s, const float *src, int64_t lds, const int3
     CATNN_REQUIRE((rows + 63) / 64 < 65536, CATNN_ERR_SHAPE_MISMATCH, "transpose: too many rows");
     transpose_kernel<float><<<tgrid(rows, cols), 256, 0, s>>>(src, lds, rows_map, div, rows, cols,
                                                               dst, ldd);
+    CATNN_HIP(hipGetLastError());
+}
+
+void split3_rows(hipStream_t s, const float *x, int64_t ldx, int64_t rows, int K, bf16_t *out,
+                 int64_t ldo) {
+    if (rows <= 0 || K <= 0) return;
+    split3_rows_kernel<<<blocks_for(rows * K, 256 * 4), 256, 0, s>>>(x, ldx, rows, K, out, ldo);
+    CATNN_HIP(hipGetLastError());
+}
+
+void transpose_split3(hipStream_t s, const float *w, int64_t ldw, int K, int N, bf16_t *out,
+                      int64_t ldo) {
+    if (K <= 0 || N <= 0) return;
+    CATNN_REQUIRE((K + 63) / 64 < 65536, CATNN_ERR_SHAPE_MISMATCH, "transpose_split3: too many rows");
+    transpose_split3_kernel<<<tgrid(K, N), 256, 0, s>>>(w, ldw, K, N, out, ldo);
     CATNN_HIP(hipGetLastError());
 }
 

@@ -20,6 +20,15 @@ void transpose_bf16(hipStream_t s, const bf16_t *src, int64_t lds, const int32_t
 void transpose_f32_bf16(hipStream_t s, const float *src, int64_t lds, const int32_t *rows_map,
                         int div, int rows, int cols, bf16_t *dst, int64_t ldd);
 
+// Split-bf16 GEMM operands: A' rows [hi | hi | lo] from fp32 rows of K
+// (out row stride ldo ≥ 3K) and B' = [hi | lo | hi] rows from the columns of
+// an fp32 [K, N] matrix, so the bf16 GEMM over K' = 3K yields hi·hi + hi·lo
+// + lo·hi ≈ the fp32 product (relative error ~2⁻¹⁶).
+void split3_rows(hipStream_t s, const float *x, int64_t ldx, int64_t rows, int K, bf16_t *out,
+                 int64_t ldo);
+void transpose_split3(hipStream_t s, const float *w, int64_t ldw, int K, int N, bf16_t *out,
+                      int64_t ldo);
+
 void ln_forward_train(hipStream_t s, const float *x, const float *g, const float *b, float *y,
                       bf16_t *yb, float *mean, float *rstd, int64_t rows, int cols, float eps);
 uint64_t ln_backward_scratch_bytes(int64_t rows, int cols);

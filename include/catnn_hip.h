@@ -328,6 +328,10 @@ int catnn_hip_train_set_batch(catnn_hip_trainer *t, const catnn_tensor *input,
 /* forward, loss, backward, SGD on the resident batch; `loss` (or NULL:
  * no synchronisation) receives the step's MSE before the update. */
 int catnn_hip_train_step(catnn_hip_trainer *t, float *loss);
+/* Restores every parameter to the value it had at install (the host copy
+ * kept by the trainer), e.g. to time many steps from the same start.  Not
+ * part of reference_train; asynchronous on the device stream. */
+int catnn_hip_train_reset(catnn_hip_trainer *t);
 /* fp32 master weight / last gradient of param `port` of node `node_id`
  * (Attention's wq, wk, wv are read out of the packed projection). */
 int catnn_hip_train_read_param(catnn_hip_trainer *t, uint32_t node_id, const char *port,

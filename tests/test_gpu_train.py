@@ -1,15 +1,23 @@
-"""One training step on the GPU (catnn_hip_train_*) against the oracle's
-restatement of pipeline::reference_train (oracle_train.train_step, pinned
-by test_oracle_adjoint.py against float64 autograd).
+"""One training step on the GPU (catnn_hip_train_*) against two CPU
+restatements of pipeline::reference_train (MSE + SGD):
 
-The device step runs its GEMMs on bf16 operands with fp32 accumulation, so
-losses and gradients are held to the bf16 bar (rel L2 ≤ 1e-2).  The SGD
-update is checked bit-exactly against p − lr·g on the device's own
-gradient, and MoE routing bit-exactly wherever the router's input is the
-exact graph input."""
+  * oracle_bf16.train_step — the same algorithm in float64 with the
+    device's declared rounding points (split-bf16 forward GEMMs for Linear
+    and attention, plain bf16 operands for the MoE experts and the backward
+    GEMMs, all else wide); the device must match it to TIGHT: this is what
+    proves the kernels right, independent of bf16's own error;
+  * oracle_train.train_step — the fp32 reference step (pinned against
+    float64 autograd); the device's mixed-precision step must stay within
+    the bf16 bar (rel L2 ≤ 1e-2) of it.
+
+The SGD update is checked bit-exactly against p − lr·g on the device's own
+gradient, and MoE routing bit-exactly where the router reads the exact
+graph input."""
 import numpy as np
 import pytest
 
+import oracle
+import oracle_bf16 as ob
 import oracle_train as ot
 from catnn_amd import (CatError, IrGraph, IrNode, OpenOp, Tensor, TensorType, Trainer,
                        arena_conflict, configs, synth)
@@ -17,7 +25,14 @@ from conftest import rel_l2
 
 pytestmark = pytest.mark.gpu
 
-BF16_TOL = 1e-2
+TIGHT = 2e-3      # device vs the bf16-rounding model of the same step
+# Block → MoE at config 5's initialisation (output ≈ 27× the target) is
+# ill-conditioned: perturbing the input by 1e-6 (relative) moves the model's
+# own attention-weight gradients by 3.1e-3, so the device, whose fp32
+# accumulation differs from the model's float64 by about that much, is held
+# to twice that noise floor there.
+TIGHT_CONFIG5 = 6e-3
+BF16_TOL = 1e-2   # device (bf16 GEMM operands) vs the fp32 reference step
 LOSS_TOL = 2e-3
 
 
@@ -29,43 +44,51 @@ def _shape(g, nid, port):
     return tuple(g.nodes[nid].params[port].ty.shape)
 
 
-def _check_step(device, g, x, tgt, lr=0.05, grad_tol=BF16_TOL, loose=()):
-    """One step on both sides; returns (trainer, oracle loss, worst error)."""
+def _check_step(device, g, x, tgt, lr=0.05, fp32_tol=BF16_TOL, tight=TIGHT):
+    """One step on the device and on both CPU restatements."""
     print(f"[train] {g.name} x={x.ty.shape}", flush=True)
     tr = Trainer(device, g, lr)
     tr.set_batch(x, tgt)
     loss = tr.step()
     loss_o, grads_o, _ = ot.train_step(g, x.numpy(), tgt.numpy(), lr)
-    print(f"  loss gpu={loss:.6f} oracle={loss_o:.6f}")
+    loss_m, grads_m, routing_m = ob.train_step(g, x.numpy(), tgt.numpy())
+    print(f"  loss gpu={loss:.6f} bf16-model={loss_m:.6f} fp32-oracle={loss_o:.6f}")
+    assert abs(loss - loss_m) <= 1e-4 * max(1.0, abs(loss_m))
     assert abs(loss - loss_o) <= LOSS_TOL * max(1.0, abs(loss_o))
     out = g.outputs[-1]
     pred = tr.value(out, tuple(g.nodes[out].output_ty.shape))
     assert np.isfinite(pred).all()
-    worst = 0.0
+    for nid, idx_m in routing_m.items():
+        agree = float(np.mean(tr.routing(nid, *idx_m.shape) == idx_m))
+        print(f"  routing {g.nodes[nid].name}: agreement with the model {agree:.4f}")
+        assert agree >= 0.99
+    bad = []
     for nid, dp in grads_o.items():
         for port, go in dp.items():
             shape = _shape(g, nid, port)
             gg = tr.grad(nid, port, shape)
-            err = rel_l2(gg, go.reshape(shape))
-            tol = grad_tol * (5 if (nid, port) in loose else 1)
-            print(f"  grad {g.nodes[nid].name}.{port}: rel_l2={err:.2e}")
-            assert err < tol, (g.nodes[nid].name, port, err)
-            worst = max(worst, err)
+            e_m = rel_l2(gg, grads_m[nid][port].reshape(shape))
+            e_o = rel_l2(gg, go.reshape(shape))
+            print(f"  grad {g.nodes[nid].name}.{port}: vs model {e_m:.2e}  vs fp32 {e_o:.2e}")
+            if e_m >= tight or e_o >= fp32_tol:
+                bad.append((g.nodes[nid].name, port, e_m, e_o))
             # Sgd::put on the device's own gradient, rounded as the reference rounds.
             p0 = g.nodes[nid].params[port].numpy().reshape(shape)
             p1 = tr.param(nid, port, shape)
-            want = p0 - np.float32(lr) * gg
-            assert np.array_equal(p1, want), (g.nodes[nid].name, port)
+            assert np.array_equal(p1, p0 - np.float32(lr) * gg), (g.nodes[nid].name, port)
+    assert not bad, bad
     allocs, reserved = tr.arena()
     assert arena_conflict(allocs) is None
     assert reserved < sum(a.bytes for a in allocs)  # dead buffers share space
-    return tr, loss_o, worst
+    return tr
 
 
 def test_mlp_relu_unaligned_k(device):
-    # K = 784 and N = 10: the bf16 GEMM's element-load edges.
+    # K = 784 and N = 10: the bf16 GEMM's element-load edges.  fc1's weight
+    # gradient comes through three plain-bf16 backward GEMMs and two ReLU
+    # masks: the bf16-rounding model itself sits 1.1e-2 from the fp32 step.
     w = configs.config1(batch=64)
-    _check_step(device, w.graph, w.x, _target([64, 10], 11))
+    _check_step(device, w.graph, w.x, _target([64, 10], 11), fp32_tol=2e-2)
 
 
 @pytest.mark.parametrize("causal", [True, False])
@@ -89,52 +112,73 @@ def test_block_mfma_head_ragged(device):
 def test_moe_layer_routing_bit_exact(device):
     # The router reads the exact graph input, so its top-k matches bit for bit.
     w = configs.config4(batch=2, seq=64, d=128, n_experts=4, top_k=2, inter=96)
-    tr, _, _ = _check_step(device, w.graph, w.x, _target([2, 64, 128], 15))
-    import oracle
-
+    tr = _check_step(device, w.graph, w.x, _target([2, 64, 128], 15))
     idx, _, _ = oracle.route(w.x.numpy().reshape(-1, 128), w.graph.nodes[1].params["gate"].numpy(), 2)
     assert np.array_equal(tr.routing(1, 128, 2), idx)
 
 
 def test_block_plus_moe_config5_shape(device):
     w = configs.config5(batch=2, seq=128, d=128, heads=2, ffn=256, n_experts=4, top_k=2, inter=128)
-    tr, _, _ = _check_step(device, w.graph, w.x, w.target)
-    # The router here reads the block's bf16-GEMM output: top-k may differ on near ties.
-    import oracle
-
-    acts = {0: w.x.numpy()}
+    tr = _check_step(device, w.graph, w.x, w.target, tight=TIGHT_CONFIG5)
+    # Against the fp32 reference the router reads the block's bf16-GEMM
+    # output, so top-k may differ on near ties.
     g = w.graph
+    acts = {0: w.x.numpy()}
     for nid in oracle.topo(g)[1:]:
         preds = [e.src for e in g.edges if e.dst == nid]
         acts[nid] = oracle.eval_node(g.nodes[nid], [acts[p] for p in preds])
     idx, _, _ = oracle.route(acts[8].reshape(-1, 128), g.nodes[9].params["gate"].numpy(), 2)
-    agree = float(np.mean(np.sort(tr.routing(9, 256, 2), 1) == np.sort(idx, 1)))
-    print(f"  routing agreement {agree:.4f}")
+    agree = float(np.mean(tr.routing(9, 256, 2) == idx))
+    print(f"  routing agreement with the fp32 reference {agree:.4f}")
     assert agree > 0.97
 
 
 def test_block_plus_moe_ragged(device):
     w = configs.config5(batch=1, seq=77, d=128, heads=2, ffn=256, n_experts=4, top_k=2, inter=96)
-    _check_step(device, w.graph, w.x, w.target)
+    _check_step(device, w.graph, w.x, w.target, tight=TIGHT_CONFIG5)
 
 
-def test_three_steps_follow_the_oracle(device):
-    w = configs.config5(batch=1, seq=64, d=128, heads=2, ffn=256, n_experts=4, top_k=2, inter=128)
+@pytest.mark.parametrize("which", ["block", "moe"])
+def test_three_steps_follow_the_oracle(device, which):
+    # Parameters persist on the device between steps; the fp32 reference is
+    # re-run from its own updated parameters.  (Config 5 itself is not used:
+    # at its initialisation lr 0.05 overshoots, 7.5e2 → 1.5e10 → NaN, in the
+    # reference as on the device.)
+    if which == "block":
+        w = configs.config3(batch=1, seq=64, d=128, heads=2, ffn=256)
+    else:
+        w = configs.config4(batch=1, seq=64, d=128, n_experts=4, top_k=2, inter=128)
     g = w.graph
-    tr = Trainer(device, g, w.lr)
-    tr.set_batch(w.x, w.target)
+    tgt = _target(w.x.ty.shape, 16)
+    tr = Trainer(device, g, 0.05)
+    tr.set_batch(w.x, tgt)
     losses, losses_o = [], []
     for _ in range(3):
         losses.append(tr.step())
-        loss_o, _, new = ot.train_step(g, w.x.numpy(), w.target.numpy(), w.lr)
+        loss_o, _, new = ot.train_step(g, w.x.numpy(), tgt.numpy(), 0.05)
         losses_o.append(loss_o)
         for nid, ports in new.items():
             for port, v in ports.items():
                 g.nodes[nid].params[port] = Tensor(g.nodes[nid].params[port].ty, v.reshape(-1))
     print(f"  losses gpu={losses} oracle={losses_o}")
-    assert losses[2] < losses[0]
+    assert losses[2] < losses[1] < losses[0]
     for a, b in zip(losses, losses_o):
         assert abs(a - b) <= LOSS_TOL * max(1.0, abs(b))
+
+
+def test_reset_restores_parameters_and_steps_repeat_bit_exactly(device):
+    w = configs.config5(batch=1, seq=64, d=128, heads=2, ffn=256, n_experts=4, top_k=2, inter=128)
+    tr = Trainer(device, w.graph, w.lr)
+    tr.set_batch(w.x, w.target)
+    first = tr.step()
+    g1 = tr.grad(2, "wq", (128, 128))
+    tr.step()
+    tr.reset()
+    assert np.array_equal(tr.param(7, "w", (256, 128)), w.graph.nodes[7].params["w"].numpy())
+    assert np.array_equal(tr.param(9, "e2.w3", (128, 128)), w.graph.nodes[9].params["e2.w3"].numpy())
+    # No floating-point atomics anywhere: the same step is the same bits.
+    assert tr.step() == first
+    assert np.array_equal(tr.grad(2, "wq", (128, 128)), g1)
 
 
 def test_training_error_kinds(device):

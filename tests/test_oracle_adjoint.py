@@ -181,3 +181,45 @@ def test_train_step_matches_autograd_on_block_plus_moe():
         for port, gr in dp.items():
             assert rel_l2(gr, P[nid][port].grad) < 1e-3, (n[nid].name, port)
             assert np.allclose(new[nid][port], n[nid].params[port].numpy() - np.float32(0.05) * gr)
+
+
+# ---------------------------------------------------------------------------
+# The device-precision model (oracle_bf16): with rounding off it must be the
+# reference algorithm; its rounding must be torch's bfloat16 rounding.
+
+def test_bf16_round_known_answers_and_torch():
+    import oracle_bf16 as ob
+
+    one = 1.0
+    vals = np.array([one, one + 2.0 ** -8, one + 3 * 2.0 ** -8, -2.5, 0.0, 3.0e38, 1e-40], np.float32)
+    got = ob.bf16_round(vals)
+    assert got[:3].tolist() == [1.0, 1.0, 1.0 + 2.0 ** -6]  # ties to even
+    a = RNG.standard_normal(4096).astype(np.float32) * np.float32(10.0) ** RNG.integers(-20, 20, 4096)
+    want = torch.tensor(np.concatenate([vals, a])).to(torch.bfloat16).to(torch.float32).numpy()
+    assert np.array_equal(ob.bf16_round(np.concatenate([vals, a])).astype(np.float32), want)
+    # hi + lo carries 16 significant bits: |a − hi − lo| ≤ 2⁻¹⁶|a| (normal range)
+    b = RNG.standard_normal(4096).astype(np.float32)
+    hi, lo = ob.bf16_split(b)
+    assert np.all(np.abs(b - hi - lo) <= 2.0 ** -16 * np.abs(b))
+
+
+@pytest.mark.parametrize("which", ["mlp", "block_moe"])
+def test_bf16_model_without_rounding_is_the_reference_step(which):
+    import oracle_bf16 as ob
+    from catnn_amd import configs
+
+    if which == "mlp":
+        w = configs.config1(batch=16)
+        g, x = w.graph, w.x.numpy()
+        tgt = RNG.standard_normal((16, 10)).astype(np.float32)
+    else:
+        w = configs.config5(batch=1, seq=24, d=32, heads=2, ffn=48, n_experts=4, top_k=2, inter=40)
+        g, x, tgt = w.graph, w.x.numpy(), w.target.numpy()
+    loss_o, grads_o, _ = ot.train_step(g, x, tgt, 0.05)
+    loss_m, grads_m, _ = ob.train_step(g, x, tgt, policy=ob.WIDE)
+    assert abs(loss_m - loss_o) < 1e-5 * max(1.0, loss_o)
+    assert grads_m.keys() == grads_o.keys()
+    for nid, dp in grads_o.items():
+        assert dp.keys() == grads_m[nid].keys()
+        for port, go in dp.items():
+            assert rel_l2(grads_m[nid][port].reshape(go.shape), go) < 1e-4, (g.nodes[nid].name, port)
