@@ -291,6 +291,13 @@ def linear(dev: Device, x, w, b, r, y, m: int, k: int, n: int, act: int = 0):
                                    m, k, n, act))
 
 
+def gemm_bf16_nt(dev: Device, a, lda: int, b, ldb: int, c, ldc: int, m: int, n: int, k: int,
+                 accumulate: bool = False, tile_cfg: int = -1):
+    """c (+)= a·bᵀ with a [m, k], b [n, k] bf16 bit patterns (uint16)."""
+    check(lib.catnn_hip_gemm_bf16_nt(dev.handle, _ptr(a), lda, _ptr(b), ldb, _ptr(c), ldc, m, n, k,
+                                     int(accumulate), tile_cfg))
+
+
 def act(dev: Device, x, y, n: int, kind: int):
     check(lib.catnn_hip_act_f32(dev.handle, _ptr(x), _ptr(y), n, kind))
 

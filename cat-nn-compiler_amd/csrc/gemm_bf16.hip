@@ -8,10 +8,12 @@
 // eight consecutive k values, one 16-byte LDS read per operand — and
 // accumulator r of lane l is C[8(r/4) + 4(l/32) + r%4][l%32].
 //
-// Block: 256 threads, 2×2 wavefronts of 64×64 (2×2 MFMA blocks), BK = 32
-// (two k16 steps), A and B tiles staged in LDS (row stride BK+8 bf16, so
-// eight lanes' 16-byte reads hit distinct banks), double-buffered behind
-// register prefetch.  Epilogues and grids are listed in gemm_bf16.hpp.
+// Blocks of 2×2 or 4×2 wavefronts; tiles of 128×128, 256×128 or 128×256
+// with BK = 32 or 64 (Cfg below), A and B tiles staged in LDS (row stride
+// BK+8 bf16, so eight lanes' 16-byte reads hit distinct banks),
+// double-buffered behind register prefetch; full k chunks load without
+// branches so the next chunk's loads stay in flight behind the MFMAs.
+// Epilogues and grids are listed in gemm_bf16.hpp.
 #include <hip/hip_runtime.h>
 
 #include "common.hpp"
@@ -26,12 +28,30 @@ namespace {
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
-constexpr int BM = 128, BN = 128, BK = 32, LDT = BK + 8;
-
-struct Smem {
-    bf16_t a[2][BM][LDT];
-    bf16_t b[2][BN][LDT];
+// A block of WAVES_M × WAVES_N wavefronts computes a BM × BN tile; each
+// wavefront owns (BM / WAVES_M) × (BN / WAVES_N) = FM × FN MFMA blocks of
+// 32 × 32.  Per k16 step a wavefront reads (FM + FN) KB of LDS for FM·FN
+// MFMAs, so wider wavefront tiles relieve the LDS port.
+template <int BM_, int BN_, int WAVES_M_, int WAVES_N_, int BK_>
+struct Cfg {
+    static constexpr int BM = BM_, BN = BN_, WAVES_M = WAVES_M_, WAVES_N = WAVES_N_;
+    static constexpr int BK = BK_, LDT = BK + 8;  // LDS row stride (bf16): conflict-free b128 reads
+    static constexpr int LDS_BYTES = 2 * (BM + BN) * LDT * 2;
+    static constexpr int NT = 64 * WAVES_M * WAVES_N;
+    static constexpr int FM = BM / (32 * WAVES_M), FN = BN / (32 * WAVES_N);
+    static constexpr int A_IT = BM * (BK / 8) / NT;  // 16-byte chunks per thread per k chunk
+    static constexpr int B_IT = BN * (BK / 8) / NT;
+    static_assert(FM >= 1 && FN >= 1 && FM * 32 * WAVES_M == BM && FN * 32 * WAVES_N == BN, "tile");
+    static_assert(A_IT >= 1 && B_IT >= 1 && A_IT * NT == BM * (BK / 8) && B_IT * NT == BN * (BK / 8),
+                  "load split");
 };
+
+using Cfg0 = Cfg<128, 128, 2, 2, 32>;  // 64 × 64 per wavefront
+using Cfg1 = Cfg<128, 256, 2, 2, 32>;  // 64 × 128 per wavefront
+using Cfg2 = Cfg<128, 128, 2, 2, 64>;
+using Cfg3 = Cfg<256, 128, 4, 2, 32>;  // 8 wavefronts of 64 × 64
+using Cfg4 = Cfg<256, 128, 4, 2, 64>;
+using Cfg5 = Cfg<128, 256, 2, 2, 64>;
 
 __device__ __forceinline__ float bf2f(bf16_t v) { return __uint_as_float((uint32_t)v << 16); }
 
@@ -55,39 +75,91 @@ __device__ __forceinline__ float silu_grad(float x) {
     return s + x * s * (1.0f - s);
 }
 
-template <bool VEC, bool DUAL>
-__device__ __forceinline__ void tile(Smem &sm, const GemmBf16Params &p, const bf16_t *__restrict__ B,
-                                     const bf16_t *__restrict__ B2, int row0, int row_end, int col0,
-                                     int k_lo, int k_hi, float *__restrict__ C32) {
-    constexpr int FM = 2, FN = 2;
+// Epilogue of one wavefront's FM × FN accumulator blocks, one loop nest per
+// kind (fully unrolled, so the accumulators stay in registers).  Entry r of
+// block (mi, ni) is row wrow0 + 32·mi + 8(r/4) + r%4, column wcol0 + 32·ni.
+template <class C, bool DUAL, int EPI>
+__device__ __forceinline__ void epilogue(const GemmBf16Params &p, const f32x16 (&acc)[C::FM][C::FN],
+                                         int wrow0, int wcol0, int row_end, float *__restrict__ C32) {
+    constexpr int NF = DUAL ? C::FN / 2 : C::FN;
+#pragma unroll
+    for (int mi = 0; mi < C::FM; ++mi)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int row = wrow0 + mi * 32 + 8 * (r >> 2) + (r & 3);
+            if (row >= row_end) continue;
+#pragma unroll
+            for (int ni = 0; ni < NF; ++ni) {
+                const int col = wcol0 + ni * 32;
+                if (col >= p.N) continue;
+                float v = acc[mi][ni][r];
+                if (EPI == EPI_SWIGLU_FWD) {
+                    const float c = acc[mi][ni + NF][r];
+                    const int64_t so = (int64_t)row * p.lds + col;
+                    if (p.S1) p.S1[so] = f2bf(v);
+                    if (p.S2) p.S2[so] = f2bf(c);
+                    p.Cb[(int64_t)row * p.ldcb + col] = f2bf(silu(v) * c);
+                    continue;
+                }
+                if (EPI == EPI_SWIGLU_BWD) {
+                    const int64_t so = (int64_t)row * p.lds + col;
+                    const float a = bf2f(p.S1[so]), c = bf2f(p.S2[so]);
+                    p.Cb[(int64_t)row * p.ldcb + col] = f2bf(v * c * silu_grad(a));
+                    p.Cb2[(int64_t)row * p.ldcb + col] = f2bf(v * silu(a));
+                    continue;
+                }
+                if (EPI == EPI_LINEAR) {
+                    if (p.bias) v += p.bias[col];
+                    if (p.Z) p.Z[(int64_t)row * p.ldz + col] = v;
+                    v = apply_act(v, p.act);
+                    if (p.R) v = p.R[(int64_t)row * p.ldr + col] + v;
+                } else if (EPI == EPI_GELU_BWD) {
+                    v *= gelu_grad(p.Z[(int64_t)row * p.ldz + col]);
+                }
+                if (C32) {
+                    float *dst = C32 + (int64_t)row * p.ldc32 + col;
+                    *dst = p.accumulate ? *dst + v : v;
+                }
+                if (p.Cb) p.Cb[(int64_t)row * p.ldcb + col] = f2bf(v);
+            }
+        }
+}
+
+template <class C, bool VEC, bool DUAL>
+__device__ __forceinline__ void tile(bf16_t (*sa)[C::BM][C::LDT], bf16_t (*sb)[C::BN][C::LDT], const GemmBf16Params &p,
+                                     const bf16_t *__restrict__ B, const bf16_t *__restrict__ B2, int row0,
+                                     int row_end, int col0, int k_lo, int k_hi, float *__restrict__ C32) {
+    constexpr int BM = C::BM, BN = C::BN, FM = C::FM, FN = C::FN, BK = C::BK;
+    // DUAL: B rows [0, BN/2) come from B, [BN/2, BN) from B2; a wavefront's
+    // fragment ni < FN/2 pairs with fragment ni + FN/2 (same output column).
+    constexpr int WCOLS = DUAL ? BN / 2 / C::WAVES_N : BN / C::WAVES_N;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave / C::WAVES_N, wn = wave % C::WAVES_N;
     const int lr = lane & 31, lg = lane >> 5;
     const int N = p.N;
 
-    // Load assignments: 2 × 16 B of A and of B per thread per chunk.
-    const bf16_t *a_src[2];
-    bool a_ok[2];
-    int a_r[2], a_c[2];
+    const bf16_t *a_src[C::A_IT];
+    bool a_ok[C::A_IT];
+    int a_r[C::A_IT], a_c[C::A_IT];
 #pragma unroll
-    for (int it = 0; it < 2; ++it) {
-        const int idx = tid + it * 256;
-        a_r[it] = idx >> 2;
-        a_c[it] = (idx & 3) * 8;
+    for (int it = 0; it < C::A_IT; ++it) {
+        const int idx = tid + it * C::NT;
+        a_r[it] = idx / (BK / 8);
+        a_c[it] = (idx % (BK / 8)) * 8;
         const int gr = row0 + a_r[it];
         a_ok[it] = gr < row_end;
         int src = gr;
         if (a_ok[it] && p.a_rows) src = p.a_rows[gr] / p.a_row_div;
         a_src[it] = p.A + (int64_t)(a_ok[it] ? src : 0) * p.lda;
     }
-    const bf16_t *b_src[2];
-    bool b_ok[2];
-    int b_r[2], b_c[2];
+    const bf16_t *b_src[C::B_IT];
+    bool b_ok[C::B_IT];
+    int b_r[C::B_IT], b_c[C::B_IT];
 #pragma unroll
-    for (int it = 0; it < 2; ++it) {
-        const int idx = tid + it * 256;
-        b_r[it] = idx >> 2;
-        b_c[it] = (idx & 3) * 8;
+    for (int it = 0; it < C::B_IT; ++it) {
+        const int idx = tid + it * C::NT;
+        b_r[it] = idx / (BK / 8);
+        b_c[it] = (idx % (BK / 8)) * 8;
         int n;
         const bf16_t *base;
         if (DUAL) {
@@ -102,8 +174,26 @@ __device__ __forceinline__ void tile(Smem &sm, const GemmBf16Params &p, const bf
         b_src[it] = base + (int64_t)(b_ok[it] ? n : 0) * p.ldb;
     }
 
-    // 8 consecutive k values of one row: one 16-byte load when all 8 are in
-    // range and aligned, element loads (zero past k_hi) otherwise.
+    uint4 ra[C::A_IT], rb[C::B_IT];
+    // Full chunks (VEC launches, all BK values inside [k_lo, k_hi)): one
+    // unconditional 16-byte load per row piece — rows past the edge read row
+    // 0 of the operand and are zeroed by a select — so nothing branches and
+    // the loads stay in flight behind the MFMAs of the current chunk.
+    auto gload_full = [&](int k0) {
+#pragma unroll
+        for (int it = 0; it < C::A_IT; ++it) {
+            const uint4 v = *reinterpret_cast<const uint4 *>(a_src[it] + k0 + a_c[it]);
+            ra[it] = a_ok[it] ? v : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int it = 0; it < C::B_IT; ++it) {
+            const uint4 v = *reinterpret_cast<const uint4 *>(b_src[it] + k0 + b_c[it]);
+            rb[it] = b_ok[it] ? v : make_uint4(0, 0, 0, 0);
+        }
+    };
+    // The tail chunk and unaligned launches: 8 consecutive k values of one
+    // row, one 16-byte load when all 8 are in range and aligned, element
+    // loads (zero past k_hi) otherwise.
     auto load8 = [&](const bf16_t *src, bool ok, int kk) -> uint4 {
         if (!ok || kk >= k_hi) return make_uint4(0, 0, 0, 0);
         if (VEC && kk + 8 <= k_hi) return *reinterpret_cast<const uint4 *>(src + kk);
@@ -113,19 +203,17 @@ __device__ __forceinline__ void tile(Smem &sm, const GemmBf16Params &p, const bf
         return make_uint4(v[0] | (uint32_t)v[1] << 16, v[2] | (uint32_t)v[3] << 16,
                           v[4] | (uint32_t)v[5] << 16, v[6] | (uint32_t)v[7] << 16);
     };
-    uint4 ra[2], rb[2];
     auto gload = [&](int k0) {
 #pragma unroll
-        for (int it = 0; it < 2; ++it) ra[it] = load8(a_src[it], a_ok[it], k0 + a_c[it]);
+        for (int it = 0; it < C::A_IT; ++it) ra[it] = load8(a_src[it], a_ok[it], k0 + a_c[it]);
 #pragma unroll
-        for (int it = 0; it < 2; ++it) rb[it] = load8(b_src[it], b_ok[it], k0 + b_c[it]);
+        for (int it = 0; it < C::B_IT; ++it) rb[it] = load8(b_src[it], b_ok[it], k0 + b_c[it]);
     };
     auto sstore = [&](int buf) {
 #pragma unroll
-        for (int it = 0; it < 2; ++it) {
-            *reinterpret_cast<uint4 *>(&sm.a[buf][a_r[it]][a_c[it]]) = ra[it];
-            *reinterpret_cast<uint4 *>(&sm.b[buf][b_r[it]][b_c[it]]) = rb[it];
-        }
+        for (int it = 0; it < C::A_IT; ++it) *reinterpret_cast<uint4 *>(&sa[buf][a_r[it]][a_c[it]]) = ra[it];
+#pragma unroll
+        for (int it = 0; it < C::B_IT; ++it) *reinterpret_cast<uint4 *>(&sb[buf][b_r[it]][b_c[it]]) = rb[it];
     };
 
     f32x16 acc[FM][FN];
@@ -136,18 +224,20 @@ __device__ __forceinline__ void tile(Smem &sm, const GemmBf16Params &p, const bf
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[mi][ni][r] = 0.f;
 
+    auto brow = [&](int ni) {
+        if (DUAL) return (ni < FN / 2 ? 0 : BN / 2) + wn * WCOLS + (ni % (FN / 2)) * 32 + lr;
+        return wn * WCOLS + ni * 32 + lr;
+    };
     auto compute = [&](int buf) {
 #pragma unroll
         for (int s = 0; s < BK / 16; ++s) {
             bf16x8 af[FM], bfr[FN];
 #pragma unroll
             for (int mi = 0; mi < FM; ++mi)
-                af[mi] = *reinterpret_cast<const bf16x8 *>(&sm.a[buf][wm * 64 + mi * 32 + lr][s * 16 + 8 * lg]);
+                af[mi] = *reinterpret_cast<const bf16x8 *>(&sa[buf][wm * (BM / C::WAVES_M) + mi * 32 + lr][s * 16 + 8 * lg]);
 #pragma unroll
-            for (int ni = 0; ni < FN; ++ni) {
-                const int row = DUAL ? (ni * (BN / 2) + wn * 32 + lr) : (wn * 64 + ni * 32 + lr);
-                bfr[ni] = *reinterpret_cast<const bf16x8 *>(&sm.b[buf][row][s * 16 + 8 * lg]);
-            }
+            for (int ni = 0; ni < FN; ++ni)
+                bfr[ni] = *reinterpret_cast<const bf16x8 *>(&sb[buf][brow(ni)][s * 16 + 8 * lg]);
 #pragma unroll
             for (int mi = 0; mi < FM; ++mi)
 #pragma unroll
@@ -157,102 +247,120 @@ __device__ __forceinline__ void tile(Smem &sm, const GemmBf16Params &p, const bf
     };
 
     const int nk = (k_hi - k_lo + BK - 1) / BK;
+    const int nfull = VEC ? (k_hi - k_lo) / BK : 0;
     if (nk > 0) {
-        gload(k_lo);
+        if (nfull > 0) gload_full(k_lo);
+        else gload(k_lo);
         sstore(0);
         __syncthreads();
-        for (int kt = 0; kt < nk; ++kt) {
-            const int buf = kt & 1;
+        int kt = 0;
+        for (; kt + 1 < nfull; ++kt) {  // the next chunk is full
+            gload_full(k_lo + (kt + 1) * BK);
+            compute(kt & 1);
+            sstore((kt & 1) ^ 1);
+            __syncthreads();
+        }
+        for (; kt < nk; ++kt) {  // the last full chunk and the tail
             const bool more = kt + 1 < nk;
             if (more) gload(k_lo + (kt + 1) * BK);
-            compute(buf);
-            if (more) sstore(buf ^ 1);
+            compute(kt & 1);
+            if (more) sstore((kt & 1) ^ 1);
             __syncthreads();
         }
     }
 
-#pragma unroll
-    for (int mi = 0; mi < FM; ++mi) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int row = row0 + wm * 64 + mi * 32 + 8 * (r >> 2) + 4 * lg + (r & 3);
-            if (row >= row_end) continue;
-            if (DUAL) {
-                const int col = col0 + wn * 32 + lr;
-                if (col >= N) continue;
-                const float a = acc[mi][0][r], c = acc[mi][1][r];
-                const int64_t so = (int64_t)row * p.lds + col;
-                if (p.S1) p.S1[so] = f2bf(a);
-                if (p.S2) p.S2[so] = f2bf(c);
-                p.Cb[(int64_t)row * p.ldcb + col] = f2bf(silu(a) * c);
-                continue;
-            }
-#pragma unroll
-            for (int ni = 0; ni < FN; ++ni) {
-                const int col = col0 + wn * 64 + ni * 32 + lr;
-                if (col >= N) continue;
-                float v = acc[mi][ni][r];
-                if (p.epi == EPI_LINEAR) {
-                    if (p.bias) v += p.bias[col];
-                    if (p.Z) p.Z[(int64_t)row * p.ldz + col] = v;
-                    v = apply_act(v, p.act);
-                    if (p.R) v = p.R[(int64_t)row * p.ldr + col] + v;
-                } else if (p.epi == EPI_GELU_BWD) {
-                    v *= gelu_grad(p.Z[(int64_t)row * p.ldz + col]);
-                } else if (p.epi == EPI_SWIGLU_BWD) {
-                    const int64_t so = (int64_t)row * p.lds + col;
-                    const float a = bf2f(p.S1[so]), c = bf2f(p.S2[so]);
-                    p.Cb[(int64_t)row * p.ldcb + col] = f2bf(v * c * silu_grad(a));
-                    p.Cb2[(int64_t)row * p.ldcb + col] = f2bf(v * silu(a));
-                    continue;
-                }
-                if (C32) {
-                    float *dst = C32 + (int64_t)row * p.ldc32 + col;
-                    *dst = p.accumulate ? *dst + v : v;
-                }
-                if (p.Cb) p.Cb[(int64_t)row * p.ldcb + col] = f2bf(v);
-            }
-        }
+    const int wrow0 = row0 + wm * (BM / C::WAVES_M) + 4 * lg;
+    const int wcol0 = col0 + wn * WCOLS + lr;
+    if (DUAL) {
+        epilogue<C, true, EPI_SWIGLU_FWD>(p, acc, wrow0, wcol0, row_end, C32);
+        return;
+    }
+    switch (p.epi) {
+        case EPI_LINEAR: epilogue<C, false, EPI_LINEAR>(p, acc, wrow0, wcol0, row_end, C32); break;
+        case EPI_GELU_BWD: epilogue<C, false, EPI_GELU_BWD>(p, acc, wrow0, wcol0, row_end, C32); break;
+        case EPI_SWIGLU_BWD: epilogue<C, false, EPI_SWIGLU_BWD>(p, acc, wrow0, wcol0, row_end, C32); break;
+        default: epilogue<C, false, EPI_STORE>(p, acc, wrow0, wcol0, row_end, C32);
     }
 }
 
-template <bool VEC, bool DUAL>
-__global__ __launch_bounds__(256, 2) void gemm_bf16_kernel(GemmBf16Params p) {
-    __shared__ Smem sm;
-    const int bn_out = DUAL ? BN / 2 : BN;
+template <class C, bool VEC, bool DUAL>
+__global__ __launch_bounds__(C::NT) void gemm_bf16_kernel(GemmBf16Params p) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    auto sa = reinterpret_cast<bf16_t(*)[C::BM][C::LDT]>(smem);
+    auto sb = reinterpret_cast<bf16_t(*)[C::BN][C::LDT]>(smem + 2 * C::BM * C::LDT * 2);
+    const int bn_out = DUAL ? C::BN / 2 : C::BN;
     const int tiles_n = (p.N + bn_out - 1) / bn_out;
     const int lid = xcd_remap(blockIdx.x, gridDim.x);
     if (p.grid == GRID_PLAIN) {
-        const int tiles_m = (p.M + BM - 1) / BM;
+        const int tiles_m = (p.M + C::BM - 1) / C::BM;
         int tm, tn;
         grouped_tile(lid, tiles_m, tiles_n, 8, tm, tn);
-        tile<VEC, DUAL>(sm, p, p.B, p.B2, tm * BM, p.M, tn * bn_out, 0, p.K, p.C32);
+        tile<C, VEC, DUAL>(sa, sb, p, p.B, p.B2, tm * C::BM, p.M, tn * bn_out, 0, p.K, p.C32);
     } else if (p.grid == GRID_ROWS) {
+        // Tiles of the table are kRowTile rows; C::BM equals it for this grid.
         int tm, tn;
         grouped_tile(lid, p.max_tiles, tiles_n, 8, tm, tn);
         if (tm >= *p.n_tiles) return;
         const int e = p.tile_expert[tm];
         const int end = p.seg_counts ? p.seg_offsets[e] + p.seg_counts[e] : p.seg_offsets[e + 1];
-        tile<VEC, DUAL>(sm, p, p.B_e[e], DUAL ? p.B2_e[e] : nullptr, p.tile_row0[tm], end,
-                        tn * bn_out, 0, p.K, p.C32);
+        tile<C, VEC, DUAL>(sa, sb, p, p.B_e[e], DUAL ? p.B2_e[e] : nullptr, p.tile_row0[tm], end,
+                           tn * bn_out, 0, p.K, p.C32);
     } else {  // GRID_SEGK: expert e = blockIdx.y reduces over its own K segment
-        const int tiles_m = (p.M + BM - 1) / BM;
+        const int tiles_m = (p.M + C::BM - 1) / C::BM;
         int tm, tn;
         grouped_tile(lid, tiles_m, tiles_n, 8, tm, tn);
         const int e = blockIdx.y;
         const int lo = p.seg_offsets[e];
         const int hi = p.seg_counts ? lo + p.seg_counts[e] : p.seg_offsets[e + 1];
-        tile<VEC, DUAL>(sm, p, p.B, nullptr, tm * BM, p.M, tn * bn_out, lo, hi, p.C_e[e]);
+        tile<C, VEC, DUAL>(sa, sb, p, p.B, nullptr, tm * C::BM, p.M, tn * bn_out, lo, hi, p.C_e[e]);
     }
 }
 
 bool al16(const void *q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; }
 
+
+constexpr int kRowTile = 128;  // rows per tile of the grouped tile table (build_tiles)
+
+template <class C>
+void launch_cfg(hipStream_t s, const GemmBf16Params &p, bool vec, bool dual, unsigned gy) {
+    const int bn_out = dual ? C::BN / 2 : C::BN;
+    int64_t blocks;
+    if (p.grid == GRID_ROWS) {
+        // The tile table holds kRowTile-row tiles.
+        CATNN_REQUIRE(C::BM == kRowTile, CATNN_ERR_INVALID_ARGUMENT, "bf16 gemm: grouped rows need 128-row tiles");
+        blocks = (int64_t)p.max_tiles * ((p.N + bn_out - 1) / bn_out);
+    } else blocks = (int64_t)((p.M + C::BM - 1) / C::BM) * ((p.N + bn_out - 1) / bn_out);
+    if (blocks == 0) return;
+    CATNN_REQUIRE(blocks < (1ll << 31), CATNN_ERR_SHAPE_MISMATCH, "bf16 gemm: grid too large");
+    dim3 grid((unsigned)blocks, gy), block(C::NT);
+    // Tiles above 64 KiB of LDS need the per-kernel opt-in (gfx950: 160 KiB per CU).
+    static bool attr_set = false;
+    if (!attr_set) {
+        CATNN_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_bf16_kernel<C, true, true>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS_BYTES));
+        CATNN_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_bf16_kernel<C, false, true>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS_BYTES));
+        CATNN_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_bf16_kernel<C, true, false>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS_BYTES));
+        CATNN_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_bf16_kernel<C, false, false>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS_BYTES));
+        attr_set = true;
+    }
+    if (dual) {
+        if (vec) gemm_bf16_kernel<C, true, true><<<grid, block, C::LDS_BYTES, s>>>(p);
+        else gemm_bf16_kernel<C, false, true><<<grid, block, C::LDS_BYTES, s>>>(p);
+    } else {
+        if (vec) gemm_bf16_kernel<C, true, false><<<grid, block, C::LDS_BYTES, s>>>(p);
+        else gemm_bf16_kernel<C, false, false><<<grid, block, C::LDS_BYTES, s>>>(p);
+    }
+    CATNN_HIP(hipGetLastError());
+}
+
 }  // namespace
 
-int gemm_bf16_tile_rows() { return BM; }
+int gemm_bf16_tile_rows() { return kRowTile; }
 
-void gemm_bf16_launch(hipStream_t s, const GemmBf16Params &p) {
+void gemm_bf16_launch_cfg(hipStream_t s, const GemmBf16Params &p, int cfg) {
     CATNN_REQUIRE(p.M >= 0 && p.N >= 0 && p.K >= 0, CATNN_ERR_SHAPE_MISMATCH, "bf16 gemm: dims");
     const bool dual = p.epi == EPI_SWIGLU_FWD;
     CATNN_REQUIRE(!dual || p.Cb, CATNN_ERR_INVALID_ARGUMENT, "swiglu epilogue needs Cb");
@@ -261,38 +369,46 @@ void gemm_bf16_launch(hipStream_t s, const GemmBf16Params &p) {
     CATNN_REQUIRE(p.epi != EPI_GELU_BWD || p.Z, CATNN_ERR_INVALID_ARGUMENT, "gelu backward needs Z");
     if (p.N == 0) return;
     bool vec = p.K % 8 == 0 && p.lda % 8 == 0 && p.ldb % 8 == 0 && al16(p.A);
-    const int bn_out = dual ? BN / 2 : BN;
-    int64_t blocks;
     unsigned gy = 1;
     if (p.grid == GRID_PLAIN) {
         if (p.M == 0) return;
         vec = vec && al16(p.B) && (!p.B2 || al16(p.B2));
-        blocks = (int64_t)((p.M + BM - 1) / BM) * ((p.N + bn_out - 1) / bn_out);
     } else {
         CATNN_REQUIRE(p.n_experts > 0 && p.n_experts <= kMaxExperts, CATNN_ERR_SHAPE_MISMATCH,
                       "bf16 gemm: n_experts out of range");
         if (p.grid == GRID_ROWS) {
             for (int e = 0; e < p.n_experts; ++e)
                 vec = vec && al16(p.B_e[e]) && (!dual || al16(p.B2_e[e]));
-            blocks = (int64_t)p.max_tiles * ((p.N + bn_out - 1) / bn_out);
         } else {
             // K segments start on multiples of 8 only when the caller pads them.
             vec = vec && al16(p.B) && p.segk_aligned;
-            blocks = (int64_t)((p.M + BM - 1) / BM) * ((p.N + bn_out - 1) / bn_out);
             gy = (unsigned)p.n_experts;
         }
     }
-    if (blocks == 0) return;
-    CATNN_REQUIRE(blocks < (1ll << 31), CATNN_ERR_SHAPE_MISMATCH, "bf16 gemm: grid too large");
-    dim3 grid((unsigned)blocks, gy), block(256);
-    if (dual) {
-        if (vec) gemm_bf16_kernel<true, true><<<grid, block, 0, s>>>(p);
-        else gemm_bf16_kernel<false, true><<<grid, block, 0, s>>>(p);
-    } else {
-        if (vec) gemm_bf16_kernel<true, false><<<grid, block, 0, s>>>(p);
-        else gemm_bf16_kernel<false, false><<<grid, block, 0, s>>>(p);
+    switch (cfg) {
+        case 0: launch_cfg<Cfg0>(s, p, vec, dual, gy); break;
+        case 1: launch_cfg<Cfg1>(s, p, vec, dual, gy); break;
+        case 2: launch_cfg<Cfg2>(s, p, vec, dual, gy); break;
+        case 3: launch_cfg<Cfg3>(s, p, vec, dual, gy); break;
+        case 4: launch_cfg<Cfg4>(s, p, vec, dual, gy); break;
+        case 5: launch_cfg<Cfg5>(s, p, vec, dual, gy); break;
+        default: fail(CATNN_ERR_INVALID_ARGUMENT, "bf16 gemm: unknown tile configuration");
     }
-    CATNN_HIP(hipGetLastError());
+}
+
+// Tile choice, from a sweep of the training step's shapes on MI355X
+// (TFLOP/s of cfg 3 / 4 / 2): 256×128 tiles with BK 32 when there are at
+// least four of them per CU (8192×4096×3072: 831/785/800), BK 64 when there
+// are one to four (8192×1024×12288: 665/917/883), 128×128 with BK 64 below
+// that (4096×1024×8192: 385/510/613).  Grouped-row grids need 128-row tiles.
+void gemm_bf16_launch(hipStream_t s, const GemmBf16Params &p) {
+    int cfg = 2;
+    if (p.grid != GRID_ROWS && p.epi != EPI_SWIGLU_FWD) {
+        const int64_t t3 = (int64_t)((p.M + 255) / 256) * ((p.N + 127) / 128) *
+                           (p.grid == GRID_SEGK ? p.n_experts : 1);
+        cfg = t3 >= 1024 ? 3 : t3 >= 256 ? 4 : 2;
+    }
+    gemm_bf16_launch_cfg(s, p, cfg);
 }
 
 }  // namespace k

@@ -713,6 +713,25 @@ using namespace catnn;
 
 extern "C" {
 
+int catnn_hip_gemm_bf16_nt(catnn_hip_device *dev, const uint16_t *a, int64_t lda, const uint16_t *b,
+                           int64_t ldb, float *c, int64_t ldc, int64_t m, int64_t n, int64_t k,
+                           int32_t accumulate, int32_t tile_cfg) {
+    return guard([&] {
+        require_device(dev);
+        CATNN_REQUIRE(m >= 0 && n >= 0 && k >= 0 && m < (1ll << 31) && n < (1ll << 31) && k < (1ll << 31),
+                      CATNN_ERR_SHAPE_MISMATCH, "gemm_bf16: dims");
+        CATNN_REQUIRE(lda >= k && ldb >= k && ldc >= n, CATNN_ERR_SHAPE_MISMATCH, "gemm_bf16: leading dims");
+        CATNN_REQUIRE((a && b && c) || m * n == 0, CATNN_ERR_INVALID_ARGUMENT, "gemm_bf16: null operand");
+        CATNN_REQUIRE(tile_cfg >= -1 && tile_cfg <= 5, CATNN_ERR_INVALID_ARGUMENT, "gemm_bf16: tile_cfg");
+        k::GemmBf16Params p = gp();
+        p.A = a; p.lda = lda; p.B = b; p.ldb = ldb;
+        p.M = (int)m; p.N = (int)n; p.K = (int)k;
+        p.epi = k::EPI_STORE; p.C32 = c; p.ldc32 = ldc; p.accumulate = accumulate ? 1 : 0;
+        if (tile_cfg < 0) k::gemm_bf16_launch(dev->stream, p);
+        else k::gemm_bf16_launch_cfg(dev->stream, p, tile_cfg);
+    });
+}
+
 int catnn_hip_train_install(catnn_hip_device *dev, const catnn_graph *g, float lr,
                             catnn_hip_trainer **out) {
     return guard([&] {

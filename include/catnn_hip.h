@@ -376,6 +376,15 @@ int catnn_hip_linear_f32(catnn_hip_device *dev, const float *x, const float *w,
                          const float *b, const float *r, float *y,
                          int64_t m, int64_t k, int64_t n, int32_t act);
 
+/* C[m,n] (+)= Σ_k A[m,k]·B[n,k] on bf16 operands (raw bit patterns, both
+ * k-contiguous) with fp32 accumulation: the kernel behind every GEMM of the
+ * training step (the bf16 counterpart of linear_backward's products,
+ * adjoint.rs:35-61), exposed for tests and benchmarks.  tile_cfg: -1
+ * automatic, 0..5 a fixed tile configuration (gemm_bf16.hip). */
+int catnn_hip_gemm_bf16_nt(catnn_hip_device *dev, const uint16_t *a, int64_t lda, const uint16_t *b,
+                           int64_t ldb, float *c, int64_t ldc, int64_t m, int64_t n, int64_t k,
+                           int32_t accumulate, int32_t tile_cfg);
+
 /* Replaces cpu::relu / cpu::gelu (cpu.rs:14-29) as standalone passes. */
 int catnn_hip_act_f32(catnn_hip_device *dev, const float *x, float *y,
                       int64_t n, int32_t act);

@@ -69,6 +69,52 @@ def test_linear_matches_oracle(device, m, k, n, act, bias, res):
         assert rel_l2(got, want_ref) < TOL
 
 
+def _bf16_bits(a):
+    """Round to bf16 (ties to even) and return (uint16 bits, float64 value)."""
+    import oracle_bf16
+
+    v = oracle_bf16.bf16_round(a)
+    return (v.astype(np.float32).view(np.uint32) >> 16).astype(np.uint16), v
+
+
+GEMM_BF16_CASES = [
+    (1, 1, 1), (5, 7, 3), (130, 100, 70), (129, 257, 255), (300, 64, 520),
+    (256, 512, 384), (1024, 1024, 1024), (200, 3 * 784, 10),
+]
+
+
+@pytest.mark.parametrize("tile_cfg", [0, 1, 2, 3, 4, 5])
+@pytest.mark.parametrize("m,n,k", GEMM_BF16_CASES)
+def test_gemm_bf16_matches_float64(device, m, n, k, tile_cfg):
+    # bf16 operands, fp32 accumulation: only the accumulation rounds.
+    a_bits, a = _bf16_bits(RNG.standard_normal((m, k)))
+    b_bits, b = _bf16_bits(RNG.standard_normal((n, k)))
+    c0 = RNG.standard_normal((m, n)).astype(np.float32)
+    want = a @ b.T
+    da, db, dc = _put(device, a_bits), _put(device, b_bits), _put(device, c0)
+    D.gemm_bf16_nt(device, da, k, db, k, dc, n, m, n, k, accumulate=False, tile_cfg=tile_cfg)
+    got = _get(dc, (m, n))
+    err = rel_l2(got, want)
+    print(f"gemm_bf16 m={m} n={n} k={k} cfg={tile_cfg}: rel_l2={err:.2e}")
+    assert err < 1e-6
+    D.gemm_bf16_nt(device, da, k, db, k, dc, n, m, n, k, accumulate=True, tile_cfg=tile_cfg)
+    assert rel_l2(_get(dc, (m, n)), 2 * want) < 1e-6
+
+
+def test_gemm_bf16_strided_operands(device):
+    # Leading dimensions larger than k (the split-bf16 operands' hi part).
+    m, n, k = 190, 150, 96
+    a_bits, a = _bf16_bits(RNG.standard_normal((m, 3 * k)))
+    b_bits, b = _bf16_bits(RNG.standard_normal((n, 3 * k)))
+    dc = device.alloc(m * 200 * 4)
+    D.gemm_bf16_nt(device, _put(device, a_bits), 3 * k, _put(device, b_bits), 3 * k, dc, 200, m, n, k)
+    got = _get(dc, (m, 200))[:, :n]
+    assert rel_l2(got, a[:, :k] @ b[:, :k].T) < 1e-6
+    with pytest.raises(CatError) as e:
+        D.gemm_bf16_nt(device, dc, 4, dc, 4, dc, 4, 4, 4, 8)
+    assert e.value.kind == "ShapeMismatch"
+
+
 def test_linear_empty_and_bad_act(device):
     dx = device.alloc(64)
     D.linear(device, dx, dx, None, None, dx, 0, 4, 4, 0)  # M = 0: nothing to do
