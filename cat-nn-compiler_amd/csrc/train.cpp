@@ -73,6 +73,12 @@ struct TNode {
     std::vector<uint32_t> ins;
     std::vector<std::vector<int64_t>> in_dims;
     std::vector<bool> first_writer;  // per input: this adjoint overwrites the cotangent
+    // Linear(A) → GELU → Linear(B) with single consumers: B's input-gradient
+    // GEMM applies gelu'(A's output) in its epilogue and writes A's cotangent
+    // (fp32 and its bf16 copy); the GELU node's adjoint is then skipped.
+    bool skip_bwd = false;         // this GELU node's adjoint runs inside B's GEMM
+    uint32_t gelu_pre = UINT32_MAX;  // on B: the Linear A before the GELU
+    bool dyb_ready = false;        // on A: its bf16 cotangent is written by B
     std::vector<int64_t> dims;
     std::map<std::string, TParam *> params;
     // tapes and scratch (named pointers, assigned after planning)
@@ -96,6 +102,8 @@ struct catnn_hip_trainer {
     std::set<uint32_t> has_grad;  // ids whose cotangent some adjoint (or the loss) writes
     uint32_t out_id = 0;
     float *target = nullptr, *loss = nullptr, *mse_scratch = nullptr;
+    catnn::k::SgdParam *sgd_table = nullptr;  // device copy of every parameter's update entry
+    int sgd_n = 0, sgd_tiles = 0;
     std::vector<catnn::BufferReq> reqs;
     std::vector<void **> req_slot;
     std::vector<catnn::ArenaAlloc> plan;
@@ -215,6 +223,25 @@ static void plan_trainer(Tr &t) {
         }
     }
 
+    // GELU adjoints fused into the next Linear's input-gradient GEMM.
+    std::map<uint32_t, std::vector<uint32_t>> consumers;
+    for (auto &tn : t.nodes)
+        for (uint32_t v : tn.ins) consumers[v].push_back(tn.id);
+    auto is_linear = [&](const TNode &x) { return x.kind == CATNN_OP_LINEAR || x.kind == CATNN_OP_MATMUL; };
+    std::map<uint32_t, uint64_t> grad_from;  // cotangents first written earlier than their first consumer
+    for (auto &gn : t.nodes) {
+        if (gn.kind != CATNN_OP_GELU || gn.ins.size() != 1 || gn.id == t.out_id || !t.has_grad.count(gn.id)) continue;
+        const uint32_t a = gn.ins[0];
+        const auto &ca = consumers[a], &cg = consumers[gn.id];
+        if (ca.size() != 1 || cg.size() != 1 || t.input_ids.count(a) || a == t.out_id) continue;
+        TNode &an = t.nodes[t.index.at(a)], &bn = t.nodes[t.index.at(cg[0])];
+        if (!is_linear(an) || !is_linear(bn) || bn.ins.size() != 1 || !t.has_grad.count(bn.id)) continue;
+        gn.skip_bwd = true;
+        bn.gelu_pre = a;
+        an.dyb_ready = true;
+        grad_from[a] = bwd(bn.tick);
+    }
+
     // Values and cotangents.
     std::map<uint32_t, uint64_t> last_read;  // last tick a value is read
     for (auto &tn : t.nodes) {
@@ -231,7 +258,8 @@ static void plan_trainer(Tr &t) {
         request(t, "act:" + std::to_string(tn.id), bytes, is_input ? 0 : tn.tick,
                 is_input ? upd : last_read[tn.id], reinterpret_cast<void **>(&t.val[tn.id]));
         if (is_input) continue;
-        const uint64_t from = tn.id == t.out_id ? n : bwd(first_consumer_tick.count(tn.id) ? first_consumer_tick[tn.id] : tn.tick);
+        uint64_t from = tn.id == t.out_id ? n : bwd(first_consumer_tick.count(tn.id) ? first_consumer_tick[tn.id] : tn.tick);
+        if (grad_from.count(tn.id)) from = std::min(from, grad_from[tn.id]);
         request(t, "grad:" + std::to_string(tn.id), bytes, std::min<uint64_t>(from, bwd(tn.tick)),
                 bwd(tn.tick), reinterpret_cast<void **>(&t.grad[tn.id]));
     }
@@ -284,7 +312,11 @@ static void plan_trainer(Tr &t) {
                 if (const HostTensor *b = nd.param("b")) add_param(tn, "b", 1, N, false, false, b->data);
                 tape(tn, "x3", (uint64_t)(M * 3 * K) * 2);
                 scratch(tn, "xbt", (uint64_t)(M * K) * 2);
-                scratch(tn, "dyb", (uint64_t)(M * N) * 2);
+                if (tn.dyb_ready)  // written by the next Linear's backward (the fused GELU adjoint)
+                    request(t, "scratch:" + tn.node->name + ":dyb", (uint64_t)(M * N) * 2, grad_from.at(tn.id),
+                            bwd(tn.tick), &tn.B("dyb"));
+                else
+                    scratch(tn, "dyb", (uint64_t)(M * N) * 2);
                 scratch(tn, "dybt", (uint64_t)(M * N) * 2);
                 scratch(tn, "colsum", k::colsum_scratch_bytes(M, (int)N));
                 break;
@@ -369,18 +401,46 @@ static void plan_trainer(Tr &t) {
                 break;
         }
     }
+    // One multi-tensor update entry per parameter.
+    request(t, "sgd_table", (uint64_t)t.params.size() * sizeof(k::SgdParam), 0, upd,
+            reinterpret_cast<void **>(&t.sgd_table));
+}
+
+// The multi-tensor update table: every parameter, trained ones (nodes that
+// receive a cotangent) with their gradient, in 64×64 tiles.
+static void build_sgd_table(Tr &t, std::vector<k::SgdParam> &tab) {
+    int tiles = 0;
+    for (auto &tn : t.nodes) {
+        if (t.input_ids.count(tn.id)) continue;
+        const bool trained = t.has_grad.count(tn.id) != 0;
+        for (auto &kv : tn.params) {
+            TParam *p = kv.second;
+            k::SgdParam e{};
+            e.p = p->master;
+            e.g = trained ? p->grad : nullptr;
+            e.b = p->want_b ? p->b : nullptr;
+            e.bt = p->want_bt ? p->bt : nullptr;
+            e.bt3 = p->want_bt3 ? p->bt3 : nullptr;
+            e.rows = (int)p->rows;
+            e.cols = (int)p->cols;
+            e.tiles_c = (int)((p->cols + 63) / 64);
+            e.tile0 = tiles;
+            const int64_t nt = (int64_t)((p->rows + 63) / 64) * e.tiles_c;
+            CATNN_REQUIRE(tiles + nt < (1ll << 31), CATNN_ERR_SHAPE_MISMATCH, "training: too many parameter tiles");
+            tiles += (int)nt;
+            tab.push_back(e);
+        }
+    }
+    t.sgd_tiles = tiles;
+    t.sgd_n = (int)tab.size();
 }
 
 // Masters from the host copies, then the bf16 operand copies from the masters.
 static void upload_params(Tr &t) {
     hipStream_t s = t.dev->stream;
-    for (auto &p : t.params) {
+    for (auto &p : t.params)
         CATNN_HIP(hipMemcpyAsync(p->master, p->init.data(), p->init.size() * 4, hipMemcpyHostToDevice, s));
-        if (p->want_b) k::cast_f32_bf16(s, p->master, p->b, p->rows * p->cols);
-        if (p->want_bt)
-            k::transpose_bf16(s, p->b, p->cols, nullptr, 1, (int)p->rows, (int)p->cols, p->bt, p->rows);
-        if (p->want_bt3) k::transpose_split3(s, p->master, p->cols, (int)p->rows, (int)p->cols, p->bt3, 3 * p->rows);
-    }
+    k::sgd_multi(s, t.sgd_table, t.sgd_n, t.sgd_tiles, 0.f, false);
 }
 
 static void reserve_and_upload(Tr &t) {
@@ -400,8 +460,13 @@ static void reserve_and_upload(Tr &t) {
     for (auto &p : t.params)
         CATNN_REQUIRE((int64_t)p->init.size() == p->rows * p->cols, CATNN_ERR_SHAPE_MISMATCH,
                       p->name + ": parameter size");
+    std::vector<k::SgdParam> tab;
+    build_sgd_table(t, tab);
+    CATNN_REQUIRE(tab.size() == t.params.size(), CATNN_ERR_WIRING, "training: update table size");
+    CATNN_HIP(hipMemcpyAsync(t.sgd_table, tab.data(), tab.size() * sizeof(k::SgdParam), hipMemcpyHostToDevice,
+                             t.dev->stream));
     upload_params(t);
-    CATNN_HIP(hipStreamSynchronize(t.dev->stream));
+    CATNN_HIP(hipStreamSynchronize(t.dev->stream));  // before `tab` goes out of scope
 }
 
 // ------------------------------------------------------------ forward
@@ -543,8 +608,20 @@ static void backward_node(Tr &t, TNode &tn) {
             const int64_t K = w->rows, N = w->cols, M = nx / K;
             bf16_t *dyb = (bf16_t *)tn.B("dyb"), *dybt = (bf16_t *)tn.B("dybt");
             bf16_t *x3 = (bf16_t *)tn.B("x3"), *xbt = (bf16_t *)tn.B("xbt");
-            k::cast_f32_bf16(s, dy, dyb, M * N);
-            if (dst(0)) gemm_nt(s, dyb, N, w->b, N, (int)M, (int)K, (int)N, dst(0), K, !tn.first_writer[0]);
+            if (!tn.dyb_ready) k::cast_f32_bf16(s, dy, dyb, M * N);
+            if (tn.gelu_pre != UINT32_MAX) {
+                // dA = (dy·Wᵀ) ∘ gelu'(A's output): A's cotangent and its bf16 copy.
+                TNode &an = t.nodes[t.index.at(tn.gelu_pre)];
+                k::GemmBf16Params p = gp();
+                p.A = dyb; p.lda = N; p.B = w->b; p.ldb = N;
+                p.M = (int)M; p.N = (int)K; p.K = (int)N;
+                p.epi = k::EPI_GELU_BWD; p.Z = t.val.at(an.id); p.ldz = K;
+                p.C32 = t.grad.at(an.id); p.ldc32 = K; p.accumulate = 0;
+                p.Cb = (bf16_t *)an.B("dyb"); p.ldcb = K;
+                k::gemm_bf16_launch(s, p);
+            } else if (dst(0)) {
+                gemm_nt(s, dyb, N, w->b, N, (int)M, (int)K, (int)N, dst(0), K, !tn.first_writer[0]);
+            }
             k::transpose_bf16(s, dyb, N, nullptr, 1, (int)M, (int)N, dybt, M);
             k::transpose_bf16(s, x3, 3 * K, nullptr, 1, (int)M, (int)K, xbt, M);  // hi part of x
             gemm_nt(s, xbt, M, dybt, M, (int)K, (int)N, (int)M, w->grad, N, false);
@@ -663,19 +740,10 @@ static void train_step(Tr &t) {
     // A node whose output nobody reads receives no cotangent and is skipped,
     // as reference_train skips ids without an entry in `grads`.
     for (auto it = t.nodes.rbegin(); it != t.nodes.rend(); ++it)
-        if (!t.input_ids.count(it->id) && t.has_grad.count(it->id)) backward_node(t, *it);
-    // Sgd::put on the parameters of every node that received a cotangent.
-    for (auto &tn : t.nodes) {
-        if (t.input_ids.count(tn.id) || !t.has_grad.count(tn.id)) continue;
-        for (auto &kv : tn.params) {
-            TParam *p = kv.second;
-            k::sgd(s, p->master, p->grad, p->cols, p->rows, (int)p->cols, t.lr, p->want_b ? p->b : nullptr);
-            if (p->want_bt)
-                k::transpose_bf16(s, p->b, p->cols, nullptr, 1, (int)p->rows, (int)p->cols, p->bt, p->rows);
-            if (p->want_bt3)
-                k::transpose_split3(s, p->master, p->cols, (int)p->rows, (int)p->cols, p->bt3, 3 * p->rows);
-        }
-    }
+        if (!t.input_ids.count(it->id) && t.has_grad.count(it->id) && !it->skip_bwd) backward_node(t, *it);
+    // Sgd::put on the parameters of every node that received a cotangent,
+    // and the refresh of their bf16 copies, in one launch.
+    k::sgd_multi(s, t.sgd_table, t.sgd_n, t.sgd_tiles, t.lr, true);
 }
 
 static TParam *find_param(Tr &t, uint32_t node_id, const std::string &port, int64_t *col0,

@@ -170,76 +170,134 @@ __global__ __launch_bounds__(256) void ln_fwd_kernel(const float *__restrict__ x
     }
 }
 
-// LayerNorm adjoint: dx (+=) per row, and per-block partial sums of dγ, dβ
-// (block b covers rows [b·rows_per_block, ...)).
-constexpr int kLnRowsPerBlock = 64;
+// Column sums of [rows, cols] tensors (bias and LayerNorm parameter
+// gradients, the router's gate gradient) in two fixed-order stages, no
+// atomics: col_partials sums groups of kColRows rows per column (threads
+// along columns, so every row read is coalesced), reduce_partials adds the
+// groups with four wavefronts per 64 columns.
+constexpr int kColRows = 64;
 
-__global__ __launch_bounds__(256) void ln_bwd_kernel(const float *__restrict__ x,
-                                                     const float *__restrict__ g,
-                                                     const float *__restrict__ mean,
-                                                     const float *__restrict__ rstd,
-                                                     const float *__restrict__ dy,
-                                                     float *__restrict__ dx, int accumulate,
-                                                     float *__restrict__ part_g,
-                                                     float *__restrict__ part_b, int64_t rows,
-                                                     int cols) {
-    // Phase 1: one wavefront per row, dx.
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int64_t r0 = (int64_t)blockIdx.x * kLnRowsPerBlock;
-    const float n = (float)cols;
-    for (int64_t row = r0 + wave; dx && row < r0 + kLnRowsPerBlock && row < rows; row += 4) {
-        const float mu = mean[row], inv = rstd[row];
-        const float *xr = x + row * cols, *gr = dy + row * cols;
-        float sd = 0.f, sdx = 0.f;
-        for (int c = lane; c < cols; c += 64) {
-            const float xh = (xr[c] - mu) * inv;
-            const float d = gr[c] * g[c];
-            sd += d;
-            sdx += d * xh;
+// part_a[g][c] = Σ_r dy[r][c] and, for LayerNorm (LN), part_a = Σ_r dy·x̂,
+// part_b = Σ_r dy with x̂ = (x − mean)·rstd, over the rows r of group g.
+template <bool LN>
+__global__ __launch_bounds__(256) void col_partials_kernel(const float *__restrict__ dy,
+                                                           const float *__restrict__ x,
+                                                           const float *__restrict__ mean,
+                                                           const float *__restrict__ rstd, int64_t rows,
+                                                           int cols, float *__restrict__ part_a,
+                                                           float *__restrict__ part_b) {
+    const int c = blockIdx.x * 256 + threadIdx.x;
+    if (c >= cols) return;
+    const int64_t r0 = (int64_t)blockIdx.y * kColRows;
+    const int64_t r1 = r0 + kColRows < rows ? r0 + kColRows : rows;
+    float sa = 0.f, sb = 0.f;
+    for (int64_t r = r0; r < r1; ++r) {
+        const float d = dy[r * cols + c];
+        if (LN) {
+            const float xh = (x[r * cols + c] - mean[r]) * rstd[r];
+            sa += d * xh;
+            sb += d;
+        } else {
+            sa += d;
         }
-        sd = wave_sum(sd);
-        sdx = wave_sum(sdx);
-        for (int c = lane; c < cols; c += 64) {
-            const float xh = (xr[c] - mu) * inv;
-            const float d = gr[c] * g[c];
-            const float v = (inv / n) * (n * d - sd - xh * sdx);
+    }
+    part_a[(int64_t)blockIdx.y * cols + c] = sa;
+    if (LN) part_b[(int64_t)blockIdx.y * cols + c] = sb;
+}
+
+// out[c] (+)= Σ_g part[g][c]: wavefront w sums groups w, w+4, …; the four
+// sums are added in a fixed order.
+__global__ __launch_bounds__(256) void reduce_partials_kernel(const float *__restrict__ part, int ng,
+                                                              int cols, float *__restrict__ out,
+                                                              int accumulate) {
+    __shared__ float red[4][64];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int c = blockIdx.x * 64 + lane;
+    float s = 0.f;
+    if (c < cols)
+        for (int g = w; g < ng; g += 4) s += part[(int64_t)g * cols + c];
+    red[w][lane] = s;
+    __syncthreads();
+    if (w == 0 && c < cols) {
+        const float t = (red[0][lane] + red[1][lane]) + (red[2][lane] + red[3][lane]);
+        out[c] = accumulate ? out[c] + t : t;
+    }
+}
+
+// LayerNorm adjoint, dx (+)= (rstd/n)(n·g − Σg − x̂·Σ(g·x̂)) with g = dy·γ:
+// one wavefront per row, the row held in registers (NV values per lane,
+// cols ≤ 64·NV), so x and dy are read once.
+template <int NV>
+__global__ __launch_bounds__(256) void ln_bwd_dx_kernel(const float *__restrict__ x,
+                                                        const float *__restrict__ gam,
+                                                        const float *__restrict__ mean,
+                                                        const float *__restrict__ rstd,
+                                                        const float *__restrict__ dy,
+                                                        float *__restrict__ dx, int accumulate,
+                                                        int64_t rows, int cols) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const float mu = mean[row], inv = rstd[row];
+    const float *xr = x + row * cols, *gr = dy + row * cols;
+    float xh[NV], gd[NV];
+    float sd = 0.f, sdx = 0.f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int c = lane + 64 * j;
+        xh[j] = 0.f;
+        gd[j] = 0.f;
+        if (c < cols) {
+            xh[j] = (xr[c] - mu) * inv;
+            gd[j] = gr[c] * gam[c];
+            sd += gd[j];
+            sdx += gd[j] * xh[j];
+        }
+    }
+    sd = wave_sum(sd);
+    sdx = wave_sum(sdx);
+    const float n = (float)cols;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int c = lane + 64 * j;
+        if (c < cols) {
+            const float v = (inv / n) * (n * gd[j] - sd - xh[j] * sdx);
             float *o = dx + row * cols + c;
             *o = accumulate ? *o + v : v;
         }
     }
-    // Phase 2: column partials over this block's rows (fixed row order).
-    for (int c = threadIdx.x; c < cols; c += 256) {
-        float pg = 0.f, pb = 0.f;
-        for (int64_t row = r0; row < r0 + kLnRowsPerBlock && row < rows; ++row) {
-            const float xh = (x[row * cols + c] - mean[row]) * rstd[row];
-            const float d = dy[row * cols + c];
-            pg += d * xh;
-            pb += d;
-        }
-        part_g[(int64_t)blockIdx.x * cols + c] = pg;
-        part_b[(int64_t)blockIdx.x * cols + c] = pb;
+}
+
+// Any width: the same with two passes over the row in memory.
+__global__ __launch_bounds__(256) void ln_bwd_dx_any_kernel(const float *__restrict__ x,
+                                                            const float *__restrict__ gam,
+                                                            const float *__restrict__ mean,
+                                                            const float *__restrict__ rstd,
+                                                            const float *__restrict__ dy,
+                                                            float *__restrict__ dx, int accumulate,
+                                                            int64_t rows, int cols) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const float mu = mean[row], inv = rstd[row];
+    const float *xr = x + row * cols, *gr = dy + row * cols;
+    float sd = 0.f, sdx = 0.f;
+    for (int c = lane; c < cols; c += 64) {
+        const float xh = (xr[c] - mu) * inv;
+        const float d = gr[c] * gam[c];
+        sd += d;
+        sdx += d * xh;
     }
-}
-
-// out[c] (+)= Σ_b part[b][c], b ascending.
-__global__ void reduce_parts_kernel(const float *__restrict__ part, int nb, int cols,
-                                    float *__restrict__ out, int accumulate) {
-    const int c = blockIdx.x * blockDim.x + threadIdx.x;
-    if (c >= cols) return;
-    float s = 0.f;
-    for (int b = 0; b < nb; ++b) s += part[(int64_t)b * cols + c];
-    out[c] = accumulate ? out[c] + s : s;
-}
-
-// Column partial sums of y [rows, cols] over blocks of 64 rows.
-__global__ void colsum_parts_kernel(const float *__restrict__ y, int64_t rows, int cols,
-                                    float *__restrict__ part) {
-    const int c = blockIdx.x * blockDim.x + threadIdx.x;
-    if (c >= cols) return;
-    const int64_t r0 = (int64_t)blockIdx.y * 64;
-    float s = 0.f;
-    for (int64_t r = r0; r < r0 + 64 && r < rows; ++r) s += y[r * cols + c];
-    part[(int64_t)blockIdx.y * cols + c] = s;
+    sd = wave_sum(sd);
+    sdx = wave_sum(sdx);
+    const float n = (float)cols;
+    for (int c = lane; c < cols; c += 64) {
+        const float xh = (xr[c] - mu) * inv;
+        const float d = gr[c] * gam[c];
+        const float v = (inv / n) * (n * d - sd - xh * sdx);
+        float *o = dx + row * cols + c;
+        *o = accumulate ? *o + v : v;
+    }
 }
 
 __global__ void act_bwd_kernel(const float *__restrict__ z, const float *__restrict__ dy,
@@ -282,12 +340,15 @@ __global__ __launch_bounds__(256) void mse_kernel(const float *__restrict__ pred
     if (threadIdx.x == 0) part[blockIdx.x] = (ws[0] + ws[1]) + (ws[2] + ws[3]);
 }
 
-__global__ void mse_finish_kernel(const float *__restrict__ part, int nb, int64_t n,
-                                  float *__restrict__ loss) {
-    if (threadIdx.x != 0) return;
+__global__ __launch_bounds__(256) void mse_finish_kernel(const float *__restrict__ part, int nb,
+                                                         int64_t n, float *__restrict__ loss) {
+    __shared__ float ws[4];
     float s = 0.f;
-    for (int b = 0; b < nb; ++b) s += part[b];
-    *loss = s / (float)n;
+    for (int b = threadIdx.x; b < nb; b += 256) s += part[b];
+    s = wave_sum(s);
+    if ((threadIdx.x & 63) == 0) ws[threadIdx.x >> 6] = s;
+    __syncthreads();
+    if (threadIdx.x == 0) *loss = ((ws[0] + ws[1]) + (ws[2] + ws[3])) / (float)n;
 }
 
 // p −= lr·g; pb = bf16(p) when given.  g may have a row stride (packed
@@ -307,6 +368,58 @@ __global__ void sgd_kernel(float *__restrict__ p, const float *__restrict__ g, i
     }
 }
 
+// Multi-tensor SGD: block b updates one 64×64 tile of the parameter whose
+// tile range holds b (binary search of the table), writes the master and
+// the row-major bf16 copy, and through LDS the transposed copies.
+__global__ __launch_bounds__(256) void sgd_multi_kernel(const SgdParam *__restrict__ tab, int n,
+                                                        float lr, int use_grad) {
+#pragma clang fp contract(off)
+    __shared__ bf16_t th[64][66], tl[64][66];
+    const int b = blockIdx.x;
+    int lo = 0, hi = n - 1;
+    while (lo < hi) {  // last entry with tile0 <= b
+        const int mid = (lo + hi + 1) >> 1;
+        if (tab[mid].tile0 <= b) lo = mid;
+        else hi = mid - 1;
+    }
+    const SgdParam P = tab[lo];
+    const int t = b - P.tile0;
+    const int r0 = (t / P.tiles_c) * 64, c0 = (t % P.tiles_c) * 64;
+    const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+    const bool grad = use_grad && P.g;
+    for (int i = ty; i < 64; i += 4) {
+        const int r = r0 + i, c = c0 + tx;
+        bf16_t h = 0, l = 0;
+        if (r < P.rows && c < P.cols) {
+            const int64_t e = (int64_t)r * P.cols + c;
+            float v = P.p[e];
+            if (grad) {
+                v = v - lr * P.g[e];
+                P.p[e] = v;
+            }
+            h = f2bf(v);
+            l = f2bf(v - __uint_as_float((uint32_t)h << 16));
+            if (P.b) P.b[e] = h;
+        }
+        th[i][tx] = h;
+        tl[i][tx] = l;
+    }
+    if (!P.bt && !P.bt3) return;  // uniform per block
+    __syncthreads();
+    for (int i = ty; i < 64; i += 4) {
+        const int c = c0 + i, r = r0 + tx;
+        if (c < P.cols && r < P.rows) {
+            if (P.bt) P.bt[(int64_t)c * P.rows + r] = th[tx][i];
+            if (P.bt3) {
+                bf16_t *o = P.bt3 + (int64_t)c * 3 * P.rows;
+                o[r] = th[tx][i];
+                o[P.rows + r] = tl[tx][i];
+                o[2 * P.rows + r] = th[tx][i];
+            }
+        }
+    }
+}
+
 // Router STE, per token: dlogits[t, idx_k] = w_k (dw_k − Σ_j w_j dw_j).
 __global__ void router_dlogits_kernel(const int32_t *__restrict__ idx, const float *__restrict__ w,
                                       const float *__restrict__ dw, int T, int E, int K,
@@ -322,19 +435,20 @@ __global__ void router_dlogits_kernel(const int32_t *__restrict__ idx, const flo
     }
 }
 
-// Partials of dgate[h][e] = Σ_t x[t][h]·dl[t][e] over blocks of 64 tokens.
-__global__ void router_dgate_parts_kernel(const float *__restrict__ x, const float *__restrict__ dl,
-                                          int T, int H, int E, float *__restrict__ part) {
-    const int h = blockIdx.x * blockDim.x + threadIdx.x;
-    if (h >= H) return;
-    const int t0 = blockIdx.y * 64;
-    float acc[64];
-    for (int e = 0; e < E; ++e) acc[e] = 0.f;
-    for (int t = t0; t < t0 + 64 && t < T; ++t) {
-        const float xv = x[(int64_t)t * H + h];
-        for (int e = 0; e < E; ++e) acc[e] += xv * dl[(int64_t)t * E + e];
-    }
-    for (int e = 0; e < E; ++e) part[((int64_t)blockIdx.y * H + h) * E + e] = acc[e];
+// Partials of dgate[h][e] = Σ_t x[t][h]·dl[t][e] over groups of kColRows
+// tokens; thread j owns entry j = h·E + e of the [H, E] gradient.
+__global__ __launch_bounds__(256) void router_dgate_parts_kernel(const float *__restrict__ x,
+                                                                 const float *__restrict__ dl, int T,
+                                                                 int H, int E,
+                                                                 float *__restrict__ part) {
+    const int j = blockIdx.x * 256 + threadIdx.x;
+    if (j >= H * E) return;
+    const int h = j / E, e = j - h * E;
+    const int t0 = blockIdx.y * kColRows;
+    const int t1 = t0 + kColRows < T ? t0 + kColRows : T;
+    float s = 0.f;
+    for (int t = t0; t < t1; ++t) s += x[(int64_t)t * H + h] * dl[(int64_t)t * E + e];
+    part[(int64_t)blockIdx.y * H * E + j] = s;
 }
 
 // Per permuted position: dys[pos] = bf16(w[slot]·dout[tok]) and
@@ -365,22 +479,36 @@ __global__ __launch_bounds__(256) void moe_slot_grad_kernel(
     if (threadIdx.x == 0) dw[slot] = (ws[0] + ws[1]) + (ws[2] + ws[3]);
 }
 
-// dx[t][h] (+)= Σ_k dxs[pos(t,k)][h] + Σ_e dl[t][e]·gate[h][e].
+// dx[t][h] (+)= Σ_k dxs[pos(t,k)][h] + Σ_e dl[t][e]·gate[h][e].  A thread
+// owns one h for kMoeDxTokens tokens, so gate[h][·] is read once per
+// thread and dl[t][·] is uniform across the block.
+constexpr int kMoeDxTokens = 16;
+
 __global__ __launch_bounds__(256) void moe_dx_kernel(const float *__restrict__ dxs,
                                                      const int32_t *__restrict__ pos_of_slot,
                                                      const float *__restrict__ dl,
                                                      const float *__restrict__ gate, int T, int K,
                                                      int H, int E, float *__restrict__ dx,
                                                      int accumulate) {
-    const int t = blockIdx.x;
-    if (t >= T) return;
-    for (int h = threadIdx.x; h < H; h += 256) {
+    const int h = blockIdx.x * 256 + threadIdx.x;
+    const int t0 = blockIdx.y * kMoeDxTokens;
+    if (h >= H) return;
+    float r[kMoeDxTokens];
+#pragma unroll
+    for (int i = 0; i < kMoeDxTokens; ++i) r[i] = 0.f;
+    for (int e = 0; e < E; ++e) {
+        const float g = gate[(int64_t)h * E + e];
+#pragma unroll
+        for (int i = 0; i < kMoeDxTokens; ++i)
+            if (t0 + i < T) r[i] += dl[(int64_t)(t0 + i) * E + e] * g;
+    }
+#pragma unroll
+    for (int i = 0; i < kMoeDxTokens; ++i) {
+        const int t = t0 + i;
+        if (t >= T) break;
         float s = 0.f;
-        for (int kk = 0; kk < K; ++kk)
-            s += dxs[(int64_t)pos_of_slot[(int64_t)t * K + kk] * H + h];
-        float r = 0.f;
-        for (int e = 0; e < E; ++e) r += dl[(int64_t)t * E + e] * gate[(int64_t)h * E + e];
-        s += r;
+        for (int kk = 0; kk < K; ++kk) s += dxs[(int64_t)pos_of_slot[(int64_t)t * K + kk] * H + h];
+        s += r[i];
         float *o = dx + (int64_t)t * H + h;
         *o = accumulate ? *o + s : s;
     }
@@ -452,36 +580,54 @@ void ln_forward_train(hipStream_t s, const float *x, const float *g, const float
 }
 
 uint64_t ln_backward_scratch_bytes(int64_t rows, int cols) {
-    const int64_t nb = (rows + kLnRowsPerBlock - 1) / kLnRowsPerBlock;
-    return (uint64_t)nb * cols * 4 * 2;
+    const int64_t ng = (rows + kColRows - 1) / kColRows;
+    return (uint64_t)ng * cols * 4 * 2;
+}
+
+static void reduce_partials(hipStream_t s, const float *part, int64_t ng, int cols, float *out,
+                            bool accumulate) {
+    reduce_partials_kernel<<<(unsigned)((cols + 63) / 64), 256, 0, s>>>(part, (int)ng, cols, out,
+                                                                        accumulate ? 1 : 0);
+    CATNN_HIP(hipGetLastError());
 }
 
 void ln_backward(hipStream_t s, const float *x, const float *g, const float *mean, const float *rstd,
                  const float *dy, float *dx, bool accumulate, float *dg, float *db, bool acc_params,
                  int64_t rows, int cols, float *scratch) {
     if (rows <= 0) return;
-    const int64_t nb = (rows + kLnRowsPerBlock - 1) / kLnRowsPerBlock;
-    float *pg = scratch, *pb = scratch + nb * cols;
-    ln_bwd_kernel<<<(unsigned)nb, 256, 0, s>>>(x, g, mean, rstd, dy, dx, accumulate ? 1 : 0, pg, pb,
-                                               rows, cols);
+    const int64_t ng = (rows + kColRows - 1) / kColRows;
+    CATNN_REQUIRE(ng < 65536, CATNN_ERR_SHAPE_MISMATCH, "layer_norm backward: too many rows");
+    if (dx) {
+        const unsigned blocks = (unsigned)((rows + 3) / 4);
+        const int acc = accumulate ? 1 : 0;
+        if (cols <= 256) ln_bwd_dx_kernel<4><<<blocks, 256, 0, s>>>(x, g, mean, rstd, dy, dx, acc, rows, cols);
+        else if (cols <= 512) ln_bwd_dx_kernel<8><<<blocks, 256, 0, s>>>(x, g, mean, rstd, dy, dx, acc, rows, cols);
+        else if (cols <= 1024) ln_bwd_dx_kernel<16><<<blocks, 256, 0, s>>>(x, g, mean, rstd, dy, dx, acc, rows, cols);
+        else if (cols <= 2048) ln_bwd_dx_kernel<32><<<blocks, 256, 0, s>>>(x, g, mean, rstd, dy, dx, acc, rows, cols);
+        else ln_bwd_dx_any_kernel<<<blocks, 256, 0, s>>>(x, g, mean, rstd, dy, dx, acc, rows, cols);
+        CATNN_HIP(hipGetLastError());
+    }
+    float *pg = scratch, *pb = scratch + ng * cols;
+    col_partials_kernel<true><<<dim3((cols + 255) / 256, (unsigned)ng), 256, 0, s>>>(dy, x, mean, rstd, rows,
+                                                                                    cols, pg, pb);
     CATNN_HIP(hipGetLastError());
-    reduce_parts_kernel<<<(cols + 255) / 256, 256, 0, s>>>(pg, (int)nb, cols, dg, acc_params);
-    reduce_parts_kernel<<<(cols + 255) / 256, 256, 0, s>>>(pb, (int)nb, cols, db, acc_params);
-    CATNN_HIP(hipGetLastError());
+    reduce_partials(s, pg, ng, cols, dg, acc_params);
+    reduce_partials(s, pb, ng, cols, db, acc_params);
 }
 
 uint64_t colsum_scratch_bytes(int64_t rows, int cols) {
-    return (uint64_t)((rows + 63) / 64) * cols * 4;
+    return (uint64_t)((rows + kColRows - 1) / kColRows) * cols * 4;
 }
 
 void colsum(hipStream_t s, const float *y, int64_t rows, int cols, float *out, bool accumulate,
             float *scratch) {
     if (rows <= 0 || cols <= 0) return;
-    const int64_t nb = (rows + 63) / 64;
-    CATNN_REQUIRE(nb < 65536, CATNN_ERR_SHAPE_MISMATCH, "colsum: too many rows");
-    colsum_parts_kernel<<<dim3((cols + 255) / 256, (unsigned)nb), 256, 0, s>>>(y, rows, cols, scratch);
-    reduce_parts_kernel<<<(cols + 255) / 256, 256, 0, s>>>(scratch, (int)nb, cols, out, accumulate);
+    const int64_t ng = (rows + kColRows - 1) / kColRows;
+    CATNN_REQUIRE(ng < 65536, CATNN_ERR_SHAPE_MISMATCH, "colsum: too many rows");
+    col_partials_kernel<false><<<dim3((cols + 255) / 256, (unsigned)ng), 256, 0, s>>>(
+        y, nullptr, nullptr, nullptr, rows, cols, scratch, nullptr);
     CATNN_HIP(hipGetLastError());
+    reduce_partials(s, scratch, ng, cols, out, accumulate);
 }
 
 void act_backward(hipStream_t s, const float *z, const float *dy, float *dx, int64_t n, int act,
@@ -499,7 +645,7 @@ void mse(hipStream_t s, const float *pred, const float *tgt, float *d, int64_t n
          float *scratch) {
     CATNN_REQUIRE(n > 0, CATNN_ERR_SHAPE_MISMATCH, "mse on empty tensors");
     mse_kernel<<<kMseBlocks, 256, 0, s>>>(pred, tgt, d, n, scratch);
-    mse_finish_kernel<<<1, 64, 0, s>>>(scratch, kMseBlocks, n, loss);
+    mse_finish_kernel<<<1, 256, 0, s>>>(scratch, kMseBlocks, n, loss);
     CATNN_HIP(hipGetLastError());
 }
 
@@ -510,21 +656,28 @@ void sgd(hipStream_t s, float *p, const float *g, int64_t ldg, int64_t rows, int
     CATNN_HIP(hipGetLastError());
 }
 
+void sgd_multi(hipStream_t s, const SgdParam *table, int n, int tiles, float lr, bool use_grad) {
+    if (n <= 0 || tiles <= 0) return;
+    sgd_multi_kernel<<<(unsigned)tiles, 256, 0, s>>>(table, n, lr, use_grad ? 1 : 0);
+    CATNN_HIP(hipGetLastError());
+}
+
 void router_backward(hipStream_t s, const int32_t *idx, const float *w, const float *dw,
                      const float *x, int T, int H, int E, int K, float *dl, float *dgate,
                      float *scratch) {
     CATNN_REQUIRE(E <= 64, CATNN_ERR_SHAPE_MISMATCH, "router backward: more than 64 experts");
     if (T <= 0) return;
     router_dlogits_kernel<<<(T + 255) / 256, 256, 0, s>>>(idx, w, dw, T, E, K, dl);
-    const int nb = (T + 63) / 64;
-    router_dgate_parts_kernel<<<dim3((H + 127) / 128, (unsigned)nb), 128, 0, s>>>(x, dl, T, H, E,
-                                                                                 scratch);
-    reduce_parts_kernel<<<(H * E + 255) / 256, 256, 0, s>>>(scratch, nb, H * E, dgate, false);
+    const int ng = (T + kColRows - 1) / kColRows;
+    CATNN_REQUIRE(ng < 65536, CATNN_ERR_SHAPE_MISMATCH, "router backward: too many tokens");
+    router_dgate_parts_kernel<<<dim3((unsigned)((H * E + 255) / 256), (unsigned)ng), 256, 0, s>>>(x, dl, T, H, E,
+                                                                                               scratch);
     CATNN_HIP(hipGetLastError());
+    reduce_partials(s, scratch, ng, H * E, dgate, false);
 }
 
 uint64_t router_backward_scratch_bytes(int T, int H, int E) {
-    return (uint64_t)((T + 63) / 64) * H * E * 4;
+    return (uint64_t)((T + kColRows - 1) / kColRows) * H * E * 4;
 }
 
 void moe_slot_grads(hipStream_t s, const int32_t *slot_of_pos, const float *w, const float *y,
@@ -537,8 +690,9 @@ void moe_slot_grads(hipStream_t s, const int32_t *slot_of_pos, const float *w, c
 void moe_dx(hipStream_t s, const float *dxs, const int32_t *pos_of_slot, const float *dl,
             const float *gate, int T, int K, int H, int E, float *dx, bool accumulate) {
     if (T <= 0) return;
-    moe_dx_kernel<<<(unsigned)T, 256, 0, s>>>(dxs, pos_of_slot, dl, gate, T, K, H, E, dx,
-                                              accumulate ? 1 : 0);
+    CATNN_REQUIRE((T + kMoeDxTokens - 1) / kMoeDxTokens < 65536, CATNN_ERR_SHAPE_MISMATCH, "moe dx: too many tokens");
+    moe_dx_kernel<<<dim3((unsigned)((H + 255) / 256), (unsigned)((T + kMoeDxTokens - 1) / kMoeDxTokens)), 256, 0, s>>>(
+        dxs, pos_of_slot, dl, gate, T, K, H, E, dx, accumulate ? 1 : 0);
     CATNN_HIP(hipGetLastError());
 }
 

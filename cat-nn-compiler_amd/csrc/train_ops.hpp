@@ -48,6 +48,23 @@ void mse(hipStream_t s, const float *pred, const float *tgt, float *d, int64_t n
 void sgd(hipStream_t s, float *p, const float *g, int64_t ldg, int64_t rows, int cols, float lr,
          bf16_t *pb);
 
+// One parameter of the multi-tensor update: fp32 master p [rows, cols] and
+// its gradient g (same layout, or null: refresh only), and the bf16 copies
+// to rewrite from the new value: b [rows, cols], bt [cols, rows] and the
+// split-bf16 transposed bt3 [cols, 3·rows] = hi | lo | hi (each may be null).
+struct SgdParam {
+    float *p;
+    const float *g;
+    bf16_t *b, *bt, *bt3;
+    int rows, cols;
+    int tile0;    // first 64×64 tile of this parameter in the launch
+    int tiles_c;  // tiles across cols
+};
+// p −= lr·g on every parameter of `table` (device memory, n entries, tile0
+// ascending, `tiles` in total) in one launch, then the bf16 copies; with
+// use_grad false only the copies are refreshed.
+void sgd_multi(hipStream_t s, const SgdParam *table, int n, int tiles, float lr, bool use_grad);
+
 uint64_t router_backward_scratch_bytes(int T, int H, int E);
 void router_backward(hipStream_t s, const int32_t *idx, const float *w, const float *dw,
                      const float *x, int T, int H, int E, int K, float *dl, float *dgate,
