@@ -34,6 +34,13 @@ namespace {
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr float kLog2e = 1.4426950408889634f;
+// Masked scores: far below any real score but finite, so a row whose keys
+// are all masked so far never produces inf − inf.
+constexpr float kMasked = -1e30f;
+
+// 2^x on the hardware exp unit (v_exp_f32); results below 2^-126 flush to
+// zero, which no softmax weight in the fp32 tolerance can see.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 template <int DH>
 __global__ __launch_bounds__(256, 2) void attn_mfma_kernel(const float *__restrict__ q,
@@ -44,21 +51,24 @@ __global__ __launch_bounds__(256, 2) void attn_mfma_kernel(const float *__restri
                                                            int S, int H, float qscale, int causal,
                                                            int n_qblocks) {
     static_assert(DH == 64, "MFMA attention is written for d_head = 64");
-    constexpr int BQ = 128, BKV = 64, LDK = DH + 4;
+    constexpr int BQ = 128, BKV = 64, LDK = DH + 4, LDV = BKV + 4;
     constexpr int KV_IT = BKV * DH / 4 / 256;  // float4 per thread per tile, per operand
+    // K row-major; V transposed (Vt[d][key]) so that the four keys a lane
+    // feeds to four consecutive P·V MFMAs are one 16-byte LDS read.
     __shared__ float Ks[2][BKV][LDK];
-    __shared__ float Vs[2][BKV][LDK];
+    __shared__ float Vt[2][DH][LDV];
 
-    const int bid = blockIdx.x;
-    // Causal work grows with the query block: start the heavy ones first.
-    const int qb = n_qblocks - 1 - (bid % n_qblocks);
-    const int bh = bid / n_qblocks;
+    // Causal work grows with the query block: start the heavy ones first,
+    // spread evenly over the XCDs.
+    int blk, bh;
+    split_bh_block(blockIdx.x, n_qblocks, (int)(gridDim.x / n_qblocks), blk, bh);
+    const int qb = n_qblocks - 1 - blk;
     const int b = bh / H, h = bh % H;
     const int q0 = qb * BQ;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int lr = lane & 31, g = lane >> 5;
     const int qi = q0 + wave * 32 + lr;
-    const int wave_qmax = q0 + wave * 32 + 31;
+    const int wave_qmin = q0 + wave * 32, wave_qmax = wave_qmin + 31;
     const int64_t row_base = (int64_t)b * S;
 
     // This lane's query, pre-scaled into the log2 domain: Q[i][32g + s].
@@ -112,7 +122,10 @@ __global__ __launch_bounds__(256, 2) void attn_mfma_kernel(const float *__restri
             const int idx = tid + it * 256;
             const int key = idx / (DH / 4), c4 = idx % (DH / 4);
             *reinterpret_cast<float4 *>(&Ks[buf][key][4 * c4]) = pk[it];
-            *reinterpret_cast<float4 *>(&Vs[buf][key][4 * c4]) = pv[it];
+            Vt[buf][4 * c4 + 0][key] = pv[it].x;
+            Vt[buf][4 * c4 + 1][key] = pv[it].y;
+            Vt[buf][4 * c4 + 2][key] = pv[it].z;
+            Vt[buf][4 * c4 + 3][key] = pv[it].w;
         }
     };
 
@@ -127,17 +140,25 @@ __global__ __launch_bounds__(256, 2) void attn_mfma_kernel(const float *__restri
 
         f32x16 sacc[BKV / 32];
         bool active[BKV / 32];
+        // A tile with every key in range and (causal) at or below every query
+        // of the wavefront needs no mask.  Queries ≥ S are padding: their
+        // scores are computed but never stored.
+        const bool full = __builtin_amdgcn_readfirstlane(
+            j0 + BKV <= S && (!causal || j0 + BKV - 1 <= wave_qmin));
 #pragma unroll
         for (int kb = 0; kb < BKV / 32; ++kb) {
             const int jb = j0 + kb * 32;
-            active[kb] = jb < S && (!causal || jb <= wave_qmax);  // wave-uniform
+            active[kb] = __builtin_amdgcn_readfirstlane(jb < S && (!causal || jb <= wave_qmax));
 #pragma unroll
             for (int r = 0; r < 16; ++r) sacc[kb][r] = 0.f;
             if (active[kb]) {
                 const float *krow = &Ks[buf][kb * 32 + lr][32 * g];
+                float4 kf[8];
+#pragma unroll
+                for (int c = 0; c < 8; ++c) kf[c] = *reinterpret_cast<const float4 *>(krow + 4 * c);
 #pragma unroll
                 for (int c = 0; c < 8; ++c) {
-                    const float4 kv = *reinterpret_cast<const float4 *>(krow + 4 * c);
+                    const float4 kv = kf[c];
                     sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.x, qf[4 * c + 0], sacc[kb], 0, 0, 0);
                     sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.y, qf[4 * c + 1], sacc[kb], 0, 0, 0);
                     sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.z, qf[4 * c + 2], sacc[kb], 0, 0, 0);
@@ -146,30 +167,35 @@ __global__ __launch_bounds__(256, 2) void attn_mfma_kernel(const float *__restri
             }
         }
 
-        // Mask and running max for this lane's query.  Entry r of block kb
-        // is key j0 + 32kb + 8(r/4) + 4g + r%4.
-        float mx = -INFINITY;
+        // Mask (edge tiles only) and running max for this lane's query.
+        // Entry r of block kb is key j0 + 32kb + 8(r/4) + 4g + r%4.
+        float mx = kMasked;
+        if (full) {
 #pragma unroll
-        for (int kb = 0; kb < BKV / 32; ++kb)
+            for (int kb = 0; kb < BKV / 32; ++kb)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int j = j0 + kb * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-                const bool ok = active[kb] && j < S && (!causal || j <= qi);
-                const float sv = ok ? sacc[kb][r] : -INFINITY;
-                sacc[kb][r] = sv;
-                mx = fmaxf(mx, sv);
-            }
+                for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kb][r]);
+        } else {
+#pragma unroll
+            for (int kb = 0; kb < BKV / 32; ++kb)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int j = j0 + kb * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+                    const bool ok = active[kb] && j < S && (!causal || j <= qi);
+                    const float sv = ok ? sacc[kb][r] : kMasked;
+                    sacc[kb][r] = sv;
+                    mx = fmaxf(mx, sv);
+                }
+        }
         mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        const float m_new = fmaxf(m, mx);
-        // All keys so far masked (only possible for padded queries ≥ S).
-        const bool none = m_new == -INFINITY;
-        const float factor = none ? 1.f : exp2f(m - m_new);
+        const float m_new = fmaxf(m, mx);  // finite from the first tile on
+        const float factor = fast_exp2(m - m_new);
         float psum = 0.f;
 #pragma unroll
         for (int kb = 0; kb < BKV / 32; ++kb)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const float p = none ? 0.f : exp2f(sacc[kb][r] - m_new);
+                const float p = fast_exp2(sacc[kb][r] - m_new);
                 sacc[kb][r] = p;
                 psum += p;
             }
@@ -182,18 +208,26 @@ __global__ __launch_bounds__(256, 2) void attn_mfma_kernel(const float *__restri
             for (int r = 0; r < 16; ++r) oacc[db][r] *= factor;
 
         // Oᵀ += Vᵀ·Pᵀ: step s feeds key 32kb + 8(s/4) + 4g + s%4 from lane
-        // half g — the key whose probability this lane holds in sacc[kb][s].
+        // half g — the key whose probability this lane holds in sacc[kb][s];
+        // steps 4s4 … 4s4+3 read their four V values as one float4.
 #pragma unroll
         for (int kb = 0; kb < BKV / 32; ++kb) {
             if (!active[kb]) continue;
+            float4 vf[4][DH / 32];
 #pragma unroll
-            for (int s = 0; s < 16; ++s) {
-                const int jl = kb * 32 + 8 * (s >> 2) + 4 * g + (s & 3);
+            for (int s4 = 0; s4 < 4; ++s4)
 #pragma unroll
                 for (int db = 0; db < DH / 32; ++db)
-                    oacc[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(Vs[buf][jl][db * 32 + lr],
-                                                                    sacc[kb][s], oacc[db], 0, 0, 0);
-            }
+                    vf[s4][db] = *reinterpret_cast<const float4 *>(&Vt[buf][db * 32 + lr][kb * 32 + 8 * s4 + 4 * g]);
+#pragma unroll
+            for (int s4 = 0; s4 < 4; ++s4)
+#pragma unroll
+                for (int db = 0; db < DH / 32; ++db) {
+                    oacc[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(vf[s4][db].x, sacc[kb][4 * s4 + 0], oacc[db], 0, 0, 0);
+                    oacc[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(vf[s4][db].y, sacc[kb][4 * s4 + 1], oacc[db], 0, 0, 0);
+                    oacc[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(vf[s4][db].z, sacc[kb][4 * s4 + 2], oacc[db], 0, 0, 0);
+                    oacc[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(vf[s4][db].w, sacc[kb][4 * s4 + 3], oacc[db], 0, 0, 0);
+                }
         }
         if (more) sstore(buf ^ 1);
         __syncthreads();

@@ -28,6 +28,9 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr float kLog2e = 1.4426950408889634f;
 
+// 2^x on the hardware exp unit (v_exp_f32; below 2^-126 flushes to zero).
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
 // D[row·H + h] = Σ_d dO·O over head h.
 __global__ __launch_bounds__(256) void attn_dot_kernel(const float *__restrict__ o,
                                                        const float *__restrict__ dout, int64_t ldo,
@@ -52,15 +55,19 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkdv_kernel(
     const float *__restrict__ Dv, float *__restrict__ dk, float *__restrict__ dv, int64_t ldd, int S,
     int H, float qscale, float scale, int causal, int n_kblocks) {
     static_assert(DH == 64, "written for d_head = 64");
-    constexpr int BKEY = 128, BQ = 64, LDQ = DH + 4;
+    constexpr int BKEY = 128, BQ = 64, LDQ = DH + 4, LDT = BQ + 4;
     constexpr int IT = BQ * DH / 4 / 256;
+    // Q and dO tiles row-major (the S and dP products read rows along d)
+    // and transposed (dV and dK read four consecutive queries per float4).
     __shared__ float Qs[BQ][LDQ];
     __shared__ float Os[BQ][LDQ];
+    __shared__ float Qt[DH][LDT];
+    __shared__ float Ot[DH][LDT];
     __shared__ float Ls[BQ], Ds[BQ];
 
-    const int bid = blockIdx.x;
-    const int kb = bid % n_kblocks;  // low key blocks see the most queries: first
-    const int bh = bid / n_kblocks;
+    // Low key blocks see the most queries: first, spread over the XCDs.
+    int kb, bh;
+    split_bh_block(blockIdx.x, n_kblocks, (int)(gridDim.x / n_kblocks), kb, bh);
     const int b = bh / H, h = bh % H;
     const int k0 = kb * BKEY;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -89,32 +96,62 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkdv_kernel(
 #pragma unroll
         for (int r = 0; r < 16; ++r) dka[db][r] = dva[db][r] = 0.f;
 
-    const int q_start = causal ? (k0 / BQ) * BQ : 0;
-    for (int q0 = q_start; q0 < S; q0 += BQ) {
+    // The next Q/dO tile is loaded into registers while the current one is
+    // consumed from LDS.
+    float4 pq[IT], po[IT];
+    float pl = 0.f, pd = 0.f;
+    auto gload = [&](int q0) {
 #pragma unroll
         for (int it = 0; it < IT; ++it) {
             const int idx = tid + it * 256;
             const int r = idx / (DH / 4), c4 = idx % (DH / 4);
             const int qi = q0 + r;
-            float4 a = make_float4(0.f, 0.f, 0.f, 0.f), d = a;
+            pq[it] = make_float4(0.f, 0.f, 0.f, 0.f);
+            po[it] = pq[it];
             if (qi < S) {
-                a = *reinterpret_cast<const float4 *>(q + (row_base + qi) * ld + (int64_t)h * DH + 4 * c4);
-                d = *reinterpret_cast<const float4 *>(dout + (row_base + qi) * ldo + (int64_t)h * DH + 4 * c4);
+                pq[it] = *reinterpret_cast<const float4 *>(q + (row_base + qi) * ld + (int64_t)h * DH + 4 * c4);
+                po[it] = *reinterpret_cast<const float4 *>(dout + (row_base + qi) * ldo + (int64_t)h * DH + 4 * c4);
             }
-            *reinterpret_cast<float4 *>(&Qs[r][4 * c4]) = a;
-            *reinterpret_cast<float4 *>(&Os[r][4 * c4]) = d;
         }
         if (tid < BQ) {
             const int qi = q0 + tid;
-            Ls[tid] = qi < S ? lse[(row_base + qi) * H + h] : 0.f;
-            Ds[tid] = qi < S ? Dv[(row_base + qi) * H + h] : 0.f;
+            pl = qi < S ? lse[(row_base + qi) * H + h] : 0.f;
+            pd = qi < S ? Dv[(row_base + qi) * H + h] : 0.f;
         }
+    };
+    auto sstore = [&]() {
+#pragma unroll
+        for (int it = 0; it < IT; ++it) {
+            const int idx = tid + it * 256;
+            const int r = idx / (DH / 4), c4 = idx % (DH / 4);
+            *reinterpret_cast<float4 *>(&Qs[r][4 * c4]) = pq[it];
+            *reinterpret_cast<float4 *>(&Os[r][4 * c4]) = po[it];
+            Qt[4 * c4 + 0][r] = pq[it].x; Qt[4 * c4 + 1][r] = pq[it].y;
+            Qt[4 * c4 + 2][r] = pq[it].z; Qt[4 * c4 + 3][r] = pq[it].w;
+            Ot[4 * c4 + 0][r] = po[it].x; Ot[4 * c4 + 1][r] = po[it].y;
+            Ot[4 * c4 + 2][r] = po[it].z; Ot[4 * c4 + 3][r] = po[it].w;
+        }
+        if (tid < BQ) {
+            Ls[tid] = pl;
+            Ds[tid] = pd;
+        }
+    };
+
+    const int q_start = causal ? (k0 / BQ) * BQ : 0;
+    if (q_start < S) gload(q_start);
+    for (int q0 = q_start; q0 < S; q0 += BQ) {
+        sstore();
         __syncthreads();
+        if (q0 + BQ < S) gload(q0 + BQ);
 #pragma unroll
         for (int qb = 0; qb < BQ / 32; ++qb) {
             const int qs0 = q0 + qb * 32;
-            const bool active = qs0 < S && (!causal || qs0 + 31 >= wave_kmin);  // wave-uniform
+            const bool active = __builtin_amdgcn_readfirstlane(qs0 < S && (!causal || qs0 + 31 >= wave_kmin));
             if (!active) continue;
+            // No mask needed: every query of the 32 and every key of the
+            // wavefront in range, and (causal) every key at or before every query.
+            const bool full = __builtin_amdgcn_readfirstlane(qs0 + 31 < S && wave_kmin + 31 < S &&
+                                                             (!causal || wave_kmin + 31 <= qs0));
             f32x16 sa, pa;
 #pragma unroll
             for (int r = 0; r < 16; ++r) sa[r] = pa[r] = 0.f;
@@ -138,19 +175,29 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkdv_kernel(
             for (int r = 0; r < 16; ++r) {
                 const int il = qb * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
                 const int qi = q0 + il;
-                const bool ok = qi < S && kj < S && (!causal || kj <= qi);
-                const float p = ok ? exp2f(sa[r] * qscale - Ls[il]) : 0.f;
+                const bool ok = full || (qi < S && kj < S && (!causal || kj <= qi));
+                const float p = ok ? fast_exp2(sa[r] * qscale - Ls[il]) : 0.f;
                 pa[r] = p * (pa[r] - Ds[il]);
                 sa[r] = p;
             }
             // dVᵀ[d][j] += Σ_i dO[i][d]·P[i][j];  dKᵀ[d][j] += Σ_i Q[i][d]·dS[i][j]
+            // Step s uses query qb·32 + 8(s/4) + 4g + s%4: steps 4s4…4s4+3
+            // read four consecutive queries of the transposed tiles.
 #pragma unroll
-            for (int s = 0; s < 16; ++s) {
-                const int il = qb * 32 + 8 * (s >> 2) + 4 * g + (s & 3);
+            for (int s4 = 0; s4 < 4; ++s4) {
+                const int il0 = qb * 32 + 8 * s4 + 4 * g;
 #pragma unroll
                 for (int db = 0; db < DH / 32; ++db) {
-                    dva[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(Os[il][db * 32 + lr], sa[s], dva[db], 0, 0, 0);
-                    dka[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(Qs[il][db * 32 + lr], pa[s], dka[db], 0, 0, 0);
+                    const float4 ov = *reinterpret_cast<const float4 *>(&Ot[db * 32 + lr][il0]);
+                    const float4 qv = *reinterpret_cast<const float4 *>(&Qt[db * 32 + lr][il0]);
+                    dva[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(ov.x, sa[4 * s4 + 0], dva[db], 0, 0, 0);
+                    dka[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(qv.x, pa[4 * s4 + 0], dka[db], 0, 0, 0);
+                    dva[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(ov.y, sa[4 * s4 + 1], dva[db], 0, 0, 0);
+                    dka[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(qv.y, pa[4 * s4 + 1], dka[db], 0, 0, 0);
+                    dva[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(ov.z, sa[4 * s4 + 2], dva[db], 0, 0, 0);
+                    dka[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(qv.z, pa[4 * s4 + 2], dka[db], 0, 0, 0);
+                    dva[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(ov.w, sa[4 * s4 + 3], dva[db], 0, 0, 0);
+                    dka[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(qv.w, pa[4 * s4 + 3], dka[db], 0, 0, 0);
                 }
             }
         }
@@ -180,20 +227,23 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(
     const float *__restrict__ Dv, float *__restrict__ dq, int64_t ldd, int S, int H, float qscale,
     float scale, int causal, int n_qblocks) {
     static_assert(DH == 64, "written for d_head = 64");
-    constexpr int BQ = 128, BKV = 64, LDK = DH + 4;
+    constexpr int BQ = 128, BKV = 64, LDK = DH + 4, LDT = BKV + 4;
     constexpr int KV_IT = BKV * DH / 4 / 256;
+    // K and V row-major (Sᵀ and dPᵀ read rows along d); K also transposed,
+    // so dQ reads four consecutive keys per float4.
     __shared__ float Ks[1][BKV][LDK];
     __shared__ float Vs[1][BKV][LDK];
+    __shared__ float Kt[DH][LDT];
 
-    const int bid = blockIdx.x;
-    const int qb = n_qblocks - 1 - (bid % n_qblocks);
-    const int bh = bid / n_qblocks;
+    int blk, bh;
+    split_bh_block(blockIdx.x, n_qblocks, (int)(gridDim.x / n_qblocks), blk, bh);
+    const int qb = n_qblocks - 1 - blk;
     const int b = bh / H, h = bh % H;
     const int q0 = qb * BQ;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int lr = lane & 31, g = lane >> 5;
     const int qi = q0 + wave * 32 + lr;
-    const int wave_qmax = q0 + wave * 32 + 31;
+    const int wave_qmin = q0 + wave * 32, wave_qmax = wave_qmin + 31;
     const int64_t row_base = (int64_t)b * S;
 
     float qf[32], of[32];
@@ -222,27 +272,45 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(
 
     const int kv_end = causal ? min(S, q0 + BQ) : S;
     const int ntiles = (kv_end + BKV - 1) / BKV;
+    // The next K/V tile is loaded into registers while the current one is
+    // consumed from LDS.
+    float4 pk[KV_IT], pv[KV_IT];
+    auto gload = [&](int t) {
+#pragma unroll
+        for (int it = 0; it < KV_IT; ++it) {
+            const int idx = tid + it * 256;
+            const int kr = idx / (DH / 4), c4 = idx % (DH / 4);
+            const int key = t * BKV + kr;
+            pk[it] = make_float4(0.f, 0.f, 0.f, 0.f);
+            pv[it] = pk[it];
+            if (key < S) {
+                const int64_t off = (row_base + key) * ld + (int64_t)h * DH + 4 * c4;
+                pk[it] = *reinterpret_cast<const float4 *>(k + off);
+                pv[it] = *reinterpret_cast<const float4 *>(v + off);
+            }
+        }
+    };
+    if (ntiles > 0) gload(0);
     for (int t = 0; t < ntiles; ++t) {
         const int buf = 0;
 #pragma unroll
         for (int it = 0; it < KV_IT; ++it) {
             const int idx = tid + it * 256;
             const int kr = idx / (DH / 4), c4 = idx % (DH / 4);
-            const int key = t * BKV + kr;
-            float4 a = make_float4(0.f, 0.f, 0.f, 0.f), bb = a;
-            if (key < S) {
-                const int64_t off = (row_base + key) * ld + (int64_t)h * DH + 4 * c4;
-                a = *reinterpret_cast<const float4 *>(k + off);
-                bb = *reinterpret_cast<const float4 *>(v + off);
-            }
-            *reinterpret_cast<float4 *>(&Ks[buf][kr][4 * c4]) = a;
-            *reinterpret_cast<float4 *>(&Vs[buf][kr][4 * c4]) = bb;
+            *reinterpret_cast<float4 *>(&Ks[buf][kr][4 * c4]) = pk[it];
+            *reinterpret_cast<float4 *>(&Vs[buf][kr][4 * c4]) = pv[it];
+            Kt[4 * c4 + 0][kr] = pk[it].x; Kt[4 * c4 + 1][kr] = pk[it].y;
+            Kt[4 * c4 + 2][kr] = pk[it].z; Kt[4 * c4 + 3][kr] = pk[it].w;
         }
         __syncthreads();
+        if (t + 1 < ntiles) gload(t + 1);
         const int j0 = t * BKV;
         for (int kb = 0; kb < BKV / 32; ++kb) {
             const int jb = j0 + kb * 32;
-            if (!(jb < S && (!causal || jb <= wave_qmax))) continue;  // wave-uniform
+            if (!__builtin_amdgcn_readfirstlane(jb < S && (!causal || jb <= wave_qmax))) continue;
+            // No mask: all 32 keys in range and (causal) none after any query of
+            // the wavefront.  Padded queries (≥ S) are never stored.
+            const bool full = __builtin_amdgcn_readfirstlane(jb + 31 < S && (!causal || jb + 31 <= wave_qmin));
             f32x16 sa, pa;
 #pragma unroll
             for (int r = 0; r < 16; ++r) sa[r] = pa[r] = 0.f;
@@ -266,18 +334,22 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int j = jb + 8 * (r >> 2) + 4 * g + (r & 3);
-                const bool ok = qi < S && j < S && (!causal || j <= qi);
-                const float p = ok ? exp2f(sa[r] - lse_i) : 0.f;
+                const bool ok = full || (qi < S && j < S && (!causal || j <= qi));
+                const float p = ok ? fast_exp2(sa[r] - lse_i) : 0.f;
                 pa[r] = p * (pa[r] - D_i);  // dSᵀ entry
             }
-            // dQᵀ[d][i] += Σ_j K[j][d]·dSᵀ[j][i]
+            // dQᵀ[d][i] += Σ_j K[j][d]·dSᵀ[j][i]; steps 4s4…4s4+3 take keys
+            // kb·32 + 8s4 + 4g + 0…3, one float4 of the transposed tile.
 #pragma unroll
-            for (int s = 0; s < 16; ++s) {
-                const int jl = kb * 32 + 8 * (s >> 2) + 4 * g + (s & 3);
+            for (int s4 = 0; s4 < 4; ++s4)
 #pragma unroll
-                for (int db = 0; db < DH / 32; ++db)
-                    dqa[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(Ks[buf][jl][db * 32 + lr], pa[s], dqa[db], 0, 0, 0);
-            }
+                for (int db = 0; db < DH / 32; ++db) {
+                    const float4 kv = *reinterpret_cast<const float4 *>(&Kt[db * 32 + lr][kb * 32 + 8 * s4 + 4 * g]);
+                    dqa[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.x, pa[4 * s4 + 0], dqa[db], 0, 0, 0);
+                    dqa[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.y, pa[4 * s4 + 1], dqa[db], 0, 0, 0);
+                    dqa[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.z, pa[4 * s4 + 2], dqa[db], 0, 0, 0);
+                    dqa[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.w, pa[4 * s4 + 3], dqa[db], 0, 0, 0);
+                }
         }
         __syncthreads();
     }

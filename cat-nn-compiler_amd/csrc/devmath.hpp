@@ -46,6 +46,18 @@ __device__ __forceinline__ int xcd_remap(int pid, int nblocks) {
     return (pid & 7) * (nblocks >> 3) + (pid >> 3);
 }
 
+// Block b of a launch over n_bh (batch, head) pairs × nb blocks each: its
+// block index `blk` (0 = the heaviest under a causal mask) and pair `bh`.
+// blk is the slowest-varying index, so all blocks of one weight are
+// launched before the lighter ones (longest first: the last blocks to start
+// are the shortest).  Blocks go to XCD b % 8 round-robin, and consecutive
+// blocks take different pairs, so every XCD receives every weight equally.
+__device__ __forceinline__ void split_bh_block(int b, int nb, int n_bh, int &blk, int &bh) {
+    (void)nb;
+    blk = b / n_bh;
+    bh = b - blk * n_bh;
+}
+
 // Grouped tile order: walk `group` row-tiles down a column of tiles before
 // moving right, so that blocks resident together reuse the same B panel
 // and a small set of A panels.
