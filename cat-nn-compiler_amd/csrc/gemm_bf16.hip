@@ -46,12 +46,13 @@ struct Cfg {
                   "load split");
 };
 
-using Cfg0 = Cfg<128, 128, 2, 2, 32>;  // 64 × 64 per wavefront
-using Cfg1 = Cfg<128, 256, 2, 2, 32>;  // 64 × 128 per wavefront
+// All with 64 × 64 per wavefront: wider wavefront tiles (64 × 128) ran
+// slower on the training shapes (one wavefront per SIMD at 270+ registers).
+using Cfg0 = Cfg<128, 128, 2, 2, 32>;
 using Cfg2 = Cfg<128, 128, 2, 2, 64>;
-using Cfg3 = Cfg<256, 128, 4, 2, 32>;  // 8 wavefronts of 64 × 64
+using Cfg3 = Cfg<256, 128, 4, 2, 32>;  // 8 wavefronts
 using Cfg4 = Cfg<256, 128, 4, 2, 64>;
-using Cfg5 = Cfg<128, 256, 2, 2, 64>;
+
 
 __device__ __forceinline__ float bf2f(bf16_t v) { return __uint_as_float((uint32_t)v << 16); }
 
@@ -125,7 +126,7 @@ __device__ __forceinline__ void epilogue(const GemmBf16Params &p, const f32x16 (
         }
 }
 
-template <class C, bool VEC, bool DUAL>
+template <class C, bool VEC, bool DUAL, int GRID>
 __device__ __forceinline__ void tile(bf16_t (*sa)[C::BM][C::LDT], bf16_t (*sb)[C::BN][C::LDT], const GemmBf16Params &p,
                                      const bf16_t *__restrict__ B, const bf16_t *__restrict__ B2, int row0,
                                      int row_end, int col0, int k_lo, int k_hi, float *__restrict__ C32) {
@@ -275,15 +276,22 @@ __device__ __forceinline__ void tile(bf16_t (*sa)[C::BM][C::LDT], bf16_t (*sb)[C
         epilogue<C, true, EPI_SWIGLU_FWD>(p, acc, wrow0, wcol0, row_end, C32);
         return;
     }
-    switch (p.epi) {
-        case EPI_LINEAR: epilogue<C, false, EPI_LINEAR>(p, acc, wrow0, wcol0, row_end, C32); break;
-        case EPI_GELU_BWD: epilogue<C, false, EPI_GELU_BWD>(p, acc, wrow0, wcol0, row_end, C32); break;
-        case EPI_SWIGLU_BWD: epilogue<C, false, EPI_SWIGLU_BWD>(p, acc, wrow0, wcol0, row_end, C32); break;
-        default: epilogue<C, false, EPI_STORE>(p, acc, wrow0, wcol0, row_end, C32);
+    // Each grid is built only with the epilogues the training step uses on it.
+    if constexpr (GRID == GRID_PLAIN) {
+        switch (p.epi) {
+            case EPI_LINEAR: epilogue<C, false, EPI_LINEAR>(p, acc, wrow0, wcol0, row_end, C32); break;
+            case EPI_GELU_BWD: epilogue<C, false, EPI_GELU_BWD>(p, acc, wrow0, wcol0, row_end, C32); break;
+            default: epilogue<C, false, EPI_STORE>(p, acc, wrow0, wcol0, row_end, C32);
+        }
+    } else if constexpr (GRID == GRID_ROWS) {
+        if (p.epi == EPI_SWIGLU_BWD) epilogue<C, false, EPI_SWIGLU_BWD>(p, acc, wrow0, wcol0, row_end, C32);
+        else epilogue<C, false, EPI_STORE>(p, acc, wrow0, wcol0, row_end, C32);
+    } else {
+        epilogue<C, false, EPI_STORE>(p, acc, wrow0, wcol0, row_end, C32);
     }
 }
 
-template <class C, bool VEC, bool DUAL>
+template <class C, bool VEC, bool DUAL, int GRID>
 __global__ __launch_bounds__(C::NT) void gemm_bf16_kernel(GemmBf16Params p) {
     extern __shared__ __align__(16) unsigned char smem[];
     auto sa = reinterpret_cast<bf16_t(*)[C::BM][C::LDT]>(smem);
@@ -291,20 +299,20 @@ __global__ __launch_bounds__(C::NT) void gemm_bf16_kernel(GemmBf16Params p) {
     const int bn_out = DUAL ? C::BN / 2 : C::BN;
     const int tiles_n = (p.N + bn_out - 1) / bn_out;
     const int lid = xcd_remap(blockIdx.x, gridDim.x);
-    if (p.grid == GRID_PLAIN) {
+    if constexpr (GRID == GRID_PLAIN) {
         const int tiles_m = (p.M + C::BM - 1) / C::BM;
         int tm, tn;
         grouped_tile(lid, tiles_m, tiles_n, 8, tm, tn);
-        tile<C, VEC, DUAL>(sa, sb, p, p.B, p.B2, tm * C::BM, p.M, tn * bn_out, 0, p.K, p.C32);
-    } else if (p.grid == GRID_ROWS) {
+        tile<C, VEC, DUAL, GRID>(sa, sb, p, p.B, p.B2, tm * C::BM, p.M, tn * bn_out, 0, p.K, p.C32);
+    } else if constexpr (GRID == GRID_ROWS) {
         // Tiles of the table are kRowTile rows; C::BM equals it for this grid.
         int tm, tn;
         grouped_tile(lid, p.max_tiles, tiles_n, 8, tm, tn);
         if (tm >= *p.n_tiles) return;
         const int e = p.tile_expert[tm];
         const int end = p.seg_counts ? p.seg_offsets[e] + p.seg_counts[e] : p.seg_offsets[e + 1];
-        tile<C, VEC, DUAL>(sa, sb, p, p.B_e[e], DUAL ? p.B2_e[e] : nullptr, p.tile_row0[tm], end,
-                           tn * bn_out, 0, p.K, p.C32);
+        tile<C, VEC, DUAL, GRID>(sa, sb, p, p.B_e[e], DUAL ? p.B2_e[e] : nullptr, p.tile_row0[tm], end,
+                                 tn * bn_out, 0, p.K, p.C32);
     } else {  // GRID_SEGK: expert e = blockIdx.y reduces over its own K segment
         const int tiles_m = (p.M + C::BM - 1) / C::BM;
         int tm, tn;
@@ -312,48 +320,65 @@ __global__ __launch_bounds__(C::NT) void gemm_bf16_kernel(GemmBf16Params p) {
         const int e = blockIdx.y;
         const int lo = p.seg_offsets[e];
         const int hi = p.seg_counts ? lo + p.seg_counts[e] : p.seg_offsets[e + 1];
-        tile<C, VEC, DUAL>(sa, sb, p, p.B, nullptr, tm * C::BM, p.M, tn * bn_out, lo, hi, p.C_e[e]);
+        tile<C, VEC, DUAL, GRID>(sa, sb, p, p.B, nullptr, tm * C::BM, p.M, tn * bn_out, lo, hi, p.C_e[e]);
     }
 }
 
 bool al16(const void *q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; }
 
-
 constexpr int kRowTile = 128;  // rows per tile of the grouped tile table (build_tiles)
 
-template <class C>
-void launch_cfg(hipStream_t s, const GemmBf16Params &p, bool vec, bool dual, unsigned gy) {
-    const int bn_out = dual ? C::BN / 2 : C::BN;
-    int64_t blocks;
-    if (p.grid == GRID_ROWS) {
-        // The tile table holds kRowTile-row tiles.
-        CATNN_REQUIRE(C::BM == kRowTile, CATNN_ERR_INVALID_ARGUMENT, "bf16 gemm: grouped rows need 128-row tiles");
-        blocks = (int64_t)p.max_tiles * ((p.N + bn_out - 1) / bn_out);
-    } else blocks = (int64_t)((p.M + C::BM - 1) / C::BM) * ((p.N + bn_out - 1) / bn_out);
-    if (blocks == 0) return;
-    CATNN_REQUIRE(blocks < (1ll << 31), CATNN_ERR_SHAPE_MISMATCH, "bf16 gemm: grid too large");
-    dim3 grid((unsigned)blocks, gy), block(C::NT);
+template <class C, int GRID, bool DUAL>
+void launch_kernel(hipStream_t s, const GemmBf16Params &p, bool vec, dim3 grid) {
     // Tiles above 64 KiB of LDS need the per-kernel opt-in (gfx950: 160 KiB per CU).
     static bool attr_set = false;
     if (!attr_set) {
-        CATNN_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_bf16_kernel<C, true, true>),
+        CATNN_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_bf16_kernel<C, true, DUAL, GRID>),
                                       hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS_BYTES));
-        CATNN_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_bf16_kernel<C, false, true>),
-                                      hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS_BYTES));
-        CATNN_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_bf16_kernel<C, true, false>),
-                                      hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS_BYTES));
-        CATNN_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_bf16_kernel<C, false, false>),
+        CATNN_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_bf16_kernel<C, false, DUAL, GRID>),
                                       hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS_BYTES));
         attr_set = true;
     }
-    if (dual) {
-        if (vec) gemm_bf16_kernel<C, true, true><<<grid, block, C::LDS_BYTES, s>>>(p);
-        else gemm_bf16_kernel<C, false, true><<<grid, block, C::LDS_BYTES, s>>>(p);
-    } else {
-        if (vec) gemm_bf16_kernel<C, true, false><<<grid, block, C::LDS_BYTES, s>>>(p);
-        else gemm_bf16_kernel<C, false, false><<<grid, block, C::LDS_BYTES, s>>>(p);
-    }
+    if (vec) gemm_bf16_kernel<C, true, DUAL, GRID><<<grid, dim3(C::NT), C::LDS_BYTES, s>>>(p);
+    else gemm_bf16_kernel<C, false, DUAL, GRID><<<grid, dim3(C::NT), C::LDS_BYTES, s>>>(p);
     CATNN_HIP(hipGetLastError());
+}
+
+// Grids and epilogues each configuration is built with: plain (store,
+// linear, GELU adjoint) and per-expert K segments (store) for all; grouped
+// rows (store, SwiGLU adjoint, and with DUAL the SwiGLU forward) for the
+// 128-row tiles.
+template <class C, bool DUAL_OK>
+void launch_cfg(hipStream_t s, const GemmBf16Params &p, bool vec, bool dual, unsigned gy) {
+    CATNN_REQUIRE(DUAL_OK || !dual, CATNN_ERR_INVALID_ARGUMENT, "bf16 gemm: SwiGLU forward needs tile configuration 0");
+    const bool ok_epi = p.grid == GRID_PLAIN ? (p.epi == EPI_STORE || p.epi == EPI_LINEAR || p.epi == EPI_GELU_BWD)
+                        : p.grid == GRID_ROWS ? (p.epi == EPI_STORE || p.epi == EPI_SWIGLU_FWD || p.epi == EPI_SWIGLU_BWD)
+                                              : p.epi == EPI_STORE;
+    CATNN_REQUIRE(ok_epi, CATNN_ERR_INVALID_ARGUMENT, "bf16 gemm: epilogue not built for this grid");
+    const int bn_out = dual ? C::BN / 2 : C::BN;
+    int64_t blocks;
+    if (p.grid == GRID_ROWS) blocks = (int64_t)p.max_tiles * ((p.N + bn_out - 1) / bn_out);
+    else blocks = (int64_t)((p.M + C::BM - 1) / C::BM) * ((p.N + bn_out - 1) / bn_out);
+    if (blocks == 0) return;
+    CATNN_REQUIRE(blocks < (1ll << 31), CATNN_ERR_SHAPE_MISMATCH, "bf16 gemm: grid too large");
+    const dim3 grid((unsigned)blocks, gy);
+    if (p.grid == GRID_PLAIN) {
+        launch_kernel<C, GRID_PLAIN, false>(s, p, vec, grid);
+    } else if (p.grid == GRID_SEGK) {
+        launch_kernel<C, GRID_SEGK, false>(s, p, vec, grid);
+    } else {
+        if constexpr (C::BM == kRowTile) {
+            if constexpr (DUAL_OK) {
+                if (dual) {
+                    launch_kernel<C, GRID_ROWS, true>(s, p, vec, grid);
+                    return;
+                }
+            }
+            launch_kernel<C, GRID_ROWS, false>(s, p, vec, grid);
+        } else {
+            fail(CATNN_ERR_INVALID_ARGUMENT, "bf16 gemm: grouped rows need 128-row tiles");
+        }
+    }
 }
 
 }  // namespace
@@ -386,12 +411,10 @@ void gemm_bf16_launch_cfg(hipStream_t s, const GemmBf16Params &p, int cfg) {
         }
     }
     switch (cfg) {
-        case 0: launch_cfg<Cfg0>(s, p, vec, dual, gy); break;
-        case 1: launch_cfg<Cfg1>(s, p, vec, dual, gy); break;
-        case 2: launch_cfg<Cfg2>(s, p, vec, dual, gy); break;
-        case 3: launch_cfg<Cfg3>(s, p, vec, dual, gy); break;
-        case 4: launch_cfg<Cfg4>(s, p, vec, dual, gy); break;
-        case 5: launch_cfg<Cfg5>(s, p, vec, dual, gy); break;
+        case 0: launch_cfg<Cfg0, true>(s, p, vec, dual, gy); break;
+        case 2: launch_cfg<Cfg2, false>(s, p, vec, dual, gy); break;
+        case 3: launch_cfg<Cfg3, false>(s, p, vec, dual, gy); break;
+        case 4: launch_cfg<Cfg4, false>(s, p, vec, dual, gy); break;
         default: fail(CATNN_ERR_INVALID_ARGUMENT, "bf16 gemm: unknown tile configuration");
     }
 }
@@ -402,7 +425,9 @@ void gemm_bf16_launch_cfg(hipStream_t s, const GemmBf16Params &p, int cfg) {
 // are one to four (8192×1024×12288: 665/917/883), 128×128 with BK 64 below
 // that (4096×1024×8192: 385/510/613).  Grouped-row grids need 128-row tiles.
 void gemm_bf16_launch(hipStream_t s, const GemmBf16Params &p) {
-    int cfg = 2;
+    // The SwiGLU epilogues (two outputs per element) run best on the
+    // 128×128×32 tile (config-5 expert GEMMs: 442 vs 545 µs forward).
+    int cfg = p.epi == EPI_SWIGLU_FWD || p.epi == EPI_SWIGLU_BWD ? 0 : 2;
     if (p.grid != GRID_ROWS && p.epi != EPI_SWIGLU_FWD) {
         const int64_t t3 = (int64_t)((p.M + 255) / 256) * ((p.N + 127) / 128) *
                            (p.grid == GRID_SEGK ? p.n_experts : 1);

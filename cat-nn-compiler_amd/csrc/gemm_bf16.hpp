@@ -69,7 +69,7 @@ struct GemmBf16Params {
 };
 
 void gemm_bf16_launch(hipStream_t s, const GemmBf16Params &p);
-// The same with a fixed tile configuration (0..5, see gemm_bf16.hip).
+// The same with a fixed tile configuration (0, 2, 3 or 4; see gemm_bf16.hip).
 void gemm_bf16_launch_cfg(hipStream_t s, const GemmBf16Params &p, int cfg);
 int gemm_bf16_tile_rows();
 
