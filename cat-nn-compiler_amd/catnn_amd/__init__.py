@@ -10,13 +10,14 @@ from .arena import ArenaAlloc, BufferReq, arena_conflict, place_arena
 from .device import (Device, DeviceBuffer, DeviceHandler, Program, eval_graph_hip)
 from .ir import (FLAG_CAUSAL, FusionGroup, IrEdge, IrGraph, IrNode, OpenOp, Tensor, TensorType)
 from .train import Trainer
+from .irjson import CGraph, to_serde_json
 from .spec import (Architecture, NetworkSpec, lower_architecture, mlp_spec, parse_catnn,
                    propose_fusions, to_architecture, transformer_block_spec)
 
 __all__ = [
-    "ArenaAlloc", "Architecture", "BufferReq", "CatError", "Device", "DeviceBuffer",
+    "ArenaAlloc", "Architecture", "BufferReq", "CGraph", "CatError", "Device", "DeviceBuffer",
     "DeviceHandler", "FLAG_CAUSAL", "FusionGroup", "IrEdge", "IrGraph", "IrNode", "LIB_PATH",
     "NetworkSpec", "OpenOp", "Program", "STATUS_NAMES", "Tensor", "TensorType", "Trainer",
     "arena_conflict", "eval_graph_hip", "lib", "lower_architecture", "mlp_spec", "parse_catnn",
-    "place_arena", "propose_fusions", "to_architecture", "transformer_block_spec",
+    "place_arena", "propose_fusions", "to_architecture", "to_serde_json", "transformer_block_spec",
 ]

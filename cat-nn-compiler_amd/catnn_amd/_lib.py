@@ -100,6 +100,8 @@ SIGNATURES = {
     "catnn_graph_add_output": [_VP, ctypes.c_uint32],
     "catnn_graph_add_fusion": [_VP, ctypes.POINTER(ctypes.c_char_p), _I32],
     "catnn_graph_topo": [_VP, ctypes.POINTER(ctypes.c_uint32), _I32, _PI32],
+    "catnn_graph_from_json": [ctypes.c_char_p, _U64, ctypes.POINTER(_F), _U64, ctypes.POINTER(_VP)],
+    "catnn_graph_to_json": [_VP, _I32, ctypes.c_char_p, _U64, _PU64, ctypes.POINTER(_F), _U64, _PU64],
     "catnn_tensor_lcg": [_U64, ctypes.POINTER(ctypes.c_float), _I64],
     "catnn_tensor_checksum": [ctypes.POINTER(ctypes.c_float), _I64, _PU64],
     "catnn_hip_device_count": [_PI32],

@@ -191,6 +191,14 @@ class DeviceHandler:
         return self.device.events()
 
 
+def graph_handle(graph):
+    """(catnn_graph handle, whether the caller frees it) for an IrGraph or
+    a backend-held graph (irjson.CGraph)."""
+    if hasattr(graph, "handle") and not isinstance(graph, IrGraph):
+        return graph.handle, False
+    return graph.to_c(), True
+
+
 @dataclass
 class ProgramIO:
     in_ptr: int
@@ -206,12 +214,13 @@ class Program:
         self.device = device
         self.graph = graph
         self.out_ty: Optional[TensorType] = None
-        h = graph.to_c()
+        h, owned = graph_handle(graph)
         self.handle = VP()
         try:
             check(lib.catnn_hip_install(device.handle, h, ctypes.byref(self.handle)))
         finally:
-            lib.catnn_graph_free(h)
+            if owned:
+                lib.catnn_graph_free(h)
         device._adopt(self)
 
     def forward(self, x: Optional[Tensor]) -> Tensor:

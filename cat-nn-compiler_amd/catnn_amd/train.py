@@ -15,7 +15,7 @@ import numpy as np
 
 from ._lib import CArenaAlloc, check, lib
 from .arena import ArenaAlloc
-from .device import Device
+from .device import Device, graph_handle
 from .ir import IrGraph, Tensor, ctensor
 
 _FP = ctypes.POINTER(ctypes.c_float)
@@ -26,13 +26,14 @@ class Trainer:
         self.device = device
         self.graph = graph
         self.lr = lr
-        h = graph.to_c()
+        h, owned = graph_handle(graph)
         self.handle = ctypes.c_void_p()
         try:
             check(lib.catnn_hip_train_install(device.handle, h, ctypes.c_float(lr),
                                               ctypes.byref(self.handle)))
         finally:
-            lib.catnn_graph_free(h)
+            if owned:
+                lib.catnn_graph_free(h)
         device._adopt(self)
 
     def set_batch(self, x: Tensor, target: Tensor):

@@ -197,6 +197,22 @@ int catnn_graph_add_output(catnn_graph *g, uint32_t id);
 /* `Realization.fusions` entry (FusionGroup, realization.rs:40-45): the named
  * ops run as one kernel when they are placed on the same device. */
 int catnn_graph_add_fusion(catnn_graph *g, const char *const *op_names, int32_t n);
+/* Builds a graph from the reference's serde JSON of `IrGraph`
+ * (crates/catnn-compile/src/ir.rs:13-41 serialised with serde_json, as the
+ * control plane ships it, dist.rs), replacing serde_json::from_slice on the
+ * member side.  A parameter whose "data" is [] takes its numel floats from
+ * `blob` (node order, then port order; blob_floats must match exactly), so
+ * large parameter sets need not pass through the 64 MiB frame.  Also reads
+ * "causal": true inside "attention" and a top-level "fusions" list.  Parse
+ * errors are CATNN_ERR_PARSE with the byte offset. */
+int catnn_graph_from_json(const char *json, uint64_t len, const float *blob, uint64_t blob_floats,
+                          catnn_graph **out);
+/* The inverse (serde_json::to_vec of the same IrGraph): writes the JSON to
+ * buf (NUL-terminated when cap > *len; call with buf = NULL for the size)
+ * and, unless inline_params, every parameter to `blob` with "data": [].
+ * *blob_floats receives the blob length. */
+int catnn_graph_to_json(const catnn_graph *g, int32_t inline_params, char *buf, uint64_t cap,
+                        uint64_t *len, float *blob, uint64_t blob_cap, uint64_t *blob_floats);
 /* Kahn order as `IrGraph::topo` (ir.rs:67-92); cycles → CATNN_ERR_WIRING. */
 int catnn_graph_topo(const catnn_graph *g, uint32_t *order, int32_t cap, int32_t *n);
 

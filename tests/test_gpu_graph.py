@@ -220,3 +220,36 @@ def test_program_arena_aliases_dead_activations(device):
     assert reserved < sum(a.bytes for a in allocs)
     assert {a.id for a in acts} == {"act:0", "act:2", "act:4", "act:5"}
     prog.free()
+
+
+def test_graph_from_serde_json_runs(device):
+    # The hand-written serde form of a Linear(4→3, bias) → ReLU graph.
+    import json
+
+    from catnn_amd import CGraph
+
+    text = open(os.path.join(GOLDEN, "mlp_ir.json")).read()
+    doc = json.loads(text)
+    w = np.array(doc["nodes"]["1"]["params"]["w"]["data"], np.float32).reshape(4, 3)
+    b = np.array(doc["nodes"]["1"]["params"]["b"]["data"], np.float32)
+    x = Tensor.lcg(TensorType.f32([2, 4]), 5)
+    got = Program(device, CGraph.from_json(text)).forward(x).numpy()
+    want = oracle.relu(oracle.linear(x.numpy(), w, b))
+    assert rel_l2(got, want) < TOL
+
+
+def test_json_blob_graph_matches_the_ir_graph(device):
+    from catnn_amd import CGraph, Trainer, to_serde_json
+
+    w = configs.config3(batch=1, seq=64, d=128, heads=2, ffn=256, causal=True)
+    lean, blob = to_serde_json(w.graph, inline=False)
+    cg = CGraph.from_json(lean, blob)
+    a = Program(device, cg).forward(w.x).numpy()
+    b = Program(device, w.graph).forward(w.x).numpy()
+    assert np.array_equal(a, b)
+    tgt = Tensor(w.x.ty, np.zeros(w.x.ty.numel(), np.float32))
+    t1, t2 = Trainer(device, cg, 0.05), Trainer(device, w.graph, 0.05)
+    t1.set_batch(w.x, tgt)
+    t2.set_batch(w.x, tgt)
+    assert t1.step() == t2.step()
+    assert np.array_equal(t1.grad(5, "w", (128, 256)), t2.grad(5, "w", (128, 256)))
