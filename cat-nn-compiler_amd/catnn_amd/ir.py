@@ -181,6 +181,37 @@ class OpenOp:
         return OpenOp("residual_add")
 
     @staticmethod
+    def rms_norm(eps_e6: int = 1):
+        return OpenOp("rms_norm", (eps_e6,))
+
+    @staticmethod
+    def embedding(vocab: int, hidden: int):
+        return OpenOp("embedding", (vocab, hidden))
+
+    @staticmethod
+    def gqa_attention(n_heads: int, n_kv_heads: int, head_dim: int, d_model: int,
+                      sliding_window=None, rope_theta: int = 10000):
+        """sliding_window None (Option::None) is stored as −1."""
+        return OpenOp("gqa_attention", (n_heads, n_kv_heads, head_dim, d_model,
+                                        -1 if sliding_window is None else sliding_window, rope_theta))
+
+    @staticmethod
+    def swiglu(hidden: int, intermediate: int):
+        return OpenOp("swiglu", (hidden, intermediate))
+
+    @staticmethod
+    def router(n_experts: int, top_k: int):
+        return OpenOp("router", (n_experts, top_k))
+
+    @staticmethod
+    def lm_head(hidden: int, vocab: int):
+        return OpenOp("lm_head", (hidden, vocab))
+
+    @staticmethod
+    def mix():
+        return OpenOp("mix")
+
+    @staticmethod
     def moe(n_experts: int, top_k: int, hidden: int, intermediate: int):
         return OpenOp("moe", (n_experts, top_k, hidden, intermediate))
 

@@ -51,7 +51,12 @@ def _op(op):
         return {name: {"out": [int(d) for d in op.fields]}}
     body = {}
     for f, v in zip(fields, op.fields):
-        body[f] = bool(v) if (op.kind == "linear" and f == "bias") else int(v)
+        if op.kind == "linear" and f == "bias":
+            body[f] = bool(v)
+        elif op.kind == "gqa_attention" and f == "sliding_window" and v < 0:
+            body[f] = None  # Option::None
+        else:
+            body[f] = int(v)
     if op.kind == "attention" and op.flags & 1:
         body["causal"] = True
     return {name: body}

@@ -505,6 +505,118 @@ int orc_arena_conflict(const uint64_t *bytes, const uint64_t *offsets, const uin
     return 0;
 }
 
+// ---------------------------------------------------------- Mixtral ops
+// moe::rmsnorm, moe.rs:17-32: y = x · 1/sqrt(Σx²/n + eps) · w per row.
+void orc_rmsnorm(const float *x, const float *w, int64_t rows, int64_t cols, float eps, float *y) {
+    for (int64_t r = 0; r < rows; ++r) {
+        const float *row = x + r * cols;
+        float ss = 0.0f;
+        for (int64_t i = 0; i < cols; ++i) ss += row[i] * row[i];
+        const float mean_sq = ss / (float)cols;
+        const float inv = 1.0f / std::sqrt(mean_sq + eps);
+        for (int64_t i = 0; i < cols; ++i) y[r * cols + i] = row[i] * inv * w[i];
+    }
+}
+
+// The Embedding arm of eval_cpu (mod.rs:81-96) over moe::embedding
+// (moe.rs:34-45): ids arrive as f32, rounded half away from zero and
+// clamped to [0, u32::MAX]; an id ≥ vocab is ShapeMismatch (returns 2).
+int orc_embedding(const float *ids, int64_t n, const float *table, int64_t vocab, int64_t hidden,
+                  float *y) {
+    for (int64_t t = 0; t < n; ++t) {
+        float v = std::round(ids[t]);
+        if (!(v >= 0.0f)) v = 0.0f;  // NaN and negatives clamp to 0
+        if (v >= (float)vocab) return 2;
+        const int64_t id = (int64_t)v;
+        std::memcpy(y + t * hidden, table + id * hidden, (size_t)hidden * 4);
+    }
+    return 0;
+}
+
+// moe::apply_rope, moe.rs:47-60: pairs (2i, 2i+1) rotated by pos·θ^(−2i/hd),
+// angles in f64, sin/cos cast to f32.
+static void apply_rope(float *q, int64_t head_dim, int64_t pos, double theta) {
+    for (int64_t i = 0; i < head_dim / 2; ++i) {
+        const double freq = 1.0 / std::pow(theta, 2.0 * (double)i / (double)head_dim);
+        const double ang = (double)pos * freq;
+        const float s = (float)std::sin(ang), c = (float)std::cos(ang);
+        const float a = q[2 * i], b = q[2 * i + 1];
+        q[2 * i] = a * c - b * s;
+        q[2 * i + 1] = a * s + b * c;
+    }
+}
+
+// moe::gqa, moe.rs:62-136: q/k/v projections (linear_seq), RoPE on q and k
+// at position t, per (b, h) causal softmax over keys [start, i] with
+// start = i − (window − 1) when a window is given (window ≤ 0: none), kv head
+// h / (n_heads / n_kv), then the output projection.  Returns 2 on a shape
+// mismatch.
+int orc_gqa(const float *x, const float *wq, const float *wk, const float *wv, const float *wo, int64_t B,
+            int64_t S, int64_t D, int64_t n_heads, int64_t n_kv, int64_t head_dim, double theta,
+            int64_t window, float *y) {
+    if (n_heads * head_dim != D || n_kv <= 0 || n_heads % n_kv != 0) return 2;
+    const int64_t T = B * S, KV = n_kv * head_dim;
+    std::vector<float> q((size_t)(T * D)), k((size_t)(T * KV)), v((size_t)(T * KV));
+    orc_matmul_seq(x, wq, q.data(), T, D, D);
+    orc_matmul_seq(x, wk, k.data(), T, D, KV);
+    orc_matmul_seq(x, wv, v.data(), T, D, KV);
+    for (int64_t bi = 0; bi < B; ++bi)
+        for (int64_t t = 0; t < S; ++t) {
+            for (int64_t h = 0; h < n_heads; ++h)
+                apply_rope(&q[(size_t)(((bi * S + t) * n_heads + h) * head_dim)], head_dim, t, theta);
+            for (int64_t h = 0; h < n_kv; ++h)
+                apply_rope(&k[(size_t)(((bi * S + t) * n_kv + h) * head_dim)], head_dim, t, theta);
+        }
+    const int64_t repeats = std::max<int64_t>(n_heads / std::max<int64_t>(n_kv, 1), 1);
+    const float scale = 1.0f / std::sqrt((float)head_dim);
+    std::vector<float> ctx((size_t)(T * D), 0.0f), scores((size_t)S);
+    for (int64_t bi = 0; bi < B; ++bi)
+        for (int64_t h = 0; h < n_heads; ++h) {
+            const int64_t kv_h = h / repeats;
+            for (int64_t i = 0; i < S; ++i) {
+                const int64_t start = window > 0 ? std::max<int64_t>(i - (window - 1), 0) : 0;
+                const float *qi = &q[(size_t)(((bi * S + i) * n_heads + h) * head_dim)];
+                float mx = -INFINITY;
+                for (int64_t j = start; j <= i; ++j) {
+                    const float *kj = &k[(size_t)(((bi * S + j) * n_kv + kv_h) * head_dim)];
+                    float dot = 0.0f;
+                    for (int64_t t = 0; t < head_dim; ++t) dot += qi[t] * kj[t];
+                    scores[(size_t)j] = dot * scale;
+                    mx = std::max(mx, scores[(size_t)j]);
+                }
+                float sum = 0.0f;
+                for (int64_t j = start; j <= i; ++j) {
+                    scores[(size_t)j] = std::exp(scores[(size_t)j] - mx);
+                    sum += scores[(size_t)j];
+                }
+                const float inv = 1.0f / std::max(sum, 1e-30f);
+                float *o = &ctx[(size_t)(((bi * S + i) * n_heads + h) * head_dim)];
+                for (int64_t j = start; j <= i; ++j) {
+                    const float wgt = scores[(size_t)j] * inv;
+                    const float *vj = &v[(size_t)(((bi * S + j) * n_kv + kv_h) * head_dim)];
+                    for (int64_t t = 0; t < head_dim; ++t) o[t] += wgt * vj[t];
+                }
+            }
+        }
+    orc_matmul_seq(ctx.data(), wo, y, T, D, D);
+    return 0;
+}
+
+// moe::lm_head, moe.rs:325-333: w is [V, H] (HF layout); y = x·wᵀ via the
+// transposed copy and linear_seq.
+void orc_lm_head(const float *x, const float *w, int64_t rows, int64_t H, int64_t V, float *y) {
+    std::vector<float> wt((size_t)(H * V));
+    for (int64_t i = 0; i < V; ++i)
+        for (int64_t j = 0; j < H; ++j) wt[(size_t)(j * V + i)] = w[i * H + j];
+    orc_matmul_seq(x, wt.data(), y, rows, H, V);
+}
+
+// deepseek::mix, deepseek.rs:229-239: y = σ(g)·a + (1 − σ(g))·b.
+void orc_mix(const float *a, const float *b, float gate, int64_t n, float *y) {
+    const float s = 1.0f / (1.0f + std::exp(-gate));
+    for (int64_t i = 0; i < n; ++i) y[i] = s * a[i] + (1.0f - s) * b[i];
+}
+
 }  // extern "C"
 
 // ============================================================ adjoint.rs

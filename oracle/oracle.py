@@ -69,6 +69,12 @@ _SIG = {
     "orc_place_arena": ([_U64P, _U64P, _U64P, _I64, ctypes.c_uint64, _U64P, _I64P, _I64P],
                         ctypes.c_int),
     "orc_arena_conflict": ([_U64P, _U64P, _U64P, _U64P, _I64], ctypes.c_int),
+    "orc_rmsnorm": ([_F, _F, _I64, _I64, ctypes.c_float, _F], None),
+    "orc_embedding": ([_F, _I64, _F, _I64, _I64, _F], ctypes.c_int),
+    "orc_gqa": ([_F, _F, _F, _F, _F, _I64, _I64, _I64, _I64, _I64, _I64, ctypes.c_double, _I64, _F],
+                ctypes.c_int),
+    "orc_lm_head": ([_F, _F, _I64, _I64, _I64, _F], None),
+    "orc_mix": ([_F, _F, ctypes.c_float, _I64, _F], None),
 }
 for _name, (_args, _res) in _SIG.items():
     _fn = getattr(_lib, _name)
@@ -232,6 +238,53 @@ def moe(x, gate, w1s, w3s, w2s, top_k, tokens=None, reference=False):
     return out
 
 
+def rmsnorm(x, w, eps):
+    """moe::rmsnorm, moe.rs:17-32."""
+    x, w = _c(x), _c(w)
+    y = np.empty_like(x)
+    _lib.orc_rmsnorm(_f(x), _f(w), x.size // x.shape[-1], x.shape[-1], np.float32(eps), _f(y))
+    return y
+
+
+def embedding(ids, table):
+    """Embedding arm of eval_cpu (mod.rs:81-96): [.., n] f32 ids → [.., n, H]."""
+    ids, table = _c(ids), _c(table)
+    V, H = table.shape
+    y = np.empty(ids.shape + (H,), np.float32)
+    if _lib.orc_embedding(_f(ids), ids.size, _f(table), V, H, _f(y)):
+        raise ValueError("token id >= vocab")
+    return y
+
+
+def gqa(x, wq, wk, wv, wo, n_heads, n_kv, head_dim, theta, window=None):
+    """moe::gqa, moe.rs:62-136 (window None: no sliding window)."""
+    x = _c(x)
+    B, S, D = x.shape
+    y = np.empty_like(x)
+    rc = _lib.orc_gqa(_f(x), _f(_c(wq)), _f(_c(wk)), _f(_c(wv)), _f(_c(wo)), B, S, D, n_heads, n_kv,
+                      head_dim, float(theta), -1 if window is None else int(window), _f(y))
+    if rc:
+        raise ValueError("gqa shape")
+    return y
+
+
+def lm_head(x, w):
+    """moe::lm_head, moe.rs:325-333 (w is [V, H])."""
+    x, w = _c(x), _c(w)
+    V, H = w.shape
+    y = np.empty(x.shape[:-1] + (V,), np.float32)
+    _lib.orc_lm_head(_f(x), _f(w), x.size // H, H, V, _f(y))
+    return y
+
+
+def mix(a, b, gate):
+    """deepseek::mix, deepseek.rs:229-239."""
+    a, b = _c(a), _c(b)
+    y = np.empty_like(a)
+    _lib.orc_mix(_f(a), _f(b), np.float32(gate), a.size, _f(y))
+    return y
+
+
 def moe_permute(idx, n_experts):
     idx = np.ascontiguousarray(idx, np.int32)
     T, k = idx.shape
@@ -327,6 +380,24 @@ def eval_node(node, inputs, reference=False):
         w3 = np.stack([P[f"e{e}.w3"] for e in range(E)])
         w2 = np.stack([P[f"e{e}.w2"] for e in range(E)])
         return moe(x, P["gate"], w1, w3, w2, k)
+    # Mixtral / DeepSeek arms of eval_cpu (mod.rs:74-131, :186-193); eval_reference
+    # sends these to eval_cpu as well (mod.rs:240-249).
+    if kind == "rms_norm":
+        return rmsnorm(x, P["w"], np.float32(node.op.fields[0]) * np.float32(1e-6))
+    if kind == "embedding":
+        return embedding(x, P["w"])
+    if kind == "swiglu":
+        return swiglu(x, P["w1"], P["w3"], P["w2"])
+    if kind == "gqa_attention":
+        nh, nkv, hd, _, window, theta = node.op.fields
+        return gqa(x, P["wq"], P["wk"], P["wv"], P["wo"], nh, nkv, hd, float(theta),
+                   None if window < 0 else window)
+    if kind == "lm_head":
+        return lm_head(x, P["w"])
+    if kind == "router":
+        return x.copy()
+    if kind == "mix":
+        return mix(x, inputs[1], float(P["gate"][0]) if "gate" in P else 0.0)
     raise NotImplementedError(kind)
 
 
