@@ -214,3 +214,84 @@ def config5(batch: int = 8, seq: int = 1024, d: int = 1024, heads: int = 16, ffn
 
 def config5_graph(**kw) -> IrGraph:
     return config5(**kw).graph
+
+
+@dataclass
+class MixtralShape:
+    """MixtralConfig fields the graph needs (crates/catnn-core/src/spec/mixtral.rs:
+    107-130 gives the tiny values used as defaults)."""
+    vocab: int = 32
+    hidden: int = 32
+    inter: int = 64
+    layers: int = 2
+    heads: int = 4
+    kv_heads: int = 2
+    experts: int = 4
+    top_k: int = 2
+    eps: float = 1e-5
+    rope_theta: int = 10000
+    sliding_window: Optional[int] = 8
+
+
+def mixtral(batch: int = 2, seq: int = 4, shape: Optional[MixtralShape] = None, seed: int = 7) -> Workload:
+    """The IrGraph of mixtral_architecture (mixtral.rs:180-292): tokens →
+    embed → per layer rms_attn → gqa → rms_moe → moe → final_norm → lm_head,
+    a plain chain (the architecture lowers without residual adds).  Weights
+    are seeded normals scaled 1/fan_in (the RMSNorm weights 1 + N(0, 0.01));
+    token ids are uniform over the vocabulary, stored as f32 like every
+    value the reference evaluates."""
+    c = shape or MixtralShape()
+    seeds = iter(range(1000 * seed, 1000 * seed + 100000))
+    h, hd = c.hidden, c.hidden // c.heads
+    eps_e6 = int(np.float32(c.eps) * np.float32(1e6))  # (eps · 1e6) as u32, in f32
+
+    def normal(shape, var):
+        n = int(np.prod(shape))
+        return Tensor(TensorType.f32(shape), synth.normal(n, next(seeds), var).reshape(shape))
+
+    def norm_w():
+        return Tensor(TensorType.f32([h]), 1.0 + synth.normal(h, next(seeds), 0.01))
+
+    ty = TensorType.f32([batch, seq, h])
+    g = IrGraph(f"mixtral_{c.layers}l_{h}")
+    g.add_node(IrNode(0, "tokens", OpenOp.identity(), TensorType.f32([batch, seq])))
+    g.inputs.append(0)
+    nodes = [IrNode(1, "embed", OpenOp.embedding(c.vocab, h), ty, {"w": normal([c.vocab, h], 1.0)})]
+    for layer in range(c.layers):
+        gqa_params = {"wq": normal([h, h], 1.0 / h), "wk": normal([h, c.kv_heads * hd], 1.0 / h),
+                      "wv": normal([h, c.kv_heads * hd], 1.0 / h), "wo": normal([h, h], 1.0 / h)}
+        moe_params = {"gate": normal([h, c.experts], 1.0 / h)}
+        for e in range(c.experts):
+            moe_params[f"e{e}.w1"] = normal([h, c.inter], 1.0 / h)
+            moe_params[f"e{e}.w3"] = normal([h, c.inter], 1.0 / h)
+            moe_params[f"e{e}.w2"] = normal([c.inter, h], 1.0 / c.inter)
+        nid = len(nodes) + 1
+        nodes += [
+            IrNode(nid, f"L{layer}.rms_attn", OpenOp.rms_norm(eps_e6), ty, {"w": norm_w()}),
+            IrNode(nid + 1, f"L{layer}.gqa",
+                   OpenOp.gqa_attention(c.heads, c.kv_heads, hd, h, c.sliding_window, c.rope_theta), ty,
+                   gqa_params),
+            IrNode(nid + 2, f"L{layer}.rms_moe", OpenOp.rms_norm(eps_e6), ty, {"w": norm_w()}),
+            IrNode(nid + 3, f"L{layer}.moe", OpenOp.moe(c.experts, c.top_k, h, c.inter), ty, moe_params),
+        ]
+    nid = len(nodes) + 1
+    nodes += [IrNode(nid, "final_norm", OpenOp.rms_norm(eps_e6), ty, {"w": norm_w()}),
+              IrNode(nid + 1, "lm_head", OpenOp.lm_head(h, c.vocab), TensorType.f32([batch, seq, c.vocab]),
+                     {"w": normal([c.vocab, h], 1.0 / h)})]
+    prev = 0
+    for n in nodes:
+        g.add_node(n)
+        g.add_edge(prev, n.id)
+        prev = n.id
+    g.outputs.append(prev)
+    T = batch * seq
+    ids = synth.uniform(T, next(seeds), 0.0, float(c.vocab))
+    x = Tensor(TensorType.f32([batch, seq]), np.minimum(np.floor(ids), c.vocab - 1).astype(np.float32))
+    kvw = c.kv_heads * hd
+    win = seq if c.sliding_window is None else min(seq, c.sliding_window)
+    attn_pairs = sum(min(i + 1, win) for i in range(seq)) * batch
+    per_layer = (2 * T * h * (2 * h + 2 * kvw) + 4 * attn_pairs * c.heads * hd +
+                 2 * T * h * c.experts + T * c.top_k * 6 * h * c.inter)
+    flops = c.layers * per_layer + 2 * T * h * c.vocab
+    params = sum(t.data.size for n in g.nodes.values() for t in n.params.values())
+    return Workload(g.name, g, x, flops, 4 * (params + T + T * c.vocab), T)

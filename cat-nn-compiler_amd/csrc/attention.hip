@@ -42,11 +42,15 @@ constexpr float kMasked = -1e30f;
 // zero, which no softmax weight in the fp32 tolerance can see.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// K and V rows have their own stride ldk and hold H / group heads (grouped-
+// query attention: head h reads K/V head h / group); window > 0 restricts
+// query i to keys [i − window + 1, i] (with causal set).
 template <int DH>
 __global__ __launch_bounds__(256, 2) void attn_mfma_kernel(const float *__restrict__ q,
                                                            const float *__restrict__ k,
                                                            const float *__restrict__ v,
-                                                           int64_t ld, float *__restrict__ o,
+                                                           int64_t ld, int64_t ldk, int group, int window,
+                                                           float *__restrict__ o,
                                                            int64_t ldo, float *__restrict__ lse,
                                                            int S, int H, float qscale, int causal,
                                                            int n_qblocks) {
@@ -63,7 +67,7 @@ __global__ __launch_bounds__(256, 2) void attn_mfma_kernel(const float *__restri
     int blk, bh;
     split_bh_block(blockIdx.x, n_qblocks, (int)(gridDim.x / n_qblocks), blk, bh);
     const int qb = n_qblocks - 1 - blk;
-    const int b = bh / H, h = bh % H;
+    const int b = bh / H, h = bh % H, hk = h / group;
     const int q0 = qb * BQ;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int lr = lane & 31, g = lane >> 5;
@@ -98,6 +102,8 @@ __global__ __launch_bounds__(256, 2) void attn_mfma_kernel(const float *__restri
 
     const int kv_end = causal ? min(S, q0 + BQ) : S;
     const int ntiles = (kv_end + BKV - 1) / BKV;
+    // Sliding window: tiles before the first key of the block's first query are skipped.
+    const int t_first = window > 0 ? max(0, q0 - window + 1) / BKV : 0;
 
     float4 pk[KV_IT], pv[KV_IT];
     auto gload = [&](int t) {
@@ -107,7 +113,7 @@ __global__ __launch_bounds__(256, 2) void attn_mfma_kernel(const float *__restri
             const int key = t * BKV + idx / (DH / 4);
             const int c4 = idx % (DH / 4);
             if (key < S) {
-                const int64_t off = (row_base + key) * ld + (int64_t)h * DH + 4 * c4;
+                const int64_t off = (row_base + key) * ldk + (int64_t)hk * DH + 4 * c4;
                 pk[it] = *reinterpret_cast<const float4 *>(k + off);
                 pv[it] = *reinterpret_cast<const float4 *>(v + off);
             } else {
@@ -129,10 +135,10 @@ __global__ __launch_bounds__(256, 2) void attn_mfma_kernel(const float *__restri
         }
     };
 
-    gload(0);
-    sstore(0);
+    gload(t_first);
+    sstore(t_first & 1);
     __syncthreads();
-    for (int t = 0; t < ntiles; ++t) {
+    for (int t = t_first; t < ntiles; ++t) {
         const int buf = t & 1;
         const bool more = t + 1 < ntiles;
         if (more) gload(t + 1);
@@ -144,11 +150,13 @@ __global__ __launch_bounds__(256, 2) void attn_mfma_kernel(const float *__restri
         // of the wavefront needs no mask.  Queries ≥ S are padding: their
         // scores are computed but never stored.
         const bool full = __builtin_amdgcn_readfirstlane(
-            j0 + BKV <= S && (!causal || j0 + BKV - 1 <= wave_qmin));
+            j0 + BKV <= S && (!causal || j0 + BKV - 1 <= wave_qmin) &&
+            (window <= 0 || j0 >= wave_qmax - window + 1));
 #pragma unroll
         for (int kb = 0; kb < BKV / 32; ++kb) {
             const int jb = j0 + kb * 32;
-            active[kb] = __builtin_amdgcn_readfirstlane(jb < S && (!causal || jb <= wave_qmax));
+            active[kb] = __builtin_amdgcn_readfirstlane(jb < S && (!causal || jb <= wave_qmax) &&
+                                                        (window <= 0 || jb + 31 >= wave_qmin - window + 1));
 #pragma unroll
             for (int r = 0; r < 16; ++r) sacc[kb][r] = 0.f;
             if (active[kb]) {
@@ -181,7 +189,8 @@ __global__ __launch_bounds__(256, 2) void attn_mfma_kernel(const float *__restri
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int j = j0 + kb * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-                    const bool ok = active[kb] && j < S && (!causal || j <= qi);
+                    const bool ok = active[kb] && j < S && (!causal || j <= qi) &&
+                                    (window <= 0 || j >= qi - window + 1);
                     const float sv = ok ? sacc[kb][r] : kMasked;
                     sacc[kb][r] = sv;
                     mx = fmaxf(mx, sv);
@@ -254,7 +263,8 @@ __global__ __launch_bounds__(256, 2) void attn_mfma_kernel(const float *__restri
 __global__ __launch_bounds__(256) void attn_generic_kernel(const float *__restrict__ q,
                                                            const float *__restrict__ k,
                                                            const float *__restrict__ v,
-                                                           int64_t ld, float *__restrict__ o,
+                                                           int64_t ld, int64_t ldk, int group, int window,
+                                                           float *__restrict__ o,
                                                            int64_t ldo, float *__restrict__ lse,
                                                            int B, int S, int H, int DH, float scale,
                                                            int causal) {
@@ -264,7 +274,7 @@ __global__ __launch_bounds__(256) void attn_generic_kernel(const float *__restri
     if (gw >= total) return;
     const int i = (int)(gw % S);
     const int64_t bh = gw / S;
-    const int h = (int)(bh % H), b = (int)(bh / H);
+    const int h = (int)(bh % H), b = (int)(bh / H), hk = h / group;
     const int64_t row_base = (int64_t)b * S;
     float qv[4], acc[4];
 #pragma unroll
@@ -275,8 +285,9 @@ __global__ __launch_bounds__(256) void attn_generic_kernel(const float *__restri
     }
     float m = -INFINITY, l = 0.f;
     const int jend = causal ? i + 1 : S;
-    for (int j = 0; j < jend; ++j) {
-        const float *kr = k + (row_base + j) * ld + (int64_t)h * DH;
+    const int jstart = window > 0 ? max(0, i - window + 1) : 0;
+    for (int j = jstart; j < jend; ++j) {
+        const float *kr = k + (row_base + j) * ldk + (int64_t)hk * DH;
         float part = 0.f;
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
@@ -289,7 +300,7 @@ __global__ __launch_bounds__(256) void attn_generic_kernel(const float *__restri
         const float p = expf(sc - m_new);
         l = l * factor + p;
         m = m_new;
-        const float *vr = v + (row_base + j) * ld + (int64_t)h * DH;
+        const float *vr = v + (row_base + j) * ldk + (int64_t)hk * DH;
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
             const int d = lane + 64 * c;
@@ -309,32 +320,40 @@ bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 
 
 }  // namespace
 
+// ld_qkv: row stride of q; ldk: of k and v, which hold n_heads / group
+// heads; window > 0: sliding window (with causal).
 static void attention_fwd(hipStream_t s, const float *q, const float *k, const float *v,
-                          int64_t ld_qkv, float *ctx, int64_t ldo, float *lse, int64_t batch,
-                          int64_t seq, int64_t n_heads, int64_t d_head, bool causal) {
+                          int64_t ld_qkv, int64_t ldk, int64_t group, int64_t window, float *ctx,
+                          int64_t ldo, float *lse, int64_t batch, int64_t seq, int64_t n_heads,
+                          int64_t d_head, bool causal) {
     CATNN_REQUIRE(batch >= 0 && seq >= 0 && n_heads > 0 && d_head > 0, CATNN_ERR_SHAPE_MISMATCH,
                   "attention: bad dims");
     CATNN_REQUIRE(d_head <= 256, CATNN_ERR_SHAPE_MISMATCH, "attention: d_head > 256");
-    CATNN_REQUIRE(n_heads * d_head <= ld_qkv && n_heads * d_head <= ldo, CATNN_ERR_SHAPE_MISMATCH,
-                  "attention: heads exceed the row width");
+    CATNN_REQUIRE(group >= 1 && n_heads % group == 0, CATNN_ERR_SHAPE_MISMATCH,
+                  "attention: n_heads not a multiple of the kv groups");
+    CATNN_REQUIRE(n_heads * d_head <= ld_qkv && n_heads * d_head <= ldo &&
+                      (n_heads / group) * d_head <= ldk,
+                  CATNN_ERR_SHAPE_MISMATCH, "attention: heads exceed the row width");
+    CATNN_REQUIRE(window <= 0 || causal, CATNN_ERR_INVALID_ARGUMENT, "attention: a window needs causal");
     CATNN_REQUIRE(batch * seq < (1ll << 31), CATNN_ERR_SHAPE_MISMATCH, "attention: too many rows");
     if (batch == 0 || seq == 0) return;
     const float scale = 1.0f / sqrtf((float)d_head);
-    const bool mfma = d_head == 64 && ld_qkv % 4 == 0 && ldo % 4 == 0 && aligned16(q) &&
+    const bool mfma = d_head == 64 && ld_qkv % 4 == 0 && ldk % 4 == 0 && ldo % 4 == 0 && aligned16(q) &&
                       aligned16(k) && aligned16(v) && aligned16(ctx);
+    const int win = (int)std::min<int64_t>(std::max<int64_t>(window, 0), seq);
     if (mfma) {
         const int nqb = (int)((seq + 127) / 128);
         const int64_t blocks = batch * n_heads * nqb;
         CATNN_REQUIRE(blocks < (1ll << 31), CATNN_ERR_SHAPE_MISMATCH, "attention: grid too large");
         attn_mfma_kernel<64><<<(unsigned)blocks, 256, 0, s>>>(
-            q, k, v, ld_qkv, ctx, ldo, lse, (int)seq, (int)n_heads, scale * kLog2e, causal ? 1 : 0,
-            nqb);
+            q, k, v, ld_qkv, ldk, (int)group, win, ctx, ldo, lse, (int)seq, (int)n_heads, scale * kLog2e,
+            causal ? 1 : 0, nqb);
     } else {
         const int64_t waves = batch * n_heads * seq;
         const int64_t blocks = (waves + 3) / 4;
         CATNN_REQUIRE(blocks < (1ll << 31), CATNN_ERR_SHAPE_MISMATCH, "attention: grid too large");
-        attn_generic_kernel<<<(unsigned)blocks, 256, 0, s>>>(q, k, v, ld_qkv, ctx, ldo, lse,
-                                                             (int)batch, (int)seq, (int)n_heads,
+        attn_generic_kernel<<<(unsigned)blocks, 256, 0, s>>>(q, k, v, ld_qkv, ldk, (int)group, win, ctx,
+                                                             ldo, lse, (int)batch, (int)seq, (int)n_heads,
                                                              (int)d_head, scale, causal ? 1 : 0);
     }
     CATNN_HIP(hipGetLastError());
@@ -343,13 +362,19 @@ static void attention_fwd(hipStream_t s, const float *q, const float *k, const f
 void attention_core_f32(hipStream_t s, const float *q, const float *k, const float *v,
                         int64_t ld_qkv, float *ctx, int64_t ldo, int64_t batch, int64_t seq,
                         int64_t n_heads, int64_t d_head, bool causal) {
-    attention_fwd(s, q, k, v, ld_qkv, ctx, ldo, nullptr, batch, seq, n_heads, d_head, causal);
+    attention_fwd(s, q, k, v, ld_qkv, ld_qkv, 1, 0, ctx, ldo, nullptr, batch, seq, n_heads, d_head, causal);
+}
+
+void attention_core_gqa_f32(hipStream_t s, const float *q, const float *k, const float *v, int64_t ldq,
+                            int64_t ldk, int64_t group, int64_t window, float *ctx, int64_t ldo,
+                            int64_t batch, int64_t seq, int64_t n_heads, int64_t d_head) {
+    attention_fwd(s, q, k, v, ldq, ldk, group, window, ctx, ldo, nullptr, batch, seq, n_heads, d_head, true);
 }
 
 void attention_core_fwd_lse(hipStream_t s, const float *q, const float *k, const float *v, int64_t ld,
                             float *ctx, int64_t ldo, float *lse, int64_t batch, int64_t seq,
                             int64_t n_heads, int64_t d_head, bool causal) {
-    attention_fwd(s, q, k, v, ld, ctx, ldo, lse, batch, seq, n_heads, d_head, causal);
+    attention_fwd(s, q, k, v, ld, ld, 1, 0, ctx, ldo, lse, batch, seq, n_heads, d_head, causal);
 }
 
 }  // namespace k

@@ -189,6 +189,58 @@ std::vector<int64_t> infer_dims(const Node &node, const std::vector<std::vector<
             }
             return x;
         }
+        case CATNN_OP_ROUTER:  // identity in eval_cpu (mod.rs:128)
+            return x;
+        case CATNN_OP_RMS_NORM: {  // moe.rs:17-22
+            if (x.empty()) fail(CATNN_ERR_SHAPE_MISMATCH, "rms scalar");
+            if (numel_of(pdims(node, "w")) != x.back()) fail(CATNN_ERR_SHAPE_MISMATCH, "rmsnorm weight");
+            return x;
+        }
+        case CATNN_OP_EMBEDDING: {  // mod.rs:81-96: [B,S] ids → [B,S,hidden], else [n, hidden]
+            const int64_t hidden = node.op.a[1];
+            const auto &t = pdims(node, "w");
+            if (t.size() != 2 || t[1] != hidden)
+                fail(CATNN_ERR_SHAPE_MISMATCH,
+                     "embedding table " + dims_str(t) + " for hidden " + std::to_string(hidden));
+            if (x.size() == 2) return {x[0], x[1], hidden};
+            return {numel_of(x), hidden};
+        }
+        case CATNN_OP_GQA_ATTENTION: {  // moe.rs:64-82
+            if (x.size() != 3) fail(CATNN_ERR_SHAPE_MISMATCH, "gqa expects [B,S,H]");
+            const int64_t nh = node.op.a[0], nkv = node.op.a[1], hd = node.op.a[2], d = x[2];
+            if (nh <= 0 || nkv <= 0 || hd <= 0 || nh % nkv != 0)
+                fail(CATNN_ERR_SHAPE_MISMATCH, "gqa: n_heads must be a positive multiple of n_kv_heads");
+            const int64_t qw = nh * hd, kw = nkv * hd;
+            const std::pair<const char *, std::vector<int64_t>> want[] = {
+                {"wq", {d, qw}}, {"wk", {d, kw}}, {"wv", {d, kw}}, {"wo", {qw, d}}};
+            for (const auto &w : want)
+                if (pdims(node, w.first) != w.second)
+                    fail(CATNN_ERR_SHAPE_MISMATCH, std::string("gqa ") + w.first + " " +
+                                                       dims_str(pdims(node, w.first)) + ", expected " +
+                                                       dims_str(w.second));
+            return x;
+        }
+        case CATNN_OP_SWIGLU: {  // moe.rs:159-174
+            if (x.empty()) fail(CATNN_ERR_SHAPE_MISMATCH, "swiglu on scalar");
+            const int64_t hid = x.back();
+            const auto &w1 = pdims(node, "w1");
+            if (w1.size() != 2 || w1[0] != hid || pdims(node, "w3") != w1 ||
+                pdims(node, "w2") != std::vector<int64_t>{w1[1], hid})
+                fail(CATNN_ERR_SHAPE_MISMATCH, "swiglu weights " + dims_str(w1) + " for hidden " +
+                                                   std::to_string(hid));
+            return x;
+        }
+        case CATNN_OP_LM_HEAD: {  // moe.rs:325-333: w [V, H], [B,S,H] → [B,S,V]
+            if (x.size() != 3) fail(CATNN_ERR_SHAPE_MISMATCH, "lm_head expects [B,S,H]");
+            const int64_t vocab = node.op.a[1];
+            if (pdims(node, "w") != std::vector<int64_t>{vocab, x[2]})
+                fail(CATNN_ERR_SHAPE_MISMATCH, "lm_head w " + dims_str(pdims(node, "w")));
+            return {x[0], x[1], vocab};
+        }
+        case CATNN_OP_MIX:  // mod.rs:186-193, deepseek.rs:229-232
+            if (ins.size() < 2) fail(CATNN_ERR_WIRING, "mix needs two inputs");
+            if (numel_of(x) != numel_of(ins[1])) fail(CATNN_ERR_SHAPE_MISMATCH, "mix operands differ");
+            return x;
         default:
             fail(CATNN_ERR_UNSUPPORTED,
                  "op " + op_name(kind) + " (node " + node.name + ") is not executable on the HIP backend");
@@ -196,6 +248,10 @@ std::vector<int64_t> infer_dims(const Node &node, const std::vector<std::vector<
 }
 
 static int64_t moe_intermediate(const Node &node) { return pdims(node, "e0.w1")[1]; }
+
+static k::GqaLayout gqa_layout_of(const Node &node, const std::vector<int64_t> &x) {
+    return k::gqa_layout(x[0] * x[1], x[1], node.op.a[0], node.op.a[1], node.op.a[2]);
+}
 
 uint64_t scratch_bytes(const Node &node, const std::vector<std::vector<int64_t>> &ins) {
     if (ins.empty()) return 0;
@@ -211,6 +267,13 @@ uint64_t scratch_bytes(const Node &node, const std::vector<std::vector<int64_t>>
                                        node.op.a[0], node.op.a[1])
             .total;
     }
+    if (node.op.kind == CATNN_OP_EMBEDDING) return 256;  // the bad-id flag
+    if (node.op.kind == CATNN_OP_GQA_ATTENTION) return (uint64_t)gqa_layout_of(node, ins[0]).floats * 4;
+    if (node.op.kind == CATNN_OP_SWIGLU) {
+        const int64_t hid = ins[0].back();
+        return (uint64_t)(numel_of(ins[0]) / hid) * (uint64_t)pdims(node, "w1")[1] * 4;
+    }
+    if (node.op.kind == CATNN_OP_LM_HEAD) return (uint64_t)numel_of(pdims(node, "w")) * 4;  // wᵀ
     return 0;
 }
 
@@ -282,8 +345,8 @@ void exec_node(catnn_hip_device *dev, const Node &node, const ExecArgs &a) {
                           CATNN_ERR_INVALID_ARGUMENT, "attention: scratch too small");
             float *qkv = a.scratch;          // [T, 3D]
             float *ctx = a.scratch + T * 3 * D;  // [T, D]
-            if (a.packed_qkv) {
-                k::linear_f32(s, x, D, a.packed_qkv, 3 * D, nullptr, nullptr, 0, qkv, 3 * D, T, D,
+            if (a.derived) {
+                k::linear_f32(s, x, D, a.derived, 3 * D, nullptr, nullptr, 0, qkv, 3 * D, T, D,
                               3 * D, 0);
             } else {
                 k::linear_f32(s, x, D, need("wq"), D, nullptr, nullptr, 0, qkv, 3 * D, T, D, D, 0);
@@ -314,6 +377,74 @@ void exec_node(catnn_hip_device *dev, const Node &node, const ExecArgs &a) {
                        a.out, a.scratch, L);
             break;
         }
+        case CATNN_OP_ROUTER:
+            k::copy_f32(s, x, a.out, nx);
+            break;
+        case CATNN_OP_RMS_NORM: {
+            const int64_t last = a.in_dims[0].back();
+            const float eps = (float)node.op.a[0] * 1e-6f;  // eps_e6 as f32 · 1e-6 (mod.rs:79)
+            k::rms_norm_f32(s, x, need("w"), a.out, nx / last, last, eps);
+            break;
+        }
+        case CATNN_OP_EMBEDDING: {
+            const int64_t vocab = pdims(node, "w")[0], hidden = node.op.a[1];
+            CATNN_REQUIRE(a.scratch && a.scratch_bytes >= 4, CATNN_ERR_INVALID_ARGUMENT,
+                          "embedding: scratch too small");
+            int *bad = reinterpret_cast<int *>(a.scratch);
+            CATNN_HIP(hipMemsetAsync(bad, 0, sizeof(int), s));
+            k::embedding_f32(s, x, nx, need("w"), vocab, hidden, a.out, bad);
+            // The reference fails the op on an out-of-range id (moe.rs:38-40):
+            // read the flag back before anything consumes the rows.
+            int host_bad = 0;
+            CATNN_HIP(hipMemcpyAsync(&host_bad, bad, sizeof(int), hipMemcpyDeviceToHost, s));
+            CATNN_HIP(hipStreamSynchronize(s));
+            if (host_bad)
+                fail(CATNN_ERR_SHAPE_MISMATCH, "embedding " + node.name + ": token id >= vocab " +
+                                                   std::to_string(vocab));
+            break;
+        }
+        case CATNN_OP_GQA_ATTENTION: {
+            const auto &xd = a.in_dims[0];
+            const k::GqaLayout L = gqa_layout_of(node, xd);
+            CATNN_REQUIRE(a.scratch && a.scratch_bytes >= (uint64_t)L.floats * 4, CATNN_ERR_INVALID_ARGUMENT,
+                          "gqa: scratch too small");
+            const bool packed = a.derived != nullptr;
+            // sliding_window None is −1 here; Some(0) behaves as no window, as the
+            // reference's saturating start does in a release build (moe.rs:102).
+            k::gqa_f32(s, x, a.derived, packed ? nullptr : need("wq"), packed ? nullptr : need("wk"),
+                       packed ? nullptr : need("wv"), need("wo"), xd[0], xd[1], xd[2], node.op.a[0],
+                       node.op.a[1], node.op.a[2], (double)node.op.a[5], node.op.a[4], a.residual, a.out,
+                       a.scratch, L);
+            residual_done = true;
+            break;
+        }
+        case CATNN_OP_SWIGLU: {
+            const int64_t hid = a.in_dims[0].back(), inter = pdims(node, "w1")[1];
+            const int64_t T = nx / hid;
+            CATNN_REQUIRE(a.scratch && a.scratch_bytes >= (uint64_t)(T * inter) * 4, CATNN_ERR_INVALID_ARGUMENT,
+                          "swiglu: scratch too small");
+            k::swiglu_f32(s, x, need("w1"), need("w3"), need("w2"), T, hid, inter, a.residual, a.out,
+                          a.scratch);
+            residual_done = true;
+            break;
+        }
+        case CATNN_OP_LM_HEAD: {
+            const auto &xd = a.in_dims[0];
+            const int64_t vocab = node.op.a[1], hid = xd[2], T = xd[0] * xd[1];
+            const float *wt = a.derived;
+            if (!wt) {
+                CATNN_REQUIRE(a.scratch && a.scratch_bytes >= (uint64_t)(vocab * hid) * 4,
+                              CATNN_ERR_INVALID_ARGUMENT, "lm_head: scratch too small");
+                k::transpose_f32(s, need("w"), vocab, hid, a.scratch);
+                wt = a.scratch;
+            }
+            k::linear_f32(s, x, hid, wt, vocab, nullptr, a.residual, vocab, a.out, vocab, T, hid, vocab, 0);
+            residual_done = true;
+            break;
+        }
+        case CATNN_OP_MIX:
+            k::mix_f32(s, x, a.inputs[1], a.param("gate"), a.out, nx);
+            break;
         default:
             fail(CATNN_ERR_UNSUPPORTED, "op " + op_name(kind) + " (node " + node.name +
                                             ") is not executable on the HIP backend");
@@ -425,6 +556,7 @@ static std::string param_id(const Node &n, const std::string &port) {
     return "param:" + n.name + ":" + port;
 }
 static std::string scratch_id(const Node &n) { return "scratch:" + n.name; }
+static std::string derived_id(const Node &n) { return "derived:" + n.name; }
 
 static bool fusion_listed(const catnn_graph &g, const std::string &a, const std::string &b) {
     for (const auto &f : g.fusions)
@@ -480,7 +612,8 @@ static void build_program(catnn_hip_program &p) {
             }
         }
         // ResidualAdd folded into the producing GEMM's epilogue.
-        if (gemm_like || n.op.kind == CATNN_OP_ATTENTION) {
+        if (gemm_like || n.op.kind == CATNN_OP_ATTENTION || n.op.kind == CATNN_OP_GQA_ATTENTION ||
+            n.op.kind == CATNN_OP_SWIGLU) {
             const auto sc = g.succs(st.out);
             const bool is_out =
                 std::find(g.outputs.begin(), g.outputs.end(), st.out) != g.outputs.end();
@@ -499,7 +632,8 @@ static void build_program(catnn_hip_program &p) {
                 }
             }
         }
-        st.scratch = scratch_bytes(n, st.in_dims);
+        // LmHead reads the wᵀ copy made at install instead of scratch.
+        st.scratch = n.op.kind == CATNN_OP_LM_HEAD && n.param("w") ? 0 : scratch_bytes(n, st.in_dims);
         p.dims[st.out] = out_dims;
         p.steps.push_back(st);
     }
@@ -509,6 +643,41 @@ static void build_program(catnn_hip_program &p) {
         if (!p.steps[i].is_input) p.exec_steps.push_back(i);
     p.total_ms.assign(p.exec_steps.size(), 0.0);
     p.calls.assign(p.exec_steps.size(), 0);
+}
+
+// Weight copies made once at install (host side, from the params): the
+// projections of Attention / GqaAttention packed per row as [wq | wk | wv],
+// so q, k and v come from one GEMM, and LmHead's wᵀ [H, V], so the head is a
+// plain GEMM (moe.rs:328 transposes per call).
+static int64_t derived_floats(const Node &n) {
+    if ((n.op.kind == CATNN_OP_ATTENTION || n.op.kind == CATNN_OP_GQA_ATTENTION) && n.param("wq") &&
+        n.param("wk") && n.param("wv"))
+        return n.param("wq")->numel() + n.param("wk")->numel() + n.param("wv")->numel();
+    if (n.op.kind == CATNN_OP_LM_HEAD && n.param("w")) return n.param("w")->numel();
+    return 0;
+}
+
+static std::vector<float> derived_weight(const Node &n) {
+    std::vector<float> out((size_t)derived_floats(n));
+    if (n.op.kind == CATNN_OP_LM_HEAD) {
+        const HostTensor &w = *n.param("w");
+        const int64_t V = w.dims[0], H = w.dims[1];
+        for (int64_t v = 0; v < V; ++v)
+            for (int64_t h = 0; h < H; ++h) out[(size_t)(h * V + v)] = w.data[(size_t)(v * H + h)];
+        return out;
+    }
+    const HostTensor *parts[3] = {n.param("wq"), n.param("wk"), n.param("wv")};
+    const int64_t rows = parts[0]->dims[0];
+    int64_t ld = 0;
+    for (const HostTensor *t : parts) ld += t->dims[1];
+    int64_t col = 0;
+    for (const HostTensor *t : parts) {
+        const int64_t c = t->dims[1];
+        for (int64_t r = 0; r < rows; ++r)
+            std::memcpy(&out[(size_t)(r * ld + col)], &t->data[(size_t)(r * c)], (size_t)c * 4);
+        col += c;
+    }
+    return out;
 }
 
 static void plan_and_upload(catnn_hip_program &p) {
@@ -533,14 +702,13 @@ static void plan_and_upload(catnn_hip_program &p) {
     // Step scratch: live for its own tick only.
     for (const Step &st : p.steps)
         if (st.scratch) reqs.push_back(BufferReq{scratch_id(g.node(st.node)), st.scratch, st.tick, st.tick, false});
-    // Params (and the packed attention projection) live throughout.
+    // Params (and the derived weight copies) live throughout.
     for (uint32_t id : g.node_order) {
         const Node &n = g.node(id);
         for (const auto &pr : n.params)
             reqs.push_back(BufferReq{param_id(n, pr.first), (uint64_t)pr.second.numel() * 4, 0, n_ticks, false});
-        if (n.op.kind == CATNN_OP_ATTENTION && n.param("wq"))
-            reqs.push_back(BufferReq{param_id(n, "wqkv"), (uint64_t)n.param("wq")->numel() * 3 * 4, 0,
-                                     n_ticks, false});
+        if (derived_floats(n))
+            reqs.push_back(BufferReq{derived_id(n), (uint64_t)derived_floats(n) * 4, 0, n_ticks, false});
     }
     // Every buffer starts on a 256-byte boundary: round sizes up.
     for (auto &r : reqs) r.bytes = (r.bytes + 255) & ~uint64_t(255);
@@ -565,16 +733,9 @@ static void plan_and_upload(catnn_hip_program &p) {
                 CATNN_HIP(hipMemcpyAsync(p.ptr[param_id(n, pr.first)], pr.second.data.data(),
                                          (size_t)pr.second.numel() * 4, hipMemcpyHostToDevice,
                                          dev->stream));
-        if (n.op.kind == CATNN_OP_ATTENTION && n.param("wq")) {
-            const HostTensor &wq = *n.param("wq"), &wk = *n.param("wk"), &wv = *n.param("wv");
-            const int64_t d = wq.dims[0], c = wq.dims[1];
-            std::vector<float> packed((size_t)(d * 3 * c));
-            for (int64_t r = 0; r < d; ++r) {
-                std::memcpy(&packed[(size_t)(r * 3 * c)], &wq.data[(size_t)(r * c)], (size_t)c * 4);
-                std::memcpy(&packed[(size_t)(r * 3 * c + c)], &wk.data[(size_t)(r * c)], (size_t)c * 4);
-                std::memcpy(&packed[(size_t)(r * 3 * c + 2 * c)], &wv.data[(size_t)(r * c)], (size_t)c * 4);
-            }
-            CATNN_HIP(hipMemcpyAsync(p.ptr[param_id(n, "wqkv")], packed.data(), packed.size() * 4,
+        if (derived_floats(n)) {
+            const std::vector<float> d = derived_weight(n);
+            CATNN_HIP(hipMemcpyAsync(p.ptr[derived_id(n)], d.data(), d.size() * 4,
                                      hipMemcpyHostToDevice, dev->stream));
             CATNN_HIP(hipStreamSynchronize(dev->stream));
         }
@@ -616,10 +777,7 @@ static void run_program(catnn_hip_program &p) {
             a.scratch = p.ptr.at(scratch_id(n));
             a.scratch_bytes = st.scratch;
         }
-        if (n.op.kind == CATNN_OP_ATTENTION) {
-            auto it = p.ptr.find(param_id(n, "wqkv"));
-            if (it != p.ptr.end()) a.packed_qkv = it->second;
-        }
+        if (derived_floats(n)) a.derived = p.ptr.at(derived_id(n));
         exec_node(p.dev, n, a);
         ++executed;
         if (evs) CATNN_HIP(hipEventRecord((*evs)[executed], p.dev->stream));

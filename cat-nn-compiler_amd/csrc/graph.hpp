@@ -60,7 +60,9 @@ struct ExecArgs {
     // Attention scratch: qkv [T, 3D] and ctx [T, D]; MoE workspace.
     float *scratch = nullptr;
     uint64_t scratch_bytes = 0;
-    const float *packed_qkv = nullptr;  // [D, 3D] = [wq | wk | wv] per row
+    // Weight copy made at install: Attention/GqaAttention [wq | wk | wv] per
+    // row, LmHead wᵀ [H, V].  Null: built from the params (or scratch) per call.
+    const float *derived = nullptr;
 };
 
 // Scratch bytes `node` needs beyond its output (0 for most ops).

@@ -32,6 +32,39 @@ void attention_core_f32(hipStream_t s, const float *q, const float *k, const flo
                         int64_t ld_qkv, float *ctx, int64_t ldo, int64_t batch, int64_t seq,
                         int64_t n_heads, int64_t d_head, bool causal);
 
+// The same with grouped K/V heads: q rows have stride ldq and n_heads heads,
+// k/v rows stride ldk and n_heads / group heads (head h reads K/V head
+// h / group); causal, and window > 0 restricts query i to keys
+// [i − window + 1, i].
+void attention_core_gqa_f32(hipStream_t s, const float *q, const float *k, const float *v, int64_t ldq,
+                            int64_t ldk, int64_t group, int64_t window, float *ctx, int64_t ldo,
+                            int64_t batch, int64_t seq, int64_t n_heads, int64_t d_head);
+
+// Decoder ops (decoder.hip).
+void rms_norm_f32(hipStream_t s, const float *x, const float *w, float *y, int64_t rows, int64_t cols,
+                  float eps);
+// ids: n f32 token ids; *bad (device int) is set to 1 when an id ≥ vocab.
+void embedding_f32(hipStream_t s, const float *ids, int64_t n, const float *table, int64_t vocab,
+                   int64_t hidden, float *y, int *bad);
+void mix_f32(hipStream_t s, const float *a, const float *b, const float *gate, float *y, int64_t n);
+void transpose_f32(hipStream_t s, const float *src, int64_t rows, int64_t cols, float *dst);
+
+// GQA scratch, in floats: packed q|k|v rows [T, qkv_ld], ctx [T, n_heads·hd]
+// and the RoPE table [S, hd/2] of (cos, sin).
+struct GqaLayout {
+    int64_t qkv_ld, qkv, ctx, rope, floats;
+};
+GqaLayout gqa_layout(int64_t tokens, int64_t seq, int64_t n_heads, int64_t n_kv, int64_t head_dim);
+// y = GQA(x) (+ residual).  wqkv [D, qkv_ld] = [wq | wk | wv] per row, or
+// null to use the three projections separately.
+void gqa_f32(hipStream_t s, const float *x, const float *wqkv, const float *wq, const float *wk,
+             const float *wv, const float *wo, int64_t B, int64_t S, int64_t D, int64_t n_heads,
+             int64_t n_kv, int64_t head_dim, double theta, int64_t window, const float *residual,
+             float *y, float *scratch, const GqaLayout &L);
+// y = (silu(x·w1) ⊙ (x·w3))·w2 (+ residual); h is [T, I] scratch.
+void swiglu_f32(hipStream_t s, const float *x, const float *w1, const float *w3, const float *w2,
+                int64_t T, int64_t H, int64_t I, const float *residual, float *y, float *h);
+
 // MoE pieces.
 void moe_route_f32(hipStream_t s, const float *x, const float *gate, int64_t tokens,
                    int64_t hidden, int64_t n_experts, int64_t top_k, int32_t *idx, float *w,

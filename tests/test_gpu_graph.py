@@ -158,6 +158,10 @@ def test_error_kinds(device):
     emb = IrNode(1, "emb", OpenOp("embedding", (10, 4)), TensorType.f32([2, 8, 4]))
     with pytest.raises(CatError) as e:
         h.run_kernel(emb, [x])
+    assert e.value.kind == "UnknownPort" and "w" in str(e.value)  # mod.rs:82-85
+    mla = IrNode(1, "mla", OpenOp("mla", (2, 4, 4, 4, 4, 4, 10000)), TensorType.f32([2, 8]))
+    with pytest.raises(CatError) as e:
+        h.run_kernel(mla, [x])
     assert e.value.kind == "Unsupported"
     with pytest.raises(CatError) as e:
         h.run_kernel(IrNode(1, "r", OpenOp.relu(), x.ty), [])
