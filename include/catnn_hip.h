@@ -97,16 +97,17 @@ enum catnn_op_kind {
     CATNN_OP_RESHAPE = 10,      /* a = {out dims...}; data copy as eval_cpu */
     CATNN_OP_ATTENTION = 11,    /* a = {n_heads, d_model, d_head} */
     CATNN_OP_RESIDUAL_ADD = 12,
-    CATNN_OP_EMBEDDING = 13,
-    CATNN_OP_RMS_NORM = 14,
-    CATNN_OP_GQA_ATTENTION = 15,
-    CATNN_OP_SWIGLU = 16,
-    CATNN_OP_ROUTER = 17,
+    CATNN_OP_EMBEDDING = 13,    /* a = {vocab, hidden}; param "w" [vocab, hidden]; ids as f32 */
+    CATNN_OP_RMS_NORM = 14,     /* a = {eps_e6}; param "w" */
+    CATNN_OP_GQA_ATTENTION = 15, /* a = {n_heads, n_kv_heads, head_dim, d_model,
+                                    sliding_window (-1: None), rope_theta} */
+    CATNN_OP_SWIGLU = 16,       /* a = {hidden, intermediate}; params w1, w3, w2 */
+    CATNN_OP_ROUTER = 17,       /* a = {n_experts, top_k}; identity, as eval_cpu */
     CATNN_OP_MOE = 18,          /* a = {n_experts, top_k, hidden, intermediate} */
-    CATNN_OP_LM_HEAD = 19,
-    CATNN_OP_MLA = 20,
-    CATNN_OP_DEEPSEEK_MOE = 21,
-    CATNN_OP_MIX = 22
+    CATNN_OP_LM_HEAD = 19,      /* a = {hidden, vocab}; param "w" [vocab, hidden] */
+    CATNN_OP_MLA = 20,          /* not executable here: CATNN_ERR_UNSUPPORTED */
+    CATNN_OP_DEEPSEEK_MOE = 21, /* not executable here: CATNN_ERR_UNSUPPORTED */
+    CATNN_OP_MIX = 22           /* two inputs; optional param "gate" [1] */
 };
 
 /* Attention extension: causal mask with the masking convention of
