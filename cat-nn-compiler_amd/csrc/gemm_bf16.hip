@@ -34,6 +34,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 // MFMAs, so wider wavefront tiles relieve the LDS port.
 template <int BM_, int BN_, int WAVES_M_, int WAVES_N_, int BK_>
 struct Cfg {
+    static constexpr bool DMA = false;
     static constexpr int BM = BM_, BN = BN_, WAVES_M = WAVES_M_, WAVES_N = WAVES_N_;
     static constexpr int BK = BK_, LDT = BK + 8;  // LDS row stride (bf16): conflict-free b128 reads
     static constexpr int LDS_BYTES = 2 * (BM + BN) * LDT * 2;
@@ -46,12 +47,41 @@ struct Cfg {
                   "load split");
 };
 
-// All with 64 × 64 per wavefront: wider wavefront tiles (64 × 128) ran
-// slower on the training shapes (one wavefront per SIMD at 270+ registers).
+// Register-staged tiles of 64 × 64 per wavefront: the SwiGLU forward (two
+// B operands) and launches without 16-byte aligned rows.
 using Cfg0 = Cfg<128, 128, 2, 2, 32>;
 using Cfg2 = Cfg<128, 128, 2, 2, 64>;
-using Cfg3 = Cfg<256, 128, 4, 2, 32>;  // 8 wavefronts
-using Cfg4 = Cfg<256, 128, 4, 2, 64>;
+
+// Direct-to-LDS configurations: full k chunks (BK = 64) travel from HBM
+// into LDS by global_load_lds_dwordx4 without passing through registers,
+// STAGES chunks deep.  One such load fills 1 KiB of LDS contiguously, lane
+// l at byte 16·l, so rows are 128 bytes (8 chunks of 8 k values) with no
+// padding; a row's chunk c sits at position c ^ (row mod 8), which keeps the
+// MFMA operand reads (8 rows × one chunk per 8 lanes) on distinct banks.
+template <int BM_, int BN_, int WAVES_M_, int WAVES_N_, int STAGES_>
+struct DCfg {
+    static constexpr bool DMA = true;
+    static constexpr int BM = BM_, BN = BN_, WAVES_M = WAVES_M_, WAVES_N = WAVES_N_, STAGES = STAGES_;
+    static constexpr int BK = 64;
+    static constexpr int NT = 64 * WAVES_M * WAVES_N, NW = WAVES_M * WAVES_N;
+    static constexpr int FM = BM / (32 * WAVES_M), FN = BN / (32 * WAVES_N);
+    static constexpr int STAGE_BYTES = (BM + BN) * 128;
+    static constexpr int LDS_BYTES = STAGES * STAGE_BYTES;
+    // wave loads (8 rows each) per wavefront and k chunk
+    static constexpr int A_LD = BM / (8 * NW), B_LD = BN / (8 * NW), LPC = A_LD + B_LD;
+    static_assert(FM >= 1 && FN >= 1 && FM * 32 * WAVES_M == BM && FN * 32 * WAVES_N == BN, "tile");
+    static_assert(A_LD >= 1 && B_LD >= 1 && A_LD * 8 * NW == BM && B_LD * 8 * NW == BN, "load split");
+    static_assert(STAGES >= 2 && LDS_BYTES <= 160 * 1024, "LDS");
+    static_assert(LPC * (STAGES - 2) < 64, "vmcnt range");
+};
+
+// 128 × 128 tiles of four 64 × 64 wavefronts: two stages (64 KiB, two
+// blocks per CU) or three (96 KiB).  A sweep over the training shapes also
+// tried 256 × 128 tiles of eight wavefronts (three stages), 256 × 128 of four
+// 128 × 64 wavefronts and 256 × 256 of eight 128 × 64 wavefronts: those won
+// only on 8192³ (1067 against 981 TFLOP/s) and lost on the rest.
+using Cfg7 = DCfg<128, 128, 2, 2, 2>;
+using Cfg9 = DCfg<128, 128, 2, 2, 3>;
 
 
 __device__ __forceinline__ float bf2f(bf16_t v) { return __uint_as_float((uint32_t)v << 16); }
@@ -63,68 +93,106 @@ __device__ __forceinline__ bf16_t f2bf(float f) {
     return (bf16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
 }
 
-__device__ __forceinline__ float gelu_grad(float z) {
+// Activation functions of the training epilogues on the hardware exp2 and
+// reciprocal (about 1e-7 relative; every output they feed is rounded to
+// bf16 or enters a bf16 product).
+__device__ __forceinline__ float sigmoid_hw(float x) {
+    return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-1.44269504088896341f * x));
+}
+
+// tanh(u) = 1 − 2/(1 + e^{2u}); saturates to ±1 where e^{2u} overflows or
+// vanishes.
+__device__ __forceinline__ float tanh_hw(float u) {
+    return 1.0f - 2.0f * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(2.88539008177792682f * u));
+}
+
+__device__ __forceinline__ float gelu_hw(float z) {
+    const float c = 0.797884523868560791f;
+    return 0.5f * z * (1.0f + tanh_hw(c * (z + 0.044715f * z * z * z)));
+}
+
+__device__ __forceinline__ float gelu_grad_hw(float z) {
     const float C = 0.044715f, kk = 0.797884523868560791f;
-    const float u = kk * (z + C * z * z * z);
-    const float t = tanhf(u);
+    const float t = tanh_hw(kk * (z + C * z * z * z));
     const float du = kk * (1.0f + 3.0f * C * z * z);
     return 0.5f * (1.0f + t) + 0.5f * z * (1.0f - t * t) * du;
 }
 
-__device__ __forceinline__ float silu_grad(float x) {
-    const float s = 1.0f / (1.0f + expf(-x));
-    return s + x * s * (1.0f - s);
+// One output element of the epilogue kind EPI.
+template <bool DUAL, int EPI>
+__device__ __forceinline__ void epi_elem(const GemmBf16Params &p, float v, float c2, int row, int col,
+                                         float *__restrict__ C32) {
+    if constexpr (EPI == EPI_SWIGLU_FWD) {
+        const int64_t so = (int64_t)row * p.lds + col;
+        if (p.S1) p.S1[so] = f2bf(v);
+        if (p.S2) p.S2[so] = f2bf(c2);
+        p.Cb[(int64_t)row * p.ldcb + col] = f2bf(v * sigmoid_hw(v) * c2);
+        return;
+    } else if constexpr (EPI == EPI_SWIGLU_BWD) {
+        const int64_t so = (int64_t)row * p.lds + col;
+        const float a = bf2f(p.S1[so]), c = bf2f(p.S2[so]);
+        const float sg = sigmoid_hw(a);
+        // silu'(a) = σ(a)·(1 + a·(1 − σ(a)))
+        p.Cb[(int64_t)row * p.ldcb + col] = f2bf(v * c * (sg * (1.0f + a * (1.0f - sg))));
+        p.Cb2[(int64_t)row * p.ldcb + col] = f2bf(v * (a * sg));
+        return;
+    } else {
+        if constexpr (EPI == EPI_LINEAR) {
+            if (p.bias) v += p.bias[col];
+            if (p.Z) p.Z[(int64_t)row * p.ldz + col] = v;
+            if (p.act == 2) v = fmaxf(v, 0.0f);
+            else if (p.act == 3) v = gelu_hw(v);
+            if (p.R) v = p.R[(int64_t)row * p.ldr + col] + v;
+        } else if constexpr (EPI == EPI_GELU_BWD) {
+            v *= gelu_grad_hw(p.Z[(int64_t)row * p.ldz + col]);
+        }
+        if (C32) {
+            float *dst = C32 + (int64_t)row * p.ldc32 + col;
+            *dst = p.accumulate ? *dst + v : v;
+        }
+        if (p.Cb) p.Cb[(int64_t)row * p.ldcb + col] = f2bf(v);
+    }
 }
 
 // Epilogue of one wavefront's FM × FN accumulator blocks, one loop nest per
 // kind (fully unrolled, so the accumulators stay in registers).  Entry r of
 // block (mi, ni) is row wrow0 + 32·mi + 8(r/4) + r%4, column wcol0 + 32·ni.
-template <class C, bool DUAL, int EPI>
-__device__ __forceinline__ void epilogue(const GemmBf16Params &p, const f32x16 (&acc)[C::FM][C::FN],
-                                         int wrow0, int wcol0, int row_end, float *__restrict__ C32) {
+// A wavefront whose whole tile lies inside the output takes the loop
+// without bounds checks.
+template <class C, bool DUAL, int EPI, bool CHECK>
+__device__ __forceinline__ void epilogue_loop(const GemmBf16Params &p, const f32x16 (&acc)[C::FM][C::FN],
+                                              int wrow0, int wcol0, int row_end, float *__restrict__ C32) {
     constexpr int NF = DUAL ? C::FN / 2 : C::FN;
 #pragma unroll
     for (int mi = 0; mi < C::FM; ++mi)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const int row = wrow0 + mi * 32 + 8 * (r >> 2) + (r & 3);
-            if (row >= row_end) continue;
+            if (CHECK && row >= row_end) continue;
 #pragma unroll
             for (int ni = 0; ni < NF; ++ni) {
                 const int col = wcol0 + ni * 32;
-                if (col >= p.N) continue;
-                float v = acc[mi][ni][r];
-                if (EPI == EPI_SWIGLU_FWD) {
-                    const float c = acc[mi][ni + NF][r];
-                    const int64_t so = (int64_t)row * p.lds + col;
-                    if (p.S1) p.S1[so] = f2bf(v);
-                    if (p.S2) p.S2[so] = f2bf(c);
-                    p.Cb[(int64_t)row * p.ldcb + col] = f2bf(silu(v) * c);
-                    continue;
-                }
-                if (EPI == EPI_SWIGLU_BWD) {
-                    const int64_t so = (int64_t)row * p.lds + col;
-                    const float a = bf2f(p.S1[so]), c = bf2f(p.S2[so]);
-                    p.Cb[(int64_t)row * p.ldcb + col] = f2bf(v * c * silu_grad(a));
-                    p.Cb2[(int64_t)row * p.ldcb + col] = f2bf(v * silu(a));
-                    continue;
-                }
-                if (EPI == EPI_LINEAR) {
-                    if (p.bias) v += p.bias[col];
-                    if (p.Z) p.Z[(int64_t)row * p.ldz + col] = v;
-                    v = apply_act(v, p.act);
-                    if (p.R) v = p.R[(int64_t)row * p.ldr + col] + v;
-                } else if (EPI == EPI_GELU_BWD) {
-                    v *= gelu_grad(p.Z[(int64_t)row * p.ldz + col]);
-                }
-                if (C32) {
-                    float *dst = C32 + (int64_t)row * p.ldc32 + col;
-                    *dst = p.accumulate ? *dst + v : v;
-                }
-                if (p.Cb) p.Cb[(int64_t)row * p.ldcb + col] = f2bf(v);
+                if (CHECK && col >= p.N) continue;
+                epi_elem<DUAL, EPI>(p, acc[mi][ni][r], DUAL ? acc[mi][ni + NF][r] : 0.f, row, col, C32);
             }
         }
 }
+
+template <class C, bool DUAL, int EPI>
+__device__ __forceinline__ void epilogue(const GemmBf16Params &p, const f32x16 (&acc)[C::FM][C::FN], int wrow0,
+                                         int wcol0, int row_end, float *__restrict__ C32) {
+    constexpr int NF = DUAL ? C::FN / 2 : C::FN;
+    const int lane = threadIdx.x & 63;
+    // The wavefront's first row and column (lane 0's) and its extent.
+    const int r0 = wrow0 - 4 * (lane >> 5), c0 = wcol0 - (lane & 31);
+    const bool full = __builtin_amdgcn_readfirstlane(r0 + C::FM * 32 <= row_end && c0 + NF * 32 <= p.N);
+    if (full) epilogue_loop<C, DUAL, EPI, false>(p, acc, wrow0, wcol0, row_end, C32);
+    else epilogue_loop<C, DUAL, EPI, true>(p, acc, wrow0, wcol0, row_end, C32);
+}
+
+template <class C, bool DUAL, int GRID>
+__device__ __forceinline__ void finish(const GemmBf16Params &p, const f32x16 (&acc)[C::FM][C::FN], int wrow0,
+                                       int wcol0, int row_end, float *__restrict__ C32);
 
 template <class C, bool VEC, bool DUAL, int GRID>
 __device__ __forceinline__ void tile(bf16_t (*sa)[C::BM][C::LDT], bf16_t (*sb)[C::BN][C::LDT], const GemmBf16Params &p,
@@ -270,14 +338,18 @@ __device__ __forceinline__ void tile(bf16_t (*sa)[C::BM][C::LDT], bf16_t (*sb)[C
         }
     }
 
-    const int wrow0 = row0 + wm * (BM / C::WAVES_M) + 4 * lg;
-    const int wcol0 = col0 + wn * WCOLS + lr;
-    if (DUAL) {
+    finish<C, DUAL, GRID>(p, acc, row0 + wm * (BM / C::WAVES_M) + 4 * lg, col0 + wn * WCOLS + lr, row_end,
+                          C32);
+}
+
+// Each grid is built only with the epilogues the training step uses on it.
+template <class C, bool DUAL, int GRID>
+__device__ __forceinline__ void finish(const GemmBf16Params &p, const f32x16 (&acc)[C::FM][C::FN], int wrow0,
+                                       int wcol0, int row_end, float *__restrict__ C32) {
+    if constexpr (DUAL) {
         epilogue<C, true, EPI_SWIGLU_FWD>(p, acc, wrow0, wcol0, row_end, C32);
         return;
-    }
-    // Each grid is built only with the epilogues the training step uses on it.
-    if constexpr (GRID == GRID_PLAIN) {
+    } else if constexpr (GRID == GRID_PLAIN) {
         switch (p.epi) {
             case EPI_LINEAR: epilogue<C, false, EPI_LINEAR>(p, acc, wrow0, wcol0, row_end, C32); break;
             case EPI_GELU_BWD: epilogue<C, false, EPI_GELU_BWD>(p, acc, wrow0, wcol0, row_end, C32); break;
@@ -291,11 +363,339 @@ __device__ __forceinline__ void tile(bf16_t (*sa)[C::BM][C::LDT], bf16_t (*sb)[C
     }
 }
 
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// s_waitcnt with vmcnt ≤ N, lgkmcnt 0 (every LDS access of this wavefront
+// done), expcnt unconstrained; then the block barrier.  The empty asm
+// statements keep the compiler from moving memory accesses across; the
+// barrier builtin itself carries no fence, so the waits stay exactly these.
+template <int N>
+__device__ __forceinline__ void dma_sync() {
+    static_assert(N >= 0 && N < 64, "vmcnt");
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+__device__ __forceinline__ void unpack8(uint4 w, float (&f)[8]) {
+    const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        f[2 * j] = __uint_as_float(u[j] << 16);
+        f[2 * j + 1] = __uint_as_float(u[j] & 0xffff0000u);
+    }
+}
+
+__device__ __forceinline__ uint4 pack8(const float (&f)[8]) {
+    uint32_t u[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) u[j] = (uint32_t)f2bf(f[2 * j]) | ((uint32_t)f2bf(f[2 * j + 1]) << 16);
+    return make_uint4(u[0], u[1], u[2], u[3]);
+}
+
+__device__ __forceinline__ void load8f(const float *src, float (&f)[8]) {
+    const float4 a = *reinterpret_cast<const float4 *>(src), b = *reinterpret_cast<const float4 *>(src + 4);
+    f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w; f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+}
+
+__device__ __forceinline__ void store8f(float *dst, const float (&f)[8]) {
+    *reinterpret_cast<float4 *>(dst) = make_float4(f[0], f[1], f[2], f[3]);
+    *reinterpret_cast<float4 *>(dst + 4) = make_float4(f[4], f[5], f[6], f[7]);
+}
+
+// Eight consecutive outputs (row, col … col+7) of epilogue kind EPI with
+// 16-byte accesses; the same arithmetic per element as epi_elem.
+template <int EPI>
+__device__ __forceinline__ void epi_vec8(const GemmBf16Params &p, float (&v)[8], int row, int col,
+                                         float *__restrict__ C32) {
+    if constexpr (EPI == EPI_SWIGLU_BWD) {
+        const int64_t so = (int64_t)row * p.lds + col;
+        float a[8], c[8], d1[8], d2[8];
+        unpack8(*reinterpret_cast<const uint4 *>(p.S1 + so), a);
+        unpack8(*reinterpret_cast<const uint4 *>(p.S2 + so), c);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float sg = sigmoid_hw(a[j]);
+            d1[j] = v[j] * c[j] * (sg * (1.0f + a[j] * (1.0f - sg)));
+            d2[j] = v[j] * (a[j] * sg);
+        }
+        *reinterpret_cast<uint4 *>(p.Cb + (int64_t)row * p.ldcb + col) = pack8(d1);
+        *reinterpret_cast<uint4 *>(p.Cb2 + (int64_t)row * p.ldcb + col) = pack8(d2);
+    } else {
+        if constexpr (EPI == EPI_LINEAR) {
+            if (p.bias) {
+                float b[8];
+                load8f(p.bias + col, b);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) v[j] += b[j];
+            }
+            if (p.Z) store8f(p.Z + (int64_t)row * p.ldz + col, v);
+            if (p.act == 2) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) v[j] = fmaxf(v[j], 0.0f);
+            } else if (p.act == 3) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) v[j] = gelu_hw(v[j]);
+            }
+            if (p.R) {
+                float r[8];
+                load8f(p.R + (int64_t)row * p.ldr + col, r);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) v[j] = r[j] + v[j];
+            }
+        } else if constexpr (EPI == EPI_GELU_BWD) {
+            float z[8];
+            load8f(p.Z + (int64_t)row * p.ldz + col, z);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] *= gelu_grad_hw(z[j]);
+        }
+        if (C32) {
+            float *dst = C32 + (int64_t)row * p.ldc32 + col;
+            if (p.accumulate) {
+                float o[8];
+                load8f(dst, o);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) v[j] = o[j] + v[j];
+            }
+            store8f(dst, v);
+        }
+        if (p.Cb) *reinterpret_cast<uint4 *>(p.Cb + (int64_t)row * p.ldcb + col) = pack8(v);
+    }
+}
+
+// Epilogue of a block whose whole tile lies inside the output: the
+// accumulators go through LDS (free once the last k chunk is consumed) so
+// that each thread finishes runs of 8 consecutive columns with 16-byte
+// loads and stores.
+// DUAL (SwiGLU forward): the staged tile holds a = x·w1 in columns
+// [0, BN/2) and c = x·w3 in [BN/2, BN) for the BN/2 output columns.
+template <class C, bool DUAL>
+__device__ __forceinline__ int staged_col(int wn, int ni, int lr) {
+    if constexpr (DUAL) {
+        constexpr int H = C::FN / 2, WCOLS = C::BN / 2 / C::WAVES_N;
+        return (ni < H ? 0 : C::BN / 2) + wn * WCOLS + (ni % H) * 32 + lr;
+    } else {
+        return wn * (C::BN / C::WAVES_N) + ni * 32 + lr;
+    }
+}
+
+template <class C, bool DUAL, int EPI>
+__device__ __forceinline__ void epilogue_staged(unsigned char *smem, const GemmBf16Params &p,
+                                                const f32x16 (&acc)[C::FM][C::FN], int row0, int col0,
+                                                float *__restrict__ C32) {
+    constexpr int BM = C::BM, BN = C::BN, WM = BM / C::WAVES_M, CH = (DUAL ? BN / 2 : BN) / 8;
+    static_assert(BM * BN * 4 <= C::LDS_BYTES, "the staged tile must fit the operand stages");
+    float *t = reinterpret_cast<float *>(smem);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = wave / C::WAVES_N, wn = wave % C::WAVES_N, lr = lane & 31, lg = lane >> 5;
+    dma_sync<0>();  // every wavefront is done with the operand stages
+#pragma unroll
+    for (int mi = 0; mi < C::FM; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < C::FN; ++ni)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                t[(wm * WM + mi * 32 + 8 * (r >> 2) + 4 * lg + (r & 3)) * BN + staged_col<C, DUAL>(wn, ni, lr)] =
+                    acc[mi][ni][r];
+    dma_sync<0>();
+    for (int idx = threadIdx.x; idx < BM * CH; idx += C::NT) {
+        const int r = idx / CH, c = (idx % CH) * 8;
+        float v[8];
+        load8f(t + r * BN + c, v);
+        if constexpr (DUAL) {
+            float cv[8], h[8];
+            load8f(t + r * BN + BN / 2 + c, cv);
+            const int64_t so = (int64_t)(row0 + r) * p.lds + col0 + c;
+            if (p.S1) *reinterpret_cast<uint4 *>(p.S1 + so) = pack8(v);
+            if (p.S2) *reinterpret_cast<uint4 *>(p.S2 + so) = pack8(cv);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) h[j] = v[j] * sigmoid_hw(v[j]) * cv[j];
+            *reinterpret_cast<uint4 *>(p.Cb + (int64_t)(row0 + r) * p.ldcb + col0 + c) = pack8(h);
+        } else {
+            epi_vec8<EPI>(p, v, row0 + r, col0 + c, C32);
+        }
+    }
+}
+
+template <class C, bool DUAL, int GRID>
+__device__ __forceinline__ void finish_staged(unsigned char *smem, const GemmBf16Params &p,
+                                              const f32x16 (&acc)[C::FM][C::FN], int row0, int col0,
+                                              float *__restrict__ C32) {
+    if constexpr (DUAL) {
+        epilogue_staged<C, true, EPI_SWIGLU_FWD>(smem, p, acc, row0, col0, C32);
+    } else if constexpr (GRID == GRID_PLAIN) {
+        switch (p.epi) {
+            case EPI_LINEAR: epilogue_staged<C, false, EPI_LINEAR>(smem, p, acc, row0, col0, C32); break;
+            case EPI_GELU_BWD: epilogue_staged<C, false, EPI_GELU_BWD>(smem, p, acc, row0, col0, C32); break;
+            default: epilogue_staged<C, false, EPI_STORE>(smem, p, acc, row0, col0, C32);
+        }
+    } else if constexpr (GRID == GRID_ROWS) {
+        if (p.epi == EPI_SWIGLU_BWD) epilogue_staged<C, false, EPI_SWIGLU_BWD>(smem, p, acc, row0, col0, C32);
+        else epilogue_staged<C, false, EPI_STORE>(smem, p, acc, row0, col0, C32);
+    } else {
+        epilogue_staged<C, false, EPI_STORE>(smem, p, acc, row0, col0, C32);
+    }
+}
+
+// The direct-to-LDS main loop (DCfg): chunk kt lands in stage kt mod STAGES;
+// at the top of iteration kt a wavefront waits for its own loads of chunk kt
+// (later chunks may stay in flight), the barrier makes every wavefront's
+// loads visible and retires the reads of chunk kt−1, whose stage then takes
+// chunk kt+STAGES−1.  A partial last chunk goes through registers (zero
+// past k_hi).
+// DUAL: B rows [0, BN/2) of the tile come from B (W1ᵀ) and [BN/2, BN) from
+// B2 (W3ᵀ) at the same BN/2 output columns.
+template <class C, bool DUAL, int GRID>
+__device__ __forceinline__ void tile_dma(unsigned char *smem, const GemmBf16Params &p, const bf16_t *__restrict__ B,
+                                         const bf16_t *__restrict__ B2, int row0, int row_end, int col0, int k_lo,
+                                         int k_hi, float *__restrict__ C32) {
+    constexpr int BM = C::BM, BN = C::BN, FM = C::FM, FN = C::FN, BK = C::BK;
+    constexpr int BN_OUT = DUAL ? BN / 2 : BN, WCOLS = BN_OUT / C::WAVES_N;
+    // B row r of the tile: operand and output column.
+    auto b_row_src = [&](int r, int &n) -> const bf16_t * {
+        if (DUAL && r >= BN / 2) {
+            n = col0 + r - BN / 2;
+            return B2;
+        }
+        n = col0 + r;
+        return B;
+    };
+    // wave is uniform across the wavefront; readfirstlane lets the LDS
+    // destinations (M0) come from a scalar register.
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / C::WAVES_N, wn = wave % C::WAVES_N;
+    const int lr = lane & 31, lg = lane >> 5;
+
+    // Wave load q of a wavefront fills tile rows 8·(wave·LD + q) … +7: lane l
+    // row … + l/8 at position l mod 8, i.e. k chunk (l mod 8) ^ (l/8).  Rows
+    // past the tile's end read row row0 (col0 for B): their outputs are never
+    // stored.
+    const int dk = (((lane & 7) ^ (lane >> 3)) * 8);
+    const bf16_t *a_src[C::A_LD];
+#pragma unroll
+    for (int q = 0; q < C::A_LD; ++q) {
+        int gr = row0 + (wave * C::A_LD + q) * 8 + (lane >> 3);
+        if (gr >= row_end) gr = row0;
+        const int src = p.a_rows ? p.a_rows[gr] / p.a_row_div : gr;
+        a_src[q] = p.A + (int64_t)src * p.lda + dk;
+    }
+    const bf16_t *b_src[C::B_LD];
+#pragma unroll
+    for (int q = 0; q < C::B_LD; ++q) {
+        int n;
+        const bf16_t *base = b_row_src((wave * C::B_LD + q) * 8 + (lane >> 3), n);
+        if (n >= p.N) n = col0;
+        b_src[q] = base + (int64_t)n * p.ldb + dk;
+    }
+    auto issue = [&](int kt) {
+        unsigned char *st = smem + (kt % C::STAGES) * C::STAGE_BYTES;
+        const int k0 = k_lo + kt * BK;
+#pragma unroll
+        for (int q = 0; q < C::A_LD; ++q)
+            __builtin_amdgcn_global_load_lds(a_src[q] + k0, (lds_void_t *)(st + (wave * C::A_LD + q) * 1024), 16, 0, 0);
+#pragma unroll
+        for (int q = 0; q < C::B_LD; ++q)
+            __builtin_amdgcn_global_load_lds(b_src[q] + k0,
+                                             (lds_void_t *)(st + BM * 128 + (wave * C::B_LD + q) * 1024), 16, 0, 0);
+    };
+
+    f32x16 acc[FM][FN];
+#pragma unroll
+    for (int mi = 0; mi < FM; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < FN; ++ni)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[mi][ni][r] = 0.f;
+
+    // Lane l reads k values 16s + 8(l/32) … +7 of row l mod 32 of each block.
+    const int a_off = (wm * (BM / C::WAVES_M) + lr) * 128;
+    const int sw = lr & 7;
+    auto b_off = [&](int ni) { return (BM + staged_col<C, DUAL>(wn, ni, lr)) * 128; };
+    auto compute = [&](const unsigned char *st) {
+#pragma unroll
+        for (int s = 0; s < BK / 16; ++s) {
+            const int pos = ((2 * s + lg) ^ sw) << 4;
+            bf16x8 af[FM], bfr[FN];
+#pragma unroll
+            for (int mi = 0; mi < FM; ++mi)
+                af[mi] = *reinterpret_cast<const bf16x8 *>(st + a_off + mi * 32 * 128 + pos);
+#pragma unroll
+            for (int ni = 0; ni < FN; ++ni)
+                bfr[ni] = *reinterpret_cast<const bf16x8 *>(st + b_off(ni) + pos);
+#pragma unroll
+            for (int mi = 0; mi < FM; ++mi)
+#pragma unroll
+                for (int ni = 0; ni < FN; ++ni)
+                    acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mi], bfr[ni], acc[mi][ni], 0, 0, 0);
+        }
+    };
+
+    const int nfull = (k_hi - k_lo) / BK;
+#pragma unroll
+    for (int j = 0; j < C::STAGES - 1; ++j)
+        if (j < nfull) issue(j);
+    for (int kt = 0; kt < nfull; ++kt) {
+        if (C::STAGES > 2 && kt + 1 < nfull) dma_sync<C::LPC * (C::STAGES - 2)>();
+        else dma_sync<0>();
+        if (kt + C::STAGES - 1 < nfull) issue(kt + C::STAGES - 1);
+        compute(smem + (kt % C::STAGES) * C::STAGE_BYTES);
+    }
+    const int kt0 = k_lo + nfull * BK;
+    if (kt0 < k_hi) {
+        dma_sync<0>();
+        for (int idx = tid; idx < (BM + C::BN) * 8; idx += C::NT) {
+            const int r = idx >> 3, c = idx & 7, kk = kt0 + 8 * c;
+            const bf16_t *src = nullptr;
+            if (r < BM) {
+                const int gr = row0 + r;
+                if (gr < row_end) src = p.A + (int64_t)(p.a_rows ? p.a_rows[gr] / p.a_row_div : gr) * p.lda;
+            } else {
+                int n;
+                const bf16_t *base = b_row_src(r - BM, n);
+                if (n < p.N) src = base + (int64_t)n * p.ldb;
+            }
+            uint4 v = make_uint4(0, 0, 0, 0);
+            if (src && kk < k_hi) {
+                if (kk + 8 <= k_hi) {
+                    v = *reinterpret_cast<const uint4 *>(src + kk);
+                } else {
+                    uint16_t e[8];
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) e[j] = kk + j < k_hi ? src[kk + j] : 0;
+                    v = make_uint4(e[0] | (uint32_t)e[1] << 16, e[2] | (uint32_t)e[3] << 16,
+                                   e[4] | (uint32_t)e[5] << 16, e[6] | (uint32_t)e[7] << 16);
+                }
+            }
+            *reinterpret_cast<uint4 *>(smem + r * 128 + ((c ^ (r & 7)) << 4)) = v;
+        }
+        dma_sync<0>();
+        compute(smem);
+    }
+    if (p.vec_epi && row0 + BM <= row_end && col0 + BN_OUT <= p.N)
+        finish_staged<C, DUAL, GRID>(smem, p, acc, row0, col0, C32);
+    else
+        finish<C, DUAL, GRID>(p, acc, row0 + wm * (BM / C::WAVES_M) + 4 * lg, col0 + wn * WCOLS + lr, row_end,
+                              C32);
+}
+
+template <class C, bool VEC, bool DUAL, int GRID>
+__device__ __forceinline__ void run_tile(unsigned char *smem, const GemmBf16Params &p, const bf16_t *B,
+                                         const bf16_t *B2, int row0, int row_end, int col0, int k_lo, int k_hi,
+                                         float *C32) {
+    if constexpr (C::DMA) {
+        static_assert(VEC, "direct-to-LDS tiles take 16-byte aligned rows");
+        tile_dma<C, DUAL, GRID>(smem, p, B, B2, row0, row_end, col0, k_lo, k_hi, C32);
+    } else {
+        auto sa = reinterpret_cast<bf16_t(*)[C::BM][C::LDT]>(smem);
+        auto sb = reinterpret_cast<bf16_t(*)[C::BN][C::LDT]>(smem + 2 * C::BM * C::LDT * 2);
+        tile<C, VEC, DUAL, GRID>(sa, sb, p, B, B2, row0, row_end, col0, k_lo, k_hi, C32);
+    }
+}
+
 template <class C, bool VEC, bool DUAL, int GRID>
 __global__ __launch_bounds__(C::NT) void gemm_bf16_kernel(GemmBf16Params p) {
     extern __shared__ __align__(16) unsigned char smem[];
-    auto sa = reinterpret_cast<bf16_t(*)[C::BM][C::LDT]>(smem);
-    auto sb = reinterpret_cast<bf16_t(*)[C::BN][C::LDT]>(smem + 2 * C::BM * C::LDT * 2);
     const int bn_out = DUAL ? C::BN / 2 : C::BN;
     const int tiles_n = (p.N + bn_out - 1) / bn_out;
     const int lid = xcd_remap(blockIdx.x, gridDim.x);
@@ -303,7 +703,7 @@ __global__ __launch_bounds__(C::NT) void gemm_bf16_kernel(GemmBf16Params p) {
         const int tiles_m = (p.M + C::BM - 1) / C::BM;
         int tm, tn;
         grouped_tile(lid, tiles_m, tiles_n, 8, tm, tn);
-        tile<C, VEC, DUAL, GRID>(sa, sb, p, p.B, p.B2, tm * C::BM, p.M, tn * bn_out, 0, p.K, p.C32);
+        run_tile<C, VEC, DUAL, GRID>(smem, p, p.B, p.B2, tm * C::BM, p.M, tn * bn_out, 0, p.K, p.C32);
     } else if constexpr (GRID == GRID_ROWS) {
         // Tiles of the table are kRowTile rows; C::BM equals it for this grid.
         int tm, tn;
@@ -311,8 +711,8 @@ __global__ __launch_bounds__(C::NT) void gemm_bf16_kernel(GemmBf16Params p) {
         if (tm >= *p.n_tiles) return;
         const int e = p.tile_expert[tm];
         const int end = p.seg_counts ? p.seg_offsets[e] + p.seg_counts[e] : p.seg_offsets[e + 1];
-        tile<C, VEC, DUAL, GRID>(sa, sb, p, p.B_e[e], DUAL ? p.B2_e[e] : nullptr, p.tile_row0[tm], end,
-                                 tn * bn_out, 0, p.K, p.C32);
+        run_tile<C, VEC, DUAL, GRID>(smem, p, p.B_e[e], DUAL ? p.B2_e[e] : nullptr, p.tile_row0[tm], end,
+                                     tn * bn_out, 0, p.K, p.C32);
     } else {  // GRID_SEGK: expert e = blockIdx.y reduces over its own K segment
         const int tiles_m = (p.M + C::BM - 1) / C::BM;
         int tm, tn;
@@ -320,11 +720,20 @@ __global__ __launch_bounds__(C::NT) void gemm_bf16_kernel(GemmBf16Params p) {
         const int e = blockIdx.y;
         const int lo = p.seg_offsets[e];
         const int hi = p.seg_counts ? lo + p.seg_counts[e] : p.seg_offsets[e + 1];
-        tile<C, VEC, DUAL, GRID>(sa, sb, p, p.B, nullptr, tm * C::BM, p.M, tn * bn_out, lo, hi, p.C_e[e]);
+        run_tile<C, VEC, DUAL, GRID>(smem, p, p.B, nullptr, tm * C::BM, p.M, tn * bn_out, lo, hi, p.C_e[e]);
     }
 }
 
 bool al16(const void *q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; }
+
+bool epi_rows_aligned(const GemmBf16Params &p) {
+    auto ok = [](const void *ptr, int64_t ld) { return !ptr || (al16(ptr) && ld % 8 == 0); };
+    bool a = ok(p.C32, p.ldc32) && ok(p.Cb, p.ldcb) && ok(p.Cb2, p.ldcb) && ok(p.S1, p.lds) && ok(p.S2, p.lds) &&
+             ok(p.Z, p.ldz) && ok(p.R, p.ldr) && (!p.bias || al16(p.bias));
+    if (p.grid == GRID_SEGK)
+        for (int e = 0; e < p.n_experts; ++e) a = a && ok(p.C_e[e], p.ldc32);
+    return a;
+}
 
 constexpr int kRowTile = 128;  // rows per tile of the grouped tile table (build_tiles)
 
@@ -332,15 +741,25 @@ template <class C, int GRID, bool DUAL>
 void launch_kernel(hipStream_t s, const GemmBf16Params &p, bool vec, dim3 grid) {
     // Tiles above 64 KiB of LDS need the per-kernel opt-in (gfx950: 160 KiB per CU).
     static bool attr_set = false;
-    if (!attr_set) {
-        CATNN_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_bf16_kernel<C, true, DUAL, GRID>),
-                                      hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS_BYTES));
-        CATNN_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_bf16_kernel<C, false, DUAL, GRID>),
-                                      hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS_BYTES));
-        attr_set = true;
+    if constexpr (C::DMA) {
+        CATNN_REQUIRE(vec, CATNN_ERR_INVALID_ARGUMENT, "bf16 gemm: direct-to-LDS tiles need 16-byte aligned rows");
+        if (!attr_set) {
+            CATNN_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_bf16_kernel<C, true, DUAL, GRID>),
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS_BYTES));
+            attr_set = true;
+        }
+        gemm_bf16_kernel<C, true, DUAL, GRID><<<grid, dim3(C::NT), C::LDS_BYTES, s>>>(p);
+    } else {
+        if (!attr_set) {
+            CATNN_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_bf16_kernel<C, true, DUAL, GRID>),
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS_BYTES));
+            CATNN_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(gemm_bf16_kernel<C, false, DUAL, GRID>),
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS_BYTES));
+            attr_set = true;
+        }
+        if (vec) gemm_bf16_kernel<C, true, DUAL, GRID><<<grid, dim3(C::NT), C::LDS_BYTES, s>>>(p);
+        else gemm_bf16_kernel<C, false, DUAL, GRID><<<grid, dim3(C::NT), C::LDS_BYTES, s>>>(p);
     }
-    if (vec) gemm_bf16_kernel<C, true, DUAL, GRID><<<grid, dim3(C::NT), C::LDS_BYTES, s>>>(p);
-    else gemm_bf16_kernel<C, false, DUAL, GRID><<<grid, dim3(C::NT), C::LDS_BYTES, s>>>(p);
     CATNN_HIP(hipGetLastError());
 }
 
@@ -410,30 +829,40 @@ void gemm_bf16_launch_cfg(hipStream_t s, const GemmBf16Params &p, int cfg) {
             gy = (unsigned)p.n_experts;
         }
     }
+    if (cfg >= 7 && !vec) cfg = dual ? 0 : 2;  // direct-to-LDS tiles need 16-byte aligned rows
+    // The staged epilogue moves 8 consecutive outputs per access: every
+    // output, saved and residual row must start on a 16-byte boundary.
+    GemmBf16Params q = p;
+    q.vec_epi = epi_rows_aligned(p);
     switch (cfg) {
-        case 0: launch_cfg<Cfg0, true>(s, p, vec, dual, gy); break;
-        case 2: launch_cfg<Cfg2, false>(s, p, vec, dual, gy); break;
-        case 3: launch_cfg<Cfg3, false>(s, p, vec, dual, gy); break;
-        case 4: launch_cfg<Cfg4, false>(s, p, vec, dual, gy); break;
+        case 0: launch_cfg<Cfg0, true>(s, q, vec, dual, gy); break;
+        case 2: launch_cfg<Cfg2, false>(s, q, vec, dual, gy); break;
+        case 7: launch_cfg<Cfg7, true>(s, q, vec, dual, gy); break;
+        case 9: launch_cfg<Cfg9, false>(s, q, vec, dual, gy); break;
         default: fail(CATNN_ERR_INVALID_ARGUMENT, "bf16 gemm: unknown tile configuration");
     }
 }
 
 // Tile choice, from a sweep of the training step's shapes on MI355X
-// (TFLOP/s of cfg 3 / 4 / 2): 256×128 tiles with BK 32 when there are at
-// least four of them per CU (8192×4096×3072: 831/785/800), BK 64 when there
-// are one to four (8192×1024×12288: 665/917/883), 128×128 with BK 64 below
-// that (4096×1024×8192: 385/510/613).  Grouped-row grids need 128-row tiles.
+// (TFLOP/s).  The direct-to-LDS 128×128 tile with two blocks per CU
+// (configuration 7) leads on nearly all of them: 8192×4096×3072 898 (best
+// register-staged tile 742), 8192×1024×12288 947 (881), 8192×1024×4096 809
+// (778).  When the grid holds at most one 128×128 tile per CU — the long-k
+// weight gradients, 4096×1024×8192 — three stages in flight (configuration
+// 9) gain a little more: 773 against 745.  The SwiGLU forward (two B
+// operands, half the output columns) runs on configuration 7 as well;
+// launches without 16-byte aligned rows run on the register-staged tiles
+// (configuration 0 for the SwiGLU forward, 2 otherwise).
 void gemm_bf16_launch(hipStream_t s, const GemmBf16Params &p) {
-    // The SwiGLU epilogues (two outputs per element) run best on the
-    // 128×128×32 tile (config-5 expert GEMMs: 442 vs 545 µs forward).
-    int cfg = p.epi == EPI_SWIGLU_FWD || p.epi == EPI_SWIGLU_BWD ? 0 : 2;
-    if (p.grid != GRID_ROWS && p.epi != EPI_SWIGLU_FWD) {
-        const int64_t t3 = (int64_t)((p.M + 255) / 256) * ((p.N + 127) / 128) *
-                           (p.grid == GRID_SEGK ? p.n_experts : 1);
-        cfg = t3 >= 1024 ? 3 : t3 >= 256 ? 4 : 2;
+    if (p.epi == EPI_SWIGLU_FWD) {
+        gemm_bf16_launch_cfg(s, p, 7);
+        return;
     }
-    gemm_bf16_launch_cfg(s, p, cfg);
+    const int64_t tn = (p.N + 127) / 128;
+    const int64_t tiles = p.grid == GRID_ROWS ? (int64_t)p.max_tiles * tn
+                                              : (int64_t)((p.M + 127) / 128) * tn *
+                                                    (p.grid == GRID_SEGK ? p.n_experts : 1);
+    gemm_bf16_launch_cfg(s, p, p.grid != GRID_ROWS && tiles <= 256 ? 9 : 7);
 }
 
 }  // namespace k

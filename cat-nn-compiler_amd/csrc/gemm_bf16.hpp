@@ -61,6 +61,7 @@ struct GemmBf16Params {
     const int32_t *seg_offsets;  // segment e starts at seg_offsets[e]
     const int32_t *seg_counts;   // ... and holds seg_counts[e] rows (null: ends at seg_offsets[e+1])
     int segk_aligned;            // GRID_SEGK: caller guarantees seg_offsets[e] % 8 == 0
+    int vec_epi;                 // set by the launcher: output rows allow 16-byte epilogue accesses
     int max_tiles;
     int n_experts;
     const bf16_t *B_e[kMaxExperts];
@@ -69,7 +70,7 @@ struct GemmBf16Params {
 };
 
 void gemm_bf16_launch(hipStream_t s, const GemmBf16Params &p);
-// The same with a fixed tile configuration (0, 2, 3 or 4; see gemm_bf16.hip).
+// The same with a fixed tile configuration (0, 2, 7 or 9; see gemm_bf16.hip).
 void gemm_bf16_launch_cfg(hipStream_t s, const GemmBf16Params &p, int cfg);
 int gemm_bf16_tile_rows();
 

@@ -80,10 +80,12 @@ def _bf16_bits(a):
 GEMM_BF16_CASES = [
     (1, 1, 1), (5, 7, 3), (130, 100, 70), (129, 257, 255), (300, 64, 520),
     (256, 512, 384), (1024, 1024, 1024), (200, 3 * 784, 10),
+    # 16-byte rows with a partial last k chunk, and k below one chunk
+    (129, 257, 264), (77, 130, 136), (300, 200, 40), (513, 385, 1000),
 ]
 
 
-@pytest.mark.parametrize("tile_cfg", [0, 2, 3, 4])
+@pytest.mark.parametrize("tile_cfg", [0, 2, 7, 9])
 @pytest.mark.parametrize("m,n,k", GEMM_BF16_CASES)
 def test_gemm_bf16_matches_float64(device, m, n, k, tile_cfg):
     # bf16 operands, fp32 accumulation: only the accumulation rounds.
