@@ -84,6 +84,72 @@ __global__ __launch_bounds__(256) void transpose_kernel(const TS *__restrict__ s
     }
 }
 
+// The same transpose for full 64×64 tiles with 16-byte global accesses:
+// each thread reads 16-byte runs of source rows (8 bf16 or 4 f32) into an
+// LDS tile (row stride 72 bf16), then gathers 8 consecutive source rows of
+// one column — a wavefront reads 128 contiguous LDS bytes per step — and
+// writes them as one 16-byte run of a destination row.  Launched only where
+// the host has checked alignment; edge tiles take transpose_kernel.
+template <typename TS>
+__global__ __launch_bounds__(256) void transpose_vec_kernel(const TS *__restrict__ src, int64_t lds,
+                                                            const int32_t *__restrict__ rows_map, int div,
+                                                            int rows, int cols, bf16_t *__restrict__ dst,
+                                                            int64_t ldd) {
+    constexpr int VPL = 16 / sizeof(TS);  // source values per 16-byte load
+    __shared__ __align__(16) bf16_t t[64][72];
+    const int r0 = blockIdx.y * 64, c0 = blockIdx.x * 64;
+    const int tid = threadIdx.x;
+    if (r0 + 64 > rows || c0 + 64 > cols) {
+        // edge tile: element path
+        const int tx = tid & 63, ty = tid >> 6;
+        for (int i = ty; i < 64; i += 4) {
+            const int r = r0 + i, c = c0 + tx;
+            bf16_t v = 0;
+            if (r < rows && c < cols) {
+                const int sr = rows_map ? (rows_map[r] < 0 ? -1 : rows_map[r] / div) : r;
+                if (sr >= 0) {
+                    if constexpr (sizeof(TS) == 4) v = f2bf(src[(int64_t)sr * lds + c]);
+                    else v = src[(int64_t)sr * lds + c];
+                }
+            }
+            t[i][tx] = v;
+        }
+        __syncthreads();
+        for (int i = ty; i < 64; i += 4) {
+            const int c = c0 + i, r = r0 + tx;
+            if (c < cols && r < rows) dst[(int64_t)c * ldd + r] = t[tx][i];
+        }
+        return;
+    }
+    constexpr int PER_ROW = 64 / VPL;
+#pragma unroll
+    for (int j = 0; j < 64 * PER_ROW / 256; ++j) {
+        const int idx = tid + 256 * j, i = idx / PER_ROW, cc = (idx % PER_ROW) * VPL;
+        const int r = r0 + i;
+        const int sr = rows_map ? (rows_map[r] < 0 ? -1 : rows_map[r] / div) : r;
+        uint4 w = make_uint4(0, 0, 0, 0);
+        if (sr >= 0) w = *reinterpret_cast<const uint4 *>(src + (int64_t)sr * lds + c0 + cc);
+        if constexpr (sizeof(TS) == 4) {
+            const uint32_t lo = (uint32_t)f2bf(__uint_as_float(w.x)) | ((uint32_t)f2bf(__uint_as_float(w.y)) << 16);
+            const uint32_t hi = (uint32_t)f2bf(__uint_as_float(w.z)) | ((uint32_t)f2bf(__uint_as_float(w.w)) << 16);
+            *reinterpret_cast<uint2 *>(&t[i][cc]) = make_uint2(lo, hi);
+        } else {
+            *reinterpret_cast<uint4 *>(&t[i][cc]) = w;
+        }
+    }
+    __syncthreads();
+    const int oc = tid & 63;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int k = (tid >> 6) + 4 * j;  // source rows 8k … 8k+7
+        uint32_t u[4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+            u[m] = (uint32_t)t[8 * k + 2 * m][oc] | ((uint32_t)t[8 * k + 2 * m + 1][oc] << 16);
+        *reinterpret_cast<uint4 *>(dst + (int64_t)(c0 + oc) * ldd + r0 + 8 * k) = make_uint4(u[0], u[1], u[2], u[3]);
+    }
+}
+
 // Split-bf16 operands.  v = hi + lo + O(2⁻¹⁷|v|) with hi = bf16(v) and
 // lo = bf16(v − hi).  A row of A' = [hi | hi | lo] against a row of
 // B' = [hi | lo | hi] sums to hi·hi + hi·lo + lo·hi over 3K: an fp32 product
@@ -534,26 +600,34 @@ void cast_f32_bf16(hipStream_t s, const float *x, bf16_t *y, int64_t n) {
     CATNN_HIP(hipGetLastError());
 }
 
+static bool al16(const void *q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; }
+
 static dim3 tgrid(int rows, int cols) {
     return dim3((unsigned)((cols + 63) / 64), (unsigned)((rows + 63) / 64));
 }
 
-void transpose_bf16(hipStream_t s, const bf16_t *src, int64_t lds, const int32_t *rows_map, int div,
-                    int rows, int cols, bf16_t *dst, int64_t ldd) {
+// The 16-byte path needs 16-byte aligned source and destination rows.
+template <typename TS>
+static void transpose_any(hipStream_t s, const TS *src, int64_t lds, const int32_t *rows_map, int div, int rows,
+                          int cols, bf16_t *dst, int64_t ldd) {
     if (rows <= 0 || cols <= 0) return;
     CATNN_REQUIRE((rows + 63) / 64 < 65536, CATNN_ERR_SHAPE_MISMATCH, "transpose: too many rows");
-    transpose_kernel<bf16_t><<<tgrid(rows, cols), 256, 0, s>>>(src, lds, rows_map, div, rows, cols,
-                                                               dst, ldd);
+    const bool vec = al16(src) && al16(dst) && (lds * (int64_t)sizeof(TS)) % 16 == 0 && ldd % 8 == 0;
+    if (vec)
+        transpose_vec_kernel<TS><<<tgrid(rows, cols), 256, 0, s>>>(src, lds, rows_map, div, rows, cols, dst, ldd);
+    else
+        transpose_kernel<TS><<<tgrid(rows, cols), 256, 0, s>>>(src, lds, rows_map, div, rows, cols, dst, ldd);
     CATNN_HIP(hipGetLastError());
+}
+
+void transpose_bf16(hipStream_t s, const bf16_t *src, int64_t lds, const int32_t *rows_map, int div,
+                    int rows, int cols, bf16_t *dst, int64_t ldd) {
+    transpose_any<bf16_t>(s, src, lds, rows_map, div, rows, cols, dst, ldd);
 }
 
 void transpose_f32_bf16(hipStream_t s, const float *src, int64_t lds, const int32_t *rows_map,
                         int div, int rows, int cols, bf16_t *dst, int64_t ldd) {
-    if (rows <= 0 || cols <= 0) return;
-    CATNN_REQUIRE((rows + 63) / 64 < 65536, CATNN_ERR_SHAPE_MISMATCH, "transpose: too many rows");
-    transpose_kernel<float><<<tgrid(rows, cols), 256, 0, s>>>(src, lds, rows_map, div, rows, cols,
-                                                              dst, ldd);
-    CATNN_HIP(hipGetLastError());
+    transpose_any<float>(s, src, lds, rows_map, div, rows, cols, dst, ldd);
 }
 
 void split3_rows(hipStream_t s, const float *x, int64_t ldx, int64_t rows, int K, bf16_t *out,
