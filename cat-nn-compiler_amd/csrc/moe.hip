@@ -43,6 +43,9 @@ constexpr int kPermChunk = 4096;  // slots per permutation block
 constexpr int kMaxRouteExperts = 256;
 constexpr int kMaxTopK = 16;
 
+__device__ void select_topk(const float *row, int E, int K, int64_t base, int32_t *__restrict__ idx_out,
+                            float *__restrict__ w_out);
+
 // One thread per (token, expert); tokens_per_block = 256 / E.
 __global__ __launch_bounds__(256) void route_kernel(const float *__restrict__ x,
                                                     const float *__restrict__ gate, int T, int H,
@@ -87,8 +90,14 @@ __global__ __launch_bounds__(256) void route_kernel(const float *__restrict__ x,
     }
     __syncthreads();
     if (!active || e != 0) return;
-    // Top-k of a stable descending order: repeated first-maximum selection.
-    const float *row = lg + tl * E;
+    select_topk(lg + tl * E, E, K, (int64_t)(t0 + tl) * K, idx_out, w_out);
+}
+
+// Top-k of a stable descending order (repeated first-maximum selection) and
+// the softmax of the selected logits, lens/moe.rs:175-187.
+__device__ void select_topk(const float *row, int E, int K, int64_t base, int32_t *__restrict__ idx_out,
+                            float *__restrict__ w_out) {
+#pragma clang fp contract(off)
     int sel[kMaxTopK];
     unsigned long long taken[kMaxRouteExperts / 64] = {0, 0, 0, 0};
     for (int kk = 0; kk < K; ++kk) {
@@ -109,11 +118,64 @@ __global__ __launch_bounds__(256) void route_kernel(const float *__restrict__ x,
         sum = sum + ex[kk];
     }
     const float inv = 1.0f / fmaxf(sum, 1e-30f);
-    const int64_t base = (int64_t)(t0 + tl) * K;
     for (int kk = 0; kk < K; ++kk) {
         if (idx_out) idx_out[base + kk] = sel[kk];
         if (w_out) w_out[base + kk] = ex[kk] * inv;
     }
+}
+
+constexpr int kRouteGateFloats = 12288;  // LDS floats for one staged gate chunk (48 KiB)
+
+// Rows of x 16-byte aligned (H % 4 == 0): each thread streams its token's
+// row straight from memory as float4 (the E threads of a token read the
+// same addresses), and the gate is staged transposed in LDS, gsT[e][p] with
+// row stride HC + 4, HC hidden elements per chunk (all of H for the usual
+// shapes), so a thread reads its expert's weights as float4 too.  The sum
+// runs over p ascending with separate multiply and add, as route_kernel.
+__global__ __launch_bounds__(256) void route_vec_kernel(const float *__restrict__ x,
+                                                        const float *__restrict__ gate, int T, int H, int E,
+                                                        int K, int tpb, int HC,
+                                                        int32_t *__restrict__ idx_out,
+                                                        float *__restrict__ w_out,
+                                                        float *__restrict__ logits_out) {
+#pragma clang fp contract(off)
+    extern __shared__ float smem[];
+    float *gsT = smem;                 // [E][HC + 4]
+    float *lg = gsT + E * (HC + 4);    // [tpb][E]
+    const int tid = threadIdx.x;
+    const int t0 = blockIdx.x * tpb;
+    const int tl = tid / E, e = tid % E;
+    const bool active = tl < tpb && t0 + tl < T;
+    const float4 *xr = reinterpret_cast<const float4 *>(x + (int64_t)(active ? t0 + tl : 0) * H);
+    float s = 0.0f;
+    for (int p0 = 0; p0 < H; p0 += HC) {
+        const int pc = min(HC, H - p0);
+        __syncthreads();  // the previous chunk is consumed
+        for (int i = tid; i < pc * E; i += 256) {
+            const int pp = i / E, ee = i - pp * E;
+            gsT[ee * (HC + 4) + pp] = gate[(int64_t)(p0 + pp) * E + ee];
+        }
+        __syncthreads();
+        if (active) {
+            const float4 *gr = reinterpret_cast<const float4 *>(gsT + e * (HC + 4));
+            const float4 *xc = xr + p0 / 4;
+#pragma unroll 8
+            for (int q = 0; q < pc / 4; ++q) {
+                const float4 xv = xc[q], gv = gr[q];
+                s = s + xv.x * gv.x;
+                s = s + xv.y * gv.y;
+                s = s + xv.z * gv.z;
+                s = s + xv.w * gv.w;
+            }
+        }
+    }
+    if (active) {
+        lg[tl * E + e] = s;
+        if (logits_out) logits_out[(int64_t)(t0 + tl) * E + e] = s;
+    }
+    __syncthreads();
+    if (!active || e != 0) return;
+    select_topk(lg + tl * E, E, K, (int64_t)(t0 + tl) * K, idx_out, w_out);
 }
 
 // Per-block expert histogram of the slots [b·chunk, (b+1)·chunk).  Slots
@@ -292,10 +354,17 @@ void moe_route_f32(hipStream_t s, const float *x, const float *gate, int64_t tok
     const int E = (int)n_experts;
     const int tpb = std::min(64, 256 / E);  // ≤ 64 tokens keeps the LDS stage under 20 KB
     const int64_t blocks = (tokens + tpb - 1) / tpb;
-    const size_t smem = sizeof(float) * ((size_t)tpb * (kRouteChunk + 1) +
-                                         (size_t)kRouteChunk * E + (size_t)tpb * E);
-    route_kernel<<<(unsigned)blocks, 256, smem, s>>>(x, gate, (int)tokens, (int)hidden, E,
-                                                     (int)top_k, tpb, idx, w, logits);
+    if (hidden % 4 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0) {
+        const int HC = (int)std::min<int64_t>(hidden, (kRouteGateFloats / E - 4) & ~3);
+        const size_t smem = sizeof(float) * ((size_t)E * (HC + 4) + (size_t)tpb * E);
+        route_vec_kernel<<<(unsigned)blocks, 256, smem, s>>>(x, gate, (int)tokens, (int)hidden, E, (int)top_k,
+                                                             tpb, HC, idx, w, logits);
+    } else {
+        const size_t smem = sizeof(float) * ((size_t)tpb * (kRouteChunk + 1) +
+                                             (size_t)kRouteChunk * E + (size_t)tpb * E);
+        route_kernel<<<(unsigned)blocks, 256, smem, s>>>(x, gate, (int)tokens, (int)hidden, E,
+                                                         (int)top_k, tpb, idx, w, logits);
+    }
     CATNN_HIP(hipGetLastError());
 }
 
