@@ -11,6 +11,7 @@ from .device import (Device, DeviceBuffer, DeviceHandler, Program, eval_graph_hi
 from .ir import (FLAG_CAUSAL, FusionGroup, IrEdge, IrGraph, IrNode, OpenOp, Tensor, TensorType)
 from .train import Trainer
 from .irjson import CGraph, to_serde_json
+from .describe import KernelLaunch, KernelResource, describe, kernel_table
 from .spec import (Architecture, NetworkSpec, lower_architecture, mlp_spec, parse_catnn,
                    propose_fusions, to_architecture, transformer_block_spec)
 

@@ -79,6 +79,22 @@ class CEvent(ctypes.Structure):
                 ("kind", ctypes.c_int32), ("checksum", ctypes.c_uint64)]
 
 
+class CKernelLaunch(ctypes.Structure):
+    _fields_ = [("kernel", ctypes.c_char * 256), ("grid", ctypes.c_uint32 * 3),
+                ("block", ctypes.c_uint32 * 3), ("dynamic_lds_bytes", ctypes.c_uint64),
+                ("code_bytes", ctypes.c_uint64), ("vgprs", ctypes.c_uint32), ("agprs", ctypes.c_uint32),
+                ("sgprs", ctypes.c_uint32), ("static_lds_bytes", ctypes.c_uint64),
+                ("kernarg_bytes", ctypes.c_uint64), ("scratch_bytes_per_lane", ctypes.c_uint64)]
+
+
+class CKernelResource(ctypes.Structure):
+    _fields_ = [("code_bytes", ctypes.c_uint64), ("code_estimated", ctypes.c_int32),
+                ("registers_per_thread", ctypes.c_uint32), ("static_smem_bytes", ctypes.c_uint64),
+                ("dynamic_smem_bytes", ctypes.c_uint64), ("grid", ctypes.c_uint32 * 3),
+                ("block", ctypes.c_uint32 * 3), ("launch_arg_bytes", ctypes.c_uint64),
+                ("temp_bytes", ctypes.c_uint64), ("n_launches", ctypes.c_int32)]
+
+
 _VP = ctypes.c_void_p
 _I32 = ctypes.c_int32
 _I64 = ctypes.c_int64
@@ -121,6 +137,10 @@ SIGNATURES = {
     "catnn_hip_memset": [_VP, _VP, _I32, _U64],
     "catnn_hip_timer_start": [_VP],
     "catnn_hip_timer_stop": [_VP, ctypes.POINTER(_F)],
+    "catnn_hip_describe": [ctypes.POINTER(CNode), ctypes.POINTER(CTensor), _I32, ctypes.POINTER(CKernelResource),
+                           ctypes.POINTER(CKernelLaunch), _I32],
+    "catnn_hip_kernel_table_size": [_PI32],
+    "catnn_hip_kernel_table_entry": [_I32, ctypes.POINTER(CKernelLaunch)],
     "catnn_hip_run_kernel": [_VP, ctypes.POINTER(CNode), ctypes.POINTER(CTensor), _I32,
                              ctypes.POINTER(CTensor)],
     "catnn_hip_run_node": [_VP, ctypes.POINTER(CNode), ctypes.POINTER(ctypes.c_char_p),

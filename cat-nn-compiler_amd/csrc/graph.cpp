@@ -85,6 +85,10 @@ static Node node_from_c(const catnn_node *c, bool need_param_data = true) {
     return n;
 }
 
+Node node_shape_from_c(const catnn_node *c) { return node_from_c(c, false); }
+
+std::vector<int64_t> dims_from_c(const catnn_tensor &t) { return from_c(t, false).dims; }
+
 static const std::vector<int64_t> &pdims(const Node &n, const std::string &port) {
     const HostTensor *t = n.param(port);
     if (!t) fail(CATNN_ERR_UNKNOWN_PORT, "unknown port " + port + " on interface " + n.name);

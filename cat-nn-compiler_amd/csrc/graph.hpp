@@ -65,6 +65,11 @@ struct ExecArgs {
     const float *derived = nullptr;
 };
 
+// A node from its C form with parameter types only (no data), and the dims
+// of a C tensor; both check ranks and dimensions.
+Node node_shape_from_c(const catnn_node *c);
+std::vector<int64_t> dims_from_c(const catnn_tensor &t);
+
 // Scratch bytes `node` needs beyond its output (0 for most ops).
 uint64_t scratch_bytes(const Node &node, const std::vector<std::vector<int64_t>> &ins);
 

@@ -255,6 +255,49 @@ int catnn_hip_memset(catnn_hip_device *dev, void *dst, int32_t value, uint64_t b
 int catnn_hip_timer_start(catnn_hip_device *dev);
 int catnn_hip_timer_stop(catnn_hip_device *dev, float *ms);
 
+/* ------------------------------------------------------- describe() */
+/* One kernel launch of a node, with the kernel's resources as built: the
+ * counts come from this build's gfx950 code objects (AMDGPU metadata note
+ * and symbol table), read at build time. */
+#define CATNN_KERNEL_NAME_MAX 256
+typedef struct catnn_kernel_launch {
+    char kernel[CATNN_KERNEL_NAME_MAX]; /* mangled kernel symbol */
+    uint32_t grid[3];                   /* workgroups */
+    uint32_t block[3];                  /* work-items per workgroup */
+    uint64_t dynamic_lds_bytes;
+    uint64_t code_bytes;                /* the kernel's function symbol */
+    uint32_t vgprs, agprs, sgprs;
+    uint64_t static_lds_bytes;          /* group segment */
+    uint64_t kernarg_bytes;             /* kernel-argument segment */
+    uint64_t scratch_bytes_per_lane;    /* private segment */
+} catnn_kernel_launch;
+
+/* `KernelResource` (crates/catnn-compile/src/kernel/resource.rs:28-45) of
+ * a node on this backend, aggregated over its launches. */
+typedef struct catnn_kernel_resource {
+    uint64_t code_bytes;           /* sum over the distinct kernels */
+    int32_t code_estimated;        /* 0: measured from the code objects */
+    uint32_t registers_per_thread; /* largest VGPR + AGPR count */
+    uint64_t static_smem_bytes;    /* largest static LDS */
+    uint64_t dynamic_smem_bytes;   /* largest dynamic LDS */
+    uint32_t grid[3], block[3];    /* the launch with the most work-items */
+    uint64_t launch_arg_bytes;     /* largest kernel-argument segment */
+    uint64_t temp_bytes;           /* device scratch beyond the output */
+    int32_t n_launches;
+} catnn_kernel_resource;
+
+/* Replaces kernel::resource::describe (resource.rs:155-186) for the HIP
+ * backend: the launches `node` makes on inputs of the given types (as an
+ * installed graph runs it; params need types only), the first `cap` of
+ * them written to `launches`.  Host-only (no GPU needed).  Shape errors as
+ * catnn_hip_run_kernel; unsupported ops → CATNN_ERR_UNSUPPORTED. */
+int catnn_hip_describe(const catnn_node *node, const catnn_tensor *in_types, int32_t n_in,
+                       catnn_kernel_resource *out, catnn_kernel_launch *launches, int32_t cap);
+/* Every kernel of the build (resources only; block[0] = the largest
+ * workgroup it accepts).  Host-only. */
+int catnn_hip_kernel_table_size(int32_t *n);
+int catnn_hip_kernel_table_entry(int32_t i, catnn_kernel_launch *out);
+
 /* ---------------------------------------------------- the handler seam */
 /* Drop-in for `DeviceHandler::run_kernel` (handler.rs:34-57) with
  * host tensors in and out: params ride inside `node` (as the reference
