@@ -58,7 +58,11 @@ __global__ __launch_bounds__(256, 2) void attn_mfma_kernel(const float *__restri
     constexpr int BQ = 128, BKV = 64, LDK = DH + 4, LDV = BKV + 4;
     constexpr int KV_IT = BKV * DH / 4 / 256;  // float4 per thread per tile, per operand
     // K row-major; V transposed (Vt[d][key]) so that the four keys a lane
-    // feeds to four consecutive P·V MFMAs are one 16-byte LDS read.
+    // feeds to four consecutive P·V MFMAs are one 16-byte LDS read.  Row d
+    // of Vt holds key j at column j ^ vsw(d): rows 8 apart land on other
+    // banks, so the transposing stores (16 rows 4 apart per wavefront) are
+    // 2-way instead of 8-way conflicted, while a read's 8 rows share one
+    // swizzle and stay conflict-free.
     __shared__ float Ks[2][BKV][LDK];
     __shared__ float Vt[2][DH][LDV];
 
@@ -105,6 +109,7 @@ __global__ __launch_bounds__(256, 2) void attn_mfma_kernel(const float *__restri
     // Sliding window: tiles before the first key of the block's first query are skipped.
     const int t_first = window > 0 ? max(0, q0 - window + 1) / BKV : 0;
 
+    auto vsw = [](int d) { return ((d >> 3) & 7) << 2; };
     float4 pk[KV_IT], pv[KV_IT];
     auto gload = [&](int t) {
 #pragma unroll
@@ -128,10 +133,12 @@ __global__ __launch_bounds__(256, 2) void attn_mfma_kernel(const float *__restri
             const int idx = tid + it * 256;
             const int key = idx / (DH / 4), c4 = idx % (DH / 4);
             *reinterpret_cast<float4 *>(&Ks[buf][key][4 * c4]) = pk[it];
-            Vt[buf][4 * c4 + 0][key] = pv[it].x;
-            Vt[buf][4 * c4 + 1][key] = pv[it].y;
-            Vt[buf][4 * c4 + 2][key] = pv[it].z;
-            Vt[buf][4 * c4 + 3][key] = pv[it].w;
+            // rows 4c4 … 4c4+3 share d >> 3, hence one swizzle
+            const int kc = key ^ vsw(4 * c4);
+            Vt[buf][4 * c4 + 0][kc] = pv[it].x;
+            Vt[buf][4 * c4 + 1][kc] = pv[it].y;
+            Vt[buf][4 * c4 + 2][kc] = pv[it].z;
+            Vt[buf][4 * c4 + 3][kc] = pv[it].w;
         }
     };
 
@@ -159,7 +166,29 @@ __global__ __launch_bounds__(256, 2) void attn_mfma_kernel(const float *__restri
                                                         (window <= 0 || jb + 31 >= wave_qmin - window + 1));
 #pragma unroll
             for (int r = 0; r < 16; ++r) sacc[kb][r] = 0.f;
-            if (active[kb]) {
+        }
+        static_assert(BKV == 64, "two 32-key blocks per tile");
+        if (active[0] && active[1]) {
+            // Both key blocks: alternate their accumulator chains so that
+            // consecutive MFMAs are independent.
+            const float *k0 = &Ks[buf][lr][32 * g], *k1 = &Ks[buf][32 + lr][32 * g];
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+                const float4 a = *reinterpret_cast<const float4 *>(k0 + 4 * c);
+                const float4 b = *reinterpret_cast<const float4 *>(k1 + 4 * c);
+                sacc[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.x, qf[4 * c + 0], sacc[0], 0, 0, 0);
+                sacc[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(b.x, qf[4 * c + 0], sacc[1], 0, 0, 0);
+                sacc[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.y, qf[4 * c + 1], sacc[0], 0, 0, 0);
+                sacc[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(b.y, qf[4 * c + 1], sacc[1], 0, 0, 0);
+                sacc[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.z, qf[4 * c + 2], sacc[0], 0, 0, 0);
+                sacc[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(b.z, qf[4 * c + 2], sacc[1], 0, 0, 0);
+                sacc[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.w, qf[4 * c + 3], sacc[0], 0, 0, 0);
+                sacc[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(b.w, qf[4 * c + 3], sacc[1], 0, 0, 0);
+            }
+        } else {
+#pragma unroll
+            for (int kb = 0; kb < BKV / 32; ++kb) {
+                if (!active[kb]) continue;
                 const float *krow = &Ks[buf][kb * 32 + lr][32 * g];
                 float4 kf[8];
 #pragma unroll
@@ -227,7 +256,8 @@ __global__ __launch_bounds__(256, 2) void attn_mfma_kernel(const float *__restri
             for (int s4 = 0; s4 < 4; ++s4)
 #pragma unroll
                 for (int db = 0; db < DH / 32; ++db)
-                    vf[s4][db] = *reinterpret_cast<const float4 *>(&Vt[buf][db * 32 + lr][kb * 32 + 8 * s4 + 4 * g]);
+                    vf[s4][db] = *reinterpret_cast<const float4 *>(
+                        &Vt[buf][db * 32 + lr][(kb * 32 + 8 * s4 + 4 * g) ^ vsw(db * 32 + lr)]);
 #pragma unroll
             for (int s4 = 0; s4 < 4; ++s4)
 #pragma unroll
