@@ -106,6 +106,31 @@ def time_train_step(dev, steps, warmup):
                          "GEMMs for Linear/attention; attention core fp32 MFMA"}
 
 
+def time_mixtral(dev, steps, warmup):
+    """A Mixtral-style decoder forward through the (f)3 ops: the
+    mixtral_architecture chain (embed → [RMSNorm → GQA+RoPE → RMSNorm → MoE]
+    × 2 → RMSNorm → LmHead) at the config-4 MoE shape, 16 heads × 64 with 4
+    K/V heads, a 32000-token vocabulary, on 8192 tokens; fp32."""
+    import catnn_amd
+    from catnn_amd import configs
+    from catnn_amd.configs import MixtralShape
+
+    shape = MixtralShape(vocab=32000, hidden=1024, inter=3584, layers=2, heads=16, kv_heads=4, experts=8,
+                         top_k=2, sliding_window=4096)
+    wl = configs.mixtral(batch=4, seq=2048, shape=shape)
+    log("mixtral decoder built")
+    prog = catnn_amd.Program(dev, wl.graph)
+    ms, _, timings = time_program(dev, prog, wl.x, steps, warmup)
+    prog.free()
+    rate = wl.flops / (ms / 1e3)
+    log(f"mixtral decoder: {ms:.3f} ms/step, {rate / 1e12:.1f} TFLOP/s")
+    return {"tokens_per_s": round(wl.tokens / (ms / 1e3)), "ms_per_step": round(ms, 4),
+            "GFLOP_per_s": round(rate / 1e9, 1), "mfma_frac": round(rate / 1e12 / FP32_MFMA_PEAK_TFLOPS, 4),
+            "shape": {"tokens": wl.tokens, "hidden": 1024, "heads": 16, "kv_heads": 4, "head_dim": 64,
+                      "experts": 8, "top_k": 2, "intermediate": 3584, "vocab": 32000, "layers": 2},
+            "steps_ms": {t[0]: round(t[3] / max(t[2], 1), 4) for t in timings}}
+
+
 def cpu_baseline_mlp(wl, target_s):
     """Oracle restatement of the reference CPU path on a row subset."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
@@ -280,6 +305,7 @@ def main():
         del w3
         log(f"config 3: {ms3:.3f} ms/step")
         sec["train_step_config5"] = time_train_step(dev, max(3, args.steps // 2), 2)
+        sec["mixtral_decoder"] = time_mixtral(dev, max(3, args.steps // 4), 2)
         result["secondary"] = sec
 
     if not args.no_cpu_baseline:
