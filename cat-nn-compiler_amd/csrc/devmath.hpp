@@ -24,6 +24,29 @@ __device__ __forceinline__ float apply_act(float v, int act) {
     return v;
 }
 
+// Direct HBM → LDS loads (global_load_lds_dwordx4): the LDS destination is
+// an address-space-3 pointer, uniform across the wavefront; lane l writes
+// its 16 bytes at destination + 16·l.
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+__device__ __forceinline__ void load_lds16(const void *src, void *lds_wave_base) {
+    __builtin_amdgcn_global_load_lds(src, (lds_void_t *)lds_wave_base, 16, 0, 0);
+}
+
+// s_waitcnt with vmcnt ≤ N, lgkmcnt 0 (every LDS access of this wavefront
+// done), expcnt unconstrained; then the block barrier.  Direct-to-LDS loads
+// count in vmcnt until their data is in LDS.  The empty asm statements keep
+// the compiler from moving memory accesses across; the barrier builtin
+// itself carries no fence, so the waits stay exactly these.
+template <int N>
+__device__ __forceinline__ void dma_sync() {
+    static_assert(N >= 0 && N < 64, "vmcnt");
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 // Butterfly reductions across the 64 lanes of a wavefront.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

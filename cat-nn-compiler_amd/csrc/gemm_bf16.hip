@@ -363,20 +363,6 @@ __device__ __forceinline__ void finish(const GemmBf16Params &p, const f32x16 (&a
     }
 }
 
-typedef __attribute__((address_space(3))) void lds_void_t;
-
-// s_waitcnt with vmcnt ≤ N, lgkmcnt 0 (every LDS access of this wavefront
-// done), expcnt unconstrained; then the block barrier.  The empty asm
-// statements keep the compiler from moving memory accesses across; the
-// barrier builtin itself carries no fence, so the waits stay exactly these.
-template <int N>
-__device__ __forceinline__ void dma_sync() {
-    static_assert(N >= 0 && N < 64, "vmcnt");
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-}
 
 __device__ __forceinline__ void unpack8(uint4 w, float (&f)[8]) {
     const uint32_t u[4] = {w.x, w.y, w.z, w.w};
@@ -593,11 +579,10 @@ __device__ __forceinline__ void tile_dma(unsigned char *smem, const GemmBf16Para
         const int k0 = k_lo + kt * BK;
 #pragma unroll
         for (int q = 0; q < C::A_LD; ++q)
-            __builtin_amdgcn_global_load_lds(a_src[q] + k0, (lds_void_t *)(st + (wave * C::A_LD + q) * 1024), 16, 0, 0);
+            load_lds16(a_src[q] + k0, st + (wave * C::A_LD + q) * 1024);
 #pragma unroll
         for (int q = 0; q < C::B_LD; ++q)
-            __builtin_amdgcn_global_load_lds(b_src[q] + k0,
-                                             (lds_void_t *)(st + BM * 128 + (wave * C::B_LD + q) * 1024), 16, 0, 0);
+            load_lds16(b_src[q] + k0, st + BM * 128 + (wave * C::B_LD + q) * 1024);
     };
 
     f32x16 acc[FM][FN];

@@ -126,6 +126,121 @@ __device__ void select_topk(const float *row, int E, int K, int64_t base, int32_
 
 constexpr int kRouteGateFloats = 12288;  // LDS floats for one staged gate chunk (48 KiB)
 
+// gsT[e][p − p0] = gate[p][e] for p in [p0, p0 + pc), rows ldt floats
+// apart: a block-wide transposing copy with 8 loads in flight per thread.
+__device__ __forceinline__ void stage_gate_t(const float *__restrict__ gate, int p0, int pc, int E,
+                                             float *__restrict__ gsT, int ldt) {
+    constexpr int GB = 8;
+    const int n = pc * E;
+    const float *src = gate + (int64_t)p0 * E;
+    for (int i0 = threadIdx.x; i0 < n; i0 += 256 * GB) {
+        float v[GB];
+#pragma unroll
+        for (int u = 0; u < GB; ++u) {
+            const int i = i0 + u * 256;
+            v[u] = i < n ? src[i] : 0.f;
+        }
+#pragma unroll
+        for (int u = 0; u < GB; ++u) {
+            const int i = i0 + u * 256;
+            if (i < n) {
+                const int p = i / E;
+                gsT[(i - p * E) * ldt + p] = v[u];
+            }
+        }
+    }
+}
+constexpr int kRouteXC = 64;  // hidden elements of x per staged chunk (16 float4)
+
+constexpr int kRouteStages = 4;  // x chunks in LDS: three in flight while one is summed
+
+// Token rows staged in LDS by direct loads (global_load_lds_dwordx4),
+// kRouteStages chunks of kRouteXC columns deep.  One wave load fills 1 KiB: the
+// chunk of a group of 4 token rows, row g at 64·g floats, its float4 j at
+// position (j + 2g) mod 16; groups are 260 floats apart.  With that
+// rotation and the 16-byte gap, the 8 tokens a wavefront reads at one step
+// sit on 8 different bank quads.  The gate is staged transposed whole
+// (E·(H+4) floats).  Each thread then runs its (token, expert) sum over p
+// ascending with separate multiply and add, as route_kernel, reading x and
+// its expert's weights as float4 from LDS.  tpb = 16·LPW tokens per block
+// (each wavefront issues LPW wave loads per chunk); needs H % kRouteXC == 0
+// and 16-byte aligned rows.
+template <int LPW>
+__global__ __launch_bounds__(256) void route_dma_kernel(const float *__restrict__ x,
+                                                        const float *__restrict__ gate, int T, int H, int E,
+                                                        int K, int tpb, int32_t *__restrict__ idx_out,
+                                                        float *__restrict__ w_out,
+                                                        float *__restrict__ logits_out) {
+#pragma clang fp contract(off)
+    extern __shared__ float smem[];
+    constexpr int GROUP = 4 * kRouteXC + 4;  // floats per staged group of 4 rows
+    constexpr int groups = 4 * LPW;
+    float *xs = smem;                         // [kRouteStages][groups][GROUP]
+    float *gsT = xs + kRouteStages * groups * GROUP;  // [E][H + 4]
+    float *lg = gsT + E * (H + 4);            // [tpb][E]
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int t0 = blockIdx.x * tpb;
+    const int tl = tid / E, e = tid % E;
+    const bool active = tl < tpb && t0 + tl < T;
+    // Wave loads: group q for q = wave, wave + 4, …; lane l fills row
+    // 4q + l/16 at position l mod 16 with its float4 (l − 2·(l/16)) mod 16.
+    // Rows past T read row T−1 (their sums are never stored).
+    const int lrow = lane >> 4, lpos = lane & 15;
+    const int lcol = 4 * ((lpos - 2 * lrow) & 15);
+    auto issue = [&](int c) {
+        float *st = xs + (c % kRouteStages) * groups * GROUP;
+#pragma unroll
+        for (int j = 0; j < LPW; ++j) {
+            const int q = wave + 4 * j;
+            const int row = min(t0 + 4 * q + lrow, T - 1);
+            load_lds16(x + (int64_t)row * H + c * kRouteXC + lcol, st + q * GROUP);
+        }
+    };
+    const int nc = H / kRouteXC;
+#pragma unroll
+    for (int c = 0; c < kRouteStages - 1; ++c)
+        if (c < nc) issue(c);
+    stage_gate_t(gate, 0, H, E, gsT, H + 4);
+    float s = 0.0f;
+    const float4 *gr = reinterpret_cast<const float4 *>(gsT + e * (H + 4));
+    const int rg = tl & 3;
+    const int xoff = (tl >> 2) * GROUP + rg * kRouteXC;
+    for (int c = 0; c < nc; ++c) {
+        // Chunk c in LDS (and the gate); chunk c−1 consumed by every thread.
+        // Chunks c+1 and c+2 may stay in flight.
+        if (c + 2 < nc) dma_sync<2 * LPW>();
+        else if (c + 1 < nc) dma_sync<LPW>();
+        else dma_sync<0>();
+        if (c + kRouteStages - 1 < nc) issue(c + kRouteStages - 1);
+        if (active) {
+            const float *xr = xs + (c % kRouteStages) * groups * GROUP + xoff;
+            const float4 *gc = gr + c * (kRouteXC / 4);
+            // All of the chunk's operands first (one LDS wait), then the chain.
+            float4 xv[kRouteXC / 4], gv[kRouteXC / 4];
+#pragma unroll
+            for (int q = 0; q < kRouteXC / 4; ++q) {
+                xv[q] = *reinterpret_cast<const float4 *>(xr + 4 * ((q + 2 * rg) & 15));
+                gv[q] = gc[q];
+            }
+#pragma unroll
+            for (int q = 0; q < kRouteXC / 4; ++q) {
+                s = s + xv[q].x * gv[q].x;
+                s = s + xv[q].y * gv[q].y;
+                s = s + xv[q].z * gv[q].z;
+                s = s + xv[q].w * gv[q].w;
+            }
+        }
+    }
+    if (active) {
+        lg[tl * E + e] = s;
+        if (logits_out) logits_out[(int64_t)(t0 + tl) * E + e] = s;
+    }
+    __syncthreads();
+    if (!active || e != 0) return;
+    select_topk(lg + tl * E, E, K, (int64_t)(t0 + tl) * K, idx_out, w_out);
+}
+
 // Rows of x 16-byte aligned (H % 4 == 0): each thread streams its token's
 // row straight from memory as float4 (the E threads of a token read the
 // same addresses), and the gate is staged transposed in LDS, gsT[e][p] with
@@ -151,10 +266,7 @@ __global__ __launch_bounds__(256) void route_vec_kernel(const float *__restrict_
     for (int p0 = 0; p0 < H; p0 += HC) {
         const int pc = min(HC, H - p0);
         __syncthreads();  // the previous chunk is consumed
-        for (int i = tid; i < pc * E; i += 256) {
-            const int pp = i / E, ee = i - pp * E;
-            gsT[ee * (HC + 4) + pp] = gate[(int64_t)(p0 + pp) * E + ee];
-        }
+        stage_gate_t(gate, p0, pc, E, gsT, HC + 4);
         __syncthreads();
         if (active) {
             const float4 *gr = reinterpret_cast<const float4 *>(gsT + e * (HC + 4));
@@ -340,6 +452,21 @@ void moe_combine(hipStream_t s, const float *y, const int32_t *pos_of_slot, cons
     CATNN_HIP(hipGetLastError());
 }
 
+// Above 64 KiB of LDS a kernel needs the opt-in; two blocks per CU still fit.
+template <int LPW>
+static void launch_route_dma(hipStream_t s, int64_t blocks, size_t smem, const float *x, const float *gate,
+                             int64_t tokens, int64_t hidden, int E, int64_t top_k, int tpb, int32_t *idx, float *w,
+                             float *logits) {
+    static bool attr = false;
+    if (!attr) {
+        CATNN_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(route_dma_kernel<LPW>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, 80 * 1024));
+        attr = true;
+    }
+    route_dma_kernel<LPW><<<(unsigned)blocks, 256, smem, s>>>(x, gate, (int)tokens, (int)hidden, E, (int)top_k, tpb,
+                                                              idx, w, logits);
+}
+
 void moe_route_f32(hipStream_t s, const float *x, const float *gate, int64_t tokens, int64_t hidden,
                    int64_t n_experts, int64_t top_k, int32_t *idx, float *w, float *logits) {
     CATNN_REQUIRE(tokens >= 0 && hidden > 0 && n_experts > 0, CATNN_ERR_SHAPE_MISMATCH,
@@ -354,7 +481,14 @@ void moe_route_f32(hipStream_t s, const float *x, const float *gate, int64_t tok
     const int E = (int)n_experts;
     const int tpb = std::min(64, 256 / E);  // ≤ 64 tokens keeps the LDS stage under 20 KB
     const int64_t blocks = (tokens + tpb - 1) / tpb;
-    if (hidden % 4 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0) {
+    const size_t dma_smem = sizeof(float) * ((size_t)kRouteStages * (tpb / 4) * (4 * kRouteXC + 4) +
+                                             (size_t)E * (hidden + 4) + (size_t)tpb * E);
+    if (hidden % kRouteXC == 0 && tpb % 16 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
+        dma_smem <= 80 * 1024) {
+        if (tpb == 16) launch_route_dma<1>(s, blocks, dma_smem, x, gate, tokens, hidden, E, top_k, tpb, idx, w, logits);
+        else if (tpb == 32) launch_route_dma<2>(s, blocks, dma_smem, x, gate, tokens, hidden, E, top_k, tpb, idx, w, logits);
+        else launch_route_dma<4>(s, blocks, dma_smem, x, gate, tokens, hidden, E, top_k, tpb, idx, w, logits);
+    } else if (hidden % 4 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0) {
         const int HC = (int)std::min<int64_t>(hidden, (kRouteGateFloats / E - 4) & ~3);
         const size_t smem = sizeof(float) * ((size_t)E * (HC + 4) + (size_t)tpb * E);
         route_vec_kernel<<<(unsigned)blocks, 256, smem, s>>>(x, gate, (int)tokens, (int)hidden, E, (int)top_k,

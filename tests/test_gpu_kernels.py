@@ -186,7 +186,9 @@ def test_attention_core_matches_float64(device, B, S, H, dh, causal):
                                      (1, 8, 2, 2),
                                      (50, 30, 4, 2),          # H % 4 != 0: the LDS-staged kernel
                                      (300, 1000, 64, 2),      # gate staged in several chunks
-                                     (20, 200, 256, 8)])
+                                     (20, 200, 256, 8),
+                                     (500, 256, 16, 4),       # direct-to-LDS staging, 16 tokens a block
+                                     (300, 128, 4, 1)])       # … 64 tokens a block
 def test_route_is_bit_exact(device, T, H, E, k):
     x = RNG.standard_normal((T, H)).astype(np.float32)
     gate = (RNG.standard_normal((H, E)) * math.sqrt(0.5)).astype(np.float32)
