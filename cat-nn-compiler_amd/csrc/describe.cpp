@@ -138,7 +138,13 @@ std::vector<Launch> launches_of(const Node &node, const std::vector<std::vector<
             const int64_t H = last, T = nx / H, E = node.op.a[0], K = node.op.a[1];
             const int64_t I = pd(node, "e0.w1")[1];
             const int64_t tpb = std::min<int64_t>(64, 256 / E);
-            if (H % 4 == 0) {
+            // moe.hip moe_route_f32: the LDS-staged kernel (four 64-column chunks of 4-row
+            // groups, whole transposed gate) when it fits 80 KiB, else the streaming one
+            const uint64_t dma = 4 * (uint64_t)(4 * (tpb / 4) * (4 * 64 + 4) + E * (H + 4) + tpb * E);
+            if (H % 64 == 0 && tpb % 16 == 0 && dma <= 80 * 1024) {
+                L.push_back({"16route_dma_kernelILi" + std::to_string(tpb / 16) + "EE", clamp_grid(cdiv(T, tpb)), 256,
+                             dma});
+            } else if (H % 4 == 0) {
                 const int64_t HC = std::min<int64_t>(H, (12288 / E - 4) & ~int64_t(3));
                 L.push_back({"16route_vec_kernel", clamp_grid(cdiv(T, tpb)), 256,
                              (uint64_t)(4 * (E * (HC + 4) + tpb * E))});
@@ -253,7 +259,8 @@ int catnn_hip_describe(const catnn_node *node, const catnn_tensor *in_types, int
                 seen.push_back(&k);
                 out->code_bytes += k.code_bytes;
             }
-            out->registers_per_thread = std::max(out->registers_per_thread, k.vgprs + k.agprs);
+            // .vgpr_count of gfx950 code objects is the unified VGPR + AGPR allocation
+            out->registers_per_thread = std::max(out->registers_per_thread, k.vgprs);
             out->static_smem_bytes = std::max(out->static_smem_bytes, k.lds_static);
             out->dynamic_smem_bytes = std::max(out->dynamic_smem_bytes, L[i].dyn_lds);
             out->launch_arg_bytes = std::max(out->launch_arg_bytes, k.kernarg_bytes);

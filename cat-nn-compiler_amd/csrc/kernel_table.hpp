@@ -9,7 +9,8 @@ namespace catnn {
 struct KernelInfo {
     const char *symbol;         // mangled kernel name
     uint64_t code_bytes;        // size of the kernel's function symbol
-    uint32_t vgprs, agprs, sgprs;
+    uint32_t vgprs;             // unified VGPR + AGPR allocation per lane (.vgpr_count)
+    uint32_t agprs, sgprs;      // the AGPR part of it; SGPRs
     uint64_t lds_static;        // group segment bytes
     uint64_t kernarg_bytes;     // kernel-argument segment bytes
     uint64_t scratch_per_lane;  // private segment bytes

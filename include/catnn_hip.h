@@ -266,7 +266,8 @@ typedef struct catnn_kernel_launch {
     uint32_t block[3];                  /* work-items per workgroup */
     uint64_t dynamic_lds_bytes;
     uint64_t code_bytes;                /* the kernel's function symbol */
-    uint32_t vgprs, agprs, sgprs;
+    uint32_t vgprs;                     /* unified VGPR + AGPR registers per lane */
+    uint32_t agprs, sgprs;              /* the AGPR part of vgprs; SGPRs */
     uint64_t static_lds_bytes;          /* group segment */
     uint64_t kernarg_bytes;             /* kernel-argument segment */
     uint64_t scratch_bytes_per_lane;    /* private segment */
@@ -277,7 +278,7 @@ typedef struct catnn_kernel_launch {
 typedef struct catnn_kernel_resource {
     uint64_t code_bytes;           /* sum over the distinct kernels */
     int32_t code_estimated;        /* 0: measured from the code objects */
-    uint32_t registers_per_thread; /* largest VGPR + AGPR count */
+    uint32_t registers_per_thread; /* largest unified VGPR + AGPR count */
     uint64_t static_smem_bytes;    /* largest static LDS */
     uint64_t dynamic_smem_bytes;   /* largest dynamic LDS */
     uint32_t grid[3], block[3];    /* the launch with the most work-items */

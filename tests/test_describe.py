@@ -22,7 +22,10 @@ def test_kernel_table_reads_the_code_objects():
         assert r.block[0] in (256, 512, 1024), r.kernel
     # the fp32 MFMA GEMM keeps its accumulators in registers, no scratch
     g = next(r for r in rows if "gemm_plain_kernelILi128ELi128ELi16ELb1ELb0E" in r.kernel)
-    assert g.scratch_bytes_per_lane == 0 and g.vgprs + g.agprs >= 64 and g.static_lds_bytes > 0
+    assert g.scratch_bytes_per_lane == 0 and g.vgprs >= 64 and g.static_lds_bytes > 0
+    # the bf16 GEMM keeps its accumulators in AGPRs, counted inside the unified VGPR total
+    b = next(r for r in rows if "gemm_bf16_kernelINS1_4DCfg" in r.kernel)
+    assert 0 < b.agprs < b.vgprs
 
 
 def test_linear_is_one_gemm_launch():
@@ -35,7 +38,7 @@ def test_linear_is_one_gemm_launch():
     assert "gemm_plain_kernelILi128ELi128ELi16ELb1ELb0E" in k.kernel
     assert k.grid == (64 * 128, 1, 1) and k.block == (256, 1, 1)
     assert r.code_bytes == k.code_bytes and not r.code_estimated
-    assert r.registers_per_thread == k.vgprs + k.agprs
+    assert r.registers_per_thread == k.vgprs  # unified VGPR + AGPR count
     assert r.scratch_bytes() == k.static_lds_bytes + r.registers_per_thread * 4 * 256
     # K not a multiple of 4: the element-load variant
     odd = IrNode(1, "fc", OpenOp.linear(7, 5, False), TensorType.f32([3, 5]), {"w": _z([7, 5])})
@@ -54,10 +57,10 @@ def test_attention_block_and_moe_layer():
     moe = m.graph.nodes[1]
     r = describe(moe, [TensorType.f32([8, 2048, 1024])])
     names = [k.kernel for k in r.launches]
-    assert "route_vec_kernel" in names[0] and "combine4_kernel" in names[-1]
+    assert "route_dma_kernelILi2E" in names[0] and "combine4_kernel" in names[-1]
     dual = next(k for k in r.launches if "gemm_grouped_kernelILi128ELi128ELi16ELb1ELb1E" in k.kernel)
     assert dual.grid[0] == (32768 // 128 + 8) * (3584 // 64)
-    assert r.launches[0].dynamic_lds_bytes == 4 * (8 * (1024 + 4) + 32 * 8)
+    assert r.launches[0].dynamic_lds_bytes == 4 * (4 * 8 * 260 + 8 * (1024 + 4) + 32 * 8)
     assert r.code_bytes == sum({k.kernel: k.code_bytes for k in r.launches}.values())
 
 
@@ -92,6 +95,11 @@ def _every_kernel_path():
     for e in range(4):
         moe.update({f"e{e}.w1": _z([10, 12]), f"e{e}.w3": _z([10, 12]), f"e{e}.w2": _z([12, 10])})
     yield IrNode(1, "moe_odd", OpenOp.moe(4, 2, 10, 12), f([5, 10]), moe), [f([5, 10])]
+    for E, H in ((4, 64), (16, 128), (8, 100)):  # staged router (64 and 16 tokens a block), streaming one
+        moe = {"gate": _z([H, E])}
+        for e in range(E):
+            moe.update({f"e{e}.w1": _z([H, 8]), f"e{e}.w3": _z([H, 8]), f"e{e}.w2": _z([8, H])})
+        yield IrNode(1, f"moe{E}", OpenOp.moe(E, 2, H, 8), f([40, H]), moe), [f([40, H])]
 
 
 def test_every_kernel_named_resolves_once():
@@ -103,6 +111,8 @@ def test_every_kernel_named_resolves_once():
             assert k.code_bytes > 0 and k.grid[0] >= 1
             seen.add(k.kernel)
     assert any("route_kernel" in k for k in seen) and any("combine_kernel" in k for k in seen)
+    assert any("route_vec_kernel" in k for k in seen)
+    assert any("route_dma_kernelILi4E" in k for k in seen) and any("route_dma_kernelILi1E" in k for k in seen)
     assert any("attn_generic_kernel" in k for k in seen) and any("attn_mfma_kernel" in k for k in seen)
     assert any("rms_norm_any_kernel" in k for k in seen) and any("embedding_kernelILb0E" in k for k in seen)
     # copies launch no kernel
