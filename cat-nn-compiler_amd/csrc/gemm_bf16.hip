@@ -58,21 +58,29 @@ using Cfg2 = Cfg<128, 128, 2, 2, 64>;
 // l at byte 16·l, so rows are 128 bytes (8 chunks of 8 k values) with no
 // padding; a row's chunk c sits at position c ^ (row mod 8), which keeps the
 // MFMA operand reads (8 rows × one chunk per 8 lanes) on distinct banks.
-template <int BM_, int BN_, int WAVES_M_, int WAVES_N_, int STAGES_>
+//
+// With BK = 32 rows are 64 bytes (4 chunks) and a wave load fills 16 rows;
+// chunk c of row r then sits at c ^ ((r / 2) mod 4), again one bank group per
+// lane for 8 consecutive rows.
+template <int BM_, int BN_, int WAVES_M_, int WAVES_N_, int STAGES_, int BK_ = 64>
 struct DCfg {
     static constexpr bool DMA = true;
     static constexpr int BM = BM_, BN = BN_, WAVES_M = WAVES_M_, WAVES_N = WAVES_N_, STAGES = STAGES_;
-    static constexpr int BK = 64;
+    static constexpr int BK = BK_;
+    static constexpr int ROWB = BK * 2, CPR = BK / 8, RPL = 64 / CPR;  // row bytes, chunks a row, rows a wave load
     static constexpr int NT = 64 * WAVES_M * WAVES_N, NW = WAVES_M * WAVES_N;
     static constexpr int FM = BM / (32 * WAVES_M), FN = BN / (32 * WAVES_N);
-    static constexpr int STAGE_BYTES = (BM + BN) * 128;
+    static constexpr int STAGE_BYTES = (BM + BN) * ROWB;
     static constexpr int LDS_BYTES = STAGES * STAGE_BYTES;
-    // wave loads (8 rows each) per wavefront and k chunk
-    static constexpr int A_LD = BM / (8 * NW), B_LD = BN / (8 * NW), LPC = A_LD + B_LD;
+    // wave loads (RPL rows each) per wavefront and k chunk
+    static constexpr int A_LD = BM / (RPL * NW), B_LD = BN / (RPL * NW), LPC = A_LD + B_LD;
+    // chunk position swizzle of row r
+    static __device__ __forceinline__ int sw(int r) { return CPR == 8 ? (r & 7) : ((r >> 1) & (CPR - 1)); }
+    static_assert(BK == 64 || BK == 32, "k chunk");
     static_assert(FM >= 1 && FN >= 1 && FM * 32 * WAVES_M == BM && FN * 32 * WAVES_N == BN, "tile");
-    static_assert(A_LD >= 1 && B_LD >= 1 && A_LD * 8 * NW == BM && B_LD * 8 * NW == BN, "load split");
+    static_assert(A_LD >= 1 && B_LD >= 1 && A_LD * RPL * NW == BM && B_LD * RPL * NW == BN, "load split");
     static_assert(STAGES >= 2 && LDS_BYTES <= 160 * 1024, "LDS");
-    static_assert(LPC * (STAGES - 2) < 64, "vmcnt range");
+    static_assert(STAGES <= 4 && LPC * (STAGES - 2) < 64, "vmcnt range (the main loop waits for up to 2 chunks ahead)");
 };
 
 // 128 × 128 tiles of four 64 × 64 wavefronts: two stages (64 KiB, two
@@ -82,6 +90,7 @@ struct DCfg {
 // only on 8192³ (1067 against 981 TFLOP/s) and lost on the rest.
 using Cfg7 = DCfg<128, 128, 2, 2, 2>;
 using Cfg9 = DCfg<128, 128, 2, 2, 3>;
+using Cfg10 = DCfg<128, 128, 2, 2, 4, 32>;  // 32-deep chunks, four stages in the same 64 KiB
 
 
 __device__ __forceinline__ float bf2f(bf16_t v) { return __uint_as_float((uint32_t)v << 16); }
@@ -557,11 +566,13 @@ __device__ __forceinline__ void tile_dma(unsigned char *smem, const GemmBf16Para
     // row … + l/8 at position l mod 8, i.e. k chunk (l mod 8) ^ (l/8).  Rows
     // past the tile's end read row row0 (col0 for B): their outputs are never
     // stored.
-    const int dk = (((lane & 7) ^ (lane >> 3)) * 8);
+    constexpr int CPR = C::CPR, RPL = C::RPL, ROWB = C::ROWB;
+    const int lrow = lane / CPR, lpos = lane % CPR;
+    const int dk = (lpos ^ C::sw(lrow)) * 8;  // wave-load rows start on multiples of RPL
     const bf16_t *a_src[C::A_LD];
 #pragma unroll
     for (int q = 0; q < C::A_LD; ++q) {
-        int gr = row0 + (wave * C::A_LD + q) * 8 + (lane >> 3);
+        int gr = row0 + (wave * C::A_LD + q) * RPL + lrow;
         if (gr >= row_end) gr = row0;
         const int src = p.a_rows ? p.a_rows[gr] / p.a_row_div : gr;
         a_src[q] = p.A + (int64_t)src * p.lda + dk;
@@ -570,7 +581,7 @@ __device__ __forceinline__ void tile_dma(unsigned char *smem, const GemmBf16Para
 #pragma unroll
     for (int q = 0; q < C::B_LD; ++q) {
         int n;
-        const bf16_t *base = b_row_src((wave * C::B_LD + q) * 8 + (lane >> 3), n);
+        const bf16_t *base = b_row_src((wave * C::B_LD + q) * RPL + lrow, n);
         if (n >= p.N) n = col0;
         b_src[q] = base + (int64_t)n * p.ldb + dk;
     }
@@ -579,10 +590,10 @@ __device__ __forceinline__ void tile_dma(unsigned char *smem, const GemmBf16Para
         const int k0 = k_lo + kt * BK;
 #pragma unroll
         for (int q = 0; q < C::A_LD; ++q)
-            load_lds16(a_src[q] + k0, st + (wave * C::A_LD + q) * 1024);
+            load_lds16(a_src[q] + k0, st + (wave * C::A_LD + q) * 1024);  // RPL rows × ROWB = 1 KiB
 #pragma unroll
         for (int q = 0; q < C::B_LD; ++q)
-            load_lds16(b_src[q] + k0, st + BM * 128 + (wave * C::B_LD + q) * 1024);
+            load_lds16(b_src[q] + k0, st + BM * ROWB + (wave * C::B_LD + q) * 1024);
     };
 
     f32x16 acc[FM][FN];
@@ -594,9 +605,9 @@ __device__ __forceinline__ void tile_dma(unsigned char *smem, const GemmBf16Para
             for (int r = 0; r < 16; ++r) acc[mi][ni][r] = 0.f;
 
     // Lane l reads k values 16s + 8(l/32) … +7 of row l mod 32 of each block.
-    const int a_off = (wm * (BM / C::WAVES_M) + lr) * 128;
-    const int sw = lr & 7;
-    auto b_off = [&](int ni) { return (BM + staged_col<C, DUAL>(wn, ni, lr)) * 128; };
+    const int a_off = (wm * (BM / C::WAVES_M) + lr) * ROWB;
+    const int sw = C::sw(lr);  // fragment rows start on multiples of 32
+    auto b_off = [&](int ni) { return (BM + staged_col<C, DUAL>(wn, ni, lr)) * ROWB; };
     auto compute = [&](const unsigned char *st) {
 #pragma unroll
         for (int s = 0; s < BK / 16; ++s) {
@@ -604,7 +615,7 @@ __device__ __forceinline__ void tile_dma(unsigned char *smem, const GemmBf16Para
             bf16x8 af[FM], bfr[FN];
 #pragma unroll
             for (int mi = 0; mi < FM; ++mi)
-                af[mi] = *reinterpret_cast<const bf16x8 *>(st + a_off + mi * 32 * 128 + pos);
+                af[mi] = *reinterpret_cast<const bf16x8 *>(st + a_off + mi * 32 * ROWB + pos);
 #pragma unroll
             for (int ni = 0; ni < FN; ++ni)
                 bfr[ni] = *reinterpret_cast<const bf16x8 *>(st + b_off(ni) + pos);
@@ -621,7 +632,10 @@ __device__ __forceinline__ void tile_dma(unsigned char *smem, const GemmBf16Para
     for (int j = 0; j < C::STAGES - 1; ++j)
         if (j < nfull) issue(j);
     for (int kt = 0; kt < nfull; ++kt) {
-        if (C::STAGES > 2 && kt + 1 < nfull) dma_sync<C::LPC * (C::STAGES - 2)>();
+        // Chunks issued after kt: min(STAGES − 2, nfull − 1 − kt); their loads may stay in flight.
+        const int ahead = min(C::STAGES - 2, nfull - 1 - kt);
+        if (C::STAGES > 3 && ahead >= 2) dma_sync<C::LPC * (C::STAGES > 3 ? 2 : 0)>();
+        else if (C::STAGES > 2 && ahead >= 1) dma_sync<C::LPC>();
         else dma_sync<0>();
         if (kt + C::STAGES - 1 < nfull) issue(kt + C::STAGES - 1);
         compute(smem + (kt % C::STAGES) * C::STAGE_BYTES);
@@ -629,8 +643,8 @@ __device__ __forceinline__ void tile_dma(unsigned char *smem, const GemmBf16Para
     const int kt0 = k_lo + nfull * BK;
     if (kt0 < k_hi) {
         dma_sync<0>();
-        for (int idx = tid; idx < (BM + C::BN) * 8; idx += C::NT) {
-            const int r = idx >> 3, c = idx & 7, kk = kt0 + 8 * c;
+        for (int idx = tid; idx < (BM + C::BN) * CPR; idx += C::NT) {
+            const int r = idx / CPR, c = idx % CPR, kk = kt0 + 8 * c;
             const bf16_t *src = nullptr;
             if (r < BM) {
                 const int gr = row0 + r;
@@ -652,7 +666,8 @@ __device__ __forceinline__ void tile_dma(unsigned char *smem, const GemmBf16Para
                                    e[4] | (uint32_t)e[5] << 16, e[6] | (uint32_t)e[7] << 16);
                 }
             }
-            *reinterpret_cast<uint4 *>(smem + r * 128 + ((c ^ (r & 7)) << 4)) = v;
+            // B rows start at BM, a multiple of 8: the same swizzle as row r − BM
+            *reinterpret_cast<uint4 *>(smem + r * ROWB + ((c ^ C::sw(r)) << 4)) = v;
         }
         dma_sync<0>();
         compute(smem);
@@ -824,31 +839,21 @@ void gemm_bf16_launch_cfg(hipStream_t s, const GemmBf16Params &p, int cfg) {
         case 2: launch_cfg<Cfg2, false>(s, q, vec, dual, gy); break;
         case 7: launch_cfg<Cfg7, true>(s, q, vec, dual, gy); break;
         case 9: launch_cfg<Cfg9, false>(s, q, vec, dual, gy); break;
+        case 10: launch_cfg<Cfg10, true>(s, q, vec, dual, gy); break;
         default: fail(CATNN_ERR_INVALID_ARGUMENT, "bf16 gemm: unknown tile configuration");
     }
 }
 
-// Tile choice, from a sweep of the training step's shapes on MI355X
-// (TFLOP/s).  The direct-to-LDS 128×128 tile with two blocks per CU
-// (configuration 7) leads on nearly all of them: 8192×4096×3072 898 (best
-// register-staged tile 742), 8192×1024×12288 947 (881), 8192×1024×4096 809
-// (778).  When the grid holds at most one 128×128 tile per CU — the long-k
-// weight gradients, 4096×1024×8192 — three stages in flight (configuration
-// 9) gain a little more: 773 against 745.  The SwiGLU forward (two B
-// operands, half the output columns) runs on configuration 7 as well;
-// launches without 16-byte aligned rows run on the register-staged tiles
-// (configuration 0 for the SwiGLU forward, 2 otherwise).
-void gemm_bf16_launch(hipStream_t s, const GemmBf16Params &p) {
-    if (p.epi == EPI_SWIGLU_FWD) {
-        gemm_bf16_launch_cfg(s, p, 7);
-        return;
-    }
-    const int64_t tn = (p.N + 127) / 128;
-    const int64_t tiles = p.grid == GRID_ROWS ? (int64_t)p.max_tiles * tn
-                                              : (int64_t)((p.M + 127) / 128) * tn *
-                                                    (p.grid == GRID_SEGK ? p.n_experts : 1);
-    gemm_bf16_launch_cfg(s, p, p.grid != GRID_ROWS && tiles <= 256 ? 9 : 7);
-}
+// Tile choice, from sweeps of the training step's shapes on MI355X
+// (TFLOP/s).  The direct-to-LDS 128×128 tile with two stages and two blocks
+// per CU (configuration 7) leads on all of them once the epilogue is staged:
+// 8192×4096×3072 839, 8192×1024×12288 898, 4096×1024×8192 732, against 603,
+// 663 and 683 for three stages at one block per CU (configuration 9) and 749,
+// 782 and 655 for four 32-deep stages (configuration 10); the register-staged
+// tiles reached 742, 881 and 585.  Launches without 16-byte aligned rows run
+// on the register-staged tiles (configuration 0 for the SwiGLU forward, 2
+// otherwise).
+void gemm_bf16_launch(hipStream_t s, const GemmBf16Params &p) { gemm_bf16_launch_cfg(s, p, 7); }
 
 }  // namespace k
 }  // namespace catnn

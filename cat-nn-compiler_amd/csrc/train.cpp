@@ -790,7 +790,8 @@ int catnn_hip_gemm_bf16_nt(catnn_hip_device *dev, const uint16_t *a, int64_t lda
                       CATNN_ERR_SHAPE_MISMATCH, "gemm_bf16: dims");
         CATNN_REQUIRE(lda >= k && ldb >= k && ldc >= n, CATNN_ERR_SHAPE_MISMATCH, "gemm_bf16: leading dims");
         CATNN_REQUIRE((a && b && c) || m * n == 0, CATNN_ERR_INVALID_ARGUMENT, "gemm_bf16: null operand");
-        CATNN_REQUIRE(tile_cfg == -1 || tile_cfg == 0 || tile_cfg == 2 || tile_cfg == 7 || tile_cfg == 9,
+        CATNN_REQUIRE(tile_cfg == -1 || tile_cfg == 0 || tile_cfg == 2 || tile_cfg == 7 || tile_cfg == 9 ||
+                          tile_cfg == 10,
                       CATNN_ERR_INVALID_ARGUMENT, "gemm_bf16: tile_cfg");
         k::GemmBf16Params p = gp();
         p.A = a; p.lda = lda; p.B = b; p.ldb = ldb;
