@@ -279,7 +279,7 @@ def main():
                      "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4),
                      "traffic": measured_traffic(),
-                     "kernel": "gemm_plain_kernel<128,128,16> (fp32 MFMA 32x32x2)",
+                     "kernel": "gemm_dma_kernel<4 stages> 128x128x16 direct-to-LDS (fp32 MFMA 32x32x2)",
                      "per_launch_flop": per_launch, "avg_launch_ms": round(gemm_ms, 4)},
     }
 

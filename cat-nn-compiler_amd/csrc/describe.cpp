@@ -37,18 +37,25 @@ uint32_t grid_for(int64_t n, int64_t per_thread) {
     return (uint32_t)std::max<int64_t>(1, std::min<int64_t>(cdiv(n, 256 * per_thread), 1 << 20));
 }
 
-// gemm_f32.hip: 128 × 128 tiles (64 output columns in the dual SwiGLU mode),
-// the 16-byte variant when K, N and both row strides are multiples of 4.
+// gemm_f32.hip: 128 × 128 tiles (64 output columns in the dual SwiGLU mode);
+// when K, N and both row strides are multiples of 4 (16-byte rows) the
+// direct-to-LDS kernel with 4 stages of 16 KiB dynamic LDS, otherwise the
+// register-staged kernel of the plain or the grouped grid.
 void gemm_f32(std::vector<Launch> &L, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb, bool dual,
               int64_t grouped_tiles) {
     const bool vec = K % 4 == 0 && N % 4 == 0 && lda % 4 == 0 && ldb % 4 == 0;
+    const bool grouped = grouped_tiles > 0;
     const int64_t bn = dual ? 64 : 128;
-    const int64_t tiles = grouped_tiles > 0 ? grouped_tiles * cdiv(N, bn) : cdiv(M, 128) * cdiv(N, bn);
+    const int64_t tiles = grouped ? grouped_tiles * cdiv(N, bn) : cdiv(M, 128) * cdiv(N, bn);
     if (tiles == 0) return;
-    std::string p = grouped_tiles > 0 ? "19gemm_grouped_kernelILi128ELi128ELi16ELb" : "17gemm_plain_kernelILi128ELi128ELi16ELb";
-    p += vec ? "1" : "0";
-    p += dual ? "ELb1E" : "ELb0E";
-    L.push_back({p, clamp_grid(tiles), 256, 0});
+    const std::string d = dual ? "1" : "0";
+    if (vec) {
+        L.push_back({"15gemm_dma_kernelILi4ELb" + d + "ELb" + (grouped ? "1" : "0") + "E", clamp_grid(tiles), 256,
+                     4 * 16384});
+        return;
+    }
+    std::string p = grouped ? "19gemm_grouped_kernelILi128ELi128ELi16ELb0ELb" : "17gemm_plain_kernelILi128ELi128ELi16ELb0ELb";
+    L.push_back({p + d + "E", clamp_grid(tiles), 256, 0});
 }
 
 // rowops.hip / decoder.hip row kernels: one wavefront per row, 4 rows per

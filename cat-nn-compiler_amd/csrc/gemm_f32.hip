@@ -260,6 +260,182 @@ __global__ __launch_bounds__(256, 2) void gemm_grouped_kernel(GemmParams p) {
                                       p.N, p.K, p.bias, p.R, p.ldr, p.C, p.ldc, p.act);
 }
 
+// Direct-to-LDS form of the 128 × 128 tile for 16-byte aligned launches, on
+// the plain or the grouped grid, single or dual (SwiGLU gate/up) operand: k
+// chunks of 16 go HBM → LDS by global_load_lds_dwordx4,
+// STAGES deep, with no registers in between.  A rows (k-contiguous) are 64
+// bytes, 4 chunks of 4 k values, chunk c of row r at position
+// c ^ ((r / 2) mod 4), so the 8 rows a read touches sit on distinct banks;
+// B rows (n-contiguous) are 512 bytes and need no swizzle.  A wave load
+// fills 1 KiB: 16 A rows or 2 B rows.  The MFMA schedule, the k split across
+// lane halves and the epilogue are those of gemm_block.
+template <int STAGES, bool DUAL, bool GROUPED>
+__global__ __launch_bounds__(256, 2) void gemm_dma_kernel(GemmParams p) {
+    constexpr int BM = 128, BN = 128, BK = 16, KH = BK / 2;
+    constexpr int WM = BM / 2, WN = BN / 2, FM = WM / 32, FN = WN / 32;
+    constexpr int BN_OUT = DUAL ? BN / 2 : BN;
+    constexpr int A_BYTES = BM * BK * 4, STAGE = A_BYTES + BK * BN * 4;  // 8 KiB + 8 KiB
+    constexpr int LPC = 4;  // wave loads per wavefront and chunk: 2 for A, 2 for B
+    static_assert(STAGES >= 2 && STAGES <= 4, "the main loop waits for up to 2 chunks ahead");
+    static_assert(!DUAL || FN == 2, "dual mode pairs one W1 and one W3 fragment");
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int tiles_n = (p.N + BN_OUT - 1) / BN_OUT;
+    const int lid = xcd_remap(blockIdx.x, gridDim.x);
+    int tm, tn, row0, M;  // M: the end of this tile's rows
+    const float *B = p.B, *B2 = p.B2;
+    if constexpr (GROUPED) {
+        grouped_tile(lid, p.max_tiles, tiles_n, 8, tm, tn);
+        if (tm >= *p.n_tiles) return;
+        const int e = p.tile_expert[tm];
+        row0 = p.tile_row0[tm];
+        M = p.seg_offsets[e + 1];
+        B = p.B_e[e];
+        B2 = DUAL ? p.B2_e[e] : nullptr;
+    } else {
+        grouped_tile(lid, (p.M + BM - 1) / BM, tiles_n, 8, tm, tn);
+        row0 = tm * BM;
+        M = p.M;
+    }
+    const int col0 = tn * BN_OUT, N = p.N, K = p.K;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1, lr = lane & 31, lg = lane >> 5;
+
+    // A: wave load q of wavefront w fills rows 16(2w + q) … +15, lane l row
+    // … + l/4 at position l mod 4 = chunk (l mod 4) ^ ((row / 2) mod 4).
+    const float *a_src[2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        const int r = (2 * wave + q) * 16 + (lane >> 2);
+        const int gr = row0 + r < M ? row0 + r : row0;  // rows past the end read row0; never stored
+        const int src = p.a_rows ? p.a_rows[gr] / p.a_row_div : gr;
+        a_src[q] = p.A + (int64_t)src * p.lda + 4 * ((lane & 3) ^ ((r >> 1) & 3));
+    }
+    // B: wave load q fills k rows 2(2w + q), +1: lane l row l/32, tile
+    // columns 4(l mod 32) … +3 — output columns col0 + those, or with DUAL
+    // W1 for the first BN/2 and W3 for the rest at the same output columns
+    // (past N: column col0, never stored).
+    const float *b_src[2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        const int kr = (2 * wave + q) * 2 + (lane >> 5);
+        const int tc = 4 * (lane & 31);
+        const bool second = DUAL && tc >= BN / 2;
+        const int c = col0 + tc - (second ? BN / 2 : 0);
+        b_src[q] = (second ? B2 : B) + (int64_t)kr * p.ldb + (c + 4 <= N ? c : col0);
+    }
+    auto issue = [&](int kt) {
+        unsigned char *st = smem + (kt % STAGES) * STAGE;
+        const int k0 = kt * BK;
+#pragma unroll
+        for (int q = 0; q < 2; ++q) load_lds16(a_src[q] + k0, st + (2 * wave + q) * 1024);
+#pragma unroll
+        for (int q = 0; q < 2; ++q) load_lds16(b_src[q] + (int64_t)k0 * p.ldb, st + A_BYTES + (2 * wave + q) * 1024);
+    };
+
+    f32x16 acc[FM][FN];
+#pragma unroll
+    for (int mi = 0; mi < FM; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < FN; ++ni)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[mi][ni][r] = 0.f;
+
+    // Lane half g takes k values g·KH … g·KH + KH − 1: A chunks 2g and 2g + 1.
+    auto compute = [&](const unsigned char *st) {
+        float af[FM][KH], bf[FN][KH];
+#pragma unroll
+        for (int mi = 0; mi < FM; ++mi) {
+            const int r = wm * WM + mi * 32 + lr;
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                const float4 v = *reinterpret_cast<const float4 *>(st + r * 64 + (((2 * lg + q) ^ ((r >> 1) & 3)) << 4));
+                af[mi][4 * q + 0] = v.x;
+                af[mi][4 * q + 1] = v.y;
+                af[mi][4 * q + 2] = v.z;
+                af[mi][4 * q + 3] = v.w;
+            }
+        }
+        const float *bt = reinterpret_cast<const float *>(st + A_BYTES);
+#pragma unroll
+        for (int ni = 0; ni < FN; ++ni) {
+            const int col = DUAL ? (ni * (BN / 2) + wn * 32 + lr) : (wn * WN + ni * 32 + lr);
+#pragma unroll
+            for (int s2 = 0; s2 < KH; ++s2) bf[ni][s2] = bt[(lg * KH + s2) * BN + col];
+        }
+#pragma unroll
+        for (int s2 = 0; s2 < KH; ++s2)
+#pragma unroll
+            for (int mi = 0; mi < FM; ++mi)
+#pragma unroll
+                for (int ni = 0; ni < FN; ++ni)
+                    acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[mi][s2], bf[ni][s2], acc[mi][ni], 0, 0, 0);
+    };
+
+    const int nfull = K / BK;
+#pragma unroll
+    for (int j = 0; j < STAGES - 1; ++j)
+        if (j < nfull) issue(j);
+    for (int kt = 0; kt < nfull; ++kt) {
+        const int ahead = min(STAGES - 2, nfull - 1 - kt);  // chunks issued after kt
+        if (STAGES > 3 && ahead >= 2) dma_sync<2 * LPC>();
+        else if (STAGES > 2 && ahead >= 1) dma_sync<LPC>();
+        else dma_sync<0>();
+        if (kt + STAGES - 1 < nfull) issue(kt + STAGES - 1);
+        compute(smem + (kt % STAGES) * STAGE);
+    }
+    const int k0 = nfull * BK;
+    if (k0 < K) {  // partial last chunk through registers, zero past K (K % 4 == 0 here)
+        dma_sync<0>();
+        for (int i = tid; i < BM * 4 + BK * (BN / 4); i += 256) {
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            unsigned char *dst;
+            if (i < BM * 4) {
+                const int r = i >> 2, c = i & 3, kk = k0 + 4 * c;
+                if (row0 + r < M && kk < K) {
+                    const int src = p.a_rows ? p.a_rows[row0 + r] / p.a_row_div : row0 + r;
+                    v = *reinterpret_cast<const float4 *>(p.A + (int64_t)src * p.lda + kk);
+                }
+                dst = smem + r * 64 + ((c ^ ((r >> 1) & 3)) << 4);
+            } else {
+                const int j = i - BM * 4, kr = j / (BN / 4), tc = (j % (BN / 4)) * 4;
+                const bool second = DUAL && tc >= BN / 2;
+                const int c = col0 + tc - (second ? BN / 2 : 0);
+                if (k0 + kr < K && c + 4 <= N)
+                    v = *reinterpret_cast<const float4 *>((second ? B2 : B) + (int64_t)(k0 + kr) * p.ldb + c);
+                dst = smem + A_BYTES + (kr * BN + tc) * 4;
+            }
+            *reinterpret_cast<float4 *>(dst) = v;
+        }
+        dma_sync<0>();
+        compute(smem);
+    }
+
+#pragma unroll
+    for (int mi = 0; mi < FM; ++mi) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int row = row0 + wm * WM + mi * 32 + 8 * (r >> 2) + 4 * lg + (r & 3);
+            if (row >= M) continue;
+            if constexpr (DUAL) {
+                const int col = col0 + wn * 32 + lr;
+                if (col < N) p.C[(int64_t)row * p.ldc + col] = silu(acc[mi][0][r]) * acc[mi][1][r];
+            } else {
+#pragma unroll
+                for (int ni = 0; ni < FN; ++ni) {
+                    const int col = col0 + wn * WN + ni * 32 + lr;
+                    if (col >= N) continue;
+                    float v = acc[mi][ni][r];
+                    if (p.bias) v += p.bias[col];
+                    v = apply_act(v, p.act);
+                    if (p.R) v = p.R[(int64_t)row * p.ldr + col] + v;
+                    p.C[(int64_t)row * p.ldc + col] = v;
+                }
+            }
+        }
+    }
+}
+
 // Tile-table builder for the grouped grid: one entry per BM-row tile of each
 // expert's segment, in expert order.  Single wavefront; n_experts is small.
 __global__ void build_tiles_kernel(const int32_t *__restrict__ offsets, int n_experts, int bm,
@@ -278,6 +454,7 @@ __global__ void build_tiles_kernel(const int32_t *__restrict__ offsets, int n_ex
 }
 
 constexpr int kBM = 128, kBN = 128, kBK = 16;
+constexpr int kDmaStages = 4;  // gemm_dma_kernel chunks in LDS (16 KiB each)
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
@@ -294,12 +471,15 @@ void gemm_launch(hipStream_t s, const GemmParams &p, bool dual) {
     const int64_t tiles = (int64_t)((p.M + kBM - 1) / kBM) * ((p.N + bn_out - 1) / bn_out);
     CATNN_REQUIRE(tiles < (1ll << 31), CATNN_ERR_SHAPE_MISMATCH, "gemm: grid too large");
     dim3 grid((unsigned)tiles), block(256);
-    if (dual) {
-        if (vec) gemm_plain_kernel<kBM, kBN, kBK, true, true><<<grid, block, 0, s>>>(p);
-        else gemm_plain_kernel<kBM, kBN, kBK, false, true><<<grid, block, 0, s>>>(p);
+    constexpr size_t dma_lds = kDmaStages * 16384;
+    if (vec && dual) {
+        gemm_dma_kernel<kDmaStages, true, false><<<grid, block, dma_lds, s>>>(p);
+    } else if (vec) {
+        gemm_dma_kernel<kDmaStages, false, false><<<grid, block, dma_lds, s>>>(p);
+    } else if (dual) {
+        gemm_plain_kernel<kBM, kBN, kBK, false, true><<<grid, block, 0, s>>>(p);
     } else {
-        if (vec) gemm_plain_kernel<kBM, kBN, kBK, true, false><<<grid, block, 0, s>>>(p);
-        else gemm_plain_kernel<kBM, kBN, kBK, false, false><<<grid, block, 0, s>>>(p);
+        gemm_plain_kernel<kBM, kBN, kBK, false, false><<<grid, block, 0, s>>>(p);
     }
     CATNN_HIP(hipGetLastError());
 }
@@ -316,13 +496,11 @@ void gemm_grouped_launch(hipStream_t s, const GemmParams &p, bool dual) {
     if (tiles == 0) return;
     CATNN_REQUIRE(tiles < (1ll << 31), CATNN_ERR_SHAPE_MISMATCH, "grouped gemm: grid too large");
     dim3 grid((unsigned)tiles), block(256);
-    if (dual) {
-        if (vec) gemm_grouped_kernel<kBM, kBN, kBK, true, true><<<grid, block, 0, s>>>(p);
-        else gemm_grouped_kernel<kBM, kBN, kBK, false, true><<<grid, block, 0, s>>>(p);
-    } else {
-        if (vec) gemm_grouped_kernel<kBM, kBN, kBK, true, false><<<grid, block, 0, s>>>(p);
-        else gemm_grouped_kernel<kBM, kBN, kBK, false, false><<<grid, block, 0, s>>>(p);
-    }
+    constexpr size_t dma_lds = kDmaStages * 16384;
+    if (vec && dual) gemm_dma_kernel<kDmaStages, true, true><<<grid, block, dma_lds, s>>>(p);
+    else if (vec) gemm_dma_kernel<kDmaStages, false, true><<<grid, block, dma_lds, s>>>(p);
+    else if (dual) gemm_grouped_kernel<kBM, kBN, kBK, false, true><<<grid, block, 0, s>>>(p);
+    else gemm_grouped_kernel<kBM, kBN, kBK, false, false><<<grid, block, 0, s>>>(p);
     CATNN_HIP(hipGetLastError());
 }
 

@@ -20,9 +20,12 @@ def test_kernel_table_reads_the_code_objects():
     for r in rows:
         assert r.code_bytes > 0 and r.kernarg_bytes > 0 and r.sgprs > 0, r.kernel
         assert r.block[0] in (256, 512, 1024), r.kernel
-    # the fp32 MFMA GEMM keeps its accumulators in registers, no scratch
-    g = next(r for r in rows if "gemm_plain_kernelILi128ELi128ELi16ELb1ELb0E" in r.kernel)
+    # the fp32 MFMA GEMM keeps its accumulators in registers, no scratch; the
+    # register-staged form declares its LDS, the direct-to-LDS form takes it at launch
+    g = next(r for r in rows if "gemm_plain_kernelILi128ELi128ELi16ELb0ELb0E" in r.kernel)
     assert g.scratch_bytes_per_lane == 0 and g.vgprs >= 64 and g.static_lds_bytes > 0
+    g = next(r for r in rows if "gemm_dma_kernelILi4ELb0ELb0E" in r.kernel)
+    assert g.scratch_bytes_per_lane == 0 and g.vgprs >= 64 and g.static_lds_bytes == 0
     # the bf16 GEMM keeps its accumulators in AGPRs, counted inside the unified VGPR total
     b = next(r for r in rows if "gemm_bf16_kernelINS1_4DCfg" in r.kernel)
     assert 0 < b.agprs < b.vgprs
@@ -35,14 +38,15 @@ def test_linear_is_one_gemm_launch():
     r = describe(node, [TensorType.f32([8192, 4096])])
     assert len(r.launches) == 1
     k = r.launches[0]
-    assert "gemm_plain_kernelILi128ELi128ELi16ELb1ELb0E" in k.kernel
+    assert "gemm_dma_kernelILi4ELb0ELb0E" in k.kernel
     assert k.grid == (64 * 128, 1, 1) and k.block == (256, 1, 1)
+    assert k.dynamic_lds_bytes == 4 * 16384
     assert r.code_bytes == k.code_bytes and not r.code_estimated
     assert r.registers_per_thread == k.vgprs  # unified VGPR + AGPR count
-    assert r.scratch_bytes() == k.static_lds_bytes + r.registers_per_thread * 4 * 256
-    # K not a multiple of 4: the element-load variant
+    assert r.scratch_bytes() == 4 * 16384 + r.registers_per_thread * 4 * 256
+    # K not a multiple of 4: the register-staged element-load variant
     odd = IrNode(1, "fc", OpenOp.linear(7, 5, False), TensorType.f32([3, 5]), {"w": _z([7, 5])})
-    assert "ELb0ELb0E" in describe(odd, [TensorType.f32([3, 7])]).launches[0].kernel
+    assert "gemm_plain_kernelILi128ELi128ELi16ELb0ELb0E" in describe(odd, [TensorType.f32([3, 7])]).launches[0].kernel
 
 
 def test_attention_block_and_moe_layer():
@@ -58,7 +62,7 @@ def test_attention_block_and_moe_layer():
     r = describe(moe, [TensorType.f32([8, 2048, 1024])])
     names = [k.kernel for k in r.launches]
     assert "route_dma_kernelILi2E" in names[0] and "combine4_kernel" in names[-1]
-    dual = next(k for k in r.launches if "gemm_grouped_kernelILi128ELi128ELi16ELb1ELb1E" in k.kernel)
+    dual = next(k for k in r.launches if "gemm_dma_kernelILi4ELb1ELb1E" in k.kernel)
     assert dual.grid[0] == (32768 // 128 + 8) * (3584 // 64)
     assert r.launches[0].dynamic_lds_bytes == 4 * (4 * 8 * 260 + 8 * (1024 + 4) + 32 * 8)
     assert r.code_bytes == sum({k.kernel: k.code_bytes for k in r.launches}.values())
@@ -87,8 +91,9 @@ def _every_kernel_path():
         yield (IrNode(1, f"gqa{hd}", OpenOp.gqa_attention(4, 2, hd, d, 8, 10000), f([2, 9, d]),
                       {"wq": _z([d, d]), "wk": _z([d, 2 * hd]), "wv": _z([d, 2 * hd]), "wo": _z([d, d])}),
                [f([2, 9, d])])
-    yield (IrNode(1, "swiglu", OpenOp.swiglu(16, 30), ty, {"w1": _z([16, 30]), "w3": _z([16, 30]),
-                                                           "w2": _z([30, 16])}), [ty])
+    for inter in (30, 32):  # register-staged dual tile, direct-to-LDS dual tile
+        yield (IrNode(1, f"swiglu{inter}", OpenOp.swiglu(16, inter), ty,
+                      {"w1": _z([16, inter]), "w3": _z([16, inter]), "w2": _z([inter, 16])}), [ty])
     yield IrNode(1, "lm", OpenOp.lm_head(16, 50), f([2, 8, 50]), {"w": _z([50, 16])}), [ty]
     yield IrNode(1, "mix", OpenOp.mix(), ty), [ty, ty]
     moe = {"gate": _z([10, 4])}
@@ -115,6 +120,7 @@ def test_every_kernel_named_resolves_once():
     assert any("route_dma_kernelILi4E" in k for k in seen) and any("route_dma_kernelILi1E" in k for k in seen)
     assert any("attn_generic_kernel" in k for k in seen) and any("attn_mfma_kernel" in k for k in seen)
     assert any("rms_norm_any_kernel" in k for k in seen) and any("embedding_kernelILb0E" in k for k in seen)
+    assert any("gemm_grouped_kernel" in k for k in seen) and any("gemm_dma_kernelILi4ELb1ELb0E" in k for k in seen)
     # copies launch no kernel
     ty = TensorType.f32([2, 3])
     r = describe(IrNode(1, "t", OpenOp.transpose(0, 1), ty), [ty])
