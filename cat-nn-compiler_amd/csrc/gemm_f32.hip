@@ -276,7 +276,7 @@ __global__ __launch_bounds__(256, 2) void gemm_dma_kernel(GemmParams p) {
     constexpr int BN_OUT = DUAL ? BN / 2 : BN;
     constexpr int A_BYTES = BM * BK * 4, STAGE = A_BYTES + BK * BN * 4;  // 8 KiB + 8 KiB
     constexpr int LPC = 4;  // wave loads per wavefront and chunk: 2 for A, 2 for B
-    static_assert(STAGES >= 2 && STAGES <= 4, "the main loop waits for up to 2 chunks ahead");
+    static_assert(STAGES >= 2 && STAGES <= 4, "the waits cover up to 3 chunks in flight");
     static_assert(!DUAL || FN == 2, "dual mode pairs one W1 and one W3 fragment");
     extern __shared__ __align__(16) unsigned char smem[];
     const int tiles_n = (p.N + BN_OUT - 1) / BN_OUT;
@@ -342,18 +342,20 @@ __global__ __launch_bounds__(256, 2) void gemm_dma_kernel(GemmParams p) {
             for (int r = 0; r < 16; ++r) acc[mi][ni][r] = 0.f;
 
     // Lane half g takes k values g·KH … g·KH + KH − 1: A chunks 2g and 2g + 1.
-    auto compute = [&](const unsigned char *st) {
-        float af[FM][KH], bf[FN][KH];
+    struct Frags {
+        float a[FM][KH], b[FN][KH];
+    };
+    auto load_frags = [&](const unsigned char *st, Frags &f) {
 #pragma unroll
         for (int mi = 0; mi < FM; ++mi) {
             const int r = wm * WM + mi * 32 + lr;
 #pragma unroll
             for (int q = 0; q < 2; ++q) {
                 const float4 v = *reinterpret_cast<const float4 *>(st + r * 64 + (((2 * lg + q) ^ ((r >> 1) & 3)) << 4));
-                af[mi][4 * q + 0] = v.x;
-                af[mi][4 * q + 1] = v.y;
-                af[mi][4 * q + 2] = v.z;
-                af[mi][4 * q + 3] = v.w;
+                f.a[mi][4 * q + 0] = v.x;
+                f.a[mi][4 * q + 1] = v.y;
+                f.a[mi][4 * q + 2] = v.z;
+                f.a[mi][4 * q + 3] = v.w;
             }
         }
         const float *bt = reinterpret_cast<const float *>(st + A_BYTES);
@@ -361,28 +363,61 @@ __global__ __launch_bounds__(256, 2) void gemm_dma_kernel(GemmParams p) {
         for (int ni = 0; ni < FN; ++ni) {
             const int col = DUAL ? (ni * (BN / 2) + wn * 32 + lr) : (wn * WN + ni * 32 + lr);
 #pragma unroll
-            for (int s2 = 0; s2 < KH; ++s2) bf[ni][s2] = bt[(lg * KH + s2) * BN + col];
+            for (int s2 = 0; s2 < KH; ++s2) f.b[ni][s2] = bt[(lg * KH + s2) * BN + col];
         }
+    };
+    auto mma = [&](const Frags &f) {
 #pragma unroll
         for (int s2 = 0; s2 < KH; ++s2)
 #pragma unroll
             for (int mi = 0; mi < FM; ++mi)
 #pragma unroll
                 for (int ni = 0; ni < FN; ++ni)
-                    acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[mi][s2], bf[ni][s2], acc[mi][ni], 0, 0, 0);
+                    acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x2f32(f.a[mi][s2], f.b[ni][s2], acc[mi][ni], 0, 0, 0);
     };
 
+    // Software pipeline: the fragments of chunk kt + 1 are read from LDS
+    // while the MFMAs of chunk kt (already in registers) run.  Chunk kt + S
+    // goes into chunk kt's slot once every wavefront has read chunk kt (the
+    // lgkmcnt(0) before the barrier of step kt).  The wait before that
+    // barrier lets the loads of the chunks issued after kt + 1 stay in
+    // flight: up to S − 2 of them.
     const int nfull = K / BK;
+    Frags f0, f1;
 #pragma unroll
-    for (int j = 0; j < STAGES - 1; ++j)
+    for (int j = 0; j < STAGES; ++j)
         if (j < nfull) issue(j);
-    for (int kt = 0; kt < nfull; ++kt) {
-        const int ahead = min(STAGES - 2, nfull - 1 - kt);  // chunks issued after kt
-        if (STAGES > 3 && ahead >= 2) dma_sync<2 * LPC>();
-        else if (STAGES > 2 && ahead >= 1) dma_sync<LPC>();
+    // Chunk c landed for every wavefront, with the loads of up to `most`
+    // chunks issued after c still in flight (fewer near the end of K).
+    auto wait_chunk = [&](int c, int most) {
+        const int ahead = min(most, nfull - 1 - c);
+        if (STAGES > 3 && ahead >= 3) dma_sync<3 * LPC>();
+        else if (STAGES > 2 && ahead >= 2) dma_sync<2 * LPC>();
+        else if (ahead >= 1) dma_sync<LPC>();
         else dma_sync<0>();
-        if (kt + STAGES - 1 < nfull) issue(kt + STAGES - 1);
-        compute(smem + (kt % STAGES) * STAGE);
+    };
+    // Step kt for kt + 1 < nfull.  No LDS read is left pending on any path
+    // into mma(cur), so the compiler's own wait there is for cur alone.
+    auto step = [&](int kt, Frags &cur, Frags &nxt) {
+        wait_chunk(kt + 1, STAGES - 2);  // issued so far: chunks up to kt + S − 1
+        if (kt + STAGES < nfull) issue(kt + STAGES);
+        load_frags(smem + ((kt + 1) % STAGES) * STAGE, nxt);
+        mma(cur);
+    };
+    if (nfull > 0) {
+        wait_chunk(0, STAGES - 1);  // issued so far: chunks 0 … S − 1
+        load_frags(smem, f0);
+        int kt = 0;
+        for (; kt + 2 < nfull; kt += 2) {
+            step(kt, f0, f1);
+            step(kt + 1, f1, f0);
+        }
+        if (kt + 1 < nfull) {  // two chunks left
+            step(kt, f0, f1);
+            mma(f1);
+        } else {
+            mma(f0);
+        }
     }
     const int k0 = nfull * BK;
     if (k0 < K) {  // partial last chunk through registers, zero past K (K % 4 == 0 here)
@@ -408,7 +443,8 @@ __global__ __launch_bounds__(256, 2) void gemm_dma_kernel(GemmParams p) {
             *reinterpret_cast<float4 *>(dst) = v;
         }
         dma_sync<0>();
-        compute(smem);
+        load_frags(smem, f0);
+        mma(f0);
     }
 
 #pragma unroll
