@@ -718,8 +718,14 @@ __global__ __launch_bounds__(C::NT) void gemm_bf16_kernel(GemmBf16Params p) {
         int tm, tn;
         grouped_tile(lid, tiles_m, tiles_n, 8, tm, tn);
         const int e = blockIdx.y;
-        const int lo = p.seg_offsets[e];
-        const int hi = p.seg_counts ? lo + p.seg_counts[e] : p.seg_offsets[e + 1];
+        int lo, hi;
+        if (p.seg_offsets) {
+            lo = p.seg_offsets[e];
+            hi = p.seg_counts ? lo + p.seg_counts[e] : p.seg_offsets[e + 1];
+        } else {  // split K: equal segments of ksplit
+            lo = e * p.ksplit;
+            hi = min(p.K, lo + p.ksplit);
+        }
         run_tile<C, VEC, DUAL, GRID>(smem, p, p.B, nullptr, tm * C::BM, p.M, tn * bn_out, lo, hi, p.C_e[e]);
     }
 }
@@ -803,6 +809,24 @@ void launch_cfg(hipStream_t s, const GemmBf16Params &p, bool vec, bool dual, uns
 }  // namespace
 
 int gemm_bf16_tile_rows() { return kRowTile; }
+
+// Up to 8 splits while the split grid stays within 512 tiles (two per CU)
+// and each segment keeps 1024 or more k values; only grids of at most 128
+// tiles (half the CUs) with 16-byte output rows are split.  The case is a
+// weight gradient with few outputs and many tokens: config 5's wo gradient
+// (1024 × 1024 × 8192, 64 tiles) took 89 µs unsplit, 193 TFLOP/s; the
+// 192–256-tile gradients already reach 550–640 TFLOP/s on one tile per CU,
+// and splitting them measured no faster once the partial sums are added.
+int gemm_bf16_splitk(int64_t M, int64_t N, int64_t K) {
+    const int64_t tiles = ((M + 127) / 128) * ((N + 127) / 128);
+    if (tiles > 128 || K < 2048 || N % 4 != 0) return 1;
+    int s = 1;
+    while (s < 8 && tiles * s * 2 <= 512 && K / (s * 2) >= 1024) s *= 2;
+    return s;
+}
+
+// Segment length: whole 64-deep chunks (the last segment takes the rest).
+int gemm_bf16_splitk_len(int64_t K, int splits) { return (int)((K / splits + 63) / 64 * 64); }
 
 void gemm_bf16_launch_cfg(hipStream_t s, const GemmBf16Params &p, int cfg) {
     CATNN_REQUIRE(p.M >= 0 && p.N >= 0 && p.K >= 0, CATNN_ERR_SHAPE_MISMATCH, "bf16 gemm: dims");

@@ -61,6 +61,7 @@ struct GemmBf16Params {
     const int32_t *seg_offsets;  // segment e starts at seg_offsets[e]
     const int32_t *seg_counts;   // ... and holds seg_counts[e] rows (null: ends at seg_offsets[e+1])
     int segk_aligned;            // GRID_SEGK: caller guarantees seg_offsets[e] % 8 == 0
+    int ksplit;                  // GRID_SEGK with seg_offsets null: segment e is [e·ksplit, (e+1)·ksplit) ∩ [0, K)
     int vec_epi;                 // set by the launcher: output rows allow 16-byte epilogue accesses
     int max_tiles;
     int n_experts;
@@ -73,6 +74,10 @@ void gemm_bf16_launch(hipStream_t s, const GemmBf16Params &p);
 // The same with a fixed tile configuration (0, 2, 7 or 9; see gemm_bf16.hip).
 void gemm_bf16_launch_cfg(hipStream_t s, const GemmBf16Params &p, int cfg);
 int gemm_bf16_tile_rows();
+// K splits for a plain store/accumulate GEMM whose tiles alone leave the
+// GPU's CUs idle (1 = no split); gemm_bf16_splitk_len gives the segment.
+int gemm_bf16_splitk(int64_t M, int64_t N, int64_t K);
+int gemm_bf16_splitk_len(int64_t K, int splits);
 
 }  // namespace k
 }  // namespace catnn

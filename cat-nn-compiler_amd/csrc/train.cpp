@@ -128,9 +128,39 @@ k::GemmBf16Params gp() {
     return p;
 }
 
-// C32 (=/+=) A[M,K]·B[N,K]ᵀ on bf16 operands.
+// Bytes of split-K partial sums gemm_nt needs for an M×N×K product (at
+// least one 256-byte block, so that the request is never empty).
+uint64_t wparts_bytes(int64_t M, int64_t N, int64_t K) {
+    const int sp = k::gemm_bf16_splitk(M, N, K);
+    return sp > 1 ? (uint64_t)sp * M * N * 4 : 256;
+}
+
+// C32 (=/+=) A[M,K]·B[N,K]ᵀ on bf16 operands.  With `wparts` (wparts_bytes
+// of scratch) a grid too small for the GPU is split along K: each segment
+// stores its partial product there and sum_parts adds them into C in order.
 void gemm_nt(hipStream_t s, const bf16_t *A, int64_t lda, const bf16_t *B, int64_t ldb, int M, int N,
-             int K, float *C, int64_t ldc, bool accumulate) {
+             int K, float *C, int64_t ldc, bool accumulate, float *wparts = nullptr) {
+    const int sp = wparts ? k::gemm_bf16_splitk(M, N, K) : 1;
+    if (sp > 1 && ldc == N) {
+        k::GemmBf16Params p = gp();
+        p.A = A;
+        p.lda = lda;
+        p.B = B;
+        p.ldb = ldb;
+        p.M = M;
+        p.N = N;
+        p.K = K;
+        p.epi = k::EPI_STORE;
+        p.ldc32 = N;
+        p.grid = k::GRID_SEGK;
+        p.ksplit = k::gemm_bf16_splitk_len(K, sp);
+        p.segk_aligned = p.ksplit % 8 == 0;
+        p.n_experts = sp;
+        for (int e = 0; e < sp; ++e) p.C_e[e] = wparts + (int64_t)e * M * N;
+        k::gemm_bf16_launch(s, p);
+        k::sum_parts(s, wparts, sp, (int64_t)M * N, C, accumulate);
+        return;
+    }
     k::GemmBf16Params p = gp();
     p.A = A;
     p.lda = lda;
@@ -319,6 +349,7 @@ static void plan_trainer(Tr &t) {
                     scratch(tn, "dyb", (uint64_t)(M * N) * 2);
                 scratch(tn, "dybt", (uint64_t)(M * N) * 2);
                 scratch(tn, "colsum", k::colsum_scratch_bytes(M, (int)N));
+                scratch(tn, "wparts", wparts_bytes(K, N, M));
                 break;
             }
             case CATNN_OP_LAYER_NORM: {
@@ -355,6 +386,7 @@ static void plan_trainer(Tr &t) {
                 scratch(tn, "dqkvt", (uint64_t)(T * 3 * D) * 2);
                 scratch(tn, "xbt", (uint64_t)(T * D) * 2);
                 scratch(tn, "dscr", k::attention_bwd_scratch_bytes(Bt, S, H));
+                scratch(tn, "wparts", std::max(wparts_bytes(D, D, T), wparts_bytes(D, 3 * D, T)));
                 break;
             }
             case CATNN_OP_MOE: {
@@ -624,7 +656,7 @@ static void backward_node(Tr &t, TNode &tn) {
             }
             k::transpose_bf16(s, dyb, N, nullptr, 1, (int)M, (int)N, dybt, M);
             k::transpose_bf16(s, x3, 3 * K, nullptr, 1, (int)M, (int)K, xbt, M);  // hi part of x
-            gemm_nt(s, xbt, M, dybt, M, (int)K, (int)N, (int)M, w->grad, N, false);
+            gemm_nt(s, xbt, M, dybt, M, (int)K, (int)N, (int)M, w->grad, N, false, (float *)tn.B("wparts"));
             if (b) k::colsum(s, dy, M, (int)N, b->grad, false, (float *)tn.B("colsum"));
             break;
         }
@@ -650,7 +682,7 @@ static void backward_node(Tr &t, TNode &tn) {
             gemm_nt(s, dyb, D, wo->b, D, (int)T, (int)D, (int)D, dctx, D, false);
             k::transpose_bf16(s, dyb, D, nullptr, 1, (int)T, (int)D, dybt, T);
             k::transpose_bf16(s, (bf16_t *)tn.B("ctx3"), 3 * D, nullptr, 1, (int)T, (int)D, ctxt, T);
-            gemm_nt(s, ctxt, T, dybt, T, (int)D, (int)D, (int)T, wo->grad, D, false);
+            gemm_nt(s, ctxt, T, dybt, T, (int)D, (int)D, (int)T, wo->grad, D, false, (float *)tn.B("wparts"));
             k::attention_core_bwd(s, qkv, qkv + D, qkv + 2 * D, 3 * D, (float *)tn.B("ctx"), dctx, D,
                                   (float *)tn.B("lse"), dqkv, dqkv + D, dqkv + 2 * D, 3 * D, Bt, S, H, dh,
                                   causal, (float *)tn.B("dscr"));
@@ -660,7 +692,8 @@ static void backward_node(Tr &t, TNode &tn) {
                         !tn.first_writer[0]);
             k::transpose_bf16(s, dqkvb, 3 * D, nullptr, 1, (int)T, (int)(3 * D), dqkvt, T);
             k::transpose_bf16(s, x3, 3 * D, nullptr, 1, (int)T, (int)D, xbt, T);
-            gemm_nt(s, xbt, T, dqkvt, T, (int)D, (int)(3 * D), (int)T, wqkv->grad, 3 * D, false);
+            gemm_nt(s, xbt, T, dqkvt, T, (int)D, (int)(3 * D), (int)T, wqkv->grad, 3 * D, false,
+                    (float *)tn.B("wparts"));
             break;
         }
         case CATNN_OP_MOE: {

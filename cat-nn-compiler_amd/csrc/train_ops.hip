@@ -290,6 +290,30 @@ __global__ __launch_bounds__(256) void reduce_partials_kernel(const float *__res
     }
 }
 
+// out[i] (+)= part[0][i] + part[1][i] + … in that order, four floats a
+// thread per step (the split-K partial sums of one GEMM).
+__global__ __launch_bounds__(256) void sum_parts_kernel(const float4 *__restrict__ part, int np, int64_t n4,
+                                                        float4 *__restrict__ out, int accumulate) {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (int64_t)gridDim.x * 256) {
+        float4 t = part[i];
+        for (int e = 1; e < np; ++e) {
+            const float4 u = part[(int64_t)e * n4 + i];
+            t.x += u.x;
+            t.y += u.y;
+            t.z += u.z;
+            t.w += u.w;
+        }
+        if (accumulate) {
+            const float4 o = out[i];
+            t.x = o.x + t.x;
+            t.y = o.y + t.y;
+            t.z = o.z + t.z;
+            t.w = o.w + t.w;
+        }
+        out[i] = t;
+    }
+}
+
 // LayerNorm adjoint, dx (+)= (rstd/n)(n·g − Σg − x̂·Σ(g·x̂)) with g = dy·γ:
 // one wavefront per row, the row held in registers (NV values per lane,
 // cols ≤ 64·NV), so x and dy are read once.
@@ -656,6 +680,18 @@ void ln_forward_train(hipStream_t s, const float *x, const float *g, const float
 uint64_t ln_backward_scratch_bytes(int64_t rows, int cols) {
     const int64_t ng = (rows + kColRows - 1) / kColRows;
     return (uint64_t)ng * cols * 4 * 2;
+}
+
+void sum_parts(hipStream_t s, const float *parts, int np, int64_t n, float *out, bool accumulate) {
+    CATNN_REQUIRE(np >= 1 && n % 4 == 0 && (reinterpret_cast<uintptr_t>(parts) & 15) == 0 &&
+                      (reinterpret_cast<uintptr_t>(out) & 15) == 0,
+                  CATNN_ERR_SHAPE_MISMATCH, "sum_parts: needs 16-byte aligned rows of floats");
+    if (n == 0) return;
+    const int64_t n4 = n / 4;
+    const unsigned blocks = (unsigned)std::min<int64_t>((n4 + 255) / 256, 4096);
+    sum_parts_kernel<<<blocks, 256, 0, s>>>(reinterpret_cast<const float4 *>(parts), np, n4,
+                                            reinterpret_cast<float4 *>(out), accumulate ? 1 : 0);
+    CATNN_HIP(hipGetLastError());
 }
 
 static void reduce_partials(hipStream_t s, const float *part, int64_t ng, int cols, float *out,

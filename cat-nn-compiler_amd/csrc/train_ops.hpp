@@ -36,6 +36,9 @@ void ln_backward(hipStream_t s, const float *x, const float *g, const float *mea
                  const float *dy, float *dx, bool accumulate, float *dg, float *db, bool acc_params,
                  int64_t rows, int cols, float *scratch);
 
+// out (=/+=) Σ_e parts[e], e = 0 … np−1 in order, each part n floats.
+void sum_parts(hipStream_t s, const float *parts, int np, int64_t n, float *out, bool accumulate);
+
 uint64_t colsum_scratch_bytes(int64_t rows, int cols);
 void colsum(hipStream_t s, const float *y, int64_t rows, int cols, float *out, bool accumulate,
             float *scratch);

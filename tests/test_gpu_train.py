@@ -133,6 +133,14 @@ def test_block_plus_moe_config5_shape(device):
     assert agree > 0.97
 
 
+def test_block_plus_moe_split_k_weight_gradients(device):
+    # 2048 tokens over 128-wide layers: the weight-gradient GEMMs have one or
+    # two output tiles and K = 2048, so they run split along K (two segments
+    # whose partial sums are added afterwards).
+    w = configs.config5(batch=2, seq=1024, d=128, heads=2, ffn=256, n_experts=4, top_k=2, inter=128)
+    _check_step(device, w.graph, w.x, w.target, tight=TIGHT_CONFIG5)
+
+
 def test_block_plus_moe_ragged(device):
     w = configs.config5(batch=1, seq=77, d=128, heads=2, ffn=256, n_experts=4, top_k=2, inter=96)
     _check_step(device, w.graph, w.x, w.target, tight=TIGHT_CONFIG5)
