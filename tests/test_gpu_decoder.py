@@ -97,7 +97,7 @@ def test_gqa_long_positions_rotate_like_the_f64_table(device):
     assert _run(device, node, [r.standard_normal((1, 2048, 128))])[2] < TOL
 
 
-@pytest.mark.parametrize("T,H,I", [(8, 32, 64), (300, 96, 200), (1024, 256, 704)])
+@pytest.mark.parametrize("T,H,I", [(8, 32, 64), (300, 96, 200), (1024, 256, 704), (37, 100, 52)])
 def test_swiglu(device, T, H, I):
     r = np.random.default_rng(T)
     node = IrNode(1, "swiglu", OpenOp.swiglu(H, I), TensorType.f32([T, H]),
