@@ -29,7 +29,6 @@ __device__ __forceinline__ float apply_act(float v, int act) {
 // its 16 bytes at destination + 16·l.
 typedef __attribute__((address_space(3))) void lds_void_t;
 
-//
 // Issued from inline assembly rather than __builtin_amdgcn_global_load_lds:
 // for the builtin the compiler makes every later LDS access of the wavefront
 // wait for all direct-to-LDS loads in flight (vmcnt(0)), whatever stage they
@@ -37,10 +36,17 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 // Here the compiler sees no LDS write, so the caller's dma_sync waits are the
 // only ones and must cover every read of the stage a load fills.  M0 holds
 // the wavefront's LDS base; one wait state separates its write from the load.
-__device__ __forceinline__ void load_lds16(const void *src, void *lds_wave_base) {
-    const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(size_t)(lds_void_t *)lds_wave_base);
+// load_lds16_at takes the destination as an LDS byte address (lds_addr),
+// which saves the generic-to-LDS pointer conversion per load when the
+// caller keeps the base.
+__device__ __forceinline__ uint32_t lds_addr(const void *p) { return (uint32_t)(size_t)(lds_void_t *)p; }
+__device__ __forceinline__ void load_lds16_at(const void *src, uint32_t lds_wave_base) {
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_wave_base);
     asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(m0), "v"(src)
                  : "memory", "m0");
+}
+__device__ __forceinline__ void load_lds16(const void *src, void *lds_wave_base) {
+    load_lds16_at(src, lds_addr(lds_wave_base));
 }
 
 // s_waitcnt with vmcnt ≤ N, lgkmcnt 0 (every LDS access of this wavefront

@@ -269,6 +269,8 @@ __global__ __launch_bounds__(256, 2) void gemm_grouped_kernel(GemmParams p) {
 // B rows (n-contiguous) are 512 bytes and need no swizzle.  A wave load
 // fills 1 KiB: 16 A rows or 2 B rows.  The MFMA schedule, the k split across
 // lane halves and the epilogue are those of gemm_block.
+constexpr int kDmaLead = 2;  // k slots of MFMAs issued before each step's loads
+
 template <int STAGES, bool DUAL, bool GROUPED>
 __global__ __launch_bounds__(256, 2) void gemm_dma_kernel(GemmParams p) {
     constexpr int BM = 128, BN = 128, BK = 16, KH = BK / 2;
@@ -324,13 +326,14 @@ __global__ __launch_bounds__(256, 2) void gemm_dma_kernel(GemmParams p) {
         const int c = col0 + tc - (second ? BN / 2 : 0);
         b_src[q] = (second ? B2 : B) + (int64_t)kr * p.ldb + (c + 4 <= N ? c : col0);
     }
+    const uint32_t lds0 = lds_addr(smem) + 2 * wave * 1024;  // this wavefront's first A load, stage 0
     auto issue = [&](int kt) {
-        unsigned char *st = smem + (kt % STAGES) * STAGE;
+        const uint32_t st = lds0 + (kt % STAGES) * STAGE;
         const int k0 = kt * BK;
 #pragma unroll
-        for (int q = 0; q < 2; ++q) load_lds16(a_src[q] + k0, st + (2 * wave + q) * 1024);
+        for (int q = 0; q < 2; ++q) load_lds16_at(a_src[q] + k0, st + q * 1024);
 #pragma unroll
-        for (int q = 0; q < 2; ++q) load_lds16(b_src[q] + (int64_t)k0 * p.ldb, st + A_BYTES + (2 * wave + q) * 1024);
+        for (int q = 0; q < 2; ++q) load_lds16_at(b_src[q] + (int64_t)k0 * p.ldb, st + A_BYTES + q * 1024);
     };
 
     f32x16 acc[FM][FN];
@@ -366,15 +369,20 @@ __global__ __launch_bounds__(256, 2) void gemm_dma_kernel(GemmParams p) {
             for (int s2 = 0; s2 < KH; ++s2) f.b[ni][s2] = bt[(lg * KH + s2) * BN + col];
         }
     };
-    auto mma = [&](const Frags &f) {
+    // MFMAs of k slots [lo, hi) of f (compile-time bounds).
+    auto mma_part = [&](const Frags &f, auto lo, auto hi) {
 #pragma unroll
-        for (int s2 = 0; s2 < KH; ++s2)
+        for (int s2 = decltype(lo)::value; s2 < decltype(hi)::value; ++s2)
 #pragma unroll
             for (int mi = 0; mi < FM; ++mi)
 #pragma unroll
                 for (int ni = 0; ni < FN; ++ni)
                     acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x2f32(f.a[mi][s2], f.b[ni][s2], acc[mi][ni], 0, 0, 0);
     };
+    using K0 = std::integral_constant<int, 0>;
+    using KS = std::integral_constant<int, kDmaLead>;
+    using KE = std::integral_constant<int, KH>;
+    auto mma = [&](const Frags &f) { mma_part(f, K0{}, KE{}); };
 
     // Software pipeline: the fragments of chunk kt + 1 are read from LDS
     // while the MFMAs of chunk kt (already in registers) run.  Chunk kt + S
@@ -398,11 +406,17 @@ __global__ __launch_bounds__(256, 2) void gemm_dma_kernel(GemmParams p) {
     };
     // Step kt for kt + 1 < nfull.  No LDS read is left pending on any path
     // into mma(cur), so the compiler's own wait there is for cur alone.
+    // The first kDmaLead k slots of MFMAs go ahead of the load issue, so the
+    // matrix pipe starts right after the barrier while the address work and
+    // the loads issue behind it (the scheduler keeps this order).
     auto step = [&](int kt, Frags &cur, Frags &nxt) {
         wait_chunk(kt + 1, STAGES - 2);  // issued so far: chunks up to kt + S − 1
+        mma_part(cur, K0{}, KS{});
+        __builtin_amdgcn_sched_barrier(0);
         if (kt + STAGES < nfull) issue(kt + STAGES);
         load_frags(smem + ((kt + 1) % STAGES) * STAGE, nxt);
-        mma(cur);
+        __builtin_amdgcn_sched_barrier(0);
+        mma_part(cur, KS{}, KE{});
     };
     if (nfull > 0) {
         wait_chunk(0, STAGES - 1);  // issued so far: chunks 0 … S − 1
