@@ -585,15 +585,16 @@ __device__ __forceinline__ void tile_dma(unsigned char *smem, const GemmBf16Para
         if (n >= p.N) n = col0;
         b_src[q] = base + (int64_t)n * p.ldb + dk;
     }
+    const uint32_t lds0 = lds_addr(smem);
     auto issue = [&](int kt) {
-        unsigned char *st = smem + (kt % C::STAGES) * C::STAGE_BYTES;
+        const uint32_t st = lds0 + (kt % C::STAGES) * C::STAGE_BYTES;
         const int k0 = k_lo + kt * BK;
 #pragma unroll
         for (int q = 0; q < C::A_LD; ++q)
-            load_lds16(a_src[q] + k0, st + (wave * C::A_LD + q) * 1024);  // RPL rows × ROWB = 1 KiB
+            load_lds16_at(a_src[q] + k0, st + (wave * C::A_LD + q) * 1024);  // RPL rows × ROWB = 1 KiB
 #pragma unroll
         for (int q = 0; q < C::B_LD; ++q)
-            load_lds16(b_src[q] + k0, st + BM * ROWB + (wave * C::B_LD + q) * 1024);
+            load_lds16_at(b_src[q] + k0, st + BM * ROWB + (wave * C::B_LD + q) * 1024);
     };
 
     f32x16 acc[FM][FN];
@@ -608,9 +609,10 @@ __device__ __forceinline__ void tile_dma(unsigned char *smem, const GemmBf16Para
     const int a_off = (wm * (BM / C::WAVES_M) + lr) * ROWB;
     const int sw = C::sw(lr);  // fragment rows start on multiples of 32
     auto b_off = [&](int ni) { return (BM + staged_col<C, DUAL>(wn, ni, lr)) * ROWB; };
-    auto compute = [&](const unsigned char *st) {
+    // k steps [lo, hi) of the chunk in st (compile-time bounds).
+    auto compute_part = [&](const unsigned char *st, auto lo, auto hi) {
 #pragma unroll
-        for (int s = 0; s < BK / 16; ++s) {
+        for (int s = decltype(lo)::value; s < decltype(hi)::value; ++s) {
             const int pos = ((2 * s + lg) ^ sw) << 4;
             bf16x8 af[FM], bfr[FN];
 #pragma unroll
@@ -626,6 +628,10 @@ __device__ __forceinline__ void tile_dma(unsigned char *smem, const GemmBf16Para
                     acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mi], bfr[ni], acc[mi][ni], 0, 0, 0);
         }
     };
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+    using SE = std::integral_constant<int, BK / 16>;
+    auto compute = [&](const unsigned char *st) { compute_part(st, S0{}, SE{}); };
 
     const int nfull = (k_hi - k_lo) / BK;
 #pragma unroll
@@ -637,8 +643,14 @@ __device__ __forceinline__ void tile_dma(unsigned char *smem, const GemmBf16Para
         if (C::STAGES > 3 && ahead >= 2) dma_sync<C::LPC * (C::STAGES > 3 ? 2 : 0)>();
         else if (C::STAGES > 2 && ahead >= 1) dma_sync<C::LPC>();
         else dma_sync<0>();
+        // The first k step's MFMAs go ahead of the load issue (which fills
+        // the slot chunk kt − 1 used), so the matrix pipe starts at once.
+        const unsigned char *st = smem + (kt % C::STAGES) * C::STAGE_BYTES;
+        compute_part(st, S0{}, S1{});
+        __builtin_amdgcn_sched_barrier(0);
         if (kt + C::STAGES - 1 < nfull) issue(kt + C::STAGES - 1);
-        compute(smem + (kt % C::STAGES) * C::STAGE_BYTES);
+        __builtin_amdgcn_sched_barrier(0);
+        compute_part(st, S1{}, SE{});
     }
     const int kt0 = k_lo + nfull * BK;
     if (kt0 < k_hi) {
