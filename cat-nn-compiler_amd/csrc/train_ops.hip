@@ -477,34 +477,97 @@ __global__ __launch_bounds__(256) void sgd_multi_kernel(const SgdParam *__restri
     const int r0 = (t / P.tiles_c) * 64, c0 = (t % P.tiles_c) * 64;
     const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
     const bool grad = use_grad && P.g;
-    for (int i = ty; i < 64; i += 4) {
-        const int r = r0 + i, c = c0 + tx;
-        bf16_t h = 0, l = 0;
-        if (r < P.rows && c < P.cols) {
-            const int64_t e = (int64_t)r * P.cols + c;
-            float v = P.p[e];
-            if (grad) {
-                v = v - lr * P.g[e];
-                P.p[e] = v;
-            }
-            h = f2bf(v);
-            l = f2bf(v - __uint_as_float((uint32_t)h << 16));
-            if (P.b) P.b[e] = h;
+    auto al = [](const void *q, int a) { return (reinterpret_cast<uintptr_t>(q) & (a - 1)) == 0; };
+    // One element: update, split into hi/lo bf16, row-major copy.
+    auto one = [&](int64_t e, bf16_t &h, bf16_t &l) {
+        float v = P.p[e];
+        if (grad) {
+            v = v - lr * P.g[e];
+            P.p[e] = v;
         }
-        th[i][tx] = h;
-        tl[i][tx] = l;
+        h = f2bf(v);
+        l = f2bf(v - __uint_as_float((uint32_t)h << 16));
+        if (P.b) P.b[e] = h;
+    };
+    // Four consecutive columns a thread (16-byte master and gradient, 8-byte
+    // bf16 rows) when the rows allow it; the same arithmetic either way.
+    const bool vec = P.cols % 4 == 0 && al(P.p, 16) && (!grad || al(P.g, 16)) && (!P.b || al(P.b, 8));
+    if (vec) {
+        const int cq = 4 * (threadIdx.x & 15), rq = threadIdx.x >> 4;
+        for (int i = rq; i < 64; i += 16) {
+            const int r = r0 + i, c = c0 + cq;
+            float v[4] = {0.f, 0.f, 0.f, 0.f};
+            bf16_t h[4] = {0, 0, 0, 0}, l[4] = {0, 0, 0, 0};
+            if (r < P.rows && c < P.cols) {  // c + 3 < cols: cols and c0 are multiples of 4
+                const int64_t e = (int64_t)r * P.cols + c;
+                const float4 pv = *reinterpret_cast<const float4 *>(P.p + e);
+                v[0] = pv.x; v[1] = pv.y; v[2] = pv.z; v[3] = pv.w;
+                if (grad) {
+                    const float4 gv = *reinterpret_cast<const float4 *>(P.g + e);
+                    v[0] = v[0] - lr * gv.x;
+                    v[1] = v[1] - lr * gv.y;
+                    v[2] = v[2] - lr * gv.z;
+                    v[3] = v[3] - lr * gv.w;
+                    *reinterpret_cast<float4 *>(P.p + e) = make_float4(v[0], v[1], v[2], v[3]);
+                }
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    h[j] = f2bf(v[j]);
+                    l[j] = f2bf(v[j] - __uint_as_float((uint32_t)h[j] << 16));
+                }
+                if (P.b)
+                    *reinterpret_cast<uint2 *>(P.b + e) =
+                        make_uint2(h[0] | (uint32_t)h[1] << 16, h[2] | (uint32_t)h[3] << 16);
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                th[i][cq + j] = h[j];
+                tl[i][cq + j] = l[j];
+            }
+        }
+    } else {
+        for (int i = ty; i < 64; i += 4) {
+            const int r = r0 + i, c = c0 + tx;
+            bf16_t h = 0, l = 0;
+            if (r < P.rows && c < P.cols) one((int64_t)r * P.cols + c, h, l);
+            th[i][tx] = h;
+            tl[i][tx] = l;
+        }
     }
     if (!P.bt && !P.bt3) return;  // uniform per block
     __syncthreads();
-    for (int i = ty; i < 64; i += 4) {
-        const int c = c0 + i, r = r0 + tx;
-        if (c < P.cols && r < P.rows) {
-            if (P.bt) P.bt[(int64_t)c * P.rows + r] = th[tx][i];
-            if (P.bt3) {
-                bf16_t *o = P.bt3 + (int64_t)c * 3 * P.rows;
-                o[r] = th[tx][i];
-                o[P.rows + r] = tl[tx][i];
-                o[2 * P.rows + r] = th[tx][i];
+    // Transposed copies: four consecutive rows a thread (8-byte stores) when
+    // every destination row starts on 8 bytes.
+    const bool tvec = P.rows % 4 == 0 && (!P.bt || al(P.bt, 8)) && (!P.bt3 || al(P.bt3, 8));
+    if (tvec) {
+        const int rq = 4 * (threadIdx.x & 15), cq = threadIdx.x >> 4;
+        for (int i = cq; i < 64; i += 16) {
+            const int c = c0 + i, r = r0 + rq;
+            if (c < P.cols && r < P.rows) {  // r + 3 < rows
+                const uint2 hv = make_uint2(th[rq][i] | (uint32_t)th[rq + 1][i] << 16,
+                                            th[rq + 2][i] | (uint32_t)th[rq + 3][i] << 16);
+                if (P.bt) *reinterpret_cast<uint2 *>(P.bt + (int64_t)c * P.rows + r) = hv;
+                if (P.bt3) {
+                    const uint2 lv = make_uint2(tl[rq][i] | (uint32_t)tl[rq + 1][i] << 16,
+                                                tl[rq + 2][i] | (uint32_t)tl[rq + 3][i] << 16);
+                    bf16_t *o = P.bt3 + (int64_t)c * 3 * P.rows;
+                    *reinterpret_cast<uint2 *>(o + r) = hv;
+                    *reinterpret_cast<uint2 *>(o + P.rows + r) = lv;
+                    *reinterpret_cast<uint2 *>(o + 2 * P.rows + r) = hv;
+                }
+            }
+        }
+    } else {
+        for (int i = ty; i < 64; i += 4) {
+            const int c = c0 + i, r = r0 + tx;
+            if (c < P.cols && r < P.rows) {
+                if (P.bt) P.bt[(int64_t)c * P.rows + r] = th[tx][i];
+                if (P.bt3) {
+                    bf16_t *o = P.bt3 + (int64_t)c * 3 * P.rows;
+                    o[r] = th[tx][i];
+                    o[P.rows + r] = tl[tx][i];
+                    o[2 * P.rows + r] = th[tx][i];
+                }
             }
         }
     }
