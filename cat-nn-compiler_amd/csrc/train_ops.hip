@@ -257,6 +257,9 @@ __global__ __launch_bounds__(256) void col_partials_kernel(const float *__restri
     const int64_t r0 = (int64_t)blockIdx.y * kColRows;
     const int64_t r1 = r0 + kColRows < rows ? r0 + kColRows : rows;
     float sa = 0.f, sb = 0.f;
+    // Unrolled so that several rows' loads are in flight; the sums still
+    // run row by row in order.
+#pragma unroll 8
     for (int64_t r = r0; r < r1; ++r) {
         const float d = dy[r * cols + c];
         if (LN) {
@@ -280,8 +283,10 @@ __global__ __launch_bounds__(256) void reduce_partials_kernel(const float *__res
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int c = blockIdx.x * 64 + lane;
     float s = 0.f;
-    if (c < cols)
+    if (c < cols) {
+#pragma unroll 8
         for (int g = w; g < ng; g += 4) s += part[(int64_t)g * cols + c];
+    }
     red[w][lane] = s;
     __syncthreads();
     if (w == 0 && c < cols) {
