@@ -50,6 +50,19 @@ __global__ void cast_kernel(const float *__restrict__ x, bf16_t *__restrict__ y,
         y[i] = f2bf(x[i]);
 }
 
+__device__ __forceinline__ uint2 pack4(bf16_t a, bf16_t b, bf16_t c, bf16_t d) {
+    return make_uint2(a | (uint32_t)b << 16, c | (uint32_t)d << 16);
+}
+
+// The same four elements a thread: 16-byte loads, 8-byte stores.
+__global__ void cast4_kernel(const float4 *__restrict__ x, uint2 *__restrict__ y, int64_t n4) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride) {
+        const float4 v = x[i];
+        y[i] = pack4(f2bf(v.x), f2bf(v.y), f2bf(v.z), f2bf(v.w));
+    }
+}
+
 // dst[c][r] = src[map(r)][c] for r < rows (map(r) = rows_map[r] / div when
 // given; a negative map entry is a padding row and yields 0), c < cols.
 // 64×64 tiles through LDS so both the read and the write are coalesced.
@@ -176,6 +189,28 @@ __global__ void split3_rows_kernel(const float *__restrict__ x, int64_t ldx, int
     }
 }
 
+// split3_rows_kernel four columns a thread: block row y (and every
+// gridDim.y-th after it), column quad x·256 + t; 16-byte loads, 8-byte
+// stores, no 64-bit division.
+__global__ __launch_bounds__(256) void split3_rows4_kernel(const float4 *__restrict__ x, int64_t ldx4, int64_t rows,
+                                                           int K4, uint2 *__restrict__ out, int64_t ldo4) {
+    const int c = blockIdx.x * 256 + threadIdx.x;
+    if (c >= K4) return;
+    for (int64_t r = blockIdx.y; r < rows; r += gridDim.y) {
+        const float4 v = x[r * ldx4 + c];
+        bf16_t h[4], l[4];
+        split_bf16(v.x, h[0], l[0]);
+        split_bf16(v.y, h[1], l[1]);
+        split_bf16(v.z, h[2], l[2]);
+        split_bf16(v.w, h[3], l[3]);
+        const uint2 hv = pack4(h[0], h[1], h[2], h[3]);
+        uint2 *o = out + r * ldo4;
+        o[c] = hv;
+        o[K4 + c] = hv;
+        o[2 * K4 + c] = pack4(l[0], l[1], l[2], l[3]);
+    }
+}
+
 // w [K, N] row-major → out [N, 3K] with out[n] = [hi(w[:,n]) | lo(w[:,n]) | hi(w[:,n])].
 __global__ __launch_bounds__(256) void transpose_split3_kernel(const float *__restrict__ w, int64_t ldw,
                                                                int K, int N, bf16_t *__restrict__ out,
@@ -204,6 +239,7 @@ __global__ __launch_bounds__(256) void transpose_split3_kernel(const float *__re
 
 // LayerNorm forward for training: y (fp32 and/or bf16), mean and rstd per
 // row.  One wavefront per row; any width.
+template <bool VEC>
 __global__ __launch_bounds__(256) void ln_fwd_kernel(const float *__restrict__ x,
                                                      const float *__restrict__ g,
                                                      const float *__restrict__ b,
@@ -215,6 +251,43 @@ __global__ __launch_bounds__(256) void ln_fwd_kernel(const float *__restrict__ x
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= rows) return;
     const float *xr = x + row * cols;
+    if (VEC) {  // four consecutive columns a lane per step: 16-byte x, γ, β, y and 8-byte yb accesses
+        const int c4n = cols / 4;
+        const float4 *x4 = reinterpret_cast<const float4 *>(xr);
+        float s = 0.f;
+        for (int c = lane; c < c4n; c += 64) {
+            const float4 v = x4[c];
+            s += v.x;
+            s += v.y;
+            s += v.z;
+            s += v.w;
+        }
+        const float n = (float)cols;
+        const float mu = wave_sum(s) / n;
+        float q = 0.f;
+        for (int c = lane; c < c4n; c += 64) {
+            const float4 v = x4[c];
+            const float d0 = v.x - mu, d1 = v.y - mu, d2 = v.z - mu, d3 = v.w - mu;
+            q += d0 * d0;
+            q += d1 * d1;
+            q += d2 * d2;
+            q += d3 * d3;
+        }
+        const float inv = 1.0f / sqrtf(wave_sum(q) / n + eps);
+        const float4 *g4 = reinterpret_cast<const float4 *>(g), *b4 = reinterpret_cast<const float4 *>(b);
+        for (int c = lane; c < c4n; c += 64) {
+            const float4 v = x4[c], gv = g4[c], bv = b4[c];
+            const float4 o = make_float4((v.x - mu) * inv * gv.x + bv.x, (v.y - mu) * inv * gv.y + bv.y,
+                                         (v.z - mu) * inv * gv.z + bv.z, (v.w - mu) * inv * gv.w + bv.w);
+            if (y) reinterpret_cast<float4 *>(y + row * cols)[c] = o;
+            if (yb) reinterpret_cast<uint2 *>(yb + row * cols)[c] = pack4(f2bf(o.x), f2bf(o.y), f2bf(o.z), f2bf(o.w));
+        }
+        if (lane == 0) {
+            mean[row] = mu;
+            rstd[row] = inv;
+        }
+        return;
+    }
     float s = 0.f;
     for (int c = lane; c < cols; c += 64) s += xr[c];
     const float n = (float)cols;
@@ -688,7 +761,11 @@ void fill_bf16_zero(hipStream_t s, bf16_t *y, int64_t n) {
 
 void cast_f32_bf16(hipStream_t s, const float *x, bf16_t *y, int64_t n) {
     if (n <= 0) return;
-    cast_kernel<<<blocks_for(n, 256 * 4), 256, 0, s>>>(x, y, n);
+    if (n % 4 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 && (reinterpret_cast<uintptr_t>(y) & 7) == 0)
+        cast4_kernel<<<blocks_for(n / 4, 256 * 2), 256, 0, s>>>(reinterpret_cast<const float4 *>(x),
+                                                                 reinterpret_cast<uint2 *>(y), n / 4);
+    else
+        cast_kernel<<<blocks_for(n, 256 * 4), 256, 0, s>>>(x, y, n);
     CATNN_HIP(hipGetLastError());
 }
 
@@ -725,7 +802,14 @@ void transpose_f32_bf16(hipStream_t s, const float *src, int64_t lds, const int3
 void split3_rows(hipStream_t s, const float *x, int64_t ldx, int64_t rows, int K, bf16_t *out,
                  int64_t ldo) {
     if (rows <= 0 || K <= 0) return;
-    split3_rows_kernel<<<blocks_for(rows * K, 256 * 4), 256, 0, s>>>(x, ldx, rows, K, out, ldo);
+    if (K % 4 == 0 && ldx % 4 == 0 && ldo % 4 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
+        (reinterpret_cast<uintptr_t>(out) & 7) == 0) {
+        const dim3 grid((unsigned)((K / 4 + 255) / 256), (unsigned)std::min<int64_t>(rows, 65535));
+        split3_rows4_kernel<<<grid, 256, 0, s>>>(reinterpret_cast<const float4 *>(x), ldx / 4, rows, K / 4,
+                                                 reinterpret_cast<uint2 *>(out), ldo / 4);
+    } else {
+        split3_rows_kernel<<<blocks_for(rows * K, 256 * 4), 256, 0, s>>>(x, ldx, rows, K, out, ldo);
+    }
     CATNN_HIP(hipGetLastError());
 }
 
@@ -740,8 +824,11 @@ void transpose_split3(hipStream_t s, const float *w, int64_t ldw, int K, int N, 
 void ln_forward_train(hipStream_t s, const float *x, const float *g, const float *b, float *y,
                       bf16_t *yb, float *mean, float *rstd, int64_t rows, int cols, float eps) {
     if (rows <= 0) return;
-    ln_fwd_kernel<<<(unsigned)((rows + 3) / 4), 256, 0, s>>>(x, g, b, y, yb, mean, rstd, rows, cols,
-                                                             eps);
+    auto al = [](const void *q, uintptr_t a) { return (reinterpret_cast<uintptr_t>(q) & (a - 1)) == 0; };
+    const bool vec = cols % 4 == 0 && al(x, 16) && al(g, 16) && al(b, 16) && (!y || al(y, 16)) && (!yb || al(yb, 8));
+    const unsigned blocks = (unsigned)((rows + 3) / 4);
+    if (vec) ln_fwd_kernel<true><<<blocks, 256, 0, s>>>(x, g, b, y, yb, mean, rstd, rows, cols, eps);
+    else ln_fwd_kernel<false><<<blocks, 256, 0, s>>>(x, g, b, y, yb, mean, rstd, rows, cols, eps);
     CATNN_HIP(hipGetLastError());
 }
 
