@@ -97,19 +97,21 @@ __global__ __launch_bounds__(256) void transpose_kernel(const TS *__restrict__ s
     }
 }
 
-// The same transpose for full 64×64 tiles with 16-byte global accesses:
-// each thread reads 16-byte runs of source rows (8 bf16 or 4 f32) into an
-// LDS tile (row stride 72 bf16), then gathers 8 consecutive source rows of
-// one column — a wavefront reads 128 contiguous LDS bytes per step — and
-// writes them as one 16-byte run of a destination row.  Launched only where
-// the host has checked alignment; edge tiles take transpose_kernel.
+// The same transpose for full 64×64 tiles with 16-byte global accesses.
+// Each thread reads 16-byte runs of source rows (8 bf16 or 4 f32) into an
+// LDS tile of 64-element rows whose 16-byte chunk c of row i sits at
+// position c ^ (i/8 mod 8).  Then 8 lanes gather the 8 chunks of one
+// destination row: lane k takes source rows 8k … 8k+7 of column oc (chunk
+// (oc/8) ^ k of each, so a wavefront's reads fall on distinct banks) and
+// the 8 lanes store one contiguous 128-byte run.  Launched only where the
+// host has checked alignment; edge tiles take the element path.
 template <typename TS>
 __global__ __launch_bounds__(256) void transpose_vec_kernel(const TS *__restrict__ src, int64_t lds,
                                                             const int32_t *__restrict__ rows_map, int div,
                                                             int rows, int cols, bf16_t *__restrict__ dst,
                                                             int64_t ldd) {
     constexpr int VPL = 16 / sizeof(TS);  // source values per 16-byte load
-    __shared__ __align__(16) bf16_t t[64][72];
+    __shared__ __align__(16) bf16_t t[64 * 66];  // swizzled 64 × 64, or 64 rows of 66 on edge tiles
     const int r0 = blockIdx.y * 64, c0 = blockIdx.x * 64;
     const int tid = threadIdx.x;
     if (r0 + 64 > rows || c0 + 64 > cols) {
@@ -125,15 +127,17 @@ __global__ __launch_bounds__(256) void transpose_vec_kernel(const TS *__restrict
                     else v = src[(int64_t)sr * lds + c];
                 }
             }
-            t[i][tx] = v;
+            t[i * 66 + tx] = v;
         }
         __syncthreads();
         for (int i = ty; i < 64; i += 4) {
             const int c = c0 + i, r = r0 + tx;
-            if (c < cols && r < rows) dst[(int64_t)c * ldd + r] = t[tx][i];
+            if (c < cols && r < rows) dst[(int64_t)c * ldd + r] = t[tx * 66 + i];
         }
         return;
     }
+    // element (i, c) of the tile
+    auto at = [](int i, int c) { return i * 64 + ((((c >> 3) ^ (i >> 3)) & 7) << 3) + (c & 7); };
     constexpr int PER_ROW = 64 / VPL;
 #pragma unroll
     for (int j = 0; j < 64 * PER_ROW / 256; ++j) {
@@ -145,20 +149,19 @@ __global__ __launch_bounds__(256) void transpose_vec_kernel(const TS *__restrict
         if constexpr (sizeof(TS) == 4) {
             const uint32_t lo = (uint32_t)f2bf(__uint_as_float(w.x)) | ((uint32_t)f2bf(__uint_as_float(w.y)) << 16);
             const uint32_t hi = (uint32_t)f2bf(__uint_as_float(w.z)) | ((uint32_t)f2bf(__uint_as_float(w.w)) << 16);
-            *reinterpret_cast<uint2 *>(&t[i][cc]) = make_uint2(lo, hi);
+            *reinterpret_cast<uint2 *>(&t[at(i, cc)]) = make_uint2(lo, hi);
         } else {
-            *reinterpret_cast<uint4 *>(&t[i][cc]) = w;
+            *reinterpret_cast<uint4 *>(&t[at(i, cc)]) = w;
         }
     }
     __syncthreads();
-    const int oc = tid & 63;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-        const int k = (tid >> 6) + 4 * j;  // source rows 8k … 8k+7
+        const int item = tid + 256 * j, k = item & 7, oc = item >> 3;  // source rows 8k … 8k+7, column oc
         uint32_t u[4];
 #pragma unroll
         for (int m = 0; m < 4; ++m)
-            u[m] = (uint32_t)t[8 * k + 2 * m][oc] | ((uint32_t)t[8 * k + 2 * m + 1][oc] << 16);
+            u[m] = (uint32_t)t[at(8 * k + 2 * m, oc)] | ((uint32_t)t[at(8 * k + 2 * m + 1, oc)] << 16);
         *reinterpret_cast<uint4 *>(dst + (int64_t)(c0 + oc) * ldd + r0 + 8 * k) = make_uint4(u[0], u[1], u[2], u[3]);
     }
 }
