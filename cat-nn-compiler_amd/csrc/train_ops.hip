@@ -669,6 +669,35 @@ __global__ void router_dlogits_kernel(const int32_t *__restrict__ idx, const flo
     }
 }
 
+// The same partials with thread h owning the E entries of row h: x[t][h] is
+// read once (coalesced across h) and dl[t][·] is the same for every lane.
+// EM ≥ E accumulators in registers; each entry still sums its tokens in
+// order, so the result equals router_dgate_parts_kernel's.
+template <int EM>
+__global__ __launch_bounds__(256) void router_dgate_rows_kernel(const float *__restrict__ x,
+                                                                const float *__restrict__ dl, int T, int H,
+                                                                int E, float *__restrict__ part) {
+    const int h = blockIdx.x * 256 + threadIdx.x;
+    if (h >= H) return;
+    const int t0 = blockIdx.y * kColRows;
+    const int t1 = t0 + kColRows < T ? t0 + kColRows : T;
+    float acc[EM];
+#pragma unroll
+    for (int e = 0; e < EM; ++e) acc[e] = 0.f;
+#pragma unroll 8
+    for (int t = t0; t < t1; ++t) {  // unrolled: several tokens' loads in flight
+        const float xv = x[(int64_t)t * H + h];
+        const float *d = dl + (int64_t)t * E;
+#pragma unroll
+        for (int e = 0; e < EM; ++e)
+            if (e < E) acc[e] += xv * d[e];
+    }
+    float *o = part + (int64_t)blockIdx.y * H * E + (int64_t)h * E;
+#pragma unroll
+    for (int e = 0; e < EM; ++e)
+        if (e < E) o[e] = acc[e];
+}
+
 // Partials of dgate[h][e] = Σ_t x[t][h]·dl[t][e] over groups of kColRows
 // tokens; thread j owns entry j = h·E + e of the [H, E] gradient.
 __global__ __launch_bounds__(256) void router_dgate_parts_kernel(const float *__restrict__ x,
@@ -938,8 +967,11 @@ void router_backward(hipStream_t s, const int32_t *idx, const float *w, const fl
     router_dlogits_kernel<<<(T + 255) / 256, 256, 0, s>>>(idx, w, dw, T, E, K, dl);
     const int ng = (T + kColRows - 1) / kColRows;
     CATNN_REQUIRE(ng < 65536, CATNN_ERR_SHAPE_MISMATCH, "router backward: too many tokens");
-    router_dgate_parts_kernel<<<dim3((unsigned)((H * E + 255) / 256), (unsigned)ng), 256, 0, s>>>(x, dl, T, H, E,
-                                                                                               scratch);
+    const dim3 rgrid((unsigned)((H + 255) / 256), (unsigned)ng);
+    if (E <= 8) router_dgate_rows_kernel<8><<<rgrid, 256, 0, s>>>(x, dl, T, H, E, scratch);
+    else if (E <= 16) router_dgate_rows_kernel<16><<<rgrid, 256, 0, s>>>(x, dl, T, H, E, scratch);
+    else router_dgate_parts_kernel<<<dim3((unsigned)((H * E + 255) / 256), (unsigned)ng), 256, 0, s>>>(x, dl, T, H, E,
+                                                                                                  scratch);
     CATNN_HIP(hipGetLastError());
     reduce_partials(s, scratch, ng, H * E, dgate, false);
 }
