@@ -48,6 +48,15 @@ __global__ __launch_bounds__(256) void attn_dot_kernel(const float *__restrict__
     if (lane == 0) D[gw] = s;
 }
 
+// Column swizzle of the transposed K tile of the dQ kernel (row d = head
+// dimension): row d holds key j at j ^ tsw(d).  The transposing stores put
+// 16 rows 4 apart into one wavefront store; with the swizzle those rows
+// spread over the banks (2-way instead of 8-way conflicts), while a float4
+// read of four consecutive keys stays contiguous (tsw is a multiple of 4).
+// (The dK/dV kernel keeps its transposed tiles unswizzled: the swizzled
+// reads lose their constant offsets and the kernel then spills.)
+__device__ __forceinline__ int tsw(int d) { return ((d >> 3) & 7) << 2; }
+
 template <int DH>
 __global__ __launch_bounds__(256, 2) void attn_bwd_dkdv_kernel(
     const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v, int64_t ld,
@@ -299,8 +308,9 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(
             const int kr = idx / (DH / 4), c4 = idx % (DH / 4);
             *reinterpret_cast<float4 *>(&Ks[buf][kr][4 * c4]) = pk[it];
             *reinterpret_cast<float4 *>(&Vs[buf][kr][4 * c4]) = pv[it];
-            Kt[4 * c4 + 0][kr] = pk[it].x; Kt[4 * c4 + 1][kr] = pk[it].y;
-            Kt[4 * c4 + 2][kr] = pk[it].z; Kt[4 * c4 + 3][kr] = pk[it].w;
+            const int kc = kr ^ tsw(4 * c4);  // rows 4c4 … 4c4+3 share one swizzle
+            Kt[4 * c4 + 0][kc] = pk[it].x; Kt[4 * c4 + 1][kc] = pk[it].y;
+            Kt[4 * c4 + 2][kc] = pk[it].z; Kt[4 * c4 + 3][kc] = pk[it].w;
         }
         __syncthreads();
         if (t + 1 < ntiles) gload(t + 1);
@@ -344,7 +354,8 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(
             for (int s4 = 0; s4 < 4; ++s4)
 #pragma unroll
                 for (int db = 0; db < DH / 32; ++db) {
-                    const float4 kv = *reinterpret_cast<const float4 *>(&Kt[db * 32 + lr][kb * 32 + 8 * s4 + 4 * g]);
+                    const float4 kv = *reinterpret_cast<const float4 *>(
+                        &Kt[db * 32 + lr][(kb * 32 + 8 * s4 + 4 * g) ^ tsw(db * 32 + lr)]);
                     dqa[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.x, pa[4 * s4 + 0], dqa[db], 0, 0, 0);
                     dqa[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.y, pa[4 * s4 + 1], dqa[db], 0, 0, 0);
                     dqa[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.z, pa[4 * s4 + 2], dqa[db], 0, 0, 0);
