@@ -307,6 +307,16 @@ def gemm_bf16_nt(dev: Device, a, lda: int, b, ldb: int, c, ldc: int, m: int, n: 
                                      int(accumulate), tile_cfg))
 
 
+def sgd(dev: Device, p, g, n: int, lr: float):
+    """Sgd::put in place on n values (apply_update, pipeline.rs:455-472)."""
+    check(lib.catnn_hip_sgd_f32(dev.handle, _ptr(p), _ptr(g), n, lr))
+
+
+def adam(dev: Device, p, g, m, v, n: int, t: int, lr: float):
+    """Adam::put in place on n values; `t` is AdamState.t before the step."""
+    check(lib.catnn_hip_adam_f32(dev.handle, _ptr(p), _ptr(g), _ptr(m), _ptr(v), n, t, lr))
+
+
 def act(dev: Device, x, y, n: int, kind: int):
     check(lib.catnn_hip_act_f32(dev.handle, _ptr(x), _ptr(y), n, kind))
 

@@ -1,8 +1,10 @@
 """One training step of an IrGraph on the GPU (catnn_hip_train_*).
 
 `Trainer.step()` replaces one step of pipeline::reference_train
-(crates/catnn-compile/src/pipeline.rs:476-547) with MSE and SGD: forward,
-loss, reverse-topo adjoints, SGD on fp32 master weights.  GEMM operands are
+(crates/catnn-compile/src/pipeline.rs:476-547) with MSE and the optimizer
+TrainOptions.opt names (OptimizerKind, crates/catnn-core/src/lens/optim.rs:
+142-145): forward, loss, reverse-topo adjoints, then Sgd::put or Adam::put
+on the fp32 master weights.  GEMM operands are
 bf16 (bf16 MFMA, fp32 accumulation); masters, residual stream, norms,
 router and gradient accumulation are fp32.
 """
@@ -20,17 +22,23 @@ from .ir import IrGraph, Tensor, ctensor
 
 _FP = ctypes.POINTER(ctypes.c_float)
 
+OPTIMIZERS = {"sgd": 0, "adam": 1}  # CATNN_OPT_SGD, CATNN_OPT_ADAM
+
 
 class Trainer:
-    def __init__(self, device: Device, graph: IrGraph, lr: float = 0.05):
+    def __init__(self, device: Device, graph: IrGraph, lr: float = 0.05, opt: str = "sgd"):
+        """`opt` is OptimizerKind::parse's spelling: "sgd" or "adam"."""
+        if opt not in OPTIMIZERS:
+            raise ValueError(f"unknown optimizer {opt!r} (expected sgd or adam)")
         self.device = device
         self.graph = graph
         self.lr = lr
+        self.opt = opt
         h, owned = graph_handle(graph)
         self.handle = ctypes.c_void_p()
         try:
-            check(lib.catnn_hip_train_install(device.handle, h, ctypes.c_float(lr),
-                                              ctypes.byref(self.handle)))
+            check(lib.catnn_hip_train_install_opt(device.handle, h, OPTIMIZERS[opt], ctypes.c_float(lr),
+                                                  ctypes.byref(self.handle)))
         finally:
             if owned:
                 lib.catnn_graph_free(h)
@@ -63,6 +71,19 @@ class Trainer:
 
     def grad(self, node_id: int, port: str, shape) -> np.ndarray:
         return self._read(lib.catnn_hip_train_read_grad, node_id, port, shape)
+
+    def moment(self, node_id: int, port: str, which: str, shape) -> np.ndarray:
+        """Adam's first ("m") or second ("v") moment of a parameter."""
+        out = np.empty(shape, np.float32)
+        check(lib.catnn_hip_train_read_moment(self.handle, node_id, port.encode(), {"m": 0, "v": 1}[which],
+                                              out.ctypes.data_as(_FP), out.size))
+        return out
+
+    def adam_step(self) -> int:
+        """AdamState.t: Adam steps taken since install or reset."""
+        t = ctypes.c_uint64()
+        check(lib.catnn_hip_train_adam_step(self.handle, ctypes.byref(t)))
+        return int(t.value)
 
     def value(self, node_id: int, shape) -> np.ndarray:
         out = np.empty(shape, np.float32)

@@ -11,8 +11,10 @@
 //             a value's cotangent is written by the first of its consumers
 //             to run and accumulated by the others (add_tensors,
 //             adjoint.rs:22-24);
-//   update    p −= lr·g on the fp32 master weights (Sgd::put,
-//             lens/optim.rs:32-42), then the bf16 copies are refreshed.
+//   update    the optimizer on the fp32 master weights — Sgd::put
+//             (lens/optim.rs:32-42) or Adam::put (:95-118) with its moments
+//             resident beside them, as apply_update (pipeline.rs:455-472)
+//             chooses — then the bf16 copies are refreshed.
 //
 // Precision: every GEMM runs on v_mfma_f32_32x32x16_bf16 with fp32
 // accumulation.  The forward GEMMs of Linear and attention take split-bf16
@@ -61,6 +63,7 @@ struct TParam {
     std::vector<float> init;  // host values uploaded at install
     bool want_b = false, want_bt = false, want_bt3 = false;
     float *master = nullptr, *grad = nullptr;
+    float *m = nullptr, *v = nullptr;  // Adam moments "adam:{node}:{port}:m|v"
     bf16_t *b = nullptr, *bt = nullptr;
     bf16_t *bt3 = nullptr;  // [cols, 3·rows] split-bf16 transposed copy (hi | lo | hi)
 };
@@ -93,6 +96,8 @@ struct catnn_hip_trainer {
     catnn_hip_device *dev = nullptr;
     catnn_graph graph;
     float lr = 0.05f;
+    int opt = CATNN_OPT_SGD;
+    uint64_t adam_t = 0;  // AdamState.t shared by every trained parameter
     std::vector<catnn::TNode> nodes;
     std::map<uint32_t, size_t> index;                 // node id → nodes[]
     std::vector<std::unique_ptr<catnn::TParam>> params;
@@ -310,6 +315,10 @@ static void plan_trainer(Tr &t) {
         const uint64_t e = (uint64_t)(rows * cols);
         request(t, p->name, e * 4, 0, upd, reinterpret_cast<void **>(&p->master));
         request(t, "grad:" + p->name, e * 4, bwd(tn.tick), upd, reinterpret_cast<void **>(&p->grad));
+        if (t.opt == CATNN_OPT_ADAM)  // pipeline.rs:366-376
+            for (const char *mom : {"m", "v"})
+                request(t, "adam:" + tn.node->name + ":" + port + ":" + mom, e * 4, 0, upd,
+                        reinterpret_cast<void **>(mom[0] == 'm' ? &p->m : &p->v));
         if (p->want_b) request(t, "bf16:" + p->name, e * 2, 0, upd, reinterpret_cast<void **>(&p->b));
         if (p->want_bt) request(t, "bf16t:" + p->name, e * 2, 0, upd, reinterpret_cast<void **>(&p->bt));
         if (p->want_bt3) request(t, "bf16t3:" + p->name, e * 6, 0, upd, reinterpret_cast<void **>(&p->bt3));
@@ -450,6 +459,8 @@ static void build_sgd_table(Tr &t, std::vector<k::SgdParam> &tab) {
             k::SgdParam e{};
             e.p = p->master;
             e.g = trained ? p->grad : nullptr;
+            e.m = p->m;
+            e.v = p->v;
             e.b = p->want_b ? p->b : nullptr;
             e.bt = p->want_bt ? p->bt : nullptr;
             e.bt3 = p->want_bt3 ? p->bt3 : nullptr;
@@ -467,12 +478,17 @@ static void build_sgd_table(Tr &t, std::vector<k::SgdParam> &tab) {
     t.sgd_n = (int)tab.size();
 }
 
-// Masters from the host copies, then the bf16 operand copies from the masters.
+// Masters from the host copies, then the bf16 operand copies from the
+// masters; Adam's moments start at zero (AdamState::zeros_like, optim.rs:71-75).
 static void upload_params(Tr &t) {
     hipStream_t s = t.dev->stream;
-    for (auto &p : t.params)
+    for (auto &p : t.params) {
         CATNN_HIP(hipMemcpyAsync(p->master, p->init.data(), p->init.size() * 4, hipMemcpyHostToDevice, s));
-    k::sgd_multi(s, t.sgd_table, t.sgd_n, t.sgd_tiles, 0.f, false);
+        if (p->m) k::fill_f32(s, p->m, 0.f, p->rows * p->cols);
+        if (p->v) k::fill_f32(s, p->v, 0.f, p->rows * p->cols);
+    }
+    t.adam_t = 0;
+    k::sgd_multi(s, t.sgd_table, t.sgd_n, t.sgd_tiles, k::sgd_rule(0.f), false);
 }
 
 static void reserve_and_upload(Tr &t) {
@@ -774,9 +790,10 @@ static void train_step(Tr &t) {
     // as reference_train skips ids without an entry in `grads`.
     for (auto it = t.nodes.rbegin(); it != t.nodes.rend(); ++it)
         if (!t.input_ids.count(it->id) && t.has_grad.count(it->id) && !it->skip_bwd) backward_node(t, *it);
-    // Sgd::put on the parameters of every node that received a cotangent,
-    // and the refresh of their bf16 copies, in one launch.
-    k::sgd_multi(s, t.sgd_table, t.sgd_n, t.sgd_tiles, t.lr, true);
+    // apply_update on the parameters of every node that received a
+    // cotangent, and the refresh of their bf16 copies, in one launch.
+    const k::UpdateRule rule = t.opt == CATNN_OPT_ADAM ? k::adam_rule(t.lr, ++t.adam_t) : k::sgd_rule(t.lr);
+    k::sgd_multi(s, t.sgd_table, t.sgd_n, t.sgd_tiles, rule, true);
 }
 
 static TParam *find_param(Tr &t, uint32_t node_id, const std::string &port, int64_t *col0,
@@ -837,15 +854,23 @@ int catnn_hip_gemm_bf16_nt(catnn_hip_device *dev, const uint16_t *a, int64_t lda
 
 int catnn_hip_train_install(catnn_hip_device *dev, const catnn_graph *g, float lr,
                             catnn_hip_trainer **out) {
+    return catnn_hip_train_install_opt(dev, g, CATNN_OPT_SGD, lr, out);
+}
+
+int catnn_hip_train_install_opt(catnn_hip_device *dev, const catnn_graph *g, int32_t optimizer, float lr,
+                                catnn_hip_trainer **out) {
     return guard([&] {
         require_device(dev);
         CATNN_REQUIRE(g && out, CATNN_ERR_INVALID_ARGUMENT, "null argument");
+        CATNN_REQUIRE(optimizer == CATNN_OPT_SGD || optimizer == CATNN_OPT_ADAM, CATNN_ERR_INVALID_ARGUMENT,
+                      "unknown optimizer " + std::to_string(optimizer) + " (expected sgd or adam)");
         *out = nullptr;
         auto *t = new catnn_hip_trainer();
         try {
             t->dev = dev;
             t->graph = *g;
             t->lr = lr;
+            t->opt = optimizer;
             plan_trainer(*t);
             reserve_and_upload(*t);
         } catch (...) {
@@ -926,6 +951,46 @@ int catnn_hip_train_read_grad(catnn_hip_trainer *t, uint32_t node_id, const char
         int64_t col0, ncols;
         TParam *p = find_param(*t, node_id, port, &col0, &ncols);
         read_cols(*t, p->grad, p->rows, p->cols, col0, ncols, host, n);
+    });
+}
+
+int catnn_hip_train_read_moment(catnn_hip_trainer *t, uint32_t node_id, const char *port, int32_t which,
+                                float *host, int64_t n) {
+    return guard([&] {
+        CATNN_REQUIRE(t && port && host, CATNN_ERR_INVALID_ARGUMENT, "null argument");
+        CATNN_REQUIRE(which == 0 || which == 1, CATNN_ERR_INVALID_ARGUMENT, "moment: 0 (m) or 1 (v)");
+        CATNN_REQUIRE(t->opt == CATNN_OPT_ADAM, CATNN_ERR_UNSUPPORTED, "trainer was installed with SGD: no moments");
+        require_device(t->dev);
+        int64_t col0, ncols;
+        TParam *p = find_param(*t, node_id, port, &col0, &ncols);
+        read_cols(*t, which == 0 ? p->m : p->v, p->rows, p->cols, col0, ncols, host, n);
+    });
+}
+
+int catnn_hip_train_adam_step(catnn_hip_trainer *t, uint64_t *step) {
+    return guard([&] {
+        CATNN_REQUIRE(t && step, CATNN_ERR_INVALID_ARGUMENT, "null argument");
+        *step = t->adam_t;
+    });
+}
+
+int catnn_hip_sgd_f32(catnn_hip_device *dev, float *p, const float *g, int64_t n, float lr) {
+    return guard([&] {
+        require_device(dev);
+        CATNN_REQUIRE(n >= 0, CATNN_ERR_SHAPE_MISMATCH, "sgd: negative length");
+        CATNN_REQUIRE((p && g) || n == 0, CATNN_ERR_INVALID_ARGUMENT, "sgd: null buffer");
+        k::apply_update(dev->stream, k::sgd_rule(lr), p, g, nullptr, nullptr, n);
+    });
+}
+
+int catnn_hip_adam_f32(catnn_hip_device *dev, float *p, const float *g, float *m, float *v, int64_t n,
+                       uint64_t t, float lr) {
+    return guard([&] {
+        require_device(dev);
+        CATNN_REQUIRE(n >= 0, CATNN_ERR_SHAPE_MISMATCH, "adam: negative length");
+        CATNN_REQUIRE((p && g && m && v) || n == 0, CATNN_ERR_INVALID_ARGUMENT, "adam: null buffer");
+        const uint64_t next = t == UINT64_MAX ? t : t + 1;  // saturating_add (optim.rs:98)
+        k::apply_update(dev->stream, k::adam_rule(lr, next), p, g, m, v, n);
     });
 }
 

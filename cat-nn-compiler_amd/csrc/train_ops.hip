@@ -539,11 +539,76 @@ __global__ void sgd_kernel(float *__restrict__ p, const float *__restrict__ g, i
     }
 }
 
-// Multi-tensor SGD: block b updates one 64×64 tile of the parameter whose
-// tile range holds b (binary search of the table), writes the master and
-// the row-major bf16 copy, and through LDS the transposed copies.
+// One parameter value under the update rule: Sgd::put (optim.rs:38-40),
+// p − lr·g, or Adam::put (optim.rs:104-115) with moments m, v updated in
+// place.  Every product, quotient, square root and sum is rounded on its
+// own, in the reference's order ((1−β₂)·g·g is ((1−β₂)·g)·g, and lr·m̂/(…)
+// is (lr·m̂)/(…)); division and sqrtf are correctly rounded in this build,
+// so the new value is bit-identical to the reference's for the same inputs.
+__device__ __forceinline__ float update_value(const UpdateRule &u, float p, float g, float &m, float &v) {
+#pragma clang fp contract(off)
+    if (!u.adam) return p - u.lr * g;
+    const float mi = u.beta1 * m + (1.f - u.beta1) * g;
+    const float vi = u.beta2 * v + (1.f - u.beta2) * g * g;
+    m = mi;
+    v = vi;
+    const float mhat = mi / fmaxf(u.b1t, 1e-30f);
+    const float vhat = vi / fmaxf(u.b2t, 1e-30f);
+    return p - u.lr * mhat / (sqrtf(vhat) + u.eps);
+}
+
+// The update rule over n values: four a thread with 16-byte accesses when
+// every buffer allows it, the same arithmetic either way.
+__global__ void apply_update_kernel(UpdateRule u, float *__restrict__ p, const float *__restrict__ g,
+                                    float *__restrict__ m, float *__restrict__ v, int64_t n, int vec) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    const int64_t i0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (vec) {
+        const int64_t nq = n / 4;
+        for (int64_t q = i0; q < nq; q += stride) {
+            float4 pv = reinterpret_cast<const float4 *>(p)[q];
+            const float4 gv = reinterpret_cast<const float4 *>(g)[q];
+            float4 mv = make_float4(0.f, 0.f, 0.f, 0.f), vv = mv;
+            if (u.adam) {
+                mv = reinterpret_cast<const float4 *>(m)[q];
+                vv = reinterpret_cast<const float4 *>(v)[q];
+            }
+            pv.x = update_value(u, pv.x, gv.x, mv.x, vv.x);
+            pv.y = update_value(u, pv.y, gv.y, mv.y, vv.y);
+            pv.z = update_value(u, pv.z, gv.z, mv.z, vv.z);
+            pv.w = update_value(u, pv.w, gv.w, mv.w, vv.w);
+            reinterpret_cast<float4 *>(p)[q] = pv;
+            if (u.adam) {
+                reinterpret_cast<float4 *>(m)[q] = mv;
+                reinterpret_cast<float4 *>(v)[q] = vv;
+            }
+        }
+        for (int64_t i = nq * 4 + i0; i < n; i += stride) {
+            float mi = u.adam ? m[i] : 0.f, vi = u.adam ? v[i] : 0.f;
+            p[i] = update_value(u, p[i], g[i], mi, vi);
+            if (u.adam) {
+                m[i] = mi;
+                v[i] = vi;
+            }
+        }
+    } else {
+        for (int64_t i = i0; i < n; i += stride) {
+            float mi = u.adam ? m[i] : 0.f, vi = u.adam ? v[i] : 0.f;
+            p[i] = update_value(u, p[i], g[i], mi, vi);
+            if (u.adam) {
+                m[i] = mi;
+                v[i] = vi;
+            }
+        }
+    }
+}
+
+// Multi-tensor update: block b updates one 64×64 tile of the parameter whose
+// tile range holds b (binary search of the table), writes the master (and
+// Adam's moments) and the row-major bf16 copy, and through LDS the
+// transposed copies.
 __global__ __launch_bounds__(256) void sgd_multi_kernel(const SgdParam *__restrict__ tab, int n,
-                                                        float lr, int use_grad) {
+                                                        UpdateRule u, int use_grad) {
 #pragma clang fp contract(off)
     __shared__ bf16_t th[64][66], tl[64][66];
     const int b = blockIdx.x;
@@ -563,8 +628,13 @@ __global__ __launch_bounds__(256) void sgd_multi_kernel(const SgdParam *__restri
     auto one = [&](int64_t e, bf16_t &h, bf16_t &l) {
         float v = P.p[e];
         if (grad) {
-            v = v - lr * P.g[e];
+            float mo = u.adam ? P.m[e] : 0.f, ve = u.adam ? P.v[e] : 0.f;
+            v = update_value(u, v, P.g[e], mo, ve);
             P.p[e] = v;
+            if (u.adam) {
+                P.m[e] = mo;
+                P.v[e] = ve;
+            }
         }
         h = f2bf(v);
         l = f2bf(v - __uint_as_float((uint32_t)h << 16));
@@ -572,7 +642,8 @@ __global__ __launch_bounds__(256) void sgd_multi_kernel(const SgdParam *__restri
     };
     // Four consecutive columns a thread (16-byte master and gradient, 8-byte
     // bf16 rows) when the rows allow it; the same arithmetic either way.
-    const bool vec = P.cols % 4 == 0 && al(P.p, 16) && (!grad || al(P.g, 16)) && (!P.b || al(P.b, 8));
+    const bool vec = P.cols % 4 == 0 && al(P.p, 16) && (!grad || al(P.g, 16)) && (!P.b || al(P.b, 8)) &&
+                     (!grad || !u.adam || (al(P.m, 16) && al(P.v, 16)));
     if (vec) {
         const int cq = 4 * (threadIdx.x & 15), rq = threadIdx.x >> 4;
         for (int i = rq; i < 64; i += 16) {
@@ -585,11 +656,20 @@ __global__ __launch_bounds__(256) void sgd_multi_kernel(const SgdParam *__restri
                 v[0] = pv.x; v[1] = pv.y; v[2] = pv.z; v[3] = pv.w;
                 if (grad) {
                     const float4 gv = *reinterpret_cast<const float4 *>(P.g + e);
-                    v[0] = v[0] - lr * gv.x;
-                    v[1] = v[1] - lr * gv.y;
-                    v[2] = v[2] - lr * gv.z;
-                    v[3] = v[3] - lr * gv.w;
+                    float4 mo = make_float4(0.f, 0.f, 0.f, 0.f), ve = mo;
+                    if (u.adam) {
+                        mo = *reinterpret_cast<const float4 *>(P.m + e);
+                        ve = *reinterpret_cast<const float4 *>(P.v + e);
+                    }
+                    v[0] = update_value(u, v[0], gv.x, mo.x, ve.x);
+                    v[1] = update_value(u, v[1], gv.y, mo.y, ve.y);
+                    v[2] = update_value(u, v[2], gv.z, mo.z, ve.z);
+                    v[3] = update_value(u, v[3], gv.w, mo.w, ve.w);
                     *reinterpret_cast<float4 *>(P.p + e) = make_float4(v[0], v[1], v[2], v[3]);
+                    if (u.adam) {
+                        *reinterpret_cast<float4 *>(P.m + e) = mo;
+                        *reinterpret_cast<float4 *>(P.v + e) = ve;
+                    }
                 }
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
@@ -953,9 +1033,54 @@ void sgd(hipStream_t s, float *p, const float *g, int64_t ldg, int64_t rows, int
     CATNN_HIP(hipGetLastError());
 }
 
-void sgd_multi(hipStream_t s, const SgdParam *table, int n, int tiles, float lr, bool use_grad) {
+void sgd_multi(hipStream_t s, const SgdParam *table, int n, int tiles, const UpdateRule &u, bool use_grad) {
     if (n <= 0 || tiles <= 0) return;
-    sgd_multi_kernel<<<(unsigned)tiles, 256, 0, s>>>(table, n, lr, use_grad ? 1 : 0);
+    sgd_multi_kernel<<<(unsigned)tiles, 256, 0, s>>>(table, n, u, use_grad ? 1 : 0);
+    CATNN_HIP(hipGetLastError());
+}
+
+float powi_f32(float b, int32_t t) {
+#pragma clang fp contract(off)
+    const bool recip = t < 0;
+    uint32_t e = recip ? 0u - (uint32_t)t : (uint32_t)t;
+    float r = 1.f;
+    for (;;) {
+        if (e & 1u) r *= b;
+        e >>= 1;
+        if (e == 0) break;
+        b *= b;
+    }
+    return recip ? 1.f / r : r;
+}
+
+UpdateRule sgd_rule(float lr) {
+    UpdateRule u{};
+    u.adam = 0;
+    u.lr = lr;
+    return u;
+}
+
+// Adam::default (optim.rs:86-90) with the given lr; the step counter is
+// AdamState.t saturating_add(1) and powi takes it `as i32` (optim.rs:98-103).
+UpdateRule adam_rule(float lr, uint64_t t) {
+#pragma clang fp contract(off)
+    UpdateRule u{};
+    u.adam = 1;
+    u.lr = lr;
+    u.beta1 = 0.9f;
+    u.beta2 = 0.999f;
+    u.eps = 1e-8f;
+    u.b1t = 1.f - powi_f32(u.beta1, (int32_t)t);
+    u.b2t = 1.f - powi_f32(u.beta2, (int32_t)t);
+    return u;
+}
+
+void apply_update(hipStream_t s, const UpdateRule &u, float *p, const float *g, float *m, float *v,
+                  int64_t n) {
+    if (n <= 0) return;
+    auto al = [](const void *q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
+    const int vec = al(p) && al(g) && (!u.adam || (al(m) && al(v))) ? 1 : 0;
+    apply_update_kernel<<<blocks_for(vec ? (n + 3) / 4 : n, 256), 256, 0, s>>>(u, p, g, m, v, n, vec);
     CATNN_HIP(hipGetLastError());
 }
 

@@ -51,6 +51,25 @@ void mse(hipStream_t s, const float *pred, const float *tgt, float *d, int64_t n
 void sgd(hipStream_t s, float *p, const float *g, int64_t ldg, int64_t rows, int cols, float lr,
          bf16_t *pb);
 
+// The update morphism of one launch (OptimizerKind, lens/optim.rs:142-145).
+// Adam's bias corrections b1t = 1 − β₁ᵗ and b2t = 1 − β₂ᵗ are computed on
+// the host for the step about to run (adam_bias_corrections).
+struct UpdateRule {
+    int adam;  // 0: Sgd::put (optim.rs:32-42), 1: Adam::put (optim.rs:95-118)
+    float lr, beta1, beta2, eps, b1t, b2t;
+};
+UpdateRule sgd_rule(float lr);
+// Adam with the reference's defaults (β₁ 0.9, β₂ 0.999, eps 1e-8) at step t
+// (t ≥ 1 is the step being taken: AdamState.t + 1).
+UpdateRule adam_rule(float lr, uint64_t t);
+// f32 β^t by binary exponentiation, the lowering of Rust's f32::powi for a
+// run-time exponent (compiler-builtins' __powisf2).
+float powi_f32(float b, int32_t t);
+// p ← update(p, g) elementwise over n values; m, v are Adam's moments
+// (ignored for SGD), updated in place.
+void apply_update(hipStream_t s, const UpdateRule &u, float *p, const float *g, float *m, float *v,
+                  int64_t n);
+
 // One parameter of the multi-tensor update: fp32 master p [rows, cols] and
 // its gradient g (same layout, or null: refresh only), and the bf16 copies
 // to rewrite from the new value: b [rows, cols], bt [cols, rows] and the
@@ -58,15 +77,16 @@ void sgd(hipStream_t s, float *p, const float *g, int64_t ldg, int64_t rows, int
 struct SgdParam {
     float *p;
     const float *g;
+    float *m, *v;  // Adam moments, same layout as p (null under SGD)
     bf16_t *b, *bt, *bt3;
     int rows, cols;
     int tile0;    // first 64×64 tile of this parameter in the launch
     int tiles_c;  // tiles across cols
 };
-// p −= lr·g on every parameter of `table` (device memory, n entries, tile0
-// ascending, `tiles` in total) in one launch, then the bf16 copies; with
-// use_grad false only the copies are refreshed.
-void sgd_multi(hipStream_t s, const SgdParam *table, int n, int tiles, float lr, bool use_grad);
+// The update rule on every parameter of `table` (device memory, n entries,
+// tile0 ascending, `tiles` in total) in one launch, then the bf16 copies;
+// with use_grad false only the copies are refreshed.
+void sgd_multi(hipStream_t s, const SgdParam *table, int n, int tiles, const UpdateRule &u, bool use_grad);
 
 uint64_t router_backward_scratch_bytes(int T, int H, int E);
 void router_backward(hipStream_t s, const int32_t *idx, const float *w, const float *dw,

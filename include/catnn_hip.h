@@ -381,6 +381,18 @@ typedef struct catnn_hip_trainer catnn_hip_trainer;
 
 int catnn_hip_train_install(catnn_hip_device *dev, const catnn_graph *g, float lr,
                             catnn_hip_trainer **out);
+/* The update morphism (OptimizerKind, crates/catnn-core/src/lens/optim.rs:
+ * 142-145; chosen by TrainOptions.opt and applied by apply_update,
+ * crates/catnn-compile/src/pipeline.rs:455-472). */
+enum { CATNN_OPT_SGD = 0, CATNN_OPT_ADAM = 1 };
+/* As catnn_hip_train_install with the optimizer named: CATNN_OPT_SGD is
+ * Sgd::put (optim.rs:32-42), CATNN_OPT_ADAM is Adam::put (optim.rs:95-118)
+ * with Adam::default's β₁ 0.9, β₂ 0.999, eps 1e-8 and the given lr, its
+ * moments m, v resident in the arena as "adam:{node}:{port}:m|v"
+ * (pipeline.rs:366-376), zero at install and after train_reset.  Unknown
+ * optimizer: CATNN_ERR_INVALID_ARGUMENT. */
+int catnn_hip_train_install_opt(catnn_hip_device *dev, const catnn_graph *g, int32_t optimizer,
+                                float lr, catnn_hip_trainer **out);
 int catnn_hip_train_free(catnn_hip_trainer *t);
 /* Upload the batch: `input` is bound to every graph input, `target` is the
  * MSE target of the last output. */
@@ -399,6 +411,12 @@ int catnn_hip_train_read_param(catnn_hip_trainer *t, uint32_t node_id, const cha
                                float *host, int64_t n);
 int catnn_hip_train_read_grad(catnn_hip_trainer *t, uint32_t node_id, const char *port,
                               float *host, int64_t n);
+/* Adam moment `which` (0: m, 1: v) of param `port` of node `node_id`;
+ * CATNN_ERR_UNSUPPORTED on an SGD trainer. */
+int catnn_hip_train_read_moment(catnn_hip_trainer *t, uint32_t node_id, const char *port,
+                                int32_t which, float *host, int64_t n);
+/* AdamState.t: the number of Adam steps taken since install or reset. */
+int catnn_hip_train_adam_step(catnn_hip_trainer *t, uint64_t *step);
 /* Forward value of node `node_id` from the last step. */
 int catnn_hip_train_read_value(catnn_hip_trainer *t, uint32_t node_id, float *host, int64_t n);
 /* Expert indices [T, top_k] chosen by MoE node `node_id` in the last step. */
@@ -447,6 +465,18 @@ int catnn_hip_linear_f32(catnn_hip_device *dev, const float *x, const float *w,
 int catnn_hip_gemm_bf16_nt(catnn_hip_device *dev, const uint16_t *a, int64_t lda, const uint16_t *b,
                            int64_t ldb, float *c, int64_t ldc, int64_t m, int64_t n, int64_t k,
                            int32_t accumulate, int32_t tile_cfg);
+
+/* apply_update (crates/catnn-compile/src/pipeline.rs:455-472, the seam
+ * coord.rs:481 calls) on n values in device memory, in place.
+ * catnn_hip_sgd_f32 replaces Sgd::put (lens/optim.rs:32-42): p −= lr·g.
+ * catnn_hip_adam_f32 replaces Adam::put (optim.rs:95-118) with Adam's
+ * default β₁, β₂, eps: `t` is AdamState.t before the step (0 for a fresh
+ * state), the step taken is t + 1, and m, v are updated in place.  Both are
+ * bit-identical to the reference for the same inputs (every operation
+ * rounded separately, in the reference's order). */
+int catnn_hip_sgd_f32(catnn_hip_device *dev, float *p, const float *g, int64_t n, float lr);
+int catnn_hip_adam_f32(catnn_hip_device *dev, float *p, const float *g, float *m, float *v,
+                       int64_t n, uint64_t t, float lr);
 
 /* Replaces cpu::relu / cpu::gelu (cpu.rs:14-29) as standalone passes. */
 int catnn_hip_act_f32(catnn_hip_device *dev, const float *x, float *y,

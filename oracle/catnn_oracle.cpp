@@ -905,4 +905,47 @@ void orc_sgd(float *p, const float *g, int64_t n, float lr) {
     for (int64_t i = 0; i < n; ++i) p[i] -= lr * g[i];
 }
 
+// f32::powi for a run-time exponent.  The reference calls b1.powi(t as i32)
+// (optim.rs:102-103); rustc lowers that to llvm.powi.f32, which for a
+// non-constant exponent becomes a call of __powisf2 from Rust's
+// compiler-builtins crate (the version pinned by the toolchain, absent
+// here): binary exponentiation — multiply the result by the base when the
+// low bit is set, halve the exponent, square the base — in f32, reciprocal
+// for a negative exponent.
+float orc_powi(float b, int32_t t) {
+    const bool recip = t < 0;
+    uint32_t e = recip ? 0u - (uint32_t)t : (uint32_t)t;
+    float r = 1.f;
+    for (;;) {
+        if (e & 1u) r *= b;
+        e >>= 1;
+        if (e == 0) break;
+        b *= b;
+    }
+    return recip ? 1.f / r : r;
+}
+
+// Adam::put, crates/catnn-core/src/lens/optim.rs:95-118, on n values in
+// place: `t` is AdamState.t before the step (t' = t saturating_add 1),
+// b1t = 1 − β₁^t', b2t = 1 − β₂^t', then per element m' = β₁m + (1−β₁)g,
+// v' = β₂v + (1−β₂)·g·g (left to right), p' = p − lr·m̂/(√v̂ + eps) with
+// m̂ = m'/max(b1t, 1e-30), v̂ = v'/max(b2t, 1e-30).  Built with
+// -ffp-contract=off, so every operation rounds as Rust's does.
+void orc_adam(float *p, const float *g, float *m, float *v, int64_t n, uint64_t t, float lr, float beta1,
+              float beta2, float eps) {
+    const uint64_t t1 = t == UINT64_MAX ? t : t + 1;
+    const float b1t = 1.0f - orc_powi(beta1, (int32_t)t1);
+    const float b2t = 1.0f - orc_powi(beta2, (int32_t)t1);
+    for (int64_t i = 0; i < n; ++i) {
+        const float gi = g[i];
+        const float mi = beta1 * m[i] + (1.0f - beta1) * gi;
+        const float vi = beta2 * v[i] + (1.0f - beta2) * gi * gi;
+        m[i] = mi;
+        v[i] = vi;
+        const float mhat = mi / std::max(b1t, 1e-30f);
+        const float vhat = vi / std::max(b2t, 1e-30f);
+        p[i] = p[i] - lr * mhat / (std::sqrt(vhat) + eps);
+    }
+}
+
 }  // extern "C"

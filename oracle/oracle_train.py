@@ -5,8 +5,10 @@ training step restating pipeline::reference_train
 (crates/catnn-compile/src/pipeline.rs:476-547): forward in topo order with
 eval_cpu, MSE (adjoint.rs:106-119), reverse topo with adjoint_of
 (adjoint.rs:762-951) summing cotangents from several successors with
-add_tensors (adjoint.rs:22-24), then Sgd::put on every parameter
-(optim.rs:32-42).  Pinned by tests/test_oracle_adjoint.py.
+add_tensors (adjoint.rs:22-24), then apply_update (pipeline.rs:455-472) on
+every parameter: Sgd::put (optim.rs:32-42) or Adam::put (optim.rs:95-118)
+with its per-parameter state.  Pinned by tests/test_oracle_adjoint.py and
+tests/test_oracle_adam.py.
 """
 from __future__ import annotations
 
@@ -31,6 +33,9 @@ _SIG = {
     "orc_moe_backward": ([_F, _F, _F, _F, _F, _I64, _I64, _I64, _I64, _I64, _F, _F, _F, _F, _F, _F],
                          None),
     "orc_sgd": ([_F, _F, _I64, ctypes.c_float], None),
+    "orc_powi": ([ctypes.c_float, ctypes.c_int32], ctypes.c_float),
+    "orc_adam": ([_F, _F, _F, _F, _I64, ctypes.c_uint64, ctypes.c_float, ctypes.c_float, ctypes.c_float,
+                  ctypes.c_float], None),
 }
 for _name, (_args, _res) in _SIG.items():
     _fn = getattr(_lib, _name)
@@ -134,6 +139,43 @@ def sgd(p, g, lr):
     return p
 
 
+ADAM_DEFAULTS = (np.float32(0.9), np.float32(0.999), np.float32(1e-8))  # Adam::default, optim.rs:86-90
+
+
+def powi(b, t):
+    """f32::powi with a run-time exponent (binary exponentiation in f32)."""
+    return np.float32(_lib.orc_powi(np.float32(b), int(t)))
+
+
+class AdamState:
+    """AdamState (optim.rs:63-76): moments m, v and the step counter t."""
+
+    def __init__(self, shape):
+        self.m = np.zeros(shape, np.float32)
+        self.v = np.zeros(shape, np.float32)
+        self.t = 0
+
+
+def adam(p, g, state, lr, betas=ADAM_DEFAULTS):
+    """Adam::put: returns the new parameter; `state` advances in place."""
+    b1, b2, eps = betas
+    p = _c(p).copy()
+    g = _c(g)
+    assert p.size == g.size == state.m.size
+    _lib.orc_adam(_f(p), _f(g), _f(state.m), _f(state.v), p.size, state.t, np.float32(lr), b1, b2, eps)
+    state.t = min(state.t + 1, 2**64 - 1)
+    return p
+
+
+def apply_update(p, g, opt, lr, state):
+    """pipeline.rs:455-472: Sgd::put, or Adam::put creating the state on first use."""
+    if opt == "sgd":
+        return sgd(p, g, lr), state
+    if state is None:
+        state = AdamState(np.shape(p))
+    return adam(p, g, state, lr), state
+
+
 def adjoint_of(node, inputs, output, dy):
     """adjoint.rs:762-951 for the executable op set: (cotangents per input,
     {port: parameter cotangent})."""
@@ -178,9 +220,11 @@ def adjoint_of(node, inputs, output, dy):
     raise NotImplementedError(kind)
 
 
-def train_step(graph, x, target, lr):
-    """One step of pipeline::reference_train with MSE and SGD: returns
-    (loss, {node_id: {port: grad}}, {node_id: {port: updated param}})."""
+def train_step(graph, x, target, lr, opt="sgd", adam_states=None):
+    """One step of pipeline::reference_train with MSE and `opt` ("sgd" or
+    "adam"): returns (loss, {node_id: {port: grad}}, {node_id: {port:
+    updated param}}).  For Adam, `adam_states` ({(node_id, port):
+    AdamState}, updated in place) carries the moments between steps."""
     order = oracle.topo(graph)
     acts = {}
     for nid in order:
@@ -204,7 +248,14 @@ def train_step(graph, x, target, lr):
             grads[p] = oracle.add(grads[p], dx) if p in grads else dx
         dparams[nid] = dp
     new = {}
+    if adam_states is None:
+        adam_states = {}
     for nid, dp in dparams.items():
         node = graph.nodes[nid]
-        new[nid] = {port: sgd(node.params[port].numpy(), g, lr) for port, g in dp.items()}
+        new[nid] = {}
+        for port, g in dp.items():
+            st = adam_states.get((nid, port))
+            new[nid][port], st = apply_update(node.params[port].numpy(), g, opt, lr, st)
+            if st is not None:
+                adam_states[(nid, port)] = st
     return loss, dparams, new
