@@ -158,6 +158,8 @@ SIGNATURES = {
     "catnn_hip_train_read_moment": [_VP, ctypes.c_uint32, ctypes.c_char_p, _I32, ctypes.POINTER(_F), _I64],
     "catnn_hip_train_adam_step": [_VP, _PU64],
     "catnn_hip_sgd_f32": [_VP, _VP, _VP, _I64, _F],
+    "catnn_hip_run_adjoint": [_VP, _VP, ctypes.POINTER(CTensor), _I32, ctypes.POINTER(CTensor),
+                              ctypes.POINTER(CTensor), ctypes.POINTER(CTensor), ctypes.POINTER(CTensor), _I32],
     "catnn_hip_adam_f32": [_VP, _VP, _VP, _VP, _VP, _I64, ctypes.c_uint64, _F],
     "catnn_hip_train_free": [_VP],
     "catnn_hip_train_set_batch": [_VP, ctypes.POINTER(CTensor), ctypes.POINTER(CTensor)],

@@ -17,7 +17,7 @@ from __future__ import annotations
 import ctypes
 import weakref
 from dataclasses import dataclass
-from typing import List, Optional, Sequence, Tuple
+from typing import Dict, List, Optional, Sequence, Tuple
 
 import numpy as np
 
@@ -186,6 +186,26 @@ class DeviceHandler:
         shape = tuple(out.dims[i] for i in range(out.rank))
         ty = TensorType(shape, "f32")
         return Tensor(ty, buf[: ty.numel()].copy())
+
+    def adjoint_of(self, node: IrNode, inputs: Sequence[Tensor], output: Optional[Tensor],
+                   dy: Tensor) -> Tuple[List[Tensor], Dict[str, Tensor]]:
+        """adjoint_of (crates/catnn-compile/src/kernel/adjoint.rs:762-951) on
+        the GPU: (cotangent per input, {port: parameter cotangent}) in the
+        node's param order.  `output` is recomputed on the device and may be
+        None.  GEMMs on bf16 MFMA with fp32 accumulation, as the training step."""
+        cnode, keep = node.to_c()
+        cins = (CTensor * max(len(inputs), 1))(*[ctensor(t) for t in inputs])
+        dxs = [np.empty(max(t.ty.numel(), 1), np.float32) for t in inputs]
+        cdx = (CTensor * max(len(inputs), 1))(*[ctensor(ty=t.ty, buf=b) for t, b in zip(inputs, dxs)])
+        ports = list(node.params)
+        dps = [np.empty(max(node.params[p].ty.numel(), 1), np.float32) for p in ports]
+        cdp = (CTensor * max(len(ports), 1))(*[ctensor(ty=node.params[p].ty, buf=b) for p, b in zip(ports, dps)])
+        cdy = ctensor(dy)
+        check(lib.catnn_hip_run_adjoint(self.device.handle, ctypes.byref(cnode), cins, len(inputs), None,
+                                        ctypes.byref(cdy), cdx, cdp, len(ports)))
+        dx = [Tensor(t.ty, b[: t.ty.numel()].copy()) for t, b in zip(inputs, dxs)]
+        dp = {p: Tensor(node.params[p].ty, b[: node.params[p].ty.numel()].copy()) for p, b in zip(ports, dps)}
+        return dx, dp
 
     def events(self):
         return self.device.events()

@@ -98,6 +98,7 @@ struct catnn_hip_trainer {
     float lr = 0.05f;
     int opt = CATNN_OPT_SGD;
     uint64_t adam_t = 0;  // AdamState.t shared by every trained parameter
+    bool input_grads = false;  // keep the graph inputs' cotangents (run_adjoint)
     std::vector<catnn::TNode> nodes;
     std::map<uint32_t, size_t> index;                 // node id → nodes[]
     std::vector<std::unique_ptr<catnn::TParam>> params;
@@ -292,7 +293,13 @@ static void plan_trainer(Tr &t) {
         const bool is_input = t.input_ids.count(tn.id) != 0;
         request(t, "act:" + std::to_string(tn.id), bytes, is_input ? 0 : tn.tick,
                 is_input ? upd : last_read[tn.id], reinterpret_cast<void **>(&t.val[tn.id]));
-        if (is_input) continue;
+        if (is_input) {
+            // An input's cotangent, when kept, stays readable after the pass.
+            if (t.input_grads && first_consumer_tick.count(tn.id))
+                request(t, "grad:" + std::to_string(tn.id), bytes, bwd(first_consumer_tick[tn.id]), upd,
+                        reinterpret_cast<void **>(&t.grad[tn.id]));
+            continue;
+        }
         uint64_t from = tn.id == t.out_id ? n : bwd(first_consumer_tick.count(tn.id) ? first_consumer_tick[tn.id] : tn.tick);
         if (grad_from.count(tn.id)) from = std::min(from, grad_from[tn.id]);
         request(t, "grad:" + std::to_string(tn.id), bytes, std::min<uint64_t>(from, bwd(tn.tick)),
@@ -633,7 +640,7 @@ static void backward_node(Tr &t, TNode &tn) {
     const Node &nd = *tn.node;
     const float *dy = t.grad.at(tn.id);
     auto dst = [&](size_t i) -> float * {
-        return t.input_ids.count(tn.ins[i]) ? nullptr : t.grad.at(tn.ins[i]);
+        return t.input_ids.count(tn.ins[i]) && !t.input_grads ? nullptr : t.grad.at(tn.ins[i]);
     };
     const float *x = tn.ins.empty() ? nullptr : t.val.at(tn.ins[0]);
     const auto &xd = tn.ins.empty() ? tn.dims : tn.in_dims[0];
@@ -794,6 +801,15 @@ static void train_step(Tr &t) {
     // cotangent, and the refresh of their bf16 copies, in one launch.
     const k::UpdateRule rule = t.opt == CATNN_OPT_ADAM ? k::adam_rule(t.lr, ++t.adam_t) : k::sgd_rule(t.lr);
     k::sgd_multi(s, t.sgd_table, t.sgd_n, t.sgd_tiles, rule, true);
+}
+
+// adjoint_of over the graph with the output's cotangent already in place
+// (no loss, no update): forward for the tapes, then the reverse pass.
+static void adjoint_pass(Tr &t) {
+    for (auto &tn : t.nodes)
+        if (!t.input_ids.count(tn.id)) forward_node(t, tn);
+    for (auto it = t.nodes.rbegin(); it != t.nodes.rend(); ++it)
+        if (!t.input_ids.count(it->id) && t.has_grad.count(it->id) && !it->skip_bwd) backward_node(t, *it);
 }
 
 static TParam *find_param(Tr &t, uint32_t node_id, const std::string &port, int64_t *col0,
@@ -991,6 +1007,106 @@ int catnn_hip_adam_f32(catnn_hip_device *dev, float *p, const float *g, float *m
         CATNN_REQUIRE((p && g && m && v) || n == 0, CATNN_ERR_INVALID_ARGUMENT, "adam: null buffer");
         const uint64_t next = t == UINT64_MAX ? t : t + 1;  // saturating_add (optim.rs:98)
         k::apply_update(dev->stream, k::adam_rule(lr, next), p, g, m, v, n);
+    });
+}
+
+int catnn_hip_run_adjoint(catnn_hip_device *dev, const catnn_node *node, const catnn_tensor *inputs,
+                          int32_t n_inputs, const catnn_tensor *output, const catnn_tensor *dy,
+                          catnn_tensor *dx, catnn_tensor *dparams, int32_t n_dparams) {
+    (void)output;  // recomputed from the inputs on the device
+    return guard([&] {
+        require_device(dev);
+        CATNN_REQUIRE(node && dy && (n_inputs == 0 || (inputs && dx)) && (n_dparams == 0 || dparams),
+                      CATNN_ERR_INVALID_ARGUMENT, "null argument");
+        // adjoint.rs:768-770
+        CATNN_REQUIRE(n_inputs > 0, CATNN_ERR_WIRING,
+                      std::string(node->name ? node->name : "?") + " adjoint has no inputs");
+        CATNN_REQUIRE(n_inputs <= 16, CATNN_ERR_INVALID_ARGUMENT, "run_adjoint: more than 16 inputs");
+        CATNN_REQUIRE(n_dparams == node->n_params, CATNN_ERR_SHAPE_MISMATCH,
+                      "run_adjoint: " + std::to_string(n_dparams) + " parameter cotangents for " +
+                          std::to_string(node->n_params) + " params");
+        // The one-node graph in0 … in{n-1} → node, its preds in edge order.
+        auto ok = [](int rc) {
+            if (rc != CATNN_OK) fail(rc, catnn_hip_last_error());
+        };
+        catnn_graph g;
+        g.name = "adjoint";
+        const uint32_t nid = (uint32_t)n_inputs;
+        std::vector<std::string> names;
+        for (int32_t i = 0; i < n_inputs; ++i) names.push_back("in" + std::to_string(i));
+        for (int32_t i = 0; i < n_inputs; ++i) {
+            catnn_node in{};
+            in.id = (uint32_t)i;
+            in.name = names[(size_t)i].c_str();
+            in.op.kind = CATNN_OP_IDENTITY;
+            in.output_ty = inputs[i];
+            in.output_ty.data = nullptr;
+            ok(catnn_graph_add_node(&g, &in));
+            ok(catnn_graph_add_input(&g, in.id));
+        }
+        catnn_node self = *node;
+        self.id = nid;
+        ok(catnn_graph_add_node(&g, &self));
+        for (int32_t i = 0; i < n_inputs; ++i) ok(catnn_graph_add_edge(&g, (uint32_t)i, nid, "out", "in"));
+        ok(catnn_graph_add_output(&g, nid));
+
+        std::unique_ptr<catnn_hip_trainer> t(new catnn_hip_trainer());
+        struct Free {
+            catnn_hip_trainer *t;
+            ~Free() {
+                if (t->base) (void)hipFree(t->base);
+            }
+        } free_arena{t.get()};
+        t->dev = dev;
+        t->graph = g;
+        t->lr = 0.f;
+        t->input_grads = true;
+        plan_trainer(*t);
+        reserve_and_upload(*t);
+        hipStream_t s = dev->stream;
+        for (int32_t i = 0; i < n_inputs; ++i) {
+            const int64_t ni = numel(dims_from_c(inputs[i]));
+            CATNN_REQUIRE(inputs[i].data || ni == 0, CATNN_ERR_INVALID_ARGUMENT, "input " + std::to_string(i) + ": no data");
+            if (ni) CATNN_HIP(hipMemcpyAsync(t->val.at((uint32_t)i), inputs[i].data, (size_t)ni * 4,
+                                             hipMemcpyHostToDevice, s));
+        }
+        const std::vector<int64_t> &od = t->dims.at(nid);
+        const int64_t nd = numel(dims_from_c(*dy));
+        CATNN_REQUIRE(nd == numel(od) && (dy->data || nd == 0), CATNN_ERR_SHAPE_MISMATCH,
+                      "dy has " + std::to_string(nd) + " values, " + g.node(nid).name + " produces " + dims_str(od));
+        if (nd) CATNN_HIP(hipMemcpyAsync(t->grad.at(nid), dy->data, (size_t)nd * 4, hipMemcpyHostToDevice, s));
+        adjoint_pass(*t);
+        for (int32_t i = 0; i < n_inputs; ++i) {
+            const std::vector<int64_t> &xd = t->dims.at((uint32_t)i);
+            const int64_t nx = numel(xd);
+            int64_t cap = 1;
+            for (int r = 0; r < dx[i].rank; ++r) cap *= dx[i].dims[r];
+            CATNN_REQUIRE(dx[i].rank >= 0 && cap >= nx && (dx[i].data || nx == 0), CATNN_ERR_SHAPE_MISMATCH,
+                          "dx[" + std::to_string(i) + "] holds " + std::to_string(cap) + " values, input has " +
+                              dims_str(xd));
+            if (nx) read_cols(*t, t->grad.at((uint32_t)i), 1, nx, 0, nx, dx[i].data, nx);
+            dx[i].rank = (int32_t)xd.size();
+            for (size_t r = 0; r < xd.size(); ++r) dx[i].dims[r] = xd[r];
+            dx[i].dtype = inputs[i].dtype;
+        }
+        const Node &self_node = g.node(nid);
+        for (int32_t j = 0; j < n_dparams; ++j) {
+            const auto &pr = self_node.params[(size_t)j];
+            int64_t col0, ncols;
+            TParam *p = find_param(*t, nid, pr.first, &col0, &ncols);
+            const int64_t np = pr.second.numel();
+            int64_t cap = 1;
+            for (int r = 0; r < dparams[j].rank; ++r) cap *= dparams[j].dims[r];
+            CATNN_REQUIRE(dparams[j].rank >= 0 && cap >= np && (dparams[j].data || np == 0),
+                          CATNN_ERR_SHAPE_MISMATCH,
+                          "dparams[" + std::to_string(j) + "] (" + pr.first + ") holds " + std::to_string(cap) +
+                              " values, the param has " + std::to_string(np));
+            if (np) read_cols(*t, p->grad, p->rows, p->cols, col0, ncols, dparams[j].data, np);
+            dparams[j].rank = (int32_t)pr.second.dims.size();
+            for (size_t r = 0; r < pr.second.dims.size(); ++r) dparams[j].dims[r] = pr.second.dims[r];
+            dparams[j].dtype = CATNN_F32;
+        }
+        CATNN_HIP(hipStreamSynchronize(s));
     });
 }
 

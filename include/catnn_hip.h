@@ -309,6 +309,23 @@ int catnn_hip_run_kernel(catnn_hip_device *dev, const catnn_node *node,
                          const catnn_tensor *inputs, int32_t n_inputs,
                          catnn_tensor *out);
 
+/* Drop-in for `adjoint_of(node, inputs, output, dy) -> Adjoint { dx,
+ * dparams }` (crates/catnn-compile/src/kernel/adjoint.rs:762-951), the seam
+ * the training wave calls at crates/catnn-rt/src/coord.rs:413, with host
+ * tensors: `dx[i]` receives the cotangent of inputs[i] (n_inputs entries)
+ * and `dparams[j]` that of the node's j-th param in IndexMap order
+ * (n_dparams == node->n_params); each must hold the value's numel floats,
+ * and dims, rank and dtype are written.  The forward value is recomputed on
+ * the device from `inputs` (as attention_backward recomputes its forward,
+ * adjoint.rs:582-722), so `output` may be NULL and is not read.  Ops as the
+ * training step executes them (bf16 MFMA GEMMs with fp32 accumulation);
+ * others → CATNN_ERR_UNSUPPORTED; no inputs → CATNN_ERR_WIRING
+ * (adjoint.rs:768-770). */
+int catnn_hip_run_adjoint(catnn_hip_device *dev, const catnn_node *node,
+                          const catnn_tensor *inputs, int32_t n_inputs,
+                          const catnn_tensor *output, const catnn_tensor *dy,
+                          catnn_tensor *dx, catnn_tensor *dparams, int32_t n_dparams);
+
 /* Device-resident variant: inputs, output and params are arena buffer ids
  * (params bound as "param:{node.name}:{port}"; the node's params need only
  * dims here, data may be NULL).  `in_types` gives each input's type (data

@@ -1,0 +1,123 @@
+"""adjoint_of on the GPU, node by node (catnn_hip_run_adjoint through
+DeviceHandler.adjoint_of), against the oracle's restatement of
+crates/catnn-compile/src/kernel/adjoint.rs:762-951 on the same seeded inputs
+and cotangent.  Ops whose adjoint the device computes in fp32 (Identity,
+ReLU, GELU, Add/ResidualAdd, LayerNorm) are held to the fp32 bar (rel L2
+1e-4); ops with GEMMs (Linear, Attention, MoE) run them on bf16 MFMA with
+fp32 accumulation, as the training step does, and are held to the bf16 bar
+(1e-2)."""
+import numpy as np
+import pytest
+
+import oracle
+import oracle_train as ot
+from catnn_amd import CatError, DeviceHandler, IrNode, OpenOp, Tensor, TensorType
+from conftest import rel_l2
+
+pytestmark = pytest.mark.gpu
+
+FP32_TOL = 1e-4
+BF16_TOL = 1e-2
+
+
+def _t(a):
+    return Tensor.from_numpy(np.ascontiguousarray(a, np.float32))
+
+
+def _check(device, node, ins, tol, seed=0):
+    r = np.random.default_rng(seed)
+    ins = [np.asarray(a, np.float32) for a in ins]
+    out = oracle.eval_node(node, ins)
+    dy = r.standard_normal(out.shape).astype(np.float32)
+    print(f"[adjoint] {node.name} {node.op.kind} ins={[a.shape for a in ins]}", flush=True)
+    dx, dp = DeviceHandler(device).adjoint_of(node, [_t(a) for a in ins], None, _t(dy))
+    dx_o, dp_o = ot.adjoint_of(node, ins, out, dy)
+    assert len(dx) == len(dx_o) == len(ins)
+    for i, (a, b) in enumerate(zip(dx, dx_o)):
+        assert a.ty.shape == ins[i].shape
+        e = rel_l2(a.numpy(), np.asarray(b).reshape(ins[i].shape))
+        print(f"  dx[{i}] rel_l2 {e:.2e}")
+        assert e < tol, (node.name, i, e)
+    assert list(dp) == list(node.params)
+    for port, g in dp.items():
+        want = np.asarray(dp_o[port]).reshape(node.params[port].ty.shape)
+        e = rel_l2(g.numpy(), want)
+        print(f"  d{port} rel_l2 {e:.2e}")
+        assert g.ty.shape == tuple(node.params[port].ty.shape)
+        assert e < tol, (node.name, port, e)
+    return dx, dp
+
+
+@pytest.mark.parametrize("m,k,n,bias", [(64, 128, 96, True), (37, 784, 10, True), (256, 512, 512, False)])
+def test_linear(device, m, k, n, bias):
+    r = np.random.default_rng(k + n)
+    params = {"w": _t(r.standard_normal((k, n)) / np.sqrt(k))}
+    if bias:
+        params["b"] = _t(r.standard_normal(n))
+    node = IrNode(3, "fc", OpenOp.linear(k, n, bias), TensorType.f32([m, n]), params)
+    _check(device, node, [r.standard_normal((m, k))], BF16_TOL)
+
+
+@pytest.mark.parametrize("op", ["relu", "gelu", "identity"])
+def test_elementwise(device, op):
+    r = np.random.default_rng(1)
+    x = r.standard_normal((33, 65)) * 2
+    node = IrNode(1, op, getattr(OpenOp, op)(), TensorType.f32([33, 65]))
+    dx, _ = _check(device, node, [x], FP32_TOL)
+
+
+@pytest.mark.parametrize("op", ["add", "residual_add"])
+def test_two_input_add(device, op):
+    r = np.random.default_rng(2)
+    a, b = r.standard_normal((4, 50)), r.standard_normal((4, 50))
+    node = IrNode(5, op, getattr(OpenOp, op)(), TensorType.f32([4, 50]))
+    dx, _ = _check(device, node, [a, b], FP32_TOL)
+    assert np.array_equal(dx[0].numpy(), dx[1].numpy())  # dy to both inputs (adjoint.rs:778-784)
+
+
+@pytest.mark.parametrize("rows,cols", [(64, 128), (9, 1000)])
+def test_layer_norm(device, rows, cols):
+    r = np.random.default_rng(cols)
+    node = IrNode(2, "ln", OpenOp.layer_norm(1), TensorType.f32([rows, cols]),
+                  {"gamma": _t(1 + 0.1 * r.standard_normal(cols)), "beta": _t(0.1 * r.standard_normal(cols))})
+    _check(device, node, [r.standard_normal((rows, cols)) * 2 + 0.5], FP32_TOL)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_attention(device, causal):
+    r = np.random.default_rng(3)
+    d, heads, dh, b, s = 128, 2, 64, 2, 96
+    params = {p: _t(0.05 * r.standard_normal((d, d))) for p in ("wq", "wk", "wv", "wo")}
+    node = IrNode(4, "attn", OpenOp.attention(heads, d, dh, causal), TensorType.f32([b, s, d]), params)
+    _check(device, node, [r.standard_normal((b, s, d))], BF16_TOL)
+
+
+def test_moe(device):
+    r = np.random.default_rng(4)
+    E, k, H, I, T = 4, 2, 128, 96, 200
+    params = {"gate": _t(0.5 * r.standard_normal((H, E)))}
+    for e in range(E):
+        params[f"e{e}.w1"] = _t(0.05 * r.standard_normal((H, I)))
+        params[f"e{e}.w3"] = _t(0.05 * r.standard_normal((H, I)))
+        params[f"e{e}.w2"] = _t(0.05 * r.standard_normal((I, H)))
+    node = IrNode(6, "moe", OpenOp.moe(E, k, H, I), TensorType.f32([T, H]), params)
+    _check(device, node, [r.standard_normal((T, H))], BF16_TOL)
+
+
+def test_adjoint_errors(device):
+    h = DeviceHandler(device)
+    node = IrNode(1, "r", OpenOp.relu(), TensorType.f32([4]))
+    with pytest.raises(CatError) as e:
+        h.adjoint_of(node, [], None, _t(np.ones(4)))
+    assert e.value.kind == "Wiring"
+    with pytest.raises(CatError) as e:
+        h.adjoint_of(node, [_t(np.ones(4))], None, _t(np.ones(5)))
+    assert e.value.kind == "ShapeMismatch"
+    sm = IrNode(1, "sm", OpenOp.softmax(), TensorType.f32([2, 4]))
+    with pytest.raises(CatError) as e:
+        h.adjoint_of(sm, [_t(np.ones((2, 4)))], None, _t(np.ones((2, 4))))
+    assert e.value.kind == "Unsupported"
+    fc = IrNode(1, "fc", OpenOp.linear(8, 4, False), TensorType.f32([2, 4]), {"w": _t(np.ones((8, 4)))})
+    with pytest.raises(CatError) as e:
+        h.adjoint_of(fc, [_t(np.ones((2, 7)))], None, _t(np.ones((2, 4))))
+    assert e.value.kind == "ShapeMismatch"
