@@ -66,18 +66,21 @@ def time_program(dev, prog, x, steps, warmup):
 BF16_MFMA_PEAK_TFLOPS = 2500.0
 
 
-def time_train_step(dev, steps, warmup):
+def time_train_step(dev, steps, warmup, opt="sgd"):
     """Config 5: one training step (forward, MSE, backward, SGD) of the
     config-3 block followed by the config-4 MoE layer.  Every timed step
     starts from the installed weights (Trainer.reset, outside the timed
     region): at this initialisation lr 0.05 drives the weights to NaN within
-    two steps, which would collapse the routing and time another workload."""
+    two steps, which would collapse the routing and time another workload.
+    With opt="adam" the same step ends in Adam::put at Adam's default lr
+    1e-3 (reset also zeroes the moments, so every timed step is Adam's
+    first)."""
     import catnn_amd
     from catnn_amd import configs
 
     wl = configs.config5()
-    log("config 5 built")
-    tr = catnn_amd.Trainer(dev, wl.graph, wl.lr)
+    log(f"config 5 built ({opt})")
+    tr = catnn_amd.Trainer(dev, wl.graph, wl.lr if opt == "sgd" else 1e-3, opt=opt)
     tr.set_batch(wl.x, wl.target)
     for _ in range(warmup):
         tr.reset()
@@ -96,7 +99,7 @@ def time_train_step(dev, steps, warmup):
     tr.free()
     ms = total / steps
     tflops = wl.flops / (ms / 1e3) / 1e12
-    log(f"config 5: {ms:.3f} ms/step, {tflops:.1f} TFLOP/s algorithmic, loss {loss:.3f}")
+    log(f"config 5 ({opt}): {ms:.3f} ms/step, {tflops:.1f} TFLOP/s algorithmic, loss {loss:.3f}")
     return {"ms_per_step": round(ms, 4), "tokens_per_s": round(wl.tokens / (ms / 1e3)),
             "algorithmic_TFLOP_per_s": round(tflops, 2),
             "bf16_mfma_frac": round(tflops / BF16_MFMA_PEAK_TFLOPS, 4),
@@ -305,6 +308,7 @@ def main():
         del w3
         log(f"config 3: {ms3:.3f} ms/step")
         sec["train_step_config5"] = time_train_step(dev, max(3, args.steps // 2), 2)
+        sec["train_step_config5_adam"] = time_train_step(dev, max(3, args.steps // 4), 1, opt="adam")
         sec["mixtral_decoder"] = time_mixtral(dev, max(3, args.steps // 4), 2)
         result["secondary"] = sec
 

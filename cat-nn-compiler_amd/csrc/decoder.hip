@@ -92,7 +92,8 @@ __device__ __forceinline__ int64_t token_id(float v) {
 }
 
 // One wavefront per token copies its table row.  An id ≥ vocab sets *bad and
-// writes zeros (the table is never read out of range).
+// writes zeros (the table is never read out of range).  Rows of 1024 floats
+// take embedding_pair_kernel instead.
 template <bool VEC>
 __global__ __launch_bounds__(256) void embedding_kernel(const float *__restrict__ ids, int64_t n,
                                                         const float *__restrict__ table,
@@ -110,11 +111,51 @@ __global__ __launch_bounds__(256) void embedding_kernel(const float *__restrict_
     }
     const float *src = table + id * hidden;
     if (VEC) {
+        // Four 16-byte loads in flight per lane before their stores.
         const float4 *s4 = reinterpret_cast<const float4 *>(src);
         float4 *y4 = reinterpret_cast<float4 *>(yr);
-        for (int64_t c = lane; c < hidden / 4; c += 64) y4[c] = s4[c];
+        const int64_t nq = hidden / 4;
+        int64_t c = lane;
+        for (; c + 192 < nq; c += 256) {
+            const float4 a = s4[c], b = s4[c + 64], d = s4[c + 128], e = s4[c + 192];
+            y4[c] = a;
+            y4[c + 64] = b;
+            y4[c + 128] = d;
+            y4[c + 192] = e;
+        }
+        for (; c < nq; c += 64) y4[c] = s4[c];
     } else {
         for (int64_t c = lane; c < hidden; c += 64) yr[c] = src[c];
+    }
+}
+
+// Rows of exactly 1024 floats (16-byte aligned): one wavefront copies two
+// tokens' rows, all eight of a lane's 16-byte loads issued before its
+// stores.  Same id conversion and bad-id handling as embedding_kernel.
+__global__ __launch_bounds__(256) void embedding_pair_kernel(const float *__restrict__ ids, int64_t n,
+                                                             const float4 *__restrict__ table, int64_t vocab,
+                                                             float4 *__restrict__ y, int *__restrict__ bad) {
+    constexpr int kQ = 256;  // float4 per row
+    const int lane = threadIdx.x & 63;
+    const int64_t t0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 2;
+    if (t0 >= n) return;
+    const bool two = t0 + 1 < n;
+    const int64_t id0 = token_id(ids[t0]);
+    const int64_t id1 = two ? token_id(ids[t0 + 1]) : 0;
+    const bool ok0 = id0 < vocab, ok1 = two && id1 < vocab;
+    const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+    float4 a[4], b[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        a[j] = ok0 ? table[id0 * kQ + lane + 64 * j] : z;
+        b[j] = ok1 ? table[id1 * kQ + lane + 64 * j] : z;
+    }
+    if (lane == 0 && (!ok0 || (two && !ok1))) *bad = 1;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) y[t0 * kQ + lane + 64 * j] = a[j];
+    if (two) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) y[(t0 + 1) * kQ + lane + 64 * j] = b[j];
     }
 }
 
@@ -147,6 +188,30 @@ __global__ void rope_apply_kernel(float *__restrict__ qk, int64_t ld, int64_t ro
     const float a = q[0], b = q[1];
     q[0] = a * cs.x - b * cs.y;
     q[1] = a * cs.y + b * cs.x;
+}
+
+// The same rotation, two pairs a thread with 16-byte accesses (hd a multiple
+// of 4, rows and the table 16-byte aligned): (cos, sin) of pairs i and i+1
+// come as one float4.
+__global__ void rope_apply2_kernel(float *__restrict__ qk, int64_t ld, int64_t rows, int S, int heads,
+                                   int hd, const float4 *__restrict__ tab) {
+#pragma clang fp contract(off)
+    const int half = hd / 2;
+    const int64_t per_row = (int64_t)heads * (half / 2);
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= rows * per_row) return;
+    const int64_t r = idx / per_row;
+    const int p = 2 * (int)(idx - r * per_row);
+    const int head = p / half, i = p - head * half;
+    const float4 cs = tab[((r % S) * half + i) / 2];
+    float4 *q = reinterpret_cast<float4 *>(qk + r * ld + (int64_t)head * hd + 2 * i);
+    const float4 v = *q;
+    float4 o;
+    o.x = v.x * cs.x - v.y * cs.y;
+    o.y = v.x * cs.y + v.y * cs.x;
+    o.z = v.z * cs.z - v.w * cs.w;
+    o.w = v.z * cs.w + v.w * cs.z;
+    *q = o;
 }
 
 // y = σ(g)·a + (1 − σ(g))·b with σ(g) = 1 / (1 + e^(−g)), g = gate[0].
@@ -202,6 +267,12 @@ void rms_norm_f32(hipStream_t s, const float *x, const float *w, float *y, int64
 void embedding_f32(hipStream_t s, const float *ids, int64_t n, const float *table, int64_t vocab,
                    int64_t hidden, float *y, int *bad) {
     if (n <= 0 || hidden <= 0) return;
+    if (hidden == 1024 && aligned16(table) && aligned16(y)) {
+        embedding_pair_kernel<<<blocks_for((n + 1) / 2, 4), kThreads, 0, s>>>(
+            ids, n, reinterpret_cast<const float4 *>(table), vocab, reinterpret_cast<float4 *>(y), bad);
+        CATNN_HIP(hipGetLastError());
+        return;
+    }
     const unsigned grid = blocks_for(n, 4);
     if (hidden % 4 == 0 && aligned16(table) && aligned16(y))
         embedding_kernel<true><<<grid, kThreads, 0, s>>>(ids, n, table, vocab, hidden, y, bad);
@@ -260,9 +331,13 @@ void gqa_f32(hipStream_t s, const float *x, const float *wqkv, const float *wq, 
         rope_table_kernel<<<blocks_for(nt, kThreads), kThreads, 0, s>>>(tab, nt, half, (int)head_dim, theta);
         CATNN_HIP(hipGetLastError());
         const int64_t np = T * (n_heads + n_kv) * half;
-        rope_apply_kernel<<<blocks_for(np, kThreads), kThreads, 0, s>>>(qkv, LD, T, (int)S,
-                                                                        (int)(n_heads + n_kv),
-                                                                        (int)head_dim, tab);
+        if (half % 2 == 0 && LD % 4 == 0 && aligned16(qkv) && aligned16(tab))
+            rope_apply2_kernel<<<blocks_for(np / 2, kThreads), kThreads, 0, s>>>(
+                qkv, LD, T, (int)S, (int)(n_heads + n_kv), (int)head_dim, reinterpret_cast<const float4 *>(tab));
+        else
+            rope_apply_kernel<<<blocks_for(np, kThreads), kThreads, 0, s>>>(qkv, LD, T, (int)S,
+                                                                            (int)(n_heads + n_kv),
+                                                                            (int)head_dim, tab);
         CATNN_HIP(hipGetLastError());
     }
     attention_core_gqa_f32(s, qkv, qkv + QW, qkv + QW + KW, LD, LD, n_heads / n_kv, window, ctx, QW, B,

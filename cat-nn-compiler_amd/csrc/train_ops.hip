@@ -645,45 +645,60 @@ __global__ __launch_bounds__(256) void sgd_multi_kernel(const SgdParam *__restri
     const bool vec = P.cols % 4 == 0 && al(P.p, 16) && (!grad || al(P.g, 16)) && (!P.b || al(P.b, 8)) &&
                      (!grad || !u.adam || (al(P.m, 16) && al(P.v, 16)));
     if (vec) {
+        // A thread's four rows (rq, rq+16, rq+32, rq+48): every load of the
+        // four is issued before the first update and store.
         const int cq = 4 * (threadIdx.x & 15), rq = threadIdx.x >> 4;
-        for (int i = rq; i < 64; i += 16) {
-            const int r = r0 + i, c = c0 + cq;
-            float v[4] = {0.f, 0.f, 0.f, 0.f};
-            bf16_t h[4] = {0, 0, 0, 0}, l[4] = {0, 0, 0, 0};
-            if (r < P.rows && c < P.cols) {  // c + 3 < cols: cols and c0 are multiples of 4
+        const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
+        float4 pv[4], gv[4], mo[4], ve[4];
+        bool in[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int r = r0 + rq + 16 * j, c = c0 + cq;
+            in[j] = r < P.rows && c < P.cols;  // c + 3 < cols: cols and c0 are multiples of 4
+            pv[j] = gv[j] = mo[j] = ve[j] = z4;
+            if (in[j]) {
                 const int64_t e = (int64_t)r * P.cols + c;
-                const float4 pv = *reinterpret_cast<const float4 *>(P.p + e);
-                v[0] = pv.x; v[1] = pv.y; v[2] = pv.z; v[3] = pv.w;
+                pv[j] = *reinterpret_cast<const float4 *>(P.p + e);
                 if (grad) {
-                    const float4 gv = *reinterpret_cast<const float4 *>(P.g + e);
-                    float4 mo = make_float4(0.f, 0.f, 0.f, 0.f), ve = mo;
+                    gv[j] = *reinterpret_cast<const float4 *>(P.g + e);
                     if (u.adam) {
-                        mo = *reinterpret_cast<const float4 *>(P.m + e);
-                        ve = *reinterpret_cast<const float4 *>(P.v + e);
+                        mo[j] = *reinterpret_cast<const float4 *>(P.m + e);
+                        ve[j] = *reinterpret_cast<const float4 *>(P.v + e);
                     }
-                    v[0] = update_value(u, v[0], gv.x, mo.x, ve.x);
-                    v[1] = update_value(u, v[1], gv.y, mo.y, ve.y);
-                    v[2] = update_value(u, v[2], gv.z, mo.z, ve.z);
-                    v[3] = update_value(u, v[3], gv.w, mo.w, ve.w);
+                }
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int i = rq + 16 * j;
+            bf16_t h[4] = {0, 0, 0, 0}, l[4] = {0, 0, 0, 0};
+            if (in[j]) {
+                const int64_t e = (int64_t)(r0 + i) * P.cols + c0 + cq;
+                float v[4] = {pv[j].x, pv[j].y, pv[j].z, pv[j].w};
+                if (grad) {
+                    v[0] = update_value(u, v[0], gv[j].x, mo[j].x, ve[j].x);
+                    v[1] = update_value(u, v[1], gv[j].y, mo[j].y, ve[j].y);
+                    v[2] = update_value(u, v[2], gv[j].z, mo[j].z, ve[j].z);
+                    v[3] = update_value(u, v[3], gv[j].w, mo[j].w, ve[j].w);
                     *reinterpret_cast<float4 *>(P.p + e) = make_float4(v[0], v[1], v[2], v[3]);
                     if (u.adam) {
-                        *reinterpret_cast<float4 *>(P.m + e) = mo;
-                        *reinterpret_cast<float4 *>(P.v + e) = ve;
+                        *reinterpret_cast<float4 *>(P.m + e) = mo[j];
+                        *reinterpret_cast<float4 *>(P.v + e) = ve[j];
                     }
                 }
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    h[j] = f2bf(v[j]);
-                    l[j] = f2bf(v[j] - __uint_as_float((uint32_t)h[j] << 16));
+                for (int q = 0; q < 4; ++q) {
+                    h[q] = f2bf(v[q]);
+                    l[q] = f2bf(v[q] - __uint_as_float((uint32_t)h[q] << 16));
                 }
                 if (P.b)
                     *reinterpret_cast<uint2 *>(P.b + e) =
                         make_uint2(h[0] | (uint32_t)h[1] << 16, h[2] | (uint32_t)h[3] << 16);
             }
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                th[i][cq + j] = h[j];
-                tl[i][cq + j] = l[j];
+            for (int q = 0; q < 4; ++q) {
+                th[i][cq + q] = h[q];
+                tl[i][cq + q] = l[q];
             }
         }
     } else {

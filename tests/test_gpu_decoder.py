@@ -53,6 +53,32 @@ def test_embedding_is_an_exact_gather(device):
     assert got.shape == (300, 16) and np.array_equal(got, want)
 
 
+@pytest.mark.parametrize("n", [1, 7, 64])
+def test_embedding_1024_wide_rows(device, n):
+    # hidden 1024 takes the two-tokens-per-wavefront kernel; odd counts
+    # leave the last wavefront one token.
+    r = np.random.default_rng(n)
+    table = r.standard_normal((300, 1024)).astype(np.float32)
+    ids = r.integers(0, 300, n).astype(np.float32)
+    for j, v in enumerate([-3.0, np.nan, 2.5, 298.5, 0.49][: (n + 2) // 3]):
+        ids[3 * j] = v  # negative and NaN → 0, halves round away from zero
+    node = IrNode(1, "emb", OpenOp.embedding(300, 1024), TensorType.f32([n, 1024]), {"w": _t(table)})
+    got, want, _ = _run(device, node, [ids])
+    assert got.shape == (n, 1024) and np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("bad_at", [0, 1, 2])
+def test_embedding_1024_wide_rows_reject_an_id_past_the_vocabulary(device, bad_at):
+    table = np.zeros((10, 1024), np.float32)
+    node = IrNode(1, "emb", OpenOp.embedding(10, 1024), TensorType.f32([3, 1024]), {"w": _t(table)})
+    ids = np.array([1.0, 2.0, 3.0], np.float32)
+    ids[bad_at] = 10.0
+    with pytest.raises(CatError) as e:
+        DeviceHandler(device).run_kernel(node, [_t(ids)])
+    assert e.value.kind == "ShapeMismatch"
+    assert DeviceHandler(device).run_kernel(node, [_t([9.0])]).numpy().shape == (1, 1024)
+
+
 def test_embedding_rejects_an_id_past_the_vocabulary(device):
     node = IrNode(1, "emb", OpenOp.embedding(10, 4), TensorType.f32([3, 4]),
                   {"w": _t(np.zeros((10, 4)))})
