@@ -399,16 +399,33 @@ __device__ __forceinline__ void store8f(float *dst, const float (&f)[8]) {
     *reinterpret_cast<float4 *>(dst + 4) = make_float4(f[4], f[5], f[6], f[7]);
 }
 
+// The epilogue's per-element operands at (row, col … col+7), loaded ahead:
+// SwiGLU adjoint: a = S1 and c = S2 (bf16, one uint4 each); GELU adjoint:
+// Z (fp32, two uint4 of float bits).
+template <int EPI>
+__device__ __forceinline__ void epi_preload(const GemmBf16Params &p, int row, int col, uint4 (&pre)[2]) {
+    if constexpr (EPI == EPI_SWIGLU_BWD) {
+        const int64_t so = (int64_t)row * p.lds + col;
+        pre[0] = *reinterpret_cast<const uint4 *>(p.S1 + so);
+        pre[1] = *reinterpret_cast<const uint4 *>(p.S2 + so);
+    } else if constexpr (EPI == EPI_GELU_BWD) {
+        const uint4 *z = reinterpret_cast<const uint4 *>(p.Z + (int64_t)row * p.ldz + col);
+        pre[0] = z[0];
+        pre[1] = z[1];
+    }
+}
+
 // Eight consecutive outputs (row, col … col+7) of epilogue kind EPI with
-// 16-byte accesses; the same arithmetic per element as epi_elem.
+// 16-byte accesses; the same arithmetic per element as epi_elem.  `pre`
+// (or null: loaded here) holds what epi_preload reads.
 template <int EPI>
 __device__ __forceinline__ void epi_vec8(const GemmBf16Params &p, float (&v)[8], int row, int col,
-                                         float *__restrict__ C32) {
+                                         float *__restrict__ C32, const uint4 *pre = nullptr) {
     if constexpr (EPI == EPI_SWIGLU_BWD) {
         const int64_t so = (int64_t)row * p.lds + col;
         float a[8], c[8], d1[8], d2[8];
-        unpack8(*reinterpret_cast<const uint4 *>(p.S1 + so), a);
-        unpack8(*reinterpret_cast<const uint4 *>(p.S2 + so), c);
+        unpack8(pre ? pre[0] : *reinterpret_cast<const uint4 *>(p.S1 + so), a);
+        unpack8(pre ? pre[1] : *reinterpret_cast<const uint4 *>(p.S2 + so), c);
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             const float sg = sigmoid_hw(a[j]);
@@ -441,7 +458,13 @@ __device__ __forceinline__ void epi_vec8(const GemmBf16Params &p, float (&v)[8],
             }
         } else if constexpr (EPI == EPI_GELU_BWD) {
             float z[8];
-            load8f(p.Z + (int64_t)row * p.ldz + col, z);
+            if (pre) {
+                const uint32_t u[8] = {pre[0].x, pre[0].y, pre[0].z, pre[0].w, pre[1].x, pre[1].y, pre[1].z, pre[1].w};
+#pragma unroll
+                for (int j = 0; j < 8; ++j) z[j] = __uint_as_float(u[j]);
+            } else {
+                load8f(p.Z + (int64_t)row * p.ldz + col, z);
+            }
 #pragma unroll
             for (int j = 0; j < 8; ++j) v[j] *= gelu_grad_hw(z[j]);
         }
@@ -485,6 +508,20 @@ __device__ __forceinline__ void epilogue_staged(unsigned char *smem, const GemmB
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = wave / C::WAVES_N, wn = wave % C::WAVES_N, lr = lane & 31, lg = lane >> 5;
     dma_sync<0>();  // every wavefront is done with the operand stages
+    // Adjoint epilogues read an operand per output: issue all of this
+    // thread's loads now, so that they are in flight while the tile is
+    // staged (the barrier below waits for the LDS writes only).
+    constexpr bool PRE = !DUAL && (EPI == EPI_SWIGLU_BWD || EPI == EPI_GELU_BWD) && (BM * CH) % C::NT == 0;
+    constexpr int IT = PRE ? BM * CH / C::NT : 1;
+    static_assert(2 * IT < 64, "preloads must fit the vmcnt counter");
+    uint4 pre[IT][2];
+    if constexpr (PRE) {
+#pragma unroll
+        for (int i = 0; i < IT; ++i) {
+            const int idx = threadIdx.x + i * C::NT;
+            epi_preload<EPI>(p, row0 + idx / CH, col0 + (idx % CH) * 8, pre[i]);
+        }
+    }
 #pragma unroll
     for (int mi = 0; mi < C::FM; ++mi)
 #pragma unroll
@@ -493,6 +530,18 @@ __device__ __forceinline__ void epilogue_staged(unsigned char *smem, const GemmB
             for (int r = 0; r < 16; ++r)
                 t[(wm * WM + mi * 32 + 8 * (r >> 2) + 4 * lg + (r & 3)) * BN + staged_col<C, DUAL>(wn, ni, lr)] =
                     acc[mi][ni][r];
+    if constexpr (PRE) {
+        dma_sync<63>();  // LDS writes of every wavefront visible; preloads may still be in flight
+#pragma unroll
+        for (int i = 0; i < IT; ++i) {
+            const int idx = threadIdx.x + i * C::NT;
+            const int r = idx / CH, c = (idx % CH) * 8;
+            float v[8];
+            load8f(t + r * BN + c, v);
+            epi_vec8<EPI>(p, v, row0 + r, col0 + c, C32, pre[i]);
+        }
+        return;
+    }
     dma_sync<0>();
     for (int idx = threadIdx.x; idx < BM * CH; idx += C::NT) {
         const int r = idx / CH, c = (idx % CH) * 8;
