@@ -175,8 +175,11 @@ std::vector<Launch> launches_of(const Node &node, const std::vector<std::vector<
             break;
         case CATNN_OP_EMBEDDING: {
             const int64_t hidden = node.op.a[1];
-            L.push_back({hidden % 4 == 0 ? "16embedding_kernelILb1E" : "16embedding_kernelILb0E",
-                         clamp_grid(cdiv(nx, 4)), 256, 0});
+            if (hidden == 1024)  // two tokens a wavefront
+                L.push_back({"21embedding_pair_kernel", clamp_grid(cdiv(cdiv(nx, 2), 4)), 256, 0});
+            else
+                L.push_back({hidden % 4 == 0 ? "16embedding_kernelILb1E" : "16embedding_kernelILb0E",
+                             clamp_grid(cdiv(nx, 4)), 256, 0});
             break;
         }
         case CATNN_OP_GQA_ATTENTION: {
@@ -186,7 +189,10 @@ std::vector<Launch> launches_of(const Node &node, const std::vector<std::vector<
             gemm_f32(L, T, LD, D, D, LD, false, 0);
             if (half > 0) {
                 L.push_back({"17rope_table_kernel", clamp_grid(cdiv(S * half, 256)), 256, 0});
-                L.push_back({"17rope_apply_kernel", clamp_grid(cdiv(T * (nh + nkv) * half, 256)), 256, 0});
+                if (half % 2 == 0 && LD % 4 == 0)  // two pairs a thread
+                    L.push_back({"18rope_apply2_kernel", clamp_grid(cdiv(T * (nh + nkv) * half / 2, 256)), 256, 0});
+                else
+                    L.push_back({"17rope_apply_kernel", clamp_grid(cdiv(T * (nh + nkv) * half, 256)), 256, 0});
             }
             attention(L, B, S, nh, hd, LD, LD, QW);
             gemm_f32(L, T, D, QW, QW, D, false, 0);

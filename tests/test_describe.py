@@ -86,7 +86,8 @@ def _every_kernel_path():
     yield IrNode(1, "rms4", OpenOp.rms_norm(10), f([3, 4096]), {"w": _z([4096])}), [f([3, 4096])]
     yield IrNode(1, "emb", OpenOp.embedding(50, 16), f([2, 4, 16]), {"w": _z([50, 16])}), [f([2, 4])]
     yield IrNode(1, "emb_odd", OpenOp.embedding(50, 6), f([2, 4, 6]), {"w": _z([50, 6])}), [f([2, 4])]
-    for hd in (8, 64):
+    yield IrNode(1, "emb1024", OpenOp.embedding(50, 1024), f([3, 1024]), {"w": _z([50, 1024])}), [f([3])]
+    for hd in (6, 8, 64):  # RoPE one pair a thread (hd/2 odd), two pairs a thread
         d = 4 * hd
         yield (IrNode(1, f"gqa{hd}", OpenOp.gqa_attention(4, 2, hd, d, 8, 10000), f([2, 9, d]),
                       {"wq": _z([d, d]), "wk": _z([d, 2 * hd]), "wv": _z([d, 2 * hd]), "wo": _z([d, d])}),
@@ -120,6 +121,8 @@ def test_every_kernel_named_resolves_once():
     assert any("route_dma_kernelILi4E" in k for k in seen) and any("route_dma_kernelILi1E" in k for k in seen)
     assert any("attn_generic_kernel" in k for k in seen) and any("attn_mfma_kernel" in k for k in seen)
     assert any("rms_norm_any_kernel" in k for k in seen) and any("embedding_kernelILb0E" in k for k in seen)
+    assert any("embedding_pair_kernel" in k for k in seen)
+    assert any("rope_apply_kernel" in k for k in seen) and any("rope_apply2_kernel" in k for k in seen)
     assert any("gemm_grouped_kernel" in k for k in seen) and any("gemm_dma_kernelILi4ELb1ELb0E" in k for k in seen)
     # copies launch no kernel
     ty = TensorType.f32([2, 3])
