@@ -163,6 +163,42 @@ def cpu_baseline_mlp(wl, target_s):
                       f"fc2+bias) in {t:.1f} s; OpenMP over rows where the reference uses Rayon"}
 
 
+def cpu_baseline_moe(wl, target_s):
+    """Config 4's MoE layer on the oracle's restatement of moe::moe
+    (moe.rs:197-223): the router over all tokens, then a sequential token
+    loop of per-expert SwiGLU calls, single-threaded as the reference is.
+    Timed as the routing alone plus the expert work of a token prefix; per
+    token cost is constant, so the layer's time is scaled to all tokens."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import numpy as np
+    import oracle
+
+    node = wl.graph.nodes[1]
+    E, k, H, I = node.op.fields
+    P = node.params
+    x = wl.x.numpy().reshape(-1, H)
+    T = x.shape[0]
+    gate = P["gate"].numpy()
+    w1s = np.stack([P[f"e{e}.w1"].numpy().reshape(H, I) for e in range(E)])
+    w3s = np.stack([P[f"e{e}.w3"].numpy().reshape(H, I) for e in range(E)])
+    w2s = np.stack([P[f"e{e}.w2"].numpy().reshape(I, H) for e in range(E)])
+
+    def run(n):
+        t0 = time.perf_counter()
+        oracle.moe(x, gate, w1s, w3s, w2s, k, tokens=np.arange(n, dtype=np.int64))
+        return time.perf_counter() - t0
+
+    t_route = run(0)
+    per_tok = max(run(2) - t_route, 1e-6) / 2
+    n = int(max(2, min(T, (target_s - t_route) / per_tok)))
+    per_tok = max(run(n) - t_route, 1e-6) / n
+    layer_s = t_route + T * per_tok
+    return {"value": round(T / layer_s, 2), "unit": "tokens/s", "cores": 1, "kind": "port",
+            "sample": f"routing of all {T} tokens ({t_route:.2f} s) plus the expert loop over the first {n} "
+                      f"tokens ({per_tok * 1e3:.1f} ms per token), scaled to {T} tokens; sequential as "
+                      f"moe::moe"}
+
+
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemm_f32_config2_hbm_traffic.txt")
 COPY_FLOATS = 128 << 20  # 512 MiB read + 512 MiB written by the calibration copy
 
@@ -296,8 +332,13 @@ def main():
             "GFLOP_per_s": round(w4.flops / (ms4 / 1e3) / 1e9, 1),
             "mfma_frac": round(w4.flops / (ms4 / 1e3) / 1e12 / FP32_MFMA_PEAK_TFLOPS, 4)}
         p4.free()
-        del w4
         log(f"config 4: {ms4:.3f} ms/step")
+        if not args.no_cpu_baseline:
+            cb = cpu_baseline_moe(w4, args.cpu_seconds)
+            sec["moe_layer_config4"]["cpu_baseline"] = cb
+            sec["moe_layer_config4"]["vs_cpu"] = round(sec["moe_layer_config4"]["tokens_per_s"] / cb["value"], 1)
+            log(f"config 4 cpu baseline: {cb}")
+        del w4
         w3 = configs.config3()
         p3 = catnn_amd.Program(dev, w3.graph)
         ms3, _, t3 = time_program(dev, p3, w3.x, max(3, args.steps // 2), 2)
