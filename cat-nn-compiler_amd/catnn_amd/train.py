@@ -48,6 +48,14 @@ class Trainer:
         cx, ct = ctensor(x), ctensor(target)
         check(lib.catnn_hip_train_set_batch(self.handle, ctypes.byref(cx), ctypes.byref(ct)))
 
+    def set_batch_classes(self, x: Tensor, ids):
+        """The batch of a graph whose output is an LmHead: one class id per
+        output row (TrainTarget::Classes, pipeline.rs:430-441)."""
+        cx = ctensor(x)
+        a = np.ascontiguousarray(np.asarray(ids).reshape(-1), np.uint32)
+        check(lib.catnn_hip_train_set_batch_classes(self.handle, ctypes.byref(cx),
+                                                    a.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)), a.size))
+
     def step(self, sync: bool = True):
         """One step; returns the loss (before the update) when `sync`."""
         if not sync:

@@ -6,7 +6,10 @@
 // apply_update (coord.rs:481).
 //
 //   forward   topo order; every op stores the tape its adjoint needs;
-//   loss      MSE against the target (adjoint.rs:106-119);
+//   loss      as loss_and_grad picks it (pipeline.rs:430-451): cross-entropy
+//             against class ids when the output node is an LmHead
+//             (adjoint.rs:123-145), else MSE against the target
+//             (adjoint.rs:106-119);
 //   backward  reverse topo order, adjoint_of per node (adjoint.rs:762-951);
 //             a value's cotangent is written by the first of its consumers
 //             to run and accumulated by the others (add_tensors,
@@ -66,6 +69,10 @@ struct TParam {
     float *m = nullptr, *v = nullptr;  // Adam moments "adam:{node}:{port}:m|v"
     bf16_t *b = nullptr, *bt = nullptr;
     bf16_t *bt3 = nullptr;  // [cols, 3·rows] split-bf16 transposed copy (hi | lo | hi)
+    // Held as the transpose of the graph's tensor (LmHead's w [V, H] is kept
+    // as wᵀ [H, V], a Linear weight, as adjoint.rs:903-913 transposes it);
+    // reads transpose back.
+    bool transposed = false;
 };
 
 struct TNode {
@@ -107,7 +114,10 @@ struct catnn_hip_trainer {
     std::set<uint32_t> input_ids;
     std::set<uint32_t> has_grad;  // ids whose cotangent some adjoint (or the loss) writes
     uint32_t out_id = 0;
-    float *target = nullptr, *loss = nullptr, *mse_scratch = nullptr;
+    bool classes = false;  // the output is an LmHead: TrainTarget::Classes, cross-entropy
+    int64_t class_rows = 0, vocab = 0;
+    uint32_t *class_ids = nullptr;
+    float *target = nullptr, *loss = nullptr, *mse_scratch = nullptr, *ce_rows = nullptr;
     catnn::k::SgdParam *sgd_table = nullptr;  // device copy of every parameter's update entry
     int sgd_n = 0, sgd_tiles = 0;
     std::vector<catnn::BufferReq> reqs;
@@ -220,6 +230,7 @@ static void plan_trainer(Tr &t) {
                 case CATNN_OP_IDENTITY: case CATNN_OP_RESHAPE: case CATNN_OP_TRANSPOSE:
                 case CATNN_OP_RELU: case CATNN_OP_GELU: case CATNN_OP_LINEAR: case CATNN_OP_MATMUL:
                 case CATNN_OP_LAYER_NORM: case CATNN_OP_ATTENTION: case CATNN_OP_MOE:
+                case CATNN_OP_LM_HEAD:
                     break;
                 case CATNN_OP_ADD: case CATNN_OP_RESIDUAL_ADD:
                     CATNN_REQUIRE(tn.ins.size() != 2 || numel(tn.in_dims[0]) == numel(tn.in_dims[1]),
@@ -305,9 +316,17 @@ static void plan_trainer(Tr &t) {
         request(t, "grad:" + std::to_string(tn.id), bytes, std::min<uint64_t>(from, bwd(tn.tick)),
                 bwd(tn.tick), reinterpret_cast<void **>(&t.grad[tn.id]));
     }
-    request(t, "target", (uint64_t)numel(t.dims[t.out_id]) * 4, 0, upd, reinterpret_cast<void **>(&t.target));
+    t.classes = g.node(t.out_id).op.kind == CATNN_OP_LM_HEAD;
+    if (t.classes) {  // pipeline.rs:430-441: an LmHead output trains on class ids
+        t.vocab = t.dims[t.out_id].back();
+        t.class_rows = numel(t.dims[t.out_id]) / std::max<int64_t>(t.vocab, 1);
+        request(t, "classes", (uint64_t)t.class_rows * 4, 0, upd, reinterpret_cast<void **>(&t.class_ids));
+        request(t, "ce_rows", (uint64_t)t.class_rows * 4, n, n, reinterpret_cast<void **>(&t.ce_rows));
+    } else {
+        request(t, "target", (uint64_t)numel(t.dims[t.out_id]) * 4, 0, upd, reinterpret_cast<void **>(&t.target));
+        request(t, "mse_scratch", k::mse_scratch_bytes(), n, n, reinterpret_cast<void **>(&t.mse_scratch));
+    }
     request(t, "loss", 256, n, upd, reinterpret_cast<void **>(&t.loss));
-    request(t, "mse_scratch", k::mse_scratch_bytes(), n, n, reinterpret_cast<void **>(&t.mse_scratch));
 
     auto add_param = [&](TNode &tn, const std::string &port, int64_t rows, int64_t cols, bool b, bool bt,
                          std::vector<float> init, bool bt3 = false) {
@@ -366,6 +385,23 @@ static void plan_trainer(Tr &t) {
                 scratch(tn, "dybt", (uint64_t)(M * N) * 2);
                 scratch(tn, "colsum", k::colsum_scratch_bytes(M, (int)N));
                 scratch(tn, "wparts", wparts_bytes(K, N, M));
+                break;
+            }
+            case CATNN_OP_LM_HEAD: {
+                // logits = x·wᵀ: a bias-free Linear with weight wᵀ [H, V].
+                const HostTensor *w = host(nd, "w");
+                const int64_t V = nd.op.a[1], K = nd.op.a[0], M = numel(x) / K;
+                CATNN_REQUIRE(w->numel() == V * K, CATNN_ERR_SHAPE_MISMATCH, "lm_head w");
+                std::vector<float> wt((size_t)(V * K));
+                for (int64_t v = 0; v < V; ++v)
+                    for (int64_t h = 0; h < K; ++h) wt[(size_t)(h * V + v)] = w->data[(size_t)(v * K + h)];
+                add_param(tn, "w", K, V, true, false, std::move(wt), true);
+                tn.params["w"]->transposed = true;
+                tape(tn, "x3", (uint64_t)(M * 3 * K) * 2);
+                scratch(tn, "xbt", (uint64_t)(M * K) * 2);
+                scratch(tn, "dyb", (uint64_t)(M * V) * 2);
+                scratch(tn, "dybt", (uint64_t)(M * V) * 2);
+                scratch(tn, "wparts", wparts_bytes(K, V, M));
                 break;
             }
             case CATNN_OP_LAYER_NORM: {
@@ -545,7 +581,7 @@ static void forward_node(Tr &t, TNode &tn) {
             if (tn.ins.size() > 1) k::add_f32(s, x, t.val.at(tn.ins[1]), y, nx, nx);
             else k::copy_f32(s, x, y, nx);
             break;
-        case CATNN_OP_LINEAR: case CATNN_OP_MATMUL: {
+        case CATNN_OP_LINEAR: case CATNN_OP_MATMUL: case CATNN_OP_LM_HEAD: {
             TParam *w = tn.params.begin()->second;
             for (auto &kv : tn.params) if (kv.first != "b") w = kv.second;
             TParam *b = tn.params.count("b") ? tn.params["b"] : nullptr;
@@ -656,7 +692,7 @@ static void backward_node(Tr &t, TNode &tn) {
         case CATNN_OP_RELU: case CATNN_OP_GELU:
             if (dst(0)) k::act_backward(s, x, dy, dst(0), nx, tn.kind, !tn.first_writer[0]);
             break;
-        case CATNN_OP_LINEAR: case CATNN_OP_MATMUL: {
+        case CATNN_OP_LINEAR: case CATNN_OP_MATMUL: case CATNN_OP_LM_HEAD: {
             TParam *w = tn.params.begin()->second;
             for (auto &kv : tn.params) if (kv.first != "b") w = kv.second;
             TParam *b = tn.params.count("b") ? tn.params["b"] : nullptr;
@@ -792,7 +828,11 @@ static void train_step(Tr &t) {
     for (auto &tn : t.nodes)
         if (!t.input_ids.count(tn.id)) forward_node(t, tn);
     const int64_t n_out = numel(t.dims[t.out_id]);
-    k::mse(s, t.val.at(t.out_id), t.target, t.grad.at(t.out_id), n_out, t.loss, t.mse_scratch);
+    if (t.classes)
+        k::cross_entropy(s, t.val.at(t.out_id), t.class_ids, t.class_rows, (int)t.vocab, t.grad.at(t.out_id), t.loss,
+                         t.ce_rows);
+    else
+        k::mse(s, t.val.at(t.out_id), t.target, t.grad.at(t.out_id), n_out, t.loss, t.mse_scratch);
     // A node whose output nobody reads receives no cotangent and is skipped,
     // as reference_train skips ids without an entry in `grads`.
     for (auto it = t.nodes.rbegin(); it != t.nodes.rend(); ++it)
@@ -829,6 +869,26 @@ static TParam *find_param(Tr &t, uint32_t node_id, const std::string &port, int6
                   "unknown port " + port + " on interface " + tn.node->name);
     *ncols = pit->second->cols;
     return pit->second;
+}
+
+static void read_cols(Tr &t, const float *src, int64_t rows, int64_t cols, int64_t col0, int64_t ncols,
+                      float *host, int64_t n);
+
+// A parameter-shaped buffer of p (master, gradient or moment) in the
+// graph's layout: columns col0 … col0+ncols, or the whole transpose back
+// when p is held transposed.
+static void read_param_buf(Tr &t, const TParam *p, const float *src, int64_t col0, int64_t ncols, float *host,
+                           int64_t n) {
+    if (!p->transposed) {
+        read_cols(t, src, p->rows, p->cols, col0, ncols, host, n);
+        return;
+    }
+    std::vector<float> tmp((size_t)(p->rows * p->cols));
+    read_cols(t, src, p->rows, p->cols, 0, p->cols, tmp.data(), p->rows * p->cols);
+    CATNN_REQUIRE(n == p->rows * p->cols, CATNN_ERR_SHAPE_MISMATCH,
+                  "host buffer holds " + std::to_string(n) + " values, tensor has " + std::to_string(p->rows * p->cols));
+    for (int64_t r = 0; r < p->rows; ++r)
+        for (int64_t c = 0; c < p->cols; ++c) host[c * p->rows + r] = tmp[(size_t)(r * p->cols + c)];
 }
 
 // Copies rows × ncols starting at column col0 of a [rows, cols] fp32 buffer.
@@ -913,6 +973,8 @@ int catnn_hip_train_set_batch(catnn_hip_trainer *t, const catnn_tensor *input, c
         CATNN_REQUIRE(t && input && target, CATNN_ERR_INVALID_ARGUMENT, "null argument");
         require_device(t->dev);
         hipStream_t s = t->dev->stream;
+        CATNN_REQUIRE(!t->classes, CATNN_ERR_INVALID_ARGUMENT,
+                      "the output is an LmHead: its targets are class ids (catnn_hip_train_set_batch_classes)");
         int64_t ni = 1, nt = 1;
         for (int i = 0; i < input->rank; ++i) ni *= input->dims[i];
         for (int i = 0; i < target->rank; ++i) nt *= target->dims[i];
@@ -924,6 +986,30 @@ int catnn_hip_train_set_batch(catnn_hip_trainer *t, const catnn_tensor *input, c
             CATNN_HIP(hipMemcpyAsync(t->val.at(id), input->data, (size_t)ni * 4, hipMemcpyHostToDevice, s));
         }
         CATNN_HIP(hipMemcpyAsync(t->target, target->data, (size_t)nt * 4, hipMemcpyHostToDevice, s));
+        CATNN_HIP(hipStreamSynchronize(s));
+    });
+}
+
+int catnn_hip_train_set_batch_classes(catnn_hip_trainer *t, const catnn_tensor *input, const uint32_t *ids,
+                                      int64_t n) {
+    return guard([&] {
+        CATNN_REQUIRE(t && input && (ids || n == 0), CATNN_ERR_INVALID_ARGUMENT, "null argument");
+        CATNN_REQUIRE(t->classes, CATNN_ERR_INVALID_ARGUMENT,
+                      "the output is not an LmHead: its target is a tensor (catnn_hip_train_set_batch)");
+        require_device(t->dev);
+        CATNN_REQUIRE(n == t->class_rows, CATNN_ERR_SHAPE_MISMATCH, "ce targets");  // adjoint.rs:126-128
+        for (int64_t r = 0; r < n; ++r)  // adjoint.rs:134-136
+            CATNN_REQUIRE((int64_t)ids[r] < t->vocab, CATNN_ERR_SHAPE_MISMATCH,
+                          "target " + std::to_string(ids[r]) + " >= " + std::to_string(t->vocab));
+        hipStream_t s = t->dev->stream;
+        int64_t ni = 1;
+        for (int i = 0; i < input->rank; ++i) ni *= input->dims[i];
+        for (uint32_t id : t->input_ids) {
+            CATNN_REQUIRE(ni == numel(t->dims[id]) && (input->data || ni == 0), CATNN_ERR_SHAPE_MISMATCH,
+                          "input size");
+            CATNN_HIP(hipMemcpyAsync(t->val.at(id), input->data, (size_t)ni * 4, hipMemcpyHostToDevice, s));
+        }
+        if (n) CATNN_HIP(hipMemcpyAsync(t->class_ids, ids, (size_t)n * 4, hipMemcpyHostToDevice, s));
         CATNN_HIP(hipStreamSynchronize(s));
     });
 }
@@ -955,7 +1041,7 @@ int catnn_hip_train_read_param(catnn_hip_trainer *t, uint32_t node_id, const cha
         require_device(t->dev);
         int64_t col0, ncols;
         TParam *p = find_param(*t, node_id, port, &col0, &ncols);
-        read_cols(*t, p->master, p->rows, p->cols, col0, ncols, host, n);
+        read_param_buf(*t, p, p->master, col0, ncols, host, n);
     });
 }
 
@@ -966,7 +1052,7 @@ int catnn_hip_train_read_grad(catnn_hip_trainer *t, uint32_t node_id, const char
         require_device(t->dev);
         int64_t col0, ncols;
         TParam *p = find_param(*t, node_id, port, &col0, &ncols);
-        read_cols(*t, p->grad, p->rows, p->cols, col0, ncols, host, n);
+        read_param_buf(*t, p, p->grad, col0, ncols, host, n);
     });
 }
 
@@ -979,7 +1065,7 @@ int catnn_hip_train_read_moment(catnn_hip_trainer *t, uint32_t node_id, const ch
         require_device(t->dev);
         int64_t col0, ncols;
         TParam *p = find_param(*t, node_id, port, &col0, &ncols);
-        read_cols(*t, which == 0 ? p->m : p->v, p->rows, p->cols, col0, ncols, host, n);
+        read_param_buf(*t, p, which == 0 ? p->m : p->v, col0, ncols, host, n);
     });
 }
 
@@ -1101,7 +1187,7 @@ int catnn_hip_run_adjoint(catnn_hip_device *dev, const catnn_node *node, const c
                           CATNN_ERR_SHAPE_MISMATCH,
                           "dparams[" + std::to_string(j) + "] (" + pr.first + ") holds " + std::to_string(cap) +
                               " values, the param has " + std::to_string(np));
-            if (np) read_cols(*t, p->grad, p->rows, p->cols, col0, ncols, dparams[j].data, np);
+            if (np) read_param_buf(*t, p, p->grad, col0, ncols, dparams[j].data, np);
             dparams[j].rank = (int32_t)pr.second.dims.size();
             for (size_t r = 0; r < pr.second.dims.size(); ++r) dparams[j].dims[r] = pr.second.dims[r];
             dparams[j].dtype = CATNN_F32;

@@ -522,6 +522,46 @@ __global__ __launch_bounds__(256) void mse_finish_kernel(const float *__restrict
     if (threadIdx.x == 0) *loss = ((ws[0] + ws[1]) + (ws[2] + ws[3])) / (float)n;
 }
 
+// cross_entropy (adjoint.rs:123-145), one block per row of logits
+// [rows, V]: softmax_last (row max, e = exp(x − max), inv = 1/max(Σe, 1e-30),
+// p = e·inv; cpu.rs:31-52), then d = p/rows with 1/rows subtracted at the
+// row's class id, and the row's loss term −ln(max(p_t, 1e-30)).  Ids are
+// checked against V on the host.
+__global__ __launch_bounds__(256) void ce_rows_kernel(const float *__restrict__ logits,
+                                                      const uint32_t *__restrict__ ids, int64_t rows, int V,
+                                                      float *__restrict__ d, float *__restrict__ row_loss) {
+#pragma clang fp contract(off)
+    __shared__ float red[4];
+    const int64_t r = blockIdx.x;
+    const float *x = logits + r * V;
+    float *o = d + r * V;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    float m = -INFINITY;
+    for (int j = threadIdx.x; j < V; j += 256) m = fmaxf(m, x[j]);
+    m = wave_max(m);
+    if (lane == 0) red[wave] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    __syncthreads();
+    float sum = 0.f;
+    for (int j = threadIdx.x; j < V; j += 256) sum += expf(x[j] - m);
+    sum = wave_sum(sum);
+    if (lane == 0) red[wave] = sum;
+    __syncthreads();
+    const float inv = 1.0f / fmaxf((red[0] + red[1]) + (red[2] + red[3]), 1e-30f);
+    const float rf = (float)rows, sub = 1.0f / rf;
+    const int t = (int)ids[r];
+    for (int j = threadIdx.x; j < V; j += 256) {
+        const float p = expf(x[j] - m) * inv;
+        float v = p / rf;
+        if (j == t) {
+            v = v - sub;
+            row_loss[r] = -logf(fmaxf(p, 1e-30f));
+        }
+        o[j] = v;
+    }
+}
+
 // p −= lr·g; pb = bf16(p) when given.  g may have a row stride (packed
 // gradients): element (r, c) of p [rows, cols] reads g[r·ldg + c].  The
 // product and the difference are rounded separately, as Sgd::put does, so
@@ -1038,6 +1078,16 @@ void mse(hipStream_t s, const float *pred, const float *tgt, float *d, int64_t n
     CATNN_REQUIRE(n > 0, CATNN_ERR_SHAPE_MISMATCH, "mse on empty tensors");
     mse_kernel<<<kMseBlocks, 256, 0, s>>>(pred, tgt, d, n, scratch);
     mse_finish_kernel<<<1, 256, 0, s>>>(scratch, kMseBlocks, n, loss);
+    CATNN_HIP(hipGetLastError());
+}
+
+void cross_entropy(hipStream_t s, const float *logits, const uint32_t *ids, int64_t rows, int V, float *d,
+                   float *loss, float *row_loss) {
+    CATNN_REQUIRE(rows > 0 && V > 0, CATNN_ERR_SHAPE_MISMATCH, "cross entropy on empty logits");
+    CATNN_REQUIRE(rows < (1ll << 31), CATNN_ERR_SHAPE_MISMATCH, "cross entropy: too many rows");
+    ce_rows_kernel<<<(unsigned)rows, 256, 0, s>>>(logits, ids, rows, V, d, row_loss);
+    // Σ of the row terms in a fixed order, divided by rows.
+    mse_finish_kernel<<<1, 256, 0, s>>>(row_loss, (int)rows, rows, loss);
     CATNN_HIP(hipGetLastError());
 }
 

@@ -50,6 +50,10 @@ void mse(hipStream_t s, const float *pred, const float *tgt, float *d, int64_t n
          float *scratch);
 void sgd(hipStream_t s, float *p, const float *g, int64_t ldg, int64_t rows, int cols, float lr,
          bf16_t *pb);
+// cross_entropy (adjoint.rs:123-145) of logits [rows, V] against class ids
+// (each < V): d [rows, V] and the mean loss; row_loss holds rows floats.
+void cross_entropy(hipStream_t s, const float *logits, const uint32_t *ids, int64_t rows, int V, float *d,
+                   float *loss, float *row_loss);
 
 // The update morphism of one launch (OptimizerKind, lens/optim.rs:142-145).
 // Adam's bias corrections b1t = 1 − β₁ᵗ and b2t = 1 − β₂ᵗ are computed on

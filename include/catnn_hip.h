@@ -390,7 +390,9 @@ int catnn_hip_program_timings(catnn_hip_program *p, catnn_step_timing *out,
  * (crates/catnn-rt/src/coord.rs:413, :470, :481), which bypass the handler
  * in the reference.  Executable ops: Identity, Linear/MatMul, Relu, Gelu,
  * LayerNorm, Add/ResidualAdd (same length), Attention (causal flag
- * honoured), MoE.  GEMM operands are bf16 (bf16 MFMA, fp32 accumulation);
+ * honoured), MoE, LmHead.  The loss is loss_and_grad's (pipeline.rs:
+ * 430-451): cross-entropy against class ids (adjoint.rs:123-145) when the
+ * output node is an LmHead (TrainTarget::Classes), else MSE.  GEMM operands are bf16 (bf16 MFMA, fp32 accumulation);
  * master weights, the residual stream, norms, router and accumulation are
  * fp32.  All buffers live in one hipMalloc arena planned by place_arena on
  * the reference's training ticks (pipeline.rs:280-284). */
@@ -415,6 +417,13 @@ int catnn_hip_train_free(catnn_hip_trainer *t);
  * MSE target of the last output. */
 int catnn_hip_train_set_batch(catnn_hip_trainer *t, const catnn_tensor *input,
                               const catnn_tensor *target);
+/* The batch of a trainer whose output is an LmHead: `input` as above and
+ * one class id per output row (`n` = rows); a wrong count or an id ≥ vocab
+ * → CATNN_ERR_SHAPE_MISMATCH, as cross_entropy refuses them
+ * (adjoint.rs:126-136).  catnn_hip_train_set_batch on such a trainer, or
+ * this call on another, → CATNN_ERR_INVALID_ARGUMENT. */
+int catnn_hip_train_set_batch_classes(catnn_hip_trainer *t, const catnn_tensor *input,
+                                      const uint32_t *ids, int64_t n);
 /* forward, loss, backward, SGD on the resident batch; `loss` (or NULL:
  * no synchronisation) receives the step's MSE before the update. */
 int catnn_hip_train_step(catnn_hip_trainer *t, float *loss);

@@ -900,6 +900,28 @@ void orc_moe_backward(const float *x, const float *gate, const float *w1s, const
     for (int64_t i = 0; i < T * H; ++i) dx[i] += dxg[(size_t)i];
 }
 
+// cross_entropy, crates/catnn-compile/src/kernel/adjoint.rs:123-145: probs
+// = softmax_last(logits); d = probs with every element of row r divided by
+// rows and 1/rows subtracted at the target; loss = Σ_r −ln(max(p_t, 1e-30))
+// summed in row order, divided by rows.  Returns 0 and writes d and *loss,
+// or −1 (ShapeMismatch) for a target ≥ last.
+int orc_cross_entropy(const float *logits, const uint32_t *targets, int64_t rows, int64_t last, float *d,
+                      float *loss) {
+    orc_softmax_last(logits, d, rows, last);
+    const float rf = (float)rows;
+    float l = 0.0f;
+    for (int64_t r = 0; r < rows; ++r) {
+        const int64_t t = targets[r];
+        if (t >= last) return -1;
+        const float p = std::max(d[r * last + t], 1e-30f);
+        l -= std::log(p);
+        for (int64_t j = 0; j < last; ++j) d[r * last + j] /= rf;
+        d[r * last + t] -= 1.0f / rf;
+    }
+    *loss = l / rf;
+    return 0;
+}
+
 // Sgd::put, crates/catnn-core/src/lens/optim.rs:32-42: p −= lr·g.
 void orc_sgd(float *p, const float *g, int64_t n, float lr) {
     for (int64_t i = 0; i < n; ++i) p[i] -= lr * g[i];

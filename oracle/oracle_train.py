@@ -33,6 +33,7 @@ _SIG = {
     "orc_moe_backward": ([_F, _F, _F, _F, _F, _I64, _I64, _I64, _I64, _I64, _F, _F, _F, _F, _F, _F],
                          None),
     "orc_sgd": ([_F, _F, _I64, ctypes.c_float], None),
+    "orc_cross_entropy": ([_F, ctypes.POINTER(ctypes.c_uint32), _I64, _I64, _F, _F], ctypes.c_int),
     "orc_powi": ([ctypes.c_float, ctypes.c_int32], ctypes.c_float),
     "orc_adam": ([_F, _F, _F, _F, _I64, ctypes.c_uint64, ctypes.c_float, ctypes.c_float, ctypes.c_float,
                   ctypes.c_float], None),
@@ -78,6 +79,30 @@ def mse_loss(pred, target):
     d = np.empty_like(pred)
     loss = _lib.orc_mse_loss(_f(pred), _f(target), pred.size, _f(d))
     return float(loss), d
+
+
+def cross_entropy(logits, targets):
+    """adjoint.rs:123-145: (loss, d) for class ids `targets`, one per row."""
+    logits = _c(logits)
+    last = logits.shape[-1]
+    rows = logits.size // last
+    t = np.ascontiguousarray(targets, np.uint32).reshape(-1)
+    assert t.size == rows, "ce targets"
+    d = np.empty_like(logits)
+    loss = np.zeros(1, np.float32)
+    rc = _lib.orc_cross_entropy(_f(logits), t.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)), rows, last,
+                                _f(d), _f(loss))
+    if rc != 0:
+        raise ValueError("target >= last")
+    return float(loss[0]), d
+
+
+def lm_head_backward(x, w, dy):
+    """The LmHead arm of adjoint_of (adjoint.rs:903-913): linear_backward
+    with wᵀ [H, V]; dW transposed back to [V, H]."""
+    V, H = w.shape
+    dx, dwt, _ = linear_backward(np.asarray(x, np.float32).reshape(-1, H), np.ascontiguousarray(w.T), dy.reshape(-1, V))
+    return dx.reshape(np.shape(x)), np.ascontiguousarray(dwt.T)
 
 
 def layer_norm_backward(x, gamma, dy, eps=1e-6):
@@ -207,6 +232,9 @@ def adjoint_of(node, inputs, output, dy):
         dx, dwq, dwk, dwv, dwo = attention_backward(x, P["wq"], P["wk"], P["wv"], P["wo"], heads, dh, dy,
                                                     causal=bool(node.op.flags & 1))
         return [dx], {"wq": dwq, "wk": dwk, "wv": dwv, "wo": dwo}
+    if kind == "lm_head":
+        dx, dw = lm_head_backward(x, P["w"], dy)
+        return [dx], {"w": dw}
     if kind == "moe":
         E, k, _, _ = node.op.fields
         w1 = np.stack([P[f"e{e}.w1"] for e in range(E)])
@@ -221,10 +249,13 @@ def adjoint_of(node, inputs, output, dy):
 
 
 def train_step(graph, x, target, lr, opt="sgd", adam_states=None):
-    """One step of pipeline::reference_train with MSE and `opt` ("sgd" or
-    "adam"): returns (loss, {node_id: {port: grad}}, {node_id: {port:
-    updated param}}).  For Adam, `adam_states` ({(node_id, port):
-    AdamState}, updated in place) carries the moments between steps."""
+    """One step of pipeline::reference_train with `opt` ("sgd" or "adam"):
+    returns (loss, {node_id: {port: grad}}, {node_id: {port: updated
+    param}}).  The loss is loss_and_grad's (pipeline.rs:446-451): MSE
+    against `target`, or cross-entropy when the output node is an LmHead, in
+    which case `target` holds one class id per row (TrainTarget::Classes).
+    For Adam, `adam_states` ({(node_id, port): AdamState}, updated in place)
+    carries the moments between steps."""
     order = oracle.topo(graph)
     acts = {}
     for nid in order:
@@ -235,7 +266,10 @@ def train_step(graph, x, target, lr, opt="sgd", adam_states=None):
         preds = [e.src for e in graph.edges if e.dst == nid]
         acts[nid] = oracle.eval_node(node, [acts[p] for p in preds])
     out_id = graph.outputs[-1]
-    loss, dy = mse_loss(acts[out_id], target)
+    if graph.nodes[out_id].op.kind == "lm_head":
+        loss, dy = cross_entropy(acts[out_id], target)
+    else:
+        loss, dy = mse_loss(acts[out_id], target)
     grads = {out_id: dy.reshape(acts[out_id].shape)}
     dparams = {}
     for nid in reversed(order):
