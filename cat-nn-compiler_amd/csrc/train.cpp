@@ -230,7 +230,7 @@ static void plan_trainer(Tr &t) {
                 case CATNN_OP_IDENTITY: case CATNN_OP_RESHAPE: case CATNN_OP_TRANSPOSE:
                 case CATNN_OP_RELU: case CATNN_OP_GELU: case CATNN_OP_LINEAR: case CATNN_OP_MATMUL:
                 case CATNN_OP_LAYER_NORM: case CATNN_OP_ATTENTION: case CATNN_OP_MOE:
-                case CATNN_OP_LM_HEAD:
+                case CATNN_OP_LM_HEAD: case CATNN_OP_RMS_NORM:
                     break;
                 case CATNN_OP_ADD: case CATNN_OP_RESIDUAL_ADD:
                     CATNN_REQUIRE(tn.ins.size() != 2 || numel(tn.in_dims[0]) == numel(tn.in_dims[1]),
@@ -385,6 +385,15 @@ static void plan_trainer(Tr &t) {
                 scratch(tn, "dybt", (uint64_t)(M * N) * 2);
                 scratch(tn, "colsum", k::colsum_scratch_bytes(M, (int)N));
                 scratch(tn, "wparts", wparts_bytes(K, N, M));
+                break;
+            }
+            case CATNN_OP_RMS_NORM: {
+                const int64_t C = x.back(), R = numel(x) / C;
+                const HostTensor *w = host(nd, "w");
+                CATNN_REQUIRE(w->numel() == C, CATNN_ERR_SHAPE_MISMATCH, "rmsnorm w");  // adjoint.rs:155-157
+                add_param(tn, "w", 1, C, false, false, w->data);
+                scratch(tn, "prod", (uint64_t)(R * C) * 4);
+                scratch(tn, "colsum", k::colsum_scratch_bytes(R, (int)C));
                 break;
             }
             case CATNN_OP_LM_HEAD: {
@@ -597,6 +606,11 @@ static void forward_node(Tr &t, TNode &tn) {
             k::gemm_bf16_launch(s, p);
             break;
         }
+        case CATNN_OP_RMS_NORM: {
+            const int64_t C = xd.back();
+            k::rms_norm_f32(s, x, tn.params["w"]->master, y, nx / C, C, (float)nd.op.a[0] * 1e-6f);
+            break;
+        }
         case CATNN_OP_LAYER_NORM: {
             const int64_t C = xd.back();
             const float eps = (float)nd.op.a[0] * 1e-6f;
@@ -717,6 +731,14 @@ static void backward_node(Tr &t, TNode &tn) {
             k::transpose_bf16(s, x3, 3 * K, nullptr, 1, (int)M, (int)K, xbt, M);  // hi part of x
             gemm_nt(s, xbt, M, dybt, M, (int)K, (int)N, (int)M, w->grad, N, false, (float *)tn.B("wparts"));
             if (b) k::colsum(s, dy, M, (int)N, b->grad, false, (float *)tn.B("colsum"));
+            break;
+        }
+        case CATNN_OP_RMS_NORM: {
+            const int64_t C = xd.back();
+            float *dx = dst(0);
+            k::rms_backward(s, x, tn.params["w"]->master, dy, dx, dx && !tn.first_writer[0], tn.params["w"]->grad,
+                            nx / C, (int)C, (float)nd.op.a[0] * 1e-6f, (float *)tn.B("prod"),
+                            (float *)tn.B("colsum"));
             break;
         }
         case CATNN_OP_LAYER_NORM: {

@@ -562,6 +562,39 @@ __global__ __launch_bounds__(256) void ce_rows_kernel(const float *__restrict__ 
     }
 }
 
+// rmsnorm_backward (adjoint.rs:147-198), one wavefront per row: ms and
+// dinv = Σ dy·x·w by wave reductions, inv = 1/√(ms+eps), dms =
+// dinv·(−0.5)·(ms+eps)^(−1.5); dx = dy·inv·w + dms·(2x/n) (stored, or added
+// to what dx holds), and the row's dw terms dy·x·inv into prod [rows, cols]
+// for the column sum.
+__global__ __launch_bounds__(256) void rms_bwd_kernel(const float *__restrict__ x, const float *__restrict__ w,
+                                                      const float *__restrict__ dy, float *__restrict__ dx,
+                                                      int acc_dx, float *__restrict__ prod, int64_t rows, int cols,
+                                                      float eps) {
+#pragma clang fp contract(off)
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const float *xr = x + row * cols, *yr = dy + row * cols;
+    float ss = 0.f, dinv = 0.f;
+    for (int c = lane; c < cols; c += 64) {
+        const float xv = xr[c];
+        ss += xv * xv;
+        dinv += yr[c] * xv * w[c];
+    }
+    ss = wave_sum(ss);
+    dinv = wave_sum(dinv);
+    const float n = (float)cols, ms = ss / n, inv = 1.0f / sqrtf(ms + eps);
+    const float dms = dinv * (-0.5f) * powf(ms + eps, -1.5f);
+    for (int c = lane; c < cols; c += 64) {
+        const float xv = xr[c], d = yr[c];
+        const float o = d * inv * w[c] + dms * (2.0f * xv / n);
+        const int64_t e = row * cols + c;
+        if (dx) dx[e] = acc_dx ? dx[e] + o : o;
+        prod[e] = d * xv * inv;
+    }
+}
+
 // p −= lr·g; pb = bf16(p) when given.  g may have a row stride (packed
 // gradients): element (r, c) of p [rows, cols] reads g[r·ldg + c].  The
 // product and the difference are rounded separately, as Sgd::put does, so
@@ -1079,6 +1112,16 @@ void mse(hipStream_t s, const float *pred, const float *tgt, float *d, int64_t n
     mse_kernel<<<kMseBlocks, 256, 0, s>>>(pred, tgt, d, n, scratch);
     mse_finish_kernel<<<1, 256, 0, s>>>(scratch, kMseBlocks, n, loss);
     CATNN_HIP(hipGetLastError());
+}
+
+void rms_backward(hipStream_t s, const float *x, const float *w, const float *dy, float *dx, bool accumulate,
+                  float *dw, int64_t rows, int cols, float eps, float *prod, float *colsum_scratch) {
+    if (rows <= 0 || cols <= 0) return;
+    CATNN_REQUIRE((rows + 3) / 4 < (1ll << 31), CATNN_ERR_SHAPE_MISMATCH, "rmsnorm backward: too many rows");
+    rms_bwd_kernel<<<(unsigned)((rows + 3) / 4), 256, 0, s>>>(x, w, dy, dx, accumulate ? 1 : 0, prod, rows, cols,
+                                                                eps);
+    CATNN_HIP(hipGetLastError());
+    colsum(s, prod, rows, cols, dw, false, colsum_scratch);
 }
 
 void cross_entropy(hipStream_t s, const float *logits, const uint32_t *ids, int64_t rows, int V, float *d,

@@ -50,6 +50,11 @@ void mse(hipStream_t s, const float *pred, const float *tgt, float *d, int64_t n
          float *scratch);
 void sgd(hipStream_t s, float *p, const float *g, int64_t ldg, int64_t rows, int cols, float lr,
          bf16_t *pb);
+// rmsnorm_backward (adjoint.rs:147-198) of rows × cols: dx (=, or += when
+// accumulate; null: not computed) and dw = Σ_rows dy·x·inv via
+// prod [rows, cols] and colsum's scratch (colsum_scratch_bytes).
+void rms_backward(hipStream_t s, const float *x, const float *w, const float *dy, float *dx, bool accumulate,
+                  float *dw, int64_t rows, int cols, float eps, float *prod, float *colsum_scratch);
 // cross_entropy (adjoint.rs:123-145) of logits [rows, V] against class ids
 // (each < V): d [rows, V] and the mean loss; row_loss holds rows floats.
 void cross_entropy(hipStream_t s, const float *logits, const uint32_t *ids, int64_t rows, int V, float *d,

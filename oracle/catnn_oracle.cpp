@@ -689,6 +689,29 @@ float orc_mse_loss(const float *pred, const float *target, int64_t n, float *d) 
 }
 
 // layer_norm_backward, adjoint.rs:530-577.
+// rmsnorm_backward, adjoint.rs:147-198: per row ms = Σx²/n (sequential),
+// inv = 1/√(ms+eps); dw_i += dy_i·x_i·inv and dinv += dy_i·x_i·w_i in column
+// order; dms = dinv·(−0.5)·(ms+eps)^(−1.5); dx_i = dy_i·inv·w_i + dms·(2·x_i/n).
+void orc_rmsnorm_backward(const float *x, const float *w, const float *dy, int64_t rows, int64_t last, float eps,
+                          float *dx, float *dw) {
+    const float n = (float)last;
+    for (int64_t i = 0; i < last; ++i) dw[i] = 0.0f;
+    for (int64_t r = 0; r < rows; ++r) {
+        const float *xr = x + r * last, *yr = dy + r * last;
+        float ss = 0.0f;
+        for (int64_t i = 0; i < last; ++i) ss += xr[i] * xr[i];
+        const float ms = ss / n;
+        const float inv = 1.0f / std::sqrt(ms + eps);
+        float dinv = 0.0f;
+        for (int64_t i = 0; i < last; ++i) {
+            dw[i] += yr[i] * xr[i] * inv;
+            dinv += yr[i] * xr[i] * w[i];
+        }
+        const float dms = dinv * (-0.5f) * std::pow(ms + eps, -1.5f);
+        for (int64_t i = 0; i < last; ++i) dx[r * last + i] = yr[i] * inv * w[i] + dms * (2.0f * xr[i] / n);
+    }
+}
+
 void orc_layer_norm_backward(const float *x, const float *gamma, const float *dy, int64_t rows,
                              int64_t last, float eps, float *dx, float *dgamma, float *dbeta) {
     std::fill(dgamma, dgamma + last, 0.0f);

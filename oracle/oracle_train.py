@@ -33,6 +33,7 @@ _SIG = {
     "orc_moe_backward": ([_F, _F, _F, _F, _F, _I64, _I64, _I64, _I64, _I64, _F, _F, _F, _F, _F, _F],
                          None),
     "orc_sgd": ([_F, _F, _I64, ctypes.c_float], None),
+    "orc_rmsnorm_backward": ([_F, _F, _F, _I64, _I64, ctypes.c_float, _F, _F], None),
     "orc_cross_entropy": ([_F, ctypes.POINTER(ctypes.c_uint32), _I64, _I64, _F, _F], ctypes.c_int),
     "orc_powi": ([ctypes.c_float, ctypes.c_int32], ctypes.c_float),
     "orc_adam": ([_F, _F, _F, _F, _I64, ctypes.c_uint64, ctypes.c_float, ctypes.c_float, ctypes.c_float,
@@ -103,6 +104,15 @@ def lm_head_backward(x, w, dy):
     V, H = w.shape
     dx, dwt, _ = linear_backward(np.asarray(x, np.float32).reshape(-1, H), np.ascontiguousarray(w.T), dy.reshape(-1, V))
     return dx.reshape(np.shape(x)), np.ascontiguousarray(dwt.T)
+
+
+def rmsnorm_backward(x, w, dy, eps):
+    """adjoint.rs:147-198: (dx, dw)."""
+    x, w, dy = _c(x), _c(w), _c(dy)
+    last = x.shape[-1]
+    dx, dw = np.empty_like(x), np.empty(last, np.float32)
+    _lib.orc_rmsnorm_backward(_f(x), _f(w), _f(dy), x.size // last, last, np.float32(eps), _f(dx), _f(dw))
+    return dx, dw
 
 
 def layer_norm_backward(x, gamma, dy, eps=1e-6):
@@ -232,6 +242,10 @@ def adjoint_of(node, inputs, output, dy):
         dx, dwq, dwk, dwv, dwo = attention_backward(x, P["wq"], P["wk"], P["wv"], P["wo"], heads, dh, dy,
                                                     causal=bool(node.op.flags & 1))
         return [dx], {"wq": dwq, "wk": dwk, "wv": dwv, "wo": dwo}
+    if kind == "rms_norm":
+        eps = np.float32(node.op.fields[0]) * np.float32(1e-6)
+        dx, dw = rmsnorm_backward(x, P["w"], dy, eps)
+        return [dx], {"w": dw}
     if kind == "lm_head":
         dx, dw = lm_head_backward(x, P["w"], dy)
         return [dx], {"w": dw}

@@ -2,8 +2,9 @@
 DeviceHandler.adjoint_of), against the oracle's restatement of
 crates/catnn-compile/src/kernel/adjoint.rs:762-951 on the same seeded inputs
 and cotangent.  Ops whose adjoint the device computes in fp32 (Identity,
-ReLU, GELU, Add/ResidualAdd, LayerNorm) are held to the fp32 bar (rel L2
-1e-4); ops with GEMMs (Linear, Attention, MoE) run them on bf16 MFMA with
+ReLU, GELU, Add/ResidualAdd, LayerNorm, RMSNorm) are held to the fp32 bar
+(rel L2 1e-4); ops with GEMMs (Linear, Attention, MoE; LmHead in
+test_gpu_classes.py) run them on bf16 MFMA with
 fp32 accumulation, as the training step does, and are held to the bf16 bar
 (1e-2)."""
 import numpy as np
@@ -80,6 +81,14 @@ def test_layer_norm(device, rows, cols):
     r = np.random.default_rng(cols)
     node = IrNode(2, "ln", OpenOp.layer_norm(1), TensorType.f32([rows, cols]),
                   {"gamma": _t(1 + 0.1 * r.standard_normal(cols)), "beta": _t(0.1 * r.standard_normal(cols))})
+    _check(device, node, [r.standard_normal((rows, cols)) * 2 + 0.5], FP32_TOL)
+
+
+@pytest.mark.parametrize("rows,cols", [(64, 1024), (9, 100)])
+def test_rms_norm(device, rows, cols):
+    r = np.random.default_rng(cols + 1)
+    node = IrNode(2, "rms", OpenOp.rms_norm(10), TensorType.f32([rows, cols]),
+                  {"w": _t(1 + 0.1 * r.standard_normal(cols))})
     _check(device, node, [r.standard_normal((rows, cols)) * 2 + 0.5], FP32_TOL)
 
 

@@ -22,12 +22,16 @@ def _t(a):
     return Tensor.from_numpy(np.ascontiguousarray(a, np.float32))
 
 
-def _lm_graph(r, B, S, H, F, V):
+def _lm_graph(r, B, S, H, F, V, norm="layer_norm"):
     g = IrGraph("lm_classes")
     T = B * S
     g.add_node(IrNode(0, "in", OpenOp.identity(), TensorType.f32([B, S, H])))
-    g.add_node(IrNode(1, "ln", OpenOp.layer_norm(1), TensorType.f32([B, S, H]),
-                      {"gamma": _t(1 + 0.1 * r.standard_normal(H)), "beta": _t(0.1 * r.standard_normal(H))}))
+    if norm == "layer_norm":
+        g.add_node(IrNode(1, "ln", OpenOp.layer_norm(1), TensorType.f32([B, S, H]),
+                          {"gamma": _t(1 + 0.1 * r.standard_normal(H)), "beta": _t(0.1 * r.standard_normal(H))}))
+    else:  # the Mixtral decoder's norm
+        g.add_node(IrNode(1, "rms", OpenOp.rms_norm(10), TensorType.f32([B, S, H]),
+                          {"w": _t(1 + 0.1 * r.standard_normal(H))}))
     g.add_node(IrNode(2, "fc", OpenOp.linear(H, F), TensorType.f32([B, S, F]),
                       {"w": _t(r.standard_normal((H, F)) / np.sqrt(H)), "b": _t(0.1 * r.standard_normal(F))}))
     g.add_node(IrNode(3, "act", OpenOp.gelu(), TensorType.f32([B, S, F])))
@@ -39,10 +43,13 @@ def _lm_graph(r, B, S, H, F, V):
     return g, T
 
 
-@pytest.mark.parametrize("B,S,H,F,V", [(2, 64, 128, 256, 1000), (1, 64, 128, 128, 32000), (1, 37, 64, 96, 77)])
-def test_classes_step_follows_the_reference(device, B, S, H, F, V):
+@pytest.mark.parametrize("B,S,H,F,V,norm", [(2, 64, 128, 256, 1000, "layer_norm"),
+                                            (1, 64, 128, 128, 32000, "layer_norm"),
+                                            (1, 37, 64, 96, 77, "layer_norm"),
+                                            (2, 64, 128, 256, 1000, "rms_norm")])
+def test_classes_step_follows_the_reference(device, B, S, H, F, V, norm):
     r = np.random.default_rng(V)
-    g, T = _lm_graph(r, B, S, H, F, V)
+    g, T = _lm_graph(r, B, S, H, F, V, norm)
     x = r.standard_normal((B, S, H)).astype(np.float32)
     ids = r.integers(0, V, T).astype(np.uint32)
     lr = 0.05
