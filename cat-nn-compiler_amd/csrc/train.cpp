@@ -232,6 +232,11 @@ static void plan_trainer(Tr &t) {
                 case CATNN_OP_LAYER_NORM: case CATNN_OP_ATTENTION: case CATNN_OP_MOE:
                 case CATNN_OP_LM_HEAD: case CATNN_OP_RMS_NORM:
                     break;
+                case CATNN_OP_MIX:
+                    CATNN_REQUIRE(tn.ins.size() == 2, CATNN_ERR_WIRING, "mix adjoint needs two inputs");
+                    CATNN_REQUIRE(numel(tn.in_dims[0]) == numel(tn.in_dims[1]), CATNN_ERR_SHAPE_MISMATCH,
+                                  "mix operands differ");
+                    break;
                 case CATNN_OP_ADD: case CATNN_OP_RESIDUAL_ADD:
                     CATNN_REQUIRE(tn.ins.size() != 2 || numel(tn.in_dims[0]) == numel(tn.in_dims[1]),
                                   CATNN_ERR_UNSUPPORTED,
@@ -385,6 +390,14 @@ static void plan_trainer(Tr &t) {
                 scratch(tn, "dybt", (uint64_t)(M * N) * 2);
                 scratch(tn, "colsum", k::colsum_scratch_bytes(M, (int)N));
                 scratch(tn, "wparts", wparts_bytes(K, N, M));
+                break;
+            }
+            case CATNN_OP_MIX: {
+                if (const HostTensor *g = nd.param("gate")) {
+                    CATNN_REQUIRE(g->numel() == 1, CATNN_ERR_SHAPE_MISMATCH, "mix gate");
+                    add_param(tn, "gate", 1, 1, false, false, g->data);
+                }
+                scratch(tn, "parts", k::mix_scratch_bytes());
                 break;
             }
             case CATNN_OP_RMS_NORM: {
@@ -606,6 +619,11 @@ static void forward_node(Tr &t, TNode &tn) {
             k::gemm_bf16_launch(s, p);
             break;
         }
+        case CATNN_OP_MIX: {
+            const float *gate = tn.params.count("gate") ? tn.params["gate"]->master : nullptr;
+            k::mix_f32(s, x, t.val.at(tn.ins[1]), gate, y, nx);
+            break;
+        }
         case CATNN_OP_RMS_NORM: {
             const int64_t C = xd.back();
             k::rms_norm_f32(s, x, tn.params["w"]->master, y, nx / C, C, (float)nd.op.a[0] * 1e-6f);
@@ -731,6 +749,13 @@ static void backward_node(Tr &t, TNode &tn) {
             k::transpose_bf16(s, x3, 3 * K, nullptr, 1, (int)M, (int)K, xbt, M);  // hi part of x
             gemm_nt(s, xbt, M, dybt, M, (int)K, (int)N, (int)M, w->grad, N, false, (float *)tn.B("wparts"));
             if (b) k::colsum(s, dy, M, (int)N, b->grad, false, (float *)tn.B("colsum"));
+            break;
+        }
+        case CATNN_OP_MIX: {
+            TParam *g = tn.params.count("gate") ? tn.params["gate"] : nullptr;
+            k::mix_backward(s, x, t.val.at(tn.ins[1]), g ? g->master : nullptr, dy, dst(0),
+                            dst(0) && !tn.first_writer[0], dst(1), dst(1) && !tn.first_writer[1], nx,
+                            g ? g->grad : nullptr, (float *)tn.B("parts"));
             break;
         }
         case CATNN_OP_RMS_NORM: {

@@ -595,6 +595,48 @@ __global__ __launch_bounds__(256) void rms_bwd_kernel(const float *__restrict__ 
     }
 }
 
+// mix_backward (deepseek.rs:241-258) with σ = σ(gate[0]) (gate null: 0):
+// da = dy·σ and db = dy·(1 − σ), each stored or added (null: skipped), and
+// per-block partial sums of (a − b)·dy for the gate.
+__global__ __launch_bounds__(256) void mix_bwd_kernel(const float *__restrict__ a, const float *__restrict__ b,
+                                                      const float *__restrict__ gate, const float *__restrict__ dy,
+                                                      float *da, int acc_a, float *db, int acc_b, int64_t n,
+                                                      float *__restrict__ parts) {
+#pragma clang fp contract(off)
+    __shared__ float ws[4];
+    const float g = gate ? gate[0] : 0.f;
+    const float sg = 1.0f / (1.0f + expf(-g)), rs = 1.0f - sg;
+    float acc = 0.f;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+        const float d = dy[i];
+        if (da) da[i] = acc_a ? da[i] + d * sg : d * sg;
+        if (db) db[i] = acc_b ? db[i] + d * rs : d * rs;
+        acc += (a[i] - b[i]) * d;
+    }
+    acc = wave_sum(acc);
+    if ((threadIdx.x & 63) == 0) ws[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) parts[blockIdx.x] = (ws[0] + ws[1]) + (ws[2] + ws[3]);
+}
+
+// dg = σ(1 − σ)·Σ parts, the parts added in a fixed order.
+__global__ __launch_bounds__(256) void mix_bwd_finish_kernel(const float *__restrict__ parts, int nb,
+                                                             const float *__restrict__ gate, float *__restrict__ dg) {
+#pragma clang fp contract(off)
+    __shared__ float ws[4];
+    float s = 0.f;
+    for (int i = threadIdx.x; i < nb; i += 256) s += parts[i];
+    s = wave_sum(s);
+    if ((threadIdx.x & 63) == 0) ws[threadIdx.x >> 6] = s;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const float g = gate ? gate[0] : 0.f;
+        const float sg = 1.0f / (1.0f + expf(-g));
+        dg[0] = ((ws[0] + ws[1]) + (ws[2] + ws[3])) * (sg * (1.0f - sg));
+    }
+}
+
 // p −= lr·g; pb = bf16(p) when given.  g may have a row stride (packed
 // gradients): element (r, c) of p [rows, cols] reads g[r·ldg + c].  The
 // product and the difference are rounded separately, as Sgd::put does, so
@@ -1122,6 +1164,16 @@ void rms_backward(hipStream_t s, const float *x, const float *w, const float *dy
                                                                 eps);
     CATNN_HIP(hipGetLastError());
     colsum(s, prod, rows, cols, dw, false, colsum_scratch);
+}
+
+uint64_t mix_scratch_bytes() { return (uint64_t)kMseBlocks * 4; }
+
+void mix_backward(hipStream_t s, const float *a, const float *b, const float *gate, const float *dy, float *da,
+                  bool acc_a, float *db, bool acc_b, int64_t n, float *dgate, float *parts) {
+    if (n <= 0) return;
+    mix_bwd_kernel<<<kMseBlocks, 256, 0, s>>>(a, b, gate, dy, da, acc_a ? 1 : 0, db, acc_b ? 1 : 0, n, parts);
+    if (dgate) mix_bwd_finish_kernel<<<1, 256, 0, s>>>(parts, kMseBlocks, gate, dgate);
+    CATNN_HIP(hipGetLastError());
 }
 
 void cross_entropy(hipStream_t s, const float *logits, const uint32_t *ids, int64_t rows, int V, float *d,

@@ -55,6 +55,12 @@ void sgd(hipStream_t s, float *p, const float *g, int64_t ldg, int64_t rows, int
 // prod [rows, cols] and colsum's scratch (colsum_scratch_bytes).
 void rms_backward(hipStream_t s, const float *x, const float *w, const float *dy, float *dx, bool accumulate,
                   float *dw, int64_t rows, int cols, float eps, float *prod, float *colsum_scratch);
+// mix_backward (deepseek.rs:241-258) over n values: da, db (= or +=, null:
+// skipped) and, when dgate is given, the gate's cotangent; parts holds
+// mix_scratch_bytes().
+uint64_t mix_scratch_bytes();
+void mix_backward(hipStream_t s, const float *a, const float *b, const float *gate, const float *dy, float *da,
+                  bool acc_a, float *db, bool acc_b, int64_t n, float *dgate, float *parts);
 // cross_entropy (adjoint.rs:123-145) of logits [rows, V] against class ids
 // (each < V): d [rows, V] and the mean loss; row_loss holds rows floats.
 void cross_entropy(hipStream_t s, const float *logits, const uint32_t *ids, int64_t rows, int V, float *d,

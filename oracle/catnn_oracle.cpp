@@ -617,6 +617,20 @@ void orc_mix(const float *a, const float *b, float gate, int64_t n, float *y) {
     for (int64_t i = 0; i < n; ++i) y[i] = s * a[i] + (1.0f - s) * b[i];
 }
 
+// deepseek::mix_backward, deepseek.rs:241-258: da = dy·σ, db = dy·(1 − σ),
+// dg = σ(1 − σ)·Σ (a − b)·dy summed in index order.  Returns dg.
+float orc_mix_backward(const float *a, const float *b, float gate, const float *dy, int64_t n, float *da,
+                       float *db) {
+    const float s = 1.0f / (1.0f + std::exp(-gate));
+    float dg = 0.0f;
+    for (int64_t i = 0; i < n; ++i) {
+        da[i] = dy[i] * s;
+        db[i] = dy[i] * (1.0f - s);
+        dg += (a[i] - b[i]) * dy[i];
+    }
+    return dg * (s * (1.0f - s));
+}
+
 }  // extern "C"
 
 // ============================================================ adjoint.rs

@@ -34,6 +34,7 @@ _SIG = {
                          None),
     "orc_sgd": ([_F, _F, _I64, ctypes.c_float], None),
     "orc_rmsnorm_backward": ([_F, _F, _F, _I64, _I64, ctypes.c_float, _F, _F], None),
+    "orc_mix_backward": ([_F, _F, ctypes.c_float, _F, _I64, _F, _F], ctypes.c_float),
     "orc_cross_entropy": ([_F, ctypes.POINTER(ctypes.c_uint32), _I64, _I64, _F, _F], ctypes.c_int),
     "orc_powi": ([ctypes.c_float, ctypes.c_int32], ctypes.c_float),
     "orc_adam": ([_F, _F, _F, _F, _I64, ctypes.c_uint64, ctypes.c_float, ctypes.c_float, ctypes.c_float,
@@ -113,6 +114,14 @@ def rmsnorm_backward(x, w, dy, eps):
     dx, dw = np.empty_like(x), np.empty(last, np.float32)
     _lib.orc_rmsnorm_backward(_f(x), _f(w), _f(dy), x.size // last, last, np.float32(eps), _f(dx), _f(dw))
     return dx, dw
+
+
+def mix_backward(a, b, gate, dy):
+    """deepseek.rs:241-258: (da, db, dg)."""
+    a, b, dy = _c(a), _c(b), _c(dy)
+    da, db = np.empty_like(a), np.empty_like(b)
+    dg = _lib.orc_mix_backward(_f(a), _f(b), np.float32(gate), _f(dy), a.size, _f(da), _f(db))
+    return da, db, float(dg)
 
 
 def layer_norm_backward(x, gamma, dy, eps=1e-6):
@@ -242,6 +251,11 @@ def adjoint_of(node, inputs, output, dy):
         dx, dwq, dwk, dwv, dwo = attention_backward(x, P["wq"], P["wk"], P["wv"], P["wo"], heads, dh, dy,
                                                     causal=bool(node.op.flags & 1))
         return [dx], {"wq": dwq, "wk": dwk, "wv": dwv, "wo": dwo}
+    if kind == "mix":
+        # adjoint.rs:918-927: the gate cotangent is reported as a [1] tensor.
+        g = float(P["gate"].reshape(-1)[0]) if "gate" in P else 0.0
+        da, db, dg = mix_backward(x, inputs[1], g, dy)
+        return [da, db], {"gate": np.array([dg], np.float32)}
     if kind == "rms_norm":
         eps = np.float32(node.op.fields[0]) * np.float32(1e-6)
         dx, dw = rmsnorm_backward(x, P["w"], dy, eps)

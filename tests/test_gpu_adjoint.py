@@ -2,7 +2,7 @@
 DeviceHandler.adjoint_of), against the oracle's restatement of
 crates/catnn-compile/src/kernel/adjoint.rs:762-951 on the same seeded inputs
 and cotangent.  Ops whose adjoint the device computes in fp32 (Identity,
-ReLU, GELU, Add/ResidualAdd, LayerNorm, RMSNorm) are held to the fp32 bar
+ReLU, GELU, Add/ResidualAdd, LayerNorm, RMSNorm, Mix) are held to the fp32 bar
 (rel L2 1e-4); ops with GEMMs (Linear, Attention, MoE; LmHead in
 test_gpu_classes.py) run them on bf16 MFMA with
 fp32 accumulation, as the training step does, and are held to the bf16 bar
@@ -12,7 +12,7 @@ import pytest
 
 import oracle
 import oracle_train as ot
-from catnn_amd import CatError, DeviceHandler, IrNode, OpenOp, Tensor, TensorType
+from catnn_amd import CatError, DeviceHandler, IrGraph, IrNode, OpenOp, Tensor, TensorType, Trainer
 from conftest import rel_l2
 
 pytestmark = pytest.mark.gpu
@@ -90,6 +90,45 @@ def test_rms_norm(device, rows, cols):
     node = IrNode(2, "rms", OpenOp.rms_norm(10), TensorType.f32([rows, cols]),
                   {"w": _t(1 + 0.1 * r.standard_normal(cols))})
     _check(device, node, [r.standard_normal((rows, cols)) * 2 + 0.5], FP32_TOL)
+
+
+@pytest.mark.parametrize("gate", [None, 0.7])
+def test_mix(device, gate):
+    r = np.random.default_rng(6)
+    params = {} if gate is None else {"gate": _t([gate])}
+    node = IrNode(3, "mix", OpenOp.mix(), TensorType.f32([5, 300]), params)
+    _check(device, node, [r.standard_normal((5, 300)), r.standard_normal((5, 300))], FP32_TOL)
+
+
+def test_mix_graph_step(device):
+    # in → relu, gelu → mix(relu, gelu) with a trained gate; the gate's and
+    # the input path's cotangents through a whole step, against the fp32 step.
+    r = np.random.default_rng(7)
+    g = IrGraph("mix")
+    ty = TensorType.f32([16, 64])
+    g.add_node(IrNode(0, "in", OpenOp.identity(), ty))
+    g.add_node(IrNode(1, "fc", OpenOp.linear(64, 64), ty,
+                      {"w": _t(r.standard_normal((64, 64)) / 8), "b": _t(r.standard_normal(64) * 0.1)}))
+    g.add_node(IrNode(2, "a", OpenOp.relu(), ty))
+    g.add_node(IrNode(3, "b", OpenOp.gelu(), ty))
+    g.add_node(IrNode(4, "mix", OpenOp.mix(), ty, {"gate": _t([0.3])}))
+    for a, b in ((0, 1), (1, 2), (1, 3), (2, 4), (3, 4)):
+        g.add_edge(a, b)
+    g.inputs, g.outputs = [0], [4]
+    x = r.standard_normal((16, 64)).astype(np.float32)
+    tgt = r.standard_normal((16, 64)).astype(np.float32)
+    tr = Trainer(device, g, 0.05)
+    tr.set_batch(_t(x), _t(tgt))
+    loss = tr.step()
+    loss_o, grads_o, _ = ot.train_step(g, x, tgt, 0.05)
+    assert abs(loss - loss_o) <= 2e-3 * max(1.0, abs(loss_o))
+    for nid, dp in grads_o.items():
+        for port, go in dp.items():
+            shape = tuple(g.nodes[nid].params[port].ty.shape)
+            e = rel_l2(tr.grad(nid, port, shape), np.asarray(go).reshape(shape))
+            print(f"  grad {g.nodes[nid].name}.{port}: {e:.2e}")
+            assert e < BF16_TOL, (nid, port, e)
+    tr.free()
 
 
 @pytest.mark.parametrize("causal", [True, False])

@@ -1,5 +1,6 @@
 """Pins the oracle's rmsnorm_backward (crates/catnn-compile/src/kernel/
-adjoint.rs:147-198) on the CPU against central finite differences of
+adjoint.rs:147-198) and mix_backward (kernel/deepseek.rs:241-258; at the
+end) on the CPU.  rmsnorm_backward against central finite differences of
 L = ⟨dy, rmsnorm(x, w)⟩ in float64 (independent of the closed form: a
 dropped term, a wrong power or a swapped operand fails it), and against
 the closed form dx = inv·(w⊙dy) − x·inv³·Σ(w⊙dy⊙x)/n, dw = Σ_rows dy⊙x·inv."""
@@ -50,3 +51,19 @@ def test_against_closed_form_at_width_4096():
     want_dx = inv * w64 * d64 - x64 * inv ** 3 * (w64 * d64 * x64).sum(axis=1, keepdims=True) / cols
     assert rel_l2(dx, want_dx) < 1e-5
     assert rel_l2(dw, (d64 * x64 * inv).sum(axis=0)) < 1e-5
+
+
+def test_mix_backward_against_float64():
+    # deepseek.rs:241-258: da = σ·dy, db = (1 − σ)·dy, dg = σ(1 − σ)·Σ(a − b)·dy.
+    r = np.random.default_rng(5)
+    a, b, dy = (r.standard_normal(1000).astype(np.float32) for _ in range(3))
+    g = 0.7
+    da, db, dg = ot.mix_backward(a, b, g, dy)
+    s = 1 / (1 + np.exp(-np.float64(np.float32(g))))
+    assert rel_l2(da, s * dy) < 1e-6 and rel_l2(db, (1 - s) * dy) < 1e-6
+    want = s * (1 - s) * ((a.astype(np.float64) - b) * dy).sum()
+    assert abs(dg - want) < 1e-5 * max(1.0, abs(want))
+    # finite differences of ⟨dy, σ(g)a + (1 − σ(g))b⟩ in the gate
+    f = lambda gg: (dy.astype(np.float64) * (a / (1 + np.exp(-gg)) + b * (1 - 1 / (1 + np.exp(-gg))))).sum()
+    h = 1e-6
+    assert abs(dg - (f(np.float64(np.float32(g)) + h) - f(np.float64(np.float32(g)) - h)) / (2 * h)) < 1e-4
