@@ -159,6 +159,61 @@ __global__ __launch_bounds__(256) void embedding_pair_kernel(const float *__rest
     }
 }
 
+// embedding_backward (adjoint.rs:187-197): dW [vocab, hidden] gets, in row
+// id_t, Σ_t dy[t] in token order.  First the ids as integers (the forward's
+// conversion; an id ≥ vocab, which the forward refuses, becomes −1) and a
+// mark per vocabulary row that occurs; then one block per row: unmarked
+// rows are zeroed, marked rows add their tokens' cotangent rows in token
+// order from zero — the reference's order, bit for bit, with no atomics.
+__global__ void fill_int_kernel(int *__restrict__ p, int v, int64_t n) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) p[i] = v;
+}
+
+__global__ void embedding_bwd_ids_kernel(const float *__restrict__ ids, int64_t n, int64_t vocab,
+                                         int *__restrict__ idi, int *__restrict__ hit) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= n) return;
+    const int64_t id = token_id(ids[t]);
+    if (id < vocab) {
+        idi[t] = (int)id;
+        hit[id] = 1;
+    } else {
+        idi[t] = -1;
+    }
+}
+
+__global__ __launch_bounds__(256) void embedding_bwd_rows_kernel(const int *__restrict__ idi, int64_t n,
+                                                                 const float *__restrict__ dy, int64_t hidden,
+                                                                 int64_t vocab, const int *__restrict__ hit,
+                                                                 float *__restrict__ dw) {
+#pragma clang fp contract(off)
+    for (int64_t v = blockIdx.x; v < vocab; v += gridDim.x) {
+        float *o = dw + v * hidden;
+        if (!hit[v]) {
+            for (int64_t c = threadIdx.x; c < hidden; c += 256) o[c] = 0.f;
+            continue;
+        }
+        for (int64_t c0 = 0; c0 < hidden; c0 += 1024) {
+            float acc[4] = {0.f, 0.f, 0.f, 0.f};
+            for (int64_t t = 0; t < n; ++t) {
+                if (idi[t] != (int)v) continue;  // the same t for every thread of the block
+                const float *d = dy + t * hidden;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int64_t c = c0 + threadIdx.x + 256 * j;
+                    if (c < hidden) acc[j] += d[c];
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int64_t c = c0 + threadIdx.x + 256 * j;
+                if (c < hidden) o[c] = acc[j];
+            }
+        }
+    }
+}
+
 // RoPE table [S, hd/2] of (cos, sin): angle pos · θ^(−2i/hd) in f64, the
 // sine and cosine rounded to f32 (moe.rs:47-53).
 __global__ void rope_table_kernel(float2 *__restrict__ tab, int64_t n, int half, int hd, double theta) {
@@ -278,6 +333,17 @@ void embedding_f32(hipStream_t s, const float *ids, int64_t n, const float *tabl
         embedding_kernel<true><<<grid, kThreads, 0, s>>>(ids, n, table, vocab, hidden, y, bad);
     else
         embedding_kernel<false><<<grid, kThreads, 0, s>>>(ids, n, table, vocab, hidden, y, bad);
+    CATNN_HIP(hipGetLastError());
+}
+
+void embedding_backward(hipStream_t s, const float *ids, int64_t n, const float *dy, int64_t vocab, int64_t hidden,
+                        float *dw, int *idi, int *hit) {
+    if (vocab <= 0 || hidden <= 0) return;
+    CATNN_REQUIRE(vocab < (1ll << 31) && n < (1ll << 31), CATNN_ERR_SHAPE_MISMATCH, "embedding backward: size");
+    fill_int_kernel<<<std::min<unsigned>(blocks_for(vocab, kThreads), 4096u), kThreads, 0, s>>>(hit, 0, vocab);
+    if (n > 0) embedding_bwd_ids_kernel<<<blocks_for(n, kThreads), kThreads, 0, s>>>(ids, n, vocab, idi, hit);
+    embedding_bwd_rows_kernel<<<(unsigned)std::min<int64_t>(vocab, 65536), kThreads, 0, s>>>(idi, n, dy, hidden, vocab,
+                                                                                            hit, dw);
     CATNN_HIP(hipGetLastError());
 }
 

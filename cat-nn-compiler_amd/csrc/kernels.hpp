@@ -47,6 +47,11 @@ void rms_norm_f32(hipStream_t s, const float *x, const float *w, float *y, int64
 void embedding_f32(hipStream_t s, const float *ids, int64_t n, const float *table, int64_t vocab,
                    int64_t hidden, float *y, int *bad);
 void mix_f32(hipStream_t s, const float *a, const float *b, const float *gate, float *y, int64_t n);
+// embedding_backward (adjoint.rs:187-197): dw [vocab, hidden] from dy
+// [n, hidden] and the n f32 ids, in token order per row; idi holds n ints,
+// hit vocab ints (scratch).
+void embedding_backward(hipStream_t s, const float *ids, int64_t n, const float *dy, int64_t vocab, int64_t hidden,
+                        float *dw, int *idi, int *hit);
 void transpose_f32(hipStream_t s, const float *src, int64_t rows, int64_t cols, float *dst);
 
 // GQA scratch, in floats: packed q|k|v rows [T, qkv_ld], ctx [T, n_heads·hd]

@@ -35,6 +35,7 @@
 // t = 2n − t, update = 2n + 1), placed by place_arena and backed by one
 // hipMalloc — the arena of schedule_device (pipeline.rs:272-401) made real.
 #include <algorithm>
+#include <cmath>
 #include <cstring>
 #include <map>
 #include <memory>
@@ -230,7 +231,7 @@ static void plan_trainer(Tr &t) {
                 case CATNN_OP_IDENTITY: case CATNN_OP_RESHAPE: case CATNN_OP_TRANSPOSE:
                 case CATNN_OP_RELU: case CATNN_OP_GELU: case CATNN_OP_LINEAR: case CATNN_OP_MATMUL:
                 case CATNN_OP_LAYER_NORM: case CATNN_OP_ATTENTION: case CATNN_OP_MOE:
-                case CATNN_OP_LM_HEAD: case CATNN_OP_RMS_NORM:
+                case CATNN_OP_LM_HEAD: case CATNN_OP_RMS_NORM: case CATNN_OP_EMBEDDING:
                     break;
                 case CATNN_OP_MIX:
                     CATNN_REQUIRE(tn.ins.size() == 2, CATNN_ERR_WIRING, "mix adjoint needs two inputs");
@@ -390,6 +391,16 @@ static void plan_trainer(Tr &t) {
                 scratch(tn, "dybt", (uint64_t)(M * N) * 2);
                 scratch(tn, "colsum", k::colsum_scratch_bytes(M, (int)N));
                 scratch(tn, "wparts", wparts_bytes(K, N, M));
+                break;
+            }
+            case CATNN_OP_EMBEDDING: {
+                const int64_t V = nd.op.a[0], H = nd.op.a[1], n_ids = numel(x);
+                const HostTensor *w = host(nd, "w");
+                CATNN_REQUIRE(w->numel() == V * H, CATNN_ERR_SHAPE_MISMATCH, "embedding table");
+                add_param(tn, "w", V, H, false, false, w->data);
+                tape(tn, "bad", 256);
+                scratch(tn, "idi", (uint64_t)n_ids * 4);
+                scratch(tn, "hit", (uint64_t)V * 4);
                 break;
             }
             case CATNN_OP_MIX: {
@@ -619,6 +630,9 @@ static void forward_node(Tr &t, TNode &tn) {
             k::gemm_bf16_launch(s, p);
             break;
         }
+        case CATNN_OP_EMBEDDING:  // ids are checked against the vocabulary by set_batch
+            k::embedding_f32(s, x, nx, tn.params["w"]->master, nd.op.a[0], nd.op.a[1], y, (int *)tn.B("bad"));
+            break;
         case CATNN_OP_MIX: {
             const float *gate = tn.params.count("gate") ? tn.params["gate"]->master : nullptr;
             k::mix_f32(s, x, t.val.at(tn.ins[1]), gate, y, nx);
@@ -751,6 +765,12 @@ static void backward_node(Tr &t, TNode &tn) {
             if (b) k::colsum(s, dy, M, (int)N, b->grad, false, (float *)tn.B("colsum"));
             break;
         }
+        case CATNN_OP_EMBEDDING:
+            // adjoint.rs:843-848: the ids receive the zero cotangent.
+            if (dst(0) && tn.first_writer[0]) k::fill_f32(s, dst(0), 0.f, nx);
+            k::embedding_backward(s, x, nx, dy, nd.op.a[0], nd.op.a[1], tn.params["w"]->grad, (int *)tn.B("idi"),
+                                  (int *)tn.B("hit"));
+            break;
         case CATNN_OP_MIX: {
             TParam *g = tn.params.count("gate") ? tn.params["gate"] : nullptr;
             k::mix_backward(s, x, t.val.at(tn.ins[1]), g ? g->master : nullptr, dy, dst(0),
@@ -921,6 +941,23 @@ static TParam *find_param(Tr &t, uint32_t node_id, const std::string &port, int6
 static void read_cols(Tr &t, const float *src, int64_t rows, int64_t cols, int64_t col0, int64_t ncols,
                       float *host, int64_t n);
 
+// An Embedding that reads a graph input gets its ids checked here, on the
+// host, before the step: the forward's conversion (round half away from
+// zero, negative and NaN → 0), then id < vocab, as the handler refuses it.
+static void check_embedding_ids(const Tr &t, const float *data, int64_t n) {
+    for (const auto &tn : t.nodes) {
+        if (tn.kind != CATNN_OP_EMBEDDING || tn.ins.empty() || !t.input_ids.count(tn.ins[0])) continue;
+        const int64_t vocab = tn.node->op.a[0];
+        for (int64_t i = 0; i < n; ++i) {
+            const float r = std::round(data[i]);
+            const int64_t id = !(r >= 0.f) ? 0 : r >= 4294967296.0f ? 4294967295ll : (int64_t)r;
+            CATNN_REQUIRE(id < vocab, CATNN_ERR_SHAPE_MISMATCH,
+                          "embedding " + tn.node->name + ": id " + std::to_string(id) + " >= vocab " +
+                              std::to_string(vocab));
+        }
+    }
+}
+
 // A parameter-shaped buffer of p (master, gradient or moment) in the
 // graph's layout: columns col0 … col0+ncols, or the whole transpose back
 // when p is held transposed.
@@ -1030,6 +1067,7 @@ int catnn_hip_train_set_batch(catnn_hip_trainer *t, const catnn_tensor *input, c
         for (uint32_t id : t->input_ids) {
             CATNN_REQUIRE(ni == numel(t->dims[id]) && (input->data || ni == 0), CATNN_ERR_SHAPE_MISMATCH,
                           "input size");
+            if (ni) check_embedding_ids(*t, input->data, ni);
             CATNN_HIP(hipMemcpyAsync(t->val.at(id), input->data, (size_t)ni * 4, hipMemcpyHostToDevice, s));
         }
         CATNN_HIP(hipMemcpyAsync(t->target, target->data, (size_t)nt * 4, hipMemcpyHostToDevice, s));
@@ -1054,6 +1092,7 @@ int catnn_hip_train_set_batch_classes(catnn_hip_trainer *t, const catnn_tensor *
         for (uint32_t id : t->input_ids) {
             CATNN_REQUIRE(ni == numel(t->dims[id]) && (input->data || ni == 0), CATNN_ERR_SHAPE_MISMATCH,
                           "input size");
+            if (ni) check_embedding_ids(*t, input->data, ni);
             CATNN_HIP(hipMemcpyAsync(t->val.at(id), input->data, (size_t)ni * 4, hipMemcpyHostToDevice, s));
         }
         if (n) CATNN_HIP(hipMemcpyAsync(t->class_ids, ids, (size_t)n * 4, hipMemcpyHostToDevice, s));
@@ -1200,6 +1239,7 @@ int catnn_hip_run_adjoint(catnn_hip_device *dev, const catnn_node *node, const c
         for (int32_t i = 0; i < n_inputs; ++i) {
             const int64_t ni = numel(dims_from_c(inputs[i]));
             CATNN_REQUIRE(inputs[i].data || ni == 0, CATNN_ERR_INVALID_ARGUMENT, "input " + std::to_string(i) + ": no data");
+            if (ni) check_embedding_ids(*t, inputs[i].data, ni);
             if (ni) CATNN_HIP(hipMemcpyAsync(t->val.at((uint32_t)i), inputs[i].data, (size_t)ni * 4,
                                              hipMemcpyHostToDevice, s));
         }

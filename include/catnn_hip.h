@@ -390,7 +390,8 @@ int catnn_hip_program_timings(catnn_hip_program *p, catnn_step_timing *out,
  * (crates/catnn-rt/src/coord.rs:413, :470, :481), which bypass the handler
  * in the reference.  Executable ops: Identity, Linear/MatMul, Relu, Gelu,
  * LayerNorm, Add/ResidualAdd (same length), Attention (causal flag
- * honoured), MoE, LmHead, RmsNorm, Mix.  The loss is loss_and_grad's (pipeline.rs:
+ * honoured), MoE, LmHead, RmsNorm, Mix, Embedding (its ids, when a graph
+ * input, are checked against the vocabulary at set_batch).  The loss is loss_and_grad's (pipeline.rs:
  * 430-451): cross-entropy against class ids (adjoint.rs:123-145) when the
  * output node is an LmHead (TrainTarget::Classes), else MSE.  GEMM operands are bf16 (bf16 MFMA, fp32 accumulation);
  * master weights, the residual stream, norms, router and accumulation are

@@ -617,6 +617,19 @@ void orc_mix(const float *a, const float *b, float gate, int64_t n, float *y) {
     for (int64_t i = 0; i < n; ++i) y[i] = s * a[i] + (1.0f - s) * b[i];
 }
 
+// embedding_backward, adjoint.rs:187-197, with the ids converted as the
+// adjoint_of arm does (adjoint.rs:845: round, max 0, as u32): dw = 0, then
+// per token in order dw[id] += dy[t].
+void orc_embedding_backward(const float *ids, int64_t n, const float *dy, int64_t vocab, int64_t hidden, float *dw) {
+    for (int64_t i = 0; i < vocab * hidden; ++i) dw[i] = 0.0f;
+    for (int64_t t = 0; t < n; ++t) {
+        const float r = std::max(std::round(ids[t]), 0.0f);
+        const int64_t id = !(r >= 0.0f) ? 0 : r >= 4294967296.0f ? 4294967295ll : (int64_t)r;
+        if (id >= vocab) continue;  // the reference indexes out of bounds; the forward refuses such ids
+        for (int64_t i = 0; i < hidden; ++i) dw[id * hidden + i] += dy[t * hidden + i];
+    }
+}
+
 // deepseek::mix_backward, deepseek.rs:241-258: da = dy·σ, db = dy·(1 − σ),
 // dg = σ(1 − σ)·Σ (a − b)·dy summed in index order.  Returns dg.
 float orc_mix_backward(const float *a, const float *b, float gate, const float *dy, int64_t n, float *da,

@@ -35,6 +35,7 @@ _SIG = {
     "orc_sgd": ([_F, _F, _I64, ctypes.c_float], None),
     "orc_rmsnorm_backward": ([_F, _F, _F, _I64, _I64, ctypes.c_float, _F, _F], None),
     "orc_mix_backward": ([_F, _F, ctypes.c_float, _F, _I64, _F, _F], ctypes.c_float),
+    "orc_embedding_backward": ([_F, _I64, _F, _I64, _I64, _F], None),
     "orc_cross_entropy": ([_F, ctypes.POINTER(ctypes.c_uint32), _I64, _I64, _F, _F], ctypes.c_int),
     "orc_powi": ([ctypes.c_float, ctypes.c_int32], ctypes.c_float),
     "orc_adam": ([_F, _F, _F, _F, _I64, ctypes.c_uint64, ctypes.c_float, ctypes.c_float, ctypes.c_float,
@@ -114,6 +115,15 @@ def rmsnorm_backward(x, w, dy, eps):
     dx, dw = np.empty_like(x), np.empty(last, np.float32)
     _lib.orc_rmsnorm_backward(_f(x), _f(w), _f(dy), x.size // last, last, np.float32(eps), _f(dx), _f(dw))
     return dx, dw
+
+
+def embedding_backward(ids, table_shape, dy):
+    """adjoint.rs:187-197 (ids as the adjoint_of arm converts them, :845)."""
+    ids, dy = _c(ids), _c(dy)
+    V, H = table_shape
+    dw = np.empty((V, H), np.float32)
+    _lib.orc_embedding_backward(_f(ids), ids.size, _f(dy), V, H, _f(dw))
+    return dw
 
 
 def mix_backward(a, b, gate, dy):
@@ -251,6 +261,9 @@ def adjoint_of(node, inputs, output, dy):
         dx, dwq, dwk, dwv, dwo = attention_backward(x, P["wq"], P["wk"], P["wv"], P["wo"], heads, dh, dy,
                                                     causal=bool(node.op.flags & 1))
         return [dx], {"wq": dwq, "wk": dwk, "wv": dwv, "wo": dwo}
+    if kind == "embedding":
+        # adjoint.rs:843-848: the ids get the zero cotangent.
+        return [np.zeros_like(np.asarray(x, np.float32))], {"w": embedding_backward(x, P["w"].shape, dy)}
     if kind == "mix":
         # adjoint.rs:918-927: the gate cotangent is reported as a [1] tensor.
         g = float(P["gate"].reshape(-1)[0]) if "gate" in P else 0.0

@@ -92,6 +92,24 @@ def test_rms_norm(device, rows, cols):
     _check(device, node, [r.standard_normal((rows, cols)) * 2 + 0.5], FP32_TOL)
 
 
+def test_embedding(device):
+    # The table's cotangent sums each row's tokens in token order, as the
+    # reference does: bit-exact.  Ids repeat; the ids get zero.
+    r = np.random.default_rng(8)
+    V, H = 50, 1024
+    ids = r.integers(0, V, (2, 300)).astype(np.float32)
+    ids[0, :3] = [1.5, -2.0, 49.4]
+    node = IrNode(1, "emb", OpenOp.embedding(V, H), TensorType.f32([2, 300, H]),
+                  {"w": _t(r.standard_normal((V, H)))})
+    dy = r.standard_normal((2, 300, H)).astype(np.float32)
+    dx, dp = DeviceHandler(device).adjoint_of(node, [_t(ids)], None, _t(dy))
+    assert not dx[0].numpy().any()
+    assert np.array_equal(dp["w"].numpy(), ot.embedding_backward(ids, (V, H), dy))
+    with pytest.raises(CatError) as e:
+        DeviceHandler(device).adjoint_of(node, [_t(np.full((2, 300), 50.0))], None, _t(dy))
+    assert e.value.kind == "ShapeMismatch"
+
+
 @pytest.mark.parametrize("gate", [None, 0.7])
 def test_mix(device, gate):
     r = np.random.default_rng(6)

@@ -75,6 +75,43 @@ def test_classes_step_follows_the_reference(device, B, S, H, F, V, norm):
     tr.free()
 
 
+def test_classes_step_from_token_ids(device):
+    # tokens → Embedding → RMSNorm → Linear → GELU → LmHead, class targets.
+    r = np.random.default_rng(9)
+    B, S, V0, H, F, V = 2, 32, 300, 128, 256, 500
+    g = IrGraph("tokens")
+    g.add_node(IrNode(0, "tokens", OpenOp.identity(), TensorType.f32([B, S])))
+    g.add_node(IrNode(1, "emb", OpenOp.embedding(V0, H), TensorType.f32([B, S, H]),
+                      {"w": _t(r.standard_normal((V0, H)))}))
+    g.add_node(IrNode(2, "rms", OpenOp.rms_norm(10), TensorType.f32([B, S, H]), {"w": _t(1 + 0.1 * r.standard_normal(H))}))
+    g.add_node(IrNode(3, "fc", OpenOp.linear(H, F), TensorType.f32([B, S, F]),
+                      {"w": _t(r.standard_normal((H, F)) / np.sqrt(H)), "b": _t(np.zeros(F))}))
+    g.add_node(IrNode(4, "act", OpenOp.gelu(), TensorType.f32([B, S, F])))
+    g.add_node(IrNode(5, "lm", OpenOp.lm_head(F, V), TensorType.f32([B, S, V]),
+                      {"w": _t(r.standard_normal((V, F)) / np.sqrt(F))}))
+    for a, b in ((0, 1), (1, 2), (2, 3), (3, 4), (4, 5)):
+        g.add_edge(a, b)
+    g.inputs, g.outputs = [0], [5]
+    toks = r.integers(0, V0, (B, S)).astype(np.float32)
+    ids = r.integers(0, V, B * S).astype(np.uint32)
+    tr = Trainer(device, g, 0.05)
+    with pytest.raises(CatError) as e:  # a token past the embedding's vocabulary
+        tr.set_batch_classes(_t(np.full((B, S), float(V0))), ids)
+    assert e.value.kind == "ShapeMismatch"
+    tr.set_batch_classes(_t(toks), ids)
+    loss = tr.step()
+    loss_o, grads_o, _ = ot.train_step(g, toks, ids, 0.05)
+    print(f"  loss gpu={loss:.6f} fp32-oracle={loss_o:.6f}")
+    assert abs(loss - loss_o) <= LOSS_TOL * max(1.0, abs(loss_o))
+    for nid, dp in grads_o.items():
+        for port, go in dp.items():
+            shape = tuple(g.nodes[nid].params[port].ty.shape)
+            e = rel_l2(tr.grad(nid, port, shape), np.asarray(go).reshape(shape))
+            print(f"  grad {g.nodes[nid].name}.{port}: {e:.2e}")
+            assert e < BF16_TOL, (nid, port, e)
+    tr.free()
+
+
 def test_lm_head_run_adjoint(device):
     r = np.random.default_rng(3)
     T, H, V = 100, 64, 500

@@ -1,6 +1,6 @@
 """Pins the oracle's rmsnorm_backward (crates/catnn-compile/src/kernel/
-adjoint.rs:147-198) and mix_backward (kernel/deepseek.rs:241-258; at the
-end) on the CPU.  rmsnorm_backward against central finite differences of
+adjoint.rs:147-198), mix_backward (kernel/deepseek.rs:241-258) and
+embedding_backward (adjoint.rs:187-197; the last two at the end) on the CPU.  rmsnorm_backward against central finite differences of
 L = ⟨dy, rmsnorm(x, w)⟩ in float64 (independent of the closed form: a
 dropped term, a wrong power or a swapped operand fails it), and against
 the closed form dx = inv·(w⊙dy) − x·inv³·Σ(w⊙dy⊙x)/n, dw = Σ_rows dy⊙x·inv."""
@@ -67,3 +67,15 @@ def test_mix_backward_against_float64():
     f = lambda gg: (dy.astype(np.float64) * (a / (1 + np.exp(-gg)) + b * (1 - 1 / (1 + np.exp(-gg))))).sum()
     h = 1e-6
     assert abs(dg - (f(np.float64(np.float32(g)) + h) - f(np.float64(np.float32(g)) - h)) / (2 * h)) < 1e-4
+
+
+def test_embedding_backward_known_answer():
+    # adjoint.rs:187-197 with the ids converted as adjoint.rs:845 does:
+    # 1.5 → 2, −3 → 0, NaN → 0; rows add in token order.
+    dy = np.arange(5 * 3, dtype=np.float32).reshape(5, 3)
+    ids = np.array([0, 2, 1.5, -3, np.nan], np.float32)
+    dw = ot.embedding_backward(ids, (4, 3), dy)
+    want = np.zeros((4, 3), np.float32)
+    for t, v in enumerate([0, 2, 2, 0, 0]):
+        want[v] += dy[t]
+    assert np.array_equal(dw, want)
