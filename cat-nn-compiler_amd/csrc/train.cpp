@@ -238,6 +238,15 @@ static void plan_trainer(Tr &t) {
                     CATNN_REQUIRE(numel(tn.in_dims[0]) == numel(tn.in_dims[1]), CATNN_ERR_SHAPE_MISMATCH,
                                   "mix operands differ");
                     break;
+                case CATNN_OP_SOFTMAX:
+                    break;
+                case CATNN_OP_ROUTER:  // adjoint.rs:915-920
+                    fail(CATNN_ERR_UNLAWFUL,
+                         "router adjoint is the straight-through estimator inside MoE, not a standalone op");
+                case CATNN_OP_MUL:
+                    CATNN_REQUIRE(tn.ins.size() != 2 || numel(tn.in_dims[0]) == numel(tn.in_dims[1]),
+                                  CATNN_ERR_SHAPE_MISMATCH, "mul operands differ");
+                    break;
                 case CATNN_OP_ADD: case CATNN_OP_RESIDUAL_ADD:
                     CATNN_REQUIRE(tn.ins.size() != 2 || numel(tn.in_dims[0]) == numel(tn.in_dims[1]),
                                   CATNN_ERR_UNSUPPORTED,
@@ -299,6 +308,8 @@ static void plan_trainer(Tr &t) {
     std::map<uint32_t, uint64_t> last_read;  // last tick a value is read
     for (auto &tn : t.nodes) {
         last_read[tn.id] = std::max<uint64_t>(last_read[tn.id], tn.tick);
+        // softmax_backward reads the forward output (adjoint.rs:92-104).
+        if (tn.kind == CATNN_OP_SOFTMAX) last_read[tn.id] = std::max<uint64_t>(last_read[tn.id], bwd(tn.tick));
         for (uint32_t v : tn.ins) last_read[v] = std::max<uint64_t>(last_read[v], bwd(tn.tick));
     }
     // The output value stays readable after the step (catnn_hip_train_read_value).
@@ -614,6 +625,15 @@ static void forward_node(Tr &t, TNode &tn) {
             if (tn.ins.size() > 1) k::add_f32(s, x, t.val.at(tn.ins[1]), y, nx, nx);
             else k::copy_f32(s, x, y, nx);
             break;
+        case CATNN_OP_MUL:
+            if (tn.ins.size() > 1) k::mul_f32(s, x, t.val.at(tn.ins[1]), y, nx);
+            else k::copy_f32(s, x, y, nx);
+            break;
+        case CATNN_OP_SOFTMAX: {
+            const int64_t C = xd.back();
+            k::softmax_f32(s, x, y, nx / C, C);
+            break;
+        }
         case CATNN_OP_LINEAR: case CATNN_OP_MATMUL: case CATNN_OP_LM_HEAD: {
             TParam *w = tn.params.begin()->second;
             for (auto &kv : tn.params) if (kv.first != "b") w = kv.second;
@@ -735,6 +755,19 @@ static void backward_node(Tr &t, TNode &tn) {
             for (size_t i = 0; i < tn.ins.size(); ++i)
                 if (dst(i)) add_into(s, dst(i), dy, nx, tn.first_writer[i]);
             break;
+        case CATNN_OP_MUL:  // adjoint.rs:787-800
+            if (tn.ins.size() == 1) {
+                if (dst(0)) add_into(s, dst(0), dy, nx, tn.first_writer[0]);
+            } else {
+                if (dst(0)) k::mul_backward(s, dy, t.val.at(tn.ins[1]), dst(0), !tn.first_writer[0], nx);
+                if (dst(1)) k::mul_backward(s, dy, x, dst(1), !tn.first_writer[1], nx);
+            }
+            break;
+        case CATNN_OP_SOFTMAX: {
+            const int64_t C = xd.back();
+            if (dst(0)) k::softmax_backward(s, t.val.at(tn.id), dy, dst(0), !tn.first_writer[0], nx / C, (int)C);
+            break;
+        }
         case CATNN_OP_RELU: case CATNN_OP_GELU:
             if (dst(0)) k::act_backward(s, x, dy, dst(0), nx, tn.kind, !tn.first_writer[0]);
             break;

@@ -637,6 +637,37 @@ __global__ __launch_bounds__(256) void mix_bwd_finish_kernel(const float *__rest
     }
 }
 
+// softmax_backward (adjoint.rs:92-104), one wavefront per row of the
+// forward output y: dot = Σ y·dy, dx = y·(dy − dot), stored or added.
+__global__ __launch_bounds__(256) void softmax_bwd_kernel(const float *__restrict__ y, const float *__restrict__ dy,
+                                                          float *__restrict__ dx, int acc, int64_t rows, int cols) {
+#pragma clang fp contract(off)
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const float *yr = y + row * cols, *gr = dy + row * cols;
+    float dot = 0.f;
+    for (int c = lane; c < cols; c += 64) dot += yr[c] * gr[c];
+    dot = wave_sum(dot);
+    for (int c = lane; c < cols; c += 64) {
+        const int64_t e = row * cols + c;
+        const float o = yr[c] * (gr[c] - dot);
+        dx[e] = acc ? dx[e] + o : o;
+    }
+}
+
+// Mul's adjoint (adjoint.rs:787-800) for one input: dx = dy·other, stored or
+// added.
+__global__ void mul_bwd_kernel(const float *__restrict__ dy, const float *__restrict__ other, float *dx, int acc,
+                               int64_t n) {
+#pragma clang fp contract(off)
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+        const float o = dy[i] * other[i];
+        dx[i] = acc ? dx[i] + o : o;
+    }
+}
+
 // p −= lr·g; pb = bf16(p) when given.  g may have a row stride (packed
 // gradients): element (r, c) of p [rows, cols] reads g[r·ldg + c].  The
 // product and the difference are rounded separately, as Sgd::put does, so
@@ -1167,6 +1198,20 @@ void rms_backward(hipStream_t s, const float *x, const float *w, const float *dy
 }
 
 uint64_t mix_scratch_bytes() { return (uint64_t)kMseBlocks * 4; }
+
+void softmax_backward(hipStream_t s, const float *y, const float *dy, float *dx, bool accumulate, int64_t rows,
+                      int cols) {
+    if (rows <= 0 || cols <= 0) return;
+    CATNN_REQUIRE((rows + 3) / 4 < (1ll << 31), CATNN_ERR_SHAPE_MISMATCH, "softmax backward: too many rows");
+    softmax_bwd_kernel<<<(unsigned)((rows + 3) / 4), 256, 0, s>>>(y, dy, dx, accumulate ? 1 : 0, rows, cols);
+    CATNN_HIP(hipGetLastError());
+}
+
+void mul_backward(hipStream_t s, const float *dy, const float *other, float *dx, bool accumulate, int64_t n) {
+    if (n <= 0) return;
+    mul_bwd_kernel<<<blocks_for(n, 256 * 4), 256, 0, s>>>(dy, other, dx, accumulate ? 1 : 0, n);
+    CATNN_HIP(hipGetLastError());
+}
 
 void mix_backward(hipStream_t s, const float *a, const float *b, const float *gate, const float *dy, float *da,
                   bool acc_a, float *db, bool acc_b, int64_t n, float *dgate, float *parts) {

@@ -59,6 +59,11 @@ void rms_backward(hipStream_t s, const float *x, const float *w, const float *dy
 // skipped) and, when dgate is given, the gate's cotangent; parts holds
 // mix_scratch_bytes().
 uint64_t mix_scratch_bytes();
+// softmax_backward (adjoint.rs:92-104) from the forward output y [rows, cols].
+void softmax_backward(hipStream_t s, const float *y, const float *dy, float *dx, bool accumulate, int64_t rows,
+                      int cols);
+// One input's cotangent of Mul (adjoint.rs:787-800): dx (=/+=) dy·other.
+void mul_backward(hipStream_t s, const float *dy, const float *other, float *dx, bool accumulate, int64_t n);
 void mix_backward(hipStream_t s, const float *a, const float *b, const float *gate, const float *dy, float *da,
                   bool acc_a, float *db, bool acc_b, int64_t n, float *dgate, float *parts);
 // cross_entropy (adjoint.rs:123-145) of logits [rows, V] against class ids

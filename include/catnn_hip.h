@@ -319,7 +319,8 @@ int catnn_hip_run_kernel(catnn_hip_device *dev, const catnn_node *node,
  * the device from `inputs` (as attention_backward recomputes its forward,
  * adjoint.rs:582-722), so `output` may be NULL and is not read.  Ops as the
  * training step executes them (bf16 MFMA GEMMs with fp32 accumulation);
- * others → CATNN_ERR_UNSUPPORTED; no inputs → CATNN_ERR_WIRING
+ * a Router → CATNN_ERR_UNLAWFUL (adjoint.rs:915-920); others →
+ * CATNN_ERR_UNSUPPORTED; no inputs → CATNN_ERR_WIRING
  * (adjoint.rs:768-770). */
 int catnn_hip_run_adjoint(catnn_hip_device *dev, const catnn_node *node,
                           const catnn_tensor *inputs, int32_t n_inputs,
@@ -390,7 +391,8 @@ int catnn_hip_program_timings(catnn_hip_program *p, catnn_step_timing *out,
  * (crates/catnn-rt/src/coord.rs:413, :470, :481), which bypass the handler
  * in the reference.  Executable ops: Identity, Linear/MatMul, Relu, Gelu,
  * LayerNorm, Add/ResidualAdd (same length), Attention (causal flag
- * honoured), MoE, LmHead, RmsNorm, Mix, Embedding (its ids, when a graph
+ * honoured), MoE, LmHead, RmsNorm, Mix, Mul, Softmax (last axis), Embedding
+ * (its ids, when a graph
  * input, are checked against the vocabulary at set_batch).  The loss is loss_and_grad's (pipeline.rs:
  * 430-451): cross-entropy against class ids (adjoint.rs:123-145) when the
  * output node is an LmHead (TrainTarget::Classes), else MSE.  GEMM operands are bf16 (bf16 MFMA, fp32 accumulation);

@@ -244,6 +244,10 @@ def adjoint_of(node, inputs, output, dy):
         return [gelu_backward(x, dy)], {}
     if kind == "softmax":
         return [softmax_backward(output, dy)], {}
+    if kind == "mul":  # adjoint.rs:787-800
+        if len(inputs) == 1:
+            return [dy.copy()], {}
+        return [_c(dy) * _c(inputs[1]).reshape(dy.shape), _c(dy) * _c(x).reshape(dy.shape)], {}
     if kind in ("add", "residual_add"):
         return ([dy.copy()] if len(inputs) == 1 else [dy.copy(), dy.copy()]), {}
     if kind in ("linear", "matmul"):

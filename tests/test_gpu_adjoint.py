@@ -2,7 +2,8 @@
 DeviceHandler.adjoint_of), against the oracle's restatement of
 crates/catnn-compile/src/kernel/adjoint.rs:762-951 on the same seeded inputs
 and cotangent.  Ops whose adjoint the device computes in fp32 (Identity,
-ReLU, GELU, Add/ResidualAdd, LayerNorm, RMSNorm, Mix) are held to the fp32 bar
+ReLU, GELU, Add/ResidualAdd, Mul, Softmax, LayerNorm, RMSNorm, Mix,
+Embedding) are held to the fp32 bar
 (rel L2 1e-4); ops with GEMMs (Linear, Attention, MoE; LmHead in
 test_gpu_classes.py) run them on bf16 MFMA with
 fp32 accumulation, as the training step does, and are held to the bf16 bar
@@ -92,6 +93,44 @@ def test_rms_norm(device, rows, cols):
     _check(device, node, [r.standard_normal((rows, cols)) * 2 + 0.5], FP32_TOL)
 
 
+def test_softmax_and_mul(device):
+    r = np.random.default_rng(10)
+    sm = IrNode(1, "sm", OpenOp.softmax(), TensorType.f32([7, 333]))
+    _check(device, sm, [3 * r.standard_normal((7, 333))], FP32_TOL)
+    mul = IrNode(2, "mul", OpenOp.mul(), TensorType.f32([4, 50]))
+    _check(device, mul, [r.standard_normal((4, 50)), r.standard_normal((4, 50))], FP32_TOL)
+
+
+def test_softmax_mul_graph_step(device):
+    # in → fc → softmax → mul(softmax, fc): the softmax adjoint reads its own
+    # output after its consumer's adjoint has run.
+    r = np.random.default_rng(11)
+    g = IrGraph("sm")
+    ty = TensorType.f32([16, 64])
+    g.add_node(IrNode(0, "in", OpenOp.identity(), ty))
+    g.add_node(IrNode(1, "fc", OpenOp.linear(64, 64), ty,
+                      {"w": _t(r.standard_normal((64, 64)) / 8), "b": _t(r.standard_normal(64) * 0.1)}))
+    g.add_node(IrNode(2, "sm", OpenOp.softmax(), ty))
+    g.add_node(IrNode(3, "mul", OpenOp.mul(), ty))
+    for a, b in ((0, 1), (1, 2), (2, 3), (1, 3)):
+        g.add_edge(a, b)
+    g.inputs, g.outputs = [0], [3]
+    x = r.standard_normal((16, 64)).astype(np.float32)
+    tgt = r.standard_normal((16, 64)).astype(np.float32)
+    tr = Trainer(device, g, 0.05)
+    tr.set_batch(_t(x), _t(tgt))
+    loss = tr.step()
+    loss_o, grads_o, _ = ot.train_step(g, x, tgt, 0.05)
+    assert abs(loss - loss_o) <= 2e-3 * max(1.0, abs(loss_o))
+    for nid, dp in grads_o.items():
+        for port, go in dp.items():
+            shape = tuple(g.nodes[nid].params[port].ty.shape)
+            e = rel_l2(tr.grad(nid, port, shape), np.asarray(go).reshape(shape))
+            print(f"  grad {g.nodes[nid].name}.{port}: {e:.2e}")
+            assert e < BF16_TOL, (nid, port, e)
+    tr.free()
+
+
 def test_embedding(device):
     # The table's cotangent sums each row's tokens in token order, as the
     # reference does: bit-exact.  Ids repeat; the ids get zero.
@@ -179,9 +218,14 @@ def test_adjoint_errors(device):
     with pytest.raises(CatError) as e:
         h.adjoint_of(node, [_t(np.ones(4))], None, _t(np.ones(5)))
     assert e.value.kind == "ShapeMismatch"
-    sm = IrNode(1, "sm", OpenOp.softmax(), TensorType.f32([2, 4]))
+    rt = IrNode(1, "rt", OpenOp.router(4, 2), TensorType.f32([2, 4]))  # STE lives inside MoE
     with pytest.raises(CatError) as e:
-        h.adjoint_of(sm, [_t(np.ones((2, 4)))], None, _t(np.ones((2, 4))))
+        h.adjoint_of(rt, [_t(np.ones((2, 4)))], None, _t(np.ones((2, 4))))
+    assert e.value.kind == "Unlawful"
+    sw = IrNode(1, "sw", OpenOp.swiglu(8, 16), TensorType.f32([2, 8]),
+                {"w1": _t(np.ones((8, 16))), "w3": _t(np.ones((8, 16))), "w2": _t(np.ones((16, 8)))})
+    with pytest.raises(CatError) as e:  # no device adjoint yet
+        h.adjoint_of(sw, [_t(np.ones((2, 8)))], None, _t(np.ones((2, 8))))
     assert e.value.kind == "Unsupported"
     fc = IrNode(1, "fc", OpenOp.linear(8, 4, False), TensorType.f32([2, 4]), {"w": _t(np.ones((8, 4)))})
     with pytest.raises(CatError) as e:
