@@ -232,6 +232,7 @@ static void plan_trainer(Tr &t) {
                 case CATNN_OP_RELU: case CATNN_OP_GELU: case CATNN_OP_LINEAR: case CATNN_OP_MATMUL:
                 case CATNN_OP_LAYER_NORM: case CATNN_OP_ATTENTION: case CATNN_OP_MOE:
                 case CATNN_OP_LM_HEAD: case CATNN_OP_RMS_NORM: case CATNN_OP_EMBEDDING:
+                case CATNN_OP_SWIGLU:
                     break;
                 case CATNN_OP_MIX:
                     CATNN_REQUIRE(tn.ins.size() == 2, CATNN_ERR_WIRING, "mix adjoint needs two inputs");
@@ -402,6 +403,28 @@ static void plan_trainer(Tr &t) {
                 scratch(tn, "dybt", (uint64_t)(M * N) * 2);
                 scratch(tn, "colsum", k::colsum_scratch_bytes(M, (int)N));
                 scratch(tn, "wparts", wparts_bytes(K, N, M));
+                break;
+            }
+            case CATNN_OP_SWIGLU: {  // moe.rs:159-174; adjoint.rs:217-251
+                const int64_t H = nd.op.a[0], I = nd.op.a[1], M = numel(x) / std::max<int64_t>(H, 1);
+                CATNN_REQUIRE(x.back() == H, CATNN_ERR_SHAPE_MISMATCH, "swiglu input");
+                const HostTensor *w1 = host(nd, "w1"), *w3 = host(nd, "w3"), *w2 = host(nd, "w2");
+                CATNN_REQUIRE(w1->numel() == H * I && w3->numel() == H * I && w2->numel() == I * H,
+                              CATNN_ERR_SHAPE_MISMATCH, "swiglu weights");
+                add_param(tn, "w1", H, I, true, false, w1->data, true);
+                add_param(tn, "w3", H, I, true, false, w3->data, true);
+                add_param(tn, "w2", I, H, true, false, w2->data, true);
+                tape(tn, "x3", (uint64_t)(M * 3 * H) * 2);
+                tape(tn, "a", (uint64_t)(M * I) * 4);
+                tape(tn, "c", (uint64_t)(M * I) * 4);
+                tape(tn, "h", (uint64_t)(M * I) * 4);
+                tape(tn, "h3", (uint64_t)(M * 3 * I) * 2);
+                scratch(tn, "dyb", (uint64_t)(M * H) * 2);
+                scratch(tn, "dybt", (uint64_t)(M * H) * 2);
+                scratch(tn, "dh", (uint64_t)(M * I) * 4);
+                for (const char *nm : {"dab", "dcb", "dabt", "dcbt", "hbt"}) scratch(tn, nm, (uint64_t)(M * I) * 2);
+                scratch(tn, "xbt", (uint64_t)(M * H) * 2);
+                scratch(tn, "wparts", std::max(wparts_bytes(H, I, M), wparts_bytes(I, H, M)));
                 break;
             }
             case CATNN_OP_EMBEDDING: {
@@ -650,6 +673,28 @@ static void forward_node(Tr &t, TNode &tn) {
             k::gemm_bf16_launch(s, p);
             break;
         }
+        case CATNN_OP_SWIGLU: {
+            // a = x·w1, c = x·w3 and y = h·w2 with h = silu(a)·c, each GEMM on
+            // split-bf16 operands as Linear's forward.
+            TParam *w1 = tn.params["w1"], *w3 = tn.params["w3"], *w2 = tn.params["w2"];
+            const int64_t H = w1->rows, I = w1->cols, M = nx / H;
+            bf16_t *x3 = (bf16_t *)tn.B("x3"), *h3 = (bf16_t *)tn.B("h3");
+            float *a = (float *)tn.B("a"), *c = (float *)tn.B("c"), *h = (float *)tn.B("h");
+            auto split_gemm = [&](const bf16_t *A3, int64_t K, const TParam *w, float *C) {
+                k::GemmBf16Params p = gp();
+                p.A = A3; p.lda = 3 * K; p.B = w->bt3; p.ldb = 3 * K;
+                p.M = (int)M; p.N = (int)w->cols; p.K = (int)(3 * K);
+                p.epi = k::EPI_LINEAR; p.C32 = C; p.ldc32 = w->cols;
+                k::gemm_bf16_launch(s, p);
+            };
+            k::split3_rows(s, x, H, M, (int)H, x3, 3 * H);
+            split_gemm(x3, H, w1, a);
+            split_gemm(x3, H, w3, c);
+            k::swiglu_h(s, a, c, h, M * I);
+            k::split3_rows(s, h, I, M, (int)I, h3, 3 * I);
+            split_gemm(h3, I, w2, y);
+            break;
+        }
         case CATNN_OP_EMBEDDING:  // ids are checked against the vocabulary by set_batch
             k::embedding_f32(s, x, nx, tn.params["w"]->master, nd.op.a[0], nd.op.a[1], y, (int *)tn.B("bad"));
             break;
@@ -796,6 +841,31 @@ static void backward_node(Tr &t, TNode &tn) {
             k::transpose_bf16(s, x3, 3 * K, nullptr, 1, (int)M, (int)K, xbt, M);  // hi part of x
             gemm_nt(s, xbt, M, dybt, M, (int)K, (int)N, (int)M, w->grad, N, false, (float *)tn.B("wparts"));
             if (b) k::colsum(s, dy, M, (int)N, b->grad, false, (float *)tn.B("colsum"));
+            break;
+        }
+        case CATNN_OP_SWIGLU: {  // swiglu_backward, adjoint.rs:217-251
+            TParam *w1 = tn.params["w1"], *w3 = tn.params["w3"], *w2 = tn.params["w2"];
+            const int64_t H = w1->rows, I = w1->cols, M = nx / H;
+            bf16_t *dyb = (bf16_t *)tn.B("dyb"), *dybt = (bf16_t *)tn.B("dybt"), *dab = (bf16_t *)tn.B("dab"),
+                   *dcb = (bf16_t *)tn.B("dcb"), *dabt = (bf16_t *)tn.B("dabt"), *dcbt = (bf16_t *)tn.B("dcbt"),
+                   *xbt = (bf16_t *)tn.B("xbt"), *hbt = (bf16_t *)tn.B("hbt"), *x3 = (bf16_t *)tn.B("x3"),
+                   *h3 = (bf16_t *)tn.B("h3");
+            float *dh = (float *)tn.B("dh"), *wparts = (float *)tn.B("wparts");
+            k::cast_f32_bf16(s, dy, dyb, M * H);
+            gemm_nt(s, dyb, H, w2->b, H, (int)M, (int)I, (int)H, dh, I, false);  // dh = dy·w2ᵀ
+            k::swiglu_dadc(s, dh, (const float *)tn.B("a"), (const float *)tn.B("c"), dab, dcb, M * I);
+            if (dst(0)) {  // dx = da·w1ᵀ + dc·w3ᵀ
+                gemm_nt(s, dab, I, w1->b, I, (int)M, (int)H, (int)I, dst(0), H, !tn.first_writer[0]);
+                gemm_nt(s, dcb, I, w3->b, I, (int)M, (int)H, (int)I, dst(0), H, true);
+            }
+            k::transpose_bf16(s, x3, 3 * H, nullptr, 1, (int)M, (int)H, xbt, M);  // hi part of x
+            k::transpose_bf16(s, dab, I, nullptr, 1, (int)M, (int)I, dabt, M);
+            k::transpose_bf16(s, dcb, I, nullptr, 1, (int)M, (int)I, dcbt, M);
+            gemm_nt(s, xbt, M, dabt, M, (int)H, (int)I, (int)M, w1->grad, I, false, wparts);  // dw1 = xᵀ·da
+            gemm_nt(s, xbt, M, dcbt, M, (int)H, (int)I, (int)M, w3->grad, I, false, wparts);  // dw3 = xᵀ·dc
+            k::transpose_bf16(s, h3, 3 * I, nullptr, 1, (int)M, (int)I, hbt, M);  // hi part of h
+            k::transpose_bf16(s, dyb, H, nullptr, 1, (int)M, (int)H, dybt, M);
+            gemm_nt(s, hbt, M, dybt, M, (int)I, (int)H, (int)M, w2->grad, H, false, wparts);  // dw2 = hᵀ·dy
             break;
         }
         case CATNN_OP_EMBEDDING:

@@ -656,6 +656,30 @@ __global__ __launch_bounds__(256) void softmax_bwd_kernel(const float *__restric
     }
 }
 
+// The dense SwiGLU's hidden activation h = silu(a)·c (moe.rs:159-174).
+__global__ void swiglu_h_kernel(const float *__restrict__ a, const float *__restrict__ c, float *__restrict__ h,
+                                int64_t n) {
+#pragma clang fp contract(off)
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+        h[i] = a[i] / (1.0f + expf(-a[i])) * c[i];
+}
+
+// swiglu_backward's elementwise step (adjoint.rs:238-242): da = dh·c·silu'(a),
+// dc = dh·silu(a) with silu'(z) = s + z·s·(1 − s), s = 1/(1 + e^(−z)); both
+// written as bf16 GEMM operands.
+__global__ void swiglu_dadc_kernel(const float *__restrict__ dh, const float *__restrict__ a,
+                                   const float *__restrict__ c, bf16_t *__restrict__ da, bf16_t *__restrict__ dc,
+                                   int64_t n) {
+#pragma clang fp contract(off)
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+        const float z = a[i], sg = 1.0f / (1.0f + expf(-z));
+        da[i] = f2bf(dh[i] * c[i] * (sg + z * sg * (1.0f - sg)));
+        dc[i] = f2bf(dh[i] * (z / (1.0f + expf(-z))));
+    }
+}
+
 // Mul's adjoint (adjoint.rs:787-800) for one input: dx = dy·other, stored or
 // added.
 __global__ void mul_bwd_kernel(const float *__restrict__ dy, const float *__restrict__ other, float *dx, int acc,
@@ -1204,6 +1228,18 @@ void softmax_backward(hipStream_t s, const float *y, const float *dy, float *dx,
     if (rows <= 0 || cols <= 0) return;
     CATNN_REQUIRE((rows + 3) / 4 < (1ll << 31), CATNN_ERR_SHAPE_MISMATCH, "softmax backward: too many rows");
     softmax_bwd_kernel<<<(unsigned)((rows + 3) / 4), 256, 0, s>>>(y, dy, dx, accumulate ? 1 : 0, rows, cols);
+    CATNN_HIP(hipGetLastError());
+}
+
+void swiglu_h(hipStream_t s, const float *a, const float *c, float *h, int64_t n) {
+    if (n <= 0) return;
+    swiglu_h_kernel<<<blocks_for(n, 256 * 4), 256, 0, s>>>(a, c, h, n);
+    CATNN_HIP(hipGetLastError());
+}
+
+void swiglu_dadc(hipStream_t s, const float *dh, const float *a, const float *c, bf16_t *da, bf16_t *dc, int64_t n) {
+    if (n <= 0) return;
+    swiglu_dadc_kernel<<<blocks_for(n, 256 * 4), 256, 0, s>>>(dh, a, c, da, dc, n);
     CATNN_HIP(hipGetLastError());
 }
 

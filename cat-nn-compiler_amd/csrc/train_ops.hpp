@@ -62,6 +62,9 @@ uint64_t mix_scratch_bytes();
 // softmax_backward (adjoint.rs:92-104) from the forward output y [rows, cols].
 void softmax_backward(hipStream_t s, const float *y, const float *dy, float *dx, bool accumulate, int64_t rows,
                       int cols);
+// The dense SwiGLU: h = silu(a)·c, and the adjoint's da, dc (bf16).
+void swiglu_h(hipStream_t s, const float *a, const float *c, float *h, int64_t n);
+void swiglu_dadc(hipStream_t s, const float *dh, const float *a, const float *c, bf16_t *da, bf16_t *dc, int64_t n);
 // One input's cotangent of Mul (adjoint.rs:787-800): dx (=/+=) dy·other.
 void mul_backward(hipStream_t s, const float *dy, const float *other, float *dx, bool accumulate, int64_t n);
 void mix_backward(hipStream_t s, const float *a, const float *b, const float *gate, const float *dy, float *da,

@@ -391,7 +391,7 @@ int catnn_hip_program_timings(catnn_hip_program *p, catnn_step_timing *out,
  * (crates/catnn-rt/src/coord.rs:413, :470, :481), which bypass the handler
  * in the reference.  Executable ops: Identity, Linear/MatMul, Relu, Gelu,
  * LayerNorm, Add/ResidualAdd (same length), Attention (causal flag
- * honoured), MoE, LmHead, RmsNorm, Mix, Mul, Softmax (last axis), Embedding
+ * honoured), MoE, SwiGlu, LmHead, RmsNorm, Mix, Mul, Softmax (last axis), Embedding
  * (its ids, when a graph
  * input, are checked against the vocabulary at set_batch).  The loss is loss_and_grad's (pipeline.rs:
  * 430-451): cross-entropy against class ids (adjoint.rs:123-145) when the

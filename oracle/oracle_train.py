@@ -265,6 +265,9 @@ def adjoint_of(node, inputs, output, dy):
         dx, dwq, dwk, dwv, dwo = attention_backward(x, P["wq"], P["wk"], P["wv"], P["wo"], heads, dh, dy,
                                                     causal=bool(node.op.flags & 1))
         return [dx], {"wq": dwq, "wk": dwk, "wv": dwv, "wo": dwo}
+    if kind == "swiglu":  # adjoint.rs:849-861
+        dx, dw1, dw3, dw2 = swiglu_backward(x, P["w1"], P["w3"], P["w2"], dy)
+        return [dx.reshape(np.shape(x))], {"w1": dw1, "w3": dw3, "w2": dw2}
     if kind == "embedding":
         # adjoint.rs:843-848: the ids get the zero cotangent.
         return [np.zeros_like(np.asarray(x, np.float32))], {"w": embedding_backward(x, P["w"].shape, dy)}

@@ -3,7 +3,8 @@ DeviceHandler.adjoint_of), against the oracle's restatement of
 crates/catnn-compile/src/kernel/adjoint.rs:762-951 on the same seeded inputs
 and cotangent.  Ops whose adjoint the device computes in fp32 (Identity,
 ReLU, GELU, Add/ResidualAdd, Mul, Softmax, LayerNorm, RMSNorm, Mix,
-Embedding) are held to the fp32 bar
+Embedding) are held to the fp32 bar; the dense SwiGLU, like the other GEMM
+ops, to the bf16 bar
 (rel L2 1e-4); ops with GEMMs (Linear, Attention, MoE; LmHead in
 test_gpu_classes.py) run them on bf16 MFMA with
 fp32 accumulation, as the training step does, and are held to the bf16 bar
@@ -197,6 +198,15 @@ def test_attention(device, causal):
     _check(device, node, [r.standard_normal((b, s, d))], BF16_TOL)
 
 
+@pytest.mark.parametrize("T,H,I", [(64, 128, 256), (37, 100, 52)])
+def test_swiglu(device, T, H, I):
+    r = np.random.default_rng(T + I)
+    params = {"w1": _t(r.standard_normal((H, I)) / np.sqrt(H)), "w3": _t(r.standard_normal((H, I)) / np.sqrt(H)),
+              "w2": _t(r.standard_normal((I, H)) / np.sqrt(I))}
+    node = IrNode(4, "sw", OpenOp.swiglu(H, I), TensorType.f32([T, H]), params)
+    _check(device, node, [r.standard_normal((T, H))], BF16_TOL)
+
+
 def test_moe(device):
     r = np.random.default_rng(4)
     E, k, H, I, T = 4, 2, 128, 96, 200
@@ -222,10 +232,11 @@ def test_adjoint_errors(device):
     with pytest.raises(CatError) as e:
         h.adjoint_of(rt, [_t(np.ones((2, 4)))], None, _t(np.ones((2, 4))))
     assert e.value.kind == "Unlawful"
-    sw = IrNode(1, "sw", OpenOp.swiglu(8, 16), TensorType.f32([2, 8]),
-                {"w1": _t(np.ones((8, 16))), "w3": _t(np.ones((8, 16))), "w2": _t(np.ones((16, 8)))})
+    gqa = IrNode(1, "gqa", OpenOp.gqa_attention(2, 1, 4, 8, 8, 10000), TensorType.f32([1, 3, 8]),
+                 {"wq": _t(np.ones((8, 8))), "wk": _t(np.ones((8, 4))), "wv": _t(np.ones((8, 4))),
+                  "wo": _t(np.ones((8, 8)))})
     with pytest.raises(CatError) as e:  # no device adjoint yet
-        h.adjoint_of(sw, [_t(np.ones((2, 8)))], None, _t(np.ones((2, 8))))
+        h.adjoint_of(gqa, [_t(np.ones((1, 3, 8)))], None, _t(np.ones((1, 3, 8))))
     assert e.value.kind == "Unsupported"
     fc = IrNode(1, "fc", OpenOp.linear(8, 4, False), TensorType.f32([2, 4]), {"w": _t(np.ones((8, 4)))})
     with pytest.raises(CatError) as e:

@@ -76,7 +76,8 @@ def test_classes_step_follows_the_reference(device, B, S, H, F, V, norm):
 
 
 def test_classes_step_from_token_ids(device):
-    # tokens → Embedding → RMSNorm → Linear → GELU → LmHead, class targets.
+    # tokens → Embedding → RMSNorm → SwiGLU FFN (+ residual) → LmHead, class
+    # targets: a one-layer dense decoder without attention.
     r = np.random.default_rng(9)
     B, S, V0, H, F, V = 2, 32, 300, 128, 256, 500
     g = IrGraph("tokens")
@@ -84,12 +85,13 @@ def test_classes_step_from_token_ids(device):
     g.add_node(IrNode(1, "emb", OpenOp.embedding(V0, H), TensorType.f32([B, S, H]),
                       {"w": _t(r.standard_normal((V0, H)))}))
     g.add_node(IrNode(2, "rms", OpenOp.rms_norm(10), TensorType.f32([B, S, H]), {"w": _t(1 + 0.1 * r.standard_normal(H))}))
-    g.add_node(IrNode(3, "fc", OpenOp.linear(H, F), TensorType.f32([B, S, F]),
-                      {"w": _t(r.standard_normal((H, F)) / np.sqrt(H)), "b": _t(np.zeros(F))}))
-    g.add_node(IrNode(4, "act", OpenOp.gelu(), TensorType.f32([B, S, F])))
-    g.add_node(IrNode(5, "lm", OpenOp.lm_head(F, V), TensorType.f32([B, S, V]),
-                      {"w": _t(r.standard_normal((V, F)) / np.sqrt(F))}))
-    for a, b in ((0, 1), (1, 2), (2, 3), (3, 4), (4, 5)):
+    g.add_node(IrNode(3, "ffn", OpenOp.swiglu(H, F), TensorType.f32([B, S, H]),
+                      {"w1": _t(r.standard_normal((H, F)) / np.sqrt(H)), "w3": _t(r.standard_normal((H, F)) / np.sqrt(H)),
+                       "w2": _t(r.standard_normal((F, H)) / np.sqrt(F))}))
+    g.add_node(IrNode(4, "res", OpenOp.residual_add(), TensorType.f32([B, S, H])))
+    g.add_node(IrNode(5, "lm", OpenOp.lm_head(H, V), TensorType.f32([B, S, V]),
+                      {"w": _t(r.standard_normal((V, H)) / np.sqrt(H))}))
+    for a, b in ((0, 1), (1, 2), (2, 3), (1, 4), (3, 4), (4, 5)):
         g.add_edge(a, b)
     g.inputs, g.outputs = [0], [5]
     toks = r.integers(0, V0, (B, S)).astype(np.float32)

@@ -190,12 +190,13 @@ def test_reset_restores_parameters_and_steps_repeat_bit_exactly(device):
 
 
 def test_training_error_kinds(device):
-    ty = TensorType.f32([4, 8])
-    g = IrGraph("sw")
+    ty = TensorType.f32([1, 4, 8])
+    g = IrGraph("gqa")
     g.add_node(IrNode(0, "in", OpenOp.identity(), ty))
     ones = lambda *s: Tensor(TensorType.f32(list(s)), np.ones(s, np.float32))
-    # the dense SwiGLU has no device adjoint yet
-    g.add_node(IrNode(1, "sw", OpenOp.swiglu(8, 16), ty, {"w1": ones(8, 16), "w3": ones(8, 16), "w2": ones(16, 8)}))
+    # GQA attention has no device adjoint yet
+    g.add_node(IrNode(1, "gqa", OpenOp.gqa_attention(2, 1, 4, 8, 8, 10000), ty,
+                      {"wq": ones(8, 8), "wk": ones(8, 4), "wv": ones(8, 4), "wo": ones(8, 8)}))
     g.add_edge(0, 1)
     g.inputs.append(0)
     g.outputs.append(1)
