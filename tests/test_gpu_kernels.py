@@ -142,7 +142,8 @@ def test_activations_and_adds(device):
     assert np.array_equal(_get(dout, a.shape), oracle.add(a, bias))
 
 
-@pytest.mark.parametrize("rows,cols", [(8192, 1024), (33, 96), (5, 4), (7, 7), (3, 4096), (2, 5000)])
+@pytest.mark.parametrize("rows,cols", [(8192, 1024), (4097, 1024), (4096, 768), (33, 96), (5, 4), (7, 7), (3, 4096),
+                                       (2, 5000)])
 def test_layer_norm_and_softmax_match_oracle(device, rows, cols):
     x = (RNG.standard_normal((rows, cols)) * 2 + 0.5).astype(np.float32)
     g = RNG.standard_normal(cols).astype(np.float32)
