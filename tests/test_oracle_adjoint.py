@@ -223,3 +223,105 @@ def test_bf16_model_without_rounding_is_the_reference_step(which):
         assert dp.keys() == grads_m[nid].keys()
         for port, go in dp.items():
             assert rel_l2(grads_m[nid][port].reshape(go.shape), go) < 1e-4, (g.nodes[nid].name, port)
+
+
+# ---- pins for oracle.mul, the Mul arm of adjoint_of and softmax_backward ----
+
+
+def test_mul_is_the_elementwise_f32_product():
+    # cpu.rs:100-109: y[i] = a[i]·b[i], one correctly rounded f32 product.
+    # The float64 product of two f32 values is exact (48 significant bits),
+    # so rounding it once to f32 is the reference value bit for bit.
+    a = RNG.standard_normal(1000).astype(np.float32)
+    b = (RNG.standard_normal(1000) * 7).astype(np.float32)
+    want = (a.astype(np.float64) * b.astype(np.float64)).astype(np.float32)
+    got = oracle.mul(a, b)
+    assert got.view(np.uint32).tolist() == want.view(np.uint32).tolist()
+    # signs and signed zeros come through as IEEE multiplication gives them
+    assert oracle.mul(np.array([-2.0, 0.5, -0.0], np.float32),
+                      np.array([3.0, -4.0, 5.0], np.float32)).tolist() == [-6.0, -2.0, -0.0]
+    with pytest.raises(Exception):
+        oracle.mul(np.ones(3, np.float32), np.ones(4, np.float32))
+
+
+def _mul_node(shape):
+    from catnn_amd import IrNode, OpenOp, TensorType
+
+    return IrNode(2, "mul", OpenOp.mul(), TensorType.f32(list(shape)))
+
+
+def test_mul_adjoint_matches_autograd_and_finite_differences():
+    # adjoint.rs:785-799: d(x·y) = (dy·y, dy·x).  The two inputs differ, so a
+    # swapped pair of cotangents fails both checks.
+    x = RNG.standard_normal((5, 11))
+    y = RNG.standard_normal((5, 11)) * 3 + 1
+    dy = RNG.standard_normal((5, 11))
+    node = _mul_node(x.shape)
+    out = oracle.mul(x.astype(np.float32), y.astype(np.float32))
+    (dx, dyy), dp = ot.adjoint_of(node, [x.astype(np.float32), y.astype(np.float32)], out,
+                                  dy.astype(np.float32))
+    assert dp == {}
+    X, Y = _t(x, True), _t(y, True)
+    (X * Y).backward(_t(dy))
+    assert rel_l2(dx, X.grad) < 1e-6 and rel_l2(dyy, Y.grad) < 1e-6
+    assert rel_l2(dyy, X.grad) > 0.1 and rel_l2(dx, Y.grad) > 0.1  # a swap is caught
+    # central differences of <dy, x·y> in float64
+    h = 1e-6
+    f = lambda a, b: float(np.sum(dy * a * b))
+    for (i, j) in [(0, 0), (2, 5), (4, 10)]:
+        e = np.zeros_like(x)
+        e[i, j] = h
+        assert abs((f(x + e, y) - f(x - e, y)) / (2 * h) - dx[i, j]) < 1e-4 * (1 + abs(dx[i, j]))
+        assert abs((f(x, y + e) - f(x, y - e)) / (2 * h) - dyy[i, j]) < 1e-4 * (1 + abs(dyy[i, j]))
+    # single input: Mul passes dy through (adjoint.rs:786-787)
+    (d1,), _ = ot.adjoint_of(node, [x.astype(np.float32)], x.astype(np.float32), dy.astype(np.float32))
+    assert np.array_equal(d1, dy.astype(np.float32))
+
+
+def test_softmax_backward_matches_autograd():
+    # adjoint.rs:92-104: dx = y·(dy − Σ y·dy), against float64 autograd of
+    # softmax.  A flipped sign or a dropped dot term both sum to zero per
+    # row, so they pass the reference's own row-sum check; this one fails
+    # them (checked below on planted mistakes).
+    x = RNG.standard_normal((6, 17)) * 2
+    dy = RNG.standard_normal((6, 17))
+    X = _t(x, True)
+    torch.softmax(X, -1).backward(_t(dy))
+    y = oracle.softmax_last(x.astype(np.float32))
+    got = ot.softmax_backward(y, dy.astype(np.float32))
+    assert rel_l2(got, X.grad) < 1e-5
+    yd = y.astype(np.float64)
+    dot = np.sum(yd * dy, -1, keepdims=True)
+    for wrong in (-yd * (dy - dot), yd * (dot - dy), yd * dy, yd * (dy - dot) * 2):
+        assert rel_l2(wrong, X.grad) > 0.3
+    # the same through adjoint_of's Softmax arm (reads the forward output)
+    from catnn_amd import IrNode, OpenOp, TensorType
+
+    node = IrNode(1, "sm", OpenOp.softmax(), TensorType.f32([6, 17]))
+    (d,), dp = ot.adjoint_of(node, [x.astype(np.float32)], y, dy.astype(np.float32))
+    assert dp == {} and rel_l2(d, X.grad) < 1e-5
+
+
+def test_softmax_backward_finite_differences_and_closed_form():
+    # central differences of <dy, softmax(x)> in float64 on one row
+    x = RNG.standard_normal(9)
+    dy = RNG.standard_normal(9)
+    sm = lambda v: np.exp(v - v.max()) / np.exp(v - v.max()).sum()
+    y = oracle.softmax_last(x.astype(np.float32)[None])
+    got = ot.softmax_backward(y, dy.astype(np.float32)[None])[0]
+    h = 1e-6
+    for i in range(9):
+        e = np.zeros(9)
+        e[i] = h
+        fd = (np.dot(dy, sm(x + e)) - np.dot(dy, sm(x - e))) / (2 * h)
+        assert abs(fd - got[i]) < 2e-5 * (1 + abs(fd))
+    # closed form: a constant cotangent moves nothing (softmax is invariant
+    # to a shift of its output's dual), and a one-hot dy on a uniform row
+    # gives (1/n)(e_i − 1/n).
+    assert np.allclose(ot.softmax_backward(y, np.full((1, 9), 3.0, np.float32)), 0.0, atol=1e-6)
+    n = 8
+    u = np.full((1, n), 1.0 / n, np.float32)
+    oh = np.zeros((1, n), np.float32)
+    oh[0, 2] = 1.0
+    want = (1.0 / n) * (oh - 1.0 / n)
+    assert np.allclose(ot.softmax_backward(u, oh), want, atol=1e-7)
