@@ -185,6 +185,9 @@ SIGNATURES = {
     "catnn_hip_moe_permute": [_VP, _VP, _I64, _I64, _I64, _VP, _VP, _VP, _VP],
     "catnn_hip_moe_f32": [_VP, _VP, _VP, ctypes.POINTER(_VP), ctypes.POINTER(_VP),
                           ctypes.POINTER(_VP), _I64, _I64, _I64, _I64, _I64, _VP, _VP, _VP, _VP],
+    "catnn_hip_moe_f32_noalloc": [_VP, _VP, _VP, ctypes.POINTER(_VP), ctypes.POINTER(_VP),
+                                  ctypes.POINTER(_VP), _I64, _I64, _I64, _I64, _I64, _VP, _VP, _VP,
+                                  _VP],
 }
 
 _RESTYPE = {"catnn_hip_last_error": ctypes.c_char_p}

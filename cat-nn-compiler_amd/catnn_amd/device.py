@@ -377,3 +377,18 @@ def moe(dev: Device, x, gate, w1s, w3s, w2s, tokens: int, hidden: int, intermedi
     check(lib.catnn_hip_moe_f32(dev.handle, _ptr(x), _ptr(gate), arr(w1s), arr(w3s), arr(w2s),
                                 tokens, hidden, intermediate, n_experts, top_k, _ptr(out),
                                 _ptr(idx), _ptr(w), _ptr(counts)))
+
+
+# Size of the fixed device scratch behind moe_noalloc (CATNN_MOE_NOALLOC_SCRATCH_BYTES).
+MOE_NOALLOC_SCRATCH_BYTES = 128 << 20
+
+
+def moe_noalloc(dev: Device, x, gate, w1s, w3s, w2s, tokens: int, hidden: int, intermediate: int,
+                n_experts: int, top_k: int, out, idx=None, w=None, counts=None):
+    """`moe` without any device allocation: the workspace is the library's
+    fixed per-GPU scratch (catnn_hip_moe_f32_noalloc).  Calls that overlap
+    on one GPU race on that scratch."""
+    arr = lambda bs: (VP * len(bs))(*[_ptr(b) for b in bs])
+    check(lib.catnn_hip_moe_f32_noalloc(dev.handle, _ptr(x), _ptr(gate), arr(w1s), arr(w3s),
+                                        arr(w2s), tokens, hidden, intermediate, n_experts, top_k,
+                                        _ptr(out), _ptr(idx), _ptr(w), _ptr(counts)))

@@ -78,6 +78,8 @@ struct catnn_hip_device {
     std::vector<catnn_event> events;
     std::chrono::steady_clock::time_point epoch;
     catnn::Workspace moe_ws;
+    void *noalloc_scratch = nullptr;  // device address of the fixed MoE scratch
+    std::string noalloc_error;
     int cu_count = 0;
 };
 

@@ -6,6 +6,7 @@
 #include <hip/hip_runtime_api.h>
 
 #include <cstdint>
+#include <string>
 
 namespace catnn {
 namespace k {
@@ -90,6 +91,12 @@ void moe_f32(hipStream_t s, const float *x, const float *gate, const float *cons
              const float *const *w3s, const float *const *w2s, int64_t tokens, int64_t hidden,
              int64_t intermediate, int64_t n_experts, int64_t top_k, float *out, void *ws,
              const MoeWorkspaceLayout &L);
+
+// The fixed device scratch of catnn_hip_moe_f32_noalloc and its size.
+// moe_noalloc_scratch returns the array's device address on the current
+// device `ordinal` (queried once per device), or null with `err` set.
+constexpr uint64_t kMoeNoAllocScratchBytes = 128ull << 20;
+void *moe_noalloc_scratch(int ordinal, std::string *err);
 
 }  // namespace k
 }  // namespace catnn

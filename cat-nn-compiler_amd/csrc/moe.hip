@@ -25,6 +25,8 @@
 
 #include <algorithm>
 #include <cstring>
+#include <mutex>
+#include <string>
 #include <vector>
 
 #include "common.hpp"
@@ -292,6 +294,11 @@ __global__ __launch_bounds__(256) void route_vec_kernel(const float *__restrict_
 
 // Per-block expert histogram of the slots [b·chunk, (b+1)·chunk).  Slots
 // with an expert id outside [0, E) are counted in bad[0] and skipped.
+// Clears the permutation's bad-id counter.  A kernel rather than
+// hipMemsetAsync so that the path stays a plain kernel sequence for callers
+// that capture it into a graph.
+__global__ void zero_i32_kernel(int32_t *__restrict__ p) { *p = 0; }
+
 __global__ __launch_bounds__(256) void perm_count_kernel(const int32_t *__restrict__ idx,
                                                          int64_t n, int E,
                                                          int32_t *__restrict__ block_counts,
@@ -523,7 +530,8 @@ void moe_permute(hipStream_t s, const int32_t *idx, int64_t tokens, int64_t top_
     int32_t *block_counts = reinterpret_cast<int32_t *>(sc);
     int32_t *block_base = reinterpret_cast<int32_t *>(sc + align256((uint64_t)nb * E * 4));
     int32_t *bad = reinterpret_cast<int32_t *>(sc + 2 * align256((uint64_t)nb * E * 4));
-    CATNN_HIP(hipMemsetAsync(bad, 0, 4, s));
+    zero_i32_kernel<<<1, 1, 0, s>>>(bad);
+    CATNN_HIP(hipGetLastError());
     if (nb > 0) {
         perm_count_kernel<<<(unsigned)nb, 256, 0, s>>>(idx, n, E, block_counts, bad);
         CATNN_HIP(hipGetLastError());
@@ -675,6 +683,39 @@ void moe_f32(hipStream_t s, const float *x, const float *gate, const float *cons
     CATNN_HIP(hipGetLastError());
 }
 
+// ---------------------------------------------------------------------
+// Allocation-free MoE layer: its workspace is a fixed device array, so the
+// entry point calls no hipMalloc/hipFree (for callers under HIP graph
+// capture, tight serving loops, harnesses that forbid allocation).  Each GPU
+// holds its own copy of the array from code-object load to process exit.
+namespace noalloc {
+
+static __device__ __align__(256) char scratch[kMoeNoAllocScratchBytes];
+static_assert(kMoeNoAllocScratchBytes == CATNN_MOE_NOALLOC_SCRATCH_BYTES, "header and library agree");
+
+std::mutex g_mu;
+std::vector<void *> g_ptr;  // per device ordinal: the array's device address
+
+}  // namespace noalloc
+
+void *moe_noalloc_scratch(int ordinal, std::string *err) {
+    // Called with `ordinal` current (catnn_hip_open).  The host-side name of
+    // the array is only a stand-in: its device address comes from the
+    // runtime, once per device, and only that address reaches kernels.
+    std::lock_guard<std::mutex> lock(noalloc::g_mu);
+    if ((int)noalloc::g_ptr.size() <= ordinal) noalloc::g_ptr.resize(ordinal + 1, nullptr);
+    if (noalloc::g_ptr[ordinal]) return noalloc::g_ptr[ordinal];
+    void *ptr = nullptr;
+    hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(noalloc::scratch));
+    if (e != hipSuccess || !ptr) {
+        (void)hipGetLastError();
+        if (err) *err = std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e);
+        return nullptr;
+    }
+    noalloc::g_ptr[ordinal] = ptr;
+    return ptr;
+}
+
 }  // namespace k
 }  // namespace catnn
 
@@ -740,6 +781,47 @@ int catnn_hip_moe_f32(catnn_hip_device *dev, const float *x, const float *gate,
         if (w && n)
             CATNN_HIP(hipMemcpyAsync(w, base + L.w, n * 4, hipMemcpyDeviceToDevice, dev->stream));
         if (counts)
+            CATNN_HIP(hipMemcpyAsync(counts, base + L.counts, (uint64_t)n_experts * 4,
+                                     hipMemcpyDeviceToDevice, dev->stream));
+    });
+}
+
+int catnn_hip_moe_f32_noalloc(catnn_hip_device *dev, const float *x, const float *gate,
+                              const float *const *w1s, const float *const *w3s,
+                              const float *const *w2s, int64_t tokens, int64_t hidden,
+                              int64_t intermediate, int64_t n_experts, int64_t top_k, float *out,
+                              int32_t *idx, float *w, int32_t *counts) {
+    return guard([&] {
+        require_device(dev);
+        CATNN_REQUIRE(w1s && w3s && w2s, CATNN_ERR_INVALID_ARGUMENT, "moe: null weight table");
+        CATNN_REQUIRE((x && gate && out) || tokens == 0, CATNN_ERR_INVALID_ARGUMENT,
+                      "moe: null operand");
+        CATNN_REQUIRE(n_experts >= 1 && n_experts <= k::kMaxExperts, CATNN_ERR_SHAPE_MISMATCH,
+                      "moe: n_experts must be in [1, 64]");
+        CATNN_REQUIRE(tokens >= 0 && top_k >= 1 && hidden > 0 && intermediate > 0,
+                      CATNN_ERR_SHAPE_MISMATCH, "moe: bad dims");
+        for (int64_t e = 0; e < n_experts; ++e)
+            CATNN_REQUIRE(w1s[e] && w3s[e] && w2s[e], CATNN_ERR_INVALID_ARGUMENT,
+                          "moe: null expert weight " + std::to_string(e));
+        CATNN_REQUIRE(dev->noalloc_scratch, CATNN_ERR_DEVICE,
+                      "moe_noalloc: no device scratch on this device (" + dev->noalloc_error + ")");
+        const k::MoeWorkspaceLayout L =
+            k::moe_workspace_layout(tokens, hidden, intermediate, n_experts, top_k);
+        CATNN_REQUIRE(L.total <= k::kMoeNoAllocScratchBytes, CATNN_ERR_SHAPE_MISMATCH,
+                      "moe_noalloc: workspace of " + std::to_string(L.total) +
+                          " bytes exceeds the fixed scratch of " +
+                          std::to_string(k::kMoeNoAllocScratchBytes) +
+                          " bytes; use catnn_hip_moe_f32 or fewer tokens");
+        void *ws = dev->noalloc_scratch;
+        k::moe_f32(dev->stream, x, gate, w1s, w3s, w2s, tokens, hidden, intermediate, n_experts,
+                   top_k, out, ws, L);
+        char *base = static_cast<char *>(ws);
+        const uint64_t n = (uint64_t)(tokens * top_k);
+        if (idx && n)
+            CATNN_HIP(hipMemcpyAsync(idx, base + L.idx, n * 4, hipMemcpyDeviceToDevice, dev->stream));
+        if (w && n)
+            CATNN_HIP(hipMemcpyAsync(w, base + L.w, n * 4, hipMemcpyDeviceToDevice, dev->stream));
+        if (counts && tokens > 0)
             CATNN_HIP(hipMemcpyAsync(counts, base + L.counts, (uint64_t)n_experts * 4,
                                      hipMemcpyDeviceToDevice, dev->stream));
     });

@@ -135,6 +135,7 @@ int catnn_hip_open(int32_t ordinal, catnn_hip_device **out) {
             hipDeviceProp_t prop;
             CATNN_HIP(hipGetDeviceProperties(&prop, ordinal));
             dev->cu_count = prop.multiProcessorCount;
+            dev->noalloc_scratch = k::moe_noalloc_scratch(ordinal, &dev->noalloc_error);
         } catch (...) {
             delete dev;
             throw;

@@ -565,6 +565,27 @@ int catnn_hip_moe_f32(catnn_hip_device *dev, const float *x, const float *gate,
                       int64_t intermediate, int64_t n_experts, int64_t top_k,
                       float *out, int32_t *idx, float *w, int32_t *counts);
 
+/* Allocation-free variant of catnn_hip_moe_f32 (same arguments, same
+ * results bit for bit).  No counterpart in the reference: it is for callers
+ * that cannot allocate device memory — code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc.  It calls no hipMalloc,
+ * hipFree or allocating library routine; its workspace (routing, the
+ * permutation and the per-slot expert activations, the layout of
+ * catnn_hip_moe_f32) lives in a fixed device array of
+ * CATNN_MOE_NOALLOC_SCRATCH_BYTES that each GPU holds from library load to
+ * process exit.  A call needing more (about tokens·top_k·4·(intermediate +
+ * hidden + 4) bytes plus a few KiB; e.g. up to ~3,600 tokens at hidden 1024,
+ * intermediate 3584, top-2) fails with CATNN_ERR_SHAPE_MISMATCH before
+ * launching anything.  Every call on a GPU shares that GPU's array: calls
+ * that overlap on one GPU (two devices handles or two threads) race; calls
+ * on one device handle are ordered by its stream. */
+#define CATNN_MOE_NOALLOC_SCRATCH_BYTES (128ull << 20)
+int catnn_hip_moe_f32_noalloc(catnn_hip_device *dev, const float *x, const float *gate,
+                              const float *const *w1s, const float *const *w3s,
+                              const float *const *w2s, int64_t tokens, int64_t hidden,
+                              int64_t intermediate, int64_t n_experts, int64_t top_k, float *out,
+                              int32_t *idx, float *w, int32_t *counts);
+
 #ifdef __cplusplus
 }
 #endif
