@@ -68,13 +68,11 @@ BF16_MFMA_PEAK_TFLOPS = 2500.0
 
 def time_train_step(dev, steps, warmup, opt="sgd"):
     """Config 5: one training step (forward, MSE, backward, SGD) of the
-    config-3 block followed by the config-4 MoE layer.  Every timed step
-    starts from the installed weights (Trainer.reset, outside the timed
-    region): at this initialisation lr 0.05 drives the weights to NaN within
-    two steps, which would collapse the routing and time another workload.
-    With opt="adam" the same step ends in Adam::put at Adam's default lr
-    1e-3 (reset also zeroes the moments, so every timed step is Adam's
-    first)."""
+    config-3 block followed by the config-4 MoE layer.  The timed steps run
+    back to back after the warm-up steps, each updating the weights the next
+    one reads, between one pair of hipEvents.  With opt="adam" the same step
+    ends in Adam::put at Adam's default lr 1e-3.  `first_step_loss` is the
+    loss of one more step from the installed weights."""
     import catnn_amd
     from catnn_amd import configs
 
@@ -83,16 +81,13 @@ def time_train_step(dev, steps, warmup, opt="sgd"):
     tr = catnn_amd.Trainer(dev, wl.graph, wl.lr if opt == "sgd" else 1e-3, opt=opt)
     tr.set_batch(wl.x, wl.target)
     for _ in range(warmup):
-        tr.reset()
-        tr.step()
-    total = 0.0
-    loss = None
-    for _ in range(steps):
-        tr.reset()
-        dev.sync()
-        dev.timer_start()
         tr.step(sync=False)
-        total += dev.timer_stop()
+    dev.sync()
+    dev.timer_start()
+    for _ in range(steps):
+        tr.step(sync=False)
+    total = dev.timer_stop()
+    last = tr.step()
     tr.reset()
     loss = tr.step()
     allocs, reserved = tr.arena()
@@ -104,9 +99,11 @@ def time_train_step(dev, steps, warmup, opt="sgd"):
             "algorithmic_TFLOP_per_s": round(tflops, 2),
             "bf16_mfma_frac": round(tflops / BF16_MFMA_PEAK_TFLOPS, 4),
             "flop_per_step": wl.flops, "first_step_loss": round(loss, 4),
+            "loss_after_timed_steps": round(last, 4),
             "arena_reserved_bytes": reserved, "arena_buffers": len(allocs),
             "precision": "bf16 MFMA, fp32 accumulation and master weights; split-bf16 forward "
-                         "GEMMs for Linear/attention; attention core fp32 MFMA"}
+                         "GEMMs for Linear/attention, split-bf16 input to the MoE gate/up GEMM; "
+                         "attention core fp32 MFMA"}
 
 
 def time_mixtral(dev, steps, warmup):
@@ -238,7 +235,6 @@ def pmc_probe(which):
         tr = catnn_amd.Trainer(dev, wl.graph, wl.lr)
         tr.set_batch(wl.x, wl.target)
         for i in range(3):
-            tr.reset()
             tr.step()
             log(f"config5: step {i} done")
         tr.free()

@@ -21,10 +21,12 @@
 //
 // Precision: every GEMM runs on v_mfma_f32_32x32x16_bf16 with fp32
 // accumulation.  The forward GEMMs of Linear and attention take split-bf16
-// operands (hi|hi|lo against hi|lo|hi over 3K: the fp32 product to ~2⁻¹⁶),
+// operands (hi|lo|hi against hi|hi|lo over 3K: the fp32 product to ~2⁻¹⁶),
 // because with plain bf16 operands there the error of the block's output
 // reaches the MoE layer and moves the step's gradients by more than 1e-2
-// from the fp32 path; the MoE expert forward and every backward GEMM take
+// from the fp32 path.  The MoE gate/up GEMM takes its input split (hi|lo
+// against the weights' hi|hi, 2K: x at split precision, the expert weights
+// rounded once), the rest of the MoE expert forward and every backward GEMM
 // plain bf16 operands.  Master weights, the residual stream, LayerNorm,
 // softmax statistics, the router and all cotangent accumulation stay fp32;
 // the attention core runs on fp32 MFMA.
@@ -69,7 +71,7 @@ struct TParam {
     float *master = nullptr, *grad = nullptr;
     float *m = nullptr, *v = nullptr;  // Adam moments "adam:{node}:{port}:m|v"
     bf16_t *b = nullptr, *bt = nullptr;
-    bf16_t *bt3 = nullptr;  // [cols, 3·rows] split-bf16 transposed copy (hi | lo | hi)
+    bf16_t *bt3 = nullptr;  // [cols, 3·rows] split-bf16 transposed copy (hi | hi | lo)
     // Held as the transpose of the graph's tensor (LmHead's w [V, H] is kept
     // as wᵀ [H, V], a Linear weight, as adjoint.rs:903-913 transposes it);
     // reads transpose back.
@@ -516,12 +518,12 @@ static void plan_trainer(Tr &t) {
                 add_param(tn, "gate", H, E, false, false, host(nd, "gate")->data);
                 for (int64_t e = 0; e < E; ++e) {
                     const std::string p = "e" + std::to_string(e);
-                    add_param(tn, p + ".w1", H, I, true, true, host(nd, p + ".w1")->data);
-                    add_param(tn, p + ".w3", H, I, true, true, host(nd, p + ".w3")->data);
+                    add_param(tn, p + ".w1", H, I, true, false, host(nd, p + ".w1")->data, true);
+                    add_param(tn, p + ".w3", H, I, true, false, host(nd, p + ".w3")->data, true);
                     add_param(tn, p + ".w2", I, H, true, true, host(nd, p + ".w2")->data);
                 }
                 const int64_t max_tiles = (T * K + k::gemm_bf16_tile_rows() - 1) / k::gemm_bf16_tile_rows() + E;
-                tape(tn, "xb", (uint64_t)(T * H) * 2);
+                tape(tn, "x3", (uint64_t)(T * 3 * H) * 2);
                 tape(tn, "idx", (uint64_t)(T * K) * 4, true);  // readable after the step
                 tape(tn, "w", (uint64_t)(T * K) * 4);
                 tape(tn, "counts", (uint64_t)E * 4);
@@ -662,7 +664,7 @@ static void forward_node(Tr &t, TNode &tn) {
             for (auto &kv : tn.params) if (kv.first != "b") w = kv.second;
             TParam *b = tn.params.count("b") ? tn.params["b"] : nullptr;
             const int64_t K = w->rows, N = w->cols, M = nx / K;
-            // Split-bf16 forward: [hi|hi|lo]·[hi|lo|hi] over 3K ≈ the fp32 product.
+            // Split-bf16 forward: [hi|lo|hi]·[hi|hi|lo] over 3K ≈ the fp32 product.
             bf16_t *x3 = (bf16_t *)tn.B("x3");
             k::split3_rows(s, x, K, M, (int)K, x3, 3 * K);
             k::GemmBf16Params p = gp();
@@ -744,19 +746,20 @@ static void forward_node(Tr &t, TNode &tn) {
             k::moe_route_f32(s, x, tn.params["gate"]->master, T, H, E, K, idx, w, nullptr);
             k::moe_permute_padded(s, idx, T, K, E, kPad, Pr, counts, offs, sop, pos, tn.B("perm_scratch"));
             k::build_tiles(s, offs, (int)E, tiles, tiles + max_tiles, tiles + 2 * max_tiles);
-            bf16_t *xb = (bf16_t *)tn.B("xb");
-            k::cast_f32_bf16(s, x, xb, T * H);
+            bf16_t *x3 = (bf16_t *)tn.B("x3");
+            k::split3_rows(s, x, H, T, (int)H, x3, 3 * H);
             k::GemmBf16Params p = gp();
             p.grid = k::GRID_ROWS;
             p.tile_expert = tiles; p.tile_row0 = tiles + max_tiles; p.n_tiles = tiles + 2 * max_tiles;
             p.seg_offsets = offs; p.seg_counts = counts; p.max_tiles = max_tiles; p.n_experts = (int)E;
-            // gate/up: h = silu(x·w1)·(x·w3), a and c kept for the adjoint
-            p.A = xb; p.lda = H; p.a_rows = sop; p.a_row_div = (int)K;
+            // gate/up: h = silu(x·w1)·(x·w3), a and c kept for the adjoint;
+            // [hi|lo] of x against [hi|hi] of the weights over 2H.
+            p.A = x3; p.lda = 3 * H; p.a_rows = sop; p.a_row_div = (int)K;
             for (int64_t e = 0; e < E; ++e) {
-                p.B_e[e] = tn.params["e" + std::to_string(e) + ".w1"]->bt;
-                p.B2_e[e] = tn.params["e" + std::to_string(e) + ".w3"]->bt;
+                p.B_e[e] = tn.params["e" + std::to_string(e) + ".w1"]->bt3;
+                p.B2_e[e] = tn.params["e" + std::to_string(e) + ".w3"]->bt3;
             }
-            p.ldb = H; p.M = 0; p.N = (int)I; p.K = (int)H;
+            p.ldb = 3 * H; p.M = 0; p.N = (int)I; p.K = (int)(2 * H);
             p.epi = k::EPI_SWIGLU_FWD;
             p.Cb = (bf16_t *)tn.B("h"); p.ldcb = I;
             p.S1 = (bf16_t *)tn.B("a"); p.S2 = (bf16_t *)tn.B("c"); p.lds = I;
@@ -963,7 +966,7 @@ static void backward_node(Tr &t, TNode &tn) {
             // Expert weight gradients: each expert reduces over its own segment.
             bf16_t *xpt = (bf16_t *)tn.B("xpt"), *ht = (bf16_t *)tn.B("ht"), *dyst = (bf16_t *)tn.B("dyst");
             bf16_t *dat = (bf16_t *)tn.B("dat"), *dct = (bf16_t *)tn.B("dct");
-            k::transpose_bf16(s, (bf16_t *)tn.B("xb"), H, sop, (int)K, (int)Pr, (int)H, xpt, Pr);
+            k::transpose_bf16(s, (bf16_t *)tn.B("x3"), 3 * H, sop, (int)K, (int)Pr, (int)H, xpt, Pr);  // hi part of x
             k::transpose_bf16(s, (bf16_t *)tn.B("h"), I, nullptr, 1, (int)Pr, (int)I, ht, Pr);
             k::transpose_bf16(s, dys, H, nullptr, 1, (int)Pr, (int)H, dyst, Pr);
             k::transpose_bf16(s, da, I, nullptr, 1, (int)Pr, (int)I, dat, Pr);

@@ -167,15 +167,17 @@ __global__ __launch_bounds__(256) void transpose_vec_kernel(const TS *__restrict
 }
 
 // Split-bf16 operands.  v = hi + lo + O(2⁻¹⁷|v|) with hi = bf16(v) and
-// lo = bf16(v − hi).  A row of A' = [hi | hi | lo] against a row of
-// B' = [hi | lo | hi] sums to hi·hi + hi·lo + lo·hi over 3K: an fp32 product
-// to ~2⁻¹⁶ relative on the bf16 matrix cores (the dropped lo·lo term).
+// lo = bf16(v − hi).  A row of A' = [hi | lo | hi] against a row of
+// B' = [hi | hi | lo] sums to hi·hi + lo·hi + hi·lo over 3K: an fp32 product
+// to ~2⁻¹⁶ relative on the bf16 matrix cores (the dropped lo·lo term).  The
+// first 2K alone, [hi | lo] against [hi | hi], give (hi + lo)·hi: A at split
+// precision against B rounded once to bf16.
 __device__ __forceinline__ void split_bf16(float v, bf16_t &hi, bf16_t &lo) {
     hi = f2bf(v);
     lo = f2bf(v - __uint_as_float((uint32_t)hi << 16));
 }
 
-// out[r] = [hi(x[r]) | hi(x[r]) | lo(x[r])], rows of K.
+// out[r] = [hi(x[r]) | lo(x[r]) | hi(x[r])], rows of K.
 __global__ void split3_rows_kernel(const float *__restrict__ x, int64_t ldx, int64_t rows, int K,
                                    bf16_t *__restrict__ out, int64_t ldo) {
     const int64_t n = rows * K;
@@ -187,8 +189,8 @@ __global__ void split3_rows_kernel(const float *__restrict__ x, int64_t ldx, int
         split_bf16(x[r * ldx + c], hi, lo);
         bf16_t *o = out + r * ldo;
         o[c] = hi;
-        o[K + c] = hi;
-        o[2 * K + c] = lo;
+        o[K + c] = lo;
+        o[2 * K + c] = hi;
     }
 }
 
@@ -209,12 +211,12 @@ __global__ __launch_bounds__(256) void split3_rows4_kernel(const float4 *__restr
         const uint2 hv = pack4(h[0], h[1], h[2], h[3]);
         uint2 *o = out + r * ldo4;
         o[c] = hv;
-        o[K4 + c] = hv;
-        o[2 * K4 + c] = pack4(l[0], l[1], l[2], l[3]);
+        o[K4 + c] = pack4(l[0], l[1], l[2], l[3]);
+        o[2 * K4 + c] = hv;
     }
 }
 
-// w [K, N] row-major → out [N, 3K] with out[n] = [hi(w[:,n]) | lo(w[:,n]) | hi(w[:,n])].
+// w [K, N] row-major → out [N, 3K] with out[n] = [hi(w[:,n]) | hi(w[:,n]) | lo(w[:,n])].
 __global__ __launch_bounds__(256) void transpose_split3_kernel(const float *__restrict__ w, int64_t ldw,
                                                                int K, int N, bf16_t *__restrict__ out,
                                                                int64_t ldo) {
@@ -234,8 +236,8 @@ __global__ __launch_bounds__(256) void transpose_split3_kernel(const float *__re
         if (n < N && k < K) {
             bf16_t *o = out + (int64_t)n * ldo;
             o[k] = th[tx][i];
-            o[K + k] = tl[tx][i];
-            o[2 * K + k] = th[tx][i];
+            o[K + k] = th[tx][i];
+            o[2 * K + k] = tl[tx][i];
         }
     }
 }
@@ -898,8 +900,8 @@ __global__ __launch_bounds__(256) void sgd_multi_kernel(const SgdParam *__restri
                                                 tl[rq + 2][i] | (uint32_t)tl[rq + 3][i] << 16);
                     bf16_t *o = P.bt3 + (int64_t)c * 3 * P.rows;
                     *reinterpret_cast<uint2 *>(o + r) = hv;
-                    *reinterpret_cast<uint2 *>(o + P.rows + r) = lv;
-                    *reinterpret_cast<uint2 *>(o + 2 * P.rows + r) = hv;
+                    *reinterpret_cast<uint2 *>(o + P.rows + r) = hv;
+                    *reinterpret_cast<uint2 *>(o + 2 * P.rows + r) = lv;
                 }
             }
         }
@@ -911,8 +913,8 @@ __global__ __launch_bounds__(256) void sgd_multi_kernel(const SgdParam *__restri
                 if (P.bt3) {
                     bf16_t *o = P.bt3 + (int64_t)c * 3 * P.rows;
                     o[r] = th[tx][i];
-                    o[P.rows + r] = tl[tx][i];
-                    o[2 * P.rows + r] = th[tx][i];
+                    o[P.rows + r] = th[tx][i];
+                    o[2 * P.rows + r] = tl[tx][i];
                 }
             }
         }

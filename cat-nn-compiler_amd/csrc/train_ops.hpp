@@ -20,8 +20,8 @@ void transpose_bf16(hipStream_t s, const bf16_t *src, int64_t lds, const int32_t
 void transpose_f32_bf16(hipStream_t s, const float *src, int64_t lds, const int32_t *rows_map,
                         int div, int rows, int cols, bf16_t *dst, int64_t ldd);
 
-// Split-bf16 GEMM operands: A' rows [hi | hi | lo] from fp32 rows of K
-// (out row stride ldo ≥ 3K) and B' = [hi | lo | hi] rows from the columns of
+// Split-bf16 GEMM operands: A' rows [hi | lo | hi] from fp32 rows of K
+// (out row stride ldo ≥ 3K) and B' = [hi | hi | lo] rows from the columns of
 // an fp32 [K, N] matrix, so the bf16 GEMM over K' = 3K yields hi·hi + hi·lo
 // + lo·hi ≈ the fp32 product (relative error ~2⁻¹⁶).
 void split3_rows(hipStream_t s, const float *x, int64_t ldx, int64_t rows, int K, bf16_t *out,
@@ -96,7 +96,7 @@ void apply_update(hipStream_t s, const UpdateRule &u, float *p, const float *g, 
 // One parameter of the multi-tensor update: fp32 master p [rows, cols] and
 // its gradient g (same layout, or null: refresh only), and the bf16 copies
 // to rewrite from the new value: b [rows, cols], bt [cols, rows] and the
-// split-bf16 transposed bt3 [cols, 3·rows] = hi | lo | hi (each may be null).
+// split-bf16 transposed bt3 [cols, 3·rows] = hi | hi | lo (each may be null).
 struct SgdParam {
     float *p;
     const float *g;

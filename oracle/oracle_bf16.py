@@ -60,10 +60,11 @@ def bf16_split(a):
 
 SITES = ("linear_fwd", "linear_bwd", "attn_fwd", "attn_bwd", "moe_fwd", "moe_bwd")
 # The GPU trainer's policy: split-bf16 forward GEMMs for Linear and attention
-# (hi·hi + hi·lo + lo·hi), plain bf16 operands for the MoE experts and every
-# backward GEMM.
+# (hi·hi + hi·lo + lo·hi); the MoE gate/up GEMM with its input split and the
+# expert weights rounded ("xsplit": (hi + lo)·bf16(w)); plain bf16 operands
+# for the rest of the MoE experts and every backward GEMM.
 DEVICE = {"linear_fwd": "split", "attn_fwd": "split", "linear_bwd": "bf16", "attn_bwd": "bf16",
-          "moe_fwd": "bf16", "moe_bwd": "bf16"}
+          "moe_fwd": "xsplit", "moe_bwd": "bf16"}
 WIDE = {site: "wide" for site in SITES}
 BF16 = {site: "bf16" for site in SITES}
 
@@ -137,7 +138,11 @@ class Model:
             w = w.astype(F64)
             y = np.zeros((T, H))
             saved = {}
-            xb = rb(xt)
+            if self.policy.get("moe_fwd") == "xsplit":
+                hi, lo = bf16_split(xt)
+                xb = hi + lo
+            else:
+                xb = rb(xt)
             for e in range(E):
                 tok, j = np.nonzero(idx == e)
                 if tok.size == 0:

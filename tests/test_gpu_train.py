@@ -149,9 +149,8 @@ def test_block_plus_moe_ragged(device):
 @pytest.mark.parametrize("which", ["block", "moe"])
 def test_three_steps_follow_the_oracle(device, which):
     # Parameters persist on the device between steps; the fp32 reference is
-    # re-run from its own updated parameters.  (Config 5 itself is not used:
-    # at its initialisation lr 0.05 overshoots, 7.5e2 → 1.5e10 → NaN, in the
-    # reference as on the device.)
+    # re-run from its own updated parameters.  (Config 5's three full-size
+    # steps are in test_gpu_fullsize.py.)
     if which == "block":
         w = configs.config3(batch=1, seq=64, d=128, heads=2, ffn=256)
     else:
