@@ -173,6 +173,7 @@ SIGNATURES = {
     "catnn_hip_train_arena": [_VP, ctypes.POINTER(CArenaAlloc), _I32, _PI32, _PU64],
     "catnn_hip_events": [_VP, ctypes.POINTER(CEvent), _I32, _PI32],
     "catnn_hip_clear_events": [_VP],
+    "catnn_hip_trace_checksums": [_VP, _I32],
     "catnn_hip_linear_f32": [_VP, _VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _I32],
     "catnn_hip_gemm_bf16_nt": [_VP, _VP, _I64, _VP, _I64, _VP, _I64, _I64, _I64, _I64, _I32, _I32],
     "catnn_hip_act_f32": [_VP, _VP, _VP, _I64, _I32],

@@ -99,6 +99,11 @@ class Device:
     def clear_events(self):
         check(lib.catnn_hip_clear_events(self.handle))
 
+    def trace_checksums(self, enable: bool):
+        """Whether run_node's KernelEnd event carries the output's FNV-1a
+        checksum (a device-to-host copy and a sync per node; on by default)."""
+        check(lib.catnn_hip_trace_checksums(self.handle, int(bool(enable))))
+
     # -- the device arena (buffer-id API) -------------------------------------
     def arena_reserve(self, nbytes: int):
         check(lib.catnn_hip_arena_reserve(self.handle, nbytes))

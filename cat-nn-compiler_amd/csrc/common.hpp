@@ -67,10 +67,22 @@ struct Workspace {
 
 }  // namespace catnn
 
+struct catnn_adjoint_cache;  // one-node trainers kept by catnn_hip_run_adjoint (train.cpp)
+
 struct catnn_hip_device {
     int ordinal = 0;
     hipStream_t stream = nullptr;
     hipEvent_t t_start = nullptr, t_stop = nullptr;
+    // Sheaf events are stamped on the device: each kernel event records a
+    // hipEvent on the stream; its time is resolved when the events are read
+    // (catnn_hip_events), as the previous stamp plus the device time between
+    // them, starting from ev_epoch (recorded at open, host time `epoch`).
+    hipEvent_t ev_epoch = nullptr, ev_last = nullptr;
+    double last_ns = 0.0;
+    std::vector<std::pair<size_t, hipEvent_t>> ev_pending;  // (index in events, stamp)
+    std::vector<hipEvent_t> ev_pool;
+    bool trace_checksums = true;  // run_node: FNV-1a of the output on KernelEnd
+    catnn_adjoint_cache *adj_cache = nullptr;
     void *arena = nullptr;
     uint64_t arena_bytes = 0;
     std::unordered_map<std::string, catnn::Binding> bindings;
@@ -90,7 +102,14 @@ void require_device(catnn_hip_device *dev);
 void *buffer(catnn_hip_device *dev, const std::string &id, uint64_t *bytes = nullptr);
 // Make sure dev->moe_ws holds at least `bytes`.
 void *workspace(catnn_hip_device *dev, Workspace &ws, uint64_t bytes);
-void push_event(catnn_hip_device *dev, const std::string &op, int kind, uint64_t checksum);
+// Appends a sheaf event stamped by a hipEvent recorded on dev's stream now
+// (the time of the work enqueued before it); returns its index in
+// dev->events so that the checksum can be filled in afterwards.
+size_t push_device_event(catnn_hip_device *dev, const std::string &op, int kind, uint64_t checksum);
+// Waits for the pending stamps and turns them into nanoseconds.
+void resolve_events(catnn_hip_device *dev);
+// The one-node trainers of catnn_hip_run_adjoint, freed with the device.
+void free_adjoint_cache(catnn_hip_device *dev);
 uint64_t fnv1a_f32(const float *data, uint64_t n);
 
 }  // namespace catnn

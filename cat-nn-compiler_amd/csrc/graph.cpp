@@ -912,7 +912,6 @@ int catnn_hip_run_kernel(catnn_hip_device *dev, const catnn_node *node, const ca
         total += rnd((uint64_t)n_out * 4);
         const uint64_t scr_off = total;
         total += rnd(scr);
-        push_event(dev, n.name, CATNN_EV_KERNEL_START, 0);
         char *base = static_cast<char *>(workspace(dev, dev->moe_ws, std::max<uint64_t>(total, 256)));
         for (size_t i = 0; i < ins.size(); ++i)
             if (ins[i].numel())
@@ -936,7 +935,9 @@ int catnn_hip_run_kernel(catnn_hip_device *dev, const catnn_node *node, const ca
             a.scratch = reinterpret_cast<float *>(base + scr_off);
             a.scratch_bytes = scr;
         }
+        push_device_event(dev, n.name, CATNN_EV_KERNEL_START, 0);
         exec_node(dev, n, a);
+        const size_t end_ev = push_device_event(dev, n.name, CATNN_EV_KERNEL_END, 0);
         if (n_out)
             CATNN_HIP(hipMemcpyAsync(out->data, base + out_off, (size_t)n_out * 4,
                                      hipMemcpyDeviceToHost, dev->stream));
@@ -944,7 +945,7 @@ int catnn_hip_run_kernel(catnn_hip_device *dev, const catnn_node *node, const ca
         out->rank = (int32_t)od.size();
         for (size_t i = 0; i < od.size(); ++i) out->dims[i] = od[i];
         out->dtype = ins.empty() ? n.output_ty.dtype : ins[0].dtype;
-        push_event(dev, n.name, CATNN_EV_KERNEL_END, fnv1a_f32(out->data, (uint64_t)n_out));
+        dev->events[end_ev].checksum = fnv1a_f32(out->data, (uint64_t)n_out);
     });
 }
 
@@ -985,9 +986,18 @@ int catnn_hip_run_node(catnn_hip_device *dev, const catnn_node *node, const char
             a.scratch = static_cast<float *>(workspace(dev, dev->moe_ws, scr));
             a.scratch_bytes = scr;
         }
-        push_event(dev, n.name, CATNN_EV_KERNEL_START, 0);
+        push_device_event(dev, n.name, CATNN_EV_KERNEL_START, 0);
         exec_node(dev, n, a);
-        push_event(dev, n.name, CATNN_EV_KERNEL_END, 0);
+        const size_t end_ev = push_device_event(dev, n.name, CATNN_EV_KERNEL_END, 0);
+        if (dev->trace_checksums) {
+            const int64_t n_out = numel_of(od);
+            std::vector<float> host((size_t)n_out);
+            if (n_out)
+                CATNN_HIP(hipMemcpyAsync(host.data(), a.out, (size_t)n_out * 4, hipMemcpyDeviceToHost,
+                                         dev->stream));
+            CATNN_HIP(hipStreamSynchronize(dev->stream));
+            dev->events[end_ev].checksum = fnv1a_f32(host.data(), (uint64_t)n_out);
+        }
     });
 }
 

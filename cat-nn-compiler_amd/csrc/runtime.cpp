@@ -4,6 +4,8 @@
 // device, one in-order stream, events timestamped in ns from open.
 #include <hip/hip_runtime_api.h>
 
+#include <algorithm>
+#include <cmath>
 #include <cstring>
 #include <string>
 
@@ -46,17 +48,44 @@ void *workspace(catnn_hip_device *dev, Workspace &ws, uint64_t bytes) {
     return ws.ptr;
 }
 
-void push_event(catnn_hip_device *dev, const std::string &op, int kind, uint64_t checksum) {
-    catnn_event ev{};
-    ev.t_ns = (uint64_t)std::chrono::duration_cast<std::chrono::nanoseconds>(
-                  std::chrono::steady_clock::now() - dev->epoch)
-                  .count();
-    if (!dev->events.empty() && ev.t_ns <= dev->events.back().t_ns)
-        ev.t_ns = dev->events.back().t_ns + 1;  // strictly increasing, as handler.rs:47
-    std::strncpy(ev.op, op.c_str(), CATNN_ID_CAP - 1);
-    ev.kind = kind;
-    ev.checksum = checksum;
-    dev->events.push_back(ev);
+size_t push_device_event(catnn_hip_device *dev, const std::string &op, int kind, uint64_t checksum) {
+    hipEvent_t ev = nullptr;
+    if (!dev->ev_pool.empty()) {
+        ev = dev->ev_pool.back();
+        dev->ev_pool.pop_back();
+    } else {
+        CATNN_HIP(hipEventCreate(&ev));
+    }
+    hipError_t e = hipEventRecord(ev, dev->stream);
+    if (e != hipSuccess) {
+        dev->ev_pool.push_back(ev);
+        fail(CATNN_ERR_DEVICE, std::string("hipEventRecord: ") + hipGetErrorString(e));
+    }
+    catnn_event rec{};
+    std::strncpy(rec.op, op.c_str(), CATNN_ID_CAP - 1);
+    rec.kind = kind;
+    rec.checksum = checksum;
+    dev->events.push_back(rec);
+    dev->ev_pending.emplace_back(dev->events.size() - 1, ev);
+    return dev->events.size() - 1;
+}
+
+void resolve_events(catnn_hip_device *dev) {
+    // Stamps complete in stream order; each adds the device time since the
+    // previous one, so long runs keep sub-microsecond spacing.
+    for (auto &pe : dev->ev_pending) {
+        CATNN_HIP(hipEventSynchronize(pe.second));
+        float ms = 0.f;
+        CATNN_HIP(hipEventElapsedTime(&ms, dev->ev_last ? dev->ev_last : dev->ev_epoch, pe.second));
+        dev->last_ns += (double)ms * 1e6;
+        if (dev->ev_last) dev->ev_pool.push_back(dev->ev_last);
+        dev->ev_last = pe.second;
+        uint64_t t = (uint64_t)std::llround(std::max(0.0, dev->last_ns));
+        const size_t i = pe.first;
+        if (i > 0 && t <= dev->events[i - 1].t_ns) t = dev->events[i - 1].t_ns + 1;  // handler.rs:47
+        dev->events[i].t_ns = t;
+    }
+    dev->ev_pending.clear();
 }
 
 // FNV-1a over the f32 bit patterns, one 32-bit word per step, as
@@ -136,6 +165,10 @@ int catnn_hip_open(int32_t ordinal, catnn_hip_device **out) {
             CATNN_HIP(hipGetDeviceProperties(&prop, ordinal));
             dev->cu_count = prop.multiProcessorCount;
             dev->noalloc_scratch = k::moe_noalloc_scratch(ordinal, &dev->noalloc_error);
+            CATNN_HIP(hipEventCreate(&dev->ev_epoch));
+            CATNN_HIP(hipEventRecord(dev->ev_epoch, dev->stream));
+            CATNN_HIP(hipEventSynchronize(dev->ev_epoch));
+            dev->epoch = std::chrono::steady_clock::now();
         } catch (...) {
             delete dev;
             throw;
@@ -150,6 +183,11 @@ int catnn_hip_close(catnn_hip_device *dev) {
         // Best effort: a failure here leaves nothing the caller can retry.
         (void)hipSetDevice(dev->ordinal);
         if (dev->stream) (void)hipStreamSynchronize(dev->stream);
+        free_adjoint_cache(dev);
+        for (auto &pe : dev->ev_pending) (void)hipEventDestroy(pe.second);
+        for (hipEvent_t ev : dev->ev_pool) (void)hipEventDestroy(ev);
+        if (dev->ev_last) (void)hipEventDestroy(dev->ev_last);
+        if (dev->ev_epoch) (void)hipEventDestroy(dev->ev_epoch);
         for (void *p : dev->allocations) (void)hipFree(p);
         if (dev->arena) (void)hipFree(dev->arena);
         if (dev->moe_ws.ptr) (void)hipFree(dev->moe_ws.ptr);
@@ -334,6 +372,8 @@ int catnn_hip_timer_stop(catnn_hip_device *dev, float *ms) {
 int catnn_hip_events(catnn_hip_device *dev, catnn_event *buf, int32_t cap, int32_t *n) {
     return guard([&] {
         CATNN_REQUIRE(dev && n, CATNN_ERR_INVALID_ARGUMENT, "null argument");
+        require_device(dev);
+        resolve_events(dev);
         const int32_t total = (int32_t)dev->events.size();
         *n = total;
         if (!buf) return;
@@ -344,7 +384,16 @@ int catnn_hip_events(catnn_hip_device *dev, catnn_event *buf, int32_t cap, int32
 int catnn_hip_clear_events(catnn_hip_device *dev) {
     return guard([&] {
         CATNN_REQUIRE(dev, CATNN_ERR_INVALID_ARGUMENT, "null device handle");
+        require_device(dev);
+        resolve_events(dev);  // keeps the chain of stamps for the next events
         dev->events.clear();
+    });
+}
+
+int catnn_hip_trace_checksums(catnn_hip_device *dev, int32_t enable) {
+    return guard([&] {
+        CATNN_REQUIRE(dev, CATNN_ERR_INVALID_ARGUMENT, "null device handle");
+        dev->trace_checksums = enable != 0;
     });
 }
 

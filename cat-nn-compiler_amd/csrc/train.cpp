@@ -200,6 +200,41 @@ void add_into(hipStream_t s, float *dst, const float *src, int64_t n, bool overw
     else k::add_f32(s, dst, src, dst, n, n);
 }
 
+// The host values of trainer parameter `port` of node `nd`, in the layout
+// the trainer keeps it: Attention's "wqkv" packs [wq | wk | wv] per row
+// ([D, 3D]); LmHead's "w" [V, H] is held as wᵀ [H, V]; every other port is
+// the node's tensor as it is.
+std::vector<float> param_values(const Node &nd, const std::string &port) {
+    auto host = [&](const std::string &p) {
+        const HostTensor *h = nd.param(p);
+        if (!h) fail(CATNN_ERR_UNKNOWN_PORT, "unknown port " + p + " on interface " + nd.name);
+        return h;
+    };
+    if (nd.op.kind == CATNN_OP_ATTENTION && port == "wqkv") {
+        const HostTensor *wq = host("wq"), *wk = host("wk"), *wv = host("wv");
+        const int64_t D = wq->dims.empty() ? 0 : wq->dims[0];
+        CATNN_REQUIRE(wq->numel() == D * D && wk->numel() == D * D && wv->numel() == D * D,
+                      CATNN_ERR_SHAPE_MISMATCH, "attention projections");
+        std::vector<float> packed((size_t)(D * 3 * D));
+        for (int64_t r = 0; r < D; ++r) {
+            std::memcpy(&packed[(size_t)(r * 3 * D)], &wq->data[(size_t)(r * D)], (size_t)D * 4);
+            std::memcpy(&packed[(size_t)(r * 3 * D + D)], &wk->data[(size_t)(r * D)], (size_t)D * 4);
+            std::memcpy(&packed[(size_t)(r * 3 * D + 2 * D)], &wv->data[(size_t)(r * D)], (size_t)D * 4);
+        }
+        return packed;
+    }
+    if (nd.op.kind == CATNN_OP_LM_HEAD && port == "w") {
+        const HostTensor *w = host("w");
+        const int64_t V = nd.op.a[1], K = nd.op.a[0];
+        CATNN_REQUIRE(w->numel() == V * K, CATNN_ERR_SHAPE_MISMATCH, "lm_head w");
+        std::vector<float> wt((size_t)(V * K));
+        for (int64_t v = 0; v < V; ++v)
+            for (int64_t h = 0; h < K; ++h) wt[(size_t)(h * V + v)] = w->data[(size_t)(v * K + h)];
+        return wt;
+    }
+    return host(port)->data;
+}
+
 }  // namespace
 
 static void plan_trainer(Tr &t) {
@@ -461,10 +496,7 @@ static void plan_trainer(Tr &t) {
                 const HostTensor *w = host(nd, "w");
                 const int64_t V = nd.op.a[1], K = nd.op.a[0], M = numel(x) / K;
                 CATNN_REQUIRE(w->numel() == V * K, CATNN_ERR_SHAPE_MISMATCH, "lm_head w");
-                std::vector<float> wt((size_t)(V * K));
-                for (int64_t v = 0; v < V; ++v)
-                    for (int64_t h = 0; h < K; ++h) wt[(size_t)(h * V + v)] = w->data[(size_t)(v * K + h)];
-                add_param(tn, "w", K, V, true, false, std::move(wt), true);
+                add_param(tn, "w", K, V, true, false, param_values(nd, "w"), true);
                 tn.params["w"]->transposed = true;
                 tape(tn, "x3", (uint64_t)(M * 3 * K) * 2);
                 scratch(tn, "xbt", (uint64_t)(M * K) * 2);
@@ -484,14 +516,7 @@ static void plan_trainer(Tr &t) {
             }
             case CATNN_OP_ATTENTION: {
                 const int64_t Bt = x[0], S = x[1], D = x[2], T = Bt * S, H = nd.op.a[0];
-                std::vector<float> packed((size_t)(D * 3 * D));
-                const HostTensor *wq = host(nd, "wq"), *wk = host(nd, "wk"), *wv = host(nd, "wv");
-                for (int64_t r = 0; r < D; ++r) {
-                    std::memcpy(&packed[(size_t)(r * 3 * D)], &wq->data[(size_t)(r * D)], (size_t)D * 4);
-                    std::memcpy(&packed[(size_t)(r * 3 * D + D)], &wk->data[(size_t)(r * D)], (size_t)D * 4);
-                    std::memcpy(&packed[(size_t)(r * 3 * D + 2 * D)], &wv->data[(size_t)(r * D)], (size_t)D * 4);
-                }
-                add_param(tn, "wqkv", D, 3 * D, true, false, std::move(packed), true);
+                add_param(tn, "wqkv", D, 3 * D, true, false, param_values(nd, "wqkv"), true);
                 add_param(tn, "wo", D, D, true, false, host(nd, "wo")->data, true);
                 tape(tn, "x3", (uint64_t)(T * 3 * D) * 2);
                 tape(tn, "qkv", (uint64_t)(T * 3 * D) * 4);
@@ -1091,6 +1116,86 @@ static void read_cols(Tr &t, const float *src, int64_t rows, int64_t cols, int64
     CATNN_HIP(hipStreamSynchronize(t.dev->stream));
 }
 
+// ------------------------------------------------ adjoint_of plan cache
+// catnn_hip_run_adjoint keeps the one-node trainers it builds, keyed by the
+// node's shape (op, flags, fields, input dims, parameter ports and dims), so
+// a training wave that calls adjoint_of on the same nodes every step plans
+// and hipMallocs each of them once.  At most kAdjointCacheEntries trainers
+// and kAdjointCacheBytes of arena are kept; the least recently used goes
+// first.
+constexpr size_t kAdjointCacheEntries = 16;
+constexpr uint64_t kAdjointCacheBytes = 16ull << 30;
+
+struct TrainerFree {
+    void operator()(catnn_hip_trainer *t) const {
+        if (!t) return;
+        (void)hipSetDevice(t->dev->ordinal);
+        (void)hipStreamSynchronize(t->dev->stream);
+        if (t->base) (void)hipFree(t->base);
+        delete t;
+    }
+};
+
+}  // namespace catnn
+
+struct catnn_adjoint_cache {
+    struct Entry {
+        std::string key;
+        std::unique_ptr<catnn_hip_trainer, catnn::TrainerFree> t;
+        uint64_t used;
+    };
+    std::vector<Entry> entries;
+    uint64_t clock = 0;
+};
+
+namespace catnn {
+
+static std::string adjoint_key(const catnn_node *node, const catnn_tensor *inputs, int32_t n_inputs) {
+    std::string k = std::to_string(node->op.kind) + "|" + std::to_string(node->op.flags);
+    for (int i = 0; i < 8; ++i) k += "," + std::to_string(node->op.a[i]);
+    for (int32_t i = 0; i < n_inputs; ++i) {
+        k += "|in";
+        for (int64_t d : dims_from_c(inputs[i])) k += "," + std::to_string(d);
+    }
+    for (int32_t j = 0; j < node->n_params; ++j) {
+        k += "|" + std::string(node->params[j].port ? node->params[j].port : "");
+        for (int64_t d : dims_from_c(node->params[j].value)) k += "," + std::to_string(d);
+    }
+    return k;
+}
+
+static catnn_hip_trainer *adjoint_cache_find(catnn_hip_device *dev, const std::string &key) {
+    if (!dev->adj_cache) return nullptr;
+    for (auto &e : dev->adj_cache->entries)
+        if (e.key == key) {
+            e.used = ++dev->adj_cache->clock;
+            return e.t.get();
+        }
+    return nullptr;
+}
+
+static catnn_hip_trainer *adjoint_cache_insert(catnn_hip_device *dev, const std::string &key,
+                                               std::unique_ptr<catnn_hip_trainer, TrainerFree> t) {
+    if (!dev->adj_cache) dev->adj_cache = new catnn_adjoint_cache();
+    auto &es = dev->adj_cache->entries;
+    auto bytes = [&] {
+        uint64_t b = t->reserved;
+        for (auto &e : es) b += e.t->reserved;
+        return b;
+    };
+    while (!es.empty() && (es.size() >= kAdjointCacheEntries || bytes() > kAdjointCacheBytes)) {
+        auto lru = std::min_element(es.begin(), es.end(), [](const auto &a, const auto &b) { return a.used < b.used; });
+        es.erase(lru);
+    }
+    es.push_back({key, std::move(t), ++dev->adj_cache->clock});
+    return es.back().t.get();
+}
+
+void free_adjoint_cache(catnn_hip_device *dev) {
+    delete dev->adj_cache;
+    dev->adj_cache = nullptr;
+}
+
 }  // namespace catnn
 
 using namespace catnn;
@@ -1303,44 +1408,55 @@ int catnn_hip_run_adjoint(catnn_hip_device *dev, const catnn_node *node, const c
         CATNN_REQUIRE(n_dparams == node->n_params, CATNN_ERR_SHAPE_MISMATCH,
                       "run_adjoint: " + std::to_string(n_dparams) + " parameter cotangents for " +
                           std::to_string(node->n_params) + " params");
-        // The one-node graph in0 … in{n-1} → node, its preds in edge order.
         auto ok = [](int rc) {
             if (rc != CATNN_OK) fail(rc, catnn_hip_last_error());
         };
-        catnn_graph g;
-        g.name = "adjoint";
         const uint32_t nid = (uint32_t)n_inputs;
-        std::vector<std::string> names;
-        for (int32_t i = 0; i < n_inputs; ++i) names.push_back("in" + std::to_string(i));
-        for (int32_t i = 0; i < n_inputs; ++i) {
-            catnn_node in{};
-            in.id = (uint32_t)i;
-            in.name = names[(size_t)i].c_str();
-            in.op.kind = CATNN_OP_IDENTITY;
-            in.output_ty = inputs[i];
-            in.output_ty.data = nullptr;
-            ok(catnn_graph_add_node(&g, &in));
-            ok(catnn_graph_add_input(&g, in.id));
-        }
-        catnn_node self = *node;
-        self.id = nid;
-        ok(catnn_graph_add_node(&g, &self));
-        for (int32_t i = 0; i < n_inputs; ++i) ok(catnn_graph_add_edge(&g, (uint32_t)i, nid, "out", "in"));
-        ok(catnn_graph_add_output(&g, nid));
-
-        std::unique_ptr<catnn_hip_trainer> t(new catnn_hip_trainer());
-        struct Free {
-            catnn_hip_trainer *t;
-            ~Free() {
-                if (t->base) (void)hipFree(t->base);
+        const std::string key = adjoint_key(node, inputs, n_inputs);
+        catnn_hip_trainer *t = adjoint_cache_find(dev, key);
+        if (t) {
+            // The same node shape ran before: its plan and arena are reused and
+            // only the parameter values are replaced.
+            catnn_graph tmp;
+            catnn_node self = *node;
+            self.id = nid;
+            ok(catnn_graph_add_node(&tmp, &self));
+            Node &cached = t->graph.nodes.at(nid);
+            cached.params = tmp.nodes.at(nid).params;
+            cached.name = tmp.nodes.at(nid).name;
+            TNode &tn = t->nodes[t->index.at(nid)];
+            for (auto &kv : tn.params) kv.second->init = param_values(cached, kv.first);
+            upload_params(*t);
+        } else {
+            // The one-node graph in0 … in{n-1} → node, its preds in edge order.
+            catnn_graph g;
+            g.name = "adjoint";
+            std::vector<std::string> names;
+            for (int32_t i = 0; i < n_inputs; ++i) names.push_back("in" + std::to_string(i));
+            for (int32_t i = 0; i < n_inputs; ++i) {
+                catnn_node in{};
+                in.id = (uint32_t)i;
+                in.name = names[(size_t)i].c_str();
+                in.op.kind = CATNN_OP_IDENTITY;
+                in.output_ty = inputs[i];
+                in.output_ty.data = nullptr;
+                ok(catnn_graph_add_node(&g, &in));
+                ok(catnn_graph_add_input(&g, in.id));
             }
-        } free_arena{t.get()};
-        t->dev = dev;
-        t->graph = g;
-        t->lr = 0.f;
-        t->input_grads = true;
-        plan_trainer(*t);
-        reserve_and_upload(*t);
+            catnn_node self = *node;
+            self.id = nid;
+            ok(catnn_graph_add_node(&g, &self));
+            for (int32_t i = 0; i < n_inputs; ++i) ok(catnn_graph_add_edge(&g, (uint32_t)i, nid, "out", "in"));
+            ok(catnn_graph_add_output(&g, nid));
+            std::unique_ptr<catnn_hip_trainer, TrainerFree> fresh(new catnn_hip_trainer());
+            fresh->dev = dev;
+            fresh->graph = g;
+            fresh->lr = 0.f;
+            fresh->input_grads = true;
+            plan_trainer(*fresh);
+            reserve_and_upload(*fresh);
+            t = adjoint_cache_insert(dev, key, std::move(fresh));
+        }
         hipStream_t s = dev->stream;
         for (int32_t i = 0; i < n_inputs; ++i) {
             const int64_t ni = numel(dims_from_c(inputs[i]));
@@ -1351,10 +1467,15 @@ int catnn_hip_run_adjoint(catnn_hip_device *dev, const catnn_node *node, const c
         }
         const std::vector<int64_t> &od = t->dims.at(nid);
         const int64_t nd = numel(dims_from_c(*dy));
+        const std::string span = std::string(node->name ? node->name : "?") + ".bwd";
         CATNN_REQUIRE(nd == numel(od) && (dy->data || nd == 0), CATNN_ERR_SHAPE_MISMATCH,
-                      "dy has " + std::to_string(nd) + " values, " + g.node(nid).name + " produces " + dims_str(od));
+                      "dy has " + std::to_string(nd) + " values, " + t->graph.node(nid).name + " produces " +
+                          dims_str(od));
         if (nd) CATNN_HIP(hipMemcpyAsync(t->grad.at(nid), dy->data, (size_t)nd * 4, hipMemcpyHostToDevice, s));
+        // note_kernel("{name}.bwd", dy.checksum()) of the training wave (coord.rs:412), stamped on the device.
+        push_device_event(dev, span, CATNN_EV_KERNEL_START, 0);
         adjoint_pass(*t);
+        push_device_event(dev, span, CATNN_EV_KERNEL_END, fnv1a_f32(dy->data, (uint64_t)nd));
         for (int32_t i = 0; i < n_inputs; ++i) {
             const std::vector<int64_t> &xd = t->dims.at((uint32_t)i);
             const int64_t nx = numel(xd);
@@ -1368,7 +1489,7 @@ int catnn_hip_run_adjoint(catnn_hip_device *dev, const catnn_node *node, const c
             for (size_t r = 0; r < xd.size(); ++r) dx[i].dims[r] = xd[r];
             dx[i].dtype = inputs[i].dtype;
         }
-        const Node &self_node = g.node(nid);
+        const Node &self_node = t->graph.node(nid);
         for (int32_t j = 0; j < n_dparams; ++j) {
             const auto &pr = self_node.params[(size_t)j];
             int64_t col0, ncols;

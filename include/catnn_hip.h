@@ -454,9 +454,17 @@ int catnn_hip_train_arena(catnn_hip_trainer *t, catnn_arena_alloc *out, int32_t 
                           uint64_t *reserved_bytes);
 
 /* ------------------------------------------------------------- events */
-/* Sheaf events (crates/catnn-rt/src/sheaf.rs:55-79) recorded by the
- * handler seam: times in ns from device open, checksum = FNV-1a over the
- * output's f32 bits on KernelEnd (tensor.rs:279-288). */
+/* Sheaf events (crates/catnn-rt/src/sheaf.rs:55-79) of the handler seams,
+ * as DeviceHandler::run_kernel and note_kernel record them
+ * (crates/catnn-rt/src/handler.rs:34-79): KernelStart / KernelEnd around
+ * each node that catnn_hip_run_kernel or catnn_hip_run_node executes, and
+ * "{name}.bwd" around each catnn_hip_run_adjoint (coord.rs:412).  Times are
+ * the device's: each event is a hipEvent recorded on the device's stream
+ * when the call enqueues its work, resolved to ns since catnn_hip_open when
+ * the events are read (strictly increasing, as handler.rs:47).  The
+ * KernelEnd checksum is FNV-1a over the output's f32 bits
+ * (tensor.rs:279-288); for the adjoint span it is that of dy, as
+ * coord.rs:412 passes it. */
 enum catnn_event_kind {
     CATNN_EV_KERNEL_START = 0, CATNN_EV_KERNEL_END = 1,
     CATNN_EV_TRANSFER_START = 2, CATNN_EV_TRANSFER_END = 3
@@ -467,7 +475,13 @@ typedef struct catnn_event {
     int32_t kind;
     uint64_t checksum;
 } catnn_event;
+/* Waits for the device work the recorded events stamp, then copies them. */
 int catnn_hip_events(catnn_hip_device *dev, catnn_event *buf, int32_t cap, int32_t *n);
+/* catnn_hip_run_node's KernelEnd checksum needs the output on the host: a
+ * device-to-host copy and a stream synchronisation per node.  On by
+ * default; with `enable` = 0 run_node records checksum 0 and does not
+ * synchronise. */
+int catnn_hip_trace_checksums(catnn_hip_device *dev, int32_t enable);
 int catnn_hip_clear_events(catnn_hip_device *dev);
 
 /* ------------------------------------------------ kernels on raw buffers */

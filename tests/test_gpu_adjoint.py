@@ -242,3 +242,26 @@ def test_adjoint_errors(device):
     with pytest.raises(CatError) as e:
         h.adjoint_of(fc, [_t(np.ones((2, 7)))], None, _t(np.ones((2, 4))))
     assert e.value.kind == "ShapeMismatch"
+
+
+def test_repeated_adjoint_calls_reuse_the_plan_and_take_new_values(device):
+    # The training wave calls adjoint_of on the same node every step with new
+    # parameter values and inputs: the cached one-node plan must take them.
+    h = DeviceHandler(device)
+    device.clear_events()
+    for step in range(3):
+        r = np.random.default_rng(100 + step)
+        params = {"w": _t(r.standard_normal((96, 64)) / 10), "b": _t(r.standard_normal(64))}
+        node = IrNode(3, "fc", OpenOp.linear(96, 64, True), TensorType.f32([32, 64]), params)
+        x = r.standard_normal((32, 96)).astype(np.float32)
+        out = oracle.eval_node(node, [x])
+        dy = r.standard_normal(out.shape).astype(np.float32)
+        dx, dp = h.adjoint_of(node, [_t(x)], None, _t(dy))
+        dx_o, dp_o = ot.adjoint_of(node, [x], out, dy)
+        assert rel_l2(dx[0].numpy(), dx_o[0]) < BF16_TOL
+        for port in ("w", "b"):
+            assert rel_l2(dp[port].numpy(), np.asarray(dp_o[port]).reshape(params[port].ty.shape)) < BF16_TOL
+        ev = device.events()[-2:]
+        # note_kernel("{name}.bwd", dy.checksum()) (coord.rs:412), stamped on the device
+        assert [(e[1], e[2]) for e in ev] == [("fc.bwd", 0), ("fc.bwd", 1)] and ev[0][0] < ev[1][0]
+        assert ev[1][3] == Tensor.from_numpy(dy).checksum()

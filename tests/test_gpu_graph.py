@@ -112,6 +112,28 @@ def test_run_kernel_seam_and_events(device):
     assert z.ty == TensorType.f32([2, 3]) and not z.data.any()
 
 
+def test_event_stamps_are_device_times(device):
+    # A node's KernelStart → KernelEnd span is the device time of its
+    # kernels: a 2048³ fp32 GEMM (17.2 GFLOP) cannot finish in less than
+    # 17.2e9 / 157.3e12 s = 109 µs on MI355X's matrix cores, however fast the
+    # host enqueues it; the host-side enqueue of the same call takes far less.
+    h = DeviceHandler(device)
+    r = np.random.default_rng(6)
+    n = 2048
+    node = IrNode(9, "big", OpenOp.linear(n, n, False), TensorType.f32([n, n]),
+                  {"w": Tensor.from_numpy(r.standard_normal((n, n)).astype(np.float32))})
+    x = Tensor.from_numpy(r.standard_normal((n, n)).astype(np.float32))
+    h.run_kernel(node, [x])  # warm-up
+    device.clear_events()
+    y = h.run_kernel(node, [x])
+    ev = device.events()
+    assert [e[2] for e in ev] == [0, 1]
+    span_ns = ev[1][0] - ev[0][0]
+    print(f"  device span {span_ns / 1e3:.1f} us")
+    assert 109_000 <= span_ns < 50_000_000
+    assert ev[1][3] == y.checksum()
+
+
 def test_run_kernel_every_executable_op(device):
     h = DeviceHandler(device)
     r = np.random.default_rng(4)
@@ -200,10 +222,20 @@ def test_run_node_on_arena_buffers(device):
     cnode, keep = node.to_c(with_data=False)
     ids = (ctypes.c_char_p * 1)(b"act:0")
     tys = (CTensor * 1)(ctensor(ty=TensorType.f32([m, k])))
+    device.clear_events()
     check(lib.catnn_hip_run_node(device.handle, ctypes.byref(cnode), ids, tys, 1, b"act:2", 3, b"act:skip"))
     got = device.download("act:2", (m, n))
     want = oracle.add(res, oracle.gelu(oracle.linear(x, w, b)))
     assert rel_l2(got, want) < TOL
+    # KernelStart/KernelEnd stamped on the device, the output's checksum on KernelEnd
+    ev = device.events()
+    assert [(e[1], e[2]) for e in ev] == [("fc", 0), ("fc", 1)] and ev[0][0] < ev[1][0]
+    assert ev[1][3] == Tensor.from_numpy(got).checksum()
+    device.trace_checksums(False)
+    check(lib.catnn_hip_run_node(device.handle, ctypes.byref(cnode), ids, tys, 1, b"act:2", 3, b"act:skip"))
+    device.trace_checksums(True)
+    ev2 = device.events()
+    assert len(ev2) == 4 and ev2[3][3] == 0 and ev2[1][0] < ev2[2][0] < ev2[3][0]
     with pytest.raises(CatError) as e:
         device.download("act:nope", (1,))
     assert e.value.kind == "UnknownPort"
