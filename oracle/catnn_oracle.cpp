@@ -602,6 +602,135 @@ int orc_gqa(const float *x, const float *wq, const float *wk, const float *wv, c
     return 0;
 }
 
+void orc_linear_backward(const float *x, const float *w, const float *dy, int64_t m, int64_t k,
+                         int64_t n, float *dx, float *dw, float *db);
+
+// apply_rope of the adjoint module, adjoint.rs:457-470: the same rotation
+// with frequencies from |θ|; a negative θ rotates by −angle (the sine cast
+// to f32, then negated).
+static void apply_rope_adj(float *q, int64_t head_dim, int64_t pos, double theta) {
+    for (int64_t i = 0; i < head_dim / 2; ++i) {
+        const double freq = 1.0 / std::pow(std::fabs(theta), 2.0 * (double)i / (double)head_dim);
+        const double ang = (double)pos * freq;
+        float s = (float)std::sin(ang);
+        const float c = (float)std::cos(ang);
+        if (theta < 0.0) s = -s;
+        const float a = q[2 * i], b = q[2 * i + 1];
+        q[2 * i] = a * c - b * s;
+        q[2 * i + 1] = a * s + b * c;
+    }
+}
+
+// gqa_backward, adjoint.rs:287-440: recompute q, k, v (linear_seq, as
+// linear3 at :442-455) and RoPE on q and k, then per (b, h, i) the windowed
+// causal softmax (keys [start, i], start = i − (window − 1) when a window is
+// given; window ≤ 0: none) kept as `attn`; dctx and dwo by linear_backward;
+// dv += a·dctx, dq += ds·scale·k, dk += ds·scale·q with ds the softmax
+// adjoint over the window, in the reference's (b, h, i, j) order; dq and dk
+// rotated back by −θ; dx = dxq + dxk + dxv from the three projections'
+// linear_backward.  Returns 2 on a shape mismatch.
+int orc_gqa_backward(const float *x, const float *wq, const float *wk, const float *wv, const float *wo,
+                     int64_t B, int64_t S, int64_t D, int64_t n_heads, int64_t n_kv, int64_t head_dim,
+                     double theta, int64_t window, const float *dy, float *dx, float *dwq, float *dwk,
+                     float *dwv, float *dwo) {
+    if (n_heads * head_dim != D || n_kv <= 0 || n_heads % n_kv != 0) return 2;
+    const int64_t T = B * S, QW = n_heads * head_dim, KV = n_kv * head_dim;
+    std::vector<float> q((size_t)(T * QW)), k((size_t)(T * KV)), v((size_t)(T * KV));
+    orc_matmul_seq(x, wq, q.data(), T, D, QW);
+    orc_matmul_seq(x, wk, k.data(), T, D, KV);
+    orc_matmul_seq(x, wv, v.data(), T, D, KV);
+    const int64_t repeats = n_heads / std::max<int64_t>(n_kv, 1);
+    for (int64_t bi = 0; bi < B; ++bi)
+        for (int64_t t = 0; t < S; ++t) {
+            for (int64_t h = 0; h < n_heads; ++h)
+                apply_rope_adj(&q[(size_t)(((bi * S + t) * n_heads + h) * head_dim)], head_dim, t, theta);
+            for (int64_t h = 0; h < n_kv; ++h)
+                apply_rope_adj(&k[(size_t)(((bi * S + t) * n_kv + h) * head_dim)], head_dim, t, theta);
+        }
+    const float scale = 1.0f / std::sqrt((float)head_dim);
+    auto start_of = [&](int64_t i) { return window > 0 ? std::max<int64_t>(i - (window - 1), 0) : 0; };
+    std::vector<float> ctx((size_t)(T * QW), 0.0f), attn((size_t)(B * n_heads * S * S), 0.0f);
+    std::vector<float> scores((size_t)S);
+    for (int64_t bi = 0; bi < B; ++bi)
+        for (int64_t h = 0; h < n_heads; ++h) {
+            const int64_t kv_h = h / std::max<int64_t>(repeats, 1);
+            for (int64_t i = 0; i < S; ++i) {
+                const int64_t start = start_of(i);
+                const int64_t q_off = ((bi * S + i) * n_heads + h) * head_dim;
+                std::fill(scores.begin(), scores.end(), -INFINITY);
+                for (int64_t j = start; j <= i; ++j) {
+                    const int64_t k_off = ((bi * S + j) * n_kv + kv_h) * head_dim;
+                    float dot = 0.0f;
+                    for (int64_t t = 0; t < head_dim; ++t) dot += q[(size_t)(q_off + t)] * k[(size_t)(k_off + t)];
+                    scores[(size_t)j] = dot * scale;
+                }
+                float mx = -INFINITY;
+                for (int64_t j = start; j <= i; ++j) mx = std::max(mx, scores[(size_t)j]);
+                float sum = 0.0f;
+                for (int64_t j = start; j <= i; ++j) {
+                    scores[(size_t)j] = std::exp(scores[(size_t)j] - mx);
+                    sum += scores[(size_t)j];
+                }
+                const float inv = 1.0f / std::max(sum, 1e-30f);
+                for (int64_t j = start; j <= i; ++j) {
+                    scores[(size_t)j] *= inv;
+                    attn[(size_t)(((bi * n_heads + h) * S + i) * S + j)] = scores[(size_t)j];
+                }
+                for (int64_t j = start; j <= i; ++j) {
+                    const int64_t v_off = ((bi * S + j) * n_kv + kv_h) * head_dim;
+                    for (int64_t t = 0; t < head_dim; ++t)
+                        ctx[(size_t)(q_off + t)] += scores[(size_t)j] * v[(size_t)(v_off + t)];
+                }
+            }
+        }
+    std::vector<float> dctx((size_t)(T * QW)), db((size_t)std::max(D, std::max(QW, KV)));
+    orc_linear_backward(ctx.data(), wo, dy, T, QW, D, dctx.data(), dwo, db.data());
+    std::vector<float> dq((size_t)(T * QW), 0.0f), dk((size_t)(T * KV), 0.0f), dv((size_t)(T * KV), 0.0f);
+    std::vector<float> dscore((size_t)S);
+    for (int64_t bi = 0; bi < B; ++bi)
+        for (int64_t h = 0; h < n_heads; ++h) {
+            const int64_t kv_h = h / std::max<int64_t>(repeats, 1);
+            for (int64_t i = 0; i < S; ++i) {
+                const int64_t start = start_of(i);
+                const int64_t o_off = ((bi * S + i) * n_heads + h) * head_dim;
+                const float *arow = &attn[(size_t)(((bi * n_heads + h) * S + i) * S)];
+                std::fill(dscore.begin(), dscore.end(), 0.0f);
+                for (int64_t j = start; j <= i; ++j) {
+                    const int64_t v_off = ((bi * S + j) * n_kv + kv_h) * head_dim;
+                    float dot = 0.0f;
+                    for (int64_t t = 0; t < head_dim; ++t) dot += dctx[(size_t)(o_off + t)] * v[(size_t)(v_off + t)];
+                    dscore[(size_t)j] = dot;
+                }
+                float dot = 0.0f;
+                for (int64_t j = start; j <= i; ++j) dot += arow[j] * dscore[(size_t)j];
+                for (int64_t j = start; j <= i; ++j) dscore[(size_t)j] = arow[j] * (dscore[(size_t)j] - dot);
+                for (int64_t j = start; j <= i; ++j) {
+                    const int64_t kv_off = ((bi * S + j) * n_kv + kv_h) * head_dim;
+                    const float a = arow[j];
+                    for (int64_t t = 0; t < head_dim; ++t) {
+                        dv[(size_t)(kv_off + t)] += a * dctx[(size_t)(o_off + t)];
+                        dq[(size_t)(o_off + t)] += dscore[(size_t)j] * scale * k[(size_t)(kv_off + t)];
+                        dk[(size_t)(kv_off + t)] += dscore[(size_t)j] * scale * q[(size_t)(o_off + t)];
+                    }
+                }
+            }
+        }
+    for (int64_t bi = 0; bi < B; ++bi)
+        for (int64_t t = 0; t < S; ++t) {
+            for (int64_t h = 0; h < n_heads; ++h)
+                apply_rope_adj(&dq[(size_t)(((bi * S + t) * n_heads + h) * head_dim)], head_dim, t, -theta);
+            for (int64_t h = 0; h < n_kv; ++h)
+                apply_rope_adj(&dk[(size_t)(((bi * S + t) * n_kv + h) * head_dim)], head_dim, t, -theta);
+        }
+    std::vector<float> dxk((size_t)(T * D)), dxv((size_t)(T * D));
+    orc_linear_backward(x, wq, dq.data(), T, D, QW, dx, dwq, db.data());
+    orc_linear_backward(x, wk, dk.data(), T, D, KV, dxk.data(), dwk, db.data());
+    orc_linear_backward(x, wv, dv.data(), T, D, KV, dxv.data(), dwv, db.data());
+    for (int64_t i = 0; i < T * D; ++i) dx[i] += dxk[(size_t)i];
+    for (int64_t i = 0; i < T * D; ++i) dx[i] += dxv[(size_t)i];
+    return 0;
+}
+
 // moe::lm_head, moe.rs:325-333: w is [V, H] (HF layout); y = x·wᵀ via the
 // transposed copy and linear_seq.
 void orc_lm_head(const float *x, const float *w, int64_t rows, int64_t H, int64_t V, float *y) {

@@ -29,6 +29,8 @@ _SIG = {
     "orc_attention_backward": ([_F, _F, _F, _F, _F, _I64, _I64, _I64, _I64, _I64, ctypes.c_int32,
                                 _F, _F, _F, _F, _F, _F], ctypes.c_int),
     "orc_swiglu_backward": ([_F, _F, _F, _F, _I64, _I64, _I64, _F, _F, _F, _F, _F], None),
+    "orc_gqa_backward": ([_F, _F, _F, _F, _F, _I64, _I64, _I64, _I64, _I64, _I64, ctypes.c_double, _I64,
+                          _F, _F, _F, _F, _F, _F], ctypes.c_int),
     "orc_router_backward_ste": ([_F, _F, _I64, _I64, _I64, _I64, _F, _F, _F], None),
     "orc_moe_backward": ([_F, _F, _F, _F, _F, _I64, _I64, _I64, _I64, _I64, _F, _F, _F, _F, _F, _F],
                          None),
@@ -156,6 +158,22 @@ def attention_backward(x, wq, wk, wv, wo, n_heads, d_head, dy, causal=False):
     return (dx, *dws)
 
 
+def gqa_backward(x, wq, wk, wv, wo, n_heads, n_kv, head_dim, theta, window, dy):
+    """gqa_backward, adjoint.rs:287-440 (window None or ≤ 0: no sliding
+    window): (dx, dwq, dwk, dwv, dwo)."""
+    x, dy = _c(x), _c(dy)
+    wq, wk, wv, wo = _c(wq), _c(wk), _c(wv), _c(wo)
+    B, S, D = x.shape
+    dx = np.empty_like(x)
+    dws = [np.empty_like(w) for w in (wq, wk, wv, wo)]
+    rc = _lib.orc_gqa_backward(_f(x), _f(wq), _f(wk), _f(wv), _f(wo), B, S, D, n_heads, n_kv, head_dim,
+                               float(theta), 0 if window is None else int(window), _f(dy), _f(dx),
+                               *[_f(w) for w in dws])
+    if rc:
+        raise ValueError("gqa shape")
+    return (dx, *dws)
+
+
 def swiglu_backward(x, w1, w3, w2, dy):
     x, dy = _c(x), _c(dy)
     H, I = w1.shape
@@ -264,6 +282,11 @@ def adjoint_of(node, inputs, output, dy):
         heads, _, dh = node.op.fields
         dx, dwq, dwk, dwv, dwo = attention_backward(x, P["wq"], P["wk"], P["wv"], P["wo"], heads, dh, dy,
                                                     causal=bool(node.op.flags & 1))
+        return [dx], {"wq": dwq, "wk": dwk, "wv": dwv, "wo": dwo}
+    if kind == "gqa_attention":  # adjoint.rs:862-883
+        nh, nkv, hd, _, window, theta = node.op.fields
+        dx, dwq, dwk, dwv, dwo = gqa_backward(x, P["wq"], P["wk"], P["wv"], P["wo"], nh, nkv, hd,
+                                              float(theta), None if window < 0 else window, dy)
         return [dx], {"wq": dwq, "wk": dwk, "wv": dwv, "wo": dwo}
     if kind == "swiglu":  # adjoint.rs:849-861
         dx, dw1, dw3, dw2 = swiglu_backward(x, P["w1"], P["w3"], P["w2"], dy)
