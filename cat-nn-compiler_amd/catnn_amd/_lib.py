@@ -155,6 +155,7 @@ SIGNATURES = {
     "catnn_hip_program_timings": [_VP, ctypes.POINTER(CStepTiming), _I32, _PI32],
     "catnn_hip_train_install": [_VP, _VP, _F, ctypes.POINTER(_VP)],
     "catnn_hip_train_install_opt": [_VP, _VP, _I32, _F, ctypes.POINTER(_VP)],
+    "catnn_hip_train_install_ex": [_VP, _VP, _I32, _F, _I32, ctypes.POINTER(_VP)],
     "catnn_hip_train_set_batch_classes": [_VP, ctypes.POINTER(CTensor), ctypes.POINTER(ctypes.c_uint32), _I64],
     "catnn_hip_train_read_moment": [_VP, ctypes.c_uint32, ctypes.c_char_p, _I32, ctypes.POINTER(_F), _I64],
     "catnn_hip_train_adam_step": [_VP, _PU64],

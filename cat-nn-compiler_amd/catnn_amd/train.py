@@ -5,8 +5,9 @@
 TrainOptions.opt names (OptimizerKind, crates/catnn-core/src/lens/optim.rs:
 142-145): forward, loss, reverse-topo adjoints, then Sgd::put or Adam::put
 on the fp32 master weights.  GEMM operands are
-bf16 (bf16 MFMA, fp32 accumulation); masters, residual stream, norms,
-router and gradient accumulation are fp32.
+bf16 (bf16 MFMA, fp32 accumulation) at precision "bf16", six-part split
+(fp32-accurate) at precision "fp32"; masters, residual stream, norms, router
+and gradient accumulation are fp32.
 """
 from __future__ import annotations
 
@@ -23,22 +24,29 @@ from .ir import IrGraph, Tensor, ctensor
 _FP = ctypes.POINTER(ctypes.c_float)
 
 OPTIMIZERS = {"sgd": 0, "adam": 1}  # CATNN_OPT_SGD, CATNN_OPT_ADAM
+PRECISIONS = {"bf16": 0, "fp32": 1}  # CATNN_PREC_BF16, CATNN_PREC_FP32
 
 
 class Trainer:
-    def __init__(self, device: Device, graph: IrGraph, lr: float = 0.05, opt: str = "sgd"):
-        """`opt` is OptimizerKind::parse's spelling: "sgd" or "adam"."""
+    def __init__(self, device: Device, graph: IrGraph, lr: float = 0.05, opt: str = "sgd",
+                 precision: str = "bf16"):
+        """`opt` is OptimizerKind::parse's spelling: "sgd" or "adam".
+        `precision` "bf16": bf16 MFMA GEMM operands (mixed precision);
+        "fp32": every GEMM on six-part split operands, fp32-accurate."""
         if opt not in OPTIMIZERS:
             raise ValueError(f"unknown optimizer {opt!r} (expected sgd or adam)")
+        if precision not in PRECISIONS:
+            raise ValueError(f"unknown precision {precision!r} (expected bf16 or fp32)")
         self.device = device
         self.graph = graph
         self.lr = lr
         self.opt = opt
+        self.precision = precision
         h, owned = graph_handle(graph)
         self.handle = ctypes.c_void_p()
         try:
-            check(lib.catnn_hip_train_install_opt(device.handle, h, OPTIMIZERS[opt], ctypes.c_float(lr),
-                                                  ctypes.byref(self.handle)))
+            check(lib.catnn_hip_train_install_ex(device.handle, h, OPTIMIZERS[opt], ctypes.c_float(lr),
+                                                 PRECISIONS[precision], ctypes.byref(self.handle)))
         finally:
             if owned:
                 lib.catnn_graph_free(h)

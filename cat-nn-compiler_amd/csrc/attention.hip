@@ -407,6 +407,12 @@ void attention_core_fwd_lse(hipStream_t s, const float *q, const float *k, const
     attention_fwd(s, q, k, v, ld, ld, 1, 0, ctx, ldo, lse, batch, seq, n_heads, d_head, causal);
 }
 
+void attention_core_fwd_lse_gqa(hipStream_t s, const float *q, int64_t ldq, const float *k, const float *v,
+                                int64_t ldk, int64_t group, int64_t window, float *ctx, int64_t ldo, float *lse,
+                                int64_t batch, int64_t seq, int64_t n_heads, int64_t d_head) {
+    attention_fwd(s, q, k, v, ldq, ldk, group, window, ctx, ldo, lse, batch, seq, n_heads, d_head, true);
+}
+
 }  // namespace k
 }  // namespace catnn
 

@@ -13,7 +13,14 @@
 //  * dQ: a block owns 128 queries, the transposed frame of the forward
 //    (Sᵀ = K·Qᵀ, dPᵀ = V·dOᵀ, dQᵀ += Kᵀ·dSᵀ), lane l owning query l%32.
 // Other head sizes use one-wavefront-per-row kernels.
+// Grouped K/V heads (gqa_backward, adjoint.rs:287-440): query head h reads
+// K/V head h / group; a dK/dV block owns the keys of one K/V head and sums
+// over the group's query heads in head order, so dK and dV need no atomics.
+// A sliding window (window > 0, with causal) limits query i to keys
+// [i − window + 1, i], as the forward.
 #include <hip/hip_runtime.h>
+
+#include <algorithm>
 
 #include "common.hpp"
 #include "devmath.hpp"
@@ -59,10 +66,10 @@ __device__ __forceinline__ int tsw(int d) { return ((d >> 3) & 7) << 2; }
 
 template <int DH>
 __global__ __launch_bounds__(256, 2) void attn_bwd_dkdv_kernel(
-    const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v, int64_t ld,
-    const float *__restrict__ dout, int64_t ldo, const float *__restrict__ lse,
+    const float *__restrict__ q, int64_t ldq, const float *__restrict__ k, const float *__restrict__ v,
+    int64_t ldk, const float *__restrict__ dout, int64_t ldo, const float *__restrict__ lse,
     const float *__restrict__ Dv, float *__restrict__ dk, float *__restrict__ dv, int64_t ldd, int S,
-    int H, float qscale, float scale, int causal, int n_kblocks) {
+    int H, int group, int window, float qscale, float scale, int causal, int n_kblocks) {
     static_assert(DH == 64, "written for d_head = 64");
     constexpr int BKEY = 128, BQ = 64, LDQ = DH + 4, LDT = BQ + 4;
     constexpr int IT = BQ * DH / 4 / 256;
@@ -77,7 +84,8 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkdv_kernel(
     // Low key blocks see the most queries: first, spread over the XCDs.
     int kb, bh;
     split_bh_block(blockIdx.x, n_kblocks, (int)(gridDim.x / n_kblocks), kb, bh);
-    const int b = bh / H, h = bh % H;
+    const int HK = H / group;
+    const int b = bh / HK, hk = bh % HK;
     const int k0 = kb * BKEY;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int lr = lane & 31, g = lane >> 5;
@@ -87,8 +95,8 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkdv_kernel(
 
     float kf[32], vf[32];
     if (kj < S) {
-        const float4 *ks = reinterpret_cast<const float4 *>(k + (row_base + kj) * ld + (int64_t)h * DH + 32 * g);
-        const float4 *vs = reinterpret_cast<const float4 *>(v + (row_base + kj) * ld + (int64_t)h * DH + 32 * g);
+        const float4 *ks = reinterpret_cast<const float4 *>(k + (row_base + kj) * ldk + (int64_t)hk * DH + 32 * g);
+        const float4 *vs = reinterpret_cast<const float4 *>(v + (row_base + kj) * ldk + (int64_t)hk * DH + 32 * g);
 #pragma unroll
         for (int c = 0; c < 8; ++c) {
             const float4 a = ks[c], bb = vs[c];
@@ -105,11 +113,19 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkdv_kernel(
 #pragma unroll
         for (int r = 0; r < 16; ++r) dka[db][r] = dva[db][r] = 0.f;
 
+    // Query tiles of every query head of the group, head by head: tile t is
+    // head hk·group + t / tiles_per_head at queries q_start + (t % tiles)·BQ.
     // The next Q/dO tile is loaded into registers while the current one is
     // consumed from LDS.
+    const int q_start = causal ? (k0 / BQ) * BQ : 0;
+    const int q_end = window > 0 ? min(S, k0 + BKEY - 1 + window) : S;
+    const int tiles_per_head = q_end > q_start ? (q_end - q_start + BQ - 1) / BQ : 0;
+    const int n_tiles = tiles_per_head * group;
     float4 pq[IT], po[IT];
     float pl = 0.f, pd = 0.f;
-    auto gload = [&](int q0) {
+    auto gload = [&](int t) {
+        const int h = hk * group + t / tiles_per_head;
+        const int q0 = q_start + (t % tiles_per_head) * BQ;
 #pragma unroll
         for (int it = 0; it < IT; ++it) {
             const int idx = tid + it * 256;
@@ -118,7 +134,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkdv_kernel(
             pq[it] = make_float4(0.f, 0.f, 0.f, 0.f);
             po[it] = pq[it];
             if (qi < S) {
-                pq[it] = *reinterpret_cast<const float4 *>(q + (row_base + qi) * ld + (int64_t)h * DH + 4 * c4);
+                pq[it] = *reinterpret_cast<const float4 *>(q + (row_base + qi) * ldq + (int64_t)h * DH + 4 * c4);
                 po[it] = *reinterpret_cast<const float4 *>(dout + (row_base + qi) * ldo + (int64_t)h * DH + 4 * c4);
             }
         }
@@ -146,21 +162,24 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkdv_kernel(
         }
     };
 
-    const int q_start = causal ? (k0 / BQ) * BQ : 0;
-    if (q_start < S) gload(q_start);
-    for (int q0 = q_start; q0 < S; q0 += BQ) {
+    if (n_tiles > 0) gload(0);
+    for (int t = 0; t < n_tiles; ++t) {
+        const int q0 = q_start + (t % tiles_per_head) * BQ;
         sstore();
         __syncthreads();
-        if (q0 + BQ < S) gload(q0 + BQ);
+        if (t + 1 < n_tiles) gload(t + 1);
 #pragma unroll
         for (int qb = 0; qb < BQ / 32; ++qb) {
             const int qs0 = q0 + qb * 32;
-            const bool active = __builtin_amdgcn_readfirstlane(qs0 < S && (!causal || qs0 + 31 >= wave_kmin));
+            const bool active = __builtin_amdgcn_readfirstlane(
+                qs0 < S && (!causal || qs0 + 31 >= wave_kmin) && (window <= 0 || qs0 <= wave_kmin + 30 + window));
             if (!active) continue;
             // No mask needed: every query of the 32 and every key of the
-            // wavefront in range, and (causal) every key at or before every query.
-            const bool full = __builtin_amdgcn_readfirstlane(qs0 + 31 < S && wave_kmin + 31 < S &&
-                                                             (!causal || wave_kmin + 31 <= qs0));
+            // wavefront in range, (causal) every key at or before every query,
+            // and (window) every key within the window of every query.
+            const bool full = __builtin_amdgcn_readfirstlane(
+                qs0 + 31 < S && wave_kmin + 31 < S && (!causal || wave_kmin + 31 <= qs0) &&
+                (window <= 0 || qs0 + 31 - wave_kmin <= window - 1));
             f32x16 sa, pa;
 #pragma unroll
             for (int r = 0; r < 16; ++r) sa[r] = pa[r] = 0.f;
@@ -184,7 +203,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkdv_kernel(
             for (int r = 0; r < 16; ++r) {
                 const int il = qb * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
                 const int qi = q0 + il;
-                const bool ok = full || (qi < S && kj < S && (!causal || kj <= qi));
+                const bool ok = full || (qi < S && kj < S && (!causal || kj <= qi) && (window <= 0 || qi - kj < window));
                 const float p = ok ? fast_exp2(sa[r] * qscale - Ls[il]) : 0.f;
                 pa[r] = p * (pa[r] - Ds[il]);
                 sa[r] = p;
@@ -213,8 +232,8 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkdv_kernel(
         __syncthreads();
     }
     if (kj < S) {
-        float *dkr = dk + (row_base + kj) * ldd + (int64_t)h * DH;
-        float *dvr = dv + (row_base + kj) * ldd + (int64_t)h * DH;
+        float *dkr = dk + (row_base + kj) * ldd + (int64_t)hk * DH;
+        float *dvr = dv + (row_base + kj) * ldd + (int64_t)hk * DH;
 #pragma unroll
         for (int db = 0; db < DH / 32; ++db)
 #pragma unroll
@@ -231,10 +250,10 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkdv_kernel(
 
 template <int DH>
 __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(
-    const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v, int64_t ld,
-    const float *__restrict__ dout, int64_t ldo, const float *__restrict__ lse,
-    const float *__restrict__ Dv, float *__restrict__ dq, int64_t ldd, int S, int H, float qscale,
-    float scale, int causal, int n_qblocks) {
+    const float *__restrict__ q, int64_t ldq, const float *__restrict__ k, const float *__restrict__ v,
+    int64_t ldk, const float *__restrict__ dout, int64_t ldo, const float *__restrict__ lse,
+    const float *__restrict__ Dv, float *__restrict__ dq, int64_t ldd, int S, int H, int group, int window,
+    float qscale, float scale, int causal, int n_qblocks) {
     static_assert(DH == 64, "written for d_head = 64");
     constexpr int BQ = 128, BKV = 64, LDK = DH + 4, LDT = BKV + 4;
     constexpr int KV_IT = BKV * DH / 4 / 256;
@@ -247,7 +266,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(
     int blk, bh;
     split_bh_block(blockIdx.x, n_qblocks, (int)(gridDim.x / n_qblocks), blk, bh);
     const int qb = n_qblocks - 1 - blk;
-    const int b = bh / H, h = bh % H;
+    const int b = bh / H, h = bh % H, hk = h / group;
     const int q0 = qb * BQ;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int lr = lane & 31, g = lane >> 5;
@@ -258,7 +277,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(
     float qf[32], of[32];
     float lse_i = 0.f, D_i = 0.f;
     if (qi < S) {
-        const float4 *qs = reinterpret_cast<const float4 *>(q + (row_base + qi) * ld + (int64_t)h * DH + 32 * g);
+        const float4 *qs = reinterpret_cast<const float4 *>(q + (row_base + qi) * ldq + (int64_t)h * DH + 32 * g);
         const float4 *os = reinterpret_cast<const float4 *>(dout + (row_base + qi) * ldo + (int64_t)h * DH + 32 * g);
 #pragma unroll
         for (int c = 0; c < 8; ++c) {
@@ -280,6 +299,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(
         for (int r = 0; r < 16; ++r) dqa[db][r] = 0.f;
 
     const int kv_end = causal ? min(S, q0 + BQ) : S;
+    const int t_first = window > 0 ? max(0, q0 - window + 1) / BKV : 0;  // tiles before the window are skipped
     const int ntiles = (kv_end + BKV - 1) / BKV;
     // The next K/V tile is loaded into registers while the current one is
     // consumed from LDS.
@@ -293,14 +313,14 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(
             pk[it] = make_float4(0.f, 0.f, 0.f, 0.f);
             pv[it] = pk[it];
             if (key < S) {
-                const int64_t off = (row_base + key) * ld + (int64_t)h * DH + 4 * c4;
+                const int64_t off = (row_base + key) * ldk + (int64_t)hk * DH + 4 * c4;
                 pk[it] = *reinterpret_cast<const float4 *>(k + off);
                 pv[it] = *reinterpret_cast<const float4 *>(v + off);
             }
         }
     };
-    if (ntiles > 0) gload(0);
-    for (int t = 0; t < ntiles; ++t) {
+    if (ntiles > t_first) gload(t_first);
+    for (int t = t_first; t < ntiles; ++t) {
         const int buf = 0;
 #pragma unroll
         for (int it = 0; it < KV_IT; ++it) {
@@ -317,10 +337,14 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(
         const int j0 = t * BKV;
         for (int kb = 0; kb < BKV / 32; ++kb) {
             const int jb = j0 + kb * 32;
-            if (!__builtin_amdgcn_readfirstlane(jb < S && (!causal || jb <= wave_qmax))) continue;
-            // No mask: all 32 keys in range and (causal) none after any query of
-            // the wavefront.  Padded queries (≥ S) are never stored.
-            const bool full = __builtin_amdgcn_readfirstlane(jb + 31 < S && (!causal || jb + 31 <= wave_qmin));
+            if (!__builtin_amdgcn_readfirstlane(jb < S && (!causal || jb <= wave_qmax) &&
+                                                (window <= 0 || jb + 31 >= wave_qmin - window + 1)))
+                continue;
+            // No mask: all 32 keys in range, (causal) none after any query of
+            // the wavefront and (window) none before any query's window.
+            // Padded queries (≥ S) are never stored.
+            const bool full = __builtin_amdgcn_readfirstlane(jb + 31 < S && (!causal || jb + 31 <= wave_qmin) &&
+                                                             (window <= 0 || jb >= wave_qmax - window + 1));
             f32x16 sa, pa;
 #pragma unroll
             for (int r = 0; r < 16; ++r) sa[r] = pa[r] = 0.f;
@@ -344,7 +368,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int j = jb + 8 * (r >> 2) + 4 * g + (r & 3);
-                const bool ok = full || (qi < S && j < S && (!causal || j <= qi));
+                const bool ok = full || (qi < S && j < S && (!causal || j <= qi) && (window <= 0 || j > qi - window));
                 const float p = ok ? fast_exp2(sa[r] - lse_i) : 0.f;
                 pa[r] = p * (pa[r] - D_i);  // dSᵀ entry
             }
@@ -380,30 +404,30 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(
 
 // Any head size ≤ 256: one wavefront per (b, h, query) for dQ ...
 __global__ __launch_bounds__(256) void attn_bwd_dq_generic(
-    const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v, int64_t ld,
-    const float *__restrict__ dout, int64_t ldo, const float *__restrict__ lse,
+    const float *__restrict__ q, int64_t ldq, const float *__restrict__ k, const float *__restrict__ v,
+    int64_t ldk, const float *__restrict__ dout, int64_t ldo, const float *__restrict__ lse,
     const float *__restrict__ Dv, float *__restrict__ dq, int64_t ldd, int B, int S, int H, int DH,
-    float scale, int causal) {
+    int group, int window, float scale, int causal) {
     const int lane = threadIdx.x & 63;
     const int64_t gw = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (gw >= (int64_t)B * H * S) return;
     const int i = (int)(gw % S);
     const int64_t bh = gw / S;
-    const int h = (int)(bh % H), b = (int)(bh / H);
+    const int h = (int)(bh % H), b = (int)(bh / H), hk = h / group;
     const int64_t rb = (int64_t)b * S;
     float qv[4], ov[4], acc[4];
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
         const int d = lane + 64 * c;
-        qv[c] = d < DH ? q[(rb + i) * ld + (int64_t)h * DH + d] : 0.f;
+        qv[c] = d < DH ? q[(rb + i) * ldq + (int64_t)h * DH + d] : 0.f;
         ov[c] = d < DH ? dout[(rb + i) * ldo + (int64_t)h * DH + d] : 0.f;
         acc[c] = 0.f;
     }
     const float l2 = lse[(rb + i) * H + h], Di = Dv[(rb + i) * H + h];
     const int jend = causal ? i + 1 : S;
-    for (int j = 0; j < jend; ++j) {
-        const float *kr = k + (rb + j) * ld + (int64_t)h * DH;
-        const float *vr = v + (rb + j) * ld + (int64_t)h * DH;
+    for (int j = window > 0 ? max(0, i - window + 1) : 0; j < jend; ++j) {
+        const float *kr = k + (rb + j) * ldk + (int64_t)hk * DH;
+        const float *vr = v + (rb + j) * ldk + (int64_t)hk * DH;
         float sp = 0.f, dp = 0.f;
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
@@ -430,27 +454,31 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_generic(
 
 // ... and one wavefront per (b, h, key) for dK and dV.
 __global__ __launch_bounds__(256) void attn_bwd_dkdv_generic(
-    const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v, int64_t ld,
-    const float *__restrict__ dout, int64_t ldo, const float *__restrict__ lse,
+    const float *__restrict__ q, int64_t ldq, const float *__restrict__ k, const float *__restrict__ v,
+    int64_t ldk, const float *__restrict__ dout, int64_t ldo, const float *__restrict__ lse,
     const float *__restrict__ Dv, float *__restrict__ dk, float *__restrict__ dv, int64_t ldd, int B,
-    int S, int H, int DH, float scale, int causal) {
+    int S, int H, int DH, int group, int window, float scale, int causal) {
     const int lane = threadIdx.x & 63;
+    const int HK = H / group;
     const int64_t gw = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (gw >= (int64_t)B * H * S) return;
+    if (gw >= (int64_t)B * HK * S) return;
     const int j = (int)(gw % S);
     const int64_t bh = gw / S;
-    const int h = (int)(bh % H), b = (int)(bh / H);
+    const int hk = (int)(bh % HK), b = (int)(bh / HK);
     const int64_t rb = (int64_t)b * S;
     float kv[4], vv[4], ak[4], av[4];
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
         const int d = lane + 64 * c;
-        kv[c] = d < DH ? k[(rb + j) * ld + (int64_t)h * DH + d] : 0.f;
-        vv[c] = d < DH ? v[(rb + j) * ld + (int64_t)h * DH + d] : 0.f;
+        kv[c] = d < DH ? k[(rb + j) * ldk + (int64_t)hk * DH + d] : 0.f;
+        vv[c] = d < DH ? v[(rb + j) * ldk + (int64_t)hk * DH + d] : 0.f;
         ak[c] = av[c] = 0.f;
     }
-    for (int i = causal ? j : 0; i < S; ++i) {
-        const float *qr = q + (rb + i) * ld + (int64_t)h * DH;
+    const int iend = window > 0 ? min(S, j + window) : S;
+    for (int gi = 0; gi < group; ++gi)
+    for (int i = causal ? j : 0; i < iend; ++i) {
+        const int h = hk * group + gi;
+        const float *qr = q + (rb + i) * ldq + (int64_t)h * DH;
         const float *orr = dout + (rb + i) * ldo + (int64_t)h * DH;
         float sp = 0.f, dp = 0.f;
 #pragma unroll
@@ -476,8 +504,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_generic(
     for (int c = 0; c < 4; ++c) {
         const int d = lane + 64 * c;
         if (d < DH) {
-            dk[(rb + j) * ldd + (int64_t)h * DH + d] = ak[c] * scale;
-            dv[(rb + j) * ldd + (int64_t)h * DH + d] = av[c];
+            dk[(rb + j) * ldd + (int64_t)hk * DH + d] = ak[c] * scale;
+            dv[(rb + j) * ldd + (int64_t)hk * DH + d] = av[c];
         }
     }
 }
@@ -490,43 +518,62 @@ uint64_t attention_bwd_scratch_bytes(int64_t batch, int64_t seq, int64_t n_heads
     return (uint64_t)(batch * seq * n_heads) * 4;
 }
 
-void attention_core_bwd(hipStream_t s, const float *q, const float *k, const float *v, int64_t ld,
-                        const float *o, const float *dout, int64_t ldo, const float *lse, float *dq,
-                        float *dk, float *dv, int64_t ld_d, int64_t batch, int64_t seq,
-                        int64_t n_heads, int64_t d_head, bool causal, float *scratch) {
+void attention_core_bwd_gqa(hipStream_t s, const float *q, int64_t ldq, const float *k, const float *v,
+                            int64_t ldk, int64_t group, int64_t window, const float *o, const float *dout,
+                            int64_t ldo, const float *lse, float *dq, int64_t ld_dq, float *dk, float *dv,
+                            int64_t ld_dkv, int64_t batch, int64_t seq, int64_t n_heads, int64_t d_head,
+                            bool causal, float *scratch) {
     CATNN_REQUIRE(batch >= 0 && seq >= 0 && n_heads > 0 && d_head > 0 && d_head <= 256,
                   CATNN_ERR_SHAPE_MISMATCH, "attention backward: bad dims");
+    CATNN_REQUIRE(group >= 1 && n_heads % group == 0, CATNN_ERR_SHAPE_MISMATCH,
+                  "attention backward: n_heads not a multiple of the kv groups");
+    CATNN_REQUIRE(n_heads * d_head <= ldq && n_heads * d_head <= ldo && n_heads * d_head <= ld_dq &&
+                      (n_heads / group) * d_head <= ldk && (n_heads / group) * d_head <= ld_dkv,
+                  CATNN_ERR_SHAPE_MISMATCH, "attention backward: row strides too small");
+    CATNN_REQUIRE(window <= 0 || causal, CATNN_ERR_INVALID_ARGUMENT, "attention backward: a window needs causal");
     CATNN_REQUIRE(batch * seq * n_heads < (1ll << 31), CATNN_ERR_SHAPE_MISMATCH,
                   "attention backward: too many rows");
     if (batch == 0 || seq == 0) return;
+    const int win = (int)std::min<int64_t>(std::max<int64_t>(window, 0), seq);
     const int64_t rows = batch * seq;
+    const int64_t HK = n_heads / group;
     float *D = scratch;
     attn_dot_kernel<<<(unsigned)((rows * n_heads + 3) / 4), 256, 0, s>>>(o, dout, ldo, rows, (int)n_heads,
                                                                         (int)d_head, D);
     CATNN_HIP(hipGetLastError());
     const float scale = 1.0f / sqrtf((float)d_head);
-    const bool mfma = d_head == 64 && ld % 4 == 0 && ldo % 4 == 0 && ld_d % 4 == 0 && al16(q) &&
-                      al16(k) && al16(v) && al16(dout) && al16(dq) && al16(dk) && al16(dv);
+    const bool mfma = d_head == 64 && ldq % 4 == 0 && ldk % 4 == 0 && ldo % 4 == 0 && ld_dq % 4 == 0 &&
+                      ld_dkv % 4 == 0 && al16(q) && al16(k) && al16(v) && al16(dout) && al16(dq) &&
+                      al16(dk) && al16(dv);
     if (mfma) {
         const int nkb = (int)((seq + 127) / 128);
-        attn_bwd_dkdv_kernel<64><<<(unsigned)(batch * n_heads * nkb), 256, 0, s>>>(
-            q, k, v, ld, dout, ldo, lse, D, dk, dv, ld_d, (int)seq, (int)n_heads, scale * kLog2e, scale,
-            causal ? 1 : 0, nkb);
+        attn_bwd_dkdv_kernel<64><<<(unsigned)(batch * HK * nkb), 256, 0, s>>>(
+            q, ldq, k, v, ldk, dout, ldo, lse, D, dk, dv, ld_dkv, (int)seq, (int)n_heads, (int)group, win,
+            scale * kLog2e, scale, causal ? 1 : 0, nkb);
         CATNN_HIP(hipGetLastError());
         attn_bwd_dq_kernel<64><<<(unsigned)(batch * n_heads * nkb), 256, 0, s>>>(
-            q, k, v, ld, dout, ldo, lse, D, dq, ld_d, (int)seq, (int)n_heads, scale * kLog2e, scale,
-            causal ? 1 : 0, nkb);
+            q, ldq, k, v, ldk, dout, ldo, lse, D, dq, ld_dq, (int)seq, (int)n_heads, (int)group, win,
+            scale * kLog2e, scale, causal ? 1 : 0, nkb);
         CATNN_HIP(hipGetLastError());
     } else {
-        const unsigned blocks = (unsigned)((batch * n_heads * seq + 3) / 4);
-        attn_bwd_dq_generic<<<blocks, 256, 0, s>>>(q, k, v, ld, dout, ldo, lse, D, dq, ld_d, (int)batch,
-                                                   (int)seq, (int)n_heads, (int)d_head, scale,
-                                                   causal ? 1 : 0);
-        attn_bwd_dkdv_generic<<<blocks, 256, 0, s>>>(q, k, v, ld, dout, ldo, lse, D, dk, dv, ld_d,
-                                                     (int)batch, (int)seq, (int)n_heads, (int)d_head,
-                                                     scale, causal ? 1 : 0);
+        const unsigned qblocks = (unsigned)((batch * n_heads * seq + 3) / 4);
+        const unsigned kblocks = (unsigned)((batch * HK * seq + 3) / 4);
+        attn_bwd_dq_generic<<<qblocks, 256, 0, s>>>(q, ldq, k, v, ldk, dout, ldo, lse, D, dq, ld_dq, (int)batch,
+                                                    (int)seq, (int)n_heads, (int)d_head, (int)group, win, scale,
+                                                    causal ? 1 : 0);
+        attn_bwd_dkdv_generic<<<kblocks, 256, 0, s>>>(q, ldq, k, v, ldk, dout, ldo, lse, D, dk, dv, ld_dkv,
+                                                      (int)batch, (int)seq, (int)n_heads, (int)d_head, (int)group,
+                                                      win, scale, causal ? 1 : 0);
         CATNN_HIP(hipGetLastError());
     }
+}
+
+void attention_core_bwd(hipStream_t s, const float *q, const float *k, const float *v, int64_t ld,
+                        const float *o, const float *dout, int64_t ldo, const float *lse, float *dq,
+                        float *dk, float *dv, int64_t ld_d, int64_t batch, int64_t seq,
+                        int64_t n_heads, int64_t d_head, bool causal, float *scratch) {
+    attention_core_bwd_gqa(s, q, ld, k, v, ld, 1, 0, o, dout, ldo, lse, dq, ld_d, dk, dv, ld_d, batch, seq,
+                           n_heads, d_head, causal, scratch);
 }
 
 }  // namespace k

@@ -16,6 +16,7 @@
 #include "devmath.hpp"
 #include "gemm_f32.hpp"
 #include "kernels.hpp"
+#include "train_ops.hpp"
 
 namespace catnn {
 namespace k {
@@ -228,8 +229,9 @@ __global__ void rope_table_kernel(float2 *__restrict__ tab, int64_t n, int half,
 
 // Rotates the pairs (2i, 2i+1) of `heads` consecutive heads of width hd at
 // the start of each row (row r is position r mod S), in place.
+// `sign` −1 rotates by −angle (sin negated after rounding).
 __global__ void rope_apply_kernel(float *__restrict__ qk, int64_t ld, int64_t rows, int S, int heads,
-                                  int hd, const float2 *__restrict__ tab) {
+                                  int hd, const float2 *__restrict__ tab, float sign) {
 #pragma clang fp contract(off)
     const int half = hd / 2;
     const int64_t per_row = (int64_t)heads * half;
@@ -239,17 +241,18 @@ __global__ void rope_apply_kernel(float *__restrict__ qk, int64_t ld, int64_t ro
     const int p = (int)(idx - r * per_row);
     const int head = p / half, i = p - head * half;
     const float2 cs = tab[(r % S) * half + i];
+    const float sn = sign * cs.y;
     float *q = qk + r * ld + (int64_t)head * hd + 2 * i;
     const float a = q[0], b = q[1];
-    q[0] = a * cs.x - b * cs.y;
-    q[1] = a * cs.y + b * cs.x;
+    q[0] = a * cs.x - b * sn;
+    q[1] = a * sn + b * cs.x;
 }
 
 // The same rotation, two pairs a thread with 16-byte accesses (hd a multiple
 // of 4, rows and the table 16-byte aligned): (cos, sin) of pairs i and i+1
 // come as one float4.
 __global__ void rope_apply2_kernel(float *__restrict__ qk, int64_t ld, int64_t rows, int S, int heads,
-                                   int hd, const float4 *__restrict__ tab) {
+                                   int hd, const float4 *__restrict__ tab, float sign) {
 #pragma clang fp contract(off)
     const int half = hd / 2;
     const int64_t per_row = (int64_t)heads * (half / 2);
@@ -259,13 +262,14 @@ __global__ void rope_apply2_kernel(float *__restrict__ qk, int64_t ld, int64_t r
     const int p = 2 * (int)(idx - r * per_row);
     const int head = p / half, i = p - head * half;
     const float4 cs = tab[((r % S) * half + i) / 2];
+    const float s0 = sign * cs.y, s1 = sign * cs.w;
     float4 *q = reinterpret_cast<float4 *>(qk + r * ld + (int64_t)head * hd + 2 * i);
     const float4 v = *q;
     float4 o;
-    o.x = v.x * cs.x - v.y * cs.y;
-    o.y = v.x * cs.y + v.y * cs.x;
-    o.z = v.z * cs.z - v.w * cs.w;
-    o.w = v.z * cs.w + v.w * cs.z;
+    o.x = v.x * cs.x - v.y * s0;
+    o.y = v.x * s0 + v.y * cs.x;
+    o.z = v.z * cs.z - v.w * s1;
+    o.w = v.z * s1 + v.w * cs.z;
     *q = o;
 }
 
@@ -363,6 +367,30 @@ void transpose_f32(hipStream_t s, const float *src, int64_t rows, int64_t cols, 
 
 static int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
 
+void rope_table(hipStream_t s, float *tab, int64_t S, int64_t hd, double theta) {
+    const int half = (int)(hd / 2);
+    const int64_t nt = S * half;
+    if (nt <= 0) return;
+    rope_table_kernel<<<blocks_for(nt, kThreads), kThreads, 0, s>>>(reinterpret_cast<float2 *>(tab), nt, half,
+                                                                      (int)hd, theta);
+    CATNN_HIP(hipGetLastError());
+}
+
+void rope_apply(hipStream_t s, float *qk, int64_t ld, int64_t rows, int64_t S, int64_t heads, int64_t hd,
+                const float *tab, float sign) {
+    const int half = (int)(hd / 2);
+    const int64_t np = rows * heads * half;
+    if (np <= 0) return;
+    CATNN_REQUIRE(S > 0 && heads * hd <= ld, CATNN_ERR_SHAPE_MISMATCH, "rope: heads exceed the row");
+    if (half % 2 == 0 && ld % 4 == 0 && aligned16(qk) && aligned16(tab))
+        rope_apply2_kernel<<<blocks_for(np / 2, kThreads), kThreads, 0, s>>>(
+            qk, ld, rows, (int)S, (int)heads, (int)hd, reinterpret_cast<const float4 *>(tab), sign);
+    else
+        rope_apply_kernel<<<blocks_for(np, kThreads), kThreads, 0, s>>>(
+            qk, ld, rows, (int)S, (int)heads, (int)hd, reinterpret_cast<const float2 *>(tab), sign);
+    CATNN_HIP(hipGetLastError());
+}
+
 GqaLayout gqa_layout(int64_t tokens, int64_t seq, int64_t n_heads, int64_t n_kv, int64_t head_dim) {
     GqaLayout L;
     L.qkv_ld = (n_heads + 2 * n_kv) * head_dim;
@@ -391,21 +419,8 @@ void gqa_f32(hipStream_t s, const float *x, const float *wqkv, const float *wq, 
         linear_f32(s, x, D, wk, KW, nullptr, nullptr, 0, qkv + QW, LD, T, D, KW, ACT_NONE);
         linear_f32(s, x, D, wv, KW, nullptr, nullptr, 0, qkv + QW + KW, LD, T, D, KW, ACT_NONE);
     }
-    const int half = (int)(head_dim / 2);
-    if (half > 0) {
-        const int64_t nt = S * half;
-        rope_table_kernel<<<blocks_for(nt, kThreads), kThreads, 0, s>>>(tab, nt, half, (int)head_dim, theta);
-        CATNN_HIP(hipGetLastError());
-        const int64_t np = T * (n_heads + n_kv) * half;
-        if (half % 2 == 0 && LD % 4 == 0 && aligned16(qkv) && aligned16(tab))
-            rope_apply2_kernel<<<blocks_for(np / 2, kThreads), kThreads, 0, s>>>(
-                qkv, LD, T, (int)S, (int)(n_heads + n_kv), (int)head_dim, reinterpret_cast<const float4 *>(tab));
-        else
-            rope_apply_kernel<<<blocks_for(np, kThreads), kThreads, 0, s>>>(qkv, LD, T, (int)S,
-                                                                            (int)(n_heads + n_kv),
-                                                                            (int)head_dim, tab);
-        CATNN_HIP(hipGetLastError());
-    }
+    rope_table(s, reinterpret_cast<float *>(tab), S, head_dim, theta);
+    rope_apply(s, qkv, LD, T, S, n_heads + n_kv, head_dim, reinterpret_cast<const float *>(tab), 1.0f);
     attention_core_gqa_f32(s, qkv, qkv + QW, qkv + QW + KW, LD, LD, n_heads / n_kv, window, ctx, QW, B,
                            S, n_heads, head_dim);
     linear_f32(s, ctx, QW, wo, D, nullptr, residual, D, y, D, T, QW, D, ACT_NONE);

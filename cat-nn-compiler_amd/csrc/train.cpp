@@ -72,6 +72,11 @@ struct TParam {
     float *m = nullptr, *v = nullptr;  // Adam moments "adam:{node}:{port}:m|v"
     bf16_t *b = nullptr, *bt = nullptr;
     bf16_t *bt3 = nullptr;  // [cols, 3·rows] split-bf16 transposed copy (hi | hi | lo)
+    // fp32 precision: six-part split copies in the B role, of the rows
+    // ([rows, 6·cols], the input-gradient GEMM) and of the columns
+    // ([cols, 6·rows], the forward).
+    bool want_b6 = false, want_bt6 = false;
+    bf16_t *b6 = nullptr, *bt6 = nullptr;
     // Held as the transpose of the graph's tensor (LmHead's w [V, H] is kept
     // as wᵀ [H, V], a Linear weight, as adjoint.rs:903-913 transposes it);
     // reads transpose back.
@@ -107,6 +112,7 @@ struct catnn_hip_trainer {
     catnn_graph graph;
     float lr = 0.05f;
     int opt = CATNN_OPT_SGD;
+    int prec = CATNN_PREC_BF16;
     uint64_t adam_t = 0;  // AdamState.t shared by every trained parameter
     bool input_grads = false;  // keep the graph inputs' cotangents (run_adjoint)
     std::vector<catnn::TNode> nodes;
@@ -210,16 +216,18 @@ std::vector<float> param_values(const Node &nd, const std::string &port) {
         if (!h) fail(CATNN_ERR_UNKNOWN_PORT, "unknown port " + p + " on interface " + nd.name);
         return h;
     };
-    if (nd.op.kind == CATNN_OP_ATTENTION && port == "wqkv") {
+    if ((nd.op.kind == CATNN_OP_ATTENTION || nd.op.kind == CATNN_OP_GQA_ATTENTION) && port == "wqkv") {
+        // [wq | wk | wv] per row: widths QW, KW, KW (Attention: all D).
         const HostTensor *wq = host("wq"), *wk = host("wk"), *wv = host("wv");
-        const int64_t D = wq->dims.empty() ? 0 : wq->dims[0];
-        CATNN_REQUIRE(wq->numel() == D * D && wk->numel() == D * D && wv->numel() == D * D,
+        CATNN_REQUIRE(wq->dims.size() == 2 && wk->dims.size() == 2 && wv->dims == wk->dims &&
+                          wk->dims[0] == wq->dims[0],
                       CATNN_ERR_SHAPE_MISMATCH, "attention projections");
-        std::vector<float> packed((size_t)(D * 3 * D));
+        const int64_t D = wq->dims[0], QW = wq->dims[1], KW = wk->dims[1], LD = QW + 2 * KW;
+        std::vector<float> packed((size_t)(D * LD));
         for (int64_t r = 0; r < D; ++r) {
-            std::memcpy(&packed[(size_t)(r * 3 * D)], &wq->data[(size_t)(r * D)], (size_t)D * 4);
-            std::memcpy(&packed[(size_t)(r * 3 * D + D)], &wk->data[(size_t)(r * D)], (size_t)D * 4);
-            std::memcpy(&packed[(size_t)(r * 3 * D + 2 * D)], &wv->data[(size_t)(r * D)], (size_t)D * 4);
+            std::memcpy(&packed[(size_t)(r * LD)], &wq->data[(size_t)(r * QW)], (size_t)QW * 4);
+            std::memcpy(&packed[(size_t)(r * LD + QW)], &wk->data[(size_t)(r * KW)], (size_t)KW * 4);
+            std::memcpy(&packed[(size_t)(r * LD + QW + KW)], &wv->data[(size_t)(r * KW)], (size_t)KW * 4);
         }
         return packed;
     }
@@ -236,6 +244,8 @@ std::vector<float> param_values(const Node &nd, const std::string &port) {
 }
 
 }  // namespace
+
+static void refresh_split_copies(Tr &t);
 
 static void plan_trainer(Tr &t) {
     const catnn_graph &g = t.graph;
@@ -269,7 +279,7 @@ static void plan_trainer(Tr &t) {
                 case CATNN_OP_RELU: case CATNN_OP_GELU: case CATNN_OP_LINEAR: case CATNN_OP_MATMUL:
                 case CATNN_OP_LAYER_NORM: case CATNN_OP_ATTENTION: case CATNN_OP_MOE:
                 case CATNN_OP_LM_HEAD: case CATNN_OP_RMS_NORM: case CATNN_OP_EMBEDDING:
-                case CATNN_OP_SWIGLU:
+                case CATNN_OP_SWIGLU: case CATNN_OP_GQA_ATTENTION:
                     break;
                 case CATNN_OP_MIX:
                     CATNN_REQUIRE(tn.ins.size() == 2, CATNN_ERR_WIRING, "mix adjoint needs two inputs");
@@ -330,6 +340,7 @@ static void plan_trainer(Tr &t) {
     auto is_linear = [&](const TNode &x) { return x.kind == CATNN_OP_LINEAR || x.kind == CATNN_OP_MATMUL; };
     std::map<uint32_t, uint64_t> grad_from;  // cotangents first written earlier than their first consumer
     for (auto &gn : t.nodes) {
+        if (t.prec != CATNN_PREC_BF16) break;  // the fused epilogue writes the bf16 operand of the bf16 path
         if (gn.kind != CATNN_OP_GELU || gn.ins.size() != 1 || gn.id == t.out_id || !t.has_grad.count(gn.id)) continue;
         const uint32_t a = gn.ins[0];
         const auto &ca = consumers[a], &cg = consumers[gn.id];
@@ -393,6 +404,10 @@ static void plan_trainer(Tr &t) {
         p->want_b = b || bt;
         p->want_bt = bt;
         p->want_bt3 = bt3;
+        if (t.prec == CATNN_PREC_FP32) {  // every GEMM weight: the two six-part copies instead
+            p->want_b6 = p->want_bt6 = b || bt || bt3;
+            p->want_b = p->want_bt = p->want_bt3 = false;
+        }
         const uint64_t e = (uint64_t)(rows * cols);
         request(t, p->name, e * 4, 0, upd, reinterpret_cast<void **>(&p->master));
         request(t, "grad:" + p->name, e * 4, bwd(tn.tick), upd, reinterpret_cast<void **>(&p->grad));
@@ -403,6 +418,8 @@ static void plan_trainer(Tr &t) {
         if (p->want_b) request(t, "bf16:" + p->name, e * 2, 0, upd, reinterpret_cast<void **>(&p->b));
         if (p->want_bt) request(t, "bf16t:" + p->name, e * 2, 0, upd, reinterpret_cast<void **>(&p->bt));
         if (p->want_bt3) request(t, "bf16t3:" + p->name, e * 6, 0, upd, reinterpret_cast<void **>(&p->bt3));
+        if (p->want_b6) request(t, "bf16x6:" + p->name, e * 12, 0, upd, reinterpret_cast<void **>(&p->b6));
+        if (p->want_bt6) request(t, "bf16x6t:" + p->name, e * 12, 0, upd, reinterpret_cast<void **>(&p->bt6));
         tn.params[port] = p.get();
         t.params.push_back(std::move(p));
     };
@@ -417,9 +434,140 @@ static void plan_trainer(Tr &t) {
     auto scratch = [&](TNode &tn, const std::string &nm, uint64_t bytes) {
         request(t, "scratch:" + tn.node->name + ":" + nm, bytes, bwd(tn.tick), bwd(tn.tick), &tn.B(nm));
     };
+    auto fscratch = [&](TNode &tn, const std::string &nm, uint64_t bytes) {  // forward tick only
+        request(t, "fscratch:" + tn.node->name + ":" + nm, bytes, tn.tick, tn.tick, &tn.B(nm));
+    };
+    constexpr uint64_t X6 = 12;  // bytes per element of a six-part split operand
 
     for (auto &tn : t.nodes) {
         if (t.input_ids.count(tn.id)) continue;
+        if (t.prec != CATNN_PREC_FP32) continue;
+        // fp32 precision: every GEMM on six-part split operands (an fp32
+        // product on the bf16 matrix cores), every tape and cotangent fp32.
+        const Node &nd = *tn.node;
+        const auto &x = tn.in_dims.empty() ? tn.dims : tn.in_dims[0];
+        switch (tn.kind) {
+            case CATNN_OP_LINEAR: case CATNN_OP_MATMUL: case CATNN_OP_LM_HEAD: {
+                int64_t K, N;
+                if (tn.kind == CATNN_OP_LM_HEAD) {
+                    const HostTensor *w = host(nd, "w");
+                    K = nd.op.a[0];
+                    N = nd.op.a[1];
+                    CATNN_REQUIRE(w->numel() == N * K, CATNN_ERR_SHAPE_MISMATCH, "lm_head w");
+                    add_param(tn, "w", K, N, true, false, param_values(nd, "w"), true);
+                    tn.params["w"]->transposed = true;
+                } else {
+                    const HostTensor *w = nd.param("w") ? nd.param("w") : (nd.params.empty() ? nullptr : &nd.params.front().second);
+                    CATNN_REQUIRE(w, CATNN_ERR_UNKNOWN_COMPONENT, "unknown component " + nd.name);
+                    K = w->dims[0];
+                    N = w->dims[1];
+                    add_param(tn, nd.param("w") ? "w" : nd.params.front().first, K, N, true, false, w->data, true);
+                    if (const HostTensor *b = nd.param("b")) add_param(tn, "b", 1, N, false, false, b->data);
+                }
+                const int64_t M = numel(x) / K;
+                fscratch(tn, "x6", (uint64_t)(M * K) * X6);
+                scratch(tn, "dy6", (uint64_t)(M * N) * X6);
+                scratch(tn, "xt6", (uint64_t)(M * K) * X6);
+                scratch(tn, "dyt6", (uint64_t)(M * N) * X6);
+                scratch(tn, "colsum", k::colsum_scratch_bytes(M, (int)N));
+                scratch(tn, "wparts", wparts_bytes(K, N, 6 * M));
+                break;
+            }
+            case CATNN_OP_SWIGLU: {
+                const int64_t H = nd.op.a[0], I = nd.op.a[1], M = numel(x) / std::max<int64_t>(H, 1);
+                CATNN_REQUIRE(x.back() == H, CATNN_ERR_SHAPE_MISMATCH, "swiglu input");
+                const HostTensor *w1 = host(nd, "w1"), *w3 = host(nd, "w3"), *w2 = host(nd, "w2");
+                CATNN_REQUIRE(w1->numel() == H * I && w3->numel() == H * I && w2->numel() == I * H,
+                              CATNN_ERR_SHAPE_MISMATCH, "swiglu weights");
+                add_param(tn, "w1", H, I, true, false, w1->data, true);
+                add_param(tn, "w3", H, I, true, false, w3->data, true);
+                add_param(tn, "w2", I, H, true, false, w2->data, true);
+                for (const char *nm : {"a", "c", "h"}) tape(tn, nm, (uint64_t)(M * I) * 4);
+                fscratch(tn, "x6", (uint64_t)(M * H) * X6);
+                fscratch(tn, "h6", (uint64_t)(M * I) * X6);
+                scratch(tn, "dy6", (uint64_t)(M * H) * X6);
+                for (const char *nm : {"dh", "da", "dc"}) scratch(tn, nm, (uint64_t)(M * I) * 4);
+                for (const char *nm : {"da6", "dc6", "dat6", "dct6", "ht6"}) scratch(tn, nm, (uint64_t)(M * I) * X6);
+                scratch(tn, "xt6", (uint64_t)(M * H) * X6);
+                scratch(tn, "dyt6", (uint64_t)(M * H) * X6);
+                scratch(tn, "wparts", std::max(wparts_bytes(H, I, 6 * M), wparts_bytes(I, H, 6 * M)));
+                break;
+            }
+            case CATNN_OP_ATTENTION: case CATNN_OP_GQA_ATTENTION: {
+                const bool gqa = tn.kind == CATNN_OP_GQA_ATTENTION;
+                const int64_t Bt = x[0], S = x[1], D = x[2], T = Bt * S, H = nd.op.a[0];
+                const int64_t hd = gqa ? nd.op.a[2] : nd.op.a[2], HKV = gqa ? nd.op.a[1] : H;
+                const int64_t QW = H * hd, KW = HKV * hd, LD = QW + 2 * KW;
+                add_param(tn, "wqkv", D, LD, true, false, param_values(nd, "wqkv"), true);
+                add_param(tn, "wo", QW, D, true, false, host(nd, "wo")->data, true);
+                tape(tn, "qkv", (uint64_t)(T * LD) * 4);
+                tape(tn, "ctx", (uint64_t)(T * QW) * 4);
+                tape(tn, "lse", (uint64_t)(T * H) * 4);
+                if (gqa) tape(tn, "rope", (uint64_t)(S * std::max<int64_t>(hd / 2, 1)) * 8);
+                fscratch(tn, "x6", (uint64_t)(T * D) * X6);
+                fscratch(tn, "ctx6", (uint64_t)(T * QW) * X6);
+                scratch(tn, "dy6", (uint64_t)(T * D) * X6);
+                scratch(tn, "dctx", (uint64_t)(T * QW) * 4);
+                scratch(tn, "ctxt6", (uint64_t)(T * QW) * X6);
+                scratch(tn, "dyt6", (uint64_t)(T * D) * X6);
+                scratch(tn, "dqkv", (uint64_t)(T * LD) * 4);
+                scratch(tn, "dqkv6", (uint64_t)(T * LD) * X6);
+                scratch(tn, "xt6", (uint64_t)(T * D) * X6);
+                scratch(tn, "dqkvt6", (uint64_t)(T * LD) * X6);
+                scratch(tn, "dscr", k::attention_bwd_scratch_bytes(Bt, S, H));
+                scratch(tn, "wparts", std::max(wparts_bytes(QW, D, 6 * T), wparts_bytes(D, LD, 6 * T)));
+                break;
+            }
+            case CATNN_OP_MOE: {
+                const int64_t E = nd.op.a[0], K = nd.op.a[1], H = x.back(), T = numel(x) / H;
+                const int64_t I = host(nd, "e0.w1")->dims[1];
+                const int64_t P = T * K + E * (kPad - 1);
+                const int64_t Pr = (P + kPad - 1) / kPad * kPad;
+                add_param(tn, "gate", H, E, false, false, host(nd, "gate")->data);
+                for (int64_t e = 0; e < E; ++e) {
+                    const std::string p = "e" + std::to_string(e);
+                    add_param(tn, p + ".w1", H, I, true, false, host(nd, p + ".w1")->data);
+                    add_param(tn, p + ".w3", H, I, true, false, host(nd, p + ".w3")->data);
+                    add_param(tn, p + ".w2", I, H, true, false, host(nd, p + ".w2")->data);
+                }
+                const int64_t max_tiles = (T * K + k::gemm_bf16_tile_rows() - 1) / k::gemm_bf16_tile_rows() + E;
+                tape(tn, "idx", (uint64_t)(T * K) * 4, true);  // readable after the step
+                tape(tn, "w", (uint64_t)(T * K) * 4);
+                tape(tn, "counts", (uint64_t)E * 4);
+                tape(tn, "offsets", (uint64_t)(E + 1) * 4);
+                tape(tn, "sop", (uint64_t)Pr * 4);
+                tape(tn, "pos", (uint64_t)(T * K) * 4);
+                tape(tn, "tiles", (uint64_t)(2 * max_tiles + 1) * 4);
+                tape(tn, "perm_scratch", k::moe_permute_scratch_bytes(T, K, E));
+                for (const char *nm : {"a", "c", "h"}) tape(tn, nm, (uint64_t)(Pr * I) * 4);
+                tape(tn, "ys", (uint64_t)(Pr * H) * 4);
+                fscratch(tn, "x6", (uint64_t)(T * H) * X6);
+                fscratch(tn, "h6", (uint64_t)(Pr * I) * X6);
+                scratch(tn, "dys", (uint64_t)(Pr * H) * 4);
+                scratch(tn, "dw", (uint64_t)(T * K) * 4);
+                scratch(tn, "dys6", (uint64_t)(Pr * H) * X6);
+                for (const char *nm : {"dh", "da", "dc"}) scratch(tn, nm, (uint64_t)(Pr * I) * 4);
+                for (const char *nm : {"da6", "dc6", "ht6", "dat6", "dct6"}) scratch(tn, nm, (uint64_t)(Pr * I) * X6);
+                scratch(tn, "dxs", (uint64_t)(Pr * H) * 4);
+                scratch(tn, "xpt6", (uint64_t)(Pr * H) * X6);
+                scratch(tn, "dyst6", (uint64_t)(Pr * H) * X6);
+                scratch(tn, "seg6", (uint64_t)(2 * E + 1) * 4);
+                scratch(tn, "dl", (uint64_t)(T * E) * 4);
+                scratch(tn, "router", k::router_backward_scratch_bytes((int)T, (int)H, (int)E));
+                break;
+            }
+            default:
+                break;
+        }
+    }
+
+    for (auto &tn : t.nodes) {
+        if (t.input_ids.count(tn.id)) continue;
+        if (t.prec == CATNN_PREC_FP32 &&
+            (tn.kind == CATNN_OP_LINEAR || tn.kind == CATNN_OP_MATMUL || tn.kind == CATNN_OP_LM_HEAD ||
+             tn.kind == CATNN_OP_SWIGLU || tn.kind == CATNN_OP_ATTENTION || tn.kind == CATNN_OP_GQA_ATTENTION ||
+             tn.kind == CATNN_OP_MOE))
+            continue;  // planned above
         const Node &nd = *tn.node;
         const auto &x = tn.in_dims.empty() ? tn.dims : tn.in_dims[0];
         switch (tn.kind) {
@@ -535,6 +683,30 @@ static void plan_trainer(Tr &t) {
                 scratch(tn, "wparts", std::max(wparts_bytes(D, D, T), wparts_bytes(D, 3 * D, T)));
                 break;
             }
+            case CATNN_OP_GQA_ATTENTION: {  // moe.rs:62-136; gqa_backward, adjoint.rs:287-440
+                const int64_t Bt = x[0], S = x[1], D = x[2], T = Bt * S;
+                const int64_t H = nd.op.a[0], HKV = nd.op.a[1], hd = nd.op.a[2];
+                const int64_t QW = H * hd, KW = HKV * hd, LD = QW + 2 * KW;
+                add_param(tn, "wqkv", D, LD, true, false, param_values(nd, "wqkv"), true);
+                add_param(tn, "wo", QW, D, true, false, host(nd, "wo")->data, true);
+                tape(tn, "x3", (uint64_t)(T * 3 * D) * 2);
+                tape(tn, "qkv", (uint64_t)(T * LD) * 4);  // q and k after RoPE
+                tape(tn, "ctx", (uint64_t)(T * QW) * 4);
+                tape(tn, "ctx3", (uint64_t)(T * 3 * QW) * 2);
+                tape(tn, "lse", (uint64_t)(T * H) * 4);
+                tape(tn, "rope", (uint64_t)(S * std::max<int64_t>(hd / 2, 1)) * 8);
+                scratch(tn, "dyb", (uint64_t)(T * D) * 2);
+                scratch(tn, "dybt", (uint64_t)(T * D) * 2);
+                scratch(tn, "ctxt", (uint64_t)(T * QW) * 2);
+                scratch(tn, "dctx", (uint64_t)(T * QW) * 4);
+                scratch(tn, "dqkv", (uint64_t)(T * LD) * 4);
+                scratch(tn, "dqkvb", (uint64_t)(T * LD) * 2);
+                scratch(tn, "dqkvt", (uint64_t)(T * LD) * 2);
+                scratch(tn, "xbt", (uint64_t)(T * D) * 2);
+                scratch(tn, "dscr", k::attention_bwd_scratch_bytes(Bt, S, H));
+                scratch(tn, "wparts", std::max(wparts_bytes(QW, D, T), wparts_bytes(D, LD, T)));
+                break;
+            }
             case CATNN_OP_MOE: {
                 const int64_t E = nd.op.a[0], K = nd.op.a[1], H = x.back(), T = numel(x) / H;
                 const int64_t I = host(nd, "e0.w1")->dims[1];
@@ -626,6 +798,7 @@ static void upload_params(Tr &t) {
     }
     t.adam_t = 0;
     k::sgd_multi(s, t.sgd_table, t.sgd_n, t.sgd_tiles, k::sgd_rule(0.f), false);
+    if (t.prec == CATNN_PREC_FP32) refresh_split_copies(t);
 }
 
 static void reserve_and_upload(Tr &t) {
@@ -654,9 +827,293 @@ static void reserve_and_upload(Tr &t) {
     CATNN_HIP(hipStreamSynchronize(t.dev->stream));  // before `tab` goes out of scope
 }
 
+// ------------------------------------------------- fp32 precision GEMMs
+// Every GEMM of these ops on six-part split operands (k::split6_*): A rows
+// from fp32 values, B from the weights' six-part copies (b6, bt6) or from
+// fp32 values transposed; K' = 6K.  Tapes and cotangents stay fp32.
+
+static bool is_gemm_op(int kind) {
+    return kind == CATNN_OP_LINEAR || kind == CATNN_OP_MATMUL || kind == CATNN_OP_LM_HEAD ||
+           kind == CATNN_OP_SWIGLU || kind == CATNN_OP_ATTENTION || kind == CATNN_OP_GQA_ATTENTION ||
+           kind == CATNN_OP_MOE;
+}
+
+// C = A6·B6ᵀ over the six-part K' = 6K (EPI_LINEAR: + bias).
+static void gemm6(hipStream_t s, const bf16_t *A6, int64_t lda, const bf16_t *B6, int64_t ldb, int64_t M, int64_t N,
+                  int64_t K, float *C, int64_t ldc, const float *bias = nullptr) {
+    k::GemmBf16Params p = gp();
+    p.A = A6; p.lda = lda; p.B = B6; p.ldb = ldb;
+    p.M = (int)M; p.N = (int)N; p.K = (int)(6 * K);
+    p.epi = k::EPI_LINEAR; p.bias = bias;
+    p.C32 = C; p.ldc32 = ldc;
+    k::gemm_bf16_launch(s, p);
+}
+
+static void forward_gemm_f32(Tr &t, TNode &tn) {
+    hipStream_t s = t.dev->stream;
+    const Node &nd = *tn.node;
+    float *y = t.val.at(tn.id);
+    const float *x = t.val.at(tn.ins[0]);
+    const auto &xd = tn.in_dims[0];
+    const int64_t nx = numel(xd);
+    switch (tn.kind) {
+        case CATNN_OP_LINEAR: case CATNN_OP_MATMUL: case CATNN_OP_LM_HEAD: {
+            TParam *w = tn.params.begin()->second;
+            for (auto &kv : tn.params) if (kv.first != "b") w = kv.second;
+            TParam *b = tn.params.count("b") ? tn.params["b"] : nullptr;
+            const int64_t K = w->rows, N = w->cols, M = nx / K;
+            bf16_t *x6 = (bf16_t *)tn.B("x6");
+            k::split6_rows(s, x, K, M, (int)K, false, x6, 6 * K);
+            gemm6(s, x6, 6 * K, w->bt6, 6 * K, M, N, K, y, N, b ? b->master : nullptr);
+            break;
+        }
+        case CATNN_OP_SWIGLU: {
+            TParam *w1 = tn.params["w1"], *w3 = tn.params["w3"], *w2 = tn.params["w2"];
+            const int64_t H = w1->rows, I = w1->cols, M = nx / H;
+            bf16_t *x6 = (bf16_t *)tn.B("x6"), *h6 = (bf16_t *)tn.B("h6");
+            float *a = (float *)tn.B("a"), *c = (float *)tn.B("c"), *h = (float *)tn.B("h");
+            k::split6_rows(s, x, H, M, (int)H, false, x6, 6 * H);
+            gemm6(s, x6, 6 * H, w1->bt6, 6 * H, M, I, H, a, I);
+            gemm6(s, x6, 6 * H, w3->bt6, 6 * H, M, I, H, c, I);
+            k::swiglu_h(s, a, c, h, M * I);
+            k::split6_rows(s, h, I, M, (int)I, false, h6, 6 * I);
+            gemm6(s, h6, 6 * I, w2->bt6, 6 * I, M, H, I, y, H);
+            break;
+        }
+        case CATNN_OP_ATTENTION: case CATNN_OP_GQA_ATTENTION: {
+            const bool gqa = tn.kind == CATNN_OP_GQA_ATTENTION;
+            const int64_t Bt = xd[0], S = xd[1], D = xd[2], T = Bt * S;
+            const int64_t H = nd.op.a[0], hd = nd.op.a[2], HKV = gqa ? nd.op.a[1] : H;
+            const int64_t QW = H * hd, KW = HKV * hd, LD = QW + 2 * KW;
+            bf16_t *x6 = (bf16_t *)tn.B("x6"), *ctx6 = (bf16_t *)tn.B("ctx6");
+            float *qkv = (float *)tn.B("qkv"), *ctx = (float *)tn.B("ctx"), *lse = (float *)tn.B("lse");
+            k::split6_rows(s, x, D, T, (int)D, false, x6, 6 * D);
+            gemm6(s, x6, 6 * D, tn.params["wqkv"]->bt6, 6 * D, T, LD, D, qkv, LD);
+            if (gqa) {
+                float *rope = (float *)tn.B("rope");
+                k::rope_table(s, rope, S, hd, (double)nd.op.a[5]);
+                k::rope_apply(s, qkv, LD, T, S, H + HKV, hd, rope, 1.0f);
+                k::attention_core_fwd_lse_gqa(s, qkv, LD, qkv + QW, qkv + QW + KW, LD, H / HKV,
+                                              nd.op.a[4] > 0 ? nd.op.a[4] : 0, ctx, QW, lse, Bt, S, H, hd);
+            } else {
+                k::attention_core_fwd_lse(s, qkv, qkv + D, qkv + 2 * D, 3 * D, ctx, D, lse, Bt, S, H, hd,
+                                          (nd.op.flags & CATNN_FLAG_CAUSAL) != 0);
+            }
+            k::split6_rows(s, ctx, QW, T, (int)QW, false, ctx6, 6 * QW);
+            gemm6(s, ctx6, 6 * QW, tn.params["wo"]->bt6, 6 * QW, T, D, QW, y, D);
+            break;
+        }
+        case CATNN_OP_MOE: {
+            const int64_t E = nd.op.a[0], K = nd.op.a[1], H = xd.back(), T = nx / H;
+            const int64_t I = tn.params["e0.w1"]->cols;
+            const int64_t P = T * K + E * (kPad - 1);
+            const int64_t Pr = (P + kPad - 1) / kPad * kPad;
+            int32_t *idx = (int32_t *)tn.B("idx"), *counts = (int32_t *)tn.B("counts");
+            int32_t *offs = (int32_t *)tn.B("offsets"), *sop = (int32_t *)tn.B("sop");
+            int32_t *pos = (int32_t *)tn.B("pos"), *tiles = (int32_t *)tn.B("tiles");
+            float *w = (float *)tn.B("w");
+            float *a = (float *)tn.B("a"), *c = (float *)tn.B("c"), *h = (float *)tn.B("h");
+            const int max_tiles = (int)((T * K + k::gemm_bf16_tile_rows() - 1) / k::gemm_bf16_tile_rows() + E);
+            k::moe_route_f32(s, x, tn.params["gate"]->master, T, H, E, K, idx, w, nullptr);
+            k::moe_permute_padded(s, idx, T, K, E, kPad, Pr, counts, offs, sop, pos, tn.B("perm_scratch"));
+            k::build_tiles(s, offs, (int)E, tiles, tiles + max_tiles, tiles + 2 * max_tiles);
+            bf16_t *x6 = (bf16_t *)tn.B("x6"), *h6 = (bf16_t *)tn.B("h6");
+            k::split6_rows(s, x, H, T, (int)H, false, x6, 6 * H);
+            k::GemmBf16Params p = gp();
+            p.grid = k::GRID_ROWS;
+            p.tile_expert = tiles; p.tile_row0 = tiles + max_tiles; p.n_tiles = tiles + 2 * max_tiles;
+            p.seg_offsets = offs; p.seg_counts = counts; p.max_tiles = max_tiles; p.n_experts = (int)E;
+            p.epi = k::EPI_STORE;
+            // a = x·w1, c = x·w3 per expert segment, rows gathered through the permutation
+            p.A = x6; p.lda = 6 * H; p.a_rows = sop; p.a_row_div = (int)K;
+            p.ldb = 6 * H; p.M = 0; p.N = (int)I; p.K = (int)(6 * H);
+            p.ldc32 = I;
+            for (const char *port : {".w1", ".w3"}) {
+                for (int64_t e = 0; e < E; ++e) p.B_e[e] = tn.params["e" + std::to_string(e) + port]->bt6;
+                p.C32 = port[2] == '1' ? a : c;
+                k::gemm_bf16_launch(s, p);
+            }
+            k::swiglu_h(s, a, c, h, Pr * I);
+            k::split6_rows(s, h, I, Pr, (int)I, false, h6, 6 * I);
+            // ys = h·w2
+            p.A = h6; p.lda = 6 * I; p.a_rows = nullptr; p.a_row_div = 1;
+            for (int64_t e = 0; e < E; ++e) p.B_e[e] = tn.params["e" + std::to_string(e) + ".w2"]->bt6;
+            p.ldb = 6 * I; p.N = (int)H; p.K = (int)(6 * I);
+            p.C32 = (float *)tn.B("ys"); p.ldc32 = H;
+            k::gemm_bf16_launch(s, p);
+            k::moe_combine(s, (float *)tn.B("ys"), pos, w, T, K, H, y);
+            break;
+        }
+        default:
+            fail(CATNN_ERR_UNSUPPORTED, "training: op " + op_name(tn.kind));
+    }
+}
+
+static void backward_gemm_f32(Tr &t, TNode &tn) {
+    hipStream_t s = t.dev->stream;
+    const Node &nd = *tn.node;
+    const float *dy = t.grad.at(tn.id);
+    float *dx = t.input_ids.count(tn.ins[0]) && !t.input_grads ? nullptr : t.grad.at(tn.ins[0]);
+    const bool acc = !tn.first_writer[0];
+    const float *x = t.val.at(tn.ins[0]);
+    const auto &xd = tn.in_dims[0];
+    const int64_t nx = numel(xd);
+    switch (tn.kind) {
+        case CATNN_OP_LINEAR: case CATNN_OP_MATMUL: case CATNN_OP_LM_HEAD: {
+            TParam *w = tn.params.begin()->second;
+            for (auto &kv : tn.params) if (kv.first != "b") w = kv.second;
+            TParam *b = tn.params.count("b") ? tn.params["b"] : nullptr;
+            const int64_t K = w->rows, N = w->cols, M = nx / K;
+            bf16_t *dy6 = (bf16_t *)tn.B("dy6"), *xt6 = (bf16_t *)tn.B("xt6"), *dyt6 = (bf16_t *)tn.B("dyt6");
+            k::split6_rows(s, dy, N, M, (int)N, false, dy6, 6 * N);
+            if (dx) gemm_nt(s, dy6, 6 * N, w->b6, 6 * N, (int)M, (int)K, (int)(6 * N), dx, K, acc);
+            k::split6_transpose(s, x, K, nullptr, 1, (int)M, (int)K, false, xt6, 6 * M);
+            k::split6_transpose(s, dy, N, nullptr, 1, (int)M, (int)N, true, dyt6, 6 * M);
+            gemm_nt(s, xt6, 6 * M, dyt6, 6 * M, (int)K, (int)N, (int)(6 * M), w->grad, N, false,
+                    (float *)tn.B("wparts"));
+            if (b) k::colsum(s, dy, M, (int)N, b->grad, false, (float *)tn.B("colsum"));
+            break;
+        }
+        case CATNN_OP_SWIGLU: {  // swiglu_backward, adjoint.rs:217-251
+            TParam *w1 = tn.params["w1"], *w3 = tn.params["w3"], *w2 = tn.params["w2"];
+            const int64_t H = w1->rows, I = w1->cols, M = nx / H;
+            auto B = [&](const char *nm) { return (bf16_t *)tn.B(nm); };
+            auto F = [&](const char *nm) { return (float *)tn.B(nm); };
+            float *wparts = F("wparts");
+            k::split6_rows(s, dy, H, M, (int)H, false, B("dy6"), 6 * H);
+            gemm_nt(s, B("dy6"), 6 * H, w2->b6, 6 * H, (int)M, (int)I, (int)(6 * H), F("dh"), I, false);
+            k::swiglu_dadc_f32(s, F("dh"), F("a"), F("c"), F("da"), F("dc"), M * I);
+            k::split6_rows(s, F("da"), I, M, (int)I, false, B("da6"), 6 * I);
+            k::split6_rows(s, F("dc"), I, M, (int)I, false, B("dc6"), 6 * I);
+            if (dx) {
+                gemm_nt(s, B("da6"), 6 * I, w1->b6, 6 * I, (int)M, (int)H, (int)(6 * I), dx, H, acc);
+                gemm_nt(s, B("dc6"), 6 * I, w3->b6, 6 * I, (int)M, (int)H, (int)(6 * I), dx, H, true);
+            }
+            k::split6_transpose(s, x, H, nullptr, 1, (int)M, (int)H, false, B("xt6"), 6 * M);
+            k::split6_transpose(s, F("da"), I, nullptr, 1, (int)M, (int)I, true, B("dat6"), 6 * M);
+            k::split6_transpose(s, F("dc"), I, nullptr, 1, (int)M, (int)I, true, B("dct6"), 6 * M);
+            gemm_nt(s, B("xt6"), 6 * M, B("dat6"), 6 * M, (int)H, (int)I, (int)(6 * M), w1->grad, I, false, wparts);
+            gemm_nt(s, B("xt6"), 6 * M, B("dct6"), 6 * M, (int)H, (int)I, (int)(6 * M), w3->grad, I, false, wparts);
+            k::split6_transpose(s, F("h"), I, nullptr, 1, (int)M, (int)I, false, B("ht6"), 6 * M);
+            k::split6_transpose(s, dy, H, nullptr, 1, (int)M, (int)H, true, B("dyt6"), 6 * M);
+            gemm_nt(s, B("ht6"), 6 * M, B("dyt6"), 6 * M, (int)I, (int)H, (int)(6 * M), w2->grad, H, false, wparts);
+            break;
+        }
+        case CATNN_OP_ATTENTION: case CATNN_OP_GQA_ATTENTION: {
+            const bool gqa = tn.kind == CATNN_OP_GQA_ATTENTION;
+            const int64_t Bt = xd[0], S = xd[1], D = xd[2], T = Bt * S;
+            const int64_t H = nd.op.a[0], hd = nd.op.a[2], HKV = gqa ? nd.op.a[1] : H;
+            const int64_t QW = H * hd, KW = HKV * hd, LD = QW + 2 * KW;
+            TParam *wqkv = tn.params["wqkv"], *wo = tn.params["wo"];
+            auto B = [&](const char *nm) { return (bf16_t *)tn.B(nm); };
+            auto F = [&](const char *nm) { return (float *)tn.B(nm); };
+            float *qkv = F("qkv"), *ctx = F("ctx"), *dqkv = F("dqkv"), *wparts = F("wparts");
+            k::split6_rows(s, dy, D, T, (int)D, false, B("dy6"), 6 * D);
+            gemm_nt(s, B("dy6"), 6 * D, wo->b6, 6 * D, (int)T, (int)QW, (int)(6 * D), F("dctx"), QW, false);
+            k::split6_transpose(s, ctx, QW, nullptr, 1, (int)T, (int)QW, false, B("ctxt6"), 6 * T);
+            k::split6_transpose(s, dy, D, nullptr, 1, (int)T, (int)D, true, B("dyt6"), 6 * T);
+            gemm_nt(s, B("ctxt6"), 6 * T, B("dyt6"), 6 * T, (int)QW, (int)D, (int)(6 * T), wo->grad, D, false, wparts);
+            if (gqa) {
+                k::attention_core_bwd_gqa(s, qkv, LD, qkv + QW, qkv + QW + KW, LD, H / HKV,
+                                          nd.op.a[4] > 0 ? nd.op.a[4] : 0, ctx, F("dctx"), QW, F("lse"), dqkv, LD,
+                                          dqkv + QW, dqkv + QW + KW, LD, Bt, S, H, hd, true, F("dscr"));
+                k::rope_apply(s, dqkv, LD, T, S, H + HKV, hd, F("rope"), -1.0f);
+            } else {
+                k::attention_core_bwd(s, qkv, qkv + D, qkv + 2 * D, 3 * D, ctx, F("dctx"), D, F("lse"), dqkv,
+                                      dqkv + D, dqkv + 2 * D, 3 * D, Bt, S, H, hd,
+                                      (nd.op.flags & CATNN_FLAG_CAUSAL) != 0, F("dscr"));
+            }
+            k::split6_rows(s, dqkv, LD, T, (int)LD, false, B("dqkv6"), 6 * LD);
+            if (dx) gemm_nt(s, B("dqkv6"), 6 * LD, wqkv->b6, 6 * LD, (int)T, (int)D, (int)(6 * LD), dx, D, acc);
+            k::split6_transpose(s, x, D, nullptr, 1, (int)T, (int)D, false, B("xt6"), 6 * T);
+            k::split6_transpose(s, dqkv, LD, nullptr, 1, (int)T, (int)LD, true, B("dqkvt6"), 6 * T);
+            gemm_nt(s, B("xt6"), 6 * T, B("dqkvt6"), 6 * T, (int)D, (int)LD, (int)(6 * T), wqkv->grad, LD, false,
+                    wparts);
+            break;
+        }
+        case CATNN_OP_MOE: {
+            const int64_t E = nd.op.a[0], K = nd.op.a[1], H = xd.back(), T = nx / H;
+            const int64_t I = tn.params["e0.w1"]->cols;
+            const int64_t P = T * K + E * (kPad - 1);
+            const int64_t Pr = (P + kPad - 1) / kPad * kPad;
+            auto B = [&](const char *nm) { return (bf16_t *)tn.B(nm); };
+            auto F = [&](const char *nm) { return (float *)tn.B(nm); };
+            int32_t *idx = (int32_t *)tn.B("idx"), *counts = (int32_t *)tn.B("counts");
+            int32_t *offs = (int32_t *)tn.B("offsets"), *sop = (int32_t *)tn.B("sop");
+            int32_t *pos = (int32_t *)tn.B("pos"), *tiles = (int32_t *)tn.B("tiles");
+            int32_t *seg6 = (int32_t *)tn.B("seg6");
+            const int max_tiles = (int)((T * K + k::gemm_bf16_tile_rows() - 1) / k::gemm_bf16_tile_rows() + E);
+            float *w = F("w"), *dw = F("dw"), *dys = F("dys");
+            k::moe_slot_grads_f32(s, sop, w, F("ys"), dy, (int)K, (int)H, (int)Pr, dys, dw);
+            k::split6_rows(s, dys, H, Pr, (int)H, false, B("dys6"), 6 * H);
+            k::GemmBf16Params p = gp();
+            p.grid = k::GRID_ROWS;
+            p.tile_expert = tiles; p.tile_row0 = tiles + max_tiles; p.n_tiles = tiles + 2 * max_tiles;
+            p.seg_offsets = offs; p.seg_counts = counts; p.max_tiles = max_tiles; p.n_experts = (int)E;
+            p.epi = k::EPI_STORE;
+            // dh = dys·w2ᵀ
+            p.A = B("dys6"); p.lda = 6 * H; p.ldb = 6 * H; p.N = (int)I; p.K = (int)(6 * H);
+            for (int64_t e = 0; e < E; ++e) p.B_e[e] = tn.params["e" + std::to_string(e) + ".w2"]->b6;
+            p.C32 = F("dh"); p.ldc32 = I;
+            k::gemm_bf16_launch(s, p);
+            k::swiglu_dadc_f32(s, F("dh"), F("a"), F("c"), F("da"), F("dc"), Pr * I);
+            k::split6_rows(s, F("da"), I, Pr, (int)I, false, B("da6"), 6 * I);
+            k::split6_rows(s, F("dc"), I, Pr, (int)I, false, B("dc6"), 6 * I);
+            // dxs = da·w1ᵀ + dc·w3ᵀ
+            p.lda = 6 * I; p.ldb = 6 * I; p.N = (int)H; p.K = (int)(6 * I);
+            p.C32 = F("dxs"); p.ldc32 = H;
+            p.A = B("da6"); p.accumulate = 0;
+            for (int64_t e = 0; e < E; ++e) p.B_e[e] = tn.params["e" + std::to_string(e) + ".w1"]->b6;
+            k::gemm_bf16_launch(s, p);
+            p.A = B("dc6"); p.accumulate = 1;
+            for (int64_t e = 0; e < E; ++e) p.B_e[e] = tn.params["e" + std::to_string(e) + ".w3"]->b6;
+            k::gemm_bf16_launch(s, p);
+            // Expert weight gradients: segments of the six-part K are six times the rows'.
+            k::scale_i32(s, offs, (int)(E + 1), 6, seg6);
+            k::scale_i32(s, counts, (int)E, 6, seg6 + E + 1);
+            k::split6_transpose(s, x, H, sop, (int)K, (int)Pr, (int)H, false, B("xpt6"), 6 * Pr);
+            k::split6_transpose(s, F("h"), I, nullptr, 1, (int)Pr, (int)I, false, B("ht6"), 6 * Pr);
+            k::split6_transpose(s, dys, H, nullptr, 1, (int)Pr, (int)H, true, B("dyst6"), 6 * Pr);
+            k::split6_transpose(s, F("da"), I, nullptr, 1, (int)Pr, (int)I, true, B("dat6"), 6 * Pr);
+            k::split6_transpose(s, F("dc"), I, nullptr, 1, (int)Pr, (int)I, true, B("dct6"), 6 * Pr);
+            k::GemmBf16Params r = gp();
+            r.grid = k::GRID_SEGK; r.seg_offsets = seg6; r.seg_counts = seg6 + E + 1; r.segk_aligned = 1;
+            r.n_experts = (int)E; r.epi = k::EPI_STORE;
+            auto segk = [&](const bf16_t *A, const bf16_t *Bm, int M, int N, const char *port) {
+                r.A = A; r.lda = 6 * Pr; r.B = Bm; r.ldb = 6 * Pr; r.M = M; r.N = N; r.K = (int)(6 * Pr); r.ldc32 = N;
+                for (int64_t e = 0; e < E; ++e) r.C_e[e] = tn.params["e" + std::to_string(e) + port]->grad;
+                k::gemm_bf16_launch(s, r);
+            };
+            segk(B("ht6"), B("dyst6"), (int)I, (int)H, ".w2");
+            segk(B("xpt6"), B("dat6"), (int)H, (int)I, ".w1");
+            segk(B("xpt6"), B("dct6"), (int)H, (int)I, ".w3");
+            // Router (straight-through on the indices) and the input cotangent.
+            float *dl = F("dl");
+            k::router_backward(s, idx, w, dw, x, (int)T, (int)H, (int)E, (int)K, dl, tn.params["gate"]->grad,
+                               F("router"));
+            if (dx) k::moe_dx(s, F("dxs"), pos, dl, tn.params["gate"]->master, (int)T, (int)K, (int)H, (int)E, dx, acc);
+            break;
+        }
+        default:
+            fail(CATNN_ERR_UNSUPPORTED, "training: op " + op_name(tn.kind));
+    }
+}
+
+// The six-part copies of every GEMM weight from its fp32 master.
+static void refresh_split_copies(Tr &t) {
+    hipStream_t s = t.dev->stream;
+    for (auto &p : t.params) {
+        if (p->want_b6) k::split6_rows(s, p->master, p->cols, p->rows, (int)p->cols, true, p->b6, 6 * p->cols);
+        if (p->want_bt6)
+            k::split6_transpose(s, p->master, p->cols, nullptr, 1, (int)p->rows, (int)p->cols, true, p->bt6,
+                                6 * p->rows);
+    }
+}
+
 // ------------------------------------------------------------ forward
 
 static void forward_node(Tr &t, TNode &tn) {
+    if (t.prec == CATNN_PREC_FP32 && is_gemm_op(tn.kind)) return forward_gemm_f32(t, tn);
     hipStream_t s = t.dev->stream;
     const Node &nd = *tn.node;
     float *y = t.val.at(tn.id);
@@ -758,6 +1215,26 @@ static void forward_node(Tr &t, TNode &tn) {
             gemm_nt(s, ctx3, 3 * D, tn.params["wo"]->bt3, 3 * D, (int)T, (int)D, (int)(3 * D), y, D, false);
             break;
         }
+        case CATNN_OP_GQA_ATTENTION: {
+            const int64_t Bt = xd[0], S = xd[1], D = xd[2], T = Bt * S;
+            const int64_t H = nd.op.a[0], HKV = nd.op.a[1], hd = nd.op.a[2];
+            const int64_t QW = H * hd, KW = HKV * hd, LD = QW + 2 * KW;
+            // sliding_window None is −1; Some(0) means no window, as the inference path.
+            const int64_t window = nd.op.a[4] > 0 ? nd.op.a[4] : 0;
+            bf16_t *x3 = (bf16_t *)tn.B("x3"), *ctx3 = (bf16_t *)tn.B("ctx3");
+            float *qkv = (float *)tn.B("qkv"), *ctx = (float *)tn.B("ctx"), *rope = (float *)tn.B("rope");
+            // Projections split-bf16 as Attention's; RoPE on q and k in place;
+            // the grouped, windowed causal core on fp32 MFMA with its lse kept.
+            k::split3_rows(s, x, D, T, (int)D, x3, 3 * D);
+            gemm_nt(s, x3, 3 * D, tn.params["wqkv"]->bt3, 3 * D, (int)T, (int)LD, (int)(3 * D), qkv, LD, false);
+            k::rope_table(s, rope, S, hd, (double)nd.op.a[5]);
+            k::rope_apply(s, qkv, LD, T, S, H + HKV, hd, rope, 1.0f);
+            k::attention_core_fwd_lse_gqa(s, qkv, LD, qkv + QW, qkv + QW + KW, LD, H / HKV, window, ctx, QW,
+                                          (float *)tn.B("lse"), Bt, S, H, hd);
+            k::split3_rows(s, ctx, QW, T, (int)QW, ctx3, 3 * QW);
+            gemm_nt(s, ctx3, 3 * QW, tn.params["wo"]->bt3, 3 * QW, (int)T, (int)D, (int)(3 * QW), y, D, false);
+            break;
+        }
         case CATNN_OP_MOE: {
             const int64_t E = nd.op.a[0], K = nd.op.a[1], H = xd.back(), T = nx / H;
             const int64_t I = tn.params["e0.w1"]->cols;
@@ -811,6 +1288,7 @@ static void forward_node(Tr &t, TNode &tn) {
 // ----------------------------------------------------------- backward
 
 static void backward_node(Tr &t, TNode &tn) {
+    if (t.prec == CATNN_PREC_FP32 && is_gemm_op(tn.kind)) return backward_gemm_f32(t, tn);
     hipStream_t s = t.dev->stream;
     const Node &nd = *tn.node;
     const float *dy = t.grad.at(tn.id);
@@ -953,6 +1431,38 @@ static void backward_node(Tr &t, TNode &tn) {
                     (float *)tn.B("wparts"));
             break;
         }
+        case CATNN_OP_GQA_ATTENTION: {  // gqa_backward, adjoint.rs:287-440
+            const int64_t Bt = xd[0], S = xd[1], D = xd[2], T = Bt * S;
+            const int64_t H = nd.op.a[0], HKV = nd.op.a[1], hd = nd.op.a[2];
+            const int64_t QW = H * hd, KW = HKV * hd, LD = QW + 2 * KW;
+            const int64_t window = nd.op.a[4] > 0 ? nd.op.a[4] : 0;
+            TParam *wqkv = tn.params["wqkv"], *wo = tn.params["wo"];
+            bf16_t *dyb = (bf16_t *)tn.B("dyb"), *dybt = (bf16_t *)tn.B("dybt"), *ctxt = (bf16_t *)tn.B("ctxt");
+            bf16_t *dqkvb = (bf16_t *)tn.B("dqkvb"), *dqkvt = (bf16_t *)tn.B("dqkvt");
+            bf16_t *x3 = (bf16_t *)tn.B("x3"), *xbt = (bf16_t *)tn.B("xbt");
+            float *dctx = (float *)tn.B("dctx"), *dqkv = (float *)tn.B("dqkv"), *qkv = (float *)tn.B("qkv");
+            float *wparts = (float *)tn.B("wparts");
+            // dctx = dy·woᵀ, dwo = ctxᵀ·dy
+            k::cast_f32_bf16(s, dy, dyb, T * D);
+            gemm_nt(s, dyb, D, wo->b, D, (int)T, (int)QW, (int)D, dctx, QW, false);
+            k::transpose_bf16(s, dyb, D, nullptr, 1, (int)T, (int)D, dybt, T);
+            k::transpose_bf16(s, (bf16_t *)tn.B("ctx3"), 3 * QW, nullptr, 1, (int)T, (int)QW, ctxt, T);
+            gemm_nt(s, ctxt, T, dybt, T, (int)QW, (int)D, (int)T, wo->grad, D, false, wparts);
+            // The core's adjoint on the rotated q, k: dk, dv of a K/V head sum
+            // its query heads in head order; then dq, dk rotated back by −θ.
+            k::attention_core_bwd_gqa(s, qkv, LD, qkv + QW, qkv + QW + KW, LD, H / HKV, window,
+                                      (float *)tn.B("ctx"), dctx, QW, (float *)tn.B("lse"), dqkv, LD, dqkv + QW,
+                                      dqkv + QW + KW, LD, Bt, S, H, hd, true, (float *)tn.B("dscr"));
+            k::rope_apply(s, dqkv, LD, T, S, H + HKV, hd, (float *)tn.B("rope"), -1.0f);
+            // dx = dqkv·wqkvᵀ (dxq + dxk + dxv), dwqkv = xᵀ·dqkv
+            k::cast_f32_bf16(s, dqkv, dqkvb, T * LD);
+            if (dst(0))
+                gemm_nt(s, dqkvb, LD, wqkv->b, LD, (int)T, (int)D, (int)LD, dst(0), D, !tn.first_writer[0]);
+            k::transpose_bf16(s, dqkvb, LD, nullptr, 1, (int)T, (int)LD, dqkvt, T);
+            k::transpose_bf16(s, x3, 3 * D, nullptr, 1, (int)T, (int)D, xbt, T);  // hi part of x
+            gemm_nt(s, xbt, T, dqkvt, T, (int)D, (int)LD, (int)T, wqkv->grad, LD, false, wparts);
+            break;
+        }
         case CATNN_OP_MOE: {
             const int64_t E = nd.op.a[0], K = nd.op.a[1], H = xd.back(), T = nx / H;
             const int64_t I = tn.params["e0.w1"]->cols;
@@ -1039,13 +1549,18 @@ static void train_step(Tr &t) {
     // cotangent, and the refresh of their bf16 copies, in one launch.
     const k::UpdateRule rule = t.opt == CATNN_OPT_ADAM ? k::adam_rule(t.lr, ++t.adam_t) : k::sgd_rule(t.lr);
     k::sgd_multi(s, t.sgd_table, t.sgd_n, t.sgd_tiles, rule, true);
+    if (t.prec == CATNN_PREC_FP32) refresh_split_copies(t);
 }
 
-// adjoint_of over the graph with the output's cotangent already in place
-// (no loss, no update): forward for the tapes, then the reverse pass.
-static void adjoint_pass(Tr &t) {
+// adjoint_of over the graph (no loss, no update): the forward for the
+// tapes, then — once the caller has put the output's cotangent in place, at
+// the loss tick of the plan — the reverse pass.
+static void forward_pass(Tr &t) {
     for (auto &tn : t.nodes)
         if (!t.input_ids.count(tn.id)) forward_node(t, tn);
+}
+
+static void reverse_pass(Tr &t) {
     for (auto it = t.nodes.rbegin(); it != t.nodes.rend(); ++it)
         if (!t.input_ids.count(it->id) && t.has_grad.count(it->id) && !it->skip_bwd) backward_node(t, *it);
 }
@@ -1060,6 +1575,13 @@ static TParam *find_param(Tr &t, uint32_t node_id, const std::string &port, int6
         TParam *p = tn.params.at("wqkv");
         *col0 = port == "wq" ? 0 : port == "wk" ? p->rows : 2 * p->rows;
         *ncols = p->rows;
+        return p;
+    }
+    if (tn.kind == CATNN_OP_GQA_ATTENTION && (port == "wq" || port == "wk" || port == "wv")) {
+        TParam *p = tn.params.at("wqkv");
+        const int64_t QW = tn.node->op.a[0] * tn.node->op.a[2], KW = tn.node->op.a[1] * tn.node->op.a[2];
+        *col0 = port == "wq" ? 0 : port == "wk" ? QW : QW + KW;
+        *ncols = port == "wq" ? QW : KW;
         return p;
     }
     auto pit = tn.params.find(port);
@@ -1230,11 +1752,18 @@ int catnn_hip_train_install(catnn_hip_device *dev, const catnn_graph *g, float l
 
 int catnn_hip_train_install_opt(catnn_hip_device *dev, const catnn_graph *g, int32_t optimizer, float lr,
                                 catnn_hip_trainer **out) {
+    return catnn_hip_train_install_ex(dev, g, optimizer, lr, CATNN_PREC_BF16, out);
+}
+
+int catnn_hip_train_install_ex(catnn_hip_device *dev, const catnn_graph *g, int32_t optimizer, float lr,
+                               int32_t precision, catnn_hip_trainer **out) {
     return guard([&] {
         require_device(dev);
         CATNN_REQUIRE(g && out, CATNN_ERR_INVALID_ARGUMENT, "null argument");
         CATNN_REQUIRE(optimizer == CATNN_OPT_SGD || optimizer == CATNN_OPT_ADAM, CATNN_ERR_INVALID_ARGUMENT,
                       "unknown optimizer " + std::to_string(optimizer) + " (expected sgd or adam)");
+        CATNN_REQUIRE(precision == CATNN_PREC_BF16 || precision == CATNN_PREC_FP32, CATNN_ERR_INVALID_ARGUMENT,
+                      "unknown precision " + std::to_string(precision) + " (expected bf16 or fp32)");
         *out = nullptr;
         auto *t = new catnn_hip_trainer();
         try {
@@ -1242,6 +1771,7 @@ int catnn_hip_train_install_opt(catnn_hip_device *dev, const catnn_graph *g, int
             t->graph = *g;
             t->lr = lr;
             t->opt = optimizer;
+            t->prec = precision;
             plan_trainer(*t);
             reserve_and_upload(*t);
         } catch (...) {
@@ -1452,6 +1982,7 @@ int catnn_hip_run_adjoint(catnn_hip_device *dev, const catnn_node *node, const c
             fresh->dev = dev;
             fresh->graph = g;
             fresh->lr = 0.f;
+            fresh->prec = CATNN_PREC_FP32;  // adjoint_of is fp32 throughout (adjoint.rs:35-61)
             fresh->input_grads = true;
             plan_trainer(*fresh);
             reserve_and_upload(*fresh);
@@ -1471,10 +2002,12 @@ int catnn_hip_run_adjoint(catnn_hip_device *dev, const catnn_node *node, const c
         CATNN_REQUIRE(nd == numel(od) && (dy->data || nd == 0), CATNN_ERR_SHAPE_MISMATCH,
                       "dy has " + std::to_string(nd) + " values, " + t->graph.node(nid).name + " produces " +
                           dims_str(od));
-        if (nd) CATNN_HIP(hipMemcpyAsync(t->grad.at(nid), dy->data, (size_t)nd * 4, hipMemcpyHostToDevice, s));
         // note_kernel("{name}.bwd", dy.checksum()) of the training wave (coord.rs:412), stamped on the device.
         push_device_event(dev, span, CATNN_EV_KERNEL_START, 0);
-        adjoint_pass(*t);
+        forward_pass(*t);
+        // dy's buffer is planned from the loss tick on: forward-only scratch may share it.
+        if (nd) CATNN_HIP(hipMemcpyAsync(t->grad.at(nid), dy->data, (size_t)nd * 4, hipMemcpyHostToDevice, s));
+        reverse_pass(*t);
         push_device_event(dev, span, CATNN_EV_KERNEL_END, fnv1a_f32(dy->data, (uint64_t)nd));
         for (int32_t i = 0; i < n_inputs; ++i) {
             const std::vector<int64_t> &xd = t->dims.at((uint32_t)i);

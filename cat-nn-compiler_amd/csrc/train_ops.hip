@@ -242,6 +242,94 @@ __global__ __launch_bounds__(256) void transpose_split3_kernel(const float *__re
     }
 }
 
+// Six-part split for fp32-accurate products on the bf16 matrix cores:
+// v = h + m + l + O(2⁻²⁶|v|) with h = bf16(v), m = bf16(v − h),
+// l = bf16(v − h − m) (each difference exact in fp32).  Element k of a row
+// becomes six consecutive bf16 values, interleaved along K so that any K
+// range [k0, k1) of the original is the range [6k0, 6k1) of the split; the
+// A role lays them out (h, m, h, l, h, m), the B role (h, h, m, h, l, m), so
+// a GEMM over 6K sums hh + mh + hm + lh + hl + mm: every product term above
+// 2⁻²⁴ relative.
+__device__ __forceinline__ void split6_parts(float v, int role_b, bf16_t o[6]) {
+    const bf16_t h = f2bf(v);
+    const float r1 = v - __uint_as_float((uint32_t)h << 16);
+    const bf16_t m = f2bf(r1);
+    const bf16_t l = f2bf(r1 - __uint_as_float((uint32_t)m << 16));
+    if (role_b) {
+        o[0] = h; o[1] = h; o[2] = m; o[3] = h; o[4] = l; o[5] = m;
+    } else {
+        o[0] = h; o[1] = m; o[2] = h; o[3] = l; o[4] = h; o[5] = m;
+    }
+}
+
+__device__ __forceinline__ void store6(bf16_t *dst, const bf16_t o[6]) {
+    // dst is 4-byte aligned (6 bf16 per element, even element offsets).
+    uint32_t *d = reinterpret_cast<uint32_t *>(dst);
+    d[0] = (uint32_t)o[0] | ((uint32_t)o[1] << 16);
+    d[1] = (uint32_t)o[2] | ((uint32_t)o[3] << 16);
+    d[2] = (uint32_t)o[4] | ((uint32_t)o[5] << 16);
+}
+
+// out[r][6c .. 6c+5] = split6(x[r][c]).
+__global__ void split6_rows_kernel(const float *__restrict__ x, int64_t ldx, int64_t rows, int K, int role_b,
+                                   bf16_t *__restrict__ out, int64_t ldo) {
+    const int64_t n = rows * K;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+        const int64_t r = i / K;
+        const int c = (int)(i - r * K);
+        bf16_t o[6];
+        split6_parts(x[r * ldx + c], role_b, o);
+        store6(out + r * ldo + 6 * (int64_t)c, o);
+    }
+}
+
+// out[c][6r .. 6r+5] = split6(x[map(r)][c]) with map(r) = rows_map[r] / div
+// (negative: a zero row; no map: r): a 64×64 fp32 tile through LDS.
+__global__ __launch_bounds__(256) void split6_transpose_kernel(const float *__restrict__ x, int64_t ldx,
+                                                               const int32_t *__restrict__ rows_map, int div,
+                                                               int rows, int cols, int role_b,
+                                                               bf16_t *__restrict__ out, int64_t ldo) {
+    __shared__ float t[64][65];
+    const int r0 = blockIdx.y * 64, c0 = blockIdx.x * 64;
+    const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+    for (int i = ty; i < 64; i += 4) {
+        const int r = r0 + i, c = c0 + tx;
+        float v = 0.f;
+        if (r < rows && c < cols) {
+            const int sr = rows_map ? (rows_map[r] < 0 ? -1 : rows_map[r] / div) : r;
+            if (sr >= 0) v = x[(int64_t)sr * ldx + c];
+        }
+        t[i][tx] = v;
+    }
+    __syncthreads();
+    for (int i = ty; i < 64; i += 4) {
+        const int c = c0 + i, r = r0 + tx;
+        if (c < cols && r < rows) {
+            bf16_t o[6];
+            split6_parts(t[tx][i], role_b, o);
+            store6(out + (int64_t)c * ldo + 6 * (int64_t)r, o);
+        }
+    }
+}
+
+__global__ void scale_i32_kernel(const int32_t *__restrict__ src, int n, int factor, int32_t *__restrict__ dst) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) dst[i] = src[i] * factor;
+}
+
+__global__ void swiglu_dadc_f32_kernel(const float *__restrict__ dh, const float *__restrict__ a,
+                                       const float *__restrict__ c, float *__restrict__ da, float *__restrict__ dc,
+                                       int64_t n) {
+#pragma clang fp contract(off)
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+        const float z = a[i], sg = 1.0f / (1.0f + expf(-z));
+        da[i] = dh[i] * c[i] * (sg + z * sg * (1.0f - sg));
+        dc[i] = dh[i] * (z / (1.0f + expf(-z)));
+    }
+}
+
 // LayerNorm forward for training: y (fp32 and/or bf16), mean and rstd per
 // row.  One wavefront per row; any width.
 template <bool VEC>
@@ -983,10 +1071,14 @@ __global__ __launch_bounds__(256) void router_dgate_parts_kernel(const float *__
 
 // Per permuted position: dys[pos] = bf16(w[slot]·dout[tok]) and
 // dw[slot] = Σ_h y[pos][h]·dout[tok][h]; padding positions get zeros.
+__device__ __forceinline__ void put_out(bf16_t *p, float v) { *p = f2bf(v); }
+__device__ __forceinline__ void put_out(float *p, float v) { *p = v; }
+
+template <typename OUT>
 __global__ __launch_bounds__(256) void moe_slot_grad_kernel(
     const int32_t *__restrict__ slot_of_pos, const float *__restrict__ w,
     const float *__restrict__ y, const float *__restrict__ dout, int K, int H, int n_pos,
-    bf16_t *__restrict__ dys, float *__restrict__ dw) {
+    OUT *__restrict__ dys, float *__restrict__ dw) {
     __shared__ float ws[4];
     const int pos = blockIdx.x;
     if (pos >= n_pos) return;
@@ -1001,7 +1093,7 @@ __global__ __launch_bounds__(256) void moe_slot_grad_kernel(
     for (int h = threadIdx.x; h < H; h += 256) {
         const float g = dout[(int64_t)t * H + h];
         s += y[(int64_t)pos * H + h] * g;
-        dys[(int64_t)pos * H + h] = f2bf(wt * g);
+        put_out(&dys[(int64_t)pos * H + h], wt * g);
     }
     s = wave_sum(s);
     if ((threadIdx.x & 63) == 0) ws[threadIdx.x >> 6] = s;
@@ -1351,7 +1443,47 @@ uint64_t router_backward_scratch_bytes(int T, int H, int E) {
 void moe_slot_grads(hipStream_t s, const int32_t *slot_of_pos, const float *w, const float *y,
                     const float *dout, int K, int H, int n_pos, bf16_t *dys, float *dw) {
     if (n_pos <= 0) return;
-    moe_slot_grad_kernel<<<(unsigned)n_pos, 256, 0, s>>>(slot_of_pos, w, y, dout, K, H, n_pos, dys, dw);
+    moe_slot_grad_kernel<bf16_t><<<(unsigned)n_pos, 256, 0, s>>>(slot_of_pos, w, y, dout, K, H, n_pos, dys, dw);
+    CATNN_HIP(hipGetLastError());
+}
+
+void moe_slot_grads_f32(hipStream_t s, const int32_t *slot_of_pos, const float *w, const float *y,
+                        const float *dout, int K, int H, int n_pos, float *dys, float *dw) {
+    if (n_pos <= 0) return;
+    moe_slot_grad_kernel<float><<<(unsigned)n_pos, 256, 0, s>>>(slot_of_pos, w, y, dout, K, H, n_pos, dys, dw);
+    CATNN_HIP(hipGetLastError());
+}
+
+void split6_rows(hipStream_t s, const float *x, int64_t ldx, int64_t rows, int K, bool role_b, bf16_t *out,
+                 int64_t ldo) {
+    if (rows <= 0 || K <= 0) return;
+    CATNN_REQUIRE(ldo >= 6 * (int64_t)K && ldo % 2 == 0 && (reinterpret_cast<uintptr_t>(out) & 3) == 0,
+                  CATNN_ERR_SHAPE_MISMATCH, "split6: output rows");
+    split6_rows_kernel<<<blocks_for(rows * K, 256 * 4), 256, 0, s>>>(x, ldx, rows, K, role_b ? 1 : 0, out, ldo);
+    CATNN_HIP(hipGetLastError());
+}
+
+void split6_transpose(hipStream_t s, const float *x, int64_t ldx, const int32_t *rows_map, int div, int rows,
+                      int cols, bool role_b, bf16_t *out, int64_t ldo) {
+    if (rows <= 0 || cols <= 0) return;
+    CATNN_REQUIRE((rows + 63) / 64 < 65536, CATNN_ERR_SHAPE_MISMATCH, "split6 transpose: too many rows");
+    CATNN_REQUIRE(ldo >= 6 * (int64_t)rows && ldo % 2 == 0 && (reinterpret_cast<uintptr_t>(out) & 3) == 0,
+                  CATNN_ERR_SHAPE_MISMATCH, "split6 transpose: output rows");
+    split6_transpose_kernel<<<tgrid(rows, cols), 256, 0, s>>>(x, ldx, rows_map, div, rows, cols, role_b ? 1 : 0,
+                                                              out, ldo);
+    CATNN_HIP(hipGetLastError());
+}
+
+void scale_i32(hipStream_t s, const int32_t *src, int n, int factor, int32_t *dst) {
+    if (n <= 0) return;
+    scale_i32_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(src, n, factor, dst);
+    CATNN_HIP(hipGetLastError());
+}
+
+void swiglu_dadc_f32(hipStream_t s, const float *dh, const float *a, const float *c, float *da, float *dc,
+                     int64_t n) {
+    if (n <= 0) return;
+    swiglu_dadc_f32_kernel<<<blocks_for(n, 256 * 4), 256, 0, s>>>(dh, a, c, da, dc, n);
     CATNN_HIP(hipGetLastError());
 }
 

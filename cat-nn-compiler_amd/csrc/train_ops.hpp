@@ -117,6 +117,21 @@ void router_backward(hipStream_t s, const int32_t *idx, const float *w, const fl
                      float *scratch);
 void moe_slot_grads(hipStream_t s, const int32_t *slot_of_pos, const float *w, const float *y,
                     const float *dout, int K, int H, int n_pos, bf16_t *dys, float *dw);
+// fp32 slot cotangents (the fp32-precision trainer).
+void moe_slot_grads_f32(hipStream_t s, const int32_t *slot_of_pos, const float *w, const float *y,
+                        const float *dout, int K, int H, int n_pos, float *dys, float *dw);
+// Six-part split operands (fp32-accurate GEMMs on bf16 matrix cores): each
+// element of an fp32 matrix becomes six bf16 values interleaved along K,
+// laid out for the A or the B role.  split6_rows: out [rows, 6K];
+// split6_transpose: out[c] = the split of column c of x (rows gathered
+// through rows_map[r] / div, negative → zero), [cols, 6·rows].
+void split6_rows(hipStream_t s, const float *x, int64_t ldx, int64_t rows, int K, bool role_b, bf16_t *out,
+                 int64_t ldo);
+void split6_transpose(hipStream_t s, const float *x, int64_t ldx, const int32_t *rows_map, int div, int rows,
+                      int cols, bool role_b, bf16_t *out, int64_t ldo);
+void scale_i32(hipStream_t s, const int32_t *src, int n, int factor, int32_t *dst);
+void swiglu_dadc_f32(hipStream_t s, const float *dh, const float *a, const float *c, float *da, float *dc,
+                     int64_t n);
 void moe_dx(hipStream_t s, const float *dxs, const int32_t *pos_of_slot, const float *dl,
             const float *gate, int T, int K, int H, int E, float *dx, bool accumulate);
 
@@ -144,6 +159,26 @@ void attention_core_bwd(hipStream_t s, const float *q, const float *k, const flo
                         const float *o, const float *dout, int64_t ldo, const float *lse,
                         float *dq, float *dk, float *dv, int64_t ld_d, int64_t batch, int64_t seq,
                         int64_t n_heads, int64_t d_head, bool causal, float *scratch);
+// Grouped-query forms (GqaAttention, always causal in the forward; window >
+// 0: query i sees keys [i − window + 1, i]): q (and dq) rows of stride ldq
+// hold n_heads heads, k, v (and dk, dv) rows of stride ldk hold
+// n_heads / group heads; query head h reads K/V head h / group.  dk and dv
+// of a K/V head sum its group's query heads in head order.
+void attention_core_fwd_lse_gqa(hipStream_t s, const float *q, int64_t ldq, const float *k, const float *v,
+                                int64_t ldk, int64_t group, int64_t window, float *ctx, int64_t ldo, float *lse,
+                                int64_t batch, int64_t seq, int64_t n_heads, int64_t d_head);
+void attention_core_bwd_gqa(hipStream_t s, const float *q, int64_t ldq, const float *k, const float *v,
+                            int64_t ldk, int64_t group, int64_t window, const float *o, const float *dout,
+                            int64_t ldo, const float *lse, float *dq, int64_t ld_dq, float *dk, float *dv,
+                            int64_t ld_dkv, int64_t batch, int64_t seq, int64_t n_heads, int64_t d_head,
+                            bool causal, float *scratch);
+// RoPE on the first `heads` heads of width hd of each row of qk (row r is
+// position r mod S), in place: table [S, hd/2] of (cos, sin) from rope_table
+// (angles pos·θ^(−2i/hd) in f64, rounded to f32); sign −1 rotates by −angle,
+// the adjoint of the rotation (gqa_backward's apply_rope with −θ).
+void rope_table(hipStream_t s, float *tab, int64_t S, int64_t hd, double theta);
+void rope_apply(hipStream_t s, float *qk, int64_t ld, int64_t rows, int64_t S, int64_t heads, int64_t hd,
+                const float *tab, float sign);
 
 }  // namespace k
 }  // namespace catnn

@@ -318,7 +318,9 @@ int catnn_hip_run_kernel(catnn_hip_device *dev, const catnn_node *node,
  * and dims, rank and dtype are written.  The forward value is recomputed on
  * the device from `inputs` (as attention_backward recomputes its forward,
  * adjoint.rs:582-722), so `output` may be NULL and is not read.  Ops as the
- * training step executes them (bf16 MFMA GEMMs with fp32 accumulation);
+ * training step executes them at CATNN_PREC_FP32 (the reference's adjoints
+ * are fp32 throughout); the one-node plan of a node shape is built once per
+ * device and reused (up to 16 shapes, 16 GiB, least recently used first);
  * a Router → CATNN_ERR_UNLAWFUL (adjoint.rs:915-920); others →
  * CATNN_ERR_UNSUPPORTED; no inputs → CATNN_ERR_WIRING
  * (adjoint.rs:768-770). */
@@ -415,6 +417,17 @@ enum { CATNN_OPT_SGD = 0, CATNN_OPT_ADAM = 1 };
  * optimizer: CATNN_ERR_INVALID_ARGUMENT. */
 int catnn_hip_train_install_opt(catnn_hip_device *dev, const catnn_graph *g, int32_t optimizer,
                                 float lr, catnn_hip_trainer **out);
+/* GEMM precision of a trainer.  CATNN_PREC_BF16 (catnn_hip_train_install and
+ * _opt): bf16 MFMA operands with fp32 accumulation as described above — the
+ * mixed-precision training of the benchmark's bf16 configuration.
+ * CATNN_PREC_FP32: every GEMM of the step on six-part split operands (each
+ * fp32 value as three bf16 parts, the six product terms above 2⁻²⁴ summed
+ * by the bf16 matrix cores with fp32 accumulation), every tape and
+ * cotangent fp32: the fp32 algorithm of reference_train to fp32 rounding,
+ * for fp32 graphs.  Other values: CATNN_ERR_INVALID_ARGUMENT. */
+enum { CATNN_PREC_BF16 = 0, CATNN_PREC_FP32 = 1 };
+int catnn_hip_train_install_ex(catnn_hip_device *dev, const catnn_graph *g, int32_t optimizer,
+                               float lr, int32_t precision, catnn_hip_trainer **out);
 int catnn_hip_train_free(catnn_hip_trainer *t);
 /* Upload the batch: `input` is bound to every graph input, `target` is the
  * MSE target of the last output. */

@@ -549,15 +549,15 @@ static void apply_rope(float *q, int64_t head_dim, int64_t pos, double theta) {
 // moe::gqa, moe.rs:62-136: q/k/v projections (linear_seq), RoPE on q and k
 // at position t, per (b, h) causal softmax over keys [start, i] with
 // start = i − (window − 1) when a window is given (window ≤ 0: none), kv head
-// h / (n_heads / n_kv), then the output projection.  Returns 2 on a shape
-// mismatch.
+// h / (n_heads / n_kv), then the output projection; n_heads·head_dim need
+// not equal the model width.  Returns 2 on a shape mismatch.
 int orc_gqa(const float *x, const float *wq, const float *wk, const float *wv, const float *wo, int64_t B,
             int64_t S, int64_t D, int64_t n_heads, int64_t n_kv, int64_t head_dim, double theta,
             int64_t window, float *y) {
-    if (n_heads * head_dim != D || n_kv <= 0 || n_heads % n_kv != 0) return 2;
-    const int64_t T = B * S, KV = n_kv * head_dim;
-    std::vector<float> q((size_t)(T * D)), k((size_t)(T * KV)), v((size_t)(T * KV));
-    orc_matmul_seq(x, wq, q.data(), T, D, D);
+    if (n_kv <= 0 || n_heads <= 0 || n_heads % n_kv != 0) return 2;
+    const int64_t T = B * S, KV = n_kv * head_dim, QW = n_heads * head_dim;
+    std::vector<float> q((size_t)(T * QW)), k((size_t)(T * KV)), v((size_t)(T * KV));
+    orc_matmul_seq(x, wq, q.data(), T, D, QW);
     orc_matmul_seq(x, wk, k.data(), T, D, KV);
     orc_matmul_seq(x, wv, v.data(), T, D, KV);
     for (int64_t bi = 0; bi < B; ++bi)
@@ -569,7 +569,7 @@ int orc_gqa(const float *x, const float *wq, const float *wk, const float *wv, c
         }
     const int64_t repeats = std::max<int64_t>(n_heads / std::max<int64_t>(n_kv, 1), 1);
     const float scale = 1.0f / std::sqrt((float)head_dim);
-    std::vector<float> ctx((size_t)(T * D), 0.0f), scores((size_t)S);
+    std::vector<float> ctx((size_t)(T * QW), 0.0f), scores((size_t)S);
     for (int64_t bi = 0; bi < B; ++bi)
         for (int64_t h = 0; h < n_heads; ++h) {
             const int64_t kv_h = h / repeats;
@@ -598,7 +598,7 @@ int orc_gqa(const float *x, const float *wq, const float *wk, const float *wv, c
                 }
             }
         }
-    orc_matmul_seq(ctx.data(), wo, y, T, D, D);
+    orc_matmul_seq(ctx.data(), wo, y, T, QW, D);
     return 0;
 }
 
@@ -633,7 +633,7 @@ int orc_gqa_backward(const float *x, const float *wq, const float *wk, const flo
                      int64_t B, int64_t S, int64_t D, int64_t n_heads, int64_t n_kv, int64_t head_dim,
                      double theta, int64_t window, const float *dy, float *dx, float *dwq, float *dwk,
                      float *dwv, float *dwo) {
-    if (n_heads * head_dim != D || n_kv <= 0 || n_heads % n_kv != 0) return 2;
+    if (n_kv <= 0 || n_heads <= 0 || n_heads % n_kv != 0) return 2;
     const int64_t T = B * S, QW = n_heads * head_dim, KV = n_kv * head_dim;
     std::vector<float> q((size_t)(T * QW)), k((size_t)(T * KV)), v((size_t)(T * KV));
     orc_matmul_seq(x, wq, q.data(), T, D, QW);

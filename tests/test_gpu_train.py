@@ -83,12 +83,58 @@ def _check_step(device, g, x, tgt, lr=0.05, fp32_tol=BF16_TOL, tight=TIGHT):
     return tr
 
 
+def _check_step_fp32(device, g, x, tgt, tol=1e-4, classes=False):
+    """One step at fp32 precision against the fp32 reference step: the loss
+    to 1e-5, every gradient to `tol`, Sgd::put bit-exact on the device's
+    gradient."""
+    lr = 0.05
+    tr = Trainer(device, g, lr, precision="fp32")
+    if classes:
+        tr.set_batch_classes(x, tgt)
+    else:
+        tr.set_batch(x, tgt)
+    loss = tr.step()
+    loss_o, grads_o, _ = ot.train_step(g, x.numpy(), tgt if classes else tgt.numpy(), lr)
+    print(f"  loss gpu={loss:.7f} fp32-oracle={loss_o:.7f}")
+    assert abs(loss - loss_o) <= 1e-5 * max(1.0, abs(loss_o))
+    worst = 0.0
+    for nid, dp in grads_o.items():
+        for port, go in dp.items():
+            shape = _shape(g, nid, port)
+            gg = tr.grad(nid, port, shape)
+            e = rel_l2(gg, go.reshape(shape))
+            worst = max(worst, e)
+            assert e < tol, (g.nodes[nid].name, port, e)
+            p0 = g.nodes[nid].params[port].numpy().reshape(shape)
+            assert np.array_equal(tr.param(nid, port, shape), p0 - np.float32(lr) * gg), (g.nodes[nid].name, port)
+    print(f"  worst gradient rel_l2 {worst:.2e}")
+    return tr
+
+
 def test_mlp_relu_unaligned_k(device):
-    # K = 784 and N = 10: the bf16 GEMM's element-load edges.  fc1's weight
-    # gradient comes through three plain-bf16 backward GEMMs and two ReLU
-    # masks: the bf16-rounding model itself sits 1.1e-2 from the fp32 step.
+    # Config 1 is an fp32 graph: its step at fp32 precision (K = 784 and
+    # N = 10 are the GEMM's element-load edges) holds every gradient to the
+    # fp32 bar.
     w = configs.config1(batch=64)
-    _check_step(device, w.graph, w.x, _target([64, 10], 11), fp32_tol=2e-2)
+    _check_step_fp32(device, w.graph, w.x, _target([64, 10], 11)).free()
+
+
+@pytest.mark.parametrize("which", ["block_mfma", "block_generic", "moe", "block_moe", "block_moe_ragged"])
+def test_fp32_precision_step(device, which):
+    # Every op with GEMMs at fp32 precision: six-part split operands against
+    # the fp32 reference step at 1e-4.
+    if which == "block_mfma":
+        w = configs.config3(batch=2, seq=128, d=128, heads=2, ffn=256, causal=True)
+    elif which == "block_generic":
+        w = configs.config3(batch=1, seq=77, d=64, heads=2, ffn=96, causal=False)
+    elif which == "moe":
+        w = configs.config4(batch=2, seq=64, d=128, n_experts=4, top_k=2, inter=96)
+    elif which == "block_moe":
+        w = configs.config5(batch=2, seq=128, d=128, heads=2, ffn=256, n_experts=4, top_k=2, inter=128)
+    else:
+        w = configs.config5(batch=1, seq=77, d=128, heads=2, ffn=256, n_experts=4, top_k=2, inter=96)
+    tgt = w.target if hasattr(w, "target") else _target(w.x.ty.shape, 21)
+    _check_step_fp32(device, w.graph, w.x, tgt).free()
 
 
 @pytest.mark.parametrize("causal", [True, False])
@@ -189,13 +235,11 @@ def test_reset_restores_parameters_and_steps_repeat_bit_exactly(device):
 
 
 def test_training_error_kinds(device):
-    ty = TensorType.f32([1, 4, 8])
-    g = IrGraph("gqa")
+    ty = TensorType.f32([2, 8])
+    g = IrGraph("mla")
     g.add_node(IrNode(0, "in", OpenOp.identity(), ty))
-    ones = lambda *s: Tensor(TensorType.f32(list(s)), np.ones(s, np.float32))
-    # GQA attention has no device adjoint yet
-    g.add_node(IrNode(1, "gqa", OpenOp.gqa_attention(2, 1, 4, 8, 8, 10000), ty,
-                      {"wq": ones(8, 8), "wk": ones(8, 4), "wv": ones(8, 4), "wo": ones(8, 8)}))
+    # MLA (DeepSeek's attention) is not executable on this backend
+    g.add_node(IrNode(1, "mla", OpenOp("mla", (2, 4, 4, 4, 4, 4, 10000)), ty))
     g.add_edge(0, 1)
     g.inputs.append(0)
     g.outputs.append(1)
