@@ -277,6 +277,87 @@ def lm_head(x, w):
     return y
 
 
+# ---- Mixtral-tiny (crates/catnn-compile/src/kernel/moe.rs:227-322, :418-455) ----
+
+class MixtralConfig:
+    """MixtralConfig::tiny (crates/catnn-core/src/spec/mixtral.rs:107-130):
+    the fields moe::forward reads."""
+
+    def __init__(self, vocab=32, hidden=32, inter=64, layers=2, heads=4, kv_heads=2, experts=4, top_k=2,
+                 eps=1e-5, rope_theta=10000.0, sliding_window=8):
+        self.vocab, self.hidden, self.inter, self.layers = vocab, hidden, inter, layers
+        self.heads, self.kv_heads, self.experts, self.top_k = heads, kv_heads, experts, top_k
+        self.eps, self.rope_theta, self.sliding_window = eps, rope_theta, sliding_window
+
+    def head_dim(self):
+        """MixtralConfig::head_dim, mixtral.rs:132-140."""
+        if self.heads == 0 or self.hidden % self.heads:
+            raise ValueError("hidden not divisible by heads")
+        return self.hidden // self.heads
+
+
+_U64 = (1 << 64) - 1
+
+
+def mixtral_weights_seeded(cfg, seed):
+    """MixtralWeights::seeded, moe.rs:246-285: one Tensor::lcg per weight,
+    its seed the next state of s ← s·6364136223846793005 + 1 (wrapping)
+    from s = seed, drawn in the reference's order (embed; per layer the
+    experts' (w1, w3, w2), then wq, wk, wv, wo, gate; lm_head last); RMSNorm
+    weights are ones."""
+    h, mid, hd = cfg.hidden, cfg.inter, cfg.head_dim()
+    kv = cfg.kv_heads * hd
+    state = [seed & _U64]
+
+    def nxt():
+        state[0] = (state[0] * 6364136223846793005 + 1) & _U64
+        return state[0]
+
+    def draw(rows, cols):
+        return lcg(rows * cols, nxt()).reshape(rows, cols)
+
+    w = {"embed": draw(cfg.vocab, h), "layers": []}
+    for _ in range(cfg.layers):
+        experts = [(draw(h, mid), draw(h, mid), draw(mid, h)) for _ in range(cfg.experts)]
+        layer = {"rms_attn": np.ones(h, np.float32), "wq": draw(h, h), "wk": draw(h, kv), "wv": draw(h, kv),
+                 "wo": draw(h, h), "rms_moe": np.ones(h, np.float32), "gate": draw(h, cfg.experts),
+                 "experts": experts}
+        w["layers"].append(layer)
+    w["final_norm"] = np.ones(h, np.float32)
+    w["lm_head"] = draw(cfg.vocab, h)
+    return w
+
+
+def _mixtral(cfg, w, tokens, batch, seq, reference):
+    if len(tokens) != batch * seq:
+        raise ValueError("token batch*seq")
+    h = cfg.hidden
+    x = embedding(np.asarray(tokens, np.float32).reshape(batch, seq), w["embed"])
+    for layer in w["layers"]:
+        xn = rmsnorm(x, layer["rms_attn"], cfg.eps)
+        attn = gqa(xn, layer["wq"], layer["wk"], layer["wv"], layer["wo"], cfg.heads, cfg.kv_heads,
+                   cfg.head_dim(), cfg.rope_theta, cfg.sliding_window)
+        x = add(x, attn)  # cpu::add (forward, moe.rs:309); x[i] += attn[i] (reference, :437-439)
+        xn = rmsnorm(x, layer["rms_moe"], cfg.eps)
+        w1, w3, w2 = (np.stack([e[i] for e in layer["experts"]]) for i in range(3))
+        m = moe(xn.reshape(-1, h), layer["gate"], w1, w3, w2, cfg.top_k, reference=reference).reshape(x.shape)
+        x = add(x, m)
+    x = rmsnorm(x, w["final_norm"], cfg.eps)
+    return lm_head(x, w["lm_head"])
+
+
+def mixtral_forward(cfg, w, tokens, batch, seq):
+    """moe::forward, moe.rs:288-322: embed → per layer x += gqa(rmsnorm(x)),
+    x += moe(rmsnorm(x)) → rmsnorm → lm_head."""
+    return _mixtral(cfg, w, tokens, batch, seq, reference=False)
+
+
+def mixtral_forward_reference(cfg, w, tokens, batch, seq):
+    """moe::reference::forward, moe.rs:418-455: the same chain with the
+    naïve reference MoE (moe.rs:383-416)."""
+    return _mixtral(cfg, w, tokens, batch, seq, reference=True)
+
+
 def mix(a, b, gate):
     """deepseek::mix, deepseek.rs:229-239."""
     a, b = _c(a), _c(b)

@@ -226,3 +226,63 @@ def test_residual_folds_into_gqa_and_swiglu(device):
     g.inputs.append(0)
     g.outputs.append(6)
     _check_graph(device, g, _t(r.standard_normal((2, S, d))))
+
+
+def _mixtral_reference_graph(cfg, w, B, S):
+    """moe::forward (moe.rs:288-322) as an IrGraph: embed → per layer
+    rms_attn → gqa → ResidualAdd(x, ·) → rms_moe → moe → ResidualAdd(x, ·) →
+    final_norm → lm_head, holding MixtralWeights::seeded's tensors."""
+    h, hd = cfg.hidden, cfg.head_dim()
+    eps_e6 = int(np.float32(cfg.eps) * np.float32(1e6))
+    ty = TensorType.f32([B, S, h])
+    g = IrGraph("mixtral_tiny_reference")
+    g.add_node(IrNode(0, "tokens", OpenOp.identity(), TensorType.f32([B, S])))
+    g.add_node(IrNode(1, "embed", OpenOp.embedding(cfg.vocab, h), ty, {"w": _t(w["embed"])}))
+    g.add_edge(0, 1)
+    x, nid = 1, 2
+    for li, L in enumerate(w["layers"]):
+        g.add_node(IrNode(nid, f"L{li}.rms_attn", OpenOp.rms_norm(eps_e6), ty, {"w": _t(L["rms_attn"])}))
+        g.add_node(IrNode(nid + 1, f"L{li}.gqa",
+                          OpenOp.gqa_attention(cfg.heads, cfg.kv_heads, hd, h, cfg.sliding_window,
+                                               int(cfg.rope_theta)), ty,
+                          {p: _t(L[p]) for p in ("wq", "wk", "wv", "wo")}))
+        g.add_node(IrNode(nid + 2, f"L{li}.res_attn", OpenOp.residual_add(), ty))
+        moe_p = {"gate": _t(L["gate"])}
+        for e, (w1, w3, w2) in enumerate(L["experts"]):
+            moe_p.update({f"e{e}.w1": _t(w1), f"e{e}.w3": _t(w3), f"e{e}.w2": _t(w2)})
+        g.add_node(IrNode(nid + 3, f"L{li}.rms_moe", OpenOp.rms_norm(eps_e6), ty, {"w": _t(L["rms_moe"])}))
+        g.add_node(IrNode(nid + 4, f"L{li}.moe", OpenOp.moe(cfg.experts, cfg.top_k, h, cfg.inter), ty, moe_p))
+        g.add_node(IrNode(nid + 5, f"L{li}.res_moe", OpenOp.residual_add(), ty))
+        for a, b in ((x, nid), (nid, nid + 1), (x, nid + 2), (nid + 1, nid + 2), (nid + 2, nid + 3),
+                     (nid + 3, nid + 4), (nid + 2, nid + 5), (nid + 4, nid + 5)):
+            g.add_edge(a, b)
+        x, nid = nid + 5, nid + 6
+    g.add_node(IrNode(nid, "final_norm", OpenOp.rms_norm(eps_e6), ty, {"w": _t(w["final_norm"])}))
+    g.add_node(IrNode(nid + 1, "lm_head", OpenOp.lm_head(h, cfg.vocab), TensorType.f32([B, S, cfg.vocab]),
+                      {"w": _t(w["lm_head"])}))
+    g.add_edge(x, nid)
+    g.add_edge(nid, nid + 1)
+    g.inputs, g.outputs = [0], [nid + 1]
+    return g
+
+
+@pytest.mark.parametrize("seed", [7, 123])
+def test_mixtral_tiny_known_answer(device, seed):
+    # The reference's Mixtral-tiny test (moe.rs:476-485): MixtralConfig::tiny,
+    # MixtralWeights::seeded(seed), tokens 1..8 as batch 2 × seq 4.  The same
+    # weights and tokens run as an IrGraph with ResidualAdd nodes on the GPU
+    # and are held to the reference's own bound against moe::forward (max |Δ|
+    # < 2e-4) and to the fp32 bar (rel L2 1e-4).
+    cfg = oracle.MixtralConfig()
+    w = oracle.mixtral_weights_seeded(cfg, seed)
+    toks = [1, 2, 3, 4, 5, 6, 7, 8]
+    want = oracle.mixtral_forward(cfg, w, toks, 2, 4)
+    g = _mixtral_reference_graph(cfg, w, 2, 4)
+    prog = Program(device, g)
+    got = prog.forward(Tensor(TensorType.f32([2, 4]), np.asarray(toks, np.float32))).numpy()
+    prog.free()
+    err, mx = rel_l2(got, want), float(np.abs(got - want).max())
+    print(f"mixtral-tiny seed {seed}: rel_l2 {err:.2e}, max |Δ| {mx:.2e}", flush=True)
+    assert got.shape == (2, 4, cfg.vocab)
+    assert mx < 2e-4 and err < TOL
+    assert rel_l2(got, oracle.eval_graph(g, np.asarray(toks, np.float32).reshape(2, 4))) < TOL

@@ -104,3 +104,98 @@ def test_lm_head_and_mix():
     assert np.allclose(oracle.mix(a, b, 0.0), 0.5 * a + 0.5 * b, rtol=1e-6)
     s = 1 / (1 + np.exp(-1.5))
     assert np.allclose(oracle.mix(a, b, 1.5), s * a + (1 - s) * b, rtol=1e-6)
+
+
+# ---- Mixtral-tiny known answer (moe.rs:246-322, :418-455, test at :473-485) ----
+
+def test_mixtral_tiny_forward_matches_reference_forward():
+    # The reference's own test (moe.rs:476-485): MixtralConfig::tiny, seeded
+    # weights (seed 7), tokens 1..8 as batch 2 × seq 4: moe::forward against
+    # moe::reference::forward, max |Δ| < 2e-4.
+    cfg = oracle.MixtralConfig()
+    w = oracle.mixtral_weights_seeded(cfg, 7)
+    toks = [1, 2, 3, 4, 5, 6, 7, 8]
+    a = oracle.mixtral_forward(cfg, w, toks, 2, 4)
+    b = oracle.mixtral_forward_reference(cfg, w, toks, 2, 4)
+    assert a.shape == (2, 4, 32)
+    assert float(np.abs(a - b).max()) < 2e-4
+    with pytest.raises(ValueError):
+        oracle.mixtral_forward(cfg, w, toks[:7], 2, 4)
+
+
+def test_mixtral_seeded_weights_follow_the_seed_chain():
+    # The seed of the k-th tensor is the k-th state of s ← s·6364136223846793005
+    # + 1 (mod 2^64) from s = 7, checked in Python integers together with
+    # Tensor::lcg's own formula (tensor.rs:259-268); the draw order is
+    # embed, then per layer 4 experts × (w1, w3, w2) and wq, wk, wv, wo, gate,
+    # then lm_head: 1 + 2·17 + 1 = 36 tensors.
+    cfg = oracle.MixtralConfig()
+    w = oracle.mixtral_weights_seeded(cfg, 7)
+    seeds, s = [], 7
+    for _ in range(36):
+        s = (s * 6364136223846793005 + 1) % 2**64
+        seeds.append(s)
+
+    def lcg_py(n, seed):
+        st, out = max(seed, 1), []
+        for _ in range(n):
+            st = (st * 6364136223846793005 + 1) % 2**64
+            out.append(np.float32(np.float32((st >> 33) & 0xFFFFFFFF) / np.float32(2**32 - 1)) * np.float32(2)
+                       - np.float32(1))
+        return np.array(out, np.float32)
+
+    assert np.array_equal(w["embed"].reshape(-1)[:50], lcg_py(50, seeds[0]))
+    l0 = w["layers"][0]
+    assert np.array_equal(l0["experts"][0][0].reshape(-1)[:20], lcg_py(20, seeds[1]))
+    assert np.array_equal(l0["experts"][3][2].reshape(-1)[:20], lcg_py(20, seeds[12]))
+    assert np.array_equal(l0["wq"].reshape(-1)[:20], lcg_py(20, seeds[13]))
+    assert np.array_equal(l0["gate"].reshape(-1)[:20], lcg_py(20, seeds[17]))
+    assert np.array_equal(w["layers"][1]["wq"].reshape(-1)[:20], lcg_py(20, seeds[30]))
+    assert np.array_equal(w["lm_head"].reshape(-1)[:20], lcg_py(20, seeds[35]))
+    assert l0["wk"].shape == (32, 16) and l0["experts"][0][2].shape == (64, 32)
+    assert np.all(l0["rms_attn"] == 1) and np.all(w["final_norm"] == 1)
+
+
+def _mixtral64(cfg, w, tokens, B, S):
+    """The same forward in float64 from textbook pieces: a table lookup, RMS
+    normalisation, _gqa64 (complex-rotation RoPE, repeated K/V heads,
+    explicit window), a dense top-k-masked softmax MoE with SiLU experts,
+    and x·Wᵀ for the head."""
+    f = lambda a: np.asarray(a, np.float64)
+    x = f(w["embed"])[np.asarray(tokens).reshape(B, S)]
+
+    def rms(v, g):
+        return v / np.sqrt((v * v).mean(-1, keepdims=True) + cfg.eps) * f(g)
+
+    for L in w["layers"]:
+        xn = rms(x, L["rms_attn"])
+        x = x + _gqa64(xn, L["wq"], L["wk"], L["wv"], L["wo"], cfg.heads, cfg.kv_heads, cfg.head_dim(),
+                       cfg.rope_theta, cfg.sliding_window)
+        xn = rms(x, L["rms_moe"]).reshape(-1, cfg.hidden)
+        logits = xn @ f(L["gate"])
+        top = np.argsort(-logits, axis=1, kind="stable")[:, :cfg.top_k]
+        sel = np.take_along_axis(logits, top, 1)
+        wts = np.exp(sel - sel.max(1, keepdims=True))
+        wts /= wts.sum(1, keepdims=True)
+        m = np.zeros_like(xn)
+        for t in range(xn.shape[0]):
+            for j in range(cfg.top_k):
+                w1, w3, w2 = (f(a) for a in L["experts"][top[t, j]])
+                a, c = xn[t] @ w1, xn[t] @ w3
+                m[t] += wts[t, j] * ((a / (1 + np.exp(-a)) * c) @ w2)
+        x = x + m.reshape(x.shape)
+    x = rms(x, w["final_norm"])
+    return x @ f(w["lm_head"]).T
+
+
+@pytest.mark.parametrize("seed", [7, 123])
+def test_mixtral_tiny_forward_matches_float64(seed):
+    cfg = oracle.MixtralConfig()
+    w = oracle.mixtral_weights_seeded(cfg, seed)
+    toks = [1, 2, 3, 4, 5, 6, 7, 8]
+    got = oracle.mixtral_forward(cfg, w, toks, 2, 4)
+    want = _mixtral64(cfg, w, toks, 2, 4)
+    assert rel_l2(got, want) < 1e-5
+    # the decoder layers matter: embedding → norm → head alone is far off
+    cfg_chain = oracle.MixtralConfig(layers=0)
+    assert rel_l2(got, _mixtral64(cfg_chain, {**w, "layers": []}, toks, 2, 4)) > 1e-2
