@@ -12,13 +12,15 @@ from .ir import (FLAG_CAUSAL, FusionGroup, IrEdge, IrGraph, IrNode, OpenOp, Tens
 from .train import Trainer
 from .irjson import CGraph, to_serde_json
 from .describe import KernelLaunch, KernelResource, describe, kernel_table
+from .placement import ClusterDevice, PlacedProgram, Placement, device_memory, kernels_for
 from .spec import (Architecture, NetworkSpec, lower_architecture, mlp_spec, parse_catnn,
                    propose_fusions, to_architecture, transformer_block_spec)
 
 __all__ = [
-    "ArenaAlloc", "Architecture", "BufferReq", "CGraph", "CatError", "Device", "DeviceBuffer",
+    "ArenaAlloc", "Architecture", "BufferReq", "CGraph", "CatError", "ClusterDevice", "Device", "DeviceBuffer",
     "DeviceHandler", "FLAG_CAUSAL", "FusionGroup", "IrEdge", "IrGraph", "IrNode", "LIB_PATH",
-    "NetworkSpec", "OpenOp", "Program", "STATUS_NAMES", "Tensor", "TensorType", "Trainer",
+    "NetworkSpec", "OpenOp", "PlacedProgram", "Placement", "Program", "STATUS_NAMES", "Tensor", "TensorType",
+    "Trainer", "device_memory", "kernels_for",
     "arena_conflict", "eval_graph_hip", "lib", "lower_architecture", "mlp_spec", "parse_catnn",
     "place_arena", "propose_fusions", "to_architecture", "to_serde_json", "transformer_block_spec",
 ]

@@ -74,6 +74,27 @@ class CStepTiming(ctypes.Structure):
                 ("calls", ctypes.c_int32), ("total_ms", ctypes.c_double)]
 
 
+class CPlacementEntry(ctypes.Structure):
+    _fields_ = [("op", ctypes.c_char_p), ("device", ctypes.c_char_p)]
+
+
+class CClusterDevice(ctypes.Structure):
+    _fields_ = [("id", ctypes.c_char_p), ("kind", ctypes.c_int32), ("arch", ctypes.c_char_p)]
+
+
+class CKernelChoice(ctypes.Structure):
+    _fields_ = [("op", ctypes.c_char * ID_CAP), ("backend", ctypes.c_int32)]
+
+
+class CMemoryRegion(ctypes.Structure):
+    _fields_ = [("bytes", ctypes.c_uint64), ("bandwidth_bps", ctypes.c_double), ("latency_s", ctypes.c_double),
+                ("provenance", ctypes.c_char * 256)]
+
+
+class CDeviceMemory(ctypes.Structure):
+    _fields_ = [("code", CMemoryRegion), ("buffer", CMemoryRegion), ("scratch", CMemoryRegion)]
+
+
 class CEvent(ctypes.Structure):
     _fields_ = [("t_ns", ctypes.c_uint64), ("op", ctypes.c_char * ID_CAP),
                 ("kind", ctypes.c_int32), ("checksum", ctypes.c_uint64)]
@@ -175,6 +196,16 @@ SIGNATURES = {
     "catnn_hip_events": [_VP, ctypes.POINTER(CEvent), _I32, _PI32],
     "catnn_hip_clear_events": [_VP],
     "catnn_hip_trace_checksums": [_VP, _I32],
+    "catnn_hip_kernels_for": [_VP, ctypes.POINTER(CPlacementEntry), _I32, ctypes.POINTER(CClusterDevice), _I32,
+                              ctypes.POINTER(CKernelChoice), _I32, _PI32],
+    "catnn_hip_device_memory": [_VP, ctypes.POINTER(CDeviceMemory)],
+    "catnn_hip_install_placed": [_VP, _VP, ctypes.POINTER(CPlacementEntry), _I32, ctypes.c_char_p, ctypes.c_char_p,
+                                 ctypes.POINTER(_VP)],
+    "catnn_hip_program_ports": [_VP, _VP, _I32, _PI32, _VP, _I32, _PI32],
+    "catnn_hip_program_new_pass": [_VP],
+    "catnn_hip_program_set_value": [_VP, ctypes.c_char_p, ctypes.POINTER(CTensor)],
+    "catnn_hip_forward_wave": [_VP, _PI32],
+    "catnn_hip_program_get_value": [_VP, ctypes.c_char_p, ctypes.POINTER(CTensor)],
     "catnn_hip_linear_f32": [_VP, _VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _I32],
     "catnn_hip_gemm_bf16_nt": [_VP, _VP, _I64, _VP, _I64, _VP, _I64, _I64, _I64, _I64, _I32, _I32],
     "catnn_hip_act_f32": [_VP, _VP, _VP, _I64, _I32],

@@ -551,6 +551,13 @@ struct catnn_hip_program {
     std::vector<std::vector<hipEvent_t>> event_pool;
     std::vector<double> total_ms;
     std::vector<int32_t> calls;
+    // A device's stage of a placed graph (catnn_hip_install_placed): values
+    // that arrive from elsewhere ("in") or leave ("out"), by name, and the
+    // wave state of the current forward pass (coord.rs:592-686).
+    bool placed = false;
+    std::map<std::string, uint32_t> port_in, port_out;
+    std::set<uint32_t> have;       // values present on the device this pass
+    std::vector<char> step_done;   // per step, this pass
 };
 
 namespace catnn {
@@ -699,6 +706,11 @@ static void plan_and_upload(catnn_hip_program &p) {
     }
     for (uint32_t o : g.outputs)
         if (p.dims.count(o)) last[o] = n_ticks;
+    if (p.placed)  // steps run in waves as remote values arrive, not in tick order: no aliasing
+        for (auto &kv : first) {
+            kv.second = 0;
+            last[kv.first] = n_ticks;
+        }
     for (const auto &kv : first) {
         const uint64_t bytes = (uint64_t)numel_of(p.dims[kv.first]) * 4;
         reqs.push_back(BufferReq{act_id(kv.first), bytes, kv.second, last[kv.first], false});
@@ -747,6 +759,27 @@ static void plan_and_upload(catnn_hip_program &p) {
     CATNN_HIP(hipStreamSynchronize(dev->stream));
 }
 
+static void exec_step(catnn_hip_program &p, const Step &st) {
+    const catnn_graph &g = p.graph;
+    const Node &n = g.node(st.node);
+    ExecArgs a;
+    for (uint32_t v : st.ins) a.inputs.push_back(p.ptr.at(act_id(v)));
+    a.in_dims = st.in_dims;
+    a.param = [&](const std::string &port) -> const float * {
+        auto it = p.ptr.find(param_id(n, port));
+        return it == p.ptr.end() ? nullptr : it->second;
+    };
+    a.out = p.ptr.at(act_id(st.out));
+    a.fused_act = st.fused_act;
+    a.residual = st.residual >= 0 ? p.ptr.at(act_id((uint32_t)st.residual)) : nullptr;
+    if (st.scratch) {
+        a.scratch = p.ptr.at(scratch_id(n));
+        a.scratch_bytes = st.scratch;
+    }
+    if (derived_floats(n)) a.derived = p.ptr.at(derived_id(n));
+    exec_node(p.dev, n, a);
+}
+
 static void run_program(catnn_hip_program &p) {
     const catnn_graph &g = p.graph;
     std::vector<hipEvent_t> *evs = nullptr;
@@ -766,26 +799,30 @@ static void run_program(catnn_hip_program &p) {
     size_t executed = 0;
     for (const Step &st : p.steps) {
         if (st.is_input) continue;
-        const Node &n = g.node(st.node);
-        ExecArgs a;
-        for (uint32_t v : st.ins) a.inputs.push_back(p.ptr.at(act_id(v)));
-        a.in_dims = st.in_dims;
-        a.param = [&](const std::string &port) -> const float * {
-            auto it = p.ptr.find(param_id(n, port));
-            return it == p.ptr.end() ? nullptr : it->second;
-        };
-        a.out = p.ptr.at(act_id(st.out));
-        a.fused_act = st.fused_act;
-        a.residual = st.residual >= 0 ? p.ptr.at(act_id((uint32_t)st.residual)) : nullptr;
-        if (st.scratch) {
-            a.scratch = p.ptr.at(scratch_id(n));
-            a.scratch_bytes = st.scratch;
-        }
-        if (derived_floats(n)) a.derived = p.ptr.at(derived_id(n));
-        exec_node(p.dev, n, a);
+        exec_step(p, st);
         ++executed;
         if (evs) CATNN_HIP(hipEventRecord((*evs)[executed], p.dev->stream));
     }
+}
+
+// One forward wave of a placed stage (forward_device, coord.rs:622-676):
+// every step not yet run this pass whose inputs are all present runs, in
+// topo order; its output becomes present.  Returns the steps fired.
+static int forward_wave(catnn_hip_program &p) {
+    int fired = 0;
+    for (size_t i = 0; i < p.steps.size(); ++i) {
+        const Step &st = p.steps[i];
+        if (st.is_input || p.step_done[i]) continue;
+        bool ready = true;
+        for (uint32_t v : st.ins) ready = ready && p.have.count(v);
+        if (st.residual >= 0) ready = ready && p.have.count((uint32_t)st.residual);
+        if (!ready) continue;
+        exec_step(p, st);
+        p.step_done[i] = 1;
+        p.have.insert(st.out);
+        ++fired;
+    }
+    return fired;
 }
 
 static void collect_timings(catnn_hip_program &p) {
@@ -808,6 +845,82 @@ static void destroy_events(catnn_hip_program &p) {
             for (hipEvent_t e : set) (void)hipEventDestroy(e);
     p.pending.clear();
     p.event_pool.clear();
+}
+
+// The stage of `g` that Placement puts on `device` (placement.get(name)
+// .unwrap_or(default_device), as forward_device reads it, coord.rs:629):
+// its nodes keep their ids; a value produced elsewhere and read here enters
+// as an input node "{producer}#recv" (the buffer schedule_device names
+// act:{producer}#recv, pipeline.rs:319-327); a local value read elsewhere,
+// or a graph output placed here, is an output of the stage.
+static catnn_graph stage_of(const catnn_graph &g, const std::map<std::string, std::string> &assign,
+                            const std::string &device, const std::string &default_device,
+                            std::map<std::string, uint32_t> &port_in, std::map<std::string, uint32_t> &port_out) {
+    auto home = [&](const Node &n) {
+        auto it = assign.find(n.name);
+        return it == assign.end() ? default_device : it->second;
+    };
+    catnn_graph st;
+    st.name = g.name + "@" + device;
+    st.fusions = g.fusions;
+    uint32_t next_id = 0;
+    for (const auto &kv : g.nodes) next_id = std::max(next_id, kv.first + 1);
+    std::map<uint32_t, uint32_t> recv_of;  // remote producer id → recv node id
+    const std::set<uint32_t> inputs(g.inputs.begin(), g.inputs.end());
+    for (uint32_t id : g.node_order) {
+        const Node &n = g.node(id);
+        if (home(n) != device) continue;
+        st.node_order.push_back(id);
+        st.nodes[id] = n;
+        if (inputs.count(id)) {
+            st.inputs.push_back(id);
+            port_in[n.name] = id;
+        }
+    }
+    CATNN_REQUIRE(!st.nodes.empty(), CATNN_ERR_UNKNOWN_REALIZATION,
+                  "no node of graph " + g.name + " is placed on device " + device);
+    for (const Edge &e : g.edges) {
+        if (!st.nodes.count(e.dst)) continue;
+        if (st.nodes.count(e.src)) {
+            st.edges.push_back(e);
+            continue;
+        }
+        auto it = recv_of.find(e.src);
+        if (it == recv_of.end()) {
+            const Node &src = g.node(e.src);
+            Node r;
+            r.id = next_id++;
+            r.name = src.name + "#recv";
+            std::memset(&r.op, 0, sizeof(r.op));
+            r.op.kind = CATNN_OP_IDENTITY;
+            r.output_ty = src.output_ty;
+            CATNN_REQUIRE(!r.output_ty.dims.empty(), CATNN_ERR_SHAPE_MISMATCH,
+                          "node " + src.name + " has no declared output type to receive");
+            st.nodes[r.id] = r;
+            st.node_order.push_back(r.id);
+            st.inputs.push_back(r.id);
+            port_in[r.name] = r.id;
+            it = recv_of.emplace(e.src, r.id).first;
+        }
+        Edge re = e;
+        re.src = it->second;
+        st.edges.push_back(re);
+    }
+    std::set<uint32_t> outs;
+    for (const Edge &e : g.edges)
+        if (st.nodes.count(e.src) && !st.nodes.count(e.dst) && !recv_of.count(e.src)) outs.insert(e.src);
+    for (uint32_t o : g.outputs)
+        if (st.nodes.count(o)) outs.insert(o);
+    for (uint32_t id : st.node_order)
+        if (outs.count(id)) {
+            st.outputs.push_back(id);
+            port_out[st.nodes.at(id).name] = id;
+        }
+    if (st.outputs.empty()) {  // a stage whose values all stay local: its last node
+        st.outputs.push_back(st.topo().back());
+        port_out[st.nodes.at(st.outputs.back()).name] = st.outputs.back();
+    }
+    return st;
 }
 
 }  // namespace catnn
@@ -1018,6 +1131,132 @@ int catnn_hip_install(catnn_hip_device *dev, const catnn_graph *g, catnn_hip_pro
             throw;
         }
         *out = p;
+    });
+}
+
+int catnn_hip_install_placed(catnn_hip_device *dev, const catnn_graph *g, const catnn_placement_entry *assign,
+                             int32_t n_assign, const char *device_id, const char *default_device,
+                             catnn_hip_program **out) {
+    return guard([&] {
+        require_device(dev);
+        CATNN_REQUIRE(g && out && device_id && default_device && (assign || n_assign == 0),
+                      CATNN_ERR_INVALID_ARGUMENT, "null argument");
+        *out = nullptr;
+        std::map<std::string, std::string> a;
+        for (int32_t i = 0; i < n_assign; ++i) {
+            CATNN_REQUIRE(assign[i].op && assign[i].device, CATNN_ERR_INVALID_ARGUMENT, "null placement entry");
+            a[assign[i].op] = assign[i].device;  // IndexMap::insert: a later entry replaces an earlier one
+        }
+        auto *p = new catnn_hip_program();
+        try {
+            p->dev = dev;
+            p->placed = true;
+            p->graph = stage_of(*g, a, device_id, default_device, p->port_in, p->port_out);
+            build_program(*p);
+            plan_and_upload(*p);
+            p->step_done.assign(p->steps.size(), 0);
+        } catch (...) {
+            if (p->base) (void)hipFree(p->base);
+            delete p;
+            throw;
+        }
+        *out = p;
+    });
+}
+
+int catnn_hip_program_ports(catnn_hip_program *p, char (*in_names)[CATNN_ID_CAP], int32_t in_cap, int32_t *n_in,
+                            char (*out_names)[CATNN_ID_CAP], int32_t out_cap, int32_t *n_out) {
+    return guard([&] {
+        CATNN_REQUIRE(p && n_in && n_out, CATNN_ERR_INVALID_ARGUMENT, "null argument");
+        auto fill = [](const std::map<std::string, uint32_t> &m, const std::vector<uint32_t> &order,
+                       const catnn_graph &g, char (*names)[CATNN_ID_CAP], int32_t cap, int32_t *n) {
+            int32_t k = 0;
+            for (uint32_t id : order) {
+                const std::string &nm = g.node(id).name;
+                if (!m.count(nm)) continue;
+                if (names && k < cap) {
+                    std::memset(names[k], 0, CATNN_ID_CAP);
+                    std::strncpy(names[k], nm.c_str(), CATNN_ID_CAP - 1);
+                }
+                ++k;
+            }
+            *n = k;
+        };
+        std::map<std::string, uint32_t> in = p->port_in, outp = p->port_out;
+        if (!p->placed) {  // an installed whole graph: its inputs and final output
+            for (uint32_t v : p->input_vals) in[p->graph.node(v).name] = v;
+            outp[p->graph.node(p->output_val).name] = p->output_val;
+        }
+        fill(in, p->graph.inputs, p->graph, in_names, in_cap, n_in);
+        fill(outp, p->graph.outputs, p->graph, out_names, out_cap, n_out);
+    });
+}
+
+int catnn_hip_program_new_pass(catnn_hip_program *p) {
+    return guard([&] {
+        CATNN_REQUIRE(p, CATNN_ERR_INVALID_ARGUMENT, "null program");
+        p->have.clear();
+        p->step_done.assign(p->steps.size(), 0);
+    });
+}
+
+int catnn_hip_program_set_value(catnn_hip_program *p, const char *name, const catnn_tensor *value) {
+    return guard([&] {
+        CATNN_REQUIRE(p && name && value, CATNN_ERR_INVALID_ARGUMENT, "null argument");
+        require_device(p->dev);
+        uint32_t id = UINT32_MAX;
+        auto it = p->port_in.find(name);
+        if (it != p->port_in.end()) id = it->second;
+        for (uint32_t v : p->input_vals)
+            if (!p->placed && p->graph.node(v).name == name) id = v;
+        CATNN_REQUIRE(id != UINT32_MAX, CATNN_ERR_UNKNOWN_PORT,
+                      std::string("unknown port ") + name + " on interface " + p->graph.name);
+        const HostTensor in = from_c(*value, true);
+        CATNN_REQUIRE(in.numel() == numel_of(p->dims[id]), CATNN_ERR_SHAPE_MISMATCH,
+                      std::string(name) + ": " + dims_str(in.dims) + " vs " + dims_str(p->dims[id]));
+        if (in.numel())
+            CATNN_HIP(hipMemcpyAsync(p->ptr.at(act_id(id)), in.data.data(), (size_t)in.numel() * 4,
+                                     hipMemcpyHostToDevice, p->dev->stream));
+        CATNN_HIP(hipStreamSynchronize(p->dev->stream));  // the host tensor is borrowed for the call only
+        p->have.insert(id);
+    });
+}
+
+int catnn_hip_forward_wave(catnn_hip_program *p, int32_t *fired) {
+    return guard([&] {
+        CATNN_REQUIRE(p, CATNN_ERR_INVALID_ARGUMENT, "null program");
+        require_device(p->dev);
+        if (p->step_done.size() != p->steps.size()) p->step_done.assign(p->steps.size(), 0);
+        const int n = forward_wave(*p);
+        if (fired) *fired = n;
+    });
+}
+
+int catnn_hip_program_get_value(catnn_hip_program *p, const char *name, catnn_tensor *out) {
+    return guard([&] {
+        CATNN_REQUIRE(p && name && out, CATNN_ERR_INVALID_ARGUMENT, "null argument");
+        require_device(p->dev);
+        uint32_t id = UINT32_MAX;
+        auto it = p->port_out.find(name);
+        if (it != p->port_out.end()) id = it->second;
+        if (!p->placed && p->graph.node(p->output_val).name == name) id = p->output_val;
+        CATNN_REQUIRE(id != UINT32_MAX, CATNN_ERR_UNKNOWN_PORT,
+                      std::string("unknown port ") + name + " on interface " + p->graph.name);
+        CATNN_REQUIRE(!p->placed || p->have.count(id), CATNN_ERR_WIRING,
+                      std::string(name) + " has not been computed in this pass");
+        const auto &od = p->dims[id];
+        const int64_t n = numel_of(od);
+        int64_t cap = 1;
+        for (int i = 0; i < out->rank; ++i) cap *= out->dims[i];
+        CATNN_REQUIRE(cap >= n && (out->data || n == 0), CATNN_ERR_SHAPE_MISMATCH,
+                      "output buffer holds " + std::to_string(cap) + " values, " + name + " has " + dims_str(od));
+        if (n)
+            CATNN_HIP(hipMemcpyAsync(out->data, p->ptr.at(act_id(id)), (size_t)n * 4, hipMemcpyDeviceToHost,
+                                     p->dev->stream));
+        CATNN_HIP(hipStreamSynchronize(p->dev->stream));
+        out->rank = (int32_t)od.size();
+        for (size_t i = 0; i < od.size(); ++i) out->dims[i] = od[i];
+        out->dtype = CATNN_F32;
     });
 }
 

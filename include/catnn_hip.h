@@ -384,6 +384,101 @@ int catnn_hip_program_profile(catnn_hip_program *p, int32_t enable);
 int catnn_hip_program_timings(catnn_hip_program *p, catnn_step_timing *out,
                               int32_t cap, int32_t *n);
 
+/* --------------------------------------------------- placement target */
+/* The new placement target in H.  A Realization places each IR node on a
+ * cluster device (`Placement.assign`, crates/catnn-core/src/architecture/
+ * realization.rs:13-31); a device of kind Gpu whose architecture is gfx950
+ * gets the HIP kernel backend (catnn_hip_kernels_for), and the runtime runs
+ * that device's stage of the graph here (catnn_hip_install_placed). */
+
+/* KernelBackend (realization.rs:49-55, declaration order) with the new
+ * variant last. */
+enum catnn_kernel_backend {
+    CATNN_BACKEND_CPU_RUST = 0, CATNN_BACKEND_WGSL = 1, CATNN_BACKEND_REFERENCE = 2,
+    CATNN_BACKEND_CUDA_SM121 = 3, CATNN_BACKEND_HIP = 4
+};
+/* DeviceKind (crates/catnn-core/src/architecture/hardware.rs:13-17). */
+enum catnn_device_kind { CATNN_DEVICE_CPU = 0, CATNN_DEVICE_GPU = 1, CATNN_DEVICE_ACCELERATOR = 2 };
+
+/* One device of the cluster: `Device { id, kind, .. }` (hardware.rs:39-49)
+ * plus the GPU architecture the device reports ("gfx950" for MI355X; NULL or
+ * "" for none). */
+typedef struct catnn_cluster_device {
+    const char *id;
+    int32_t kind;      /* enum catnn_device_kind */
+    const char *arch;
+} catnn_cluster_device;
+
+/* One entry of `Placement.assign`: op name → device id. */
+typedef struct catnn_placement_entry {
+    const char *op;
+    const char *device;
+} catnn_placement_entry;
+
+/* `KernelChoice { op, backend }` (realization.rs:57-61). */
+typedef struct catnn_kernel_choice {
+    char op[CATNN_ID_CAP];
+    int32_t backend;   /* enum catnn_kernel_backend */
+} catnn_kernel_choice;
+
+/* kernels_for (crates/catnn-compile/src/place.rs:152-166) with the HIP arm:
+ * for every node in IndexMap order, the backend of the device its placement
+ * names — Gpu with arch "gfx950" → CATNN_BACKEND_HIP, other Gpu or
+ * Accelerator → CATNN_BACKEND_WGSL, anything else (Cpu, an unplaced node, an
+ * unknown device) → CATNN_BACKEND_CPU_RUST.  Writes the first `cap` choices
+ * and sets *n to the node count.  Host-only. */
+int catnn_hip_kernels_for(const catnn_graph *g, const catnn_placement_entry *assign, int32_t n_assign,
+                          const catnn_cluster_device *devices, int32_t n_devices,
+                          catnn_kernel_choice *out, int32_t cap, int32_t *n);
+
+/* `MemoryRegion` (crates/catnn-core/src/architecture/memory.rs:79-88) and
+ * `DeviceMemory { code, buffer, scratch }` (memory.rs:95-100). */
+typedef struct catnn_memory_region {
+    uint64_t bytes;
+    double bandwidth_bps;
+    double latency_s;
+    char provenance[256];
+} catnn_memory_region;
+typedef struct catnn_device_memory {
+    catnn_memory_region code, buffer, scratch;
+} catnn_device_memory;
+
+/* The MI355X region profile of H, the counterpart of DeviceMemory::
+ * dgx_spark (memory.rs:136-175): buffer = the device's HBM3E (its reported
+ * size; 8 TB/s published), scratch = the 160 KiB of LDS per CU (gfx950),
+ * code = the bytes of this library's gfx950 kernels (measured from its code
+ * objects at build time).  `dev` may be NULL: then the published 288 GB is
+ * used for the buffer and nothing touches a GPU. */
+int catnn_hip_device_memory(catnn_hip_device *dev, catnn_device_memory *out);
+
+/* Installs the stage of `g` placed on `device_id` — the nodes whose
+ * placement (assign; absent: default_device, as forward_device reads it,
+ * crates/catnn-rt/src/coord.rs:629) names it.  A value produced on another
+ * device and read here enters as the input port "{producer}#recv" (the
+ * buffer act:{producer}#recv of schedule_device, pipeline.rs:319-327); a
+ * local value read elsewhere, and a graph output placed here, is an output
+ * port.  No node placed there → CATNN_ERR_UNKNOWN_REALIZATION.  The stage
+ * is an installed program (one hipMalloc arena; its activations are not
+ * aliased, since its steps run as their inputs arrive). */
+int catnn_hip_install_placed(catnn_hip_device *dev, const catnn_graph *g, const catnn_placement_entry *assign,
+                             int32_t n_assign, const char *device_id, const char *default_device,
+                             catnn_hip_program **out);
+/* The names of a program's input and output ports, in node order. */
+int catnn_hip_program_ports(catnn_hip_program *p, char (*in_names)[CATNN_ID_CAP], int32_t in_cap, int32_t *n_in,
+                            char (*out_names)[CATNN_ID_CAP], int32_t out_cap, int32_t *n_out);
+/* Starts a forward pass: no value is present, no step has run. */
+int catnn_hip_program_new_pass(catnn_hip_program *p);
+/* Delivers the value of input port `name` (a graph input placed here, or a
+ * "#recv" port) for this pass; unknown name → CATNN_ERR_UNKNOWN_PORT. */
+int catnn_hip_program_set_value(catnn_hip_program *p, const char *name, const catnn_tensor *value);
+/* One forward wave (forward_device, coord.rs:622-676): every step not yet run
+ * in this pass whose inputs are all present runs, in topo order; *fired (or
+ * NULL) receives their number — 0 when the stage is quiescent. */
+int catnn_hip_forward_wave(catnn_hip_program *p, int32_t *fired);
+/* The value of output port `name` (after the wave that computed it; else
+ * CATNN_ERR_WIRING), copied to the host, for fanout to other devices. */
+int catnn_hip_program_get_value(catnn_hip_program *p, const char *name, catnn_tensor *out);
+
 /* ------------------------------------------------------------ training */
 /* One training step of an IrGraph on this device: replaces
  * pipeline::reference_train (crates/catnn-compile/src/pipeline.rs:476-547)
