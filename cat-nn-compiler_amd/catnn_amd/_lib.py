@@ -95,6 +95,11 @@ class CDeviceMemory(ctypes.Structure):
     _fields_ = [("code", CMemoryRegion), ("buffer", CMemoryRegion), ("scratch", CMemoryRegion)]
 
 
+class CTrainOptions(ctypes.Structure):
+    _fields_ = [("optimizer", ctypes.c_int32), ("lr", ctypes.c_float), ("precision", ctypes.c_int32),
+                ("arena_cap", ctypes.c_uint64)]
+
+
 class CEvent(ctypes.Structure):
     _fields_ = [("t_ns", ctypes.c_uint64), ("op", ctypes.c_char * ID_CAP),
                 ("kind", ctypes.c_int32), ("checksum", ctypes.c_uint64)]
@@ -176,7 +181,8 @@ SIGNATURES = {
     "catnn_hip_program_timings": [_VP, ctypes.POINTER(CStepTiming), _I32, _PI32],
     "catnn_hip_train_install": [_VP, _VP, _F, ctypes.POINTER(_VP)],
     "catnn_hip_train_install_opt": [_VP, _VP, _I32, _F, ctypes.POINTER(_VP)],
-    "catnn_hip_train_install_ex": [_VP, _VP, _I32, _F, _I32, ctypes.POINTER(_VP)],
+    "catnn_hip_train_install_ex": [_VP, _VP, ctypes.POINTER(CTrainOptions), ctypes.POINTER(_VP)],
+    "catnn_hip_train_checkpointed": [_VP, _VP, _I32, _PI32],
     "catnn_hip_train_set_batch_classes": [_VP, ctypes.POINTER(CTensor), ctypes.POINTER(ctypes.c_uint32), _I64],
     "catnn_hip_train_read_moment": [_VP, ctypes.c_uint32, ctypes.c_char_p, _I32, ctypes.POINTER(_F), _I64],
     "catnn_hip_train_adam_step": [_VP, _PU64],

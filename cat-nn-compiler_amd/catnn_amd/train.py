@@ -16,7 +16,7 @@ from typing import List, Tuple
 
 import numpy as np
 
-from ._lib import CArenaAlloc, check, lib
+from ._lib import CArenaAlloc, CTrainOptions, ID_CAP, check, lib
 from .arena import ArenaAlloc
 from .device import Device, graph_handle
 from .ir import IrGraph, Tensor, ctensor
@@ -29,10 +29,12 @@ PRECISIONS = {"bf16": 0, "fp32": 1}  # CATNN_PREC_BF16, CATNN_PREC_FP32
 
 class Trainer:
     def __init__(self, device: Device, graph: IrGraph, lr: float = 0.05, opt: str = "sgd",
-                 precision: str = "bf16"):
+                 precision: str = "bf16", arena_cap: int = 0):
         """`opt` is OptimizerKind::parse's spelling: "sgd" or "adam".
         `precision` "bf16": bf16 MFMA GEMM operands (mixed precision);
-        "fp32": every GEMM on six-part split operands, fp32-accurate."""
+        "fp32": every GEMM on six-part split operands, fp32-accurate.
+        `arena_cap` (bytes, 0: the device's memory): activations are
+        checkpointed and recomputed when the plan misses it."""
         if opt not in OPTIMIZERS:
             raise ValueError(f"unknown optimizer {opt!r} (expected sgd or adam)")
         if precision not in PRECISIONS:
@@ -45,8 +47,8 @@ class Trainer:
         h, owned = graph_handle(graph)
         self.handle = ctypes.c_void_p()
         try:
-            check(lib.catnn_hip_train_install_ex(device.handle, h, OPTIMIZERS[opt], ctypes.c_float(lr),
-                                                 PRECISIONS[precision], ctypes.byref(self.handle)))
+            o = CTrainOptions(OPTIMIZERS[opt], lr, PRECISIONS[precision], int(arena_cap))
+            check(lib.catnn_hip_train_install_ex(device.handle, h, ctypes.byref(o), ctypes.byref(self.handle)))
         finally:
             if owned:
                 lib.catnn_graph_free(h)
@@ -121,6 +123,14 @@ class Trainer:
         check(lib.catnn_hip_train_arena(self.handle, buf, n.value, ctypes.byref(n), ctypes.byref(reserved)))
         return ([ArenaAlloc(a.id.decode(), a.bytes, a.offset, a.live_from, a.live_to)
                  for a in buf[: n.value]], reserved.value)
+
+    def checkpointed(self) -> List[str]:
+        """The activations the plan checkpoints ("act:{node id}")."""
+        n = ctypes.c_int32()
+        check(lib.catnn_hip_train_checkpointed(self.handle, None, 0, ctypes.byref(n)))
+        buf = (ctypes.c_char * ID_CAP * max(n.value, 1))()
+        check(lib.catnn_hip_train_checkpointed(self.handle, buf, n.value, ctypes.byref(n)))
+        return [bytes(buf[i]).split(b"\0", 1)[0].decode() for i in range(n.value)]
 
     def free(self):
         if self.handle:

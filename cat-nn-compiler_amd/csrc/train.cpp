@@ -113,7 +113,18 @@ struct catnn_hip_trainer {
     float lr = 0.05f;
     int opt = CATNN_OPT_SGD;
     int prec = CATNN_PREC_BF16;
+    uint64_t arena_cap = 0;  // 0: the device's memory
     uint64_t adam_t = 0;  // AdamState.t shared by every trained parameter
+    // Activation checkpoints (schedule.rs:155-212): value id → where its
+    // forward buffer ends and where the recomputed copy lives.
+    struct Ckpt {
+        size_t req = 0;            // index of act:{id} in reqs
+        uint64_t fwd_last = 0;     // last forward tick that reads the value
+        uint64_t bwd_first = 0;    // first backward tick that reads it
+        size_t first_reader = 0;   // nodes[] index of the node whose backward runs at bwd_first
+    };
+    std::map<uint32_t, Ckpt> ckpt_candidates, ckpt;
+    std::map<uint32_t, float *> val_fwd, val_recomp;  // per checkpointed value
     bool input_grads = false;  // keep the graph inputs' cotangents (run_adjoint)
     std::vector<catnn::TNode> nodes;
     std::map<uint32_t, size_t> index;                 // node id → nodes[]
@@ -363,11 +374,46 @@ static void plan_trainer(Tr &t) {
     }
     // The output value stays readable after the step (catnn_hip_train_read_value).
     last_read[t.out_id] = upd;
+    // Values that may be checkpointed: produced by a node (not a graph
+    // input, not the output the loss reads), read again in the backward
+    // pass, by a producer whose forward uses no forward-only scratch (it is
+    // re-run at the first backward tick that reads the value).
+    std::map<uint32_t, uint64_t> fwd_last, bwd_first;
+    std::map<uint32_t, size_t> first_reader;
+    auto bwd_read = [&](uint32_t v, size_t i) {
+        const uint64_t b = bwd(t.nodes[i].tick);
+        if (!bwd_first.count(v) || b < bwd_first[v]) {
+            bwd_first[v] = b;
+            first_reader[v] = i;
+        }
+    };
+    for (size_t i = 0; i < t.nodes.size(); ++i) {
+        const TNode &tn = t.nodes[i];
+        for (uint32_t v : tn.ins) {
+            fwd_last[v] = std::max<uint64_t>(fwd_last[v], tn.tick);
+            bwd_read(v, i);
+        }
+        if (tn.kind == CATNN_OP_SOFTMAX) bwd_read(tn.id, i);  // softmax_backward reads its own output
+        if (tn.gelu_pre != UINT32_MAX) bwd_read(tn.gelu_pre, i);  // the fused GELU adjoint reads A's output
+    }
     for (auto &tn : t.nodes) {
         const uint64_t bytes = (uint64_t)numel(tn.dims) * 4;
         // The batch (inputs and target) stays resident across steps: set_batch
         // once, step many times.
         const bool is_input = t.input_ids.count(tn.id) != 0;
+        const bool fscratch_fwd = t.prec == CATNN_PREC_FP32 &&
+            (tn.kind == CATNN_OP_LINEAR || tn.kind == CATNN_OP_MATMUL || tn.kind == CATNN_OP_LM_HEAD ||
+             tn.kind == CATNN_OP_SWIGLU || tn.kind == CATNN_OP_ATTENTION || tn.kind == CATNN_OP_GQA_ATTENTION ||
+             tn.kind == CATNN_OP_MOE);
+        if (!is_input && tn.id != t.out_id && !fscratch_fwd && fwd_last.count(tn.id) &&
+            last_read[tn.id] > fwd_last[tn.id] && bwd_first.count(tn.id)) {
+            catnn_hip_trainer::Ckpt c;
+            c.req = t.reqs.size();
+            c.fwd_last = fwd_last[tn.id];
+            c.bwd_first = bwd_first[tn.id];
+            c.first_reader = first_reader[tn.id];
+            t.ckpt_candidates[tn.id] = c;
+        }
         request(t, "act:" + std::to_string(tn.id), bytes, is_input ? 0 : tn.tick,
                 is_input ? upd : last_read[tn.id], reinterpret_cast<void **>(&t.val[tn.id]));
         if (is_input) {
@@ -801,10 +847,50 @@ static void upload_params(Tr &t) {
     if (t.prec == CATNN_PREC_FP32) refresh_split_copies(t);
 }
 
+// place_arena under the cap; when the arena misses, checkpoint the value
+// with the largest bytes × lifetime — its buffer then ends at its last
+// forward read and a copy "act:{id}#recomp" lives from its first backward
+// read, recomputed there by re-running its producer — as schedule() does
+// for one buffer (schedule.rs:155-212), repeated until the plan fits or
+// nothing is left to checkpoint.
+static void plan_arena(Tr &t, uint64_t cap) {
+    for (;;) {
+        try {
+            t.plan = place_arena(t.reqs, cap);
+            return;
+        } catch (const Failure &f) {
+            if (f.code != CATNN_ERR_FIBRATION) throw;
+            uint32_t best = UINT32_MAX;
+            uint64_t best_cost = 0;
+            for (const auto &kv : t.ckpt_candidates) {
+                if (t.ckpt.count(kv.first)) continue;
+                const BufferReq &r = t.reqs[kv.second.req];
+                const uint64_t cost = r.bytes * (r.live_to - r.live_from + 1);
+                if (best == UINT32_MAX || cost > best_cost) {
+                    best = kv.first;
+                    best_cost = cost;
+                }
+            }
+            if (best == UINT32_MAX)
+                fail(CATNN_ERR_FIBRATION, f.msg + " (no activation left to checkpoint)");
+            const catnn_hip_trainer::Ckpt c = t.ckpt_candidates.at(best);
+            BufferReq &r = t.reqs[c.req];
+            const uint64_t t1 = r.live_to;
+            r.live_to = c.fwd_last;
+            r.checkpoint = true;
+            const uint64_t bytes = r.bytes;
+            const std::string id = r.id + "#recomp";
+            t.reqs.push_back(BufferReq{id, bytes, c.bwd_first, t1, true});
+            t.req_slot.push_back(reinterpret_cast<void **>(&t.val_recomp[best]));
+            t.ckpt[best] = c;
+        }
+    }
+}
+
 static void reserve_and_upload(Tr &t) {
     hipDeviceProp_t prop;
     CATNN_HIP(hipGetDeviceProperties(&prop, t.dev->ordinal));
-    t.plan = place_arena(t.reqs, prop.totalGlobalMem);
+    plan_arena(t, t.arena_cap ? std::min<uint64_t>(t.arena_cap, prop.totalGlobalMem) : prop.totalGlobalMem);
     t.reserved = 0;
     for (const auto &a : t.plan) t.reserved = std::max(t.reserved, a.offset + a.bytes);
     hipError_t e = hipMalloc(&t.base, t.reserved);
@@ -815,6 +901,7 @@ static void reserve_and_upload(Tr &t) {
     for (const auto &a : t.plan) off[a.id] = a.offset;
     for (size_t i = 0; i < t.reqs.size(); ++i)
         *t.req_slot[i] = static_cast<char *>(t.base) + off.at(t.reqs[i].id);
+    for (const auto &kv : t.ckpt) t.val_fwd[kv.first] = t.val.at(kv.first);
     for (auto &p : t.params)
         CATNN_REQUIRE((int64_t)p->init.size() == p->rows * p->cols, CATNN_ERR_SHAPE_MISMATCH,
                       p->name + ": parameter size");
@@ -1531,8 +1618,33 @@ static void backward_node(Tr &t, TNode &tn) {
     }
 }
 
+// Checkpointed values: the forward writes their own buffer; before the
+// backward step of their first backward reader, their producer runs again
+// into the "#recomp" copy, which the rest of the backward pass reads
+// (ensure_act's rematerialisation, coord.rs:441-470, on the device).
+static void forward_values_home(Tr &t) {
+    for (const auto &kv : t.val_fwd) t.val[kv.first] = kv.second;
+}
+
+static void recompute_before(Tr &t, size_t reader) {
+    for (const auto &kv : t.ckpt) {
+        if (kv.second.first_reader != reader) continue;
+        t.val[kv.first] = t.val_recomp.at(kv.first);
+        forward_node(t, t.nodes[t.index.at(kv.first)]);
+    }
+}
+
+static void reverse_steps(Tr &t) {
+    for (size_t i = t.nodes.size(); i-- > 0;) {
+        TNode &tn = t.nodes[i];
+        if (!t.ckpt.empty()) recompute_before(t, i);
+        if (!t.input_ids.count(tn.id) && t.has_grad.count(tn.id) && !tn.skip_bwd) backward_node(t, tn);
+    }
+}
+
 static void train_step(Tr &t) {
     hipStream_t s = t.dev->stream;
+    forward_values_home(t);
     for (auto &tn : t.nodes)
         if (!t.input_ids.count(tn.id)) forward_node(t, tn);
     const int64_t n_out = numel(t.dims[t.out_id]);
@@ -1543,8 +1655,7 @@ static void train_step(Tr &t) {
         k::mse(s, t.val.at(t.out_id), t.target, t.grad.at(t.out_id), n_out, t.loss, t.mse_scratch);
     // A node whose output nobody reads receives no cotangent and is skipped,
     // as reference_train skips ids without an entry in `grads`.
-    for (auto it = t.nodes.rbegin(); it != t.nodes.rend(); ++it)
-        if (!t.input_ids.count(it->id) && t.has_grad.count(it->id) && !it->skip_bwd) backward_node(t, *it);
+    reverse_steps(t);
     // apply_update on the parameters of every node that received a
     // cotangent, and the refresh of their bf16 copies, in one launch.
     const k::UpdateRule rule = t.opt == CATNN_OPT_ADAM ? k::adam_rule(t.lr, ++t.adam_t) : k::sgd_rule(t.lr);
@@ -1556,14 +1667,12 @@ static void train_step(Tr &t) {
 // tapes, then — once the caller has put the output's cotangent in place, at
 // the loss tick of the plan — the reverse pass.
 static void forward_pass(Tr &t) {
+    forward_values_home(t);
     for (auto &tn : t.nodes)
         if (!t.input_ids.count(tn.id)) forward_node(t, tn);
 }
 
-static void reverse_pass(Tr &t) {
-    for (auto it = t.nodes.rbegin(); it != t.nodes.rend(); ++it)
-        if (!t.input_ids.count(it->id) && t.has_grad.count(it->id) && !it->skip_bwd) backward_node(t, *it);
-}
+static void reverse_pass(Tr &t) { reverse_steps(t); }
 
 static TParam *find_param(Tr &t, uint32_t node_id, const std::string &port, int64_t *col0,
                           int64_t *ncols) {
@@ -1752,14 +1861,17 @@ int catnn_hip_train_install(catnn_hip_device *dev, const catnn_graph *g, float l
 
 int catnn_hip_train_install_opt(catnn_hip_device *dev, const catnn_graph *g, int32_t optimizer, float lr,
                                 catnn_hip_trainer **out) {
-    return catnn_hip_train_install_ex(dev, g, optimizer, lr, CATNN_PREC_BF16, out);
+    const catnn_train_options o{optimizer, lr, CATNN_PREC_BF16, 0};
+    return catnn_hip_train_install_ex(dev, g, &o, out);
 }
 
-int catnn_hip_train_install_ex(catnn_hip_device *dev, const catnn_graph *g, int32_t optimizer, float lr,
-                               int32_t precision, catnn_hip_trainer **out) {
+int catnn_hip_train_install_ex(catnn_hip_device *dev, const catnn_graph *g, const catnn_train_options *opts,
+                               catnn_hip_trainer **out) {
     return guard([&] {
         require_device(dev);
-        CATNN_REQUIRE(g && out, CATNN_ERR_INVALID_ARGUMENT, "null argument");
+        CATNN_REQUIRE(g && out && opts, CATNN_ERR_INVALID_ARGUMENT, "null argument");
+        const int32_t optimizer = opts->optimizer, precision = opts->precision;
+        const float lr = opts->lr;
         CATNN_REQUIRE(optimizer == CATNN_OPT_SGD || optimizer == CATNN_OPT_ADAM, CATNN_ERR_INVALID_ARGUMENT,
                       "unknown optimizer " + std::to_string(optimizer) + " (expected sgd or adam)");
         CATNN_REQUIRE(precision == CATNN_PREC_BF16 || precision == CATNN_PREC_FP32, CATNN_ERR_INVALID_ARGUMENT,
@@ -1772,6 +1884,7 @@ int catnn_hip_train_install_ex(catnn_hip_device *dev, const catnn_graph *g, int3
             t->lr = lr;
             t->opt = optimizer;
             t->prec = precision;
+            t->arena_cap = opts->arena_cap;
             plan_trainer(*t);
             reserve_and_upload(*t);
         } catch (...) {
@@ -2069,6 +2182,21 @@ int catnn_hip_train_read_routing(catnn_hip_trainer *t, uint32_t node_id, int32_t
         CATNN_REQUIRE(n == T * tn.node->op.a[1], CATNN_ERR_SHAPE_MISMATCH, "routing buffer size");
         CATNN_HIP(hipMemcpyAsync(idx, tn.B("idx"), (size_t)n * 4, hipMemcpyDeviceToHost, t->dev->stream));
         CATNN_HIP(hipStreamSynchronize(t->dev->stream));
+    });
+}
+
+int catnn_hip_train_checkpointed(catnn_hip_trainer *t, char (*ids)[CATNN_ID_CAP], int32_t cap, int32_t *n) {
+    return guard([&] {
+        CATNN_REQUIRE(t && n, CATNN_ERR_INVALID_ARGUMENT, "null argument");
+        int32_t k = 0;
+        for (const auto &kv : t->ckpt) {
+            if (ids && k < cap) {
+                std::memset(ids[k], 0, CATNN_ID_CAP);
+                std::strncpy(ids[k], ("act:" + std::to_string(kv.first)).c_str(), CATNN_ID_CAP - 1);
+            }
+            ++k;
+        }
+        *n = k;
     });
 }
 

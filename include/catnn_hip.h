@@ -521,8 +521,26 @@ int catnn_hip_train_install_opt(catnn_hip_device *dev, const catnn_graph *g, int
  * cotangent fp32: the fp32 algorithm of reference_train to fp32 rounding,
  * for fp32 graphs.  Other values: CATNN_ERR_INVALID_ARGUMENT. */
 enum { CATNN_PREC_BF16 = 0, CATNN_PREC_FP32 = 1 };
-int catnn_hip_train_install_ex(catnn_hip_device *dev, const catnn_graph *g, int32_t optimizer,
-                               float lr, int32_t precision, catnn_hip_trainer **out);
+/* The options of a trainer.  `arena_cap` (0: the device's memory) caps the
+ * training arena, the buffer region of schedule (schedule.rs:149-212): when
+ * the plan misses it, the activation with the largest bytes × lifetime is
+ * checkpointed — its buffer ends at its last forward read and a copy
+ * "act:{id}#recomp" lives from its first backward read, where its producer
+ * runs again (rematerialisation, coord.rs:441-470) — and placement is
+ * retried, as schedule() does for one buffer, until the plan fits; nothing
+ * left to checkpoint → CATNN_ERR_FIBRATION.  Checkpointed steps give the
+ * same bits as uncheckpointed ones. */
+typedef struct catnn_train_options {
+    int32_t optimizer;   /* CATNN_OPT_SGD or CATNN_OPT_ADAM */
+    float lr;
+    int32_t precision;   /* CATNN_PREC_BF16 or CATNN_PREC_FP32 */
+    uint64_t arena_cap;
+} catnn_train_options;
+int catnn_hip_train_install_ex(catnn_hip_device *dev, const catnn_graph *g, const catnn_train_options *opts,
+                               catnn_hip_trainer **out);
+/* The values the plan checkpointed ("act:{node id}"), as DeviceStage.
+ * checkpointed lists them (pipeline.rs:385-396); *n receives their number. */
+int catnn_hip_train_checkpointed(catnn_hip_trainer *t, char (*ids)[CATNN_ID_CAP], int32_t cap, int32_t *n);
 int catnn_hip_train_free(catnn_hip_trainer *t);
 /* Upload the batch: `input` is bound to every graph input, `target` is the
  * MSE target of the last output. */

@@ -260,3 +260,55 @@ def test_training_error_kinds(device):
         tr.value(lin, tuple(w.graph.nodes[lin].output_ty.shape))
     assert e.value.kind == "Unsupported"
     tr.free()
+
+
+def _all_params(tr, g):
+    out = {}
+    for nid, node in g.nodes.items():
+        for port in node.params:
+            shape = _shape(g, nid, port)
+            out[(nid, port)] = (tr.grad(nid, port, shape), tr.param(nid, port, shape))
+    return out
+
+
+@pytest.mark.parametrize("which,precision", [("block_moe", "bf16"), ("block_moe", "fp32"), ("block_gelu", "bf16"),
+                                             ("block_gelu", "fp32")])
+def test_capped_arena_checkpoints_and_steps_bit_exactly(device, which, precision):
+    # An arena cap one byte below the uncapped plan: schedule()'s fallback
+    # (schedule.rs:155-212) checkpoints the activation with the largest
+    # bytes × lifetime and recomputes it at its first backward read; the
+    # step's loss, gradients and updated parameters are the same bits as the
+    # uncapped step's (the rematerialisation check of train.rs:826-829).
+    if which == "block_gelu":
+        w = configs.config3(batch=1, seq=128, d=128, heads=2, ffn=512)
+        tgt = _target([1, 128, 128], 32)
+    else:
+        w = configs.config5(batch=1, seq=128, d=128, heads=2, ffn=256, n_experts=4, top_k=2, inter=128)
+        tgt = w.target
+    g = w.graph
+    ref = Trainer(device, g, 0.05, precision=precision)
+    _, reserved = ref.arena()
+    assert ref.checkpointed() == []
+    ref.set_batch(w.x, tgt)
+    loss0 = ref.step()
+    want = _all_params(ref, g)
+    ref.free()
+    capped = Trainer(device, g, 0.05, precision=precision, arena_cap=reserved - 1)
+    ck = capped.checkpointed()
+    allocs, reserved_c = capped.arena()
+    print(f"  {which}/{precision}: {reserved} B uncapped, {reserved_c} B capped, checkpointed {ck}")
+    assert ck and reserved_c <= reserved - 1
+    assert arena_conflict(allocs) is None
+    assert {a.id for a in allocs if a.id.endswith("#recomp")} == {c + "#recomp" for c in ck}
+    capped.set_batch(w.x, tgt)
+    for step in range(2):  # the recomputed buffers are refilled on every step
+        loss1 = capped.step()
+        if step == 0:
+            assert loss1 == loss0
+            got = _all_params(capped, g)
+            for key, (gr, p) in want.items():
+                assert np.array_equal(got[key][0], gr) and np.array_equal(got[key][1], p), key
+    capped.free()
+    with pytest.raises(CatError) as e:
+        Trainer(device, g, 0.05, precision=precision, arena_cap=1 << 16)
+    assert e.value.kind == "Fibration"
