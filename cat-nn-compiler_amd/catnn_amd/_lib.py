@@ -175,6 +175,7 @@ SIGNATURES = {
     "catnn_hip_program_free": [_VP],
     "catnn_hip_forward": [_VP, ctypes.POINTER(CTensor), ctypes.POINTER(CTensor)],
     "catnn_hip_forward_resident": [_VP],
+    "catnn_hip_program_check": [_VP],
     "catnn_hip_program_io": [_VP, ctypes.POINTER(_VP), _PU64, ctypes.POINTER(_VP), _PU64],
     "catnn_hip_program_arena": [_VP, ctypes.POINTER(CArenaAlloc), _I32, _PI32, _PU64],
     "catnn_hip_program_profile": [_VP, _I32],

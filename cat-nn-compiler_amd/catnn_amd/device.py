@@ -265,6 +265,11 @@ class Program:
     def forward_resident(self):
         check(lib.catnn_hip_forward_resident(self.handle))
 
+    def check(self):
+        """Wait for the enqueued forwards; ShapeMismatch if one met a token
+        id ≥ vocab (catnn_hip_program_check)."""
+        check(lib.catnn_hip_program_check(self.handle))
+
     def io(self) -> ProgramIO:
         ip, op = VP(), VP()
         ib, ob = ctypes.c_uint64(), ctypes.c_uint64()

@@ -26,6 +26,7 @@
 #include "arena.hpp"
 #include "graph.hpp"
 #include "kernels.hpp"
+#include "train_ops.hpp"
 
 namespace catnn {
 
@@ -394,6 +395,10 @@ void exec_node(catnn_hip_device *dev, const Node &node, const ExecArgs &a) {
             const int64_t vocab = pdims(node, "w")[0], hidden = node.op.a[1];
             CATNN_REQUIRE(a.scratch && a.scratch_bytes >= 4, CATNN_ERR_INVALID_ARGUMENT,
                           "embedding: scratch too small");
+            if (a.embed_flag) {  // a program reads the flag once, after its last step
+                k::embedding_f32(s, x, nx, need("w"), vocab, hidden, a.out, a.embed_flag);
+                break;
+            }
             int *bad = reinterpret_cast<int *>(a.scratch);
             CATNN_HIP(hipMemsetAsync(bad, 0, sizeof(int), s));
             k::embedding_f32(s, x, nx, need("w"), vocab, hidden, a.out, bad);
@@ -558,6 +563,12 @@ struct catnn_hip_program {
     std::map<std::string, uint32_t> port_in, port_out;
     std::set<uint32_t> have;       // values present on the device this pass
     std::vector<char> step_done;   // per step, this pass
+    // Embeddings raise one device flag on an id ≥ vocab (moe.rs:38-40); it
+    // is copied to pinned host memory after the last step and checked when
+    // the program next synchronises, so no forward stalls mid-graph.
+    bool has_embedding = false;
+    int *embed_flag = nullptr;       // device (arena)
+    int *embed_flag_host = nullptr;  // pinned
 };
 
 namespace catnn {
@@ -726,6 +737,9 @@ static void plan_and_upload(catnn_hip_program &p) {
         if (derived_floats(n))
             reqs.push_back(BufferReq{derived_id(n), (uint64_t)derived_floats(n) * 4, 0, n_ticks, false});
     }
+    for (const Step &st : p.steps)
+        if (!st.is_input && g.node(st.node).op.kind == CATNN_OP_EMBEDDING) p.has_embedding = true;
+    if (p.has_embedding) reqs.push_back(BufferReq{"flags:embedding", 256, 0, n_ticks, false});
     // Every buffer starts on a 256-byte boundary: round sizes up.
     for (auto &r : reqs) r.bytes = (r.bytes + 255) & ~uint64_t(255);
     hipDeviceProp_t prop;
@@ -741,6 +755,12 @@ static void plan_and_upload(catnn_hip_program &p) {
     }
     for (const auto &a : p.plan)
         p.ptr[a.id] = reinterpret_cast<float *>(static_cast<char *>(p.base) + a.offset);
+    if (p.has_embedding) {
+        p.embed_flag = reinterpret_cast<int *>(p.ptr.at("flags:embedding"));
+        CATNN_HIP(hipHostMalloc(reinterpret_cast<void **>(&p.embed_flag_host), sizeof(int), hipHostMallocDefault));
+        *p.embed_flag_host = 0;
+        k::fill_f32(dev->stream, reinterpret_cast<float *>(p.embed_flag), 0.f, 1);
+    }
     // Params are uploaded once, here.
     for (uint32_t id : g.node_order) {
         const Node &n = g.node(id);
@@ -777,7 +797,23 @@ static void exec_step(catnn_hip_program &p, const Step &st) {
         a.scratch_bytes = st.scratch;
     }
     if (derived_floats(n)) a.derived = p.ptr.at(derived_id(n));
+    a.embed_flag = p.embed_flag;
     exec_node(p.dev, n, a);
+}
+
+// The forward's embedding flag, copied behind its last step.
+static void post_embed_flag(catnn_hip_program &p) {
+    if (p.has_embedding)
+        CATNN_HIP(hipMemcpyAsync(p.embed_flag_host, p.embed_flag, sizeof(int), hipMemcpyDeviceToHost, p.dev->stream));
+}
+
+// After a synchronisation: an out-of-range token id seen by the forward
+// fails it as moe::embedding does (ShapeMismatch, moe.rs:38-40).
+static void check_embed_flag(catnn_hip_program &p) {
+    if (!p.has_embedding || !*p.embed_flag_host) return;
+    *p.embed_flag_host = 0;
+    k::fill_f32(p.dev->stream, reinterpret_cast<float *>(p.embed_flag), 0.f, 1);
+    fail(CATNN_ERR_SHAPE_MISMATCH, "embedding: token id >= vocab in the last forward of " + p.graph.name);
 }
 
 static void run_program(catnn_hip_program &p) {
@@ -803,6 +839,7 @@ static void run_program(catnn_hip_program &p) {
         ++executed;
         if (evs) CATNN_HIP(hipEventRecord((*evs)[executed], p.dev->stream));
     }
+    post_embed_flag(p);
 }
 
 // One forward wave of a placed stage (forward_device, coord.rs:622-676):
@@ -822,6 +859,7 @@ static int forward_wave(catnn_hip_program &p) {
         p.have.insert(st.out);
         ++fired;
     }
+    if (fired) post_embed_flag(p);
     return fired;
 }
 
@@ -1254,6 +1292,7 @@ int catnn_hip_program_get_value(catnn_hip_program *p, const char *name, catnn_te
             CATNN_HIP(hipMemcpyAsync(out->data, p->ptr.at(act_id(id)), (size_t)n * 4, hipMemcpyDeviceToHost,
                                      p->dev->stream));
         CATNN_HIP(hipStreamSynchronize(p->dev->stream));
+        check_embed_flag(*p);
         out->rank = (int32_t)od.size();
         for (size_t i = 0; i < od.size(); ++i) out->dims[i] = od[i];
         out->dtype = CATNN_F32;
@@ -1267,6 +1306,7 @@ int catnn_hip_program_free(catnn_hip_program *p) {
         (void)hipStreamSynchronize(p->dev->stream);
         destroy_events(*p);
         if (p->base) (void)hipFree(p->base);
+        if (p->embed_flag_host) (void)hipHostFree(p->embed_flag_host);
         delete p;
     });
 }
@@ -1308,6 +1348,15 @@ int catnn_hip_forward_resident(catnn_hip_program *p) {
     });
 }
 
+int catnn_hip_program_check(catnn_hip_program *p) {
+    return guard([&] {
+        CATNN_REQUIRE(p, CATNN_ERR_INVALID_ARGUMENT, "null program");
+        require_device(p->dev);
+        CATNN_HIP(hipStreamSynchronize(p->dev->stream));
+        check_embed_flag(*p);
+    });
+}
+
 int catnn_hip_forward(catnn_hip_program *p, const catnn_tensor *input, catnn_tensor *output) {
     return guard([&] {
         CATNN_REQUIRE(p && output, CATNN_ERR_INVALID_ARGUMENT, "null argument");
@@ -1336,6 +1385,7 @@ int catnn_hip_forward(catnn_hip_program *p, const catnn_tensor *input, catnn_ten
             CATNN_HIP(hipMemcpyAsync(output->data, p->ptr.at(act_id(p->output_val)), (size_t)n_out * 4,
                                      hipMemcpyDeviceToHost, dev->stream));
         CATNN_HIP(hipStreamSynchronize(dev->stream));
+        check_embed_flag(*p);
         output->rank = (int32_t)od.size();
         for (size_t i = 0; i < od.size(); ++i) output->dims[i] = od[i];
         output->dtype = CATNN_F32;

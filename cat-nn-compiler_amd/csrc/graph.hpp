@@ -63,6 +63,9 @@ struct ExecArgs {
     // Weight copy made at install: Attention/GqaAttention [wq | wk | wv] per
     // row, LmHead wᵀ [H, V].  Null: built from the params (or scratch) per call.
     const float *derived = nullptr;
+    // Programs: the device flag an Embedding raises on an id ≥ vocab, read
+    // once at the end of the forward (null: checked right after the node).
+    int *embed_flag = nullptr;
 };
 
 // A node from its C form with parameter types only (no data), and the dims

@@ -660,6 +660,13 @@ static void plan_trainer(Tr &t) {
             }
             case CATNN_OP_EMBEDDING: {
                 const int64_t V = nd.op.a[0], H = nd.op.a[1], n_ids = numel(x);
+                // Its ids are checked on the host when the batch is set: they
+                // must come from a graph input (an id ≥ vocab fails the step as
+                // moe::embedding fails, moe.rs:38-40, instead of training on
+                // zero rows).
+                CATNN_REQUIRE(!tn.ins.empty() && t.input_ids.count(tn.ins[0]), CATNN_ERR_UNSUPPORTED,
+                              "training: Embedding " + nd.name + " reads a computed value; its ids must come "
+                              "from a graph input, where they are checked against the vocabulary");
                 const HostTensor *w = host(nd, "w");
                 CATNN_REQUIRE(w->numel() == V * H, CATNN_ERR_SHAPE_MISMATCH, "embedding table");
                 add_param(tn, "w", V, H, false, false, w->data);

@@ -358,8 +358,14 @@ int catnn_hip_program_free(catnn_hip_program *p);
 int catnn_hip_forward(catnn_hip_program *p, const catnn_tensor *input,
                       catnn_tensor *output);
 /* Same, with the input already in the program's input buffer and the
- * output left in the output buffer (no host copies, no sync). */
+ * output left in the output buffer (no host copies, no sync).  An Embedding
+ * that meets an id ≥ vocab (ShapeMismatch in moe::embedding, moe.rs:38-40)
+ * is reported by the next call that synchronises the program:
+ * catnn_hip_forward, catnn_hip_program_get_value or catnn_hip_program_check. */
 int catnn_hip_forward_resident(catnn_hip_program *p);
+/* Waits for the program's enqueued forwards; CATNN_ERR_SHAPE_MISMATCH if one
+ * of them met a token id ≥ vocab. */
+int catnn_hip_program_check(catnn_hip_program *p);
 /* Device buffers of the program's input and output. */
 int catnn_hip_program_io(catnn_hip_program *p, void **in_dptr, uint64_t *in_bytes,
                          void **out_dptr, uint64_t *out_bytes);

@@ -156,7 +156,17 @@ def test_mix(device, gate):
     r = np.random.default_rng(6)
     params = {} if gate is None else {"gate": _t([gate])}
     node = IrNode(3, "mix", OpenOp.mix(), TensorType.f32([5, 300]), params)
-    _check(device, node, [r.standard_normal((5, 300)), r.standard_normal((5, 300))], FP32_TOL)
+    ins = [r.standard_normal((5, 300)), r.standard_normal((5, 300))]
+    _check(device, node, ins, FP32_TOL)
+    if gate is None:
+        # The reference reports a [1] gate cotangent even for a Mix without a
+        # gate param (adjoint.rs:918-927); run_adjoint returns one cotangent
+        # per param the node holds, so a gate-less Mix gets none.
+        x = [np.asarray(a, np.float32) for a in ins]
+        dy = np.ones((5, 300), np.float32)
+        _, dp_o = ot.adjoint_of(node, x, oracle.eval_node(node, x), dy)
+        _, dp = DeviceHandler(device).adjoint_of(node, [_t(a) for a in x], None, _t(dy))
+        assert list(dp_o) == ["gate"] and dp == {}
 
 
 def test_mix_graph_step(device):

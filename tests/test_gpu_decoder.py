@@ -286,3 +286,29 @@ def test_mixtral_tiny_known_answer(device, seed):
     assert got.shape == (2, 4, cfg.vocab)
     assert mx < 2e-4 and err < TOL
     assert rel_l2(got, oracle.eval_graph(g, np.asarray(toks, np.float32).reshape(2, 4))) < TOL
+
+
+def test_program_reports_an_out_of_range_token_after_the_forward(device):
+    # A program checks its embeddings' flag once, when it next synchronises
+    # (no mid-graph stall); the next good forward runs clean.
+    w = configs.mixtral(batch=2, seq=4)
+    prog = Program(device, w.graph)
+    good = prog.forward(w.x).numpy()
+    bad = w.x.numpy().copy()
+    bad[1, 2] = 32.0  # = vocab
+    with pytest.raises(CatError) as e:
+        prog.forward(Tensor(w.x.ty, bad.reshape(-1)))
+    assert e.value.kind == "ShapeMismatch"
+    assert np.array_equal(prog.forward(w.x).numpy(), good)
+    # the resident path: ids already in the input buffer, reported by check()
+    import ctypes
+    from catnn_amd._lib import check, lib
+    io = prog.io()
+    check(lib.catnn_hip_h2d(device.handle, ctypes.c_void_p(io.in_ptr), bad.ctypes.data_as(ctypes.c_void_p),
+                            bad.nbytes))
+    prog.forward_resident()
+    with pytest.raises(CatError) as e:
+        prog.check()
+    assert e.value.kind == "ShapeMismatch"
+    prog.check()  # reported once
+    prog.free()

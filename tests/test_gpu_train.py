@@ -246,6 +246,20 @@ def test_training_error_kinds(device):
     with pytest.raises(CatError) as e:
         Trainer(device, g)
     assert e.value.kind == "Unsupported"
+    # An Embedding whose ids are a computed value: refused at install (ids
+    # from a graph input are checked on the host when the batch is set).
+    g2 = IrGraph("emb_of_value")
+    ty2 = TensorType.f32([2, 4])
+    g2.add_node(IrNode(0, "in", OpenOp.identity(), ty2))
+    g2.add_node(IrNode(1, "relu", OpenOp.relu(), ty2))
+    g2.add_node(IrNode(2, "emb", OpenOp.embedding(10, 8), TensorType.f32([2, 4, 8]),
+                       {"w": Tensor(TensorType.f32([10, 8]), np.ones(80, np.float32))}))
+    g2.add_edge(0, 1)
+    g2.add_edge(1, 2)
+    g2.inputs, g2.outputs = [0], [2]
+    with pytest.raises(CatError) as e:
+        Trainer(device, g2)
+    assert e.value.kind == "Unsupported" and "graph input" in str(e.value)
 
     w = configs.config1(batch=8)
     tr = Trainer(device, w.graph)
