@@ -27,6 +27,7 @@ Only one GPU is used: --gpus above 1 exits with a message.
 """
 import argparse
 import json
+import math
 import os
 import sys
 import time
@@ -88,6 +89,9 @@ def time_train_step(dev, steps, warmup, opt="sgd"):
         tr.step(sync=False)
     total = dev.timer_stop()
     last = tr.step()
+    if not math.isfinite(last):
+        raise RuntimeError(f"config 5 ({opt}): loss {last} after the timed steps; the steps "
+                           "timed diverged and are not the workload")
     tr.reset()
     loss = tr.step()
     allocs, reserved = tr.arena()
@@ -131,6 +135,14 @@ def time_mixtral(dev, steps, warmup):
             "steps_ms": {t[0]: round(t[3] / max(t[2], 1), 4) for t in timings}}
 
 
+def _host_cpus():
+    """The CPUs this process may run on (nproc); `cores` is the threads used."""
+    try:
+        return len(os.sched_getaffinity(0))
+    except AttributeError:
+        return os.cpu_count() or 1
+
+
 def cpu_baseline_mlp(wl, target_s):
     """Oracle restatement of the reference CPU path on a row subset."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
@@ -155,7 +167,8 @@ def cpu_baseline_mlp(wl, target_s):
     rows = max(probe_rows, (rows // probe_rows) * probe_rows)
     t = run(rows)
     flops = 2 * rows * (d * hidden + hidden * d)
-    return {"value": round(flops / t / 1e9, 3), "unit": "GFLOP/s", "cores": cores, "kind": "port",
+    return {"value": round(flops / t / 1e9, 3), "unit": "GFLOP/s", "cores": cores,
+            "host_cpus": _host_cpus(), "kind": "port",
             "sample": f"{rows} of {x.shape[0]} rows of the config-2 forward (fc1+bias, GELU, "
                       f"fc2+bias) in {t:.1f} s; OpenMP over rows where the reference uses Rayon"}
 
@@ -190,7 +203,8 @@ def cpu_baseline_moe(wl, target_s):
     n = int(max(2, min(T, (target_s - t_route) / per_tok)))
     per_tok = max(run(n) - t_route, 1e-6) / n
     layer_s = t_route + T * per_tok
-    return {"value": round(T / layer_s, 2), "unit": "tokens/s", "cores": 1, "kind": "port",
+    return {"value": round(T / layer_s, 2), "unit": "tokens/s", "cores": 1, "host_cpus": _host_cpus(),
+            "kind": "port",
             "sample": f"routing of all {T} tokens ({t_route:.2f} s) plus the expert loop over the first {n} "
                       f"tokens ({per_tok * 1e3:.1f} ms per token), scaled to {T} tokens; sequential as "
                       f"moe::moe"}
