@@ -106,8 +106,8 @@ def time_train_step(dev, steps, warmup, opt="sgd"):
             "loss_after_timed_steps": round(last, 4),
             "arena_reserved_bytes": reserved, "arena_buffers": len(allocs),
             "precision": "bf16 MFMA, fp32 accumulation and master weights; split-bf16 forward "
-                         "GEMMs for Linear/attention, split-bf16 input to the MoE gate/up GEMM; "
-                         "attention core fp32 MFMA"}
+                         "GEMMs for the attention projections, split-bf16 input to the MoE gate/up "
+                         "GEMM; attention core fp32 MFMA"}
 
 
 def time_mixtral(dev, steps, warmup):

@@ -817,7 +817,6 @@ static void check_embed_flag(catnn_hip_program &p) {
 }
 
 static void run_program(catnn_hip_program &p) {
-    const catnn_graph &g = p.graph;
     std::vector<hipEvent_t> *evs = nullptr;
     if (p.profiling) {
         std::vector<hipEvent_t> set;

@@ -20,16 +20,17 @@
 //             chooses — then the bf16 copies are refreshed.
 //
 // Precision: every GEMM runs on v_mfma_f32_32x32x16_bf16 with fp32
-// accumulation.  The forward GEMMs of Linear and attention take split-bf16
-// operands (hi|lo|hi against hi|hi|lo over 3K: the fp32 product to ~2⁻¹⁶),
-// because with plain bf16 operands there the error of the block's output
-// reaches the MoE layer and moves the step's gradients by more than 1e-2
-// from the fp32 path.  The MoE gate/up GEMM takes its input split (hi|lo
-// against the weights' hi|hi, 2K: x at split precision, the expert weights
-// rounded once), the rest of the MoE expert forward and every backward GEMM
-// plain bf16 operands.  Master weights, the residual stream, LayerNorm,
-// softmax statistics, the router and all cotangent accumulation stay fp32;
-// the attention core runs on fp32 MFMA.
+// accumulation.  Linear, MatMul, LmHead and the dense SwiGLU take bf16
+// operands.  The attention projections take split-bf16 operands (hi|lo|hi
+// against hi|hi|lo over 3K: the fp32 product to ~2⁻¹⁶): with plain bf16
+// there the gradients of wq and wk move about 1.3× further from the fp32
+// path.  The MoE gate/up GEMM takes its input split (hi|lo against the
+// weights' hi|hi, 2K: x at split precision, the expert weights rounded
+// once), because the rounding of its input reaches the router's gradient;
+// the rest of the MoE expert forward and every backward GEMM take plain
+// bf16 operands.  Master weights, the residual stream, LayerNorm, softmax
+// statistics, the router and all cotangent accumulation stay fp32; the
+// attention core runs on fp32 MFMA.
 //
 // Memory: every buffer (params, their bf16 copies and gradients, values,
 // cotangents, tapes, scratch) is a BufferReq on the reference's logical
@@ -622,9 +623,9 @@ static void plan_trainer(Tr &t) {
                 const HostTensor *w = nd.param("w") ? nd.param("w") : (nd.params.empty() ? nullptr : &nd.params.front().second);
                 CATNN_REQUIRE(w, CATNN_ERR_UNKNOWN_COMPONENT, "unknown component " + nd.name);
                 const int64_t K = w->dims[0], N = w->dims[1], M = numel(x) / K;
-                add_param(tn, nd.param("w") ? "w" : nd.params.front().first, K, N, true, false, w->data, true);
+                add_param(tn, nd.param("w") ? "w" : nd.params.front().first, K, N, true, true, w->data);
                 if (const HostTensor *b = nd.param("b")) add_param(tn, "b", 1, N, false, false, b->data);
-                tape(tn, "x3", (uint64_t)(M * 3 * K) * 2);
+                tape(tn, "xb", (uint64_t)(M * K) * 2);
                 scratch(tn, "xbt", (uint64_t)(M * K) * 2);
                 if (tn.dyb_ready)  // written by the next Linear's backward (the fused GELU adjoint)
                     request(t, "scratch:" + tn.node->name + ":dyb", (uint64_t)(M * N) * 2, grad_from.at(tn.id),
@@ -642,14 +643,14 @@ static void plan_trainer(Tr &t) {
                 const HostTensor *w1 = host(nd, "w1"), *w3 = host(nd, "w3"), *w2 = host(nd, "w2");
                 CATNN_REQUIRE(w1->numel() == H * I && w3->numel() == H * I && w2->numel() == I * H,
                               CATNN_ERR_SHAPE_MISMATCH, "swiglu weights");
-                add_param(tn, "w1", H, I, true, false, w1->data, true);
-                add_param(tn, "w3", H, I, true, false, w3->data, true);
-                add_param(tn, "w2", I, H, true, false, w2->data, true);
-                tape(tn, "x3", (uint64_t)(M * 3 * H) * 2);
+                add_param(tn, "w1", H, I, true, true, w1->data);
+                add_param(tn, "w3", H, I, true, true, w3->data);
+                add_param(tn, "w2", I, H, true, true, w2->data);
+                tape(tn, "xb", (uint64_t)(M * H) * 2);
                 tape(tn, "a", (uint64_t)(M * I) * 4);
                 tape(tn, "c", (uint64_t)(M * I) * 4);
                 tape(tn, "h", (uint64_t)(M * I) * 4);
-                tape(tn, "h3", (uint64_t)(M * 3 * I) * 2);
+                tape(tn, "hb", (uint64_t)(M * I) * 2);
                 scratch(tn, "dyb", (uint64_t)(M * H) * 2);
                 scratch(tn, "dybt", (uint64_t)(M * H) * 2);
                 scratch(tn, "dh", (uint64_t)(M * I) * 4);
@@ -697,9 +698,9 @@ static void plan_trainer(Tr &t) {
                 const HostTensor *w = host(nd, "w");
                 const int64_t V = nd.op.a[1], K = nd.op.a[0], M = numel(x) / K;
                 CATNN_REQUIRE(w->numel() == V * K, CATNN_ERR_SHAPE_MISMATCH, "lm_head w");
-                add_param(tn, "w", K, V, true, false, param_values(nd, "w"), true);
+                add_param(tn, "w", K, V, true, true, param_values(nd, "w"));
                 tn.params["w"]->transposed = true;
-                tape(tn, "x3", (uint64_t)(M * 3 * K) * 2);
+                tape(tn, "xb", (uint64_t)(M * K) * 2);
                 scratch(tn, "xbt", (uint64_t)(M * K) * 2);
                 scratch(tn, "dyb", (uint64_t)(M * V) * 2);
                 scratch(tn, "dybt", (uint64_t)(M * V) * 2);
@@ -1240,12 +1241,11 @@ static void forward_node(Tr &t, TNode &tn) {
             for (auto &kv : tn.params) if (kv.first != "b") w = kv.second;
             TParam *b = tn.params.count("b") ? tn.params["b"] : nullptr;
             const int64_t K = w->rows, N = w->cols, M = nx / K;
-            // Split-bf16 forward: [hi|lo|hi]·[hi|hi|lo] over 3K ≈ the fp32 product.
-            bf16_t *x3 = (bf16_t *)tn.B("x3");
-            k::split3_rows(s, x, K, M, (int)K, x3, 3 * K);
+            bf16_t *xb = (bf16_t *)tn.B("xb");
+            k::cast_f32_bf16(s, x, xb, M * K);
             k::GemmBf16Params p = gp();
-            p.A = x3; p.lda = 3 * K; p.B = w->bt3; p.ldb = 3 * K;
-            p.M = (int)M; p.N = (int)N; p.K = (int)(3 * K);
+            p.A = xb; p.lda = K; p.B = w->bt; p.ldb = K;
+            p.M = (int)M; p.N = (int)N; p.K = (int)K;
             p.epi = k::EPI_LINEAR; p.bias = b ? b->master : nullptr;
             p.C32 = y; p.ldc32 = N;
             k::gemm_bf16_launch(s, p);
@@ -1253,24 +1253,24 @@ static void forward_node(Tr &t, TNode &tn) {
         }
         case CATNN_OP_SWIGLU: {
             // a = x·w1, c = x·w3 and y = h·w2 with h = silu(a)·c, each GEMM on
-            // split-bf16 operands as Linear's forward.
+            // bf16 operands as Linear's forward.
             TParam *w1 = tn.params["w1"], *w3 = tn.params["w3"], *w2 = tn.params["w2"];
             const int64_t H = w1->rows, I = w1->cols, M = nx / H;
-            bf16_t *x3 = (bf16_t *)tn.B("x3"), *h3 = (bf16_t *)tn.B("h3");
+            bf16_t *xb = (bf16_t *)tn.B("xb"), *hb = (bf16_t *)tn.B("hb");
             float *a = (float *)tn.B("a"), *c = (float *)tn.B("c"), *h = (float *)tn.B("h");
-            auto split_gemm = [&](const bf16_t *A3, int64_t K, const TParam *w, float *C) {
+            auto bf16_gemm = [&](const bf16_t *A, int64_t K, const TParam *w, float *C) {
                 k::GemmBf16Params p = gp();
-                p.A = A3; p.lda = 3 * K; p.B = w->bt3; p.ldb = 3 * K;
-                p.M = (int)M; p.N = (int)w->cols; p.K = (int)(3 * K);
+                p.A = A; p.lda = K; p.B = w->bt; p.ldb = K;
+                p.M = (int)M; p.N = (int)w->cols; p.K = (int)K;
                 p.epi = k::EPI_LINEAR; p.C32 = C; p.ldc32 = w->cols;
                 k::gemm_bf16_launch(s, p);
             };
-            k::split3_rows(s, x, H, M, (int)H, x3, 3 * H);
-            split_gemm(x3, H, w1, a);
-            split_gemm(x3, H, w3, c);
+            k::cast_f32_bf16(s, x, xb, M * H);
+            bf16_gemm(xb, H, w1, a);
+            bf16_gemm(xb, H, w3, c);
             k::swiglu_h(s, a, c, h, M * I);
-            k::split3_rows(s, h, I, M, (int)I, h3, 3 * I);
-            split_gemm(h3, I, w2, y);
+            k::cast_f32_bf16(s, h, hb, M * I);
+            bf16_gemm(hb, I, w2, y);
             break;
         }
         case CATNN_OP_EMBEDDING:  // ids are checked against the vocabulary by set_batch
@@ -1422,7 +1422,7 @@ static void backward_node(Tr &t, TNode &tn) {
             TParam *b = tn.params.count("b") ? tn.params["b"] : nullptr;
             const int64_t K = w->rows, N = w->cols, M = nx / K;
             bf16_t *dyb = (bf16_t *)tn.B("dyb"), *dybt = (bf16_t *)tn.B("dybt");
-            bf16_t *x3 = (bf16_t *)tn.B("x3"), *xbt = (bf16_t *)tn.B("xbt");
+            bf16_t *xb = (bf16_t *)tn.B("xb"), *xbt = (bf16_t *)tn.B("xbt");
             if (!tn.dyb_ready) k::cast_f32_bf16(s, dy, dyb, M * N);
             if (tn.gelu_pre != UINT32_MAX) {
                 // dA = (dy·Wᵀ) ∘ gelu'(A's output): A's cotangent and its bf16 copy.
@@ -1438,7 +1438,7 @@ static void backward_node(Tr &t, TNode &tn) {
                 gemm_nt(s, dyb, N, w->b, N, (int)M, (int)K, (int)N, dst(0), K, !tn.first_writer[0]);
             }
             k::transpose_bf16(s, dyb, N, nullptr, 1, (int)M, (int)N, dybt, M);
-            k::transpose_bf16(s, x3, 3 * K, nullptr, 1, (int)M, (int)K, xbt, M);  // hi part of x
+            k::transpose_bf16(s, xb, K, nullptr, 1, (int)M, (int)K, xbt, M);
             gemm_nt(s, xbt, M, dybt, M, (int)K, (int)N, (int)M, w->grad, N, false, (float *)tn.B("wparts"));
             if (b) k::colsum(s, dy, M, (int)N, b->grad, false, (float *)tn.B("colsum"));
             break;
@@ -1448,8 +1448,8 @@ static void backward_node(Tr &t, TNode &tn) {
             const int64_t H = w1->rows, I = w1->cols, M = nx / H;
             bf16_t *dyb = (bf16_t *)tn.B("dyb"), *dybt = (bf16_t *)tn.B("dybt"), *dab = (bf16_t *)tn.B("dab"),
                    *dcb = (bf16_t *)tn.B("dcb"), *dabt = (bf16_t *)tn.B("dabt"), *dcbt = (bf16_t *)tn.B("dcbt"),
-                   *xbt = (bf16_t *)tn.B("xbt"), *hbt = (bf16_t *)tn.B("hbt"), *x3 = (bf16_t *)tn.B("x3"),
-                   *h3 = (bf16_t *)tn.B("h3");
+                   *xbt = (bf16_t *)tn.B("xbt"), *hbt = (bf16_t *)tn.B("hbt"), *xb = (bf16_t *)tn.B("xb"),
+                   *hb = (bf16_t *)tn.B("hb");
             float *dh = (float *)tn.B("dh"), *wparts = (float *)tn.B("wparts");
             k::cast_f32_bf16(s, dy, dyb, M * H);
             gemm_nt(s, dyb, H, w2->b, H, (int)M, (int)I, (int)H, dh, I, false);  // dh = dy·w2ᵀ
@@ -1458,12 +1458,12 @@ static void backward_node(Tr &t, TNode &tn) {
                 gemm_nt(s, dab, I, w1->b, I, (int)M, (int)H, (int)I, dst(0), H, !tn.first_writer[0]);
                 gemm_nt(s, dcb, I, w3->b, I, (int)M, (int)H, (int)I, dst(0), H, true);
             }
-            k::transpose_bf16(s, x3, 3 * H, nullptr, 1, (int)M, (int)H, xbt, M);  // hi part of x
+            k::transpose_bf16(s, xb, H, nullptr, 1, (int)M, (int)H, xbt, M);
             k::transpose_bf16(s, dab, I, nullptr, 1, (int)M, (int)I, dabt, M);
             k::transpose_bf16(s, dcb, I, nullptr, 1, (int)M, (int)I, dcbt, M);
             gemm_nt(s, xbt, M, dabt, M, (int)H, (int)I, (int)M, w1->grad, I, false, wparts);  // dw1 = xᵀ·da
             gemm_nt(s, xbt, M, dcbt, M, (int)H, (int)I, (int)M, w3->grad, I, false, wparts);  // dw3 = xᵀ·dc
-            k::transpose_bf16(s, h3, 3 * I, nullptr, 1, (int)M, (int)I, hbt, M);  // hi part of h
+            k::transpose_bf16(s, hb, I, nullptr, 1, (int)M, (int)I, hbt, M);
             k::transpose_bf16(s, dyb, H, nullptr, 1, (int)M, (int)H, dybt, M);
             gemm_nt(s, hbt, M, dybt, M, (int)I, (int)H, (int)M, w2->grad, H, false, wparts);  // dw2 = hᵀ·dy
             break;

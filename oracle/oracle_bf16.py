@@ -59,11 +59,12 @@ def bf16_split(a):
 
 
 SITES = ("linear_fwd", "linear_bwd", "attn_fwd", "attn_bwd", "moe_fwd", "moe_bwd")
-# The GPU trainer's policy: split-bf16 forward GEMMs for Linear and attention
-# (hi·hi + hi·lo + lo·hi); the MoE gate/up GEMM with its input split and the
-# expert weights rounded ("xsplit": (hi + lo)·bf16(w)); plain bf16 operands
-# for the rest of the MoE experts and every backward GEMM.
-DEVICE = {"linear_fwd": "split", "attn_fwd": "split", "linear_bwd": "bf16", "attn_bwd": "bf16",
+# The GPU trainer's policy: split-bf16 forward GEMMs for the attention
+# projections (hi·hi + hi·lo + lo·hi); the MoE gate/up GEMM with its input
+# split and the expert weights rounded ("xsplit": (hi + lo)·bf16(w)); plain
+# bf16 operands for Linear, the rest of the MoE experts and every backward
+# GEMM.
+DEVICE = {"linear_fwd": "bf16", "attn_fwd": "split", "linear_bwd": "bf16", "attn_bwd": "bf16",
           "moe_fwd": "xsplit", "moe_bwd": "bf16"}
 WIDE = {site: "wide" for site in SITES}
 BF16 = {site: "bf16" for site in SITES}
