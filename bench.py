@@ -107,7 +107,7 @@ def time_train_step(dev, steps, warmup, opt="sgd"):
             "arena_reserved_bytes": reserved, "arena_buffers": len(allocs),
             "precision": "bf16 MFMA, fp32 accumulation and master weights; split-bf16 forward "
                          "GEMMs for the attention projections, split-bf16 input to the MoE gate/up "
-                         "GEMM; attention core fp32 MFMA"}
+                         "GEMM; attention core on bf16 MFMA with normalised P rounded to bf16"}
 
 
 def time_mixtral(dev, steps, warmup):

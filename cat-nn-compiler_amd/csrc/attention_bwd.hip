@@ -514,6 +514,14 @@ bool al16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 }  // namespace
 
+void attention_rowdot(hipStream_t s, const float *o, const float *dout, int64_t ld, int64_t rows, int64_t n_heads,
+                      int64_t d_head, float *D) {
+    if (rows == 0) return;
+    attn_dot_kernel<<<(unsigned)((rows * n_heads + 3) / 4), 256, 0, s>>>(o, dout, ld, rows, (int)n_heads,
+                                                                        (int)d_head, D);
+    CATNN_HIP(hipGetLastError());
+}
+
 uint64_t attention_bwd_scratch_bytes(int64_t batch, int64_t seq, int64_t n_heads) {
     return (uint64_t)(batch * seq * n_heads) * 4;
 }

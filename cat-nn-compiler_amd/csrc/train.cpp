@@ -28,9 +28,10 @@
 // weights' hi|hi, 2K: x at split precision, the expert weights rounded
 // once), because the rounding of its input reaches the router's gradient;
 // the rest of the MoE expert forward and every backward GEMM take plain
-// bf16 operands.  Master weights, the residual stream, LayerNorm, softmax
-// statistics, the router and all cotangent accumulation stay fp32; the
-// attention core runs on fp32 MFMA.
+// bf16 operands.  The attention core (d_head 64) runs on bf16 MFMA with
+// q, k, v, the normalised P, dO and dS rounded (attention_bf16.hip); other
+// head sizes on fp32 MFMA.  Master weights, the residual stream, LayerNorm,
+// softmax statistics, the router and all cotangent accumulation stay fp32.
 //
 // Memory: every buffer (params, their bf16 copies and gradients, values,
 // cotangents, tapes, scratch) is a BufferReq on the reference's logical
@@ -63,6 +64,12 @@ int64_t numel(const std::vector<int64_t> &d) {
 }
 
 constexpr int kPad = 128;  // MoE expert segments start on multiples of the GEMM tile
+
+// The bf16 step runs an Attention node's core on bf16 MFMA (attention_bf16.hip)
+// where that kernel covers its head size; q, k, v then live as bf16.
+bool attn_core_bf16(const Node &nd, int64_t D) {
+    return nd.op.kind == CATNN_OP_ATTENTION && k::attention_bf16_supported(nd.op.a[2], 3 * D);
+}
 
 struct TParam {
     std::string name;       // "param:{node}:{port}"
@@ -721,7 +728,15 @@ static void plan_trainer(Tr &t) {
                 add_param(tn, "wqkv", D, 3 * D, true, false, param_values(nd, "wqkv"), true);
                 add_param(tn, "wo", D, D, true, false, host(nd, "wo")->data, true);
                 tape(tn, "x3", (uint64_t)(T * 3 * D) * 2);
-                tape(tn, "qkv", (uint64_t)(T * 3 * D) * 4);
+                if (attn_core_bf16(nd, D)) {
+                    const uint64_t Sp = (uint64_t)k::attention_bf16_seq_pad(S);
+                    tape(tn, "qkvb", (uint64_t)(T * 3 * D) * 2);
+                    tape(tn, "qkvt", (uint64_t)(Bt * 3 * D) * Sp * 2);
+                    scratch(tn, "dctxb", (uint64_t)(T * D) * 2);
+                    scratch(tn, "dctxt", (uint64_t)(Bt * D) * Sp * 2);
+                } else {
+                    tape(tn, "qkv", (uint64_t)(T * 3 * D) * 4);
+                }
                 tape(tn, "ctx", (uint64_t)(T * D) * 4);
                 tape(tn, "ctx3", (uint64_t)(T * 3 * D) * 2);
                 tape(tn, "lse", (uint64_t)(T * H) * 4);
@@ -1298,13 +1313,27 @@ static void forward_node(Tr &t, TNode &tn) {
             const int64_t H = nd.op.a[0], dh = nd.op.a[2];
             const bool causal = (nd.op.flags & CATNN_FLAG_CAUSAL) != 0;
             bf16_t *x3 = (bf16_t *)tn.B("x3"), *ctx3 = (bf16_t *)tn.B("ctx3");
-            float *qkv = (float *)tn.B("qkv"), *ctx = (float *)tn.B("ctx");
-            // Both projections split-bf16 (K' = 3D), the core on fp32 MFMA.
+            float *ctx = (float *)tn.B("ctx");
+            // Both projections split-bf16 (K' = 3D).
             k::split3_rows(s, x, D, T, (int)D, x3, 3 * D);
-            gemm_nt(s, x3, 3 * D, tn.params["wqkv"]->bt3, 3 * D, (int)T, (int)(3 * D), (int)(3 * D), qkv, 3 * D,
-                    false);
-            k::attention_core_fwd_lse(s, qkv, qkv + D, qkv + 2 * D, 3 * D, ctx, D, (float *)tn.B("lse"), Bt,
-                                      S, H, dh, causal);
+            if (attn_core_bf16(nd, D)) {
+                // q, k, v in bf16 (and transposed per batch element) for the
+                // core on bf16 MFMA.
+                bf16_t *qkvb = (bf16_t *)tn.B("qkvb"), *qkvt = (bf16_t *)tn.B("qkvt");
+                k::GemmBf16Params p = gp();
+                p.A = x3; p.lda = 3 * D; p.B = tn.params["wqkv"]->bt3; p.ldb = 3 * D;
+                p.M = (int)T; p.N = (int)(3 * D); p.K = (int)(3 * D);
+                p.epi = k::EPI_STORE; p.Cb = qkvb; p.ldcb = 3 * D;
+                k::gemm_bf16_launch(s, p);
+                k::transpose_bt(s, qkvb, 3 * D, Bt, S, 3 * D, qkvt);
+                k::attention_core_fwd_bf16(s, qkvb, 3 * D, qkvt, ctx, D, (float *)tn.B("lse"), Bt, S, H, causal);
+            } else {
+                float *qkv = (float *)tn.B("qkv");
+                gemm_nt(s, x3, 3 * D, tn.params["wqkv"]->bt3, 3 * D, (int)T, (int)(3 * D), (int)(3 * D), qkv,
+                        3 * D, false);
+                k::attention_core_fwd_lse(s, qkv, qkv + D, qkv + 2 * D, 3 * D, ctx, D, (float *)tn.B("lse"), Bt,
+                                          S, H, dh, causal);
+            }
             k::split3_rows(s, ctx, D, T, (int)D, ctx3, 3 * D);
             gemm_nt(s, ctx3, 3 * D, tn.params["wo"]->bt3, 3 * D, (int)T, (int)D, (int)(3 * D), y, D, false);
             break;
@@ -1506,15 +1535,31 @@ static void backward_node(Tr &t, TNode &tn) {
             float *dctx = (float *)tn.B("dctx"), *dqkv = (float *)tn.B("dqkv");
             bf16_t *dqkvb = (bf16_t *)tn.B("dqkvb"), *dqkvt = (bf16_t *)tn.B("dqkvt");
             bf16_t *x3 = (bf16_t *)tn.B("x3"), *xbt = (bf16_t *)tn.B("xbt");
-            float *qkv = (float *)tn.B("qkv");
+            const bool core_bf16 = attn_core_bf16(nd, D);
             k::cast_f32_bf16(s, dy, dyb, T * D);
-            gemm_nt(s, dyb, D, wo->b, D, (int)T, (int)D, (int)D, dctx, D, false);
+            {  // dctx = dy·woᵀ (and its bf16 copy for the bf16 core)
+                k::GemmBf16Params p = gp();
+                p.A = dyb; p.lda = D; p.B = wo->b; p.ldb = D;
+                p.M = (int)T; p.N = (int)D; p.K = (int)D;
+                p.epi = k::EPI_STORE; p.C32 = dctx; p.ldc32 = D;
+                if (core_bf16) { p.Cb = (bf16_t *)tn.B("dctxb"); p.ldcb = D; }
+                k::gemm_bf16_launch(s, p);
+            }
             k::transpose_bf16(s, dyb, D, nullptr, 1, (int)T, (int)D, dybt, T);
             k::transpose_bf16(s, (bf16_t *)tn.B("ctx3"), 3 * D, nullptr, 1, (int)T, (int)D, ctxt, T);
             gemm_nt(s, ctxt, T, dybt, T, (int)D, (int)D, (int)T, wo->grad, D, false, (float *)tn.B("wparts"));
-            k::attention_core_bwd(s, qkv, qkv + D, qkv + 2 * D, 3 * D, (float *)tn.B("ctx"), dctx, D,
-                                  (float *)tn.B("lse"), dqkv, dqkv + D, dqkv + 2 * D, 3 * D, Bt, S, H, dh,
-                                  causal, (float *)tn.B("dscr"));
+            if (core_bf16) {
+                bf16_t *dctxb = (bf16_t *)tn.B("dctxb"), *dctxt = (bf16_t *)tn.B("dctxt");
+                k::transpose_bt(s, dctxb, D, Bt, S, D, dctxt);
+                k::attention_core_bwd_bf16(s, (bf16_t *)tn.B("qkvb"), 3 * D, (bf16_t *)tn.B("qkvt"),
+                                           (float *)tn.B("ctx"), dctx, D, dctxb, dctxt, (float *)tn.B("lse"), dqkv,
+                                           3 * D, Bt, S, H, causal, (float *)tn.B("dscr"));
+            } else {
+                float *qkv = (float *)tn.B("qkv");
+                k::attention_core_bwd(s, qkv, qkv + D, qkv + 2 * D, 3 * D, (float *)tn.B("ctx"), dctx, D,
+                                      (float *)tn.B("lse"), dqkv, dqkv + D, dqkv + 2 * D, 3 * D, Bt, S, H, dh,
+                                      causal, (float *)tn.B("dscr"));
+            }
             k::cast_f32_bf16(s, dqkv, dqkvb, T * 3 * D);
             if (dst(0))
                 gemm_nt(s, dqkvb, 3 * D, wqkv->b, 3 * D, (int)T, (int)D, (int)(3 * D), dst(0), D,

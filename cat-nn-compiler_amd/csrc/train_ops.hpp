@@ -159,6 +159,28 @@ void attention_core_bwd(hipStream_t s, const float *q, const float *k, const flo
                         const float *o, const float *dout, int64_t ldo, const float *lse,
                         float *dq, float *dk, float *dv, int64_t ld_d, int64_t batch, int64_t seq,
                         int64_t n_heads, int64_t d_head, bool causal, float *scratch);
+// D[row·n_heads + h] = Σ_d o·dout over head h (rows of stride ld).
+void attention_rowdot(hipStream_t s, const float *o, const float *dout, int64_t ld, int64_t rows, int64_t n_heads,
+                      int64_t d_head, float *D);
+// The attention core on bf16 MFMA (attention_bf16.hip), d_head 64, one K/V
+// head per query head.  qkv: bf16 rows [q | k | v] of stride ld (n_heads·64
+// each); qkvt: its transpose per batch element from transpose_bt (3·n_heads·64
+// features × attention_bf16_seq_pad(seq)).  The forward writes ctx (fp32)
+// and lse (log2 domain, as attention_core_fwd_lse); the adjoint takes ctx,
+// dctx (fp32, stride ldo), dctx's bf16 copy dctxb (stride ldo) and its
+// transpose dctxt (n_heads·64 features) and writes dq | dk | dv (fp32) into
+// the columns of dqkv (stride ldd); scratch: attention_bwd_scratch_bytes.
+bool attention_bf16_supported(int64_t d_head, int64_t ld);
+int64_t attention_bf16_seq_pad(int64_t seq);
+// y[b][f][s] = x[b·seq + s][f] for f < F, s < attention_bf16_seq_pad(seq),
+// zero for s ≥ seq.
+void transpose_bt(hipStream_t s, const bf16_t *x, int64_t ldx, int64_t batch, int64_t seq, int64_t F, bf16_t *y);
+void attention_core_fwd_bf16(hipStream_t s, const bf16_t *qkv, int64_t ld, const bf16_t *qkvt, float *ctx,
+                             int64_t ldo, float *lse, int64_t batch, int64_t seq, int64_t n_heads, bool causal);
+void attention_core_bwd_bf16(hipStream_t s, const bf16_t *qkv, int64_t ld, const bf16_t *qkvt, const float *ctx,
+                             const float *dctx, int64_t ldo, const bf16_t *dctxb, const bf16_t *dctxt,
+                             const float *lse, float *dqkv, int64_t ldd, int64_t batch, int64_t seq,
+                             int64_t n_heads, bool causal, float *scratch);
 // Grouped-query forms (GqaAttention, always causal in the forward; window >
 // 0: query i sees keys [i − window + 1, i]): q (and dq) rows of stride ldq
 // hold n_heads heads, k, v (and dk, dv) rows of stride ldk hold

@@ -5,8 +5,10 @@ MSE, crates/catnn-compile/src/pipeline.rs:476-547; the adjoints of
 adjoint.rs:762-951), evaluated in float64 numpy with the GPU trainer's
 declared rounding points (DEVICE): GEMM operands are rounded to bfloat16
 (round to nearest even) or split into bf16 hi/lo pairs exactly where the
-device does so, and nothing else is rounded — accumulation, LayerNorm,
-activations, the attention core, the router and cotangent sums stay wide.
+device does so (the attention core's products included: q, k, v, the
+normalised softmax P, dO and dS), and nothing else is rounded —
+accumulation, LayerNorm, activations, the softmax statistics, the router
+and cotangent sums stay wide.
 MoE routing is the reference's own fp32 router (oracle.route) on the fp32
 router input, as on the device.
 
@@ -58,14 +60,15 @@ def bf16_split(a):
     return hi, bf16_round(np.asarray(a, np.float32) - hi.astype(np.float32))
 
 
-SITES = ("linear_fwd", "linear_bwd", "attn_fwd", "attn_bwd", "moe_fwd", "moe_bwd")
+SITES = ("linear_fwd", "linear_bwd", "attn_fwd", "attn_bwd", "attn_core", "moe_fwd", "moe_bwd")
 # The GPU trainer's policy: split-bf16 forward GEMMs for the attention
 # projections (hi·hi + hi·lo + lo·hi); the MoE gate/up GEMM with its input
 # split and the expert weights rounded ("xsplit": (hi + lo)·bf16(w)); plain
 # bf16 operands for Linear, the rest of the MoE experts and every backward
-# GEMM.
+# GEMM; the attention core's products on bf16 operands (attn_core: q, k, v,
+# the normalised P, dO and dS rounded).
 DEVICE = {"linear_fwd": "bf16", "attn_fwd": "split", "linear_bwd": "bf16", "attn_bwd": "bf16",
-          "moe_fwd": "xsplit", "moe_bwd": "bf16"}
+          "attn_core": "bf16", "moe_fwd": "xsplit", "moe_bwd": "bf16"}
 WIDE = {site: "wide" for site in SITES}
 BF16 = {site: "bf16" for site in SITES}
 
@@ -80,6 +83,13 @@ class Model:
         if self.policy.get(self.site, "wide") == "wide":
             return np.asarray(a, F64)
         return bf16_round(a)
+
+    def core_rb(self, dh):
+        """Operand rounding of the attention core's products (site attn_core;
+        the device's bf16 core covers d_head 64, other head sizes stay fp32)."""
+        if self.policy.get("attn_core", "wide") == "bf16" and dh == 64:
+            return bf16_round
+        return lambda a: np.asarray(a, F64)
 
     def mm(self, a, b):
         if self.policy.get(self.site, "wide") == "split":
@@ -123,12 +133,13 @@ class Model:
             wqkv = np.concatenate([P["wq"], P["wk"], P["wv"]], 1)
             qkv = self.mm(x.reshape(-1, D), wqkv).reshape(B, S, 3, heads, dh)
             q, k, v = (qkv[:, :, i].transpose(0, 2, 1, 3) for i in range(3))  # [B,H,S,dh]
-            s = q @ k.transpose(0, 1, 3, 2) / np.sqrt(dh)
+            core = self.core_rb(dh)
+            s = core(q) @ core(k).transpose(0, 1, 3, 2) / np.sqrt(dh)
             if node.op.flags & 1:
                 s = np.where(np.tril(np.ones((S, S), bool)), s, -np.inf)
             p = np.exp(s - s.max(-1, keepdims=True))
             p /= p.sum(-1, keepdims=True)
-            ctx = (p @ v).transpose(0, 2, 1, 3).reshape(B * S, D)
+            ctx = (core(p) @ core(v)).transpose(0, 2, 1, 3).reshape(B * S, D)
             y = self.mm(ctx, P["wo"])
             return y.reshape(B, S, D), (q, k, v, p, ctx, wqkv)
         if kind == "moe":
@@ -197,10 +208,16 @@ class Model:
             dyb = rb(dy.reshape(-1, D))
             dwo = rb(ctx).T @ dyb
             dctx = (dyb @ rb(P["wo"]).T).reshape(B, S, heads, dh).transpose(0, 2, 1, 3)
-            dv = p.transpose(0, 1, 3, 2) @ dctx
-            dp = dctx @ v.transpose(0, 1, 3, 2)
-            ds = p * (dp - (dp * p).sum(-1, keepdims=True)) / np.sqrt(dh)
-            dq, dk = ds @ k, ds.transpose(0, 1, 3, 2) @ q
+            # D_i = Σ_d dO·O over the forward's context, as the device takes it
+            # (equal to Σ_j dP·P when nothing is rounded); dS is rounded before
+            # the 1/√dh scale.
+            core = self.core_rb(dh)
+            D_ = (dctx * ctx.reshape(B, S, heads, dh).transpose(0, 2, 1, 3)).sum(-1)[..., None]
+            dv = core(p).transpose(0, 1, 3, 2) @ core(dctx)
+            dp = core(dctx) @ core(v).transpose(0, 1, 3, 2)
+            ds = core(p * (dp - D_))
+            dq = ds @ core(k) / np.sqrt(dh)
+            dk = ds.transpose(0, 1, 3, 2) @ core(q) / np.sqrt(dh)
             dqkv = np.stack([t.transpose(0, 2, 1, 3) for t in (dq, dk, dv)], 2).reshape(-1, 3 * D)
             dqkvb = rb(dqkv)
             dx = (dqkvb @ rb(wqkv).T).reshape(x.shape)

@@ -31,6 +31,13 @@ TIGHT = 2e-3      # device vs the bf16-rounding model of the same step
 # (perturbing the input by 1e-6, relative, moves the model's gradients by at
 # most 1.1e-5), so they are held to TIGHT as well.
 TIGHT_CONFIG5 = TIGHT
+# Where the attention core runs on bf16 MFMA (d_head 64), its rounding points
+# (q, k, v, P, dO, dS) make the model itself noisy at the fp32 level: a 1e-7
+# relative perturbation of the input moves the model's own attention-weight
+# gradients by 1.9e-3 (against 5e-4 with the core wide), so the device, whose
+# fp32 arithmetic differs from the model's float64 by about that much, is
+# held to twice that floor on such graphs.
+TIGHT_BF16_CORE = 4e-3
 BF16_TOL = 1e-2   # device (bf16 GEMM operands) vs the fp32 reference step
 LOSS_TOL = 2e-3
 
@@ -45,6 +52,8 @@ def _shape(g, nid, port):
 
 def _check_step(device, g, x, tgt, lr=0.05, fp32_tol=BF16_TOL, tight=TIGHT):
     """One step on the device and on both CPU restatements."""
+    if any(n.op.kind == "attention" and n.op.fields[2] == 64 for n in g.nodes.values()):
+        tight = max(tight, TIGHT_BF16_CORE)
     print(f"[train] {g.name} x={x.ty.shape}", flush=True)
     tr = Trainer(device, g, lr)
     tr.set_batch(x, tgt)
