@@ -24,8 +24,9 @@
 // j (j < 4), 16u + 8 + 4g + (j − 4) (j ≥ 4) for k step u; the other operand
 // then comes from a transposed tile whose 16-byte chunks are stored in that
 // order (TTile).  Every LDS tile row is 64 bf16 (128 bytes) with
-// chunk c at position c ^ (row mod 8), so the 16-byte operand reads of 8
-// consecutive rows fall on distinct banks.
+// chunk c at position c ^ ((row / 2) mod 8): a 16-byte read serves 16 lanes
+// per cycle from one 256-byte window of gfx950's 64 banks, and the 16
+// consecutive rows of one chunk then fall on distinct banks.
 //
 // Transposed copies: xt[b][f][s] (transpose_bt) for f < F features of
 // batch element b, s < Sp = S rounded up to 64, zero for s ≥ S, so that
@@ -54,7 +55,7 @@ constexpr int TILE_BYTES = 64 * ROWB;    // one 64 × 64 bf16 tile
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-__device__ __forceinline__ int chunk_pos(int row, int c) { return row * ROWB + ((c ^ (row & 7)) << 4); }
+__device__ __forceinline__ int chunk_pos(int row, int c) { return row * ROWB + ((c ^ ((row >> 1) & 7)) << 4); }
 
 __device__ __forceinline__ bf16x8 lds_frag(const unsigned char *tile, int row, int c) {
     return *reinterpret_cast<const bf16x8 *>(tile + chunk_pos(row, c));

@@ -56,12 +56,15 @@ using Cfg2 = Cfg<128, 128, 2, 2, 64>;
 // into LDS by global_load_lds_dwordx4 without passing through registers,
 // STAGES chunks deep.  One such load fills 1 KiB of LDS contiguously, lane
 // l at byte 16·l, so rows are 128 bytes (8 chunks of 8 k values) with no
-// padding; a row's chunk c sits at position c ^ (row mod 8), which keeps the
-// MFMA operand reads (8 rows × one chunk per 8 lanes) on distinct banks.
+// padding.  gfx950's LDS has 64 banks: a 16-byte operand read serves 16
+// lanes per cycle from one 256-byte bank window, i.e. 16 consecutive rows
+// of one chunk, two rows per window.  Chunk c of row r therefore sits at
+// position c ^ ((r / 2) mod 8): the 8 even and the 8 odd rows of any 16
+// each cover the 8 positions, so the 16 reads fall on distinct banks.
+// (Swizzling by r mod 8 leaves rows r and r + 8 on the same banks.)
 //
-// With BK = 32 rows are 64 bytes (4 chunks) and a wave load fills 16 rows;
-// chunk c of row r then sits at c ^ ((r / 2) mod 4), again one bank group per
-// lane for 8 consecutive rows.
+// With BK = 32 rows are 64 bytes (4 chunks, four rows per window) and a
+// wave load fills 16 rows; chunk c of row r sits at c ^ ((r / 4) mod 4).
 template <int BM_, int BN_, int WAVES_M_, int WAVES_N_, int STAGES_, int BK_ = 64>
 struct DCfg {
     static constexpr bool DMA = true;
@@ -75,7 +78,7 @@ struct DCfg {
     // wave loads (RPL rows each) per wavefront and k chunk
     static constexpr int A_LD = BM / (RPL * NW), B_LD = BN / (RPL * NW), LPC = A_LD + B_LD;
     // chunk position swizzle of row r
-    static __device__ __forceinline__ int sw(int r) { return CPR == 8 ? (r & 7) : ((r >> 1) & (CPR - 1)); }
+    static __device__ __forceinline__ int sw(int r) { return CPR == 8 ? ((r >> 1) & 7) : ((r >> 2) & 3); }
     static_assert(BK == 64 || BK == 32, "k chunk");
     static_assert(FM >= 1 && FN >= 1 && FM * 32 * WAVES_M == BM && FN * 32 * WAVES_N == BN, "tile");
     static_assert(A_LD >= 1 && B_LD >= 1 && A_LD * RPL * NW == BM && B_LD * RPL * NW == BN, "load split");
@@ -84,10 +87,14 @@ struct DCfg {
 };
 
 // 128 × 128 tiles of four 64 × 64 wavefronts: two stages (64 KiB, two
-// blocks per CU) or three (96 KiB).  A sweep over the training shapes also
+// blocks per CU) or three (96 KiB).  Sweeps over the training shapes also
 // tried 256 × 128 tiles of eight wavefronts (three stages), 256 × 128 of four
 // 128 × 64 wavefronts and 256 × 256 of eight 128 × 64 wavefronts: those won
-// only on 8192³ (1067 against 981 TFLOP/s) and lost on the rest.
+// only on 8192³ (1067 against 981 TFLOP/s) and lost on the rest.  With the
+// 64-bank swizzle, 256 × 128 and 128 × 256 tiles of four or eight
+// wavefronts in three 48 KiB stages, also with the fragments of the next k
+// step read during the current step's MFMAs, stayed at 0.8–1.0× of this
+// tile on every training shape.
 using Cfg7 = DCfg<128, 128, 2, 2, 2>;
 using Cfg9 = DCfg<128, 128, 2, 2, 3>;
 using Cfg10 = DCfg<128, 128, 2, 2, 4, 32>;  // 32-deep chunks, four stages in the same 64 KiB
@@ -611,28 +618,30 @@ __device__ __forceinline__ void tile_dma(unsigned char *smem, const GemmBf16Para
     const int wm = wave / C::WAVES_N, wn = wave % C::WAVES_N;
     const int lr = lane & 31, lg = lane >> 5;
 
-    // Wave load q of a wavefront fills tile rows 8·(wave·LD + q) … +7: lane l
-    // row … + l/8 at position l mod 8, i.e. k chunk (l mod 8) ^ (l/8).  Rows
-    // past the tile's end read row row0 (col0 for B): their outputs are never
-    // stored.
+    // Wave load q of a wavefront fills tile rows RPL·(wave·LD + q) … +RPL−1:
+    // lane l row … + l/CPR at position l mod CPR, i.e. k chunk
+    // (l mod CPR) ^ sw(row).  Rows past the tile's end read row row0 (col0
+    // for B): their outputs are never stored.  (B rows start at BM, a
+    // multiple of 32, so their swizzle is that of their row within B.)
     constexpr int CPR = C::CPR, RPL = C::RPL, ROWB = C::ROWB;
     const int lrow = lane / CPR, lpos = lane % CPR;
-    const int dk = (lpos ^ C::sw(lrow)) * 8;  // wave-load rows start on multiples of RPL
     const bf16_t *a_src[C::A_LD];
 #pragma unroll
     for (int q = 0; q < C::A_LD; ++q) {
-        int gr = row0 + (wave * C::A_LD + q) * RPL + lrow;
+        const int r = (wave * C::A_LD + q) * RPL + lrow;
+        int gr = row0 + r;
         if (gr >= row_end) gr = row0;
         const int src = p.a_rows ? p.a_rows[gr] / p.a_row_div : gr;
-        a_src[q] = p.A + (int64_t)src * p.lda + dk;
+        a_src[q] = p.A + (int64_t)src * p.lda + (lpos ^ C::sw(r)) * 8;
     }
     const bf16_t *b_src[C::B_LD];
 #pragma unroll
     for (int q = 0; q < C::B_LD; ++q) {
+        const int r = (wave * C::B_LD + q) * RPL + lrow;
         int n;
-        const bf16_t *base = b_row_src((wave * C::B_LD + q) * RPL + lrow, n);
+        const bf16_t *base = b_row_src(r, n);
         if (n >= p.N) n = col0;
-        b_src[q] = base + (int64_t)n * p.ldb + dk;
+        b_src[q] = base + (int64_t)n * p.ldb + (lpos ^ C::sw(r)) * 8;
     }
     const uint32_t lds0 = lds_addr(smem);
     auto issue = [&](int kt) {
@@ -727,7 +736,7 @@ __device__ __forceinline__ void tile_dma(unsigned char *smem, const GemmBf16Para
                                    e[4] | (uint32_t)e[5] << 16, e[6] | (uint32_t)e[7] << 16);
                 }
             }
-            // B rows start at BM, a multiple of 8: the same swizzle as row r − BM
+            // B rows start at BM, a multiple of 32: the same swizzle as row r − BM
             *reinterpret_cast<uint4 *>(smem + r * ROWB + ((c ^ C::sw(r)) << 4)) = v;
         }
         dma_sync<0>();
