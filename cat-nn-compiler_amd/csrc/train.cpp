@@ -76,6 +76,11 @@ struct TParam {
     int64_t rows = 0, cols = 0;
     std::vector<float> init;  // host values uploaded at install
     bool want_b = false, want_bt = false, want_bt3 = false;
+    // Row stride of the bf16 copy b (0: cols).  b_with: b lives inside that
+    // parameter's copy, b_col columns in (MoE w1 | w3 rows side by side, the
+    // B operand of one input-gradient GEMM over both).
+    int64_t b_ld = 0, b_col = 0;
+    TParam *b_with = nullptr;
     float *master = nullptr, *grad = nullptr;
     float *m = nullptr, *v = nullptr;  // Adam moments "adam:{node}:{port}:m|v"
     bf16_t *b = nullptr, *bt = nullptr;
@@ -449,7 +454,8 @@ static void plan_trainer(Tr &t) {
     request(t, "loss", 256, n, upd, reinterpret_cast<void **>(&t.loss));
 
     auto add_param = [&](TNode &tn, const std::string &port, int64_t rows, int64_t cols, bool b, bool bt,
-                         std::vector<float> init, bool bt3 = false) {
+                         std::vector<float> init, bool bt3 = false, int64_t b_ld = 0, TParam *b_with = nullptr,
+                         int64_t b_col = 0) {
         auto p = std::make_unique<TParam>();
         p->name = "param:" + tn.node->name + ":" + port;
         p->rows = rows;
@@ -463,13 +469,18 @@ static void plan_trainer(Tr &t) {
             p->want_b = p->want_bt = p->want_bt3 = false;
         }
         const uint64_t e = (uint64_t)(rows * cols);
+        p->b_ld = b_ld;
+        p->b_with = b_with;
+        p->b_col = b_col;
         request(t, p->name, e * 4, 0, upd, reinterpret_cast<void **>(&p->master));
         request(t, "grad:" + p->name, e * 4, bwd(tn.tick), upd, reinterpret_cast<void **>(&p->grad));
         if (t.opt == CATNN_OPT_ADAM)  // pipeline.rs:366-376
             for (const char *mom : {"m", "v"})
                 request(t, "adam:" + tn.node->name + ":" + port + ":" + mom, e * 4, 0, upd,
                         reinterpret_cast<void **>(mom[0] == 'm' ? &p->m : &p->v));
-        if (p->want_b) request(t, "bf16:" + p->name, e * 2, 0, upd, reinterpret_cast<void **>(&p->b));
+        if (p->want_b && !p->b_with)
+            request(t, "bf16:" + p->name, (uint64_t)(rows * (b_ld ? b_ld : cols)) * 2, 0, upd,
+                    reinterpret_cast<void **>(&p->b));
         if (p->want_bt) request(t, "bf16t:" + p->name, e * 2, 0, upd, reinterpret_cast<void **>(&p->bt));
         if (p->want_bt3) request(t, "bf16t3:" + p->name, e * 6, 0, upd, reinterpret_cast<void **>(&p->bt3));
         if (p->want_b6) request(t, "bf16x6:" + p->name, e * 12, 0, upd, reinterpret_cast<void **>(&p->b6));
@@ -784,8 +795,10 @@ static void plan_trainer(Tr &t) {
                 add_param(tn, "gate", H, E, false, false, host(nd, "gate")->data);
                 for (int64_t e = 0; e < E; ++e) {
                     const std::string p = "e" + std::to_string(e);
-                    add_param(tn, p + ".w1", H, I, true, false, host(nd, p + ".w1")->data, true);
-                    add_param(tn, p + ".w3", H, I, true, false, host(nd, p + ".w3")->data, true);
+                    // w1's bf16 copy holds [w1 | w3] per row: the B operand of dx = [da | dc]·[w1 | w3]ᵀ.
+                    add_param(tn, p + ".w1", H, I, true, false, host(nd, p + ".w1")->data, true, 2 * I);
+                    add_param(tn, p + ".w3", H, I, true, false, host(nd, p + ".w3")->data, true, 2 * I,
+                              tn.params[p + ".w1"], I);
                     add_param(tn, p + ".w2", I, H, true, true, host(nd, p + ".w2")->data);
                 }
                 const int64_t max_tiles = (T * K + k::gemm_bf16_tile_rows() - 1) / k::gemm_bf16_tile_rows() + E;
@@ -804,14 +817,12 @@ static void plan_trainer(Tr &t) {
                 tape(tn, "ys", (uint64_t)(Pr * H) * 4);
                 scratch(tn, "dys", (uint64_t)(Pr * H) * 2);
                 scratch(tn, "dw", (uint64_t)(T * K) * 4);
-                scratch(tn, "da", (uint64_t)(Pr * I) * 2);
-                scratch(tn, "dc", (uint64_t)(Pr * I) * 2);
+                scratch(tn, "dadc", (uint64_t)(Pr * 2 * I) * 2);  // [da | dc] per slot row
                 scratch(tn, "dxs", (uint64_t)(Pr * H) * 4);
                 scratch(tn, "xpt", (uint64_t)(H * Pr) * 2);
                 scratch(tn, "ht", (uint64_t)(I * Pr) * 2);
                 scratch(tn, "dyst", (uint64_t)(H * Pr) * 2);
-                scratch(tn, "dat", (uint64_t)(I * Pr) * 2);
-                scratch(tn, "dct", (uint64_t)(I * Pr) * 2);
+                scratch(tn, "dadct", (uint64_t)(2 * I * Pr) * 2);
                 scratch(tn, "dl", (uint64_t)(T * E) * 4);
                 scratch(tn, "router", k::router_backward_scratch_bytes((int)T, (int)H, (int)E));
                 break;
@@ -840,6 +851,7 @@ static void build_sgd_table(Tr &t, std::vector<k::SgdParam> &tab) {
             e.m = p->m;
             e.v = p->v;
             e.b = p->want_b ? p->b : nullptr;
+            e.ldb = (int)(p->b_ld ? p->b_ld : p->cols);
             e.bt = p->want_bt ? p->bt : nullptr;
             e.bt3 = p->want_bt3 ? p->bt3 : nullptr;
             e.rows = (int)p->rows;
@@ -924,6 +936,8 @@ static void reserve_and_upload(Tr &t) {
     for (const auto &a : t.plan) off[a.id] = a.offset;
     for (size_t i = 0; i < t.reqs.size(); ++i)
         *t.req_slot[i] = static_cast<char *>(t.base) + off.at(t.reqs[i].id);
+    for (auto &p : t.params)
+        if (p->b_with) p->b = p->b_with->b + p->b_col;
     for (const auto &kv : t.ckpt) t.val_fwd[kv.first] = t.val.at(kv.first);
     for (auto &p : t.params)
         CATNN_REQUIRE((int64_t)p->init.size() == p->rows * p->cols, CATNN_ERR_SHAPE_MISMATCH,
@@ -1612,7 +1626,7 @@ static void backward_node(Tr &t, TNode &tn) {
             int32_t *pos = (int32_t *)tn.B("pos"), *tiles = (int32_t *)tn.B("tiles");
             const int max_tiles = (int)((T * K + k::gemm_bf16_tile_rows() - 1) / k::gemm_bf16_tile_rows() + E);
             float *w = (float *)tn.B("w"), *dw = (float *)tn.B("dw");
-            bf16_t *dys = (bf16_t *)tn.B("dys"), *da = (bf16_t *)tn.B("da"), *dc = (bf16_t *)tn.B("dc");
+            bf16_t *dys = (bf16_t *)tn.B("dys"), *dadc = (bf16_t *)tn.B("dadc");
             float *dxs = (float *)tn.B("dxs");
             // Per slot: dys = w·dout[token], dw = <ys, dout[token]> (moe_backward's d_wts).
             k::moe_slot_grads(s, sop, w, (float *)tn.B("ys"), dy, (int)K, (int)H, (int)Pr, dys, dw);
@@ -1620,31 +1634,28 @@ static void backward_node(Tr &t, TNode &tn) {
             p.grid = k::GRID_ROWS;
             p.tile_expert = tiles; p.tile_row0 = tiles + max_tiles; p.n_tiles = tiles + 2 * max_tiles;
             p.seg_offsets = offs; p.seg_counts = counts; p.max_tiles = max_tiles; p.n_experts = (int)E;
-            // dh = dys·w2ᵀ, then da = dh·c·silu'(a), dc = dh·silu(a)
+            // dh = dys·w2ᵀ, then da = dh·c·silu'(a), dc = dh·silu(a), side by
+            // side in one row: [da | dc]
             p.A = dys; p.lda = H;
             for (int64_t e = 0; e < E; ++e) p.B_e[e] = tn.params["e" + std::to_string(e) + ".w2"]->b;
             p.ldb = H; p.N = (int)I; p.K = (int)H;
-            p.epi = k::EPI_SWIGLU_BWD; p.Cb = da; p.Cb2 = dc; p.ldcb = I;
+            p.epi = k::EPI_SWIGLU_BWD; p.Cb = dadc; p.Cb2 = dadc + I; p.ldcb = 2 * I;
             p.S1 = (bf16_t *)tn.B("a"); p.S2 = (bf16_t *)tn.B("c"); p.lds = I;
             k::gemm_bf16_launch(s, p);
-            // dxs = da·w1ᵀ + dc·w3ᵀ
+            // dxs = da·w1ᵀ + dc·w3ᵀ = [da | dc]·[w1 | w3]ᵀ, one GEMM over K = 2I
             k::GemmBf16Params q = p;
             q.epi = k::EPI_STORE; q.Cb = q.Cb2 = nullptr; q.S1 = q.S2 = nullptr;
-            q.A = da; q.lda = I; q.ldb = I; q.N = (int)H; q.K = (int)I;
+            q.A = dadc; q.lda = 2 * I; q.ldb = 2 * I; q.N = (int)H; q.K = (int)(2 * I);
             q.C32 = dxs; q.ldc32 = H; q.accumulate = 0;
             for (int64_t e = 0; e < E; ++e) q.B_e[e] = tn.params["e" + std::to_string(e) + ".w1"]->b;
             k::gemm_bf16_launch(s, q);
-            q.A = dc; q.accumulate = 1;
-            for (int64_t e = 0; e < E; ++e) q.B_e[e] = tn.params["e" + std::to_string(e) + ".w3"]->b;
-            k::gemm_bf16_launch(s, q);
             // Expert weight gradients: each expert reduces over its own segment.
             bf16_t *xpt = (bf16_t *)tn.B("xpt"), *ht = (bf16_t *)tn.B("ht"), *dyst = (bf16_t *)tn.B("dyst");
-            bf16_t *dat = (bf16_t *)tn.B("dat"), *dct = (bf16_t *)tn.B("dct");
+            bf16_t *dat = (bf16_t *)tn.B("dadct"), *dct = dat + I * Pr;
             k::transpose_bf16(s, (bf16_t *)tn.B("x3"), 3 * H, sop, (int)K, (int)Pr, (int)H, xpt, Pr);  // hi part of x
             k::transpose_bf16(s, (bf16_t *)tn.B("h"), I, nullptr, 1, (int)Pr, (int)I, ht, Pr);
             k::transpose_bf16(s, dys, H, nullptr, 1, (int)Pr, (int)H, dyst, Pr);
-            k::transpose_bf16(s, da, I, nullptr, 1, (int)Pr, (int)I, dat, Pr);
-            k::transpose_bf16(s, dc, I, nullptr, 1, (int)Pr, (int)I, dct, Pr);
+            k::transpose_bf16(s, dadc, 2 * I, nullptr, 1, (int)Pr, (int)(2 * I), dat, Pr);  // [daᵀ; dcᵀ]
             k::GemmBf16Params r = gp();
             r.grid = k::GRID_SEGK; r.seg_offsets = offs; r.seg_counts = counts; r.segk_aligned = 1;
             r.n_experts = (int)E; r.epi = k::EPI_STORE;

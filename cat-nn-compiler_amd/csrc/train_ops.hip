@@ -898,11 +898,11 @@ __global__ __launch_bounds__(256) void sgd_multi_kernel(const SgdParam *__restri
         }
         h = f2bf(v);
         l = f2bf(v - __uint_as_float((uint32_t)h << 16));
-        if (P.b) P.b[e] = h;
     };
     // Four consecutive columns a thread (16-byte master and gradient, 8-byte
     // bf16 rows) when the rows allow it; the same arithmetic either way.
-    const bool vec = P.cols % 4 == 0 && al(P.p, 16) && (!grad || al(P.g, 16)) && (!P.b || al(P.b, 8)) &&
+    const bool vec = P.cols % 4 == 0 && al(P.p, 16) && (!grad || al(P.g, 16)) &&
+                     (!P.b || (al(P.b, 8) && P.ldb % 4 == 0)) &&
                      (!grad || !u.adam || (al(P.m, 16) && al(P.v, 16)));
     if (vec) {
         // A thread's four rows (rq, rq+16, rq+32, rq+48): every load of the
@@ -952,7 +952,7 @@ __global__ __launch_bounds__(256) void sgd_multi_kernel(const SgdParam *__restri
                     l[q] = f2bf(v[q] - __uint_as_float((uint32_t)h[q] << 16));
                 }
                 if (P.b)
-                    *reinterpret_cast<uint2 *>(P.b + e) =
+                    *reinterpret_cast<uint2 *>(P.b + (int64_t)(r0 + i) * P.ldb + c0 + cq) =
                         make_uint2(h[0] | (uint32_t)h[1] << 16, h[2] | (uint32_t)h[3] << 16);
             }
 #pragma unroll
@@ -965,7 +965,10 @@ __global__ __launch_bounds__(256) void sgd_multi_kernel(const SgdParam *__restri
         for (int i = ty; i < 64; i += 4) {
             const int r = r0 + i, c = c0 + tx;
             bf16_t h = 0, l = 0;
-            if (r < P.rows && c < P.cols) one((int64_t)r * P.cols + c, h, l);
+            if (r < P.rows && c < P.cols) {
+                one((int64_t)r * P.cols + c, h, l);
+                if (P.b) P.b[(int64_t)r * P.ldb + c] = h;
+            }
             th[i][tx] = h;
             tl[i][tx] = l;
         }

@@ -102,6 +102,7 @@ struct SgdParam {
     const float *g;
     float *m, *v;  // Adam moments, same layout as p (null under SGD)
     bf16_t *b, *bt, *bt3;
+    int ldb;      // row stride of b (≥ cols)
     int rows, cols;
     int tile0;    // first 64×64 tile of this parameter in the launch
     int tiles_c;  // tiles across cols
