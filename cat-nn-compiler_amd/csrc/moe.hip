@@ -9,11 +9,13 @@
 //               cpu::linear_seq (cpu.rs:115-126: s = 0; s += x[p]·g[p] for
 //               p ascending, separate multiply and add), then per token the
 //               top-k of a stable descending order (ties → lower expert id,
-//               lens/moe.rs:175-187) and w = exp(l − max)·(1/max(Σ, 1e-30)).
+//               lens/moe.rs:175-187) by a butterfly arg-max across the
+//               token's lanes, and w = exp(l − max)·(1/max(Σ, 1e-30)).
 //               Bit-exact logits make the indices bit-exact.
 //  2. permute   stable counting sort of the flattened slots s = t·k + k'
-//               by expert: per-block histograms, a scan, and a scatter that
-//               ranks slots inside each wavefront with ballot + popcount.
+//               by expert: per-block histograms, a wavefront prefix scan
+//               for the segment starts, and a scatter that ranks slots
+//               inside each wavefront with ballot + popcount.
 //  3. gate/up   grouped fp32 MFMA GEMM over each expert's row segment, A rows
 //               gathered from x through the permutation, W1 and W3 tiles
 //               side by side, epilogue silu(a)·c → h[pos].
@@ -47,6 +49,9 @@ constexpr int kMaxTopK = 16;
 
 __device__ void select_topk(const float *row, int E, int K, int64_t base, int32_t *__restrict__ idx_out,
                             float *__restrict__ w_out);
+__device__ __forceinline__ void finish_route(float s, bool active, int tl, int e, int E, int K, int t0,
+                                             float *__restrict__ lg, int32_t *__restrict__ idx_out,
+                                             float *__restrict__ w_out, float *__restrict__ logits_out);
 
 // One thread per (token, expert); tokens_per_block = 256 / E.
 __global__ __launch_bounds__(256) void route_kernel(const float *__restrict__ x,
@@ -86,13 +91,7 @@ __global__ __launch_bounds__(256) void route_kernel(const float *__restrict__ x,
         }
         __syncthreads();
     }
-    if (active) {
-        lg[tl * E + e] = s;
-        if (logits_out) logits_out[(int64_t)(t0 + tl) * E + e] = s;
-    }
-    __syncthreads();
-    if (!active || e != 0) return;
-    select_topk(lg + tl * E, E, K, (int64_t)(t0 + tl) * K, idx_out, w_out);
+    finish_route(s, active, tl, e, E, K, t0, lg, idx_out, w_out, logits_out);
 }
 
 // Top-k of a stable descending order (repeated first-maximum selection) and
@@ -124,6 +123,68 @@ __device__ void select_topk(const float *row, int E, int K, int64_t base, int32_
         if (idx_out) idx_out[base + kk] = sel[kk];
         if (w_out) w_out[base + kk] = ex[kk] * inv;
     }
+}
+
+// The same selection with the token's E logits in E consecutive lanes of a
+// wavefront (lane e holds expert e; E a power of two ≤ 64, groups aligned
+// on multiples of E): K rounds of a butterfly arg-max inside the group,
+// an untaken expert beating a taken one, a larger logit a smaller one, and
+// equal logits going to the lower expert — the first maximum that the
+// serial selection finds.  The selected logits are the same floats, so the
+// softmax below is select_topk's, bit for bit.  Every lane of the group
+// must call it; lane `write` stores the token's entries.
+__device__ void group_topk(float v, int e, int E, int K, bool write, int64_t base, int32_t *__restrict__ idx_out,
+                           float *__restrict__ w_out) {
+#pragma clang fp contract(off)
+    bool taken = false;
+    int sel[kMaxTopK];
+    float sv[kMaxTopK];
+    for (int kk = 0; kk < K; ++kk) {
+        float bv = v;
+        int be = taken ? E : e;  // index E: taken
+        for (int off = 1; off < E; off <<= 1) {
+            const float ov = __shfl_xor(bv, off, 64);
+            const int oe = __shfl_xor(be, off, 64);
+            const bool better = oe < E && (be >= E || ov > bv || (ov == bv && oe < be));
+            if (better) {
+                bv = ov;
+                be = oe;
+            }
+        }
+        sel[kk] = be;
+        sv[kk] = bv;
+        if (e == be) taken = true;
+    }
+    if (!write) return;
+    float mx = -INFINITY;
+    for (int kk = 0; kk < K; ++kk) mx = fmaxf(mx, sv[kk]);
+    float ex[kMaxTopK];
+    float sum = 0.f;
+    for (int kk = 0; kk < K; ++kk) {
+        ex[kk] = expf(sv[kk] - mx);
+        sum = sum + ex[kk];
+    }
+    const float inv = 1.0f / fmaxf(sum, 1e-30f);
+    for (int kk = 0; kk < K; ++kk) {
+        if (idx_out) idx_out[base + kk] = sel[kk];
+        if (w_out) w_out[base + kk] = ex[kk] * inv;
+    }
+}
+
+// The end of a route kernel: logits out, then the top-k by lane groups
+// (E a power of two up to 64) or by one thread per token through LDS.
+__device__ __forceinline__ void finish_route(float s, bool active, int tl, int e, int E, int K, int t0,
+                                             float *__restrict__ lg, int32_t *__restrict__ idx_out,
+                                             float *__restrict__ w_out, float *__restrict__ logits_out) {
+    if (active && logits_out) logits_out[(int64_t)(t0 + tl) * E + e] = s;
+    if (E <= 64 && (E & (E - 1)) == 0) {  // uniform: the group sits in one wavefront
+        group_topk(s, e, E, K, active && e == 0, (int64_t)(t0 + tl) * K, idx_out, w_out);
+        return;
+    }
+    if (active) lg[tl * E + e] = s;
+    __syncthreads();
+    if (!active || e != 0) return;
+    select_topk(lg + tl * E, E, K, (int64_t)(t0 + tl) * K, idx_out, w_out);
 }
 
 constexpr int kRouteGateFloats = 12288;  // LDS floats for one staged gate chunk (48 KiB)
@@ -234,13 +295,7 @@ __global__ __launch_bounds__(256) void route_dma_kernel(const float *__restrict_
             }
         }
     }
-    if (active) {
-        lg[tl * E + e] = s;
-        if (logits_out) logits_out[(int64_t)(t0 + tl) * E + e] = s;
-    }
-    __syncthreads();
-    if (!active || e != 0) return;
-    select_topk(lg + tl * E, E, K, (int64_t)(t0 + tl) * K, idx_out, w_out);
+    finish_route(s, active, tl, e, E, K, t0, lg, idx_out, w_out, logits_out);
 }
 
 // Rows of x 16-byte aligned (H % 4 == 0): each thread streams its token's
@@ -283,13 +338,7 @@ __global__ __launch_bounds__(256) void route_vec_kernel(const float *__restrict_
             }
         }
     }
-    if (active) {
-        lg[tl * E + e] = s;
-        if (logits_out) logits_out[(int64_t)(t0 + tl) * E + e] = s;
-    }
-    __syncthreads();
-    if (!active || e != 0) return;
-    select_topk(lg + tl * E, E, K, (int64_t)(t0 + tl) * K, idx_out, w_out);
+    finish_route(s, active, tl, e, E, K, t0, lg, idx_out, w_out, logits_out);
 }
 
 // Per-block expert histogram of the slots [b·chunk, (b+1)·chunk).  Slots
@@ -298,6 +347,11 @@ __global__ __launch_bounds__(256) void route_vec_kernel(const float *__restrict_
 // hipMemsetAsync so that the path stays a plain kernel sequence for callers
 // that capture it into a graph.
 __global__ void zero_i32_kernel(int32_t *__restrict__ p) { *p = 0; }
+
+__global__ __launch_bounds__(256) void fill_i32_kernel(int32_t *__restrict__ p, int64_t n, int32_t v) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) p[i] = v;
+}
 
 __global__ __launch_bounds__(256) void perm_count_kernel(const int32_t *__restrict__ idx,
                                                          int64_t n, int E,
@@ -337,16 +391,21 @@ __global__ void perm_scan_kernel(const int32_t *__restrict__ block_counts, int n
         counts[e] = run;
     }
     __syncthreads();
-    if (e == 0) {
-        int acc = 0;
-        for (int c = 0; c < E; ++c) {
-            const int t = tot[c];
-            tot[c] = acc;
-            offsets[c] = acc;
-            acc += (t + pad - 1) / pad * pad;
-        }
-        offsets[E] = acc;
+    // Segment starts: exclusive prefix of the padded totals, a wavefront
+    // inclusive scan (E ≤ 64 lanes).
+    const int padded = e < E ? (tot[e] + pad - 1) / pad * pad : 0;
+    int incl = padded;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int o = __shfl_up(incl, off, 64);
+        if (e >= off) incl += o;
     }
+    __syncthreads();
+    if (e < E) {
+        tot[e] = incl - padded;
+        offsets[e] = incl - padded;
+    }
+    if (e == E - 1) offsets[E] = incl;
     __syncthreads();
     if (e < E) {
         const int off = tot[e];
@@ -560,8 +619,10 @@ void moe_permute_padded(hipStream_t s, const int32_t *idx, int64_t tokens, int64
     int32_t *block_counts = reinterpret_cast<int32_t *>(sc);
     int32_t *block_base = reinterpret_cast<int32_t *>(sc + align256((uint64_t)nb * E * 4));
     int32_t *bad = reinterpret_cast<int32_t *>(sc + 2 * align256((uint64_t)nb * E * 4));
-    CATNN_HIP(hipMemsetAsync(bad, 0, 4, s));
-    CATNN_HIP(hipMemsetAsync(slot_of_pos, 0xff, (size_t)n_pos_cap * 4, s));  // −1: padding
+    zero_i32_kernel<<<1, 1, 0, s>>>(bad);
+    if (n_pos_cap > 0)
+        fill_i32_kernel<<<(unsigned)((n_pos_cap + 255) / 256), 256, 0, s>>>(slot_of_pos, n_pos_cap, -1);  // padding
+    CATNN_HIP(hipGetLastError());
     if (nb > 0) {
         perm_count_kernel<<<(unsigned)nb, 256, 0, s>>>(idx, n, E, block_counts, bad);
         CATNN_HIP(hipGetLastError());

@@ -202,11 +202,14 @@ def test_route_is_bit_exact(device, T, H, E, k):
     assert np.max(np.abs(_get(dw, (T, k)) - w_w)) < 1e-6
 
 
-def test_route_ties_prefer_lower_expert(device):
-    T, H, E, k = 64, 32, 6, 3
+@pytest.mark.parametrize("E,k", [(6, 3), (8, 4), (64, 8)])  # one thread per token; lane groups (8, 64)
+def test_route_ties_prefer_lower_expert(device, E, k):
+    # Duplicated gate columns make equal logits: the selection must take the
+    # lower expert first, as the stable descending order of the reference.
+    T, H = 64, 32
     x = RNG.standard_normal((T, H)).astype(np.float32)
-    base = RNG.standard_normal((H, 2)).astype(np.float32)
-    gate = np.concatenate([base[:, :1], base, base[:, 1:], base[:, :1], base], 1)[:, :E].copy()
+    base = RNG.standard_normal((H, 3)).astype(np.float32)
+    gate = np.tile(np.concatenate([base[:, :1], base, base[:, 1:]], 1), (1, E))[:, :E].copy()
     idx_w, _, _ = oracle.route(x, gate, k)
     dx, dg, didx = _put(device, x), _put(device, gate), device.alloc(T * k * 4)
     D.moe_route(device, dx, dg, T, H, E, k, didx, None, None)
