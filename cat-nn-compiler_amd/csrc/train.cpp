@@ -110,6 +110,13 @@ struct TNode {
     bool skip_bwd = false;         // this GELU node's adjoint runs inside B's GEMM
     uint32_t gelu_pre = UINT32_MAX;  // on B: the Linear A before the GELU
     bool dyb_ready = false;        // on A: its bf16 cotangent is written by B
+    // The forward of the same pattern: A's GEMM epilogue applies the GELU
+    // and writes B's bf16 input operand (its "xb" tape) directly; the GELU
+    // node's forward and B's cast are skipped.
+    bool skip_fwd = false;            // on the GELU node
+    uint32_t gelu_next = UINT32_MAX;  // on A: B
+    bool xb_ready = false;            // on B
+    size_t xb_from = 0;               // on B: the tick its xb tape is written (A's)
     std::vector<int64_t> dims;
     std::map<std::string, TParam *> params;
     // tapes and scratch (named pointers, assigned after planning)
@@ -375,6 +382,12 @@ static void plan_trainer(Tr &t) {
         bn.gelu_pre = a;
         an.dyb_ready = true;
         grad_from[a] = bwd(bn.tick);
+        if (an.kind == CATNN_OP_LINEAR || an.kind == CATNN_OP_MATMUL) {
+            gn.skip_fwd = true;
+            an.gelu_next = bn.id;
+            bn.xb_ready = true;
+            bn.xb_from = an.tick;
+        }
     }
 
     // Values and cotangents.
@@ -643,7 +656,11 @@ static void plan_trainer(Tr &t) {
                 const int64_t K = w->dims[0], N = w->dims[1], M = numel(x) / K;
                 add_param(tn, nd.param("w") ? "w" : nd.params.front().first, K, N, true, true, w->data);
                 if (const HostTensor *b = nd.param("b")) add_param(tn, "b", 1, N, false, false, b->data);
-                tape(tn, "xb", (uint64_t)(M * K) * 2);
+                if (tn.xb_ready)  // written by the previous Linear's epilogue (the fused GELU)
+                    request(t, "tape:" + tn.node->name + ":xb", (uint64_t)(M * K) * 2, tn.xb_from, bwd(tn.tick),
+                            &tn.B("xb"));
+                else
+                    tape(tn, "xb", (uint64_t)(M * K) * 2);
                 scratch(tn, "xbt", (uint64_t)(M * K) * 2);
                 if (tn.dyb_ready)  // written by the next Linear's backward (the fused GELU adjoint)
                     request(t, "scratch:" + tn.node->name + ":dyb", (uint64_t)(M * N) * 2, grad_from.at(tn.id),
@@ -1237,6 +1254,7 @@ static void refresh_split_copies(Tr &t) {
 // ------------------------------------------------------------ forward
 
 static void forward_node(Tr &t, TNode &tn) {
+    if (tn.skip_fwd) return;  // a GELU applied by the producing Linear's epilogue
     if (t.prec == CATNN_PREC_FP32 && is_gemm_op(tn.kind)) return forward_gemm_f32(t, tn);
     hipStream_t s = t.dev->stream;
     const Node &nd = *tn.node;
@@ -1271,12 +1289,19 @@ static void forward_node(Tr &t, TNode &tn) {
             TParam *b = tn.params.count("b") ? tn.params["b"] : nullptr;
             const int64_t K = w->rows, N = w->cols, M = nx / K;
             bf16_t *xb = (bf16_t *)tn.B("xb");
-            k::cast_f32_bf16(s, x, xb, M * K);
+            if (!tn.xb_ready) k::cast_f32_bf16(s, x, xb, M * K);
             k::GemmBf16Params p = gp();
             p.A = xb; p.lda = K; p.B = w->bt; p.ldb = K;
             p.M = (int)M; p.N = (int)N; p.K = (int)K;
             p.epi = k::EPI_LINEAR; p.bias = b ? b->master : nullptr;
-            p.C32 = y; p.ldc32 = N;
+            if (tn.gelu_next != UINT32_MAX) {
+                // y = x·w + b (the GELU adjoint's Z), then GELU into the next
+                // Linear's bf16 operand.
+                p.Z = y; p.ldz = N; p.act = 3;
+                p.Cb = (bf16_t *)t.nodes[t.index.at(tn.gelu_next)].B("xb"); p.ldcb = N;
+            } else {
+                p.C32 = y; p.ldc32 = N;
+            }
             k::gemm_bf16_launch(s, p);
             break;
         }
