@@ -55,6 +55,25 @@ __global__ __launch_bounds__(256) void attn_dot_kernel(const float *__restrict__
     if (lane == 0) D[gw] = s;
 }
 
+// The same for d_head 64 on 16-byte aligned rows: 16 lanes per (row, head),
+// one float4 of each operand a lane, a 16-lane butterfly sum.
+__global__ __launch_bounds__(256) void attn_dot64_kernel(const float *__restrict__ o,
+                                                         const float *__restrict__ dout, int64_t ldo,
+                                                         int64_t rows, int H, float *__restrict__ D) {
+    const int64_t pair = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+    const int q = threadIdx.x & 15;
+    float s = 0.f;
+    if (pair < rows * H) {
+        const int64_t off = (pair / H) * ldo + (pair % H) * 64 + 4 * q;
+        const float4 a = *reinterpret_cast<const float4 *>(o + off);
+        const float4 b = *reinterpret_cast<const float4 *>(dout + off);
+        s = (a.x * b.x + a.y * b.y) + (a.z * b.z + a.w * b.w);
+    }
+#pragma unroll
+    for (int m = 8; m > 0; m >>= 1) s += __shfl_xor(s, m, 64);
+    if (pair < rows * H && q == 0) D[pair] = s;
+}
+
 // Column swizzle of the transposed K tile of the dQ kernel (row d = head
 // dimension): row d holds key j at j ^ tsw(d).  The transposing stores put
 // 16 rows 4 apart into one wavefront store; with the swizzle those rows
@@ -517,8 +536,11 @@ bool al16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 void attention_rowdot(hipStream_t s, const float *o, const float *dout, int64_t ld, int64_t rows, int64_t n_heads,
                       int64_t d_head, float *D) {
     if (rows == 0) return;
-    attn_dot_kernel<<<(unsigned)((rows * n_heads + 3) / 4), 256, 0, s>>>(o, dout, ld, rows, (int)n_heads,
-                                                                        (int)d_head, D);
+    if (d_head == 64 && ld % 4 == 0 && al16(o) && al16(dout))
+        attn_dot64_kernel<<<(unsigned)((rows * n_heads + 15) / 16), 256, 0, s>>>(o, dout, ld, rows, (int)n_heads, D);
+    else
+        attn_dot_kernel<<<(unsigned)((rows * n_heads + 3) / 4), 256, 0, s>>>(o, dout, ld, rows, (int)n_heads,
+                                                                            (int)d_head, D);
     CATNN_HIP(hipGetLastError());
 }
 
@@ -546,9 +568,7 @@ void attention_core_bwd_gqa(hipStream_t s, const float *q, int64_t ldq, const fl
     const int64_t rows = batch * seq;
     const int64_t HK = n_heads / group;
     float *D = scratch;
-    attn_dot_kernel<<<(unsigned)((rows * n_heads + 3) / 4), 256, 0, s>>>(o, dout, ldo, rows, (int)n_heads,
-                                                                        (int)d_head, D);
-    CATNN_HIP(hipGetLastError());
+    attention_rowdot(s, o, dout, ldo, rows, n_heads, d_head, D);
     const float scale = 1.0f / sqrtf((float)d_head);
     const bool mfma = d_head == 64 && ldq % 4 == 0 && ldk % 4 == 0 && ldo % 4 == 0 && ld_dq % 4 == 0 &&
                       ld_dkv % 4 == 0 && al16(q) && al16(k) && al16(v) && al16(dout) && al16(dq) &&

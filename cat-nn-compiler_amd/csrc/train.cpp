@@ -117,6 +117,12 @@ struct TNode {
     uint32_t gelu_next = UINT32_MAX;  // on A: B
     bool xb_ready = false;            // on B
     size_t xb_from = 0;               // on B: the tick its xb tape is written (A's)
+    // LayerNorm → its only consumer: the LN forward writes the consumer's
+    // GEMM operand (a Linear's bf16 "xb", an attention's split-bf16 "x3")
+    // instead of its fp32 output, which nothing else reads.
+    uint32_t ln_next = UINT32_MAX;    // on the LayerNorm
+    bool x3_ready = false;            // on the attention node
+    size_t x3_from = 0;
     std::vector<int64_t> dims;
     std::map<std::string, TParam *> params;
     // tapes and scratch (named pointers, assigned after planning)
@@ -387,6 +393,24 @@ static void plan_trainer(Tr &t) {
             an.gelu_next = bn.id;
             bn.xb_ready = true;
             bn.xb_from = an.tick;
+        }
+    }
+
+    for (auto &ln : t.nodes) {
+        if (t.prec != CATNN_PREC_BF16) break;
+        if (ln.kind != CATNN_OP_LAYER_NORM || ln.id == t.out_id || t.input_ids.count(ln.id)) continue;
+        const auto &cs = consumers[ln.id];
+        if (cs.size() != 1) continue;
+        TNode &cn = t.nodes[t.index.at(cs[0])];
+        if (cn.ins.size() != 1) continue;
+        if (is_linear(cn) && !cn.xb_ready) {
+            ln.ln_next = cn.id;
+            cn.xb_ready = true;
+            cn.xb_from = ln.tick;
+        } else if (cn.kind == CATNN_OP_ATTENTION || cn.kind == CATNN_OP_GQA_ATTENTION) {
+            ln.ln_next = cn.id;
+            cn.x3_ready = true;
+            cn.x3_from = ln.tick;
         }
     }
 
@@ -755,7 +779,11 @@ static void plan_trainer(Tr &t) {
                 const int64_t Bt = x[0], S = x[1], D = x[2], T = Bt * S, H = nd.op.a[0];
                 add_param(tn, "wqkv", D, 3 * D, true, false, param_values(nd, "wqkv"), true);
                 add_param(tn, "wo", D, D, true, false, host(nd, "wo")->data, true);
-                tape(tn, "x3", (uint64_t)(T * 3 * D) * 2);
+                if (tn.x3_ready)  // written by the LayerNorm before it
+                    request(t, "tape:" + tn.node->name + ":x3", (uint64_t)(T * 3 * D) * 2, tn.x3_from, bwd(tn.tick),
+                            &tn.B("x3"));
+                else
+                    tape(tn, "x3", (uint64_t)(T * 3 * D) * 2);
                 if (attn_core_bf16(nd, D)) {
                     const uint64_t Sp = (uint64_t)k::attention_bf16_seq_pad(S);
                     tape(tn, "qkvb", (uint64_t)(T * 3 * D) * 2);
@@ -786,7 +814,11 @@ static void plan_trainer(Tr &t) {
                 const int64_t QW = H * hd, KW = HKV * hd, LD = QW + 2 * KW;
                 add_param(tn, "wqkv", D, LD, true, false, param_values(nd, "wqkv"), true);
                 add_param(tn, "wo", QW, D, true, false, host(nd, "wo")->data, true);
-                tape(tn, "x3", (uint64_t)(T * 3 * D) * 2);
+                if (tn.x3_ready)  // written by the LayerNorm before it
+                    request(t, "tape:" + tn.node->name + ":x3", (uint64_t)(T * 3 * D) * 2, tn.x3_from, bwd(tn.tick),
+                            &tn.B("x3"));
+                else
+                    tape(tn, "x3", (uint64_t)(T * 3 * D) * 2);
                 tape(tn, "qkv", (uint64_t)(T * LD) * 4);  // q and k after RoPE
                 tape(tn, "ctx", (uint64_t)(T * QW) * 4);
                 tape(tn, "ctx3", (uint64_t)(T * 3 * QW) * 2);
@@ -1343,8 +1375,15 @@ static void forward_node(Tr &t, TNode &tn) {
         case CATNN_OP_LAYER_NORM: {
             const int64_t C = xd.back();
             const float eps = (float)nd.op.a[0] * 1e-6f;
-            k::ln_forward_train(s, x, tn.params["gamma"]->master, tn.params["beta"]->master, y, nullptr,
-                                (float *)tn.B("mean"), (float *)tn.B("rstd"), nx / C, (int)C, eps);
+            bf16_t *yb = nullptr, *y3 = nullptr;
+            if (tn.ln_next != UINT32_MAX) {
+                TNode &cn = t.nodes[t.index.at(tn.ln_next)];
+                if (cn.x3_ready) y3 = (bf16_t *)cn.B("x3");
+                else yb = (bf16_t *)cn.B("xb");
+            }
+            k::ln_forward_train(s, x, tn.params["gamma"]->master, tn.params["beta"]->master,
+                                tn.ln_next != UINT32_MAX ? nullptr : y, yb, y3, (float *)tn.B("mean"),
+                                (float *)tn.B("rstd"), nx / C, (int)C, eps);
             break;
         }
         case CATNN_OP_ATTENTION: {
@@ -1354,7 +1393,7 @@ static void forward_node(Tr &t, TNode &tn) {
             bf16_t *x3 = (bf16_t *)tn.B("x3"), *ctx3 = (bf16_t *)tn.B("ctx3");
             float *ctx = (float *)tn.B("ctx");
             // Both projections split-bf16 (K' = 3D).
-            k::split3_rows(s, x, D, T, (int)D, x3, 3 * D);
+            if (!tn.x3_ready) k::split3_rows(s, x, D, T, (int)D, x3, 3 * D);
             if (attn_core_bf16(nd, D)) {
                 // q, k, v in bf16 (and transposed per batch element) for the
                 // core on bf16 MFMA.
@@ -1387,7 +1426,7 @@ static void forward_node(Tr &t, TNode &tn) {
             float *qkv = (float *)tn.B("qkv"), *ctx = (float *)tn.B("ctx"), *rope = (float *)tn.B("rope");
             // Projections split-bf16 as Attention's; RoPE on q and k in place;
             // the grouped, windowed causal core on fp32 MFMA with its lse kept.
-            k::split3_rows(s, x, D, T, (int)D, x3, 3 * D);
+            if (!tn.x3_ready) k::split3_rows(s, x, D, T, (int)D, x3, 3 * D);
             gemm_nt(s, x3, 3 * D, tn.params["wqkv"]->bt3, 3 * D, (int)T, (int)LD, (int)(3 * D), qkv, LD, false);
             k::rope_table(s, rope, S, hd, (double)nd.op.a[5]);
             k::rope_apply(s, qkv, LD, T, S, H + HKV, hd, rope, 1.0f);

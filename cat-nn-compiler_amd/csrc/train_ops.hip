@@ -337,7 +337,7 @@ __global__ __launch_bounds__(256) void ln_fwd_kernel(const float *__restrict__ x
                                                      const float *__restrict__ g,
                                                      const float *__restrict__ b,
                                                      float *__restrict__ y, bf16_t *__restrict__ yb,
-                                                     float *__restrict__ mean,
+                                                     bf16_t *__restrict__ y3, float *__restrict__ mean,
                                                      float *__restrict__ rstd, int64_t rows,
                                                      int cols, float eps) {
     const int lane = threadIdx.x & 63;
@@ -374,6 +374,17 @@ __global__ __launch_bounds__(256) void ln_fwd_kernel(const float *__restrict__ x
                                          (v.z - mu) * inv * gv.z + bv.z, (v.w - mu) * inv * gv.w + bv.w);
             if (y) reinterpret_cast<float4 *>(y + row * cols)[c] = o;
             if (yb) reinterpret_cast<uint2 *>(yb + row * cols)[c] = pack4(f2bf(o.x), f2bf(o.y), f2bf(o.z), f2bf(o.w));
+            if (y3) {  // [hi | lo | hi], as split3_rows
+                bf16_t h[4], l[4];
+                split_bf16(o.x, h[0], l[0]);
+                split_bf16(o.y, h[1], l[1]);
+                split_bf16(o.z, h[2], l[2]);
+                split_bf16(o.w, h[3], l[3]);
+                uint2 *r3 = reinterpret_cast<uint2 *>(y3 + row * 3 * cols);
+                r3[c] = pack4(h[0], h[1], h[2], h[3]);
+                r3[c4n + c] = pack4(l[0], l[1], l[2], l[3]);
+                r3[2 * c4n + c] = pack4(h[0], h[1], h[2], h[3]);
+            }
         }
         if (lane == 0) {
             mean[row] = mu;
@@ -395,6 +406,13 @@ __global__ __launch_bounds__(256) void ln_fwd_kernel(const float *__restrict__ x
         const float v = (xr[c] - mu) * inv * g[c] + b[c];
         if (y) y[row * cols + c] = v;
         if (yb) yb[row * cols + c] = f2bf(v);
+        if (y3) {
+            bf16_t h, l;
+            split_bf16(v, h, l);
+            y3[row * 3 * cols + c] = h;
+            y3[row * 3 * cols + cols + c] = l;
+            y3[row * 3 * cols + 2 * cols + c] = h;
+        }
     }
     if (lane == 0) {
         mean[row] = mu;
@@ -1216,13 +1234,14 @@ void transpose_split3(hipStream_t s, const float *w, int64_t ldw, int K, int N, 
 }
 
 void ln_forward_train(hipStream_t s, const float *x, const float *g, const float *b, float *y,
-                      bf16_t *yb, float *mean, float *rstd, int64_t rows, int cols, float eps) {
+                      bf16_t *yb, bf16_t *y3, float *mean, float *rstd, int64_t rows, int cols, float eps) {
     if (rows <= 0) return;
     auto al = [](const void *q, uintptr_t a) { return (reinterpret_cast<uintptr_t>(q) & (a - 1)) == 0; };
-    const bool vec = cols % 4 == 0 && al(x, 16) && al(g, 16) && al(b, 16) && (!y || al(y, 16)) && (!yb || al(yb, 8));
+    const bool vec = cols % 4 == 0 && al(x, 16) && al(g, 16) && al(b, 16) && (!y || al(y, 16)) &&
+                     (!yb || al(yb, 8)) && (!y3 || al(y3, 8));
     const unsigned blocks = (unsigned)((rows + 3) / 4);
-    if (vec) ln_fwd_kernel<true><<<blocks, 256, 0, s>>>(x, g, b, y, yb, mean, rstd, rows, cols, eps);
-    else ln_fwd_kernel<false><<<blocks, 256, 0, s>>>(x, g, b, y, yb, mean, rstd, rows, cols, eps);
+    if (vec) ln_fwd_kernel<true><<<blocks, 256, 0, s>>>(x, g, b, y, yb, y3, mean, rstd, rows, cols, eps);
+    else ln_fwd_kernel<false><<<blocks, 256, 0, s>>>(x, g, b, y, yb, y3, mean, rstd, rows, cols, eps);
     CATNN_HIP(hipGetLastError());
 }
 

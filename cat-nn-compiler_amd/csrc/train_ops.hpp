@@ -29,8 +29,11 @@ void split3_rows(hipStream_t s, const float *x, int64_t ldx, int64_t rows, int K
 void transpose_split3(hipStream_t s, const float *w, int64_t ldw, int K, int N, bf16_t *out,
                       int64_t ldo);
 
+// LayerNorm forward with its mean and rstd for the adjoint; y (fp32), yb
+// (bf16, row stride cols) and y3 ([hi | lo | hi] split-bf16, row stride
+// 3·cols, as split3_rows) are each optional.
 void ln_forward_train(hipStream_t s, const float *x, const float *g, const float *b, float *y,
-                      bf16_t *yb, float *mean, float *rstd, int64_t rows, int cols, float eps);
+                      bf16_t *yb, bf16_t *y3, float *mean, float *rstd, int64_t rows, int cols, float eps);
 uint64_t ln_backward_scratch_bytes(int64_t rows, int cols);
 void ln_backward(hipStream_t s, const float *x, const float *g, const float *mean, const float *rstd,
                  const float *dy, float *dx, bool accumulate, float *dg, float *db, bool acc_params,
