@@ -123,6 +123,11 @@ struct TNode {
     uint32_t ln_next = UINT32_MAX;    // on the LayerNorm
     bool x3_ready = false;            // on the attention node
     size_t x3_from = 0;
+    // GEMM → Add (its only consumer): the GEMM's epilogue adds the other
+    // addend and writes the Add's value; the Add's forward is skipped and
+    // its value is live from the GEMM's tick.
+    uint32_t res_into = UINT32_MAX, res_other = UINT32_MAX;  // on the GEMM node
+    size_t val_from = SIZE_MAX;       // on the Add: the tick its value is written
     std::vector<int64_t> dims;
     std::map<std::string, TParam *> params;
     // tapes and scratch (named pointers, assigned after planning)
@@ -140,6 +145,10 @@ struct catnn_hip_trainer {
     int opt = CATNN_OPT_SGD;
     int prec = CATNN_PREC_BF16;
     uint64_t arena_cap = 0;  // 0: the device's memory
+    // Residual adds and LayerNorm outputs fused into the neighbouring GEMMs
+    // (their values are then not recomputable); off when a capped arena
+    // needs more checkpoints than the fused plan offers.
+    bool fuse_values = true;
     uint64_t adam_t = 0;  // AdamState.t shared by every trained parameter
     // Activation checkpoints (schedule.rs:155-212): value id → where its
     // forward buffer ends and where the recomputed copy lives.
@@ -396,8 +405,30 @@ static void plan_trainer(Tr &t) {
         }
     }
 
+    for (auto &an : t.nodes) {
+        if (t.prec != CATNN_PREC_BF16 || !t.fuse_values) break;
+        if ((an.kind != CATNN_OP_ADD && an.kind != CATNN_OP_RESIDUAL_ADD) || an.ins.size() != 2 ||
+            an.ins[0] == an.ins[1] || an.dims != t.dims[an.ins[0]] || an.dims != t.dims[an.ins[1]])
+            continue;
+        for (int j = 0; j < 2; ++j) {
+            const uint32_t g = an.ins[j], o = an.ins[1 - j];
+            if (t.input_ids.count(g) || g == t.out_id || consumers[g].size() != 1) continue;
+            TNode &gn = t.nodes[t.index.at(g)];
+            const bool gemm = (is_linear(gn) && gn.gelu_next == UINT32_MAX) ||
+                              (gn.kind == CATNN_OP_ATTENTION && attn_core_bf16(*gn.node, gn.in_dims[0].back()));
+            // the other addend must exist when the GEMM runs
+            const bool ready = t.input_ids.count(o) || t.nodes[t.index.at(o)].tick < gn.tick;
+            if (!gemm || !ready) continue;
+            gn.res_into = an.id;
+            gn.res_other = o;
+            an.skip_fwd = true;
+            an.val_from = gn.tick;
+            break;
+        }
+    }
+
     for (auto &ln : t.nodes) {
-        if (t.prec != CATNN_PREC_BF16) break;
+        if (t.prec != CATNN_PREC_BF16 || !t.fuse_values) break;
         if (ln.kind != CATNN_OP_LAYER_NORM || ln.id == t.out_id || t.input_ids.count(ln.id)) continue;
         const auto &cs = consumers[ln.id];
         if (cs.size() != 1) continue;
@@ -455,7 +486,10 @@ static void plan_trainer(Tr &t) {
             (tn.kind == CATNN_OP_LINEAR || tn.kind == CATNN_OP_MATMUL || tn.kind == CATNN_OP_LM_HEAD ||
              tn.kind == CATNN_OP_SWIGLU || tn.kind == CATNN_OP_ATTENTION || tn.kind == CATNN_OP_GQA_ATTENTION ||
              tn.kind == CATNN_OP_MOE);
-        if (!is_input && tn.id != t.out_id && !fscratch_fwd && fwd_last.count(tn.id) &&
+        // Values a fused forward writes elsewhere (or in another node's
+        // epilogue) are not recomputed.
+        const bool fused = tn.skip_fwd || tn.res_into != UINT32_MAX || tn.ln_next != UINT32_MAX;
+        if (!is_input && tn.id != t.out_id && !fscratch_fwd && !fused && fwd_last.count(tn.id) &&
             last_read[tn.id] > fwd_last[tn.id] && bwd_first.count(tn.id)) {
             catnn_hip_trainer::Ckpt c;
             c.req = t.reqs.size();
@@ -464,7 +498,7 @@ static void plan_trainer(Tr &t) {
             c.first_reader = first_reader[tn.id];
             t.ckpt_candidates[tn.id] = c;
         }
-        request(t, "act:" + std::to_string(tn.id), bytes, is_input ? 0 : tn.tick,
+        request(t, "act:" + std::to_string(tn.id), bytes, is_input ? 0 : std::min<size_t>(tn.tick, tn.val_from),
                 is_input ? upd : last_read[tn.id], reinterpret_cast<void **>(&t.val[tn.id]));
         if (is_input) {
             // An input's cotangent, when kept, stays readable after the pass.
@@ -1331,6 +1365,10 @@ static void forward_node(Tr &t, TNode &tn) {
                 // Linear's bf16 operand.
                 p.Z = y; p.ldz = N; p.act = 3;
                 p.Cb = (bf16_t *)t.nodes[t.index.at(tn.gelu_next)].B("xb"); p.ldcb = N;
+            } else if (tn.res_into != UINT32_MAX) {
+                // the Add after it: other + (x·w + b)
+                p.R = t.val.at(tn.res_other); p.ldr = N;
+                p.C32 = t.val.at(tn.res_into); p.ldc32 = N;
             } else {
                 p.C32 = y; p.ldc32 = N;
             }
@@ -1413,7 +1451,16 @@ static void forward_node(Tr &t, TNode &tn) {
                                           S, H, dh, causal);
             }
             k::split3_rows(s, ctx, D, T, (int)D, ctx3, 3 * D);
-            gemm_nt(s, ctx3, 3 * D, tn.params["wo"]->bt3, 3 * D, (int)T, (int)D, (int)(3 * D), y, D, false);
+            if (tn.res_into != UINT32_MAX) {  // the Add after it: other + ctx·wo
+                k::GemmBf16Params p = gp();
+                p.A = ctx3; p.lda = 3 * D; p.B = tn.params["wo"]->bt3; p.ldb = 3 * D;
+                p.M = (int)T; p.N = (int)D; p.K = (int)(3 * D);
+                p.epi = k::EPI_LINEAR; p.R = t.val.at(tn.res_other); p.ldr = D;
+                p.C32 = t.val.at(tn.res_into); p.ldc32 = D;
+                k::gemm_bf16_launch(s, p);
+            } else {
+                gemm_nt(s, ctx3, 3 * D, tn.params["wo"]->bt3, 3 * D, (int)T, (int)D, (int)(3 * D), y, D, false);
+            }
             break;
         }
         case CATNN_OP_GQA_ATTENTION: {
@@ -2004,22 +2051,32 @@ int catnn_hip_train_install_ex(catnn_hip_device *dev, const catnn_graph *g, cons
         CATNN_REQUIRE(precision == CATNN_PREC_BF16 || precision == CATNN_PREC_FP32, CATNN_ERR_INVALID_ARGUMENT,
                       "unknown precision " + std::to_string(precision) + " (expected bf16 or fp32)");
         *out = nullptr;
-        auto *t = new catnn_hip_trainer();
+        auto make = [&](bool fuse) {
+            auto *t = new catnn_hip_trainer();
+            try {
+                t->dev = dev;
+                t->graph = *g;
+                t->lr = lr;
+                t->opt = optimizer;
+                t->prec = precision;
+                t->arena_cap = opts->arena_cap;
+                t->fuse_values = fuse;
+                plan_trainer(*t);
+                reserve_and_upload(*t);
+            } catch (...) {
+                if (t->base) (void)hipFree(t->base);
+                delete t;
+                throw;
+            }
+            return t;
+        };
         try {
-            t->dev = dev;
-            t->graph = *g;
-            t->lr = lr;
-            t->opt = optimizer;
-            t->prec = precision;
-            t->arena_cap = opts->arena_cap;
-            plan_trainer(*t);
-            reserve_and_upload(*t);
-        } catch (...) {
-            if (t->base) (void)hipFree(t->base);
-            delete t;
-            throw;
+            *out = make(true);
+        } catch (const Failure &f) {
+            // Under a cap, the unfused plan has more recomputable activations.
+            if (f.code != CATNN_ERR_FIBRATION || !opts->arena_cap || precision != CATNN_PREC_BF16) throw;
+            *out = make(false);
         }
-        *out = t;
     });
 }
 
