@@ -266,10 +266,54 @@ def pmc_probe(which):
     dev.close()
 
 
+def gemm_probe(shapes):
+    """The training step's bf16 GEMM kernel (catnn_hip_gemm_bf16_nt, C = A·Bᵀ
+    with fp32 output) beside torch.matmul on the same bf16 operands (the
+    hipBLASLt library GEMM, bf16 output) on M×N×K shapes: five launches of
+    each for rocprofv3 --pmc, then hipEvent timings of twenty."""
+    import torch
+    import catnn_amd
+    from catnn_amd import device as D
+
+    dev = catnn_amd.Device(0)
+    for (m, n, k) in shapes:
+        a = torch.randn(m, k, device="cuda", dtype=torch.bfloat16)
+        b = torch.randn(n, k, device="cuda", dtype=torch.bfloat16)
+        bt = b.t().contiguous()
+        c = torch.empty(m, n, device="cuda", dtype=torch.float32)
+        torch.cuda.synchronize()
+        ours = lambda: D.gemm_bf16_nt(dev, a.data_ptr(), k, b.data_ptr(), k, c.data_ptr(), n, m, n, k)
+        for _ in range(5):
+            ours()
+        dev.sync()
+        for _ in range(5):
+            torch.matmul(a, bt)
+        torch.cuda.synchronize()
+        dev.timer_start()
+        for _ in range(20):
+            ours()
+        t_ours = dev.timer_stop() / 20
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(20):
+            torch.matmul(a, bt)
+        e1.record()
+        torch.cuda.synchronize()
+        t_lib = e0.elapsed_time(e1) / 20
+        fl = 2.0 * m * n * k
+        print(f"{m}x{n}x{k}: gemm_bf16 {t_ours * 1e3:8.1f} us {fl / t_ours / 1e9:6.0f} TFLOP/s | "
+              f"hipBLASLt {t_lib * 1e3:8.1f} us {fl / t_lib / 1e9:6.0f} TFLOP/s", flush=True)
+        del a, b, bt, c
+    dev.close()
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--pmc-probe", choices=["config2", "config3", "config4", "config5", "all"],
                     help="run the copy calibration and the workload for rocprofv3 --pmc, then exit")
+    ap.add_argument("--gemm-probe", nargs="*", metavar="MxNxK",
+                    help="time the bf16 training GEMM beside hipBLASLt on these shapes (default: the "
+                         "training step's), then exit")
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
@@ -280,6 +324,12 @@ def main():
     args = ap.parse_args()
     if args.pmc_probe:
         pmc_probe(args.pmc_probe)
+        return
+    if args.gemm_probe is not None:
+        shapes = [tuple(int(v) for v in s.split("x")) for s in args.gemm_probe] or [
+            (8192, 3072, 3072), (8192, 4096, 1024), (8192, 1024, 4096), (1024, 4096, 8192),
+            (16384, 7168, 2048), (16384, 1024, 3584), (8192, 8192, 8192)]
+        gemm_probe(shapes)
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build runs on a single MI355X "
