@@ -5,7 +5,7 @@
 // materialises an S×S score matrix per (b,h) and walks it sequentially; here
 // the scores never leave registers.
 //
-// d_head = 64 runs on fp32 MFMA with an online softmax.  The kernel works
+// d_head 32, 64 and 128 run on fp32 MFMA with an online softmax.  The kernel works
 // in the transposed frame so that each lane owns one query:
 //   Sᵀ[j][i] = Σ_d K[j][d]·Q[i][d]   (A = K from LDS, B = Q from registers)
 //   Oᵀ[d][i] += Σ_j V[j][d]·P[i][j]  (A = V from LDS, B = P from registers)
@@ -18,7 +18,7 @@
 // Block: 4 wavefronts × 32 queries = 128 queries of one (b, h); K/V tiles of
 // 64 keys are staged in LDS, double-buffered behind register prefetch.
 // Other head sizes use a one-wavefront-per-query kernel (the reference's
-// small demo blocks have d_head = 4).
+// small demo blocks have d_head = 4, Mixtral-tiny's 8).
 #include <hip/hip_runtime.h>
 
 #include "common.hpp"
@@ -46,7 +46,7 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 // query attention: head h reads K/V head h / group); window > 0 restricts
 // query i to keys [i − window + 1, i] (with causal set).
 template <int DH>
-__global__ __launch_bounds__(256, 2) void attn_mfma_kernel(const float *__restrict__ q,
+__global__ __launch_bounds__(256, DH == 128 ? 1 : 2) void attn_mfma_kernel(const float *__restrict__ q,
                                                            const float *__restrict__ k,
                                                            const float *__restrict__ v,
                                                            int64_t ld, int64_t ldk, int group, int window,
@@ -54,7 +54,7 @@ __global__ __launch_bounds__(256, 2) void attn_mfma_kernel(const float *__restri
                                                            int64_t ldo, float *__restrict__ lse,
                                                            int S, int H, float qscale, int causal,
                                                            int n_qblocks) {
-    static_assert(DH == 64, "MFMA attention is written for d_head = 64");
+    static_assert(DH == 32 || DH == 64 || DH == 128, "MFMA attention: d_head 32, 64 or 128");
     constexpr int BQ = 128, BKV = 64, LDK = DH + 4, LDV = BKV + 4;
     constexpr int KV_IT = BKV * DH / 4 / 256;  // float4 per thread per tile, per operand
     // K row-major; V transposed (Vt[d][key]) so that the four keys a lane
@@ -79,13 +79,14 @@ __global__ __launch_bounds__(256, 2) void attn_mfma_kernel(const float *__restri
     const int wave_qmin = q0 + wave * 32, wave_qmax = wave_qmin + 31;
     const int64_t row_base = (int64_t)b * S;
 
-    // This lane's query, pre-scaled into the log2 domain: Q[i][32g + s].
-    float qf[32];
+    // This lane's query, pre-scaled into the log2 domain: Q[i][(DH/2)·g + s].
+    constexpr int HALF = DH / 2;
+    float qf[HALF];
     if (qi < S) {
         const float4 *src =
-            reinterpret_cast<const float4 *>(q + (row_base + qi) * ld + (int64_t)h * DH + 32 * g);
+            reinterpret_cast<const float4 *>(q + (row_base + qi) * ld + (int64_t)h * DH + HALF * g);
 #pragma unroll
-        for (int c = 0; c < 8; ++c) {
+        for (int c = 0; c < HALF / 4; ++c) {
             const float4 t = src[c];
             qf[4 * c + 0] = t.x * qscale;
             qf[4 * c + 1] = t.y * qscale;
@@ -94,7 +95,7 @@ __global__ __launch_bounds__(256, 2) void attn_mfma_kernel(const float *__restri
         }
     } else {
 #pragma unroll
-        for (int s = 0; s < 32; ++s) qf[s] = 0.f;
+        for (int s = 0; s < HALF; ++s) qf[s] = 0.f;
     }
 
     f32x16 oacc[DH / 32];
@@ -171,9 +172,9 @@ __global__ __launch_bounds__(256, 2) void attn_mfma_kernel(const float *__restri
         if (active[0] && active[1]) {
             // Both key blocks: alternate their accumulator chains so that
             // consecutive MFMAs are independent.
-            const float *k0 = &Ks[buf][lr][32 * g], *k1 = &Ks[buf][32 + lr][32 * g];
+            const float *k0 = &Ks[buf][lr][HALF * g], *k1 = &Ks[buf][32 + lr][HALF * g];
 #pragma unroll
-            for (int c = 0; c < 8; ++c) {
+            for (int c = 0; c < HALF / 4; ++c) {
                 const float4 a = *reinterpret_cast<const float4 *>(k0 + 4 * c);
                 const float4 b = *reinterpret_cast<const float4 *>(k1 + 4 * c);
                 sacc[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.x, qf[4 * c + 0], sacc[0], 0, 0, 0);
@@ -189,12 +190,12 @@ __global__ __launch_bounds__(256, 2) void attn_mfma_kernel(const float *__restri
 #pragma unroll
             for (int kb = 0; kb < BKV / 32; ++kb) {
                 if (!active[kb]) continue;
-                const float *krow = &Ks[buf][kb * 32 + lr][32 * g];
-                float4 kf[8];
+                const float *krow = &Ks[buf][kb * 32 + lr][HALF * g];
+                float4 kf[HALF / 4];
 #pragma unroll
-                for (int c = 0; c < 8; ++c) kf[c] = *reinterpret_cast<const float4 *>(krow + 4 * c);
+                for (int c = 0; c < HALF / 4; ++c) kf[c] = *reinterpret_cast<const float4 *>(krow + 4 * c);
 #pragma unroll
-                for (int c = 0; c < 8; ++c) {
+                for (int c = 0; c < HALF / 4; ++c) {
                     const float4 kv = kf[c];
                     sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.x, qf[4 * c + 0], sacc[kb], 0, 0, 0);
                     sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.y, qf[4 * c + 1], sacc[kb], 0, 0, 0);
@@ -368,16 +369,20 @@ static void attention_fwd(hipStream_t s, const float *q, const float *k, const f
     CATNN_REQUIRE(batch * seq < (1ll << 31), CATNN_ERR_SHAPE_MISMATCH, "attention: too many rows");
     if (batch == 0 || seq == 0) return;
     const float scale = 1.0f / sqrtf((float)d_head);
-    const bool mfma = d_head == 64 && ld_qkv % 4 == 0 && ldk % 4 == 0 && ldo % 4 == 0 && aligned16(q) &&
-                      aligned16(k) && aligned16(v) && aligned16(ctx);
+    const bool mfma = (d_head == 32 || d_head == 64 || d_head == 128) && ld_qkv % 4 == 0 && ldk % 4 == 0 &&
+                      ldo % 4 == 0 && aligned16(q) && aligned16(k) && aligned16(v) && aligned16(ctx);
     const int win = (int)std::min<int64_t>(std::max<int64_t>(window, 0), seq);
     if (mfma) {
         const int nqb = (int)((seq + 127) / 128);
         const int64_t blocks = batch * n_heads * nqb;
         CATNN_REQUIRE(blocks < (1ll << 31), CATNN_ERR_SHAPE_MISMATCH, "attention: grid too large");
-        attn_mfma_kernel<64><<<(unsigned)blocks, 256, 0, s>>>(
-            q, k, v, ld_qkv, ldk, (int)group, win, ctx, ldo, lse, (int)seq, (int)n_heads, scale * kLog2e,
-            causal ? 1 : 0, nqb);
+        auto launch = [&](auto kern) {
+            kern<<<(unsigned)blocks, 256, 0, s>>>(q, k, v, ld_qkv, ldk, (int)group, win, ctx, ldo, lse, (int)seq,
+                                                  (int)n_heads, scale * kLog2e, causal ? 1 : 0, nqb);
+        };
+        if (d_head == 32) launch(attn_mfma_kernel<32>);
+        else if (d_head == 64) launch(attn_mfma_kernel<64>);
+        else launch(attn_mfma_kernel<128>);
     } else {
         const int64_t waves = batch * n_heads * seq;
         const int64_t blocks = (waves + 3) / 4;

@@ -107,6 +107,8 @@ def _gqa_node(r, d, nh, nkv, hd, window, theta=10000, scale=1.0):
     (1, 300, 4, 4, 64, 100),     # MFMA core with a window across tile edges
     (1, 130, 4, 2, 64, 128),     # window one tile wide
     (1, 37, 2, 1, 10, 5),        # head_dim not a multiple of 4
+    (2, 150, 4, 2, 32, None),    # MFMA core, head_dim 32
+    (1, 200, 4, 1, 128, 70),     # MFMA core, head_dim 128, window
 ])
 def test_gqa_attention(device, B, S, nh, nkv, hd, window):
     r = np.random.default_rng(S * 31 + hd)

@@ -163,7 +163,10 @@ ATTN_CASES = [
     (1, 100, 2, 64),   # ragged sequence
     (1, 1, 1, 64),
     (2, 300, 3, 64),
-    (1, 130, 2, 32),
+    (1, 130, 2, 32),   # MFMA kernel, d_head 32
+    (2, 200, 2, 128),  # MFMA kernel, d_head 128 (one block per CU)
+    (1, 65, 3, 128),
+    (1, 96, 2, 48),    # generic kernel
 ]
 
 
