@@ -12,7 +12,8 @@
 //    sit exactly where the MFMA reads its B operand;
 //  * dQ: a block owns 128 queries, the transposed frame of the forward
 //    (Sᵀ = K·Qᵀ, dPᵀ = V·dOᵀ, dQᵀ += Kᵀ·dSᵀ), lane l owning query l%32.
-// Other head sizes use one-wavefront-per-row kernels.
+// d_head 32, 64 and 128 take these kernels; other head sizes use
+// one-wavefront-per-row kernels.
 // Grouped K/V heads (gqa_backward, adjoint.rs:287-440): query head h reads
 // K/V head h / group; a dK/dV block owns the keys of one K/V head and sums
 // over the group's query heads in head order, so dK and dV need no atomics.
@@ -84,12 +85,12 @@ __global__ __launch_bounds__(256) void attn_dot64_kernel(const float *__restrict
 __device__ __forceinline__ int tsw(int d) { return ((d >> 3) & 7) << 2; }
 
 template <int DH>
-__global__ __launch_bounds__(256, 2) void attn_bwd_dkdv_kernel(
+__global__ __launch_bounds__(256, DH == 128 ? 1 : 2) void attn_bwd_dkdv_kernel(
     const float *__restrict__ q, int64_t ldq, const float *__restrict__ k, const float *__restrict__ v,
     int64_t ldk, const float *__restrict__ dout, int64_t ldo, const float *__restrict__ lse,
     const float *__restrict__ Dv, float *__restrict__ dk, float *__restrict__ dv, int64_t ldd, int S,
     int H, int group, int window, float qscale, float scale, int causal, int n_kblocks) {
-    static_assert(DH == 64, "written for d_head = 64");
+    static_assert(DH == 32 || DH == 64 || DH == 128, "d_head 32, 64 or 128");
     constexpr int BKEY = 128, BQ = 64, LDQ = DH + 4, LDT = BQ + 4;
     constexpr int IT = BQ * DH / 4 / 256;
     // Q and dO tiles row-major (the S and dP products read rows along d)
@@ -112,19 +113,19 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkdv_kernel(
     const int wave_kmin = k0 + wave * 32;
     const int64_t row_base = (int64_t)b * S;
 
-    float kf[32], vf[32];
+    float kf[DH / 2], vf[DH / 2];
     if (kj < S) {
-        const float4 *ks = reinterpret_cast<const float4 *>(k + (row_base + kj) * ldk + (int64_t)hk * DH + 32 * g);
-        const float4 *vs = reinterpret_cast<const float4 *>(v + (row_base + kj) * ldk + (int64_t)hk * DH + 32 * g);
+        const float4 *ks = reinterpret_cast<const float4 *>(k + (row_base + kj) * ldk + (int64_t)hk * DH + (DH / 2) * g);
+        const float4 *vs = reinterpret_cast<const float4 *>(v + (row_base + kj) * ldk + (int64_t)hk * DH + (DH / 2) * g);
 #pragma unroll
-        for (int c = 0; c < 8; ++c) {
+        for (int c = 0; c < DH / 8; ++c) {
             const float4 a = ks[c], bb = vs[c];
             kf[4 * c] = a.x; kf[4 * c + 1] = a.y; kf[4 * c + 2] = a.z; kf[4 * c + 3] = a.w;
             vf[4 * c] = bb.x; vf[4 * c + 1] = bb.y; vf[4 * c + 2] = bb.z; vf[4 * c + 3] = bb.w;
         }
     } else {
 #pragma unroll
-        for (int s = 0; s < 32; ++s) kf[s] = vf[s] = 0.f;
+        for (int s = 0; s < DH / 2; ++s) kf[s] = vf[s] = 0.f;
     }
     f32x16 dka[DH / 32], dva[DH / 32];
 #pragma unroll
@@ -202,10 +203,10 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkdv_kernel(
             f32x16 sa, pa;
 #pragma unroll
             for (int r = 0; r < 16; ++r) sa[r] = pa[r] = 0.f;
-            const float *qrow = &Qs[qb * 32 + lr][32 * g];
-            const float *orow = &Os[qb * 32 + lr][32 * g];
+            const float *qrow = &Qs[qb * 32 + lr][(DH / 2) * g];
+            const float *orow = &Os[qb * 32 + lr][(DH / 2) * g];
 #pragma unroll
-            for (int c = 0; c < 8; ++c) {
+            for (int c = 0; c < DH / 8; ++c) {
                 const float4 qv = *reinterpret_cast<const float4 *>(qrow + 4 * c);
                 const float4 ov = *reinterpret_cast<const float4 *>(orow + 4 * c);
                 sa = __builtin_amdgcn_mfma_f32_32x32x2f32(qv.x, kf[4 * c + 0], sa, 0, 0, 0);
@@ -268,12 +269,12 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkdv_kernel(
 }
 
 template <int DH>
-__global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(
+__global__ __launch_bounds__(256, DH == 128 ? 1 : 2) void attn_bwd_dq_kernel(
     const float *__restrict__ q, int64_t ldq, const float *__restrict__ k, const float *__restrict__ v,
     int64_t ldk, const float *__restrict__ dout, int64_t ldo, const float *__restrict__ lse,
     const float *__restrict__ Dv, float *__restrict__ dq, int64_t ldd, int S, int H, int group, int window,
     float qscale, float scale, int causal, int n_qblocks) {
-    static_assert(DH == 64, "written for d_head = 64");
+    static_assert(DH == 32 || DH == 64 || DH == 128, "d_head 32, 64 or 128");
     constexpr int BQ = 128, BKV = 64, LDK = DH + 4, LDT = BKV + 4;
     constexpr int KV_IT = BKV * DH / 4 / 256;
     // K and V row-major (Sᵀ and dPᵀ read rows along d); K also transposed,
@@ -293,13 +294,13 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(
     const int wave_qmin = q0 + wave * 32, wave_qmax = wave_qmin + 31;
     const int64_t row_base = (int64_t)b * S;
 
-    float qf[32], of[32];
+    float qf[DH / 2], of[DH / 2];
     float lse_i = 0.f, D_i = 0.f;
     if (qi < S) {
-        const float4 *qs = reinterpret_cast<const float4 *>(q + (row_base + qi) * ldq + (int64_t)h * DH + 32 * g);
-        const float4 *os = reinterpret_cast<const float4 *>(dout + (row_base + qi) * ldo + (int64_t)h * DH + 32 * g);
+        const float4 *qs = reinterpret_cast<const float4 *>(q + (row_base + qi) * ldq + (int64_t)h * DH + (DH / 2) * g);
+        const float4 *os = reinterpret_cast<const float4 *>(dout + (row_base + qi) * ldo + (int64_t)h * DH + (DH / 2) * g);
 #pragma unroll
-        for (int c = 0; c < 8; ++c) {
+        for (int c = 0; c < DH / 8; ++c) {
             const float4 a = qs[c], bb = os[c];
             qf[4 * c] = a.x * qscale; qf[4 * c + 1] = a.y * qscale;
             qf[4 * c + 2] = a.z * qscale; qf[4 * c + 3] = a.w * qscale;
@@ -309,7 +310,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(
         D_i = Dv[(row_base + qi) * H + h];
     } else {
 #pragma unroll
-        for (int s = 0; s < 32; ++s) qf[s] = of[s] = 0.f;
+        for (int s = 0; s < DH / 2; ++s) qf[s] = of[s] = 0.f;
     }
     f32x16 dqa[DH / 32];
 #pragma unroll
@@ -368,10 +369,10 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(
 #pragma unroll
             for (int r = 0; r < 16; ++r) sa[r] = pa[r] = 0.f;
             {
-                const float *krow = &Ks[buf][kb * 32 + lr][32 * g];
-                const float *vrow = &Vs[buf][kb * 32 + lr][32 * g];
+                const float *krow = &Ks[buf][kb * 32 + lr][(DH / 2) * g];
+                const float *vrow = &Vs[buf][kb * 32 + lr][(DH / 2) * g];
 #pragma unroll
-                for (int c = 0; c < 8; ++c) {
+                for (int c = 0; c < DH / 8; ++c) {
                     const float4 kv = *reinterpret_cast<const float4 *>(krow + 4 * c);
                     const float4 vv = *reinterpret_cast<const float4 *>(vrow + 4 * c);
                     sa = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.x, qf[4 * c + 0], sa, 0, 0, 0);
@@ -570,19 +571,24 @@ void attention_core_bwd_gqa(hipStream_t s, const float *q, int64_t ldq, const fl
     float *D = scratch;
     attention_rowdot(s, o, dout, ldo, rows, n_heads, d_head, D);
     const float scale = 1.0f / sqrtf((float)d_head);
-    const bool mfma = d_head == 64 && ldq % 4 == 0 && ldk % 4 == 0 && ldo % 4 == 0 && ld_dq % 4 == 0 &&
-                      ld_dkv % 4 == 0 && al16(q) && al16(k) && al16(v) && al16(dout) && al16(dq) &&
-                      al16(dk) && al16(dv);
+    const bool mfma = (d_head == 32 || d_head == 64 || d_head == 128) && ldq % 4 == 0 && ldk % 4 == 0 &&
+                      ldo % 4 == 0 && ld_dq % 4 == 0 && ld_dkv % 4 == 0 && al16(q) && al16(k) && al16(v) &&
+                      al16(dout) && al16(dq) && al16(dk) && al16(dv);
     if (mfma) {
         const int nkb = (int)((seq + 127) / 128);
-        attn_bwd_dkdv_kernel<64><<<(unsigned)(batch * HK * nkb), 256, 0, s>>>(
-            q, ldq, k, v, ldk, dout, ldo, lse, D, dk, dv, ld_dkv, (int)seq, (int)n_heads, (int)group, win,
-            scale * kLog2e, scale, causal ? 1 : 0, nkb);
-        CATNN_HIP(hipGetLastError());
-        attn_bwd_dq_kernel<64><<<(unsigned)(batch * n_heads * nkb), 256, 0, s>>>(
-            q, ldq, k, v, ldk, dout, ldo, lse, D, dq, ld_dq, (int)seq, (int)n_heads, (int)group, win,
-            scale * kLog2e, scale, causal ? 1 : 0, nkb);
-        CATNN_HIP(hipGetLastError());
+        auto launch = [&](auto dkdv, auto dqk) {
+            dkdv<<<(unsigned)(batch * HK * nkb), 256, 0, s>>>(q, ldq, k, v, ldk, dout, ldo, lse, D, dk, dv, ld_dkv,
+                                                              (int)seq, (int)n_heads, (int)group, win,
+                                                              scale * kLog2e, scale, causal ? 1 : 0, nkb);
+            CATNN_HIP(hipGetLastError());
+            dqk<<<(unsigned)(batch * n_heads * nkb), 256, 0, s>>>(q, ldq, k, v, ldk, dout, ldo, lse, D, dq, ld_dq,
+                                                                  (int)seq, (int)n_heads, (int)group, win,
+                                                                  scale * kLog2e, scale, causal ? 1 : 0, nkb);
+            CATNN_HIP(hipGetLastError());
+        };
+        if (d_head == 32) launch(attn_bwd_dkdv_kernel<32>, attn_bwd_dq_kernel<32>);
+        else if (d_head == 64) launch(attn_bwd_dkdv_kernel<64>, attn_bwd_dq_kernel<64>);
+        else launch(attn_bwd_dkdv_kernel<128>, attn_bwd_dq_kernel<128>);
     } else {
         const unsigned qblocks = (unsigned)((batch * n_heads * seq + 3) / 4);
         const unsigned kblocks = (unsigned)((batch * HK * seq + 3) / 4);

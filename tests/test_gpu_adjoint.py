@@ -201,9 +201,10 @@ def test_mix_graph_step(device):
 
 
 @pytest.mark.parametrize("causal", [True, False])
-def test_attention(device, causal):
+@pytest.mark.parametrize("heads,dh", [(2, 64), (4, 32), (1, 128)])  # the MFMA adjoint's head sizes
+def test_attention(device, causal, heads, dh):
     r = np.random.default_rng(3)
-    d, heads, dh, b, s = 128, 2, 64, 2, 96
+    d, b, s = 128, 2, 96
     params = {p: _t(0.05 * r.standard_normal((d, d))) for p in ("wq", "wk", "wv", "wo")}
     node = IrNode(4, "attn", OpenOp.attention(heads, d, dh, causal), TensorType.f32([b, s, d]), params)
     _check(device, node, [r.standard_normal((b, s, d))], FP32_TOL)
@@ -276,15 +277,17 @@ def test_repeated_adjoint_calls_reuse_the_plan_and_take_new_values(device):
         assert ev[1][3] == Tensor.from_numpy(dy).checksum()
 
 
-# GqaAttention (gqa_backward, adjoint.rs:287-440): d_head 64 takes the MFMA
-# adjoint kernels, other head sizes the generic ones; grouped K/V heads,
-# sliding windows, a ragged sequence and n_heads·head_dim ≠ d_model.
+# GqaAttention (gqa_backward, adjoint.rs:287-440): d_head 32, 64 and 128 take
+# the MFMA adjoint kernels, other head sizes the generic ones; grouped K/V
+# heads, sliding windows, a ragged sequence and n_heads·head_dim ≠ d_model.
 @pytest.mark.parametrize("B,S,D,nh,nkv,hd,window,theta", [
     (2, 128, 256, 4, 2, 64, None, 10000),
     (1, 200, 256, 4, 1, 64, 50, 1000000),
     (1, 130, 128, 2, 2, 64, 1, 10000),
     (2, 9, 32, 4, 2, 8, 3, 10000),
     (1, 77, 48, 6, 2, 10, None, 500),
+    (1, 150, 128, 4, 2, 32, 40, 10000),
+    (1, 140, 256, 2, 1, 128, None, 10000),
 ])
 def test_gqa(device, B, S, D, nh, nkv, hd, window, theta):
     r = np.random.default_rng(S + nh)
