@@ -644,15 +644,17 @@ __device__ __forceinline__ void tile_dma(unsigned char *smem, const GemmBf16Para
         b_src[q] = base + (int64_t)n * p.ldb + (lpos ^ C::sw(r)) * 8;
     }
     const uint32_t lds0 = lds_addr(smem);
+    const int kwrap = p.b_kwrap;
     auto issue = [&](int kt) {
         const uint32_t st = lds0 + (kt % C::STAGES) * C::STAGE_BYTES;
         const int k0 = k_lo + kt * BK;
+        const int kb0 = kwrap ? k0 % kwrap : k0;  // whole chunks: kwrap is a multiple of BK
 #pragma unroll
         for (int q = 0; q < C::A_LD; ++q)
             load_lds16_at(a_src[q] + k0, st + (wave * C::A_LD + q) * 1024);  // RPL rows × ROWB = 1 KiB
 #pragma unroll
         for (int q = 0; q < C::B_LD; ++q)
-            load_lds16_at(b_src[q] + k0, st + BM * ROWB + (wave * C::B_LD + q) * 1024);
+            load_lds16_at(b_src[q] + kb0, st + BM * ROWB + (wave * C::B_LD + q) * 1024);
     };
 
     f32x16 acc[FM][FN];
@@ -725,13 +727,14 @@ __device__ __forceinline__ void tile_dma(unsigned char *smem, const GemmBf16Para
                 if (n < p.N) src = base + (int64_t)n * p.ldb;
             }
             uint4 v = make_uint4(0, 0, 0, 0);
+            const int ks = (r >= BM && kwrap) ? kk % kwrap : kk;  // B's column of k = kk
             if (src && kk < k_hi) {
                 if (kk + 8 <= k_hi) {
-                    v = *reinterpret_cast<const uint4 *>(src + kk);
+                    v = *reinterpret_cast<const uint4 *>(src + ks);
                 } else {
                     uint16_t e[8];
 #pragma unroll
-                    for (int j = 0; j < 8; ++j) e[j] = kk + j < k_hi ? src[kk + j] : 0;
+                    for (int j = 0; j < 8; ++j) e[j] = kk + j < k_hi ? src[ks + j] : 0;
                     v = make_uint4(e[0] | (uint32_t)e[1] << 16, e[2] | (uint32_t)e[3] << 16,
                                    e[4] | (uint32_t)e[5] << 16, e[6] | (uint32_t)e[7] << 16);
                 }
@@ -924,6 +927,9 @@ void gemm_bf16_launch_cfg(hipStream_t s, const GemmBf16Params &p, int cfg) {
         }
     }
     if (cfg >= 7 && !vec) cfg = dual ? 0 : 2;  // direct-to-LDS tiles need 16-byte aligned rows
+    CATNN_REQUIRE(!p.b_kwrap || (cfg >= 7 && p.b_kwrap % 64 == 0 && p.K % p.b_kwrap == 0 &&
+                                 p.ldb >= p.b_kwrap),
+                  CATNN_ERR_INVALID_ARGUMENT, "bf16 gemm: a wrapping B needs aligned rows and whole k chunks");
     // The staged epilogue moves 8 consecutive outputs per access: every
     // output, saved and residual row must start on a 16-byte boundary.
     GemmBf16Params q = p;

@@ -63,6 +63,8 @@ struct GemmBf16Params {
     int segk_aligned;            // GRID_SEGK: caller guarantees seg_offsets[e] % 8 == 0
     int ksplit;                  // GRID_SEGK with seg_offsets null: segment e is [e·ksplit, (e+1)·ksplit) ∩ [0, K)
     int vec_epi;                 // set by the launcher: output rows allow 16-byte epilogue accesses
+    int b_kwrap;                 // > 0: B's k index wraps at b_kwrap (B has b_kwrap columns; K a multiple
+                                 // of it and of 64): [x_hi | x_lo]·[w | w] without a doubled copy of w
     int max_tiles;
     int n_experts;
     const bf16_t *B_e[kMaxExperts];

@@ -65,6 +65,9 @@ int64_t numel(const std::vector<int64_t> &d) {
 
 constexpr int kPad = 128;  // MoE expert segments start on multiples of the GEMM tile
 
+// The MoE gate/up B operand wraps its k index at H (whole 64-deep chunks).
+bool moe_kwrap(int64_t H) { return H % 64 == 0; }
+
 // The bf16 step runs an Attention node's core on bf16 MFMA (attention_bf16.hip)
 // where that kernel covers its head size; q, k, v then live as bf16.
 bool attn_core_bf16(const Node &nd, int64_t D) {
@@ -879,8 +882,11 @@ static void plan_trainer(Tr &t) {
                 for (int64_t e = 0; e < E; ++e) {
                     const std::string p = "e" + std::to_string(e);
                     // w1's bf16 copy holds [w1 | w3] per row: the B operand of dx = [da | dc]·[w1 | w3]ᵀ.
-                    add_param(tn, p + ".w1", H, I, true, false, host(nd, p + ".w1")->data, true, 2 * I);
-                    add_param(tn, p + ".w3", H, I, true, false, host(nd, p + ".w3")->data, true, 2 * I,
+                    // The gate/up GEMM reads wᵀ twice over K = 2H ([x_hi | x_lo]·[wᵀ | wᵀ]): as a
+                    // k-wrapping B on the plain transposed copy, or as the first 2H of the split copy.
+                    const bool wrap = moe_kwrap(H);
+                    add_param(tn, p + ".w1", H, I, true, wrap, host(nd, p + ".w1")->data, !wrap, 2 * I);
+                    add_param(tn, p + ".w3", H, I, true, wrap, host(nd, p + ".w3")->data, !wrap, 2 * I,
                               tn.params[p + ".w1"], I);
                     add_param(tn, p + ".w2", I, H, true, true, host(nd, p + ".w2")->data);
                 }
@@ -1504,12 +1510,16 @@ static void forward_node(Tr &t, TNode &tn) {
             p.seg_offsets = offs; p.seg_counts = counts; p.max_tiles = max_tiles; p.n_experts = (int)E;
             // gate/up: h = silu(x·w1)·(x·w3), a and c kept for the adjoint;
             // [hi|lo] of x against [hi|hi] of the weights over 2H.
+            const bool wrap = moe_kwrap(H);
             p.A = x3; p.lda = 3 * H; p.a_rows = sop; p.a_row_div = (int)K;
             for (int64_t e = 0; e < E; ++e) {
-                p.B_e[e] = tn.params["e" + std::to_string(e) + ".w1"]->bt3;
-                p.B2_e[e] = tn.params["e" + std::to_string(e) + ".w3"]->bt3;
+                const TParam *w1 = tn.params["e" + std::to_string(e) + ".w1"];
+                const TParam *w3 = tn.params["e" + std::to_string(e) + ".w3"];
+                p.B_e[e] = wrap ? w1->bt : w1->bt3;
+                p.B2_e[e] = wrap ? w3->bt : w3->bt3;
             }
-            p.ldb = 3 * H; p.M = 0; p.N = (int)I; p.K = (int)(2 * H);
+            p.ldb = wrap ? H : 3 * H; p.b_kwrap = wrap ? (int)H : 0;
+            p.M = 0; p.N = (int)I; p.K = (int)(2 * H);
             p.epi = k::EPI_SWIGLU_FWD;
             p.Cb = (bf16_t *)tn.B("h"); p.ldcb = I;
             p.S1 = (bf16_t *)tn.B("a"); p.S2 = (bf16_t *)tn.B("c"); p.lds = I;
@@ -1521,7 +1531,7 @@ static void forward_node(Tr &t, TNode &tn) {
                 q.B_e[e] = tn.params["e" + std::to_string(e) + ".w2"]->bt;
                 q.B2_e[e] = nullptr;
             }
-            q.ldb = I; q.N = (int)H; q.K = (int)I;
+            q.ldb = I; q.N = (int)H; q.K = (int)I; q.b_kwrap = 0;
             q.epi = k::EPI_STORE; q.Cb = nullptr; q.S1 = q.S2 = nullptr;
             q.C32 = (float *)tn.B("ys"); q.ldc32 = H;
             k::gemm_bf16_launch(s, q);
