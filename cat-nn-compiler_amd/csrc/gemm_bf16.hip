@@ -16,6 +16,8 @@
 // Epilogues and grids are listed in gemm_bf16.hpp.
 #include <hip/hip_runtime.h>
 
+#include <utility>
+
 #include "common.hpp"
 #include "devmath.hpp"
 #include "gemm_bf16.hpp"
@@ -34,7 +36,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 // MFMAs, so wider wavefront tiles relieve the LDS port.
 template <int BM_, int BN_, int WAVES_M_, int WAVES_N_, int BK_>
 struct Cfg {
-    static constexpr bool DMA = false;
+    static constexpr bool DMA = false, PP = false;
     static constexpr int BM = BM_, BN = BN_, WAVES_M = WAVES_M_, WAVES_N = WAVES_N_;
     static constexpr int BK = BK_, LDT = BK + 8;  // LDS row stride (bf16): conflict-free b128 reads
     static constexpr int LDS_BYTES = 2 * (BM + BN) * LDT * 2;
@@ -67,7 +69,7 @@ using Cfg2 = Cfg<128, 128, 2, 2, 64>;
 // wave load fills 16 rows; chunk c of row r sits at c ^ ((r / 4) mod 4).
 template <int BM_, int BN_, int WAVES_M_, int WAVES_N_, int STAGES_, int BK_ = 64>
 struct DCfg {
-    static constexpr bool DMA = true;
+    static constexpr bool DMA = true, PP = false;
     static constexpr int BM = BM_, BN = BN_, WAVES_M = WAVES_M_, WAVES_N = WAVES_N_, STAGES = STAGES_;
     static constexpr int BK = BK_;
     static constexpr int ROWB = BK * 2, CPR = BK / 8, RPL = 64 / CPR;  // row bytes, chunks a row, rows a wave load
@@ -98,6 +100,36 @@ struct DCfg {
 using Cfg7 = DCfg<128, 128, 2, 2, 2>;
 using Cfg9 = DCfg<128, 128, 2, 2, 3>;
 using Cfg10 = DCfg<128, 128, 2, 2, 4, 32>;  // 32-deep chunks, four stages in the same 64 KiB
+
+// Ping-pong tiles: 256 × 256 outputs, eight wavefronts in two groups of
+// four (group g owns rows 128g … 128g+127, wavefront i of a group columns
+// 64i … 64i+63), one block per CU.  A 128 × 128 tile at full MFMA rate asks
+// 64 B/clk per CU of its operands from L2 (two blocks per CU); this one half
+// that.  The two groups take turns: while one group's wavefronts issue their
+// MFMAs, the other's read their next fragments from LDS, so each SIMD's
+// matrix core always has one wavefront feeding it.  k chunks are 32 deep
+// (64-byte rows, chunk c of row r at c ^ (r/4 mod 4)) in four 32 KiB stages;
+// the loads of a chunk are issued by the wavefronts in their MFMA phase, one
+// after every fourth MFMA (a burst of them stalls the issuing wavefront for
+// as long as the CU's address unit takes to accept them, ~1000 cycles for a
+// whole chunk).  Measured (plain grid, TFLOP/s) against the 128 × 128 tile:
+// 8192³ 1278 vs 1011, 16384×7168×2048 1102 vs 894, 16384×1024×3584 1193
+// vs 997, 8192×4096×1024 890 vs 677; with fewer than one tile per CU it
+// loses (8192×1024×4096, 128 tiles: 812 vs 982).
+template <int STAGES_>
+struct PCfg {
+    static constexpr bool DMA = true, PP = true;
+    static constexpr int BM = 256, BN = 256, WAVES_M = 2, WAVES_N = 4, STAGES = STAGES_;
+    static constexpr int BK = 32, ROWB = 64, CPR = 4, RPL = 16;
+    static constexpr int NT = 512, NW = 8, FM = 4, FN = 2;
+    static constexpr int STAGE_BYTES = (BM + BN) * ROWB;  // 32 KiB
+    static constexpr int LDS_BYTES = STAGES * STAGE_BYTES;
+    static constexpr int LPW = (BM + BN) / (RPL * NW);  // wave loads per wavefront and chunk
+    static __device__ __forceinline__ int sw(int r) { return (r >> 2) & 3; }
+    static_assert(LPW == 4 && BM == 4 * LPW * RPL, "wavefronts 0-3 load A rows, 4-7 B rows");
+    static_assert(STAGES == 4, "the main loop's waits assume four stages");
+};
+using Cfg11 = PCfg<4>;
 
 
 __device__ __forceinline__ float bf2f(bf16_t v) { return __uint_as_float((uint32_t)v << 16); }
@@ -175,12 +207,24 @@ __device__ __forceinline__ void epi_elem(const GemmBf16Params &p, float v, float
 // block (mi, ni) is row wrow0 + 32·mi + 8(r/4) + r%4, column wcol0 + 32·ni.
 // A wavefront whose whole tile lies inside the output takes the loop
 // without bounds checks.
+// f(integral_constant<int, i>) for i = 0 … N−1, expanded at compile time
+// (a loop the compiler left rolled would index the accumulators at run time
+// and move them to scratch memory).
+template <class F, int... I>
+__device__ __forceinline__ void static_for_seq(F &&f, std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F &&f) {
+    static_for_seq(f, std::make_integer_sequence<int, N>{});
+}
+
 template <class C, bool DUAL, int EPI, bool CHECK>
 __device__ __forceinline__ void epilogue_loop(const GemmBf16Params &p, const f32x16 (&acc)[C::FM][C::FN],
                                               int wrow0, int wcol0, int row_end, float *__restrict__ C32) {
     constexpr int NF = DUAL ? C::FN / 2 : C::FN;
-#pragma unroll
-    for (int mi = 0; mi < C::FM; ++mi)
+    static_for<C::FM>([&](auto mi_c) __attribute__((always_inline)) {
+        constexpr int mi = decltype(mi_c)::value;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const int row = wrow0 + mi * 32 + 8 * (r >> 2) + (r & 3);
@@ -192,6 +236,7 @@ __device__ __forceinline__ void epilogue_loop(const GemmBf16Params &p, const f32
                 epi_elem<DUAL, EPI>(p, acc[mi][ni][r], DUAL ? acc[mi][ni + NF][r] : 0.f, row, col, C32);
             }
         }
+    });
 }
 
 template <class C, bool DUAL, int EPI>
@@ -510,62 +555,73 @@ __device__ __forceinline__ void epilogue_staged(unsigned char *smem, const GemmB
                                                 const f32x16 (&acc)[C::FM][C::FN], int row0, int col0,
                                                 float *__restrict__ C32) {
     constexpr int BM = C::BM, BN = C::BN, WM = BM / C::WAVES_M, CH = (DUAL ? BN / 2 : BN) / 8;
-    static_assert(BM * BN * 4 <= C::LDS_BYTES, "the staged tile must fit the operand stages");
+    // A tile larger than the operand stages goes through LDS in slices of
+    // SR rows (whole wavefront rows), one after the other.
+    constexpr int SL = BM * BN * 4 <= C::LDS_BYTES ? 1 : 2, SR = BM / SL;
+    static_assert(SR * BN * 4 <= C::LDS_BYTES && SR % WM == 0, "the staged slice must fit the operand stages");
     float *t = reinterpret_cast<float *>(smem);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = wave / C::WAVES_N, wn = wave % C::WAVES_N, lr = lane & 31, lg = lane >> 5;
     dma_sync<0>();  // every wavefront is done with the operand stages
     // Adjoint epilogues read an operand per output: issue all of this
-    // thread's loads now, so that they are in flight while the tile is
-    // staged (the barrier below waits for the LDS writes only).
-    constexpr bool PRE = !DUAL && (EPI == EPI_SWIGLU_BWD || EPI == EPI_GELU_BWD) && (BM * CH) % C::NT == 0;
-    constexpr int IT = PRE ? BM * CH / C::NT : 1;
+    // thread's loads of the slice now, so that they are in flight while the
+    // slice is staged (the barrier below waits for the LDS writes only).
+    constexpr bool PRE = !DUAL && (EPI == EPI_SWIGLU_BWD || EPI == EPI_GELU_BWD) && (SR * CH) % C::NT == 0;
+    constexpr int IT = PRE ? SR * CH / C::NT : 1;
     static_assert(2 * IT < 64, "preloads must fit the vmcnt counter");
-    uint4 pre[IT][2];
-    if constexpr (PRE) {
 #pragma unroll
-        for (int i = 0; i < IT; ++i) {
-            const int idx = threadIdx.x + i * C::NT;
-            epi_preload<EPI>(p, row0 + idx / CH, col0 + (idx % CH) * 8, pre[i]);
+    for (int sl = 0; sl < SL; ++sl) {
+        const int srow0 = row0 + sl * SR;
+        uint4 pre[IT][2];
+        if constexpr (PRE) {
+#pragma unroll
+            for (int i = 0; i < IT; ++i) {
+                const int idx = threadIdx.x + i * C::NT;
+                epi_preload<EPI>(p, srow0 + idx / CH, col0 + (idx % CH) * 8, pre[i]);
+            }
         }
-    }
+        if (SL == 1 || wm * WM / SR == sl) {
 #pragma unroll
-    for (int mi = 0; mi < C::FM; ++mi)
+            for (int mi = 0; mi < C::FM; ++mi)
 #pragma unroll
-        for (int ni = 0; ni < C::FN; ++ni)
+                for (int ni = 0; ni < C::FN; ++ni)
 #pragma unroll
-            for (int r = 0; r < 16; ++r)
-                t[(wm * WM + mi * 32 + 8 * (r >> 2) + 4 * lg + (r & 3)) * BN + staged_col<C, DUAL>(wn, ni, lr)] =
-                    acc[mi][ni][r];
-    if constexpr (PRE) {
-        dma_sync<63>();  // LDS writes of every wavefront visible; preloads may still be in flight
-#pragma unroll
-        for (int i = 0; i < IT; ++i) {
-            const int idx = threadIdx.x + i * C::NT;
-            const int r = idx / CH, c = (idx % CH) * 8;
-            float v[8];
-            load8f(t + r * BN + c, v);
-            epi_vec8<EPI>(p, v, row0 + r, col0 + c, C32, pre[i]);
+                    for (int r = 0; r < 16; ++r)
+                        t[(wm * WM - sl * SR + mi * 32 + 8 * (r >> 2) + 4 * lg + (r & 3)) * BN +
+                          staged_col<C, DUAL>(wn, ni, lr)] = acc[mi][ni][r];
         }
-        return;
-    }
-    dma_sync<0>();
-    for (int idx = threadIdx.x; idx < BM * CH; idx += C::NT) {
-        const int r = idx / CH, c = (idx % CH) * 8;
-        float v[8];
-        load8f(t + r * BN + c, v);
-        if constexpr (DUAL) {
-            float cv[8], h[8];
-            load8f(t + r * BN + BN / 2 + c, cv);
-            const int64_t so = (int64_t)(row0 + r) * p.lds + col0 + c;
-            if (p.S1) *reinterpret_cast<uint4 *>(p.S1 + so) = pack8(v);
-            if (p.S2) *reinterpret_cast<uint4 *>(p.S2 + so) = pack8(cv);
+        if constexpr (PRE) {
+            dma_sync<63>();  // LDS writes of every wavefront visible; preloads may still be in flight
 #pragma unroll
-            for (int j = 0; j < 8; ++j) h[j] = v[j] * sigmoid_hw(v[j]) * cv[j];
-            *reinterpret_cast<uint4 *>(p.Cb + (int64_t)(row0 + r) * p.ldcb + col0 + c) = pack8(h);
+            for (int i = 0; i < IT; ++i) {
+                const int idx = threadIdx.x + i * C::NT;
+                const int r = idx / CH, c = (idx % CH) * 8;
+                float v[8];
+                load8f(t + r * BN + c, v);
+                epi_vec8<EPI>(p, v, srow0 + r, col0 + c, C32, pre[i]);
+            }
         } else {
-            epi_vec8<EPI>(p, v, row0 + r, col0 + c, C32);
+            dma_sync<0>();
+            for (int idx = threadIdx.x; idx < SR * CH; idx += C::NT) {
+                const int r = idx / CH, c = (idx % CH) * 8;
+                float v[8];
+                load8f(t + r * BN + c, v);
+                if constexpr (DUAL) {
+                    float cv[8], h[8];
+                    load8f(t + r * BN + BN / 2 + c, cv);
+                    const int64_t so = (int64_t)(srow0 + r) * p.lds + col0 + c;
+                    if (p.S1) *reinterpret_cast<uint4 *>(p.S1 + so) = pack8(v);
+                    if (p.S2) *reinterpret_cast<uint4 *>(p.S2 + so) = pack8(cv);
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) h[j] = v[j] * sigmoid_hw(v[j]) * cv[j];
+                    *reinterpret_cast<uint4 *>(p.Cb + (int64_t)(srow0 + r) * p.ldcb + col0 + c) = pack8(h);
+                } else {
+                    epi_vec8<EPI>(p, v, srow0 + r, col0 + c, C32);
+                }
+            }
         }
+        // the next slice overwrites the staged rows: every read of them done
+        if (sl + 1 < SL) dma_sync<63>();
     }
 }
 
@@ -752,11 +808,216 @@ __device__ __forceinline__ void tile_dma(unsigned char *smem, const GemmBf16Para
                               C32);
 }
 
+// s_waitcnt vmcnt ≤ N and lgkmcnt 0, without a barrier.
+template <int N>
+__device__ __forceinline__ void wait_vm_lgkm() {
+    static_assert(N >= 0 && N < 64, "vmcnt");
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
+    asm volatile("" ::: "memory");
+}
+
+__device__ __forceinline__ void block_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// The ping-pong main loop (PCfg).  Chunk j lands in stage j mod 4.  Group
+// 1 starts one barrier later than group 0, so between consecutive barriers
+// one group is in its memory phase (read chunk j's fragments from LDS, then
+// wait until chunk j+1 is in LDS) while the other is in its MFMA phase
+// (16 MFMAs on the fragments it read, with this wavefront's four loads of
+// chunk j+3 issued among them).  Chunk j+3 goes to the stage chunk j−1
+// used, which both groups finished reading before the MFMA phase of chunk
+// j began; every wavefront waits for its own loads of chunk j+1 at the end
+// of its memory phase of chunk j, and the barrier after that wait precedes
+// the first read of chunk j+1 by either group.  After the loop group 0
+// takes one more barrier, so both groups pass the same number.  A partial
+// last chunk goes through registers, computed by all eight wavefronts.
+template <class C, bool DUAL, int GRID>
+__device__ __forceinline__ void tile_pp(unsigned char *smem, const GemmBf16Params &p, const bf16_t *__restrict__ B,
+                                        const bf16_t *__restrict__ B2, int row0, int row_end, int col0, int k_lo,
+                                        int k_hi, float *__restrict__ C32) {
+    constexpr int BM = C::BM, BN = C::BN, FM = C::FM, FN = C::FN, BK = C::BK, ROWB = C::ROWB, S = C::STAGES;
+    constexpr int LPW = C::LPW, CPR = C::CPR;
+    constexpr int BN_OUT = DUAL ? BN / 2 : BN, WCOLS = BN_OUT / C::WAVES_N;
+    auto b_row_src = [&](int r, int &n) -> const bf16_t * {
+        if (DUAL && r >= BN / 2) {
+            n = col0 + r - BN / 2;
+            return B2;
+        }
+        n = col0 + r;
+        return B;
+    };
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int g = wave / C::WAVES_N, wn = wave % C::WAVES_N;
+    const int lr = lane & 31, lg = lane >> 5;
+
+    // Wave load q of wavefront w fills combined rows 16(4w + q) … +15 of
+    // [A tile; B tile] (wavefronts 0-3: A, 4-7: B): lane l row … + l/4 at
+    // position l mod 4, i.e. k chunk (l mod 4) ^ sw(row).  Rows past the
+    // tile's end read row row0 (col0 for B): their outputs are never stored.
+    const bool ld_b = wave >= 4;
+    const int lrow = lane / CPR, lpos = lane % CPR;
+    const bf16_t *src[LPW];
+#pragma unroll
+    for (int q = 0; q < LPW; ++q) {
+        const int r = (wave & 3) * (LPW * C::RPL) + q * C::RPL + lrow;  // row within the A or B tile
+        const int off = (lpos ^ C::sw(r)) * 8;
+        if (!ld_b) {
+            int gr = row0 + r;
+            if (gr >= row_end) gr = row0;
+            const int srow = p.a_rows ? p.a_rows[gr] / p.a_row_div : gr;
+            src[q] = p.A + (int64_t)srow * p.lda + off;
+        } else {
+            int n;
+            const bf16_t *base = b_row_src(r, n);
+            if (n >= p.N) n = col0;
+            src[q] = base + (int64_t)n * p.ldb + off;
+        }
+    }
+    const uint32_t lds_w = lds_addr(smem) + wave * LPW * 1024;
+    const int kwrap = ld_b ? p.b_kwrap : 0;
+    // k offset of chunk kt in this wavefront's operand (B's wraps: whole chunks, kwrap a multiple of BK)
+    auto koff = [&](int kt) {
+        const int k0 = k_lo + kt * BK;
+        return kwrap ? k0 % kwrap : k0;
+    };
+
+    f32x16 acc[FM][FN];
+#pragma unroll
+    for (int mi = 0; mi < FM; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < FN; ++ni)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[mi][ni][r] = 0.f;
+
+    // Lane l reads k values 16s + 8(l/32) … +7 of row l mod 32 of each block;
+    // fragment rows start on multiples of 32, so their swizzle is sw(l mod 32).
+    const int swl = C::sw(lr);
+    const int a_off = (g * (BM / C::WAVES_M) + lr) * ROWB;
+    int b_off[FN];
+#pragma unroll
+    for (int ni = 0; ni < FN; ++ni) b_off[ni] = (BM + staged_col<C, DUAL>(wn, ni, lr)) * ROWB;
+
+    const int nfull = (k_hi - k_lo) / BK;
+    for (int c = 0; c < S - 1 && c < nfull; ++c) {
+        const int ko = koff(c);
+#pragma unroll
+        for (int q = 0; q < LPW; ++q) load_lds16_at(src[q] + ko, lds_w + c * C::STAGE_BYTES + q * 1024);
+    }
+    {  // chunk 0 in LDS; chunks 1 … min(nfull, S−1)−1 may stay in flight
+        const int after = min(nfull - 1, S - 2);
+        if (after >= 2) wait_vm_lgkm<2 * LPW>();
+        else if (after == 1) wait_vm_lgkm<LPW>();
+        else wait_vm_lgkm<0>();
+    }
+    block_barrier();
+    if (g == 1) block_barrier();
+    bf16x8 fa[2][FM], fb[2][FN];
+    for (int j = 0; j < nfull; ++j) {
+        // memory phase: chunk j's fragments
+        __builtin_amdgcn_sched_barrier(0);
+        const unsigned char *st = smem + (j % S) * C::STAGE_BYTES;
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            const int pos = ((2 * s + lg) ^ swl) << 4;
+#pragma unroll
+            for (int mi = 0; mi < FM; ++mi)
+                fa[s][mi] = *reinterpret_cast<const bf16x8 *>(st + a_off + mi * 32 * ROWB + pos);
+#pragma unroll
+            for (int ni = 0; ni < FN; ++ni) fb[s][ni] = *reinterpret_cast<const bf16x8 *>(st + b_off[ni] + pos);
+        }
+        {  // this wavefront's loads of chunk j+1 done; chunks j+2 … min(nfull−1, j+S−2) may stay in flight
+            const int after = min(nfull - 1, j + S - 2) - (j + 1);
+            if (after >= 1) wait_vm_lgkm<LPW>();
+            else wait_vm_lgkm<0>();
+        }
+        block_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        // MFMA phase, with the loads of chunk j+S−1
+        const int kt = j + S - 1;
+        const bool iss = kt < nfull;
+        const int ko = iss ? koff(kt) : 0;
+        const uint32_t dst = lds_w + (kt % S) * C::STAGE_BYTES;
+#pragma unroll
+        for (int t = 0; t < 2 * FM * FN; ++t) {
+            const int s = t / (FM * FN), mi = (t / FN) % FM, ni = t % FN;
+            acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[s][mi], fb[s][ni], acc[mi][ni], 0, 0, 0);
+            if ((t & 3) == 1) {
+                if (iss) load_lds16_at(src[t >> 2] + ko, dst + (t >> 2) * 1024);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        block_barrier();
+    }
+    if (g == 0) block_barrier();
+    const int kt0 = k_lo + nfull * BK;
+    if (kt0 < k_hi) {
+        // every wavefront is past its last read of the stages (the loop's barriers)
+        for (int idx = tid; idx < (BM + BN) * CPR; idx += C::NT) {
+            const int r = idx / CPR, c = idx % CPR, kk = kt0 + 8 * c;
+            const bf16_t *src1 = nullptr;
+            if (r < BM) {
+                const int gr = row0 + r;
+                if (gr < row_end) src1 = p.A + (int64_t)(p.a_rows ? p.a_rows[gr] / p.a_row_div : gr) * p.lda;
+            } else {
+                int n;
+                const bf16_t *base = b_row_src(r - BM, n);
+                if (n < p.N) src1 = base + (int64_t)n * p.ldb;
+            }
+            uint4 v = make_uint4(0, 0, 0, 0);
+            const int ks = (r >= BM && p.b_kwrap) ? kk % p.b_kwrap : kk;  // B's column of k = kk
+            if (src1 && kk < k_hi) {
+                if (kk + 8 <= k_hi) {
+                    v = *reinterpret_cast<const uint4 *>(src1 + ks);
+                } else {
+                    uint16_t e[8];
+#pragma unroll
+                    for (int q = 0; q < 8; ++q) e[q] = kk + q < k_hi ? src1[ks + q] : 0;
+                    v = make_uint4(e[0] | (uint32_t)e[1] << 16, e[2] | (uint32_t)e[3] << 16,
+                                   e[4] | (uint32_t)e[5] << 16, e[6] | (uint32_t)e[7] << 16);
+                }
+            }
+            // B rows start at BM, a multiple of 16: the same swizzle as row r − BM
+            *reinterpret_cast<uint4 *>(smem + r * ROWB + ((c ^ C::sw(r)) << 4)) = v;
+        }
+        dma_sync<0>();
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            const int pos = ((2 * s + lg) ^ swl) << 4;
+#pragma unroll
+            for (int mi = 0; mi < FM; ++mi)
+                fa[0][mi] = *reinterpret_cast<const bf16x8 *>(smem + a_off + mi * 32 * ROWB + pos);
+#pragma unroll
+            for (int ni = 0; ni < FN; ++ni) fb[0][ni] = *reinterpret_cast<const bf16x8 *>(smem + b_off[ni] + pos);
+#pragma unroll
+            for (int mi = 0; mi < FM; ++mi)
+#pragma unroll
+                for (int ni = 0; ni < FN; ++ni)
+                    acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[0][mi], fb[0][ni], acc[mi][ni], 0, 0, 0);
+        }
+    }
+    // Plain fp32 stores go straight from the accumulators (each store
+    // instruction writes whole 128-byte row runs); epilogues with bf16
+    // outputs or per-output operands go through LDS in two 128-row slices.
+    const bool staged = DUAL || p.epi != EPI_STORE || p.Cb;
+    if (staged && p.vec_epi && row0 + BM <= row_end && col0 + BN_OUT <= p.N)
+        finish_staged<C, DUAL, GRID>(smem, p, acc, row0, col0, C32);
+    else
+        finish<C, DUAL, GRID>(p, acc, row0 + g * (BM / C::WAVES_M) + 4 * lg, col0 + wn * WCOLS + lr, row_end, C32);
+}
+
 template <class C, bool VEC, bool DUAL, int GRID>
 __device__ __forceinline__ void run_tile(unsigned char *smem, const GemmBf16Params &p, const bf16_t *B,
                                          const bf16_t *B2, int row0, int row_end, int col0, int k_lo, int k_hi,
                                          float *C32) {
-    if constexpr (C::DMA) {
+    if constexpr (C::PP) {
+        static_assert(VEC, "direct-to-LDS tiles take 16-byte aligned rows");
+        tile_pp<C, DUAL, GRID>(smem, p, B, B2, row0, row_end, col0, k_lo, k_hi, C32);
+    } else if constexpr (C::DMA) {
         static_assert(VEC, "direct-to-LDS tiles take 16-byte aligned rows");
         tile_dma<C, DUAL, GRID>(smem, p, B, B2, row0, row_end, col0, k_lo, k_hi, C32);
     } else {
@@ -778,7 +1039,7 @@ __global__ __launch_bounds__(C::NT) void gemm_bf16_kernel(GemmBf16Params p) {
         grouped_tile(lid, tiles_m, tiles_n, 8, tm, tn);
         run_tile<C, VEC, DUAL, GRID>(smem, p, p.B, p.B2, tm * C::BM, p.M, tn * bn_out, 0, p.K, p.C32);
     } else if constexpr (GRID == GRID_ROWS) {
-        // Tiles of the table are kRowTile rows; C::BM equals it for this grid.
+        // Tiles of the table are C::BM rows (the launcher passes the table built for C::BM).
         int tm, tn;
         grouped_tile(lid, p.max_tiles, tiles_n, 8, tm, tn);
         if (tm >= *p.n_tiles) return;
@@ -865,7 +1126,7 @@ void launch_cfg(hipStream_t s, const GemmBf16Params &p, bool vec, bool dual, uns
     } else if (p.grid == GRID_SEGK) {
         launch_kernel<C, GRID_SEGK, false>(s, p, vec, grid);
     } else {
-        if constexpr (C::BM == kRowTile) {
+        if constexpr (C::BM == kRowTile || C::BM == 256) {
             if constexpr (DUAL_OK) {
                 if (dual) {
                     launch_kernel<C, GRID_ROWS, true>(s, p, vec, grid);
@@ -874,14 +1135,102 @@ void launch_cfg(hipStream_t s, const GemmBf16Params &p, bool vec, bool dual, uns
             }
             launch_kernel<C, GRID_ROWS, false>(s, p, vec, grid);
         } else {
-            fail(CATNN_ERR_INVALID_ARGUMENT, "bf16 gemm: grouped rows need 128-row tiles");
+            fail(CATNN_ERR_INVALID_ARGUMENT, "bf16 gemm: grouped rows need 128- or 256-row tiles");
         }
     }
+}
+
+// One thread lists the 128-row and the 256-row tiles of every segment.
+__global__ void build_tiles2_kernel(const int32_t *__restrict__ offsets, int n_experts, int32_t *__restrict__ t1,
+                                    int max1, int32_t *__restrict__ t2, int max2) {
+    if (threadIdx.x != 0 || blockIdx.x != 0) return;
+    for (int w = 0; w < 2; ++w) {
+        int32_t *t = w ? t2 : t1;
+        const int mx = w ? max2 : max1, bm = w ? 256 : kRowTile;
+        int n = 0;
+        for (int e = 0; e < n_experts; ++e)
+            for (int r = offsets[e]; r < offsets[e + 1] && n < mx; r += bm) {
+                t[n] = e;
+                t[mx + n] = r;
+                ++n;
+            }
+        t[2 * mx] = n;
+    }
+}
+
+int max_tiles_for(int64_t rows, int n_experts, int bm) { return (int)((rows + bm - 1) / bm + n_experts); }
+
+int device_cus() {
+    static int cus[64] = {};
+    int dev = 0;
+    CATNN_HIP(hipGetDevice(&dev));
+    if (dev < 0 || dev >= 64) return 256;
+    if (!cus[dev]) CATNN_HIP(hipDeviceGetAttribute(&cus[dev], hipDeviceAttributeMultiprocessorCount, dev));
+    return cus[dev];
+}
+
+// Tile configuration of an automatic launch.  The grid runs in rounds of
+// concurrent tiles: 256 × 256 tiles one per CU, 128 × 128 tiles two per CU.
+// A 256 × 256 tile does the work of four 128 × 128 tiles in 4 / 1.2 of the
+// time a CU takes for them (the measured plain-grid throughput ratio), so
+// it wins when ⌈T256 / CUs⌉ · 4 / 1.2 < ⌈T128 / 2·CUs⌉ · 2: many tiles, or
+// a grid that fills its last round.  A grouped grid's tile count is only
+// known on the device; its bound (segments padded) is used.  k ranges
+// under 256 stay on the 128 × 128 tile, and so does the SwiGLU adjoint
+// under 2048: at one block per CU nothing overlaps a tile's epilogue, and
+// that epilogue (two bf16 operands read, two written per output) outweighs
+// the main loop's gain at short k (config 5, K = 1024: 324 against 296 µs).
+int pick_cfg(const GemmBf16Params &p) {
+    if (p.epi == EPI_SWIGLU_BWD && p.K < 2048) return 7;
+    const bool dual = p.epi == EPI_SWIGLU_FWD;
+    const int64_t tn2 = (p.N + (dual ? 127 : 255)) / (dual ? 128 : 256);
+    const int64_t tn1 = (p.N + (dual ? 63 : 127)) / (dual ? 64 : 128);
+    int64_t t2, t1, klen;
+    if (p.grid == GRID_PLAIN) {
+        t2 = (p.M + 255) / 256 * tn2;
+        t1 = (p.M + 127) / 128 * tn1;
+        klen = p.K;
+    } else if (p.grid == GRID_ROWS) {
+        if (!p.tiles256) return 7;
+        t2 = (int64_t)p.max_tiles256 * tn2;
+        t1 = (int64_t)p.max_tiles * tn1;
+        klen = p.K;
+    } else {
+        const int64_t e = p.n_experts > 0 ? p.n_experts : 1;
+        t2 = (p.M + 255) / 256 * tn2 * e;
+        t1 = (p.M + 127) / 128 * tn1 * e;
+        klen = p.seg_offsets ? p.K / e : p.ksplit;
+    }
+    if (klen < 256) return 7;
+    const int64_t cus = device_cus();
+    const double pp = (double)((t2 + cus - 1) / cus) * 4.0 / 1.2;
+    const double c7 = (double)((t1 + 2 * cus - 1) / (2 * cus)) * 2.0;
+    return pp < c7 ? 11 : 7;
 }
 
 }  // namespace
 
 int gemm_bf16_tile_rows() { return kRowTile; }
+
+int64_t gemm_bf16_tiles_ints(int64_t rows, int n_experts) {
+    return 2 * (int64_t)max_tiles_for(rows, n_experts, kRowTile) + 1 + 2 * (int64_t)max_tiles_for(rows, n_experts, 256) + 1;
+}
+
+void gemm_bf16_build_tiles(hipStream_t s, const int32_t *offsets, int n_experts, int64_t rows, int32_t *tiles) {
+    const int m1 = max_tiles_for(rows, n_experts, kRowTile), m2 = max_tiles_for(rows, n_experts, 256);
+    build_tiles2_kernel<<<1, 64, 0, s>>>(offsets, n_experts, tiles, m1, tiles + 2 * m1 + 1, m2);
+    CATNN_HIP(hipGetLastError());
+}
+
+void gemm_bf16_use_tiles(GemmBf16Params &p, const int32_t *tiles, int64_t rows, int n_experts) {
+    const int m1 = max_tiles_for(rows, n_experts, kRowTile), m2 = max_tiles_for(rows, n_experts, 256);
+    p.tile_expert = tiles;
+    p.tile_row0 = tiles + m1;
+    p.n_tiles = tiles + 2 * m1;
+    p.max_tiles = m1;
+    p.tiles256 = tiles + 2 * m1 + 1;
+    p.max_tiles256 = m2;
+}
 
 // Up to 8 splits while the split grid stays within 512 tiles (two per CU)
 // and each segment keeps 1024 or more k values; only grids of at most 128
@@ -934,12 +1283,20 @@ void gemm_bf16_launch_cfg(hipStream_t s, const GemmBf16Params &p, int cfg) {
     // output, saved and residual row must start on a 16-byte boundary.
     GemmBf16Params q = p;
     q.vec_epi = epi_rows_aligned(p);
+    if (cfg == 11 && p.grid == GRID_ROWS) {
+        CATNN_REQUIRE(p.tiles256, CATNN_ERR_INVALID_ARGUMENT, "bf16 gemm: 256-row tiles need their tile table");
+        q.tile_expert = p.tiles256;
+        q.tile_row0 = p.tiles256 + p.max_tiles256;
+        q.n_tiles = p.tiles256 + 2 * p.max_tiles256;
+        q.max_tiles = p.max_tiles256;
+    }
     switch (cfg) {
         case 0: launch_cfg<Cfg0, true>(s, q, vec, dual, gy); break;
         case 2: launch_cfg<Cfg2, false>(s, q, vec, dual, gy); break;
         case 7: launch_cfg<Cfg7, true>(s, q, vec, dual, gy); break;
         case 9: launch_cfg<Cfg9, false>(s, q, vec, dual, gy); break;
         case 10: launch_cfg<Cfg10, true>(s, q, vec, dual, gy); break;
+        case 11: launch_cfg<Cfg11, true>(s, q, vec, dual, gy); break;
         default: fail(CATNN_ERR_INVALID_ARGUMENT, "bf16 gemm: unknown tile configuration");
     }
 }
@@ -952,8 +1309,9 @@ void gemm_bf16_launch_cfg(hipStream_t s, const GemmBf16Params &p, int cfg) {
 // 782 and 655 for four 32-deep stages (configuration 10); the register-staged
 // tiles reached 742, 881 and 585.  Launches without 16-byte aligned rows run
 // on the register-staged tiles (configuration 0 for the SwiGLU forward, 2
-// otherwise).
-void gemm_bf16_launch(hipStream_t s, const GemmBf16Params &p) { gemm_bf16_launch_cfg(s, p, 7); }
+// otherwise).  The ping-pong tile (configuration 11) takes over when its
+// grid fills the GPU (pick_cfg).
+void gemm_bf16_launch(hipStream_t s, const GemmBf16Params &p) { gemm_bf16_launch_cfg(s, p, pick_cfg(p)); }
 
 }  // namespace k
 }  // namespace catnn

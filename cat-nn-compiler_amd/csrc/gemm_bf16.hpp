@@ -66,6 +66,8 @@ struct GemmBf16Params {
     int b_kwrap;                 // > 0: B's k index wraps at b_kwrap (B has b_kwrap columns; K a multiple
                                  // of it and of 64): [x_hi | x_lo]·[w | w] without a doubled copy of w
     int max_tiles;
+    const int32_t *tiles256;  // GRID_ROWS: the table of 256-row tiles (gemm_bf16_build_tiles), or null
+    int max_tiles256;
     int n_experts;
     const bf16_t *B_e[kMaxExperts];
     const bf16_t *B2_e[kMaxExperts];
@@ -73,9 +75,16 @@ struct GemmBf16Params {
 };
 
 void gemm_bf16_launch(hipStream_t s, const GemmBf16Params &p);
-// The same with a fixed tile configuration (0, 2, 7 or 9; see gemm_bf16.hip).
+// The same with a fixed tile configuration (0, 2, 7, 9, 10 or 11; see gemm_bf16.hip).
 void gemm_bf16_launch_cfg(hipStream_t s, const GemmBf16Params &p, int cfg);
 int gemm_bf16_tile_rows();
+// Tile tables of the grouped grid for `rows` routed rows (T·k) over
+// n_experts segments: 128-row and 256-row tiles of each segment, in expert
+// order, built by one launch into `tiles` (gemm_bf16_tiles_ints int32s);
+// gemm_bf16_use_tiles points a GRID_ROWS launch at both.
+int64_t gemm_bf16_tiles_ints(int64_t rows, int n_experts);
+void gemm_bf16_build_tiles(hipStream_t s, const int32_t *offsets, int n_experts, int64_t rows, int32_t *tiles);
+void gemm_bf16_use_tiles(GemmBf16Params &p, const int32_t *tiles, int64_t rows, int n_experts);
 // K splits for a plain store/accumulate GEMM whose tiles alone leave the
 // GPU's CUs idle (1 = no split); gemm_bf16_splitk_len gives the segment.
 int gemm_bf16_splitk(int64_t M, int64_t N, int64_t K);

@@ -669,14 +669,13 @@ static void plan_trainer(Tr &t) {
                     add_param(tn, p + ".w3", H, I, true, false, host(nd, p + ".w3")->data);
                     add_param(tn, p + ".w2", I, H, true, false, host(nd, p + ".w2")->data);
                 }
-                const int64_t max_tiles = (T * K + k::gemm_bf16_tile_rows() - 1) / k::gemm_bf16_tile_rows() + E;
                 tape(tn, "idx", (uint64_t)(T * K) * 4, true);  // readable after the step
                 tape(tn, "w", (uint64_t)(T * K) * 4);
                 tape(tn, "counts", (uint64_t)E * 4);
                 tape(tn, "offsets", (uint64_t)(E + 1) * 4);
                 tape(tn, "sop", (uint64_t)Pr * 4);
                 tape(tn, "pos", (uint64_t)(T * K) * 4);
-                tape(tn, "tiles", (uint64_t)(2 * max_tiles + 1) * 4);
+                tape(tn, "tiles", (uint64_t)k::gemm_bf16_tiles_ints(T * K, (int)E) * 4);
                 tape(tn, "perm_scratch", k::moe_permute_scratch_bytes(T, K, E));
                 for (const char *nm : {"a", "c", "h"}) tape(tn, nm, (uint64_t)(Pr * I) * 4);
                 tape(tn, "ys", (uint64_t)(Pr * H) * 4);
@@ -890,7 +889,6 @@ static void plan_trainer(Tr &t) {
                               tn.params[p + ".w1"], I);
                     add_param(tn, p + ".w2", I, H, true, true, host(nd, p + ".w2")->data);
                 }
-                const int64_t max_tiles = (T * K + k::gemm_bf16_tile_rows() - 1) / k::gemm_bf16_tile_rows() + E;
                 tape(tn, "x3", (uint64_t)(T * 3 * H) * 2);
                 tape(tn, "idx", (uint64_t)(T * K) * 4, true);  // readable after the step
                 tape(tn, "w", (uint64_t)(T * K) * 4);
@@ -898,7 +896,7 @@ static void plan_trainer(Tr &t) {
                 tape(tn, "offsets", (uint64_t)(E + 1) * 4);
                 tape(tn, "sop", (uint64_t)Pr * 4);
                 tape(tn, "pos", (uint64_t)(T * K) * 4);
-                tape(tn, "tiles", (uint64_t)(2 * max_tiles + 1) * 4);
+                tape(tn, "tiles", (uint64_t)k::gemm_bf16_tiles_ints(T * K, (int)E) * 4);
                 tape(tn, "perm_scratch", k::moe_permute_scratch_bytes(T, K, E));
                 tape(tn, "a", (uint64_t)(Pr * I) * 2);
                 tape(tn, "c", (uint64_t)(Pr * I) * 2);
@@ -1126,16 +1124,15 @@ static void forward_gemm_f32(Tr &t, TNode &tn) {
             int32_t *pos = (int32_t *)tn.B("pos"), *tiles = (int32_t *)tn.B("tiles");
             float *w = (float *)tn.B("w");
             float *a = (float *)tn.B("a"), *c = (float *)tn.B("c"), *h = (float *)tn.B("h");
-            const int max_tiles = (int)((T * K + k::gemm_bf16_tile_rows() - 1) / k::gemm_bf16_tile_rows() + E);
             k::moe_route_f32(s, x, tn.params["gate"]->master, T, H, E, K, idx, w, nullptr);
             k::moe_permute_padded(s, idx, T, K, E, kPad, Pr, counts, offs, sop, pos, tn.B("perm_scratch"));
-            k::build_tiles(s, offs, (int)E, tiles, tiles + max_tiles, tiles + 2 * max_tiles);
+            k::gemm_bf16_build_tiles(s, offs, (int)E, T * K, tiles);
             bf16_t *x6 = (bf16_t *)tn.B("x6"), *h6 = (bf16_t *)tn.B("h6");
             k::split6_rows(s, x, H, T, (int)H, false, x6, 6 * H);
             k::GemmBf16Params p = gp();
             p.grid = k::GRID_ROWS;
-            p.tile_expert = tiles; p.tile_row0 = tiles + max_tiles; p.n_tiles = tiles + 2 * max_tiles;
-            p.seg_offsets = offs; p.seg_counts = counts; p.max_tiles = max_tiles; p.n_experts = (int)E;
+            k::gemm_bf16_use_tiles(p, tiles, T * K, (int)E);
+            p.seg_offsets = offs; p.seg_counts = counts; p.n_experts = (int)E;
             p.epi = k::EPI_STORE;
             // a = x·w1, c = x·w3 per expert segment, rows gathered through the permutation
             p.A = x6; p.lda = 6 * H; p.a_rows = sop; p.a_row_div = (int)K;
@@ -1255,14 +1252,13 @@ static void backward_gemm_f32(Tr &t, TNode &tn) {
             int32_t *offs = (int32_t *)tn.B("offsets"), *sop = (int32_t *)tn.B("sop");
             int32_t *pos = (int32_t *)tn.B("pos"), *tiles = (int32_t *)tn.B("tiles");
             int32_t *seg6 = (int32_t *)tn.B("seg6");
-            const int max_tiles = (int)((T * K + k::gemm_bf16_tile_rows() - 1) / k::gemm_bf16_tile_rows() + E);
             float *w = F("w"), *dw = F("dw"), *dys = F("dys");
             k::moe_slot_grads_f32(s, sop, w, F("ys"), dy, (int)K, (int)H, (int)Pr, dys, dw);
             k::split6_rows(s, dys, H, Pr, (int)H, false, B("dys6"), 6 * H);
             k::GemmBf16Params p = gp();
             p.grid = k::GRID_ROWS;
-            p.tile_expert = tiles; p.tile_row0 = tiles + max_tiles; p.n_tiles = tiles + 2 * max_tiles;
-            p.seg_offsets = offs; p.seg_counts = counts; p.max_tiles = max_tiles; p.n_experts = (int)E;
+            k::gemm_bf16_use_tiles(p, tiles, T * K, (int)E);
+            p.seg_offsets = offs; p.seg_counts = counts; p.n_experts = (int)E;
             p.epi = k::EPI_STORE;
             // dh = dys·w2ᵀ
             p.A = B("dys6"); p.lda = 6 * H; p.ldb = 6 * H; p.N = (int)I; p.K = (int)(6 * H);
@@ -1498,16 +1494,15 @@ static void forward_node(Tr &t, TNode &tn) {
             int32_t *offs = (int32_t *)tn.B("offsets"), *sop = (int32_t *)tn.B("sop");
             int32_t *pos = (int32_t *)tn.B("pos"), *tiles = (int32_t *)tn.B("tiles");
             float *w = (float *)tn.B("w");
-            const int max_tiles = (int)((T * K + k::gemm_bf16_tile_rows() - 1) / k::gemm_bf16_tile_rows() + E);
             k::moe_route_f32(s, x, tn.params["gate"]->master, T, H, E, K, idx, w, nullptr);
             k::moe_permute_padded(s, idx, T, K, E, kPad, Pr, counts, offs, sop, pos, tn.B("perm_scratch"));
-            k::build_tiles(s, offs, (int)E, tiles, tiles + max_tiles, tiles + 2 * max_tiles);
+            k::gemm_bf16_build_tiles(s, offs, (int)E, T * K, tiles);
             bf16_t *x3 = (bf16_t *)tn.B("x3");
             k::split3_rows(s, x, H, T, (int)H, x3, 3 * H);
             k::GemmBf16Params p = gp();
             p.grid = k::GRID_ROWS;
-            p.tile_expert = tiles; p.tile_row0 = tiles + max_tiles; p.n_tiles = tiles + 2 * max_tiles;
-            p.seg_offsets = offs; p.seg_counts = counts; p.max_tiles = max_tiles; p.n_experts = (int)E;
+            k::gemm_bf16_use_tiles(p, tiles, T * K, (int)E);
+            p.seg_offsets = offs; p.seg_counts = counts; p.n_experts = (int)E;
             // gate/up: h = silu(x·w1)·(x·w3), a and c kept for the adjoint;
             // [hi|lo] of x against [hi|hi] of the weights over 2H.
             const bool wrap = moe_kwrap(H);
@@ -1745,7 +1740,6 @@ static void backward_node(Tr &t, TNode &tn) {
             int32_t *idx = (int32_t *)tn.B("idx"), *counts = (int32_t *)tn.B("counts");
             int32_t *offs = (int32_t *)tn.B("offsets"), *sop = (int32_t *)tn.B("sop");
             int32_t *pos = (int32_t *)tn.B("pos"), *tiles = (int32_t *)tn.B("tiles");
-            const int max_tiles = (int)((T * K + k::gemm_bf16_tile_rows() - 1) / k::gemm_bf16_tile_rows() + E);
             float *w = (float *)tn.B("w"), *dw = (float *)tn.B("dw");
             bf16_t *dys = (bf16_t *)tn.B("dys"), *dadc = (bf16_t *)tn.B("dadc");
             float *dxs = (float *)tn.B("dxs");
@@ -1753,8 +1747,8 @@ static void backward_node(Tr &t, TNode &tn) {
             k::moe_slot_grads(s, sop, w, (float *)tn.B("ys"), dy, (int)K, (int)H, (int)Pr, dys, dw);
             k::GemmBf16Params p = gp();
             p.grid = k::GRID_ROWS;
-            p.tile_expert = tiles; p.tile_row0 = tiles + max_tiles; p.n_tiles = tiles + 2 * max_tiles;
-            p.seg_offsets = offs; p.seg_counts = counts; p.max_tiles = max_tiles; p.n_experts = (int)E;
+            k::gemm_bf16_use_tiles(p, tiles, T * K, (int)E);
+            p.seg_offsets = offs; p.seg_counts = counts; p.n_experts = (int)E;
             // dh = dys·w2ᵀ, then da = dh·c·silu'(a), dc = dh·silu(a), side by
             // side in one row: [da | dc]
             p.A = dys; p.lda = H;
@@ -2027,7 +2021,7 @@ int catnn_hip_gemm_bf16_nt(catnn_hip_device *dev, const uint16_t *a, int64_t lda
         CATNN_REQUIRE(lda >= k && ldb >= k && ldc >= n, CATNN_ERR_SHAPE_MISMATCH, "gemm_bf16: leading dims");
         CATNN_REQUIRE((a && b && c) || m * n == 0, CATNN_ERR_INVALID_ARGUMENT, "gemm_bf16: null operand");
         CATNN_REQUIRE(tile_cfg == -1 || tile_cfg == 0 || tile_cfg == 2 || tile_cfg == 7 || tile_cfg == 9 ||
-                          tile_cfg == 10,
+                          tile_cfg == 10 || tile_cfg == 11,
                       CATNN_ERR_INVALID_ARGUMENT, "gemm_bf16: tile_cfg");
         k::GemmBf16Params p = gp();
         p.A = a; p.lda = lda; p.B = b; p.ldb = ldb;

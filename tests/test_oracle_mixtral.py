@@ -97,13 +97,19 @@ def test_rope_pairs_are_interleaved():
 
 
 def test_lm_head_and_mix():
-    x = RNG.standard_normal((2, 3, 8)).astype(np.float32)
-    w = RNG.standard_normal((11, 8)).astype(np.float32)
+    # Own generator: the draws must not depend on which tests ran before.
+    # Values are O(1), so an absolute bar of 1e-6 covers f32 rounding where
+    # the two terms cancel and still fails a wrong gate weight (off by ~0.1).
+    rng = np.random.default_rng(99)
+    x = rng.standard_normal((2, 3, 8)).astype(np.float32)
+    w = rng.standard_normal((11, 8)).astype(np.float32)
     assert rel_l2(oracle.lm_head(x, w), x.astype(np.float64) @ w.astype(np.float64).T) < 1e-6
-    a, b = RNG.standard_normal(7).astype(np.float32), RNG.standard_normal(7).astype(np.float32)
-    assert np.allclose(oracle.mix(a, b, 0.0), 0.5 * a + 0.5 * b, rtol=1e-6)
+    a, b = rng.standard_normal(7).astype(np.float32), rng.standard_normal(7).astype(np.float32)
+    a64, b64 = a.astype(np.float64), b.astype(np.float64)
+    assert np.allclose(oracle.mix(a, b, 0.0), 0.5 * a64 + 0.5 * b64, rtol=1e-6, atol=1e-6)
     s = 1 / (1 + np.exp(-1.5))
-    assert np.allclose(oracle.mix(a, b, 1.5), s * a + (1 - s) * b, rtol=1e-6)
+    assert np.allclose(oracle.mix(a, b, 1.5), s * a64 + (1 - s) * b64, rtol=1e-6, atol=1e-6)
+    assert not np.allclose(oracle.mix(a, b, 1.5), 0.5 * a64 + 0.5 * b64, rtol=1e-6, atol=1e-6)
 
 
 # ---- Mixtral-tiny known answer (moe.rs:246-322, :418-455, test at :473-485) ----
