@@ -53,7 +53,7 @@ __global__ __launch_bounds__(256, DH == 128 ? 1 : 2) void attn_mfma_kernel(const
                                                            float *__restrict__ o,
                                                            int64_t ldo, float *__restrict__ lse,
                                                            int S, int H, float qscale, int causal,
-                                                           int n_qblocks) {
+                                                           int n_qblocks, int pair_halves) {
     static_assert(DH == 32 || DH == 64 || DH == 128, "MFMA attention: d_head 32, 64 or 128");
     constexpr int BQ = 128, BKV = 64, LDK = DH + 4, LDV = BKV + 4;
     constexpr int KV_IT = BKV * DH / 4 / 256;  // float4 per thread per tile, per operand
@@ -67,10 +67,14 @@ __global__ __launch_bounds__(256, DH == 128 ? 1 : 2) void attn_mfma_kernel(const
     __shared__ float Vt[2][DH][LDV];
 
     // Causal work grows with the query block: start the heavy ones first,
-    // spread evenly over the XCDs.
+    // spread evenly over the XCDs.  pair_halves (a grid of exactly two
+    // blocks per CU, all resident at once): the second half runs light to
+    // heavy, so block i and block i + grid/2, which share a CU, hold query
+    // blocks n−1−k and k and every CU gets the same number of key tiles.
     int blk, bh;
     split_bh_block(blockIdx.x, n_qblocks, (int)(gridDim.x / n_qblocks), blk, bh);
-    const int qb = n_qblocks - 1 - blk;
+    const int half = n_qblocks / 2;
+    const int qb = pair_halves && blk >= half ? blk - half : n_qblocks - 1 - blk;
     const int b = bh / H, h = bh % H, hk = h / group;
     const int q0 = qb * BQ;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -349,6 +353,15 @@ __global__ __launch_bounds__(256) void attn_generic_kernel(const float *__restri
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
+int device_cus() {
+    static int cus[64] = {};
+    int dev = 0;
+    CATNN_HIP(hipGetDevice(&dev));
+    if (dev < 0 || dev >= 64) return 256;
+    if (!cus[dev]) CATNN_HIP(hipDeviceGetAttribute(&cus[dev], hipDeviceAttributeMultiprocessorCount, dev));
+    return cus[dev];
+}
+
 }  // namespace
 
 // ld_qkv: row stride of q; ldk: of k and v, which hold n_heads / group
@@ -376,9 +389,12 @@ static void attention_fwd(hipStream_t s, const float *q, const float *k, const f
         const int nqb = (int)((seq + 127) / 128);
         const int64_t blocks = batch * n_heads * nqb;
         CATNN_REQUIRE(blocks < (1ll << 31), CATNN_ERR_SHAPE_MISMATCH, "attention: grid too large");
+        // Two blocks per CU (d_head ≤ 64): a causal grid of exactly that many
+        // blocks pairs heavy with light query blocks per CU.
+        const int pair = causal && win == 0 && d_head <= 64 && nqb % 2 == 0 && blocks == 2 * (int64_t)device_cus();
         auto launch = [&](auto kern) {
             kern<<<(unsigned)blocks, 256, 0, s>>>(q, k, v, ld_qkv, ldk, (int)group, win, ctx, ldo, lse, (int)seq,
-                                                  (int)n_heads, scale * kLog2e, causal ? 1 : 0, nqb);
+                                                  (int)n_heads, scale * kLog2e, causal ? 1 : 0, nqb, pair);
         };
         if (d_head == 32) launch(attn_mfma_kernel<32>);
         else if (d_head == 64) launch(attn_mfma_kernel<64>);
