@@ -12,6 +12,8 @@
 // (deepseek.rs:229-239).
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "common.hpp"
 #include "devmath.hpp"
 #include "gemm_f32.hpp"
@@ -34,8 +36,10 @@ unsigned blocks_for(int64_t n, int64_t per_block) {
 }
 
 // One wavefront per row, the row held in registers as NV float4 per lane.
-// y = x · (1 / sqrt(mean(x²) + eps)) · w, multiplied in that order.
-template <int NV>
+// y = x · (1 / sqrt(mean(x²) + eps)) · w, multiplied in that order.  FULL:
+// cols == 256·NV, so the w loads of all chunks go out before the first
+// store; the row sum uses the DPP reduction.
+template <int NV, bool FULL>
 __global__ __launch_bounds__(256) void rms_norm_reg_kernel(const float *__restrict__ x,
                                                            const float *__restrict__ w,
                                                            float *__restrict__ y, int64_t rows,
@@ -50,16 +54,16 @@ __global__ __launch_bounds__(256) void rms_norm_reg_kernel(const float *__restri
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
         const int c = lane + i * 64;
-        v[i] = c < c4 ? xr[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+        v[i] = (FULL || c < c4) ? xr[c] : make_float4(0.f, 0.f, 0.f, 0.f);
         s += (v[i].x * v[i].x + v[i].y * v[i].y) + (v[i].z * v[i].z + v[i].w * v[i].w);
     }
-    const float inv = 1.0f / sqrtf(wave_sum(s) / (float)cols + eps);
+    const float inv = 1.0f / sqrtf(wave_sum_dpp(s) / (float)cols + eps);
     const float4 *w4 = reinterpret_cast<const float4 *>(w);
     float4 *yr = reinterpret_cast<float4 *>(y + row * cols);
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
         const int c = lane + i * 64;
-        if (c < c4) {
+        if (FULL || c < c4) {
             const float4 g = w4[c];
             yr[c] = make_float4(v[i].x * inv * g.x, v[i].y * inv * g.y, v[i].z * inv * g.z,
                                 v[i].w * inv * g.w);
@@ -312,11 +316,16 @@ void rms_norm_f32(hipStream_t s, const float *x, const float *w, float *y, int64
     const int64_t c4 = cols / 4;
     if (cols % 4 == 0 && aligned16(x) && aligned16(w) && aligned16(y) && c4 <= 64 * 16) {
         const int c = (int)cols;
-        if (c4 <= 64) rms_norm_reg_kernel<1><<<grid, kThreads, 0, s>>>(x, w, y, rows, c, eps);
-        else if (c4 <= 128) rms_norm_reg_kernel<2><<<grid, kThreads, 0, s>>>(x, w, y, rows, c, eps);
-        else if (c4 <= 256) rms_norm_reg_kernel<4><<<grid, kThreads, 0, s>>>(x, w, y, rows, c, eps);
-        else if (c4 <= 512) rms_norm_reg_kernel<8><<<grid, kThreads, 0, s>>>(x, w, y, rows, c, eps);
-        else rms_norm_reg_kernel<16><<<grid, kThreads, 0, s>>>(x, w, y, rows, c, eps);
+        auto launch = [&](auto nv_c) {
+            constexpr int NV = decltype(nv_c)::value;
+            if (c4 == 64 * NV) rms_norm_reg_kernel<NV, true><<<grid, kThreads, 0, s>>>(x, w, y, rows, c, eps);
+            else rms_norm_reg_kernel<NV, false><<<grid, kThreads, 0, s>>>(x, w, y, rows, c, eps);
+        };
+        if (c4 <= 64) launch(std::integral_constant<int, 1>{});
+        else if (c4 <= 128) launch(std::integral_constant<int, 2>{});
+        else if (c4 <= 256) launch(std::integral_constant<int, 4>{});
+        else if (c4 <= 512) launch(std::integral_constant<int, 8>{});
+        else launch(std::integral_constant<int, 16>{});
     } else {
         rms_norm_any_kernel<<<grid, kThreads, 0, s>>>(x, w, y, rows, cols, eps);
     }

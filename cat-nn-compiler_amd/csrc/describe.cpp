@@ -66,9 +66,21 @@ std::string nv_suffix(int64_t c4, const int *nvs, int n_nv) {
     return "";
 }
 
-void row_kernel(std::vector<Launch> &L, const std::string &reg, const std::string &any, int64_t rows, int64_t cols) {
+// full: the kernel also takes <bool FULL>, true when the row fills its NV
+// float4 per lane exactly (rowops.hip layer_norm_f32, decoder.hip rms_norm_f32).
+void row_kernel(std::vector<Launch> &L, const std::string &reg, const std::string &any, int64_t rows, int64_t cols,
+                bool full = false) {
     static const int nvs[] = {1, 2, 4, 8, 16};
-    const std::string sfx = cols % 4 == 0 ? nv_suffix(cols / 4, nvs, 5) : "";
+    std::string sfx = cols % 4 == 0 ? nv_suffix(cols / 4, nvs, 5) : "";
+    if (full && !sfx.empty()) {
+        int nv = 0;
+        for (int v : nvs)
+            if (cols / 4 <= 64 * v) {
+                nv = v;
+                break;
+            }
+        sfx = "ILi" + std::to_string(nv) + "ELb" + (cols == 256 * nv ? "1" : "0") + "EE";
+    }
     L.push_back({sfx.empty() ? any : reg + sfx, clamp_grid(cdiv(rows, 4)), 256, 0});
 }
 
@@ -132,7 +144,7 @@ std::vector<Launch> launches_of(const Node &node, const std::vector<std::vector<
             break;
         }
         case CATNN_OP_LAYER_NORM:
-            row_kernel(L, "21layer_norm_reg_kernel", "21layer_norm_any_kernel", nx / last, last);
+            row_kernel(L, "21layer_norm_reg_kernel", "21layer_norm_any_kernel", nx / last, last, true);
             break;
         case CATNN_OP_ATTENTION: {
             const int64_t B = x[0], S = x[1], D = x[2], T = B * S;
@@ -171,7 +183,7 @@ std::vector<Launch> launches_of(const Node &node, const std::vector<std::vector<
             break;
         }
         case CATNN_OP_RMS_NORM:
-            row_kernel(L, "19rms_norm_reg_kernel", "19rms_norm_any_kernel", nx / last, last);
+            row_kernel(L, "19rms_norm_reg_kernel", "19rms_norm_any_kernel", nx / last, last, true);
             break;
         case CATNN_OP_EMBEDDING: {
             const int64_t hidden = node.op.a[1];

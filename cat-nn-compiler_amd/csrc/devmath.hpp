@@ -70,6 +70,27 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
+// Sum over the 64 lanes without LDS round trips: DPP swaps within each
+// quad (lanes ^1, ^2), then the half-row and row mirrors (lane i with
+// 7 − i, then 15 − i) leave every lane of a 16-lane row holding that row's
+// sum, the same value in each (each step adds a commutative pair); the four
+// row sums are read from lanes 0, 16, 32, 48 and added in a fixed order.
+// The result is uniform across the wavefront.
+template <int CTRL>
+__device__ __forceinline__ float dpp_move(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+    v += dpp_move<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+    v += dpp_move<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+    v += dpp_move<0x141>(v);  // row_half_mirror
+    v += dpp_move<0x140>(v);  // row_mirror
+    const int b = __float_as_int(v);
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(b, 0)), r1 = __int_as_float(__builtin_amdgcn_readlane(b, 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(b, 32)), r3 = __int_as_float(__builtin_amdgcn_readlane(b, 48));
+    return (r0 + r1) + (r2 + r3);
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));

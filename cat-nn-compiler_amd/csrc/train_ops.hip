@@ -356,7 +356,7 @@ __global__ __launch_bounds__(256) void ln_fwd_kernel(const float *__restrict__ x
             s += v.w;
         }
         const float n = (float)cols;
-        const float mu = wave_sum(s) / n;
+        const float mu = wave_sum_dpp(s) / n;
         float q = 0.f;
         for (int c = lane; c < c4n; c += 64) {
             const float4 v = x4[c];
@@ -366,7 +366,7 @@ __global__ __launch_bounds__(256) void ln_fwd_kernel(const float *__restrict__ x
             q += d2 * d2;
             q += d3 * d3;
         }
-        const float inv = 1.0f / sqrtf(wave_sum(q) / n + eps);
+        const float inv = 1.0f / sqrtf(wave_sum_dpp(q) / n + eps);
         const float4 *g4 = reinterpret_cast<const float4 *>(g), *b4 = reinterpret_cast<const float4 *>(b);
         for (int c = lane; c < c4n; c += 64) {
             const float4 v = x4[c], gv = g4[c], bv = b4[c];
@@ -395,13 +395,13 @@ __global__ __launch_bounds__(256) void ln_fwd_kernel(const float *__restrict__ x
     float s = 0.f;
     for (int c = lane; c < cols; c += 64) s += xr[c];
     const float n = (float)cols;
-    const float mu = wave_sum(s) / n;
+    const float mu = wave_sum_dpp(s) / n;
     float q = 0.f;
     for (int c = lane; c < cols; c += 64) {
         const float d = xr[c] - mu;
         q += d * d;
     }
-    const float inv = 1.0f / sqrtf(wave_sum(q) / n + eps);
+    const float inv = 1.0f / sqrtf(wave_sum_dpp(q) / n + eps);
     for (int c = lane; c < cols; c += 64) {
         const float v = (xr[c] - mu) * inv * g[c] + b[c];
         if (y) y[row * cols + c] = v;
@@ -533,8 +533,8 @@ __global__ __launch_bounds__(256) void ln_bwd_dx_kernel(const float *__restrict_
             sdx += gd[j] * xh[j];
         }
     }
-    sd = wave_sum(sd);
-    sdx = wave_sum(sdx);
+    sd = wave_sum_dpp(sd);
+    sdx = wave_sum_dpp(sdx);
     const float n = (float)cols;
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
@@ -567,8 +567,8 @@ __global__ __launch_bounds__(256) void ln_bwd_dx_any_kernel(const float *__restr
         sd += d;
         sdx += d * xh;
     }
-    sd = wave_sum(sd);
-    sdx = wave_sum(sdx);
+    sd = wave_sum_dpp(sd);
+    sdx = wave_sum_dpp(sdx);
     const float n = (float)cols;
     for (int c = lane; c < cols; c += 64) {
         const float xh = (xr[c] - mu) * inv;
