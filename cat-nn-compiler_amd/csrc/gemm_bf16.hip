@@ -116,20 +116,25 @@ using Cfg10 = DCfg<128, 128, 2, 2, 4, 32>;  // 32-deep chunks, four stages in th
 // 8192³ 1278 vs 1011, 16384×7168×2048 1102 vs 894, 16384×1024×3584 1193
 // vs 997, 8192×4096×1024 890 vs 677; with fewer than one tile per CU it
 // loses (8192×1024×4096, 128 tiles: 812 vs 982).
-template <int STAGES_>
+// (A 256 × 128 tile of eight 64 × 64 wavefronts, twice the tiles for grids
+// whose last round of 256 × 256 tiles leaves CUs idle, ran at 0.75–0.96× the
+// 128 × 128 tile on the training shapes: 16-MFMA phases of 128 × 64
+// wavefronts are what the ping-pong needs.)
+template <int BN_, int WAVES_M_, int WAVES_N_>
 struct PCfg {
     static constexpr bool DMA = true, PP = true;
-    static constexpr int BM = 256, BN = 256, WAVES_M = 2, WAVES_N = 4, STAGES = STAGES_;
+    static constexpr int BM = 256, BN = BN_, WAVES_M = WAVES_M_, WAVES_N = WAVES_N_, STAGES = 4;
     static constexpr int BK = 32, ROWB = 64, CPR = 4, RPL = 16;
-    static constexpr int NT = 512, NW = 8, FM = 4, FN = 2;
-    static constexpr int STAGE_BYTES = (BM + BN) * ROWB;  // 32 KiB
+    static constexpr int NT = 512, NW = 8, FM = BM / (32 * WAVES_M), FN = BN / (32 * WAVES_N);
+    static constexpr int STAGE_BYTES = (BM + BN) * ROWB;
     static constexpr int LDS_BYTES = STAGES * STAGE_BYTES;
     static constexpr int LPW = (BM + BN) / (RPL * NW);  // wave loads per wavefront and chunk
     static __device__ __forceinline__ int sw(int r) { return (r >> 2) & 3; }
-    static_assert(LPW == 4 && BM == 4 * LPW * RPL, "wavefronts 0-3 load A rows, 4-7 B rows");
-    static_assert(STAGES == 4, "the main loop's waits assume four stages");
+    static_assert(WAVES_M * WAVES_N == NW && WAVES_M % 2 == 0, "two groups of four wavefronts, whole rows each");
+    static_assert(LPW * RPL * NW == BM + BN && BM % RPL == 0, "wave loads cover the A and B rows");
+    static_assert((2 * FM * FN) / LPW >= 2, "one load after every second MFMA at most");
 };
-using Cfg11 = PCfg<4>;
+using Cfg11 = PCfg<256, 2, 4>;  // 256 × 256, wavefronts of 128 × 64
 
 
 __device__ __forceinline__ float bf2f(bf16_t v) { return __uint_as_float((uint32_t)v << 16); }
@@ -827,8 +832,8 @@ __device__ __forceinline__ void block_barrier() {
 // 1 starts one barrier later than group 0, so between consecutive barriers
 // one group is in its memory phase (read chunk j's fragments from LDS, then
 // wait until chunk j+1 is in LDS) while the other is in its MFMA phase
-// (16 MFMAs on the fragments it read, with this wavefront's four loads of
-// chunk j+3 issued among them).  Chunk j+3 goes to the stage chunk j−1
+// (2·FM·FN MFMAs on the fragments it read, with this wavefront's LPW
+// loads of chunk j+3 issued among them).  Chunk j+3 goes to the stage chunk j−1
 // used, which both groups finished reading before the MFMA phase of chunk
 // j began; every wavefront waits for its own loads of chunk j+1 at the end
 // of its memory phase of chunk j, and the barrier after that wait precedes
@@ -851,21 +856,24 @@ __device__ __forceinline__ void tile_pp(unsigned char *smem, const GemmBf16Param
         return B;
     };
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int g = wave / C::WAVES_N, wn = wave % C::WAVES_N;
+    const int g = wave >> 2, wn = wave % C::WAVES_N;  // group g: wavefronts 4g … 4g+3
     const int lr = lane & 31, lg = lane >> 5;
 
-    // Wave load q of wavefront w fills combined rows 16(4w + q) … +15 of
-    // [A tile; B tile] (wavefronts 0-3: A, 4-7: B): lane l row … + l/4 at
-    // position l mod 4, i.e. k chunk (l mod 4) ^ sw(row).  Rows past the
-    // tile's end read row row0 (col0 for B): their outputs are never stored.
-    const bool ld_b = wave >= 4;
+    // Wave load L = LPW·w + q of wavefront w fills combined rows 16L … 16L+15
+    // of [A tile; B tile] (A when 16L < BM; uniform per wave load): lane l
+    // row … + l/4 at position l mod 4, i.e. k chunk (l mod 4) ^ sw(row).
+    // Rows past the tile's end read row row0 (col0 for B): their outputs are
+    // never stored.
     const int lrow = lane / CPR, lpos = lane % CPR;
     const bf16_t *src[LPW];
+    bool is_b[LPW];
 #pragma unroll
     for (int q = 0; q < LPW; ++q) {
-        const int r = (wave & 3) * (LPW * C::RPL) + q * C::RPL + lrow;  // row within the A or B tile
+        const int R = (wave * LPW + q) * C::RPL + lrow;  // row of [A; B]
+        is_b[q] = (wave * LPW + q) * C::RPL >= BM;
+        const int r = is_b[q] ? R - BM : R;  // row within the A or B tile
         const int off = (lpos ^ C::sw(r)) * 8;
-        if (!ld_b) {
+        if (!is_b[q]) {
             int gr = row0 + r;
             if (gr >= row_end) gr = row0;
             const int srow = p.a_rows ? p.a_rows[gr] / p.a_row_div : gr;
@@ -878,11 +886,10 @@ __device__ __forceinline__ void tile_pp(unsigned char *smem, const GemmBf16Param
         }
     }
     const uint32_t lds_w = lds_addr(smem) + wave * LPW * 1024;
-    const int kwrap = ld_b ? p.b_kwrap : 0;
-    // k offset of chunk kt in this wavefront's operand (B's wraps: whole chunks, kwrap a multiple of BK)
-    auto koff = [&](int kt) {
-        const int k0 = k_lo + kt * BK;
-        return kwrap ? k0 % kwrap : k0;
+    // k offsets of chunk kt in A and in B (B's wraps: whole chunks, b_kwrap a multiple of BK)
+    auto koff = [&](int kt, int &ka, int &kb) {
+        ka = k_lo + kt * BK;
+        kb = p.b_kwrap ? ka % p.b_kwrap : ka;
     };
 
     f32x16 acc[FM][FN];
@@ -896,16 +903,19 @@ __device__ __forceinline__ void tile_pp(unsigned char *smem, const GemmBf16Param
     // Lane l reads k values 16s + 8(l/32) … +7 of row l mod 32 of each block;
     // fragment rows start on multiples of 32, so their swizzle is sw(l mod 32).
     const int swl = C::sw(lr);
-    const int a_off = (g * (BM / C::WAVES_M) + lr) * ROWB;
+    const int wm = wave / C::WAVES_N;
+    const int a_off = (wm * (BM / C::WAVES_M) + lr) * ROWB;
     int b_off[FN];
 #pragma unroll
     for (int ni = 0; ni < FN; ++ni) b_off[ni] = (BM + staged_col<C, DUAL>(wn, ni, lr)) * ROWB;
 
     const int nfull = (k_hi - k_lo) / BK;
     for (int c = 0; c < S - 1 && c < nfull; ++c) {
-        const int ko = koff(c);
+        int ka, kb;
+        koff(c, ka, kb);
 #pragma unroll
-        for (int q = 0; q < LPW; ++q) load_lds16_at(src[q] + ko, lds_w + c * C::STAGE_BYTES + q * 1024);
+        for (int q = 0; q < LPW; ++q)
+            load_lds16_at(src[q] + (is_b[q] ? kb : ka), lds_w + c * C::STAGE_BYTES + q * 1024);
     }
     {  // chunk 0 in LDS; chunks 1 … min(nfull, S−1)−1 may stay in flight
         const int after = min(nfull - 1, S - 2);
@@ -936,17 +946,20 @@ __device__ __forceinline__ void tile_pp(unsigned char *smem, const GemmBf16Param
         }
         block_barrier();
         __builtin_amdgcn_sched_barrier(0);
-        // MFMA phase, with the loads of chunk j+S−1
+        // MFMA phase, with the loads of chunk j+S−1: load q after MFMA q·SP+1
+        constexpr int NM = 2 * FM * FN, SP = NM / LPW;
         const int kt = j + S - 1;
         const bool iss = kt < nfull;
-        const int ko = iss ? koff(kt) : 0;
+        int ka = 0, kb = 0;
+        if (iss) koff(kt, ka, kb);
         const uint32_t dst = lds_w + (kt % S) * C::STAGE_BYTES;
 #pragma unroll
-        for (int t = 0; t < 2 * FM * FN; ++t) {
+        for (int t = 0; t < NM; ++t) {
             const int s = t / (FM * FN), mi = (t / FN) % FM, ni = t % FN;
             acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[s][mi], fb[s][ni], acc[mi][ni], 0, 0, 0);
-            if ((t & 3) == 1) {
-                if (iss) load_lds16_at(src[t >> 2] + ko, dst + (t >> 2) * 1024);
+            if (t % SP == 1 && t / SP < LPW) {
+                const int q = t / SP;
+                if (iss) load_lds16_at(src[q] + (is_b[q] ? kb : ka), dst + q * 1024);
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
@@ -1007,7 +1020,7 @@ __device__ __forceinline__ void tile_pp(unsigned char *smem, const GemmBf16Param
     if (staged && p.vec_epi && row0 + BM <= row_end && col0 + BN_OUT <= p.N)
         finish_staged<C, DUAL, GRID>(smem, p, acc, row0, col0, C32);
     else
-        finish<C, DUAL, GRID>(p, acc, row0 + g * (BM / C::WAVES_M) + 4 * lg, col0 + wn * WCOLS + lr, row_end, C32);
+        finish<C, DUAL, GRID>(p, acc, row0 + wm * (BM / C::WAVES_M) + 4 * lg, col0 + wn * WCOLS + lr, row_end, C32);
 }
 
 template <class C, bool VEC, bool DUAL, int GRID>
