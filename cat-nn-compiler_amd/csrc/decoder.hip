@@ -136,42 +136,27 @@ __global__ __launch_bounds__(256) void embedding_kernel(const float *__restrict_
 
 // Rows of exactly 1024 floats (16-byte aligned): one wavefront copies two
 // tokens' rows, all eight of a lane's 16-byte loads issued before its
-// stores.  Same id conversion and bad-id handling as embedding_kernel.  The
-// token index is wavefront-uniform (readfirstlane), so the ids come through
-// the scalar cache and the row loads sit under uniform branches: a select
-// between the table row and zeros would make the compiler pick between two
-// addresses (a zero vector in scratch), turning them into flat loads issued
-// one token at a time.
+// stores.  Same id conversion and bad-id handling as embedding_kernel.
+// (A variant with the token index made wavefront-uniform — ids through the
+// scalar cache, row loads under uniform branches — ran the same or slower
+// with the table and ids read from HBM; not kept.)
 __global__ __launch_bounds__(256) void embedding_pair_kernel(const float *__restrict__ ids, int64_t n,
                                                              const float4 *__restrict__ table, int64_t vocab,
                                                              float4 *__restrict__ y, int *__restrict__ bad) {
     constexpr int kQ = 256;  // float4 per row
     const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int64_t t0 = ((int64_t)blockIdx.x * 4 + wave) * 2;
+    const int64_t t0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 2;
     if (t0 >= n) return;
     const bool two = t0 + 1 < n;
-    const float f0 = ids[t0], f1 = two ? ids[t0 + 1] : 0.f;
-    const int64_t id0 = token_id(f0);
-    const int64_t id1 = two ? token_id(f1) : 0;
+    const int64_t id0 = token_id(ids[t0]);
+    const int64_t id1 = two ? token_id(ids[t0 + 1]) : 0;
     const bool ok0 = id0 < vocab, ok1 = two && id1 < vocab;
     const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
     float4 a[4], b[4];
-    if (ok0) {
-        const float4 *r = table + id0 * kQ + lane;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) a[j] = r[64 * j];
-    } else {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) a[j] = z;
-    }
-    if (ok1) {
-        const float4 *r = table + id1 * kQ + lane;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) b[j] = r[64 * j];
-    } else {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) b[j] = z;
+    for (int j = 0; j < 4; ++j) {
+        a[j] = ok0 ? table[id0 * kQ + lane + 64 * j] : z;
+        b[j] = ok1 ? table[id1 * kQ + lane + 64 * j] : z;
     }
     if (lane == 0 && (!ok0 || (two && !ok1))) *bad = 1;
 #pragma unroll

