@@ -91,6 +91,10 @@ struct catnn_hip_device {
     std::chrono::steady_clock::time_point epoch;
     catnn::Workspace moe_ws;
     void *noalloc_scratch = nullptr;  // device address of the fixed MoE scratch
+    // Partial tiles of the bf16 GEMM's stream-K remainder (gemm_bf16.hip
+    // configuration 12): one 256 × 256 fp32 tile per CU, allocated once on
+    // first use and shared by every GEMM on this device's stream.
+    catnn::Workspace sk_ws;
     std::string noalloc_error;
     int cu_count = 0;
 };

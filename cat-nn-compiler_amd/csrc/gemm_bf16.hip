@@ -840,10 +840,10 @@ __device__ __forceinline__ void block_barrier() {
 // the first read of chunk j+1 by either group.  After the loop group 0
 // takes one more barrier, so both groups pass the same number.  A partial
 // last chunk goes through registers, computed by all eight wavefronts.
-template <class C, bool DUAL, int GRID>
+template <class C, bool DUAL, int GRID, bool PIECE = false>
 __device__ __forceinline__ void tile_pp(unsigned char *smem, const GemmBf16Params &p, const bf16_t *__restrict__ B,
                                         const bf16_t *__restrict__ B2, int row0, int row_end, int col0, int k_lo,
-                                        int k_hi, float *__restrict__ C32) {
+                                        int k_hi, float *__restrict__ C32, float *__restrict__ part = nullptr) {
     constexpr int BM = C::BM, BN = C::BN, FM = C::FM, FN = C::FN, BK = C::BK, ROWB = C::ROWB, S = C::STAGES;
     constexpr int LPW = C::LPW, CPR = C::CPR;
     constexpr int BN_OUT = DUAL ? BN / 2 : BN, WCOLS = BN_OUT / C::WAVES_N;
@@ -1013,14 +1013,27 @@ __device__ __forceinline__ void tile_pp(unsigned char *smem, const GemmBf16Param
                     acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[0][mi], fb[0][ni], acc[mi][ni], 0, 0, 0);
         }
     }
-    // Plain fp32 stores go straight from the accumulators (each store
-    // instruction writes whole 128-byte row runs); epilogues with bf16
-    // outputs or per-output operands go through LDS in two 128-row slices.
-    const bool staged = DUAL || p.epi != EPI_STORE || p.Cb;
-    if (staged && p.vec_epi && row0 + BM <= row_end && col0 + BN_OUT <= p.N)
-        finish_staged<C, DUAL, GRID>(smem, p, acc, row0, col0, C32);
-    else
-        finish<C, DUAL, GRID>(p, acc, row0 + wm * (BM / C::WAVES_M) + 4 * lg, col0 + wn * WCOLS + lr, row_end, C32);
+    if constexpr (PIECE) {  // stream-K piece: the raw fp32 tile, BM × BN row-major (the fixup adds the pieces)
+        static_assert(!DUAL, "stream-K pieces take plain B");
+#pragma unroll
+        for (int mi = 0; mi < FM; ++mi)
+#pragma unroll
+            for (int ni = 0; ni < FN; ++ni)
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    part[(wm * (BM / C::WAVES_M) + mi * 32 + 8 * (r >> 2) + 4 * lg + (r & 3)) * BN +
+                         wn * (BN / C::WAVES_N) + ni * 32 + lr] = acc[mi][ni][r];
+    } else {
+        // Plain fp32 stores go straight from the accumulators (each store
+        // instruction writes whole 128-byte row runs); epilogues with bf16
+        // outputs or per-output operands go through LDS in two 128-row slices.
+        const bool staged = DUAL || p.epi != EPI_STORE || p.Cb;
+        if (staged && p.vec_epi && row0 + BM <= row_end && col0 + BN_OUT <= p.N)
+            finish_staged<C, DUAL, GRID>(smem, p, acc, row0, col0, C32);
+        else
+            finish<C, DUAL, GRID>(p, acc, row0 + wm * (BM / C::WAVES_M) + 4 * lg, col0 + wn * WCOLS + lr, row_end,
+                                  C32);
+    }
 }
 
 template <class C, bool VEC, bool DUAL, int GRID>
@@ -1040,26 +1053,70 @@ __device__ __forceinline__ void run_tile(unsigned char *smem, const GemmBf16Para
     }
 }
 
+// Tile t of a stream-K launch (plain or grouped-row grid, 256 × 256 tiles in
+// the grouped order of the ordinary grid over the tiles that exist).
+template <class C, int GRID>
+__device__ __forceinline__ void sk_tile(const GemmBf16Params &p, int t, int tiles_mr, int tiles_n, int &row0,
+                                        int &row_end, int &col0, const bf16_t *&B) {
+    int tm, tn;
+    grouped_tile(t, tiles_mr, tiles_n, 8, tm, tn);
+    col0 = tn * C::BN;
+    if constexpr (GRID == GRID_PLAIN) {
+        row0 = tm * C::BM;
+        row_end = p.M;
+        B = p.B;
+    } else {
+        const int e = p.tile_expert[tm];
+        row0 = p.tile_row0[tm];
+        row_end = p.seg_counts ? p.seg_offsets[e] + p.seg_counts[e] : p.seg_offsets[e + 1];
+        B = p.B_e[e];
+    }
+}
+
+template <class C, int GRID>
+__device__ __forceinline__ int sk_tiles_m(const GemmBf16Params &p) {
+    if constexpr (GRID == GRID_PLAIN) return (p.M + C::BM - 1) / C::BM;
+    else return *p.n_tiles;
+}
+
 template <class C, bool VEC, bool DUAL, int GRID>
 __global__ __launch_bounds__(C::NT) void gemm_bf16_kernel(GemmBf16Params p) {
     extern __shared__ __align__(16) unsigned char smem[];
     const int bn_out = DUAL ? C::BN / 2 : C::BN;
     const int tiles_n = (p.N + bn_out - 1) / bn_out;
     const int lid = xcd_remap(blockIdx.x, gridDim.x);
-    if constexpr (GRID == GRID_PLAIN) {
-        const int tiles_m = (p.M + C::BM - 1) / C::BM;
-        int tm, tn;
-        grouped_tile(lid, tiles_m, tiles_n, 8, tm, tn);
-        run_tile<C, VEC, DUAL, GRID>(smem, p, p.B, p.B2, tm * C::BM, p.M, tn * bn_out, 0, p.K, p.C32);
-    } else if constexpr (GRID == GRID_ROWS) {
-        // Tiles of the table are C::BM rows (the launcher passes the table built for C::BM).
-        int tm, tn;
-        grouped_tile(lid, p.max_tiles, tiles_n, 8, tm, tn);
-        if (tm >= *p.n_tiles) return;
-        const int e = p.tile_expert[tm];
-        const int end = p.seg_counts ? p.seg_offsets[e] + p.seg_counts[e] : p.seg_offsets[e + 1];
-        run_tile<C, VEC, DUAL, GRID>(smem, p, p.B_e[e], DUAL ? p.B2_e[e] : nullptr, p.tile_row0[tm], end,
-                                     tn * bn_out, 0, p.K, p.C32);
+    if constexpr (GRID == GRID_PLAIN || GRID == GRID_ROWS) {
+        int row0, row_end, col0;
+        const bf16_t *B, *B2 = nullptr;
+        if (C::PP && !DUAL && p.sk_ctas) {
+            // Stream-K launch (configuration 12): this grid runs the whole
+            // rounds of tiles, t = lid < rounds·G in the enumeration of
+            // sk_tile; gemm_bf16_sk_kernel and sk_fixup_kernel the rest.
+            const int tiles_mr = sk_tiles_m<C, GRID>(p), G = p.sk_ctas;
+            if (lid >= tiles_mr * tiles_n / G * G) return;
+            sk_tile<C, GRID>(p, lid, tiles_mr, tiles_n, row0, row_end, col0, B);
+        } else if constexpr (GRID == GRID_PLAIN) {
+            const int tiles_m = (p.M + C::BM - 1) / C::BM;
+            int tm, tn;
+            grouped_tile(lid, tiles_m, tiles_n, 8, tm, tn);
+            row0 = tm * C::BM;
+            row_end = p.M;
+            col0 = tn * bn_out;
+            B = p.B;
+            B2 = p.B2;
+        } else {
+            // Tiles of the table are C::BM rows (the launcher passes the table built for C::BM).
+            int tm, tn;
+            grouped_tile(lid, p.max_tiles, tiles_n, 8, tm, tn);
+            if (tm >= *p.n_tiles) return;
+            const int e = p.tile_expert[tm];
+            row_end = p.seg_counts ? p.seg_offsets[e] + p.seg_counts[e] : p.seg_offsets[e + 1];
+            row0 = p.tile_row0[tm];
+            col0 = tn * bn_out;
+            B = p.B_e[e];
+            B2 = DUAL ? p.B2_e[e] : nullptr;
+        }
+        run_tile<C, VEC, DUAL, GRID>(smem, p, B, B2, row0, row_end, col0, 0, p.K, p.C32);
     } else {  // GRID_SEGK: expert e = blockIdx.y reduces over its own K segment
         const int tiles_m = (p.M + C::BM - 1) / C::BM;
         int tm, tn;
@@ -1074,6 +1131,83 @@ __global__ __launch_bounds__(C::NT) void gemm_bf16_kernel(GemmBf16Params p) {
             hi = min(p.K, lo + p.ksplit);
         }
         run_tile<C, VEC, DUAL, GRID>(smem, p, p.B, nullptr, tm * C::BM, p.M, tn * bn_out, lo, hi, p.C_e[e]);
+    }
+}
+
+// Stream-K remainder (configuration 12).  The ordinary kernel runs the
+// whole rounds of tiles (rounds·G of them, G = one block per CU); the
+// remaining rem < G tiles are each cut into S = G / rem k ranges of whole
+// chunks, and this kernel (G blocks) computes piece lid = rt·S + s into
+// sk_part[lid] as a raw fp32 tile; sk_fixup_kernel adds a tile's pieces in
+// order s = 0 … S−1 and runs the epilogue.
+template <class C, int GRID>
+__global__ __launch_bounds__(C::NT) void gemm_bf16_sk_kernel(GemmBf16Params p) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int G = p.sk_ctas;
+    const int lid = xcd_remap(blockIdx.x, gridDim.x);
+    const int tiles_n = (p.N + C::BN - 1) / C::BN;
+    const int tiles_mr = sk_tiles_m<C, GRID>(p);
+    const int total = tiles_mr * tiles_n, rounds = total / G, rem = total - rounds * G;
+    if (rem == 0) return;
+    const int S = G / rem;
+    if (lid >= rem * S) return;
+    const int nk = (p.K + C::BK - 1) / C::BK, per = (nk + S - 1) / S;
+    const int k_lo = min(p.K, (lid % S) * per * C::BK), k_hi = min(p.K, k_lo + per * C::BK);
+    int row0, row_end, col0;
+    const bf16_t *B;
+    sk_tile<C, GRID>(p, rounds * G + lid / S, tiles_mr, tiles_n, row0, row_end, col0, B);
+    tile_pp<C, false, GRID, true>(smem, p, B, nullptr, row0, row_end, col0, k_lo, k_hi, nullptr,
+                                  p.sk_part + (int64_t)lid * (C::BM * C::BN));
+}
+
+// Stream-K fixup: the remainder tiles of a configuration-12 launch.  One
+// thread per 8 consecutive outputs of a tile (32 blocks a tile): the tile's
+// S partial pieces added in order s = 0 … S−1, then the launch's epilogue.
+template <int GRID>
+__global__ __launch_bounds__(256) void sk_fixup_kernel(GemmBf16Params p) {
+    using C = Cfg11;
+    constexpr int BM = C::BM, BN = C::BN, BPT = BM * BN / 8 / 256;
+    const int G = p.sk_ctas;
+    const int tiles_n = (p.N + BN - 1) / BN;
+    const int tiles_mr = sk_tiles_m<C, GRID>(p);
+    const int total = tiles_mr * tiles_n, full = total / G * G, rem = total - full;
+    const int rt = blockIdx.x / BPT;
+    if (rt >= rem) return;
+    const int S = G / rem;
+    int row0, row_end, col0;
+    const bf16_t *B;
+    sk_tile<C, GRID>(p, full + rt, tiles_mr, tiles_n, row0, row_end, col0, B);
+    const int run = (blockIdx.x % BPT) * 256 + threadIdx.x;
+    const int r = run / (BN / 8), c = (run % (BN / 8)) * 8;
+    const int row = row0 + r, col = col0 + c;
+    if (row >= row_end || col >= p.N) return;
+    const float *src = p.sk_part + (int64_t)rt * S * (BM * BN) + r * BN + c;
+    float v[8], w[8];
+    load8f(src, v);
+    for (int q = 1; q < S; ++q) {
+        load8f(src + (int64_t)q * (BM * BN), w);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] += w[j];
+    }
+    auto finish8 = [&](auto epi_c) {
+        constexpr int EPI = decltype(epi_c)::value;
+        if (p.vec_epi && col + 8 <= p.N) {
+            epi_vec8<EPI>(p, v, row, col, p.C32);
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                if (col + j < p.N) epi_elem<false, EPI>(p, v[j], 0.f, row, col + j, p.C32);
+        }
+    };
+    if constexpr (GRID == GRID_PLAIN) {
+        switch (p.epi) {
+            case EPI_LINEAR: finish8(std::integral_constant<int, EPI_LINEAR>{}); break;
+            case EPI_GELU_BWD: finish8(std::integral_constant<int, EPI_GELU_BWD>{}); break;
+            default: finish8(std::integral_constant<int, EPI_STORE>{});
+        }
+    } else {
+        if (p.epi == EPI_SWIGLU_BWD) finish8(std::integral_constant<int, EPI_SWIGLU_BWD>{});
+        else finish8(std::integral_constant<int, EPI_STORE>{});
     }
 }
 
@@ -1195,6 +1329,12 @@ int device_cus() {
 // the main loop's gain at short k (config 5, K = 1024: 324 against 296 µs).
 int pick_cfg(const GemmBf16Params &p) {
     if (p.epi == EPI_SWIGLU_BWD && p.K < 2048) return 7;
+    // Grouped rows with a single B: the MoE down and input-gradient GEMMs
+    // (N = 1024, eight experts' B operands) ran slower per unit of work on
+    // the 256 × 256 tile than on two 128 × 128 blocks per CU (config 5: one
+    // round of 256 tiles 218 µs, against 203 µs for the whole down GEMM on the
+    // 128 × 128 tile), so they stay there, stream-K remainder or not.
+    if (p.grid == GRID_ROWS && p.epi != EPI_SWIGLU_FWD) return 7;
     const bool dual = p.epi == EPI_SWIGLU_FWD;
     const int64_t tn2 = (p.N + (dual ? 127 : 255)) / (dual ? 128 : 256);
     const int64_t tn1 = (p.N + (dual ? 63 : 127)) / (dual ? 64 : 128);
@@ -1218,12 +1358,25 @@ int pick_cfg(const GemmBf16Params &p) {
     const int64_t cus = device_cus();
     const double pp = (double)((t2 + cus - 1) / cus) * 4.0 / 1.2;
     const double c7 = (double)((t1 + 2 * cus - 1) / (2 * cus)) * 2.0;
+    // Configuration 12 (stream-K remainder, scratch given, at least one whole
+    // round): the whole rounds, then the remainder's tiles cut in S = CUs /
+    // rem k ranges, plus the fixup (reads S·rem partial tiles: about 0.15 of
+    // a round, more when k is short).
+    double sk = 1e30;
+    if (p.sk_part && !dual && p.grid == GRID_PLAIN && t2 >= cus) {
+        const int64_t full = t2 / cus, rem = t2 - full * cus;
+        sk = (double)full * 4.0 / 1.2;
+        if (rem > 0) sk += 4.0 / 1.2 / (double)(cus / rem) + 0.15 + 0.3 * 1024.0 / (double)klen;
+    }
+    if (sk < pp && sk < c7) return 12;
     return pp < c7 ? 11 : 7;
 }
 
 }  // namespace
 
 int gemm_bf16_tile_rows() { return kRowTile; }
+
+int64_t gemm_bf16_sk_floats() { return (int64_t)device_cus() * Cfg11::BM * Cfg11::BN; }
 
 int64_t gemm_bf16_tiles_ints(int64_t rows, int n_experts) {
     return 2 * (int64_t)max_tiles_for(rows, n_experts, kRowTile) + 1 + 2 * (int64_t)max_tiles_for(rows, n_experts, 256) + 1;
@@ -1296,7 +1449,9 @@ void gemm_bf16_launch_cfg(hipStream_t s, const GemmBf16Params &p, int cfg) {
     // output, saved and residual row must start on a 16-byte boundary.
     GemmBf16Params q = p;
     q.vec_epi = epi_rows_aligned(p);
-    if (cfg == 11 && p.grid == GRID_ROWS) {
+    q.sk_ctas = 0;  // set for configuration 12 only
+    if (cfg == 12 && (dual || p.grid == GRID_SEGK || !p.sk_part || !vec)) cfg = 11;
+    if ((cfg == 11 || cfg == 12) && p.grid == GRID_ROWS) {
         CATNN_REQUIRE(p.tiles256, CATNN_ERR_INVALID_ARGUMENT, "bf16 gemm: 256-row tiles need their tile table");
         q.tile_expert = p.tiles256;
         q.tile_row0 = p.tiles256 + p.max_tiles256;
@@ -1310,6 +1465,39 @@ void gemm_bf16_launch_cfg(hipStream_t s, const GemmBf16Params &p, int cfg) {
         case 9: launch_cfg<Cfg9, false>(s, q, vec, dual, gy); break;
         case 10: launch_cfg<Cfg10, true>(s, q, vec, dual, gy); break;
         case 11: launch_cfg<Cfg11, true>(s, q, vec, dual, gy); break;
+        case 12: {
+            // One block per CU; the fixup finishes the remainder's tiles.
+            const bool ok_epi = p.grid == GRID_PLAIN
+                                    ? (p.epi == EPI_STORE || p.epi == EPI_LINEAR || p.epi == EPI_GELU_BWD)
+                                    : (p.epi == EPI_STORE || p.epi == EPI_SWIGLU_BWD);
+            CATNN_REQUIRE(ok_epi, CATNN_ERR_INVALID_ARGUMENT, "bf16 gemm: epilogue not built for this grid");
+            if (p.grid == GRID_PLAIN && p.M == 0) return;
+            q.sk_ctas = device_cus();
+            const int64_t tiles_n = (p.N + Cfg11::BN - 1) / Cfg11::BN;
+            // the ordinary grid: the plain grid's whole rounds, or the grouped grid's tile bound
+            const int64_t g1 = p.grid == GRID_PLAIN
+                                   ? ((p.M + Cfg11::BM - 1) / Cfg11::BM * tiles_n) / q.sk_ctas * q.sk_ctas
+                                   : (int64_t)q.max_tiles * tiles_n;
+            static bool attr_set[2] = {false, false};  // per grid: the opt-in for 128 KiB of LDS
+            auto run = [&](int gi, auto pieces, auto fix) {
+                if (!attr_set[gi]) {
+                    CATNN_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(pieces),
+                                                  hipFuncAttributeMaxDynamicSharedMemorySize, Cfg11::LDS_BYTES));
+                    attr_set[gi] = true;
+                }
+                pieces<<<(unsigned)q.sk_ctas, Cfg11::NT, Cfg11::LDS_BYTES, s>>>(q);
+                fix<<<(unsigned)q.sk_ctas * 32, 256, 0, s>>>(q);
+            };
+            if (p.grid == GRID_PLAIN) {
+                if (g1 > 0) launch_kernel<Cfg11, GRID_PLAIN, false>(s, q, vec, dim3((unsigned)g1));
+                run(0, gemm_bf16_sk_kernel<Cfg11, GRID_PLAIN>, sk_fixup_kernel<GRID_PLAIN>);
+            } else {
+                if (g1 > 0) launch_kernel<Cfg11, GRID_ROWS, false>(s, q, vec, dim3((unsigned)g1));
+                run(1, gemm_bf16_sk_kernel<Cfg11, GRID_ROWS>, sk_fixup_kernel<GRID_ROWS>);
+            }
+            CATNN_HIP(hipGetLastError());
+            break;
+        }
         default: fail(CATNN_ERR_INVALID_ARGUMENT, "bf16 gemm: unknown tile configuration");
     }
 }

@@ -68,6 +68,10 @@ struct GemmBf16Params {
     int max_tiles;
     const int32_t *tiles256;  // GRID_ROWS: the table of 256-row tiles (gemm_bf16_build_tiles), or null
     int max_tiles256;
+    // Stream-K remainder (configuration 12): fp32 partial tiles, gemm_bf16_sk_floats() of them, or null
+    // (then configuration 12 is not chosen); sk_ctas is set by the launcher.
+    float *sk_part;
+    int sk_ctas;
     int n_experts;
     const bf16_t *B_e[kMaxExperts];
     const bf16_t *B2_e[kMaxExperts];
@@ -75,9 +79,12 @@ struct GemmBf16Params {
 };
 
 void gemm_bf16_launch(hipStream_t s, const GemmBf16Params &p);
-// The same with a fixed tile configuration (0, 2, 7, 9, 10 or 11; see gemm_bf16.hip).
+// The same with a fixed tile configuration (0, 2, 7, 9, 10, 11 or 12; see gemm_bf16.hip).
 void gemm_bf16_launch_cfg(hipStream_t s, const GemmBf16Params &p, int cfg);
 int gemm_bf16_tile_rows();
+// Floats of partial-tile scratch the stream-K remainder of configuration 12
+// needs on the current device (one 256 × 256 tile per CU).
+int64_t gemm_bf16_sk_floats();
 // Tile tables of the grouped grid for `rows` routed rows (T·k) over
 // n_experts segments: 128-row and 256-row tiles of each segment, in expert
 // order, built by one launch into `tiles` (gemm_bf16_tiles_ints int32s);

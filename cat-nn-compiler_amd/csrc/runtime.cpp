@@ -191,6 +191,7 @@ int catnn_hip_close(catnn_hip_device *dev) {
         for (void *p : dev->allocations) (void)hipFree(p);
         if (dev->arena) (void)hipFree(dev->arena);
         if (dev->moe_ws.ptr) (void)hipFree(dev->moe_ws.ptr);
+        if (dev->sk_ws.ptr) (void)hipFree(dev->sk_ws.ptr);
         if (dev->t_start) (void)hipEventDestroy(dev->t_start);
         if (dev->t_stop) (void)hipEventDestroy(dev->t_stop);
         if (dev->stream) (void)hipStreamDestroy(dev->stream);

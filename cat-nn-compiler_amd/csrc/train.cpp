@@ -143,6 +143,7 @@ struct TNode {
 
 struct catnn_hip_trainer {
     catnn_hip_device *dev = nullptr;
+    float *sk_part = nullptr;  // the device's stream-K scratch for the bf16 GEMMs
     catnn_graph graph;
     float lr = 0.05f;
     int opt = CATNN_OPT_SGD;
@@ -196,10 +197,31 @@ void request(Tr &t, const std::string &id, uint64_t bytes, uint64_t from, uint64
     t.req_slot.push_back(slot);
 }
 
+// The stream-K scratch of the trainer whose step (or adjoint pass) this
+// thread is running, for every GEMM it launches (SkScope sets it).
+thread_local float *tl_sk_part = nullptr;
+
+struct SkScope {
+    float *prev;
+    explicit SkScope(float *p) : prev(tl_sk_part) { tl_sk_part = p; }
+    ~SkScope() { tl_sk_part = prev; }
+};
+
 k::GemmBf16Params gp() {
     k::GemmBf16Params p{};
     p.a_row_div = 1;
+    p.sk_part = tl_sk_part;
     return p;
+}
+
+// The device's stream-K scratch (allocated on first use, freed with the device).
+float *device_sk_scratch(catnn_hip_device *dev) {
+    if (!dev->sk_ws.ptr) {
+        const uint64_t bytes = (uint64_t)k::gemm_bf16_sk_floats() * 4;
+        CATNN_HIP(hipMalloc(&dev->sk_ws.ptr, bytes));
+        dev->sk_ws.bytes = bytes;
+    }
+    return (float *)dev->sk_ws.ptr;
 }
 
 // Bytes of split-K partial sums gemm_nt needs for an M×N×K product (at
@@ -1822,6 +1844,7 @@ static void reverse_steps(Tr &t) {
 
 static void train_step(Tr &t) {
     hipStream_t s = t.dev->stream;
+    SkScope sk(t.sk_part);
     forward_values_home(t);
     for (auto &tn : t.nodes)
         if (!t.input_ids.count(tn.id)) forward_node(t, tn);
@@ -1845,12 +1868,16 @@ static void train_step(Tr &t) {
 // tapes, then — once the caller has put the output's cotangent in place, at
 // the loss tick of the plan — the reverse pass.
 static void forward_pass(Tr &t) {
+    SkScope sk(t.sk_part);
     forward_values_home(t);
     for (auto &tn : t.nodes)
         if (!t.input_ids.count(tn.id)) forward_node(t, tn);
 }
 
-static void reverse_pass(Tr &t) { reverse_steps(t); }
+static void reverse_pass(Tr &t) {
+    SkScope sk(t.sk_part);
+    reverse_steps(t);
+}
 
 static TParam *find_param(Tr &t, uint32_t node_id, const std::string &port, int64_t *col0,
                           int64_t *ncols) {
@@ -2021,9 +2048,10 @@ int catnn_hip_gemm_bf16_nt(catnn_hip_device *dev, const uint16_t *a, int64_t lda
         CATNN_REQUIRE(lda >= k && ldb >= k && ldc >= n, CATNN_ERR_SHAPE_MISMATCH, "gemm_bf16: leading dims");
         CATNN_REQUIRE((a && b && c) || m * n == 0, CATNN_ERR_INVALID_ARGUMENT, "gemm_bf16: null operand");
         CATNN_REQUIRE(tile_cfg == -1 || tile_cfg == 0 || tile_cfg == 2 || tile_cfg == 7 || tile_cfg == 9 ||
-                          tile_cfg == 10 || tile_cfg == 11,
+                          tile_cfg == 10 || tile_cfg == 11 || tile_cfg == 12,
                       CATNN_ERR_INVALID_ARGUMENT, "gemm_bf16: tile_cfg");
         k::GemmBf16Params p = gp();
+        if (m * n > 0) p.sk_part = device_sk_scratch(dev);
         p.A = a; p.lda = lda; p.B = b; p.ldb = ldb;
         p.M = (int)m; p.N = (int)n; p.K = (int)k;
         p.epi = k::EPI_STORE; p.C32 = c; p.ldc32 = ldc; p.accumulate = accumulate ? 1 : 0;
@@ -2067,6 +2095,7 @@ int catnn_hip_train_install_ex(catnn_hip_device *dev, const catnn_graph *g, cons
                 t->fuse_values = fuse;
                 plan_trainer(*t);
                 reserve_and_upload(*t);
+                if (t->prec == CATNN_PREC_BF16) t->sk_part = device_sk_scratch(dev);
             } catch (...) {
                 if (t->base) (void)hipFree(t->base);
                 delete t;

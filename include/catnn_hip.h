@@ -634,10 +634,12 @@ int catnn_hip_linear_f32(catnn_hip_device *dev, const float *x, const float *w,
  * k-contiguous) with fp32 accumulation: the kernel behind every GEMM of the
  * training step (the bf16 counterpart of linear_backward's products,
  * adjoint.rs:35-61), exposed for tests and benchmarks.  tile_cfg: -1
- * automatic, or a fixed tile configuration: 0, 2, 7, 9, 10 or 11
- * (gemm_bf16.hip; 7, 9, 10 and 11 stage k chunks straight into LDS and take
- * 16-byte aligned rows, other launches given them run as 2; 11 is the
- * 256 × 256 ping-pong tile). */
+ * automatic, or a fixed tile configuration: 0, 2, 7, 9, 10, 11 or 12
+ * (gemm_bf16.hip; 7, 9, 10, 11 and 12 stage k chunks straight into LDS and
+ * take 16-byte aligned rows, other launches given them run as 2; 11 is the
+ * 256 × 256 ping-pong tile, 12 the same with the last round of tiles split
+ * along k over every CU — the stream-K scratch is the device's, allocated
+ * on first use). */
 int catnn_hip_gemm_bf16_nt(catnn_hip_device *dev, const uint16_t *a, int64_t lda, const uint16_t *b,
                            int64_t ldb, float *c, int64_t ldc, int64_t m, int64_t n, int64_t k,
                            int32_t accumulate, int32_t tile_cfg);

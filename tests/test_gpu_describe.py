@@ -10,6 +10,7 @@ KernelResource (crates/catnn-compile/src/kernel/resource.rs:28-45) carries.
 import ctypes
 import glob
 import os
+import re
 
 import pytest
 
@@ -17,7 +18,18 @@ import catnn_amd
 
 pytestmark = pytest.mark.gpu
 
-CO_DIR = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "cat-nn-compiler_amd", "lib", "co")
+PKG = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "cat-nn-compiler_amd")
+CO_DIR = os.path.join(PKG, "lib", "co")
+
+
+def _hip_runtime():
+    # The HIP runtime the library is bound to, opened by the soname it
+    # needs: the dynamic loader returns the copy already in the process (a
+    # process that imported torch first may hold torch's copy, and loading
+    # another by path would give an uninitialised second runtime).
+    with open(os.path.join(PKG, "lib", "libcatnn_hip.so"), "rb") as f:
+        m = re.search(rb"libamdhip64\.so\.[0-9]+", f.read())
+    return ctypes.CDLL(m.group(0).decode() if m else "libamdhip64.so")
 
 # hipFunction_attribute (hip/driver_types.h)
 MAX_THREADS_PER_BLOCK, SHARED_SIZE_BYTES, LOCAL_SIZE_BYTES, NUM_REGS = 0, 1, 3, 4
@@ -26,7 +38,7 @@ MAX_THREADS_PER_BLOCK, SHARED_SIZE_BYTES, LOCAL_SIZE_BYTES, NUM_REGS = 0, 1, 3, 
 def test_kernel_table_matches_hip_func_attributes(device):
     paths = sorted(glob.glob(os.path.join(CO_DIR, "*.co")))
     assert paths, f"no code objects under {CO_DIR}: build the library (make -C cat-nn-compiler_amd)"
-    hip = ctypes.CDLL("libamdhip64.so")
+    hip = _hip_runtime()
     mods = []
     try:
         for p in paths:
@@ -41,6 +53,8 @@ def test_kernel_table_matches_hip_func_attributes(device):
                 f = ctypes.c_void_p()
                 if hip.hipModuleGetFunction(ctypes.byref(f), m, r.kernel.encode()) == 0:
                     found.append(f)
+                else:
+                    hip.hipGetLastError()  # a miss in this module: clear it, later launches check the error state
             assert len(found) == 1, (r.kernel, len(found))
 
             def attr(a):
@@ -54,3 +68,4 @@ def test_kernel_table_matches_hip_func_attributes(device):
     finally:
         for m in mods:
             hip.hipModuleUnload(m)
+        hip.hipGetLastError()

@@ -85,7 +85,7 @@ GEMM_BF16_CASES = [
 ]
 
 
-@pytest.mark.parametrize("tile_cfg", [0, 2, 7, 9, 10, 11])
+@pytest.mark.parametrize("tile_cfg", [0, 2, 7, 9, 10, 11, 12])
 @pytest.mark.parametrize("m,n,k", GEMM_BF16_CASES)
 def test_gemm_bf16_matches_float64(device, m, n, k, tile_cfg):
     # bf16 operands, fp32 accumulation: only the accumulation rounds.
