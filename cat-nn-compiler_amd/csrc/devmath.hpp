@@ -132,5 +132,23 @@ __device__ __forceinline__ void grouped_tile(int lid, int tiles_m, int tiles_n, 
     tn = in_group / gsz;
 }
 
+// Streaming (nontemporal) 16- and 8-byte accesses, for values a kernel
+// reads or writes once and that no kernel right after it reads again
+// through the L2.
+typedef float stream_f4 __attribute__((ext_vector_type(4)));
+typedef uint32_t stream_u2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float4 load_stream(const float *q) {
+    const stream_f4 v = __builtin_nontemporal_load(reinterpret_cast<const stream_f4 *>(q));
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ void store_stream(float *q, float4 v) {
+    const stream_f4 w = {v.x, v.y, v.z, v.w};
+    __builtin_nontemporal_store(w, reinterpret_cast<stream_f4 *>(q));
+}
+__device__ __forceinline__ void store_stream(uint16_t *q, uint32_t a, uint32_t b) {
+    const stream_u2 w = {a, b};
+    __builtin_nontemporal_store(w, reinterpret_cast<stream_u2 *>(q));
+}
+
 }  // namespace k
 }  // namespace catnn
