@@ -1792,7 +1792,10 @@ static void backward_node(Tr &t, TNode &tn) {
             k::transpose_bf16(s, (bf16_t *)tn.B("x3"), 3 * H, sop, (int)K, (int)Pr, (int)H, xpt, Pr);  // hi part of x
             k::transpose_bf16(s, (bf16_t *)tn.B("h"), I, nullptr, 1, (int)Pr, (int)I, ht, Pr);
             k::transpose_bf16(s, dys, H, nullptr, 1, (int)Pr, (int)H, dyst, Pr);
-            k::transpose_bf16(s, dadc, 2 * I, nullptr, 1, (int)Pr, (int)(2 * I), dat, Pr);  // [daᵀ; dcᵀ]
+            // [daᵀ; dcᵀ].  (Written by the SwiGLU-adjoint GEMM's staged epilogue
+            // as 16-byte column runs instead, the transposed stores made that
+            // GEMM 92 us slower on config 5, as much as this transpose takes.)
+            k::transpose_bf16(s, dadc, 2 * I, nullptr, 1, (int)Pr, (int)(2 * I), dat, Pr);
             k::GemmBf16Params r = gp();
             r.grid = k::GRID_SEGK; r.seg_offsets = offs; r.seg_counts = counts; r.segk_aligned = 1;
             r.n_experts = (int)E; r.epi = k::EPI_STORE;
