@@ -1399,15 +1399,15 @@ void gemm_bf16_use_tiles(GemmBf16Params &p, const int32_t *tiles, int64_t rows, 
 }
 
 // Up to 8 splits while the split grid stays within 512 tiles (two per CU)
-// and each segment keeps 1024 or more k values; only grids of at most 128
-// tiles (half the CUs) with 16-byte output rows are split.  The case is a
+// and each segment keeps 1024 or more k values; only grids of at most 256
+// tiles (one per CU) with 16-byte output rows are split.  The case is a
 // weight gradient with few outputs and many tokens: config 5's wo gradient
-// (1024 × 1024 × 8192, 64 tiles) took 89 µs unsplit, 193 TFLOP/s; the
-// 192–256-tile gradients already reach 550–640 TFLOP/s on one tile per CU,
-// and splitting them measured no faster once the partial sums are added.
+// (1024 × 1024 × 8192, 64 tiles) took 89 µs unsplit, 193 TFLOP/s; its
+// 192–256-tile gradients (QKV, fc1, fc2), one tile per CU unsplit, take
+// 67–77 µs in two halves plus 7–9 µs of partial sums against 96–103 µs.
 int gemm_bf16_splitk(int64_t M, int64_t N, int64_t K) {
     const int64_t tiles = ((M + 127) / 128) * ((N + 127) / 128);
-    if (tiles > 128 || K < 2048 || N % 4 != 0) return 1;
+    if (tiles > 256 || K < 2048 || N % 4 != 0) return 1;
     int s = 1;
     while (s < 8 && tiles * s * 2 <= 512 && K / (s * 2) >= 1024) s *= 2;
     return s;
