@@ -1618,10 +1618,15 @@ static void backward_node(Tr &t, TNode &tn) {
             } else if (dst(0)) {
                 gemm_nt(s, dyb, N, w->b, N, (int)M, (int)K, (int)N, dst(0), K, !tn.first_writer[0]);
             }
-            k::transpose_bf16(s, dyb, N, nullptr, 1, (int)M, (int)N, dybt, M);
+            // dyᵀ in bf16 (dyb is bf16(dy), from the cast or the GELU-adjoint
+            // epilogue) and the bias gradient in one pass over dy where the
+            // shape allows, else the transpose of dyb and the column sums.
+            const bool fused =
+                b && k::transpose_colsum(s, dy, M, (int)N, dybt, M, b->grad, false, (float *)tn.B("colsum"));
+            if (!fused) k::transpose_bf16(s, dyb, N, nullptr, 1, (int)M, (int)N, dybt, M);
             k::transpose_bf16(s, xb, K, nullptr, 1, (int)M, (int)K, xbt, M);
             gemm_nt(s, xbt, M, dybt, M, (int)K, (int)N, (int)M, w->grad, N, false, (float *)tn.B("wparts"));
-            if (b) k::colsum(s, dy, M, (int)N, b->grad, false, (float *)tn.B("colsum"));
+            if (b && !fused) k::colsum(s, dy, M, (int)N, b->grad, false, (float *)tn.B("colsum"));
             break;
         }
         case CATNN_OP_SWIGLU: {  // swiglu_backward, adjoint.rs:217-251

@@ -169,6 +169,52 @@ __global__ __launch_bounds__(256) void transpose_vec_kernel(const TS *__restrict
     }
 }
 
+// A cotangent's two uses in a weight product's backward in one pass over
+// the fp32 rows: the bf16 transposed copy (the weight gradient's operand)
+// and the bias gradient's per-64-row column partial sums.  One 64 × 64 tile
+// a block: the fp32 tile goes to LDS (rows of 65 floats); 64 threads each
+// add one column over the tile's rows in order from zero (the order and
+// grouping of col_partials_kernel, so reduce_partials gives the same bits);
+// eight lanes per destination row gather eight source rows each and store
+// the rounded values as one 128-byte run.  Full tiles, 16-byte rows only.
+__global__ __launch_bounds__(256) void transpose_colsum_kernel(const float *__restrict__ src, int64_t lds,
+                                                               int cols, bf16_t *__restrict__ dst,
+                                                               int64_t ldd, float *__restrict__ part) {
+    __shared__ float f[64][65];
+    const int r0 = blockIdx.y * 64, c0 = blockIdx.x * 64;
+    const int tid = threadIdx.x;
+    float4 w[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int idx = tid + 256 * j, i = idx >> 4, cc = (idx & 15) * 4;
+        w[j] = *reinterpret_cast<const float4 *>(src + (int64_t)(r0 + i) * lds + c0 + cc);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int idx = tid + 256 * j, i = idx >> 4, cc = (idx & 15) * 4;
+        f[i][cc + 0] = w[j].x;
+        f[i][cc + 1] = w[j].y;
+        f[i][cc + 2] = w[j].z;
+        f[i][cc + 3] = w[j].w;
+    }
+    __syncthreads();
+    if (tid < 64) {
+        float sa = 0.f;
+#pragma unroll 16
+        for (int i = 0; i < 64; ++i) sa += f[i][tid];
+        part[(int64_t)blockIdx.y * cols + c0 + tid] = sa;
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int item = tid + 256 * j, k = item & 7, oc = item >> 3;  // source rows 8k … 8k+7, column oc
+        uint32_t u[4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+            u[m] = (uint32_t)f2bf(f[8 * k + 2 * m][oc]) | ((uint32_t)f2bf(f[8 * k + 2 * m + 1][oc]) << 16);
+        *reinterpret_cast<uint4 *>(dst + (int64_t)(c0 + oc) * ldd + r0 + 8 * k) = make_uint4(u[0], u[1], u[2], u[3]);
+    }
+}
+
 // Split-bf16 operands.  v = hi + lo + O(2⁻¹⁷|v|) with hi = bf16(v) and
 // lo = bf16(v − hi).  A row of A' = [hi | lo | hi] against a row of
 // B' = [hi | hi | lo] sums to hi·hi + lo·hi + hi·lo over 3K: an fp32 product
@@ -1403,6 +1449,19 @@ void colsum(hipStream_t s, const float *y, int64_t rows, int cols, float *out, b
         y, nullptr, nullptr, nullptr, rows, cols, scratch, nullptr);
     CATNN_HIP(hipGetLastError());
     reduce_partials(s, scratch, ng, cols, out, accumulate);
+}
+
+bool transpose_colsum(hipStream_t s, const float *y, int64_t rows, int cols, bf16_t *yt, int64_t ldt,
+                      float *out, bool accumulate, float *scratch) {
+    if (rows <= 0 || cols <= 0) return true;
+    if (rows % 64 != 0 || cols % 64 != 0 || !al16(y) || !al16(yt) || ldt % 8 != 0 || ldt < rows ||
+        rows / 64 >= 65536)
+        return false;
+    transpose_colsum_kernel<<<dim3((unsigned)(cols / 64), (unsigned)(rows / 64)), 256, 0, s>>>(y, cols, cols, yt,
+                                                                                              ldt, scratch);
+    CATNN_HIP(hipGetLastError());
+    reduce_partials(s, scratch, rows / 64, cols, out, accumulate);
+    return true;
 }
 
 void act_backward(hipStream_t s, const float *z, const float *dy, float *dx, int64_t n, int act,
