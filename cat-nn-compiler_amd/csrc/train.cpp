@@ -1604,7 +1604,17 @@ static void backward_node(Tr &t, TNode &tn) {
             const int64_t K = w->rows, N = w->cols, M = nx / K;
             bf16_t *dyb = (bf16_t *)tn.B("dyb"), *dybt = (bf16_t *)tn.B("dybt");
             bf16_t *xb = (bf16_t *)tn.B("xb"), *xbt = (bf16_t *)tn.B("xbt");
-            if (!tn.dyb_ready) k::cast_f32_bf16(s, dy, dyb, M * N);
+            // dyb = bf16(dy) (unless the GELU-adjoint epilogue wrote it), its
+            // transpose and the bias gradient in one pass over dy where the
+            // shape allows; else the cast, the transpose of dyb and the
+            // column sums.
+            float *cs = b ? (float *)tn.B("colsum") : nullptr;
+            bool t_done = false, b_done = false;
+            if (!tn.dyb_ready) {
+                t_done = k::transpose_colsum(s, dy, M, (int)N, dybt, M, b ? b->grad : nullptr, false, cs, dyb);
+                b_done = t_done && b;
+                if (!t_done) k::cast_f32_bf16(s, dy, dyb, M * N);
+            }
             if (tn.gelu_pre != UINT32_MAX) {
                 // dA = (dy·Wᵀ) ∘ gelu'(A's output): A's cotangent and its bf16 copy.
                 TNode &an = t.nodes[t.index.at(tn.gelu_pre)];
@@ -1618,15 +1628,11 @@ static void backward_node(Tr &t, TNode &tn) {
             } else if (dst(0)) {
                 gemm_nt(s, dyb, N, w->b, N, (int)M, (int)K, (int)N, dst(0), K, !tn.first_writer[0]);
             }
-            // dyᵀ in bf16 (dyb is bf16(dy), from the cast or the GELU-adjoint
-            // epilogue) and the bias gradient in one pass over dy where the
-            // shape allows, else the transpose of dyb and the column sums.
-            const bool fused =
-                b && k::transpose_colsum(s, dy, M, (int)N, dybt, M, b->grad, false, (float *)tn.B("colsum"));
-            if (!fused) k::transpose_bf16(s, dyb, N, nullptr, 1, (int)M, (int)N, dybt, M);
+            if (!t_done && b) t_done = b_done = k::transpose_colsum(s, dy, M, (int)N, dybt, M, b->grad, false, cs);
+            if (!t_done) k::transpose_bf16(s, dyb, N, nullptr, 1, (int)M, (int)N, dybt, M);
             k::transpose_bf16(s, xb, K, nullptr, 1, (int)M, (int)K, xbt, M);
             gemm_nt(s, xbt, M, dybt, M, (int)K, (int)N, (int)M, w->grad, N, false, (float *)tn.B("wparts"));
-            if (b && !fused) k::colsum(s, dy, M, (int)N, b->grad, false, (float *)tn.B("colsum"));
+            if (b && !b_done) k::colsum(s, dy, M, (int)N, b->grad, false, cs);
             break;
         }
         case CATNN_OP_SWIGLU: {  // swiglu_backward, adjoint.rs:217-251
@@ -1693,7 +1699,9 @@ static void backward_node(Tr &t, TNode &tn) {
             bf16_t *dqkvb = (bf16_t *)tn.B("dqkvb"), *dqkvt = (bf16_t *)tn.B("dqkvt");
             bf16_t *x3 = (bf16_t *)tn.B("x3"), *xbt = (bf16_t *)tn.B("xbt");
             const bool core_bf16 = attn_core_bf16(nd, D);
-            k::cast_f32_bf16(s, dy, dyb, T * D);
+            // bf16(dy) and its transpose in one pass where the shape allows
+            const bool dy_t = k::transpose_colsum(s, dy, T, (int)D, dybt, T, nullptr, false, nullptr, dyb);
+            if (!dy_t) k::cast_f32_bf16(s, dy, dyb, T * D);
             {  // dctx = dy·woᵀ (and its bf16 copy for the bf16 core)
                 k::GemmBf16Params p = gp();
                 p.A = dyb; p.lda = D; p.B = wo->b; p.ldb = D;
@@ -1702,7 +1710,7 @@ static void backward_node(Tr &t, TNode &tn) {
                 if (core_bf16) { p.Cb = (bf16_t *)tn.B("dctxb"); p.ldcb = D; }
                 k::gemm_bf16_launch(s, p);
             }
-            k::transpose_bf16(s, dyb, D, nullptr, 1, (int)T, (int)D, dybt, T);
+            if (!dy_t) k::transpose_bf16(s, dyb, D, nullptr, 1, (int)T, (int)D, dybt, T);
             k::transpose_bf16(s, (bf16_t *)tn.B("ctx3"), 3 * D, nullptr, 1, (int)T, (int)D, ctxt, T);
             gemm_nt(s, ctxt, T, dybt, T, (int)D, (int)D, (int)T, wo->grad, D, false, (float *)tn.B("wparts"));
             if (core_bf16) {
@@ -1717,11 +1725,12 @@ static void backward_node(Tr &t, TNode &tn) {
                                       (float *)tn.B("lse"), dqkv, dqkv + D, dqkv + 2 * D, 3 * D, Bt, S, H, dh,
                                       causal, (float *)tn.B("dscr"));
             }
-            k::cast_f32_bf16(s, dqkv, dqkvb, T * 3 * D);
+            const bool dqkv_t = k::transpose_colsum(s, dqkv, T, (int)(3 * D), dqkvt, T, nullptr, false, nullptr, dqkvb);
+            if (!dqkv_t) k::cast_f32_bf16(s, dqkv, dqkvb, T * 3 * D);
             if (dst(0))
                 gemm_nt(s, dqkvb, 3 * D, wqkv->b, 3 * D, (int)T, (int)D, (int)(3 * D), dst(0), D,
                         !tn.first_writer[0]);
-            k::transpose_bf16(s, dqkvb, 3 * D, nullptr, 1, (int)T, (int)(3 * D), dqkvt, T);
+            if (!dqkv_t) k::transpose_bf16(s, dqkvb, 3 * D, nullptr, 1, (int)T, (int)(3 * D), dqkvt, T);
             k::transpose_bf16(s, x3, 3 * D, nullptr, 1, (int)T, (int)D, xbt, T);
             gemm_nt(s, xbt, T, dqkvt, T, (int)D, (int)(3 * D), (int)T, wqkv->grad, 3 * D, false,
                     (float *)tn.B("wparts"));

@@ -169,17 +169,20 @@ __global__ __launch_bounds__(256) void transpose_vec_kernel(const TS *__restrict
     }
 }
 
-// A cotangent's two uses in a weight product's backward in one pass over
-// the fp32 rows: the bf16 transposed copy (the weight gradient's operand)
-// and the bias gradient's per-64-row column partial sums.  One 64 × 64 tile
-// a block: the fp32 tile goes to LDS (rows of 65 floats); 64 threads each
-// add one column over the tile's rows in order from zero (the order and
-// grouping of col_partials_kernel, so reduce_partials gives the same bits);
-// eight lanes per destination row gather eight source rows each and store
-// the rounded values as one 128-byte run.  Full tiles, 16-byte rows only.
+// A cotangent's uses in a weight product's backward in one pass over the
+// fp32 rows: the bf16 transposed copy (the weight gradient's operand), and
+// optionally the row-major bf16 copy (the input gradient's operand) and the
+// bias gradient's per-64-row column partial sums.  One 64 × 64 tile a
+// block: the fp32 tile goes to LDS (rows of 65 floats), the row-major copy
+// straight from registers; 64 threads each add one column over the tile's
+// rows in order from zero (the order and grouping of col_partials_kernel,
+// so reduce_partials gives the same bits); eight lanes per destination row
+// gather eight source rows each and store the rounded values as one
+// 128-byte run.  Full tiles, 16-byte rows only.
 __global__ __launch_bounds__(256) void transpose_colsum_kernel(const float *__restrict__ src, int64_t lds,
                                                                int cols, bf16_t *__restrict__ dst,
-                                                               int64_t ldd, float *__restrict__ part) {
+                                                               int64_t ldd, float *__restrict__ part,
+                                                               bf16_t *__restrict__ rowb) {
     __shared__ float f[64][65];
     const int r0 = blockIdx.y * 64, c0 = blockIdx.x * 64;
     const int tid = threadIdx.x;
@@ -188,6 +191,14 @@ __global__ __launch_bounds__(256) void transpose_colsum_kernel(const float *__re
     for (int j = 0; j < 4; ++j) {
         const int idx = tid + 256 * j, i = idx >> 4, cc = (idx & 15) * 4;
         w[j] = *reinterpret_cast<const float4 *>(src + (int64_t)(r0 + i) * lds + c0 + cc);
+    }
+    if (rowb) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int idx = tid + 256 * j, i = idx >> 4, cc = (idx & 15) * 4;
+            *reinterpret_cast<uint2 *>(rowb + (int64_t)(r0 + i) * lds + c0 + cc) =
+                pack4(f2bf(w[j].x), f2bf(w[j].y), f2bf(w[j].z), f2bf(w[j].w));
+        }
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -198,7 +209,7 @@ __global__ __launch_bounds__(256) void transpose_colsum_kernel(const float *__re
         f[i][cc + 3] = w[j].w;
     }
     __syncthreads();
-    if (tid < 64) {
+    if (part && tid < 64) {
         float sa = 0.f;
 #pragma unroll 16
         for (int i = 0; i < 64; ++i) sa += f[i][tid];
@@ -1452,15 +1463,15 @@ void colsum(hipStream_t s, const float *y, int64_t rows, int cols, float *out, b
 }
 
 bool transpose_colsum(hipStream_t s, const float *y, int64_t rows, int cols, bf16_t *yt, int64_t ldt,
-                      float *out, bool accumulate, float *scratch) {
+                      float *out, bool accumulate, float *scratch, bf16_t *yb) {
     if (rows <= 0 || cols <= 0) return true;
-    if (rows % 64 != 0 || cols % 64 != 0 || !al16(y) || !al16(yt) || ldt % 8 != 0 || ldt < rows ||
-        rows / 64 >= 65536)
+    if (rows % 64 != 0 || cols % 64 != 0 || !al16(y) || !al16(yt) || (yb && (reinterpret_cast<uintptr_t>(yb) & 7)) ||
+        ldt % 8 != 0 || ldt < rows || rows / 64 >= 65536)
         return false;
-    transpose_colsum_kernel<<<dim3((unsigned)(cols / 64), (unsigned)(rows / 64)), 256, 0, s>>>(y, cols, cols, yt,
-                                                                                              ldt, scratch);
+    transpose_colsum_kernel<<<dim3((unsigned)(cols / 64), (unsigned)(rows / 64)), 256, 0, s>>>(
+        y, cols, cols, yt, ldt, out ? scratch : nullptr, yb);
     CATNN_HIP(hipGetLastError());
-    reduce_partials(s, scratch, rows / 64, cols, out, accumulate);
+    if (out) reduce_partials(s, scratch, rows / 64, cols, out, accumulate);
     return true;
 }
 

@@ -43,12 +43,13 @@ void ln_backward(hipStream_t s, const float *x, const float *g, const float *mea
 void sum_parts(hipStream_t s, const float *parts, int np, int64_t n, float *out, bool accumulate);
 
 uint64_t colsum_scratch_bytes(int64_t rows, int cols);
-// y [rows, cols] (fp32, row stride cols): yt = bf16(y)ᵀ (row stride ldt) and
-// out (+)= column sums of y, as transpose_f32_bf16 and colsum would give
-// them, in one pass (colsum's scratch).  False, with nothing launched,
-// unless rows and cols are multiples of 64 with 16-byte aligned rows.
+// y [rows, cols] (fp32, row stride cols): yt = bf16(y)ᵀ (row stride ldt),
+// with out (or null) (+)= the column sums of y and yb (or null) = bf16(y)
+// row-major, as transpose_f32_bf16, colsum (its scratch) and cast_f32_bf16
+// would give them, in one pass.  False, with nothing launched, unless rows
+// and cols are multiples of 64 with 16-byte aligned rows.
 bool transpose_colsum(hipStream_t s, const float *y, int64_t rows, int cols, bf16_t *yt, int64_t ldt,
-                      float *out, bool accumulate, float *scratch);
+                      float *out, bool accumulate, float *scratch, bf16_t *yb = nullptr);
 void colsum(hipStream_t s, const float *y, int64_t rows, int cols, float *out, bool accumulate,
             float *scratch);
 void act_backward(hipStream_t s, const float *z, const float *dy, float *dx, int64_t n, int act,
