@@ -609,6 +609,62 @@ __global__ __launch_bounds__(256) void ln_bwd_dx_kernel(const float *__restrict_
     }
 }
 
+// Rows of 256·NV4 floats, 16-byte aligned: the same arithmetic with lane l
+// holding the float4 runs l, l + 64, …, all of a lane's loads (x, dy, γ and,
+// accumulating, the old dx) issued before the first product.
+template <int NV4>
+__global__ __launch_bounds__(256) void ln_bwd_dx4_kernel(const float *__restrict__ x,
+                                                         const float *__restrict__ gam,
+                                                         const float *__restrict__ mean,
+                                                         const float *__restrict__ rstd,
+                                                         const float *__restrict__ dy,
+                                                         float *__restrict__ dx, int accumulate,
+                                                         int64_t rows, int cols) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const float mu = mean[row], inv = rstd[row];
+    const float4 *xr = reinterpret_cast<const float4 *>(x + row * cols);
+    const float4 *gr = reinterpret_cast<const float4 *>(dy + row * cols);
+    const float4 *g4 = reinterpret_cast<const float4 *>(gam);
+    float4 *o4 = reinterpret_cast<float4 *>(dx + row * cols);
+    float4 xv[NV4], dv[NV4], gv[NV4], ov[NV4];
+#pragma unroll
+    for (int j = 0; j < NV4; ++j) {
+        const int c = lane + 64 * j;
+        xv[j] = xr[c];
+        dv[j] = gr[c];
+        gv[j] = g4[c];
+        ov[j] = accumulate ? o4[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    float xh[NV4][4], gd[NV4][4];
+    float sd = 0.f, sdx = 0.f;
+#pragma unroll
+    for (int j = 0; j < NV4; ++j) {
+        const float xs[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w}, ds[4] = {dv[j].x, dv[j].y, dv[j].z, dv[j].w},
+                    gs[4] = {gv[j].x, gv[j].y, gv[j].z, gv[j].w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            xh[j][q] = (xs[q] - mu) * inv;
+            gd[j][q] = ds[q] * gs[q];
+            sd += gd[j][q];
+            sdx += gd[j][q] * xh[j][q];
+        }
+    }
+    sd = wave_sum_dpp(sd);
+    sdx = wave_sum_dpp(sdx);
+    const float n = (float)cols;
+#pragma unroll
+    for (int j = 0; j < NV4; ++j) {
+        float v[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[q] = (inv / n) * (n * gd[j][q] - sd - xh[j][q] * sdx);
+        const float4 o = ov[j];
+        o4[lane + 64 * j] = accumulate ? make_float4(o.x + v[0], o.y + v[1], o.z + v[2], o.w + v[3])
+                                       : make_float4(v[0], v[1], v[2], v[3]);
+    }
+}
+
 // Any width: the same with two passes over the row in memory.
 __global__ __launch_bounds__(256) void ln_bwd_dx_any_kernel(const float *__restrict__ x,
                                                             const float *__restrict__ gam,
@@ -1432,7 +1488,11 @@ void ln_backward(hipStream_t s, const float *x, const float *g, const float *mea
     if (dx) {
         const unsigned blocks = (unsigned)((rows + 3) / 4);
         const int acc = accumulate ? 1 : 0;
-        if (cols <= 256) ln_bwd_dx_kernel<4><<<blocks, 256, 0, s>>>(x, g, mean, rstd, dy, dx, acc, rows, cols);
+        const bool v4 = al16(x) && al16(g) && al16(dy) && al16(dx);
+        if (v4 && cols == 1024) ln_bwd_dx4_kernel<4><<<blocks, 256, 0, s>>>(x, g, mean, rstd, dy, dx, acc, rows, cols);
+        else if (v4 && cols == 2048)
+            ln_bwd_dx4_kernel<8><<<blocks, 256, 0, s>>>(x, g, mean, rstd, dy, dx, acc, rows, cols);
+        else if (cols <= 256) ln_bwd_dx_kernel<4><<<blocks, 256, 0, s>>>(x, g, mean, rstd, dy, dx, acc, rows, cols);
         else if (cols <= 512) ln_bwd_dx_kernel<8><<<blocks, 256, 0, s>>>(x, g, mean, rstd, dy, dx, acc, rows, cols);
         else if (cols <= 1024) ln_bwd_dx_kernel<16><<<blocks, 256, 0, s>>>(x, g, mean, rstd, dy, dx, acc, rows, cols);
         else if (cols <= 2048) ln_bwd_dx_kernel<32><<<blocks, 256, 0, s>>>(x, g, mean, rstd, dy, dx, acc, rows, cols);
