@@ -391,8 +391,10 @@ __global__ void swiglu_dadc_f32_kernel(const float *__restrict__ dh, const float
 }
 
 // LayerNorm forward for training: y (fp32 and/or bf16), mean and rstd per
-// row.  One wavefront per row; any width.
-template <bool VEC>
+// row.  One wavefront per row; any width.  NV4 > 0 (rows of 256·NV4
+// floats): a lane's NV4 float4 runs of x are loaded once, into registers,
+// and the three passes read them there, in the same order (same bits).
+template <bool VEC, int NV4 = 0>
 __global__ __launch_bounds__(256) void ln_fwd_kernel(const float *__restrict__ x,
                                                      const float *__restrict__ g,
                                                      const float *__restrict__ b,
@@ -407,29 +409,41 @@ __global__ __launch_bounds__(256) void ln_fwd_kernel(const float *__restrict__ x
     if (VEC) {  // four consecutive columns a lane per step: 16-byte x, γ, β, y and 8-byte yb accesses
         const int c4n = cols / 4;
         const float4 *x4 = reinterpret_cast<const float4 *>(xr);
+        float4 xv[NV4 > 0 ? NV4 : 1];
+        if constexpr (NV4 > 0) {
+#pragma unroll
+            for (int j = 0; j < NV4; ++j) xv[j] = x4[lane + 64 * j];
+        }
+        // f(c, x4[c]) for the lane's runs c = lane, lane + 64, … in order
+        auto each = [&](auto &&f) {
+            if constexpr (NV4 > 0) {
+#pragma unroll
+                for (int j = 0; j < NV4; ++j) f(lane + 64 * j, xv[j]);
+            } else {
+                for (int c = lane; c < c4n; c += 64) f(c, x4[c]);
+            }
+        };
         float s = 0.f;
-        for (int c = lane; c < c4n; c += 64) {
-            const float4 v = x4[c];
+        each([&](int, const float4 &v) {
             s += v.x;
             s += v.y;
             s += v.z;
             s += v.w;
-        }
+        });
         const float n = (float)cols;
         const float mu = wave_sum_dpp(s) / n;
         float q = 0.f;
-        for (int c = lane; c < c4n; c += 64) {
-            const float4 v = x4[c];
+        each([&](int, const float4 &v) {
             const float d0 = v.x - mu, d1 = v.y - mu, d2 = v.z - mu, d3 = v.w - mu;
             q += d0 * d0;
             q += d1 * d1;
             q += d2 * d2;
             q += d3 * d3;
-        }
+        });
         const float inv = 1.0f / sqrtf(wave_sum_dpp(q) / n + eps);
         const float4 *g4 = reinterpret_cast<const float4 *>(g), *b4 = reinterpret_cast<const float4 *>(b);
-        for (int c = lane; c < c4n; c += 64) {
-            const float4 v = x4[c], gv = g4[c], bv = b4[c];
+        each([&](int c, const float4 &v) {
+            const float4 gv = g4[c], bv = b4[c];
             const float4 o = make_float4((v.x - mu) * inv * gv.x + bv.x, (v.y - mu) * inv * gv.y + bv.y,
                                          (v.z - mu) * inv * gv.z + bv.z, (v.w - mu) * inv * gv.w + bv.w);
             if (y) reinterpret_cast<float4 *>(y + row * cols)[c] = o;
@@ -445,7 +459,7 @@ __global__ __launch_bounds__(256) void ln_fwd_kernel(const float *__restrict__ x
                 r3[c4n + c] = pack4(l[0], l[1], l[2], l[3]);
                 r3[2 * c4n + c] = pack4(h[0], h[1], h[2], h[3]);
             }
-        }
+        });
         if (lane == 0) {
             mean[row] = mu;
             rstd[row] = inv;
@@ -1450,7 +1464,8 @@ void ln_forward_train(hipStream_t s, const float *x, const float *g, const float
     const bool vec = cols % 4 == 0 && al(x, 16) && al(g, 16) && al(b, 16) && (!y || al(y, 16)) &&
                      (!yb || al(yb, 8)) && (!y3 || al(y3, 8));
     const unsigned blocks = (unsigned)((rows + 3) / 4);
-    if (vec) ln_fwd_kernel<true><<<blocks, 256, 0, s>>>(x, g, b, y, yb, y3, mean, rstd, rows, cols, eps);
+    if (vec && cols == 1024) ln_fwd_kernel<true, 4><<<blocks, 256, 0, s>>>(x, g, b, y, yb, y3, mean, rstd, rows, cols, eps);
+    else if (vec) ln_fwd_kernel<true><<<blocks, 256, 0, s>>>(x, g, b, y, yb, y3, mean, rstd, rows, cols, eps);
     else ln_fwd_kernel<false><<<blocks, 256, 0, s>>>(x, g, b, y, yb, y3, mean, rstd, rows, cols, eps);
     CATNN_HIP(hipGetLastError());
 }
