@@ -1313,6 +1313,50 @@ __global__ __launch_bounds__(256) void moe_slot_grad_kernel(
     if (threadIdx.x == 0) dw[slot] = (ws[0] + ws[1]) + (ws[2] + ws[3]);
 }
 
+// The same for bf16 dys and rows of 256·NV4 floats (16-byte aligned): one
+// wavefront per position, four positions a block, each lane holding NV4
+// float4 runs of y and dout (all loaded before the first product), dw summed
+// over the lane's runs and then across the wavefront by DPP.
+template <int NV4>
+__global__ __launch_bounds__(256) void moe_slot_grad4_kernel(const int32_t *__restrict__ slot_of_pos,
+                                                             const float *__restrict__ w,
+                                                             const float *__restrict__ y,
+                                                             const float *__restrict__ dout, int K, int H,
+                                                             int n_pos, bf16_t *__restrict__ dys,
+                                                             float *__restrict__ dw) {
+    const int lane = threadIdx.x & 63;
+    const int pos = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (pos >= n_pos) return;
+    const int slot = slot_of_pos[pos];
+    uint2 *o = reinterpret_cast<uint2 *>(dys + (int64_t)pos * H);
+    if (slot < 0) {
+#pragma unroll
+        for (int j = 0; j < NV4; ++j) o[lane + 64 * j] = make_uint2(0u, 0u);
+        return;
+    }
+    const int t = slot / K;
+    const float wt = w[slot];
+    const float4 *g4 = reinterpret_cast<const float4 *>(dout + (int64_t)t * H);
+    const float4 *y4 = reinterpret_cast<const float4 *>(y + (int64_t)pos * H);
+    float4 gv[NV4], yv[NV4];
+#pragma unroll
+    for (int j = 0; j < NV4; ++j) {
+        gv[j] = g4[lane + 64 * j];
+        yv[j] = y4[lane + 64 * j];
+    }
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < NV4; ++j) {
+        s += yv[j].x * gv[j].x;
+        s += yv[j].y * gv[j].y;
+        s += yv[j].z * gv[j].z;
+        s += yv[j].w * gv[j].w;
+        o[lane + 64 * j] = pack4(f2bf(wt * gv[j].x), f2bf(wt * gv[j].y), f2bf(wt * gv[j].z), f2bf(wt * gv[j].w));
+    }
+    s = wave_sum_dpp(s);
+    if (lane == 0) dw[slot] = s;
+}
+
 // dx[t][h] (+)= Σ_k dxs[pos(t,k)][h] + Σ_e dl[t][e]·gate[h][e].  A thread
 // owns one h for kMoeDxTokens tokens, so gate[h][·] is read once per
 // thread and dl[t][·] is uniform across the block.
@@ -1710,7 +1754,13 @@ uint64_t router_backward_scratch_bytes(int T, int H, int E) {
 void moe_slot_grads(hipStream_t s, const int32_t *slot_of_pos, const float *w, const float *y,
                     const float *dout, int K, int H, int n_pos, bf16_t *dys, float *dw) {
     if (n_pos <= 0) return;
-    moe_slot_grad_kernel<bf16_t><<<(unsigned)n_pos, 256, 0, s>>>(slot_of_pos, w, y, dout, K, H, n_pos, dys, dw);
+    const bool v4 = (reinterpret_cast<uintptr_t>(y) & 15) == 0 && (reinterpret_cast<uintptr_t>(dout) & 15) == 0 &&
+                    (reinterpret_cast<uintptr_t>(dys) & 7) == 0;
+    if (v4 && H == 1024)
+        moe_slot_grad4_kernel<4><<<(unsigned)((n_pos + 3) / 4), 256, 0, s>>>(slot_of_pos, w, y, dout, K, H, n_pos,
+                                                                            dys, dw);
+    else
+        moe_slot_grad_kernel<bf16_t><<<(unsigned)n_pos, 256, 0, s>>>(slot_of_pos, w, y, dout, K, H, n_pos, dys, dw);
     CATNN_HIP(hipGetLastError());
 }
 
