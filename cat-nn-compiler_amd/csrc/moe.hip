@@ -475,8 +475,9 @@ __global__ __launch_bounds__(256) void combine_kernel(const float *__restrict__ 
     }
 }
 
-// (One wavefront per token with all of its slot rows loaded before the
-// sums measured 31.6 against 32.8 us on config 4 and was not kept.)
+// The same on float4 runs of 16-byte aligned rows.  (One wavefront per
+// token with all of its slot rows loaded before the sums measured 31.6
+// against 32.8 us on config 4 and was not kept.)
 __global__ __launch_bounds__(256) void combine4_kernel(const float *__restrict__ y,
                                                        const int32_t *__restrict__ pos_of_slot,
                                                        const float *__restrict__ w, int T, int K,
