@@ -43,7 +43,11 @@ namespace k {
 namespace {
 
 constexpr int kRouteChunk = 64;   // hidden elements staged per LDS pass
-constexpr int kPermChunk = 4096;  // slots per permutation block
+// Slots per permutation block: a block's scatter visits its slots 256 at a
+// time with three barriers each, so small chunks spread that serial work
+// over more CUs (config 5's 16384 slots: 4096-slot chunks, 4 blocks, took
+// 17.6 us for the scatter).
+constexpr int kPermChunk = 512;
 constexpr int kMaxRouteExperts = 256;
 constexpr int kMaxTopK = 16;
 
@@ -381,11 +385,16 @@ __global__ void perm_scan_kernel(const int32_t *__restrict__ block_counts, int n
                                  int32_t *__restrict__ offsets) {
     __shared__ int tot[kMaxExperts + 1];
     const int e = threadIdx.x;
+    // Lane e walks the blocks' counts of expert e eight at a time, the
+    // eight loads issued together (integer sums: any grouping is exact).
     if (e < E) {
         int run = 0;
-        for (int b = 0; b < nb; ++b) {
-            block_base[(int64_t)b * E + e] = run;
-            run += block_counts[(int64_t)b * E + e];
+        for (int b0 = 0; b0 < nb; b0 += 8) {
+            int v[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = b0 + j < nb ? block_counts[(int64_t)(b0 + j) * E + e] : 0;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) run += v[j];
         }
         tot[e] = run;
         counts[e] = run;
@@ -407,9 +416,20 @@ __global__ void perm_scan_kernel(const int32_t *__restrict__ block_counts, int n
     }
     if (e == E - 1) offsets[E] = incl;
     __syncthreads();
+    // block_base[b][e] = the segment start of e + the counts of e in the
+    // blocks before b
     if (e < E) {
-        const int off = tot[e];
-        for (int b = 0; b < nb; ++b) block_base[(int64_t)b * E + e] += off;
+        int run = tot[e];
+        for (int b0 = 0; b0 < nb; b0 += 8) {
+            int v[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = b0 + j < nb ? block_counts[(int64_t)(b0 + j) * E + e] : 0;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                if (b0 + j < nb) block_base[(int64_t)(b0 + j) * E + e] = run;
+                run += v[j];
+            }
+        }
     }
 }
 
