@@ -1287,21 +1287,36 @@ void launch_cfg(hipStream_t s, const GemmBf16Params &p, bool vec, bool dual, uns
     }
 }
 
-// One thread lists the 128-row and the 256-row tiles of every segment.
+// One wavefront lists the 128-row and the 256-row tiles of every segment
+// (11 us as one thread's walk on config 5's eight experts).
 __global__ void build_tiles2_kernel(const int32_t *__restrict__ offsets, int n_experts, int32_t *__restrict__ t1,
                                     int max1, int32_t *__restrict__ t2, int max2) {
-    if (threadIdx.x != 0 || blockIdx.x != 0) return;
+    // One wavefront, lane e owning expert e (n_experts ≤ 64): the tiles of
+    // expert e start at the exclusive prefix of the experts' tile counts,
+    // so the table is the one an in-order walk over the experts writes,
+    // cut at its capacity.
+    const int e = threadIdx.x;
     for (int w = 0; w < 2; ++w) {
         int32_t *t = w ? t2 : t1;
         const int mx = w ? max2 : max1, bm = w ? 256 : kRowTile;
-        int n = 0;
-        for (int e = 0; e < n_experts; ++e)
-            for (int r = offsets[e]; r < offsets[e + 1] && n < mx; r += bm) {
-                t[n] = e;
-                t[mx + n] = r;
-                ++n;
-            }
-        t[2 * mx] = n;
+        int r0 = 0, cnt = 0;
+        if (e < n_experts) {
+            r0 = offsets[e];
+            const int r1 = offsets[e + 1];
+            cnt = r1 > r0 ? (r1 - r0 + bm - 1) / bm : 0;
+        }
+        int incl = cnt;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const int o = __shfl_up(incl, off, 64);
+            if (e >= off) incl += o;
+        }
+        const int start = incl - cnt, total = __shfl(incl, 63, 64);
+        for (int i = 0; i < cnt && start + i < mx; ++i) {
+            t[start + i] = e;
+            t[mx + start + i] = r0 + i * bm;
+        }
+        if (e == 0) t[2 * mx] = total < mx ? total : mx;
     }
 }
 
@@ -1383,6 +1398,7 @@ int64_t gemm_bf16_tiles_ints(int64_t rows, int n_experts) {
 }
 
 void gemm_bf16_build_tiles(hipStream_t s, const int32_t *offsets, int n_experts, int64_t rows, int32_t *tiles) {
+    CATNN_REQUIRE(n_experts > 0 && n_experts <= kMaxExperts, CATNN_ERR_SHAPE_MISMATCH, "tile table: expert count");
     const int m1 = max_tiles_for(rows, n_experts, kRowTile), m2 = max_tiles_for(rows, n_experts, 256);
     build_tiles2_kernel<<<1, 64, 0, s>>>(offsets, n_experts, tiles, m1, tiles + 2 * m1 + 1, m2);
     CATNN_HIP(hipGetLastError());

@@ -352,9 +352,11 @@ __global__ __launch_bounds__(256) void route_vec_kernel(const float *__restrict_
 // that capture it into a graph.
 __global__ void zero_i32_kernel(int32_t *__restrict__ p) { *p = 0; }
 
-__global__ __launch_bounds__(256) void fill_i32_kernel(int32_t *__restrict__ p, int64_t n, int32_t v) {
+__global__ __launch_bounds__(256) void fill_i32_kernel(int32_t *__restrict__ p, int64_t n, int32_t v,
+                                                       int32_t *__restrict__ zero) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (i < n) p[i] = v;
+    if (zero && i == 0) *zero = 0;
 }
 
 __global__ __launch_bounds__(256) void perm_count_kernel(const int32_t *__restrict__ idx,
@@ -642,9 +644,10 @@ void moe_permute_padded(hipStream_t s, const int32_t *idx, int64_t tokens, int64
     int32_t *block_counts = reinterpret_cast<int32_t *>(sc);
     int32_t *block_base = reinterpret_cast<int32_t *>(sc + align256((uint64_t)nb * E * 4));
     int32_t *bad = reinterpret_cast<int32_t *>(sc + 2 * align256((uint64_t)nb * E * 4));
-    zero_i32_kernel<<<1, 1, 0, s>>>(bad);
-    if (n_pos_cap > 0)
-        fill_i32_kernel<<<(unsigned)((n_pos_cap + 255) / 256), 256, 0, s>>>(slot_of_pos, n_pos_cap, -1);  // padding
+    if (n_pos_cap > 0)  // padding positions, and the bad-id counter cleared by the same launch
+        fill_i32_kernel<<<(unsigned)((n_pos_cap + 255) / 256), 256, 0, s>>>(slot_of_pos, n_pos_cap, -1, bad);
+    else
+        zero_i32_kernel<<<1, 1, 0, s>>>(bad);
     CATNN_HIP(hipGetLastError());
     if (nb > 0) {
         perm_count_kernel<<<(unsigned)nb, 256, 0, s>>>(idx, n, E, block_counts, bad);
